@@ -1,0 +1,258 @@
+/*
+ * x0ne Core for MI355X: the C ABI of the decode engine, its kernel-launch API and its arena.
+ *
+ * This is the drop-in boundary for the reference's x0ne-core runtime crate
+ * (x0ne-core/runtime/src/, Rust): every entry point below names the Rust item it replaces,
+ * file:line in the reference. Plain pointers and sizes only. A Rust FFI crate binds these
+ * functions one to one (see INTEGRATION.md for the extern block and the safe wrappers that give
+ * back the reference's Engine / Session / Greedy / Gpu / Arena types).
+ *
+ * Conventions:
+ *  - Every call returns an x0ne_status; X0NE_OK is 0. The other codes are the variants of the
+ *    reference's Error (x0ne-core/runtime/src/error.rs:4-15). x0ne_last_error copies the calling
+ *    thread's message of its last failed call.
+ *  - Format errors (bad config, bad ids, sizes) are raised before any device work, as in the
+ *    reference.
+ *  - Handles are not thread-safe: one thread at a time per engine (the reference's Gpu is Send,
+ *    not Sync, and x0ne-infer serialises through a Mutex, core_backend.rs:106,281).
+ *  - No call keeps caller memory after it returns, except the logits pointer of a session, valid
+ *    until the next step or finish (engine.rs:1141-1160).
+ */
+#ifndef X0NE_CORE_H
+#define X0NE_CORE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- errors (x0ne-core/runtime/src/error.rs:4-40) ---- */
+typedef enum {
+    X0NE_OK = 0,
+    X0NE_ERR_IO = 1,              /* Error::Io */
+    X0NE_ERR_FORMAT = 2,          /* Error::Format(String) */
+    X0NE_ERR_ARENA = 3,           /* Error::Arena(String) */
+    X0NE_ERR_NOT_IMPLEMENTED = 4, /* Error::NotImplemented(&'static str) */
+    X0NE_ERR_GPU = 5,             /* Error::Gpu(String) */
+} x0ne_status;
+
+/* The message of the calling thread's last failed call, truncated to len - 1 bytes. Returns the
+   full length. */
+size_t x0ne_last_error(char* buf, size_t len);
+
+/* Library facts: kernel-set fingerprint and the compiler it was built with
+   (x0ne-core/runtime/src/lib.rs: kernel_set()). */
+size_t x0ne_kernel_set(char* buf, size_t len);
+
+/* ---- the device (x0ne-core/runtime/src/gpu.rs) ---- */
+typedef struct x0ne_gpu x0ne_gpu;
+
+/* Gpu::new (gpu.rs:799-928): device 0, one non-blocking stream at the default priority, the
+   kernel table checked against the loaded code object. X0NE_ERR_GPU without a usable GPU. */
+x0ne_status x0ne_gpu_new(x0ne_gpu** out);
+void x0ne_gpu_free(x0ne_gpu* g);
+/* Gpu::sync: waits for the stream. */
+x0ne_status x0ne_gpu_sync(x0ne_gpu* g);
+/* Name, architecture, compute units, driver and runtime versions (Engine::describe's GPU part,
+   engine.rs:578-606). */
+x0ne_status x0ne_gpu_describe(const x0ne_gpu* g, char* buf, size_t len);
+uint32_t x0ne_gpu_compute_units(const x0ne_gpu* g);
+/* Free and total device bytes (Engine::device_free_bytes, engine.rs:632-635). */
+x0ne_status x0ne_gpu_mem_info(const x0ne_gpu* g, uint64_t* free_bytes, uint64_t* total_bytes);
+
+/* Driver-call tallies (gpu.rs:93-103, Counts): the witness of "one graph launch and one 4-byte
+   copy per token". */
+typedef struct {
+    uint64_t launches, graph_launches, gemms, htod, dtoh, memsets, syncs;
+} x0ne_counts;
+x0ne_status x0ne_gpu_counts(const x0ne_gpu* g, x0ne_counts* out);
+
+/* ---- the kernel table (x0ne-core/kernels/src/lib.rs:39-132: KERNEL_NAMES, KERNEL_PARAMS) ---- */
+typedef enum { X0NE_PARAM_PTR = 0, X0NE_PARAM_U32 = 1, X0NE_PARAM_F32 = 2 } x0ne_param;
+
+/* Arg::{Ptr(u64), U32, F32} (gpu.rs:281-314). */
+typedef struct {
+    uint32_t kind; /* x0ne_param */
+    uint32_t u32;
+    float f32;
+    uint32_t pad;
+    uint64_t ptr;
+} x0ne_arg;
+
+size_t x0ne_kernel_count(void);
+/* Name of kernel i, or NULL past the table. */
+const char* x0ne_kernel_name(size_t i);
+/* params_of (lib.rs:146-151): the parameter kinds of `name` into out (up to cap); returns the
+   count, or (size_t)-1 for an unknown name. */
+size_t x0ne_kernel_params(const char* name, uint32_t* out, size_t cap);
+/* check_args (gpu.rs:317-333): X0NE_ERR_GPU naming the first argument whose kind differs, or a
+   count that differs. No device needed. */
+x0ne_status x0ne_check_args(const char* name, const x0ne_arg* args, size_t n);
+/* Gpu::launch / launch! (gpu.rs:1031-1086, :1383-1387): kernel `name` on the stream, grid
+   (gx, gy), `block` threads, the arguments checked against the table first. Not synchronised. */
+x0ne_status x0ne_gpu_launch(x0ne_gpu* g, const char* name, uint32_t gx, uint32_t gy, uint32_t block,
+                            const x0ne_arg* args, size_t n);
+
+/* Gpu::gemm (gpu.rs:1098-1149), the projection the reference hands cuBLAS: Y[n][rows] =
+   X[n][cols] W^T, W [rows][cols] row-major bf16, X bf16, f32 accumulation; out_f32 = 0 gives
+   bf16 Y, 1 f32 Y. Device addresses. Hand-written bandwidth-bound GEMV, one launch per row of X. */
+x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n, uint64_t y,
+                          int out_f32);
+
+/* Split-K plan (gpu.rs:958-985, SplitPlan): P for a geometry, and whether a grouped kernel
+   serves it (group sizes 1, 2, 4, 8). */
+typedef struct {
+    uint32_t splits, grid_x, group, grouped, per_cu;
+} x0ne_split_plan;
+x0ne_status x0ne_gpu_split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out);
+/* launch_split (ops.rs:80-122): the split kernel, then the merge kernel (last_block = 0), or the
+   grouped kernel merging in its last block (last_block = 1, `counter` holds kv_heads zeroed
+   words and is left at zero). The KV planes are paged: [pages][kv_heads][16][128] bf16. */
+x0ne_status x0ne_gpu_attention_split(x0ne_gpu* g, const x0ne_split_plan* plan, int last_block, uint64_t q,
+                                     uint64_t k, uint64_t v, uint64_t page_table, uint64_t state, uint64_t counter,
+                                     uint64_t out, uint64_t pos, uint32_t q_heads, uint32_t kv_heads,
+                                     uint32_t max_ctx, float scale);
+/* split_state_bytes (ops.rs:125-127) */
+uint64_t x0ne_split_state_bytes(uint32_t q_heads, uint32_t splits);
+
+/* Graph capture (gpu.rs:1170-1238): every launch between begin and end is recorded, then
+   replayed by x0ne_gpu_launch_graph. */
+typedef struct x0ne_graph x0ne_graph;
+x0ne_status x0ne_gpu_capture_begin(x0ne_gpu* g);
+x0ne_status x0ne_gpu_capture_end(x0ne_gpu* g, x0ne_graph** out);
+x0ne_status x0ne_gpu_launch_graph(x0ne_gpu* g, const x0ne_graph* graph);
+size_t x0ne_graph_nodes(const x0ne_graph* graph);
+void x0ne_graph_free(x0ne_graph* graph);
+
+/* ---- the arena (x0ne-core/runtime/src/arena.rs) ---- */
+typedef enum { X0NE_CLASS_WEIGHTS = 0, X0NE_CLASS_CLIENT_DATA = 1 } x0ne_class; /* arena.rs:42-45 */
+
+/* A planned region (arena.rs:49-53); only valid for the arena that issued it. */
+typedef struct {
+    uint64_t arena, offset, len;
+} x0ne_slice;
+
+typedef struct x0ne_arena x0ne_arena;
+#define X0NE_ARENA_ALIGN 256 /* arena.rs:37 */
+
+/* Arena::new (arena.rs:163-172): a Building arena. */
+x0ne_status x0ne_arena_new(x0ne_arena** out);
+void x0ne_arena_free(x0ne_arena* a);
+/* Arena<Building>::alloc (arena.rs:174-198); refused once frozen (the reference's typestate
+   makes that a compile error; here it is X0NE_ERR_ARENA). */
+x0ne_status x0ne_arena_alloc(x0ne_arena* a, const char* label, uint64_t len, uint32_t cls, x0ne_slice* out);
+uint64_t x0ne_arena_planned_bytes(const x0ne_arena* a);
+/* freeze (arena.rs:210-225): the one allocation, on `g`'s device; g == NULL gives host memory
+   poisoned with 0xA5 (HostBacking, arena.rs:91-136). */
+x0ne_status x0ne_arena_freeze(x0ne_arena* a, x0ne_gpu* g);
+/* write / read (arena.rs:242-250): checked against the slice. Device arenas copy synchronously
+   on `g`'s stream. */
+x0ne_status x0ne_arena_write(x0ne_arena* a, x0ne_slice s, uint64_t at, const void* data, uint64_t len);
+x0ne_status x0ne_arena_read(const x0ne_arena* a, x0ne_slice s, uint64_t at, void* out, uint64_t len);
+/* addr / span (arena.rs:276-303): the device (or host) address of byte `at` of a slice. */
+x0ne_status x0ne_arena_addr(const x0ne_arena* a, x0ne_slice s, uint64_t at, uint64_t* out);
+x0ne_status x0ne_arena_span(const x0ne_arena* a, x0ne_slice s, uint64_t at, uint64_t len, uint64_t* out);
+/* scrub_client_data (arena.rs:252-265): zeroes every ClientData region, returns the bytes. */
+x0ne_status x0ne_arena_scrub(x0ne_arena* a, uint64_t* zeroed);
+/* Regions in plan order: label into label_buf, class, offset and length. */
+size_t x0ne_arena_region_count(const x0ne_arena* a);
+x0ne_status x0ne_arena_region(const x0ne_arena* a, size_t i, char* label_buf, size_t label_len, uint32_t* cls,
+                              uint64_t* offset, uint64_t* len);
+/* The slice of region i, as alloc returned it (for reading a planned buffer back). */
+x0ne_status x0ne_arena_region_slice(const x0ne_arena* a, size_t i, x0ne_slice* out);
+int x0ne_arena_is_frozen(const x0ne_arena* a);
+
+/* ---- the engine (x0ne-core/runtime/src/engine.rs) ---- */
+typedef struct x0ne_engine x0ne_engine;
+typedef struct x0ne_session x0ne_session;
+typedef struct x0ne_greedy x0ne_greedy;
+
+/* EngineOptions (engine.rs:38-40), plus this build's KV-page order: page_seed 0 keeps logical
+   page i at physical page i, another seed shuffles the pages with a seeded permutation. */
+typedef struct {
+    uint64_t max_ctx;
+    uint64_t page_seed;
+} x0ne_engine_options;
+
+/* Engine::load_from (engine.rs:301-309) over safetensors files already in memory (the
+   reference's st::SliceSource::new(index_json, files), st.rs:216-277): `n_files` files named
+   names[i] with bytes data[i][0..lens[i]]; index_json may be NULL. BF16 tensors of a Qwen3 dense
+   checkpoint; [q;k;v] and [gate;up] rows are packed at upload (weights.rs:420-429). */
+x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_files, const char* const* names,
+                                  const uint8_t* const* data, const uint64_t* lens, const char* index_json,
+                                  const x0ne_engine_options* opts, x0ne_engine** out);
+/* This build's synthetic load: the checkpoint of `config_json` drawn on the device, every
+   projection and the embedding N(0, std) bf16 from `seed` (tensor i of the checkpoint order,
+   oracle/src/model.rs:63-89, takes stream key splitmix64 output i of `seed`), norm weights 1.0. */
+x0ne_status x0ne_engine_load_synthetic(const char* config_json, uint64_t seed, double std_dev,
+                                       const x0ne_engine_options* opts, x0ne_engine** out);
+void x0ne_engine_free(x0ne_engine* e);
+
+/* Engine::session (engine.rs:389-406): prefills `prompt` and holds the last position's logits.
+   One session at a time per engine (a Session borrows the Engine mutably). */
+x0ne_status x0ne_engine_session(x0ne_engine* e, const uint32_t* prompt, size_t n, x0ne_session** out);
+/* Session::logits (engine.rs:1141-1149): vocab_size f32, valid until the next step or finish. */
+x0ne_status x0ne_session_logits(const x0ne_session* s, const float** ptr, size_t* len);
+size_t x0ne_session_position(const x0ne_session* s);
+/* Session::step (engine.rs:1159-1178). */
+x0ne_status x0ne_session_step(x0ne_session* s, uint32_t token);
+/* Session::finish (engine.rs:1181-1184): zeroes client bytes, frees the session. */
+x0ne_status x0ne_session_finish(x0ne_session* s);
+/* Drop for Session (engine.rs:1346-1353): scrubs, frees. */
+void x0ne_session_drop(x0ne_session* s);
+/* Session::into_greedy_ahead (engine.rs:1199-1243): consumes the session (freed even on error;
+   a failure then scrubs, as the reference's drop does). ahead in 1..=15. */
+x0ne_status x0ne_session_into_greedy(x0ne_session* s, size_t max_tokens, size_t ahead, x0ne_greedy** out);
+/* Greedy::next_token / taken / position / finish (engine.rs:1250-1344). */
+x0ne_status x0ne_greedy_next(x0ne_greedy* g, uint32_t* token);
+size_t x0ne_greedy_taken(const x0ne_greedy* g);
+size_t x0ne_greedy_position(const x0ne_greedy* g);
+x0ne_status x0ne_greedy_finish(x0ne_greedy* g);
+void x0ne_greedy_drop(x0ne_greedy* g);
+
+/* Engine::greedy_timed (engine.rs:1026-1038): n greedy tokens after prompt, with the wall time
+   (seconds from the call) each was back on the host. times may be NULL (Engine::greedy). */
+x0ne_status x0ne_engine_greedy_timed(x0ne_engine* e, const uint32_t* prompt, size_t n_prompt, size_t n,
+                                     uint32_t* tokens, double* times);
+/* Engine::greedy_with_last_logits (engine.rs:1042-1063): logits holds vocab_size floats. */
+x0ne_status x0ne_engine_greedy_with_last_logits(x0ne_engine* e, const uint32_t* prompt, size_t n_prompt, size_t n,
+                                                uint32_t* tokens, float* logits);
+
+/* Route (engine.rs:44-48) and DecodeMode (engine.rs:51-55). */
+typedef enum { X0NE_ROUTE_PREFILL = 0, X0NE_ROUTE_DECODE = 1 } x0ne_route;
+typedef enum { X0NE_DECODE_EAGER = 0, X0NE_DECODE_GRAPH = 1 } x0ne_decode_mode;
+x0ne_status x0ne_engine_set_decode_mode(x0ne_engine* e, uint32_t mode);
+uint32_t x0ne_engine_decode_mode(const x0ne_engine* e);
+
+/* Engine::logits_at (engine.rs:1012-1020): teacher-forced f32 logits at `positions` of ids,
+   rows[k * vocab ..] for positions[k]. */
+x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids, size_t n, const size_t* positions,
+                                  size_t n_positions, uint32_t route, float* rows);
+
+/* Engine::describe, graph_nodes, splits, counts, client_data_is_zero, host_buffers_are_zero
+   (engine.rs:563-670). */
+x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, size_t len);
+size_t x0ne_engine_graph_nodes(const x0ne_engine* e);
+uint32_t x0ne_engine_splits(const x0ne_engine* e);
+x0ne_status x0ne_engine_counts(const x0ne_engine* e, x0ne_counts* out);
+x0ne_status x0ne_engine_client_data_is_zero(const x0ne_engine* e, int* out);
+int x0ne_engine_host_buffers_are_zero(const x0ne_engine* e);
+uint64_t x0ne_engine_max_ctx(const x0ne_engine* e);
+/* The engine's arena, for tests that read a buffer back (KV pages, residual). Not owned. */
+const x0ne_arena* x0ne_engine_arena(const x0ne_engine* e);
+/* Physical page of logical page i (this build's paged KV arena). */
+x0ne_status x0ne_engine_page(const x0ne_engine* e, uint64_t i, uint32_t* out);
+
+/* The reference's constants (engine.rs:67-79; kernels/src/lib.rs:135-144). */
+#define X0NE_GREEDY_AHEAD 2
+#define X0NE_GREEDY_AHEAD_MAX 15
+#define X0NE_HEAD_DIM_C 128
+#define X0NE_SPLIT_STATE_C 132
+#define X0NE_PAGE_C 16
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,239 @@
+"""The engine on small models built in memory, against the CPU oracle's forward and against
+itself: the counterpart of x0ne-core/oracle/tests/gpu_engine.rs.
+
+Bit for bit where the reference's own suite asks it: the same request twice, graph against
+eager, the device's greedy tokens against the host's, the synthetic weights drawn on the device
+against the oracle's generator. Within the model-level tolerance (logits within 0.05 of the row's
+largest magnitude, KL <= 0.02, gpu_engine.rs:29-32) against the oracle, with the greedy tokens
+equal to the oracle's up to the first position whose top-2 margin the tolerance could flip."""
+import json
+
+import numpy as np
+import pytest
+
+from common import (LOGITS_ATOL_OF_MAX, LOGITS_KL, O, reference_tensors, safetensors_bytes, tiny, top_two,
+                    wide, worst_ratio)
+
+pytestmark = pytest.mark.gpu
+
+
+class Fixture:
+    def __init__(self, cfg, seed):
+        self.cfg = cfg
+        self.tensors = reference_tensors(cfg, seed)
+        self.file = safetensors_bytes(self.tensors)
+        self.model = O.Model(cfg, weights_bf16=True)
+        for name, (_, bits) in self.tensors.items():
+            self.model.set(name, bits)
+
+    def engine(self, max_ctx, page_seed=7):
+        from x0ne_core import Engine, EngineOptions
+        return Engine.load_from(self.cfg.to_json(), {"model.safetensors": self.file},
+                                EngineOptions(max_ctx=max_ctx, page_seed=page_seed))
+
+    def tokens(self, seed, n):
+        return O.Rng(seed).tokens(n, self.cfg.vocab)
+
+
+def assert_logits(what, got, want):
+    scale = float(np.abs(want).max())
+    atol = LOGITS_ATOL_OF_MAX * scale
+    r, at = worst_ratio(got, want, atol, 0.0)
+    kl = O.kl(want, got)
+    exact = bool((np.asarray(got, np.float32).view(np.uint32) == np.asarray(want, np.float32).view(np.uint32)).all())
+    print(f"MEASURE {what}: worst logit ratio {r:.5f} of {atol:.4f}, KL {kl:.3e}, bit-equal {exact}")
+    assert r <= 1.0, f"{what}: logit {at}: got {got[at]} want {want[at]}"
+    assert kl <= LOGITS_KL, f"{what}: KL {kl}"
+    first, second = top_two(want)
+    if first - second > 2 * atol:
+        assert O.argmax(got) == O.argmax(want), f"{what}: argmax"
+
+
+FIXTURES = [("1 layer 2/1", lambda: Fixture(tiny(1, 2, 1, False), 1)),
+            ("2 layers 4/2", lambda: Fixture(tiny(2, 4, 2, False), 2)),
+            ("3 layers 16/8 tied", lambda: Fixture(wide(), 3))]
+
+
+@pytest.mark.parametrize("name,make", FIXTURES, ids=[f[0] for f in FIXTURES])
+def test_every_route_gives_the_oracle_logits_at_every_position(name, make):
+    from x0ne_core import DecodeMode, Route
+    f = make()
+    e = f.engine(256)
+    ids = f.tokens(11, 40)
+    want = f.model.logits(ids)
+    positions = list(range(len(ids)))
+    rows = {}
+    for mode in [DecodeMode.GRAPH, DecodeMode.EAGER]:
+        e.set_decode_mode(mode)
+        for route in [Route.PREFILL, Route.DECODE]:
+            got = e.logits_at(ids, positions, route)
+            rows[(mode, route)] = got
+            for p in positions:
+                assert_logits(f"{name} {mode.name} {route.name} pos {p}", got[p], want[p])
+            assert e.client_data_is_zero() and e.host_buffers_are_zero()
+    base = rows[(DecodeMode.GRAPH, Route.DECODE)]
+    for key, got in rows.items():
+        for p in positions:
+            assert (got[p].view(np.uint32) == base[p].view(np.uint32)).all(), f"{name} {key} pos {p}: graph = eager"
+    print(f"MEASURE {name}: {e.describe()}")
+
+
+def test_the_same_request_twice_gives_the_same_bits():
+    f = Fixture(wide(), 4)
+    e = f.engine(128)
+    ids = f.tokens(12, 30)
+    a = e.logits_at(ids, [0, 15, 29])
+    g1 = e.greedy(ids[:10], 20)
+    b = e.logits_at(ids, [0, 15, 29])
+    g2 = e.greedy(ids[:10], 20)
+    for x, y in zip(a, b):
+        assert (x.view(np.uint32) == y.view(np.uint32)).all()
+    assert (g1 == g2).all()
+    assert e.client_data_is_zero() and e.host_buffers_are_zero()
+
+
+@pytest.mark.parametrize("which", [0, 1])
+def test_greedy_on_the_device_is_greedy_on_the_host(which):
+    from x0ne_core import FormatError, GREEDY_AHEAD_MAX
+    f = [Fixture(tiny(2, 4, 2, False), 8), Fixture(wide(), 9)][which]
+    e = f.engine(256)
+    for prompt_len, n in [(1, 1), (1, 40), (17, 2), (30, 100), (150, 57)]:
+        prompt = f.tokens(16 + prompt_len, prompt_len)
+        engine = e.greedy(prompt, n)
+        assert engine.size == n
+        host = []
+        s = e.session(prompt)
+        for i in range(n):
+            t = O.argmax(s.logits())
+            host.append(t)
+            if i + 1 < n:
+                s.step(t)
+        s.finish()
+        assert host == engine.tolist(), f"prompt {prompt_len}, {n} tokens: host greedy against the engine's"
+        for ahead in [1, 2, 3, GREEDY_AHEAD_MAX]:
+            g = e.session(prompt).into_greedy_ahead(n, ahead)
+            device = []
+            for i in range(n):
+                device.append(g.next_token())
+                assert g.taken() == i + 1
+                assert g.position() < prompt_len + n
+                assert g.position() <= prompt_len + i + ahead
+            with pytest.raises(FormatError):
+                g.next_token()
+            g.finish()
+            assert device == engine.tolist(), f"{ahead} ahead"
+            assert e.client_data_is_zero() and e.host_buffers_are_zero()
+        # The oracle, until its choice is within the tolerance of another.
+        f.model.reset()
+        logits = f.model.extend(prompt)
+        compared = 0
+        for i, t in enumerate(engine):
+            scale = float(np.abs(logits).max())
+            first, second = top_two(logits)
+            if first - second <= 2 * LOGITS_ATOL_OF_MAX * scale:
+                break
+            assert t == O.argmax(logits), f"prompt {prompt_len}: token {i} against the oracle"
+            compared += 1
+            if i + 1 < n:
+                logits = f.model.step(int(t))
+        print(f"MEASURE greedy prompt {prompt_len}: compared {compared} of {n} tokens with the oracle")
+
+
+def test_session_refusals_and_scrub():
+    from x0ne_core import FormatError
+    f = Fixture(tiny(1, 2, 1, False), 5)
+    e = f.engine(64)
+    with pytest.raises(FormatError):
+        e.session([])
+    with pytest.raises(FormatError):
+        e.session([f.cfg.vocab])
+    with pytest.raises(FormatError):
+        e.session(list(range(65)))
+    s = e.session([1, 2, 3])
+    with pytest.raises(FormatError):
+        e.session([1])  # one session at a time
+    with pytest.raises(FormatError):
+        s.step(f.cfg.vocab)
+    assert s.position() == 3
+    s.step(4)
+    assert s.position() == 4
+    assert not e.client_data_is_zero()
+    s.finish()
+    assert e.client_data_is_zero() and e.host_buffers_are_zero()
+    s = e.session(list(range(60)))
+    for t in range(4):
+        s.step(t)
+    with pytest.raises(FormatError):
+        s.step(1)  # max_ctx
+    s.finish()
+    with pytest.raises(FormatError):
+        e.greedy(list(range(60)), 6)  # 60 + 6 - 1 > 64
+    assert e.greedy(list(range(60)), 5).size == 5
+
+
+def synthetic_config(layers=2, hidden=256, inter=512, q=4, kv=2, vocab=1000, tied=False):
+    return tiny(layers, q, kv, tied, hidden=hidden, inter=inter, vocab=vocab, max_pos=4096)
+
+
+def test_synthetic_weights_are_the_oracles_draws_bit_for_bit():
+    """The device initialiser (init.hip) and the oracle's generator draw the same bf16 bits."""
+    from x0ne_core import Engine, EngineOptions
+    cfg = synthetic_config()
+    e = Engine.load_synthetic(cfg.to_json(), 0, 0.02, EngineOptions(max_ctx=64))
+    a = e.arena()
+    slices = {}
+    for label, _, sl in a.slices():
+        slices.setdefault(label, []).append(sl)
+    names = [n for n, _ in cfg.tensors()]
+    sizes = dict(cfg.tensors())
+
+    def draws(name):
+        i = names.index(name)
+        if name.endswith("norm.weight") or "layernorm" in name:
+            return np.full(sizes[name], 0x3F80, np.uint16)
+        return O.normal_bf16(O.tensor_key(0, i), 0, sizes[name], 0.02)
+
+    def read(label, k):
+        sl = slices[label][k]
+        return a.read_array(sl, 0, sl.len // 2, np.uint16)
+
+    got = read("embed", 0)
+    assert (got == draws("model.embed_tokens.weight")).all(), "embedding"
+    for l in range(cfg.layers):
+        p = f"model.layers.{l}."
+        qkv = np.concatenate([draws(p + "self_attn.q_proj.weight"), draws(p + "self_attn.k_proj.weight"),
+                              draws(p + "self_attn.v_proj.weight")])
+        assert (read("qkv", l) == qkv).all(), f"layer {l} qkv"
+        assert (read("o", l) == draws(p + "self_attn.o_proj.weight")).all(), f"layer {l} o"
+        gu = np.concatenate([draws(p + "mlp.gate_proj.weight"), draws(p + "mlp.up_proj.weight")])
+        assert (read("gate_up", l) == gu).all(), f"layer {l} gate_up"
+        assert (read("down", l) == draws(p + "mlp.down_proj.weight")).all(), f"layer {l} down"
+        assert (read("input_norm", l) == 0x3F80).all() and (read("post_norm", l) == 0x3F80).all()
+    assert (read("lm_head", 0) == draws("lm_head.weight")).all(), "lm_head"
+
+
+def test_synthetic_greedy_against_the_oracle():
+    """N(0, 0.02) weights drawn on both sides from seed 0: the device's greedy tokens against the
+    oracle's, with the oracle's top-2 margins printed."""
+    from x0ne_core import Engine, EngineOptions
+    cfg = synthetic_config(layers=3, hidden=512, inter=1536, q=8, kv=4, vocab=4096)
+    e = Engine.load_synthetic(cfg.to_json(), 0, 0.02, EngineOptions(max_ctx=256, page_seed=3))
+    m = O.Model(cfg, weights_bf16=True)
+    m.init_normal(0, 0.02)
+    prompt = O.Rng(0).tokens(20, cfg.vocab)
+    n = 64
+    dev = e.greedy(prompt, n)
+    want, margins = m.greedy(prompt, n)
+    agree = 0
+    for a, b in zip(dev, want):
+        if a != b:
+            break
+        agree += 1
+    print(f"MEASURE synthetic greedy: {agree} of {n} tokens equal to the oracle's; smallest margin "
+          f"{margins[:max(agree, 1)].min():.3e}; first mismatch margin {margins[agree] if agree < n else None}")
+    logits_dev = e.logits_at(np.concatenate([prompt, dev[:-1]]), [19, 40, 82])
+    m.reset()
+    full = m.logits(np.concatenate([prompt, dev[:-1]]))
+    for p, row in zip([19, 40, 82], logits_dev):
+        assert_logits(f"synthetic pos {p}", row, full[p])
+    assert agree == n or margins[agree] < 2 * LOGITS_ATOL_OF_MAX * float(np.abs(full[19 + agree]).max())

@@ -1,0 +1,336 @@
+"""Every kernel against the CPU oracle on random shapes and seeds and at the edges, through the
+C ABI (x0ne_core.ops.Kernels): the counterpart of x0ne-core/oracle/tests/gpu_kernels.rs.
+
+Tolerances are the reference's (common/mod.rs:98-107): a bf16 result within 2^-7 of the
+oracle, an f32 accumulation within 1e-5 of the sum of its terms' magnitudes, an attention
+within 2^-7 of the largest V, a rotation within 1e-3 of the largest value. What a kernel copies
+is compared bit for bit, and so are KV-slot indexing (a sentinel-filled paged cache keeps every
+byte but the written rows) and the argmax."""
+import numpy as np
+import pytest
+
+from common import (ATTENTION_ATOL_OF_VMAX, BF16_ATOL, BF16_RTOL, F32_RTOL, ROPE_ATOL_OF_XMAX, O, assert_close,
+                    bf16_bits, bf16_vals, bf16s_with_edges, bits_f32, max_abs)
+
+pytestmark = pytest.mark.gpu
+
+
+def H(q, kv):
+    from x0ne_core.ops import Heads
+    return Heads(q, kv)
+
+
+def test_probe_and_launch_checks(kernels):
+    """The build path end to end (probe.cu) and the launch argument check (gpu.rs:317-333)."""
+    from x0ne_core import Arena, Arg, Class, GpuError
+    a = Arena()
+    s = a.alloc("out", 1000 * 4, Class.CLIENT_DATA)
+    a.freeze(kernels.gpu)
+    kernels.gpu.launch("x0ne_probe_iota_u32", 4, 256, [Arg.ptr(a.ptr(s)), Arg.u32(1000)])
+    kernels.gpu.sync()
+    assert (a.read_array(s, 0, 1000, np.uint32) == np.arange(1000)).all()
+    with pytest.raises(GpuError, match="argument 1"):
+        kernels.gpu.launch("x0ne_probe_iota_u32", 4, 256, [Arg.ptr(a.ptr(s)), Arg.f32(1.0)])
+    with pytest.raises(GpuError):
+        kernels.gpu.launch("x0ne_probe_iota_u32", 4, 256, [Arg.ptr(a.ptr(s))])
+    with pytest.raises(GpuError):
+        kernels.gpu.launch("x0ne_no_such_kernel", 1, 64, [])
+    print("MEASURE", kernels.gpu.describe())
+
+
+def test_embedding_copies_the_row_bit_for_bit_and_zeroes_a_token_outside(kernels):
+    rng = O.Rng(1)
+    for hidden in [8, 16, 64, 1024, 4096]:
+        for vocab in [1, 2, 7, 300]:
+            raw = np.array([rng.next_u64() & 0xFFFF for _ in range(vocab * hidden)], np.uint16)
+            table = bf16_vals(raw)
+            for token in [0, vocab - 1, rng.below(vocab), vocab, vocab + 1, 0xFFFFFFFF]:
+                got = kernels.embedding(raw, hidden, token)
+                want = bf16_bits(O.embedding(table, hidden, token))
+                # NaN payloads are copied as they are: compare bits of the copy with the table's.
+                if token < vocab:
+                    assert (got == raw[token * hidden:(token + 1) * hidden]).all(), (hidden, vocab, token)
+                else:
+                    assert (got == want).all() and (got == 0).all(), (hidden, vocab, token)
+    from x0ne_core import FormatError
+    for hidden in [0, 4, 12]:
+        with pytest.raises(FormatError):
+            kernels.embedding(np.zeros(24, np.uint16), hidden, 0)
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_add_rmsnorm_is_the_oracle_on_random_rows(kernels, seed):
+    rng = O.Rng(100 + seed)
+    h = rng.pick([1, 2, 7, 8, 64, 255, 256, 257, 1024, 4096, 5120])
+    scale = rng.pick([1e-3, 1.0, 30.0, 1e4])
+    residual = rng.f32s(h, scale)
+    x = bf16s_with_edges(rng, h, scale)
+    w = rng.bf16s(h, 2.0)
+    eps = rng.pick([1e-6, 1e-5])
+    r, out = kernels.add_rmsnorm(residual, bf16_bits(x), bf16_bits(w), eps)
+    want_r, want = O.add_rmsnorm(residual, x, w, eps)
+    assert (bits_f32(r) == bits_f32(want_r)).all(), "the residual is one f32 addition per value"
+    assert_close(f"add_rmsnorm seed {seed} h {h}", bf16_vals(out), want, BF16_ATOL, BF16_RTOL + F32_RTOL)
+    # Computed in f64 like the oracle: the bf16 values are the oracle's rounded, but for a value
+    # whose f64 lies on a rounding boundary.
+    same = (out == bf16_bits(want)).mean()
+    print(f"MEASURE add_rmsnorm seed {seed}: {same:.6f} of the values bit-equal to the rounded oracle")
+
+
+def test_add_rmsnorm_on_zero_denormal_and_non_finite_rows(kernels):
+    h = 64
+    w = np.ones(h, np.float32)
+    def run(residual, x):
+        r, out = kernels.add_rmsnorm(residual, bf16_bits(x), bf16_bits(w), 1e-6)
+        want_r, want = O.add_rmsnorm(residual, x, w, 1e-6)
+        canon = lambda v: np.where(np.isnan(v), np.float32(np.nan), v).view(np.uint32)
+        assert (canon(r) == canon(want_r)).all()
+        return bf16_vals(out), want
+    got, want = run(np.zeros(h, np.float32), np.zeros(h, np.float32))
+    assert (got == want).all(), "a zero row stays zero"
+    tiny = bf16_vals(np.full(h, 1, np.uint16))
+    got, want = run(np.zeros(h, np.float32), tiny)
+    assert_close("denormal row", got, want, 1e-30, BF16_RTOL + F32_RTOL)
+    for special in [np.nan, np.inf, -np.inf]:
+        x = np.ones(h, np.float32)
+        x[17] = special
+        got, want = run(np.full(h, 0.5, np.float32), x)
+        assert (np.isnan(got) == np.isnan(want)).all(), special
+        fin = ~np.isnan(want)
+        assert (np.abs(got[fin] - want[fin]) <= 1e-6).all(), special
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_qk_norm_rope_is_the_oracle_and_writes_one_paged_slot(kernels, seed):
+    from x0ne_core.ops import CacheAt, inv_freq
+    rng = O.Rng(200 + seed)
+    kv = rng.pick([1, 2, 4, 8])
+    h = H(kv * rng.pick([1, 2, 4]), kv)
+    layers = rng.range(1, 3)
+    max_ctx = rng.pick([1, 2, 17, 64, 513])
+    pos = rng.pick([0, max_ctx - 1, rng.below(max_ctx)])
+    at = CacheAt(layers, max_ctx, rng.below(layers), pos)
+    theta = rng.pick([1e4, 1e6])
+    qkv = bf16s_with_edges(rng, h.q_dim + 2 * h.kv_dim, 8.0)
+    qn, kn = rng.bf16s(128, 2.0), rng.bf16s(128, 2.0)
+    # Shuffled pages in a pool larger than the sequence needs.
+    pages = (max_ctx + 15) // 16
+    pool = pages + 3
+    page_of = [int(p) for p in np.random.default_rng(seed).permutation(pool)[:pages]]
+    out = kernels.qk_norm_rope_kv_write(bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), h, theta, 1e-6, at,
+                                        page_of=page_of, pool=pool)
+    q, k, v = O.qk_norm_rope(qkv, qn, kn, inv_freq(128, theta), h.q_heads, h.kv_heads, 128, pos, 1e-6)
+    what = f"seed {seed} {h} {at}"
+    assert out.rest_untouched, f"{what}: a cache byte outside the slot was written"
+    assert (out.v_row == bf16_bits(v)).all(), f"{what}: v is copied"
+    for name, got, want in [("q", out.q, q), ("k", out.k_row, k)]:
+        assert_close(f"{what} {name}", bf16_vals(got), want, ROPE_ATOL_OF_XMAX * max_abs(want) + BF16_ATOL, BF16_RTOL)
+
+
+def test_rope_far_into_a_long_context(kernels):
+    """The angle is an f32 product, here as on the device (gpu_kernels.rs:263-292)."""
+    from x0ne_core.ops import CacheAt, inv_freq
+    h = H(2, 1)
+    rng = O.Rng(299)
+    qkv = rng.bf16s(h.q_dim + 2 * h.kv_dim, 4.0)
+    ones = np.ones(128, np.float32)
+    for pos in [4095, 32767, 131071]:
+        out = kernels.qk_norm_rope_kv_write(bf16_bits(qkv), bf16_bits(ones), bf16_bits(ones), h, 1e6, 1e-6,
+                                            CacheAt(1, pos + 1, 0, pos))
+        q, _, _ = O.qk_norm_rope(qkv, ones, ones, inv_freq(128, 1e6), 2, 1, 128, pos, 1e-6)
+        assert_close(f"rope at {pos}", bf16_vals(out.q), q, ROPE_ATOL_OF_XMAX * max_abs(q), BF16_RTOL)
+        assert out.rest_untouched
+
+
+def assert_gemv(what, got, want, magnitude, rounded):
+    bound = F32_RTOL * magnitude + (BF16_RTOL * np.abs(want).astype(np.float64) + BF16_ATOL if rounded else 1e-30)
+    r = np.abs(got.astype(np.float64) - want.astype(np.float64)) / bound
+    print(f"MEASURE {what}: worst ratio {r.max():.4f}")
+    assert (r <= 1.0).all(), f"{what}: row {int(np.argmax(r))}"
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_gemv_is_the_oracle_on_random_shapes(kernels, seed):
+    rng = O.Rng(300 + seed)
+    rows = rng.pick([1, 2, 3, 8, 127, 1024, 2049])
+    cols = rng.pick([1, 2, 8, 9, 64, 1000, 1024, 4096, 12288])
+    scale = rng.pick([1e-2, 1.0, 50.0])
+    w = bf16s_with_edges(rng, rows * cols, scale)
+    x = bf16s_with_edges(rng, cols, scale)
+    want = O.gemv(w, rows, cols, x)
+    mag = O.gemv_magnitude(w, rows, cols, x)
+    what = f"gemv seed {seed} {rows}x{cols}"
+    f = kernels.gemv_f32_out(bf16_bits(w), rows, cols, bf16_bits(x))
+    assert_gemv(f"{what} f32", f, want, mag, False)
+    b = kernels.gemv_bf16_out(bf16_bits(w), rows, cols, bf16_bits(x))
+    assert_gemv(f"{what} bf16", bf16_vals(b), want, mag, True)
+    # One accumulation, two stores: the bf16 output is the f32 output rounded.
+    assert (b == bf16_bits(f)).all(), what
+
+
+def test_gemv_carries_non_finite_values_to_the_rows_that_read_them(kernels):
+    rows, cols = 16, 64
+    rng = O.Rng(399)
+    w = rng.bf16s(rows * cols, 1.0)
+    for r in range(8):
+        w[r * cols + 5] = 0.0
+    x = rng.bf16s(cols, 1.0)
+    x[5] = np.inf
+    got = kernels.gemv_f32_out(bf16_bits(w), rows, cols, bf16_bits(x))
+    want = O.gemv(w, rows, cols, x)
+    assert (np.isfinite(got) == np.isfinite(want)).all()
+    assert (np.isnan(got) == np.isnan(want)).all()
+
+
+GEOMETRIES = [(1, 1), (2, 1), (4, 2), (16, 8), (32, 8), (40, 8), (64, 8)]
+CTXS = [1, 2, 3, 15, 16, 17, 63, 64, 65, 127, 128, 129, 255, 257, 511, 513, 1000, 2048, 4097]
+
+
+def attention_inputs(rng, ctx, h, scale):
+    return (rng.bf16s(h.q_dim, scale), rng.bf16s(ctx * h.kv_dim, scale), bf16s_with_edges(rng, ctx * h.kv_dim, 4.0))
+
+
+@pytest.mark.parametrize("qh,kvh", GEOMETRIES)
+def test_decode_attention_is_the_oracle_around_every_boundary(kernels, qh, kvh):
+    """Per-head, split-K with each merge and P in {1, 4, 16, the plan's}, over shuffled pages,
+    against the oracle at contexts around the page (16), the tile (64) and larger."""
+    h = H(qh, kvh)
+    plan = kernels.split_plan(h)
+    print(f"MEASURE {qh}/{kvh} heads: P {plan.splits} grouped {plan.grouped} per CU {plan.per_cu}")
+    rng = O.Rng(400 + qh)
+    for ctx in CTXS:
+        for scale in [0.5, 0.02]:
+            q, k, v = attention_inputs(rng, ctx, h, scale * np.sqrt(128))
+            want = O.attention_decode(q, k, v, ctx, qh, kvh)
+            atol = ATTENTION_ATOL_OF_VMAX * max_abs(v)
+            what = f"attention {qh}/{kvh} ctx {ctx} scale {scale}"
+            qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+            pages = (ctx + 15) // 16
+            page_of = [int(p) for p in np.random.default_rng(ctx).permutation(pages + 2)[:pages]]
+            per_head = bf16_vals(kernels.attention_decode(qb, kb, vb, ctx, h, page_of=page_of))
+            assert_close(f"{what} per-head", per_head, want, atol, 0.0)
+            for splits in [1, 4, 16, None]:
+                split = kernels.attention_decode_split(qb, kb, vb, ctx, h, last_block=False, splits=splits,
+                                                       page_of=page_of)
+                assert_close(f"{what} split P {splits}", bf16_vals(split), want, atol, 0.0)
+                if plan.grouped:
+                    last = kernels.attention_decode_split(qb, kb, vb, ctx, h, last_block=True, splits=splits,
+                                                          page_of=page_of)
+                    assert (last == split).all(), f"{what} P {splits}: the two merges give the same bits"
+                again = kernels.attention_decode_split(qb, kb, vb, ctx, h, last_block=False, splits=splits,
+                                                       page_of=page_of)
+                assert (again == split).all(), f"{what}: split-K is not deterministic"
+
+
+def test_decode_attention_on_one_key_a_dominant_key_and_equal_keys(kernels):
+    h = H(4, 2)
+    rng = O.Rng(450)
+    q = rng.bf16s(h.q_dim, 4.0)
+    v = rng.bf16s(300 * h.kv_dim, 4.0)
+    kk = rng.bf16s(300 * h.kv_dim, 4.0)
+    for split in [False, True]:
+        def run(kk_, v_, ctx):
+            f = kernels.attention_decode_split if split else kernels.attention_decode
+            return bf16_vals(f(bf16_bits(q), bf16_bits(kk_), bf16_bits(v_), ctx, h))
+        one = run(kk, v, 1)
+        for head in range(4):
+            kh = head // 2
+            assert (bf16_bits(one[head * 128:(head + 1) * 128]) == bf16_bits(v[kh * 128:(kh + 1) * 128])).all()
+        dom = kk.copy()
+        for kh in range(2):
+            dom[137 * h.kv_dim + kh * 128:137 * h.kv_dim + (kh + 1) * 128] = O.bf16_round(
+                q[kh * 256:kh * 256 + 128] * 16.0)
+        assert_close(f"dominant key split {split}", run(dom, v, 300), O.attention_decode(q, dom, v, 300, 4, 2),
+                     ATTENTION_ATOL_OF_VMAX * 4.0, 0.0)
+        same = np.tile(kk[:h.kv_dim], 300)
+        assert_close(f"equal keys split {split}", run(same, v, 300), O.attention_decode(q, same, v, 300, 4, 2),
+                     ATTENTION_ATOL_OF_VMAX * 4.0, 0.0)
+    from x0ne_core import FormatError
+    with pytest.raises(FormatError):
+        kernels.attention_decode(bf16_bits(q), bf16_bits(kk), bf16_bits(v), 0, h)
+    with pytest.raises(FormatError):
+        kernels.attention_decode(bf16_bits(q), bf16_bits(kk), bf16_bits(v), 301, h)
+
+
+@pytest.mark.parametrize("qh,kvh", [(2, 1), (4, 2), (16, 8)])
+def test_prefill_attention_is_the_oracle_whole_and_from_a_chunk_boundary(kernels, qh, kvh):
+    h = H(qh, kvh)
+    rng = O.Rng(500 + qh)
+    for t in [1, 2, 63, 64, 65, 511, 513, 1025]:
+        q = rng.bf16s(t * h.q_dim, 0.3 * np.sqrt(128))
+        k = rng.bf16s(t * h.kv_dim, 0.3 * np.sqrt(128))
+        v = bf16s_with_edges(rng, t * h.kv_dim, 4.0)
+        atol = ATTENTION_ATOL_OF_VMAX * max_abs(v)
+        rows = sorted(set([0, t - 1, t // 2, rng.below(t)]))
+        want = O.attention_rows(q, k, v, 0, qh, kvh, 128, rows)
+        got = kernels.attention_prefill_rows(bf16_bits(q), bf16_bits(k), bf16_bits(v), t, h, rows)
+        for r, g, w in zip(rows, got, want):
+            assert_close(f"prefill {qh}/{kvh} t {t} row {r}", bf16_vals(g), w, atol, 0.0)
+        for pos0 in sorted(set([0, 1, t // 2, t - 1])):
+            if pos0 >= t:
+                continue
+            tail = list(range(0, t - pos0, max(1, (t - pos0) // 5)))
+            got = kernels.attention_prefill_at(bf16_bits(q[pos0 * h.q_dim:]), bf16_bits(k), bf16_bits(v), t, pos0,
+                                               h, tail)
+            want = O.attention_rows(q[pos0 * h.q_dim:], k, v, pos0, qh, kvh, 128, tail)
+            for r, g, w in zip(tail, got, want):
+                assert_close(f"prefill at {pos0} t {t} row {r}", bf16_vals(g), w, atol, 0.0)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_swiglu_is_the_oracle(kernels, seed):
+    rng = O.Rng(600 + seed)
+    inter = rng.pick([1, 2, 7, 8, 255, 256, 3072, 12288])
+    scale = rng.pick([1.0, 8.0, 40.0, 200.0])
+    gu = bf16s_with_edges(rng, 2 * inter, scale)
+    got = bf16_vals(kernels.swiglu(bf16_bits(gu)))
+    assert_close(f"swiglu seed {seed} inter {inter}", got, O.swiglu(gu), BF16_ATOL, BF16_RTOL)
+    rows = rng.pick([1, 2, 5])
+    many = rng.bf16s(rows * 2 * min(inter, 256), 8.0)
+    got = bf16_vals(kernels.swiglu_rows(bf16_bits(many), rows))
+    want = np.concatenate([O.swiglu(r) for r in many.reshape(rows, -1)])
+    assert_close(f"swiglu rows seed {seed}", got, want, BF16_ATOL, BF16_RTOL)
+
+
+def test_swiglu_special_values(kernels):
+    s = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 200.0, -200.0, bf16_vals(1)[0], bf16_vals(0x7F7F)[0],
+                  bf16_vals(0xFF7F)[0]], np.float32)
+    for gate, up in [(s, np.full(s.size, 2.0, np.float32)), (np.ones(s.size, np.float32), s)]:
+        gu = np.concatenate([gate, up])
+        got = bf16_vals(kernels.swiglu(bf16_bits(gu)))
+        want = O.bf16_round(O.swiglu(gu))
+        assert (np.isnan(got) == np.isnan(want)).all()
+        fin = ~np.isnan(want)
+        assert ((got[fin] == want[fin]) | (np.abs(got[fin] - want[fin]) <= BF16_RTOL * np.abs(want[fin]) + 1e-30)).all()
+
+
+def test_argmax_is_the_first_largest_and_a_nan_row_has_none(kernels):
+    from x0ne_core import FormatError, GpuError
+    rng = O.Rng(700)
+    for rnd in range(100):
+        n = rng.pick([1, 2, 3, 63, 64, 65, 1023, 1024, 1025, 2047, 4096, 151936])
+        if rng.chance(2):
+            row = np.array([rng.below(4) - 2.0 for _ in range(min(n, 4096))] + [0.0] * max(0, n - 4096), np.float32)
+        else:
+            row = rng.f32s(n, 50.0)
+        for _ in range(rng.below(4)):
+            row[rng.below(n)] = rng.pick([0.0, -0.0, np.inf, -np.inf, np.finfo(np.float32).max,
+                                          np.finfo(np.float32).min])
+        assert kernels.argmax(row) == O.argmax(row), f"round {rnd}: {n} values"
+        for at in [0, n - 1]:
+            moved = row.copy()
+            moved[at] = np.inf
+            assert kernels.argmax(moved) == O.argmax(moved)
+        nan = row.copy()
+        nan[rng.below(n)] = np.nan
+        with pytest.raises(GpuError):
+            kernels.argmax(nan)
+    assert kernels.argmax(np.full(5, -np.inf, np.float32)) == 0
+    assert kernels.argmax(np.array([-0.0, 0.0], np.float32)) == 0
+    with pytest.raises(FormatError):
+        kernels.argmax(np.zeros(0, np.float32))
+
+
+def test_advance_adds_one(kernels):
+    for v in [0, 1, 511, 512, 131071, 2**32 - 2]:
+        assert kernels.advance(v) == v + 1

@@ -1,0 +1,77 @@
+// Device helpers for the gfx950 kernels: bf16 packing, 64-lane wavefront reductions, the KV page
+// addressing. Every reduction runs in a fixed order, so a launch is bit-reproducible.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+// Every attention and RoPE kernel is written for this head size (all Qwen3 dense models;
+// x0ne-core/kernels/cuda/common.cuh:10-12).
+#define X0NE_HEAD_DIM 128
+// Positions per KV page: a page of one layer's K (or V) plane holds [kv_heads][16][128] bf16,
+// so one kv head's 16 rows are 4 KiB contiguous.
+#define X0NE_PAGE 16
+// Split-K decode attention: keys per tile (one wavefront, 4 pages), and floats per partial
+// state: m, l, 2 unused, o[128] (the reference's SPLIT_STATE, kernels/src/lib.rs:135-144).
+#define X0NE_SPLIT_TILE 64
+#define X0NE_SPLIT_STATE (X0NE_HEAD_DIM + 4)
+
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Nearest bf16, ties to even; a NaN keeps its sign and gets the quiet bit (the reference's
+// rounding, x0ne-core/oracle/src/bf16.rs:11-20).
+__device__ __forceinline__ bf16_t f2bf(float x) {
+    uint32_t b = __float_as_uint(x);
+    if (x != x) return (bf16_t)((b >> 16) | 0x0040u);
+    uint32_t lo = b & 0xFFFFu, hi = b >> 16;
+    uint32_t up = (lo > 0x8000u) | ((lo == 0x8000u) & (hi & 1u));
+    return (bf16_t)(hi + up);
+}
+
+__device__ __forceinline__ float bf_round(float x) { return bf2f(f2bf(x)); }
+
+// ---- 64-lane reductions (xor butterflies: every lane ends with the same value) ----
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum over a block of `blockDim.x` threads (a multiple of 64, at most 1024); every thread gets
+// it. `sh` holds 16 doubles. Wave sums, then the wave sums in wave order.
+__device__ __forceinline__ double block_sum_d(double v, double* sh) {
+    v = wave_sum_d(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < nw; ++w) t += sh[w];
+    return t;
+}
+
+// ---- KV pages ----
+// A layer's K (or V) plane is [pages][kv_heads][16][128] bf16; page_table maps a sequence's
+// logical page (position / 16) to its physical page.
+__device__ __forceinline__ uint32_t kv_row(const uint32_t* __restrict__ pages, uint32_t pos, uint32_t kh,
+                                         uint32_t kv_heads) {
+    const uint32_t page = pages[pos / X0NE_PAGE];
+    return ((page * kv_heads + kh) * X0NE_PAGE + (pos % X0NE_PAGE)) * X0NE_HEAD_DIM;
+}

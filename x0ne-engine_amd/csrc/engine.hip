@@ -1,0 +1,1168 @@
+// The Qwen3 dense bf16 engine on MI355X: x0ne-core/runtime/src/engine.rs (with config.rs,
+// weights.rs and st.rs for loading), re-planned for gfx950.
+//
+// One arena, frozen at load: weights, the paged KV cache, activations, logits, split-K state.
+// The decode step reads its token and position from device memory and leaves the argmax in
+// tokens[0] and pos + 1, so it is captured once into a HIP graph and replayed per token; the
+// host receives 4 bytes per token (engine.rs:1-14, :484-501, :718-839).
+//
+// Per layer the step is 6 launches (the reference's is 10 plus cuBLAS nodes): the QKV GEMV with
+// the residual add + RMSNorm fused in front (layer 0: the embedding too), QK-norm + RoPE + the
+// paged KV write, split-K attention whose last block merges, the O GEMV, the gate/up GEMV with
+// the add + RMSNorm in front and SwiGLU behind, the down GEMV. Then the LM-head GEMV with the
+// final norm in front and the greedy argmax + position advance behind. The residual stream is
+// two f32 buffers used in turn (norm j reads buffer j % 2 and writes j + 1 % 2), so no block of
+// a GEMV reads a residual another block has already advanced.
+//
+// A prompt is fed through the same step, one position at a time (a feed kernel puts ids[i] and
+// i where the step reads them); a prefill of many rows through MFMA GEMMs is not built yet.
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+
+#include "internal.h"
+#include "json.h"
+
+using namespace x0ne;
+
+namespace {
+
+constexpr size_t RING = 16;  // engine.rs:70
+
+struct Cfg {
+    uint64_t hidden = 0, inter = 0, layers = 0, q_heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, max_pos = 0;
+    double eps = 0, theta = 0;
+    bool tied = false;
+    uint64_t q_dim() const { return q_heads * head_dim; }
+    uint64_t kv_dim() const { return kv_heads * head_dim; }
+    uint64_t qkv_rows() const { return q_dim() + 2 * kv_dim(); }
+};
+
+// ---- config.json, read strictly (config.rs:59-118) ----
+
+bool positive_u64(const Json& v, const char* key, uint64_t* out, std::string* err) {
+    const Json* f = v.get(key);
+    if (!f) {
+        *err = std::string("config.json: missing ") + key;
+        return false;
+    }
+    uint64_t n = 0;
+    if (!f->as_u64(&n) || n == 0) {
+        *err = std::string("config.json: ") + key + " is not a positive integer";
+        return false;
+    }
+    *out = n;
+    return true;
+}
+
+bool positive_f64(const Json* f, const char* key, double* out, std::string* err) {
+    if (!f) {
+        *err = std::string("config.json: missing ") + key;
+        return false;
+    }
+    if (f->kind != Json::Number || !std::isfinite(f->num) || f->num <= 0) {
+        *err = std::string("config.json: ") + key + " is not a positive number";
+        return false;
+    }
+    *out = f->num;
+    return true;
+}
+
+bool off(const Json& v, const char* key) {
+    const Json* f = v.get(key);
+    return !f || f->kind == Json::Null || (f->kind == Json::Bool && !f->b);
+}
+
+x0ne_status parse_config(const char* text, Cfg* c) {
+    if (!text) return fail(X0NE_ERR_FORMAT, "config.json: null");
+    Json v;
+    try {
+        v = parse_json(text);
+    } catch (const std::exception& ex) {
+        return fail(X0NE_ERR_FORMAT, std::string("config.json: ") + ex.what());
+    }
+    if (v.kind != Json::Object) return fail(X0NE_ERR_FORMAT, "config.json: not an object");
+    const Json* mt = v.get("model_type");
+    if (!mt) return fail(X0NE_ERR_FORMAT, "config.json: missing model_type");
+    if (mt->kind != Json::String || mt->text != "qwen3") return fail(X0NE_ERR_FORMAT, "config.json: model_type is not qwen3");
+    const Json* dt = v.get("dtype");
+    if (!dt) dt = v.get("torch_dtype");
+    if (!dt || dt->kind != Json::String || dt->text != "bfloat16")
+        return fail(X0NE_ERR_FORMAT, "config.json: dtype is not bfloat16, only bfloat16 is served");
+    const Json* act = v.get("hidden_act");
+    if (!act) return fail(X0NE_ERR_FORMAT, "config.json: missing hidden_act");
+    if (act->kind != Json::String || act->text != "silu") return fail(X0NE_ERR_FORMAT, "config.json: hidden_act is not silu");
+    for (const char* key : {"attention_bias", "use_sliding_window", "rope_scaling"})
+        if (!off(v, key)) return fail(X0NE_ERR_FORMAT, std::string("config.json: ") + key + " is set, not implemented");
+    const Json* tie = v.get("tie_word_embeddings");
+    if (tie && tie->kind != Json::Bool) return fail(X0NE_ERR_FORMAT, "config.json: tie_word_embeddings is not a boolean");
+    c->tied = tie && tie->b;
+    std::string err;
+    if (!positive_u64(v, "hidden_size", &c->hidden, &err) || !positive_u64(v, "intermediate_size", &c->inter, &err) ||
+        !positive_u64(v, "num_hidden_layers", &c->layers, &err) ||
+        !positive_u64(v, "num_attention_heads", &c->q_heads, &err) ||
+        !positive_u64(v, "num_key_value_heads", &c->kv_heads, &err) || !positive_u64(v, "head_dim", &c->head_dim, &err) ||
+        !positive_u64(v, "vocab_size", &c->vocab, &err) ||
+        !positive_u64(v, "max_position_embeddings", &c->max_pos, &err) ||
+        !positive_f64(v.get("rms_norm_eps"), "rms_norm_eps", &c->eps, &err))
+        return fail(X0NE_ERR_FORMAT, err);
+    // rope_theta at the top (the reference's reader) or in rope_parameters (transformers 5,
+    // lifted by x0ne-infer, core_backend.rs:28-55).
+    const Json* theta = v.get("rope_theta");
+    if (!theta) {
+        const Json* rp = v.get("rope_parameters");
+        if (rp) theta = rp->get("rope_theta");
+    }
+    if (!positive_f64(theta, "rope_theta", &c->theta, &err)) return fail(X0NE_ERR_FORMAT, err);
+    if (c->q_heads % c->kv_heads != 0)
+        return fail(X0NE_ERR_FORMAT, "config.json: attention heads are not a multiple of KV heads");
+    if (c->head_dim % 2 != 0) return fail(X0NE_ERR_FORMAT, "config.json: head_dim is odd, RoPE needs pairs");
+    if (c->vocab > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "config.json: vocab_size does not fit a u32 token id");
+    // Every derived size must fit in 64 bits (config.rs check_sizes).
+    const long double big = (long double)c->layers * (long double)(c->qkv_rows() * c->hidden + 3 * c->inter * c->hidden) +
+                            (long double)c->vocab * c->hidden * 2;
+    if (big > 1e18L) return fail(X0NE_ERR_FORMAT, "config.json: a derived size overflows");
+    return X0NE_OK;
+}
+
+// Limits of the kernels (engine.rs:236-289, plus this build's GEMV and KV-page limits).
+x0ne_status check_config(const Cfg& c, uint64_t max_ctx) {
+    if (c.head_dim != 128) return fail(X0NE_ERR_FORMAT, "head_dim " + std::to_string(c.head_dim) + ": kernels are built for 128");
+    if (c.hidden % 8 != 0) return fail(X0NE_ERR_FORMAT, "hidden_size is not a multiple of 8");
+    if (c.inter % 8 != 0) return fail(X0NE_ERR_FORMAT, "intermediate_size is not a multiple of 8");
+    if (max_ctx == 0 || max_ctx > c.max_pos)
+        return fail(X0NE_ERR_FORMAT, "max_ctx " + std::to_string(max_ctx) + " outside 1..=" + std::to_string(c.max_pos));
+    const uint64_t pages = (max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
+    for (uint64_t s : {c.vocab, c.hidden, 2 * c.inter, c.qkv_rows(), max_ctx * c.kv_dim(), pages * X0NE_PAGE_C * c.kv_dim()})
+        if (s > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "a dimension exceeds u32");
+    for (uint64_t cols : {c.hidden, c.q_dim(), c.inter})
+        if (cols > 16 * 256 * 8) return fail(X0NE_ERR_FORMAT, "a GEMV width exceeds 32768 columns");
+    return X0NE_OK;
+}
+
+// ---- the checkpoint's tensors (oracle/src/model.rs:63-89; weights.rs) ----
+
+enum Leaf { L_INPUT_NORM, L_Q, L_K, L_V, L_QN, L_KN, L_O, L_POST_NORM, L_GATE, L_UP, L_DOWN, L_COUNT };
+const char* LEAF_NAMES[L_COUNT] = {"input_layernorm", "self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                                   "self_attn.q_norm", "self_attn.k_norm", "self_attn.o_proj",
+                                   "post_attention_layernorm", "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"};
+
+std::vector<uint64_t> leaf_shape(const Cfg& c, int leaf) {
+    switch (leaf) {
+        case L_INPUT_NORM:
+        case L_POST_NORM: return {c.hidden};
+        case L_Q: return {c.q_dim(), c.hidden};
+        case L_K:
+        case L_V: return {c.kv_dim(), c.hidden};
+        case L_QN:
+        case L_KN: return {c.head_dim};
+        case L_O: return {c.hidden, c.q_dim()};
+        case L_GATE:
+        case L_UP: return {c.inter, c.hidden};
+        default: return {c.hidden, c.inter};
+    }
+}
+
+std::string layer_name(uint64_t l, int leaf) {
+    return "model.layers." + std::to_string(l) + "." + LEAF_NAMES[leaf] + ".weight";
+}
+
+// ---- safetensors in memory (st.rs:21-277) ----
+
+struct TensorView {
+    std::string dtype;
+    std::vector<uint64_t> shape;
+    const uint8_t* data = nullptr;
+    uint64_t len = 0;
+};
+
+x0ne_status parse_safetensors(const std::string& file, const uint8_t* bytes, uint64_t len,
+                              std::map<std::string, TensorView>* out) {
+    if (len < 8) return fail(X0NE_ERR_FORMAT, file + ": shorter than a header length");
+    uint64_t n = 0;
+    for (int i = 7; i >= 0; --i) n = (n << 8) | bytes[i];
+    if (n > len - 8 || n > (100ull << 20)) return fail(X0NE_ERR_FORMAT, file + ": header length " + std::to_string(n));
+    Json h;
+    try {
+        h = parse_json(std::string((const char*)bytes + 8, n));
+    } catch (const std::exception& ex) {
+        return fail(X0NE_ERR_FORMAT, file + ": header: " + ex.what());
+    }
+    if (h.kind != Json::Object) return fail(X0NE_ERR_FORMAT, file + ": header is not an object");
+    const uint8_t* data = bytes + 8 + n;
+    const uint64_t data_len = len - 8 - n;
+    for (const auto& f : h.fields) {
+        if (f.first == "__metadata__") continue;
+        const Json& t = f.second;
+        const Json* dt = t.get("dtype");
+        const Json* sh = t.get("shape");
+        const Json* of = t.get("data_offsets");
+        if (!dt || dt->kind != Json::String || !sh || sh->kind != Json::Array || !of || of->kind != Json::Array ||
+            of->items.size() != 2)
+            return fail(X0NE_ERR_FORMAT, file + ": " + f.first + ": malformed entry");
+        TensorView v;
+        v.dtype = dt->text;
+        uint64_t count = 1;
+        for (const auto& d : sh->items) {
+            uint64_t x = 0;
+            if (!d.as_u64(&x)) return fail(X0NE_ERR_FORMAT, file + ": " + f.first + ": bad shape");
+            if (x && count > UINT64_MAX / x) return fail(X0NE_ERR_FORMAT, file + ": " + f.first + ": shape overflows");
+            count *= x;
+            v.shape.push_back(x);
+        }
+        uint64_t b = 0, e = 0;
+        if (!of->items[0].as_u64(&b) || !of->items[1].as_u64(&e) || b > e || e > data_len)
+            return fail(X0NE_ERR_FORMAT, file + ": " + f.first + ": data offsets outside the file");
+        const uint64_t es = v.dtype == "BF16" || v.dtype == "F16" ? 2 : v.dtype == "F32" ? 4 : v.dtype == "F64" ? 8 : 0;
+        if (es && (count > UINT64_MAX / es || count * es != e - b))
+            return fail(X0NE_ERR_FORMAT, file + ": " + f.first + ": size does not match the shape");
+        v.data = data + b;
+        v.len = e - b;
+        if (out->count(f.first)) return fail(X0NE_ERR_FORMAT, f.first + ": in two files");
+        (*out)[f.first] = v;
+    }
+    return X0NE_OK;
+}
+
+// weights.rs:124-165: the exact tensor set, all BF16, every shape; a tied checkpoint may carry
+// lm_head.weight only if it equals the embedding.
+x0ne_status check_tensors(const Cfg& c, const std::map<std::string, TensorView>& t) {
+    std::map<std::string, std::vector<uint64_t>> want;
+    want["model.embed_tokens.weight"] = {c.vocab, c.hidden};
+    for (uint64_t l = 0; l < c.layers; ++l)
+        for (int leaf = 0; leaf < L_COUNT; ++leaf) want[layer_name(l, leaf)] = leaf_shape(c, leaf);
+    want["model.norm.weight"] = {c.hidden};
+    if (!c.tied) want["lm_head.weight"] = {c.vocab, c.hidden};
+    for (const auto& kv : t) {
+        if (want.count(kv.first)) continue;
+        if (c.tied && kv.first == "lm_head.weight") continue;
+        return fail(X0NE_ERR_FORMAT, kv.first + ": unexpected tensor");
+    }
+    for (const auto& w : want) {
+        auto it = t.find(w.first);
+        if (it == t.end()) return fail(X0NE_ERR_FORMAT, w.first + ": missing tensor");
+        if (it->second.dtype != "BF16") return fail(X0NE_ERR_FORMAT, w.first + ": dtype " + it->second.dtype + ", expected BF16");
+        if (it->second.shape != w.second) return fail(X0NE_ERR_FORMAT, w.first + ": shape differs from the config's");
+    }
+    if (c.tied) {
+        auto h = t.find("lm_head.weight");
+        if (h != t.end()) {
+            const auto& e = t.at("model.embed_tokens.weight");
+            if (h->second.dtype != "BF16" || h->second.shape != e.shape || h->second.len != e.len ||
+                std::memcmp(h->second.data, e.data, e.len) != 0)
+                return fail(X0NE_ERR_FORMAT, "tied config, but lm_head.weight differs from the embedding");
+        }
+    }
+    return X0NE_OK;
+}
+
+// splitmix64 output `index` of a generator seeded with `seed` (the tensor keys of the synthetic
+// checkpoint; the oracle's xo_tensor_key).
+uint64_t tensor_key(uint64_t seed, uint64_t index) {
+    uint64_t z = seed + (index + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+
+struct LayerW {
+    x0ne_slice input_norm, qkv, q_norm, k_norm, o, post_norm, gate_up, down;
+};
+
+struct x0ne_engine {
+    Cfg c;
+    uint64_t max_ctx = 0, pages = 0, page_seed = 0;
+    x0ne_gpu* gpu = nullptr;
+    x0ne_arena* arena = nullptr;
+    // weights
+    x0ne_slice embed{}, final_norm{}, lm_head{};
+    bool has_lm_head = false;
+    std::vector<LayerW> L;
+    // buffers
+    x0ne_slice inv_freq{}, page_table{}, kv{}, prompt{}, tokens{}, pos{}, residual{}, delta{}, qkv{}, q{}, attn{},
+        act{}, logits{}, head_partial{}, head_counter{}, attn_state{}, attn_counter{};
+    std::vector<uint32_t> page_of;
+    x0ne_split_plan split{};
+    uint32_t grid_qkv = 0, grid_o = 0, grid_gu = 0, grid_down = 0, grid_head = 0;
+    x0ne_graph* graph = nullptr;
+    uint32_t mode = X0NE_DECODE_GRAPH;
+    // host side (pinned)
+    uint32_t* ring = nullptr;
+    hipEvent_t ring_ev[RING] = {};
+    float* host_logits = nullptr;
+    hipEvent_t logits_ev = nullptr;
+    uint32_t* host_token = nullptr;
+    bool poisoned = false;
+    bool session_open = false;
+
+    ~x0ne_engine() {
+        if (graph) x0ne_graph_free(graph);
+        if (gpu && gpu->stream) (void)hipStreamSynchronize(gpu->stream);
+        for (auto& ev : ring_ev)
+            if (ev) (void)hipEventDestroy(ev);
+        if (logits_ev) (void)hipEventDestroy(logits_ev);
+        if (ring) (void)hipHostFree(ring);
+        if (host_logits) (void)hipHostFree(host_logits);
+        if (host_token) (void)hipHostFree(host_token);
+        if (arena) x0ne_arena_free(arena);
+        if (gpu) x0ne_gpu_free(gpu);
+    }
+    uint8_t* d(x0ne_slice s) const { return dev(arena, s); }
+    uint64_t plane_bytes() const { return pages * X0NE_PAGE_C * c.kv_dim() * 2; }
+    // K (kv = 0) or V (kv = 1) plane of layer l.
+    uint8_t* plane(uint64_t l, int kvsel) const { return d(kv) + (2 * l + kvsel) * plane_bytes(); }
+};
+
+struct x0ne_session {
+    x0ne_engine* e = nullptr;
+    size_t pos = 0;
+    bool open = true;
+    bool failed = false;
+};
+
+struct x0ne_greedy {
+    x0ne_session* s = nullptr;
+    size_t max_tokens = 0, ahead = 0, taken = 0, launched = 0;
+    uint32_t first = 0;
+};
+
+namespace {
+
+x0ne_status plan(x0ne_engine* e) {
+    x0ne_arena* a = e->arena;
+    const Cfg& c = e->c;
+    const uint32_t W = X0NE_CLASS_WEIGHTS, CD = X0NE_CLASS_CLIENT_DATA;
+    auto al = [&](const char* label, uint64_t len, uint32_t cls, x0ne_slice* s) {
+        return x0ne_arena_alloc(a, label, len, cls, s);
+    };
+    X0NE_TRY(al("embed", c.vocab * c.hidden * 2, W, &e->embed));
+    e->L.resize(c.layers);
+    for (uint64_t l = 0; l < c.layers; ++l) {
+        LayerW& w = e->L[l];
+        X0NE_TRY(al("input_norm", c.hidden * 2, W, &w.input_norm));
+        X0NE_TRY(al("qkv", c.qkv_rows() * c.hidden * 2, W, &w.qkv));
+        X0NE_TRY(al("q_norm", c.head_dim * 2, W, &w.q_norm));
+        X0NE_TRY(al("k_norm", c.head_dim * 2, W, &w.k_norm));
+        X0NE_TRY(al("o", c.hidden * c.q_dim() * 2, W, &w.o));
+        X0NE_TRY(al("post_norm", c.hidden * 2, W, &w.post_norm));
+        X0NE_TRY(al("gate_up", 2 * c.inter * c.hidden * 2, W, &w.gate_up));
+        X0NE_TRY(al("down", c.hidden * c.inter * 2, W, &w.down));
+    }
+    X0NE_TRY(al("final_norm", c.hidden * 2, W, &e->final_norm));
+    e->has_lm_head = !c.tied;
+    if (e->has_lm_head) X0NE_TRY(al("lm_head", c.vocab * c.hidden * 2, W, &e->lm_head));
+    // Engine tables, not client data: the host's f32 inverse frequencies and the page order.
+    X0NE_TRY(al("inv_freq", c.head_dim / 2 * 4, W, &e->inv_freq));
+    X0NE_TRY(al("page_table", e->pages * 4, W, &e->page_table));
+    // Client data.
+    X0NE_TRY(al("kv_cache", 2 * c.layers * e->plane_bytes(), CD, &e->kv));
+    X0NE_TRY(al("prompt", e->max_ctx * 4, CD, &e->prompt));
+    X0NE_TRY(al("tokens", 4, CD, &e->tokens));
+    X0NE_TRY(al("pos", 4, CD, &e->pos));
+    X0NE_TRY(al("residual", 2 * c.hidden * 4, CD, &e->residual));
+    X0NE_TRY(al("delta", c.hidden * 2, CD, &e->delta));
+    X0NE_TRY(al("qkv_out", c.qkv_rows() * 2, CD, &e->qkv));
+    X0NE_TRY(al("q", c.q_dim() * 2, CD, &e->q));
+    X0NE_TRY(al("attn", c.q_dim() * 2, CD, &e->attn));
+    X0NE_TRY(al("act", c.inter * 2, CD, &e->act));
+    X0NE_TRY(al("logits", c.vocab * 4, CD, &e->logits));
+    X0NE_TRY(al("head_partial", (uint64_t)e->grid_head * 3 * 4, CD, &e->head_partial));
+    X0NE_TRY(al("head_counter", 4, CD, &e->head_counter));
+    X0NE_TRY(al("attention_split_state", x0ne_split_state_bytes((uint32_t)c.q_heads, e->split.splits), CD,
+                &e->attn_state));
+    X0NE_TRY(al("attention_split_counter", c.kv_heads * 4, CD, &e->attn_counter));
+    return X0NE_OK;
+}
+
+uint32_t grid_for(const x0ne_engine* e, uint64_t groups) {
+    static const char* env = std::getenv("X0NE_GEMV_BLOCKS_PER_CU");
+    uint64_t bpc = 2;
+    if (env && std::atoi(env) > 0) bpc = (uint64_t)std::atoi(env);
+    const uint64_t cap = (uint64_t)e->gpu->cus * bpc;
+    return (uint32_t)(groups < cap ? groups : cap);
+}
+
+void plan_grids(x0ne_engine* e) {
+    const Cfg& c = e->c;
+    auto groups = [](uint64_t rows, uint32_t rps) { return (rows + rps - 1) / rps; };
+    e->grid_qkv = grid_for(e, groups(c.qkv_rows(), x0ne_gemv_rows_per_step((uint32_t)c.hidden)));
+    e->grid_o = grid_for(e, groups(c.hidden, x0ne_gemv_rows_per_step((uint32_t)c.q_dim())));
+    e->grid_gu = grid_for(e, groups(c.inter, x0ne_gemv_rows_per_step((uint32_t)c.hidden) / 2));
+    e->grid_down = grid_for(e, groups(c.hidden, x0ne_gemv_rows_per_step((uint32_t)c.inter)));
+    e->grid_head = grid_for(e, groups(c.vocab, x0ne_gemv_rows_per_step((uint32_t)c.hidden)));
+}
+
+// The launches of one decode step at the device's pos on the device's tokens[0]: forward,
+// logits, argmax into tokens[0], pos += 1. No host copy and no synchronisation, so the
+// sequence can be captured (engine.rs:495-501, :718-839).
+x0ne_status step_launches(x0ne_engine* e) {
+    const Cfg& c = e->c;
+    x0ne_gpu* g = e->gpu;
+    hipStream_t s = g->stream;
+    const uint32_t h = (uint32_t)c.hidden, qd = (uint32_t)c.q_dim(), inter = (uint32_t)c.inter;
+    const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads, maxc = (uint32_t)e->max_ctx;
+    const float eps = (float)c.eps;
+    const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));  // ops.rs:217-219
+    float* r0 = (float*)e->d(e->residual);
+    float* r1 = r0 + c.hidden;
+    const uint16_t* delta = (const uint16_t*)e->d(e->delta);
+    const uint32_t* tokens = (const uint32_t*)e->d(e->tokens);
+    uint32_t* pos = (uint32_t*)e->d(e->pos);
+    for (uint64_t l = 0; l < c.layers; ++l) {
+        const LayerW& w = e->L[l];
+        // QKV: norm 2l (reads r0, writes r1); layer 0 adds the embedding to a zero residual.
+        X0neGemv a = {};
+        a.w = (const uint16_t*)e->d(w.qkv);
+        a.res_in = r0;
+        a.res_out = r1;
+        a.delta = delta;
+        a.norm_w = (const uint16_t*)e->d(w.input_norm);
+        a.embed = (const uint16_t*)e->d(e->embed);
+        a.tokens = tokens;
+        a.vocab = (uint32_t)c.vocab;
+        a.y = e->d(e->qkv);
+        a.rows = (uint32_t)c.qkv_rows();
+        a.cols = h;
+        a.eps = eps;
+        a.prologue = l == 0 ? 2 : 1;
+        a.epilogue = 0;
+        a.grid = e->grid_qkv;
+        g->counts.launches++;
+        X0NE_HIP(x0ne_launch_gemv(a, s), "qkv gemv");
+        // QK-norm, RoPE, the K/V rows into their page.
+        g->counts.launches++;
+        hipLaunchKernelGGL(x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, 1), dim3(64), 0, s,
+                           (const bf16_t*)e->d(e->qkv), (const bf16_t*)e->d(w.q_norm), (const bf16_t*)e->d(w.k_norm),
+                           (const float*)e->d(e->inv_freq), (bf16_t*)e->d(e->q), (bf16_t*)e->plane(l, 0),
+                           (bf16_t*)e->plane(l, 1), (const uint32_t*)e->d(e->page_table), (const uint32_t*)pos, qh,
+                           kvh, maxc, eps);
+        X0NE_HIP(hipGetLastError(), "qk_norm_rope_kv_write");
+        // Split-K attention, merged by its last block when grouped.
+        X0NE_TRY(attention_split(g, e->split, e->split.grouped ? 1 : 0, e->d(e->q), e->plane(l, 0), e->plane(l, 1),
+                                 e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn), pos,
+                                 qh, kvh, maxc, scale));
+        // O projection.
+        X0neGemv o = {};
+        o.w = (const uint16_t*)e->d(w.o);
+        o.x = (const uint16_t*)e->d(e->attn);
+        o.y = e->d(e->delta);
+        o.rows = h;
+        o.cols = qd;
+        o.prologue = 0;
+        o.epilogue = 0;
+        o.grid = e->grid_o;
+        g->counts.launches++;
+        X0NE_HIP(x0ne_launch_gemv(o, s), "o gemv");
+        // gate/up: norm 2l + 1 (reads r1, writes r0), SwiGLU behind.
+        X0neGemv gu = {};
+        gu.w = (const uint16_t*)e->d(w.gate_up);
+        gu.res_in = r1;
+        gu.res_out = r0;
+        gu.delta = delta;
+        gu.norm_w = (const uint16_t*)e->d(w.post_norm);
+        gu.y = e->d(e->act);
+        gu.rows = 2 * inter;
+        gu.cols = h;
+        gu.eps = eps;
+        gu.prologue = 1;
+        gu.epilogue = 2;
+        gu.grid = e->grid_gu;
+        g->counts.launches++;
+        X0NE_HIP(x0ne_launch_gemv(gu, s), "gate_up gemv");
+        // down projection.
+        X0neGemv dn = {};
+        dn.w = (const uint16_t*)e->d(w.down);
+        dn.x = (const uint16_t*)e->d(e->act);
+        dn.y = e->d(e->delta);
+        dn.rows = h;
+        dn.cols = inter;
+        dn.prologue = 0;
+        dn.epilogue = 0;
+        dn.grid = e->grid_down;
+        g->counts.launches++;
+        X0NE_HIP(x0ne_launch_gemv(dn, s), "down gemv");
+    }
+    // Final norm 2L (reads r0), the LM head, argmax into tokens[0], pos += 1.
+    X0neGemv hd = {};
+    hd.w = (const uint16_t*)e->d(e->has_lm_head ? e->lm_head : e->embed);
+    hd.res_in = r0;
+    hd.res_out = nullptr;
+    hd.delta = delta;
+    hd.norm_w = (const uint16_t*)e->d(e->final_norm);
+    hd.y = e->d(e->logits);
+    hd.partial = (float*)e->d(e->head_partial);
+    hd.counter = (uint32_t*)e->d(e->head_counter);
+    hd.token_out = (uint32_t*)tokens;
+    hd.pos = pos;
+    hd.advance = 1;
+    hd.rows = (uint32_t)c.vocab;
+    hd.cols = h;
+    hd.eps = eps;
+    hd.prologue = 1;
+    hd.epilogue = 3;
+    hd.grid = e->grid_head;
+    g->counts.launches++;
+    X0NE_HIP(x0ne_launch_gemv(hd, s), "lm_head gemv");
+    return X0NE_OK;
+}
+
+x0ne_status run_step(x0ne_engine* e) {
+    if (e->mode == X0NE_DECODE_GRAPH) {
+        if (!e->graph) return fail(X0NE_ERR_GPU, "no decode graph captured");
+        return x0ne_gpu_launch_graph(e->gpu, e->graph);
+    }
+    return step_launches(e);
+}
+
+// Prompt token i through the step: ids[i] into tokens[0], i into pos (from the prompt buffer).
+x0ne_status feed(x0ne_engine* e, uint32_t i) {
+    e->gpu->counts.launches++;
+    hipLaunchKernelGGL(x0ne_feed_u32, dim3(1), dim3(64), 0, e->gpu->stream, (const uint32_t*)e->d(e->prompt), i,
+                       (uint32_t*)e->d(e->tokens), (uint32_t*)e->d(e->pos));
+    X0NE_HIP(hipGetLastError(), "feed");
+    return run_step(e);
+}
+
+x0ne_status put_prompt(x0ne_engine* e, const uint32_t* ids, size_t n) {
+    return x0ne_arena_write(e->arena, e->prompt, 0, ids, n * 4);
+}
+
+// The ids of a request: 1..=max_ctx of them, each inside the vocabulary (engine.rs:637-645).
+x0ne_status check_ids(const x0ne_engine* e, const uint32_t* ids, size_t n) {
+    if (n == 0 || n > e->max_ctx)
+        return fail(X0NE_ERR_FORMAT, std::to_string(n) + " tokens for max_ctx " + std::to_string(e->max_ctx));
+    for (size_t i = 0; i < n; ++i)
+        if (ids[i] >= e->c.vocab) return fail(X0NE_ERR_FORMAT, "token " + std::to_string(ids[i]) + " outside the vocabulary");
+    return X0NE_OK;
+}
+
+// Zeroes every client byte: the arena's, then the host buffers once the stream is drained. A
+// failure poisons the engine (engine.rs:453-468).
+x0ne_status scrub(x0ne_engine* e) {
+    e->poisoned = true;
+    X0NE_TRY(x0ne_arena_scrub(e->arena, nullptr));
+    if (e->host_logits) std::memset(e->host_logits, 0, e->c.vocab * 4);
+    if (e->host_token) *e->host_token = 0;
+    if (e->ring) std::memset(e->ring, 0, RING * 4);
+    e->poisoned = false;
+    return X0NE_OK;
+}
+
+// The logits row into the pinned host row: one asynchronous copy, then its event.
+x0ne_status pull_logits(x0ne_engine* e) {
+    e->gpu->counts.dtoh++;
+    X0NE_HIP(hipMemcpyAsync(e->host_logits, e->d(e->logits), e->c.vocab * 4, hipMemcpyDeviceToHost, e->gpu->stream),
+             "logits copy");
+    X0NE_HIP(hipEventRecord(e->logits_ev, e->gpu->stream), "logits event");
+    X0NE_HIP(hipEventSynchronize(e->logits_ev), "logits wait");
+    return X0NE_OK;
+}
+
+// tokens[0] into ring word j % RING, then its event.
+x0ne_status ring_fetch(x0ne_engine* e, size_t j) {
+    e->gpu->counts.dtoh++;
+    X0NE_HIP(hipMemcpyAsync(&e->ring[j % RING], e->d(e->tokens), 4, hipMemcpyDeviceToHost, e->gpu->stream),
+             "ring copy");
+    X0NE_HIP(hipEventRecord(e->ring_ev[j % RING], e->gpu->stream), "ring event");
+    return X0NE_OK;
+}
+
+x0ne_status ring_take(x0ne_engine* e, size_t j, uint32_t* out) {
+    X0NE_HIP(hipEventSynchronize(e->ring_ev[j % RING]), "ring wait");
+    *out = e->ring[j % RING];
+    return X0NE_OK;
+}
+
+// tokens[0] after the stream is drained; refused when the row had no finite maximum.
+x0ne_status read_token(x0ne_engine* e, uint32_t* out) {
+    uint32_t t = 0;
+    X0NE_TRY(x0ne_arena_read(e->arena, e->tokens, 0, &t, 4));
+    if (t >= e->c.vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
+    *out = t;
+    return X0NE_OK;
+}
+
+x0ne_status prefill(x0ne_engine* e, const uint32_t* ids, size_t n) {
+    X0NE_TRY(put_prompt(e, ids, n));
+    for (size_t i = 0; i < n; ++i) X0NE_TRY(feed(e, (uint32_t)i));
+    return X0NE_OK;
+}
+
+x0ne_status capture(x0ne_engine* e) {
+    // One eager step on zeroed client buffers (the runtime loads code lazily, which a capture
+    // must not see), then the capture of the same launches; the client bytes are zeroed after.
+    X0NE_TRY(step_launches(e));
+    X0NE_TRY(x0ne_gpu_sync(e->gpu));
+    if (e->graph) {
+        x0ne_graph_free(e->graph);
+        e->graph = nullptr;
+    }
+    X0NE_TRY(x0ne_gpu_capture_begin(e->gpu));
+    x0ne_status st = step_launches(e);
+    x0ne_graph* gr = nullptr;
+    x0ne_status st2 = x0ne_gpu_capture_end(e->gpu, &gr);
+    if (st != X0NE_OK) {
+        if (gr) x0ne_graph_free(gr);
+        return st;
+    }
+    X0NE_TRY(st2);
+    e->graph = gr;
+    return x0ne_arena_scrub(e->arena, nullptr);
+}
+
+// Seeded page order: logical page i -> physical page page_of[i] (Fisher-Yates over splitmix64),
+// or the identity for seed 0.
+void page_order(x0ne_engine* e) {
+    e->page_of.resize(e->pages);
+    for (uint64_t i = 0; i < e->pages; ++i) e->page_of[i] = (uint32_t)i;
+    if (e->page_seed == 0) return;
+    uint64_t st = e->page_seed;
+    for (uint64_t i = e->pages; i > 1; --i) {
+        st += 0x9E3779B97F4A7C15ull;
+        uint64_t z = st;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        const uint64_t j = z % i;
+        std::swap(e->page_of[i - 1], e->page_of[j]);
+    }
+}
+
+// The device, the plan, the one allocation, and the tables; weights are written by the caller.
+x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engine** out) {
+    x0ne_engine* e = new x0ne_engine();
+    e->c = c;
+    e->max_ctx = opts->max_ctx;
+    e->page_seed = opts->page_seed;
+    e->pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
+    x0ne_status st = x0ne_gpu_new(&e->gpu);
+    if (st != X0NE_OK) {
+        delete e;
+        return st;
+    }
+    auto bail = [&](x0ne_status s) {
+        delete e;
+        return s;
+    };
+    if ((st = split_plan(e->gpu, (uint32_t)c.q_heads, (uint32_t)c.kv_heads, &e->split)) != X0NE_OK) return bail(st);
+    plan_grids(e);
+    if ((st = x0ne_arena_new(&e->arena)) != X0NE_OK) return bail(st);
+    if ((st = plan(e)) != X0NE_OK) return bail(st);
+    if ((st = x0ne_arena_freeze(e->arena, e->gpu)) != X0NE_OK) return bail(st);
+    // inv_freq in f32 on the host (ops.rs:210-214), and the page table.
+    std::vector<float> inv(c.head_dim / 2);
+    for (size_t i = 0; i < inv.size(); ++i)
+        inv[i] = 1.0f / std::pow((float)c.theta, (float)(2 * i) / (float)c.head_dim);
+    if ((st = x0ne_arena_write(e->arena, e->inv_freq, 0, inv.data(), inv.size() * 4)) != X0NE_OK) return bail(st);
+    page_order(e);
+    if ((st = x0ne_arena_write(e->arena, e->page_table, 0, e->page_of.data(), e->pages * 4)) != X0NE_OK)
+        return bail(st);
+    *out = e;
+    return X0NE_OK;
+}
+
+x0ne_status build_end(x0ne_engine* e) {
+    X0NE_TRY(x0ne_arena_scrub(e->arena, nullptr));
+    X0NE_HIP(hipHostMalloc((void**)&e->ring, RING * 4, hipHostMallocDefault), "pinned ring");
+    X0NE_HIP(hipHostMalloc((void**)&e->host_logits, e->c.vocab * 4, hipHostMallocDefault), "pinned logits");
+    X0NE_HIP(hipHostMalloc((void**)&e->host_token, 4, hipHostMallocDefault), "pinned token");
+    std::memset(e->ring, 0, RING * 4);
+    std::memset(e->host_logits, 0, e->c.vocab * 4);
+    *e->host_token = 0;
+    for (auto& ev : e->ring_ev) X0NE_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "ring event");
+    X0NE_HIP(hipEventCreateWithFlags(&e->logits_ev, hipEventDisableTiming), "logits event");
+    return capture(e);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// Load
+// ---------------------------------------------------------------------------------------------
+
+extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_files, const char* const* names,
+                                             const uint8_t* const* data, const uint64_t* lens, const char* index_json,
+                                             const x0ne_engine_options* opts, x0ne_engine** out) {
+    if (!out || !opts) return fail(X0NE_ERR_FORMAT, "null argument");
+    *out = nullptr;
+    Cfg c;
+    X0NE_TRY(parse_config(config_json, &c));
+    X0NE_TRY(check_config(c, opts->max_ctx));
+    // Every format check before the device is touched.
+    std::map<std::string, TensorView> tensors;
+    std::map<std::string, std::string> file_of;
+    for (size_t i = 0; i < n_files; ++i) {
+        std::map<std::string, TensorView> one;
+        const std::string fname = names && names[i] ? names[i] : ("file" + std::to_string(i));
+        X0NE_TRY(parse_safetensors(fname, data[i], lens[i], &one));
+        for (auto& kv : one) {
+            if (tensors.count(kv.first)) return fail(X0NE_ERR_FORMAT, kv.first + ": in two files");
+            tensors[kv.first] = kv.second;
+            file_of[kv.first] = fname;
+        }
+    }
+    if (index_json) {
+        Json idx;
+        try {
+            idx = parse_json(index_json);
+        } catch (const std::exception& ex) {
+            return fail(X0NE_ERR_FORMAT, std::string("index: ") + ex.what());
+        }
+        const Json* wm = idx.get("weight_map");
+        if (!wm || wm->kind != Json::Object) return fail(X0NE_ERR_FORMAT, "index: no weight_map");
+        for (const auto& f : wm->fields) {
+            if (f.second.kind != Json::String) return fail(X0NE_ERR_FORMAT, "index: " + f.first + ": file is not a string");
+            auto it = file_of.find(f.first);
+            if (it == file_of.end() || it->second != f.second.text)
+                return fail(X0NE_ERR_FORMAT, f.first + ": not in " + f.second.text);
+        }
+    }
+    X0NE_TRY(check_tensors(c, tensors));
+    x0ne_engine* e = nullptr;
+    X0NE_TRY(build_begin(c, opts, &e));
+    auto put = [&](x0ne_slice s, std::initializer_list<std::string> names_) -> x0ne_status {
+        uint64_t at = 0;
+        for (const auto& n : names_) {
+            const TensorView& t = tensors.at(n);
+            X0NE_TRY(x0ne_arena_write(e->arena, s, at, t.data, t.len));
+            at += t.len;
+        }
+        if (at != s.len) return fail(X0NE_ERR_FORMAT, "wrote " + std::to_string(at) + " bytes into a " + std::to_string(s.len) + "-byte slice");
+        return X0NE_OK;
+    };
+    x0ne_status st = put(e->embed, {"model.embed_tokens.weight"});
+    for (uint64_t l = 0; l < c.layers && st == X0NE_OK; ++l) {
+        const LayerW& w = e->L[l];
+        if ((st = put(w.input_norm, {layer_name(l, L_INPUT_NORM)})) != X0NE_OK) break;
+        if ((st = put(w.qkv, {layer_name(l, L_Q), layer_name(l, L_K), layer_name(l, L_V)})) != X0NE_OK) break;
+        if ((st = put(w.q_norm, {layer_name(l, L_QN)})) != X0NE_OK) break;
+        if ((st = put(w.k_norm, {layer_name(l, L_KN)})) != X0NE_OK) break;
+        if ((st = put(w.o, {layer_name(l, L_O)})) != X0NE_OK) break;
+        if ((st = put(w.post_norm, {layer_name(l, L_POST_NORM)})) != X0NE_OK) break;
+        if ((st = put(w.gate_up, {layer_name(l, L_GATE), layer_name(l, L_UP)})) != X0NE_OK) break;
+        st = put(w.down, {layer_name(l, L_DOWN)});
+    }
+    if (st == X0NE_OK) st = put(e->final_norm, {"model.norm.weight"});
+    if (st == X0NE_OK && e->has_lm_head) st = put(e->lm_head, {"lm_head.weight"});
+    if (st == X0NE_OK) st = build_end(e);
+    if (st != X0NE_OK) {
+        delete e;
+        return st;
+    }
+    *out = e;
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_engine_load_synthetic(const char* config_json, uint64_t seed, double std_dev,
+                                                  const x0ne_engine_options* opts, x0ne_engine** out) {
+    if (!out || !opts) return fail(X0NE_ERR_FORMAT, "null argument");
+    *out = nullptr;
+    Cfg c;
+    X0NE_TRY(parse_config(config_json, &c));
+    X0NE_TRY(check_config(c, opts->max_ctx));
+    if (!(std_dev > 0) || !std::isfinite(std_dev)) return fail(X0NE_ERR_FORMAT, "std is not a positive number");
+    x0ne_engine* e = nullptr;
+    X0NE_TRY(build_begin(c, opts, &e));
+    hipStream_t s = e->gpu->stream;
+    auto normal = [&](x0ne_slice sl, uint64_t at_elems, uint64_t n, uint64_t index) -> x0ne_status {
+        X0NE_HIP(x0ne_launch_init_normal((uint16_t*)(e->d(sl)) + at_elems, n, tensor_key(seed, index), 0, std_dev, s),
+                 "weight init");
+        return X0NE_OK;
+    };
+    auto ones = [&](x0ne_slice sl) -> x0ne_status {
+        X0NE_HIP(x0ne_launch_fill_u16((uint16_t*)e->d(sl), sl.len / 2, 0x3F80, s), "norm init");
+        return X0NE_OK;
+    };
+    // Tensor index i of the checkpoint order: 0 embed, 1 + 11 l + leaf, then the final norm,
+    // then lm_head.
+    x0ne_status st = normal(e->embed, 0, c.vocab * c.hidden, 0);
+    for (uint64_t l = 0; l < c.layers && st == X0NE_OK; ++l) {
+        const LayerW& w = e->L[l];
+        const uint64_t base = 1 + l * L_COUNT;
+        const uint64_t h = c.hidden;
+        if ((st = ones(w.input_norm)) != X0NE_OK) break;
+        if ((st = normal(w.qkv, 0, c.q_dim() * h, base + L_Q)) != X0NE_OK) break;
+        if ((st = normal(w.qkv, c.q_dim() * h, c.kv_dim() * h, base + L_K)) != X0NE_OK) break;
+        if ((st = normal(w.qkv, (c.q_dim() + c.kv_dim()) * h, c.kv_dim() * h, base + L_V)) != X0NE_OK) break;
+        if ((st = ones(w.q_norm)) != X0NE_OK) break;
+        if ((st = ones(w.k_norm)) != X0NE_OK) break;
+        if ((st = normal(w.o, 0, h * c.q_dim(), base + L_O)) != X0NE_OK) break;
+        if ((st = ones(w.post_norm)) != X0NE_OK) break;
+        if ((st = normal(w.gate_up, 0, c.inter * h, base + L_GATE)) != X0NE_OK) break;
+        if ((st = normal(w.gate_up, c.inter * h, c.inter * h, base + L_UP)) != X0NE_OK) break;
+        st = normal(w.down, 0, h * c.inter, base + L_DOWN);
+    }
+    if (st == X0NE_OK) st = ones(e->final_norm);
+    if (st == X0NE_OK && e->has_lm_head) st = normal(e->lm_head, 0, c.vocab * c.hidden, 1 + c.layers * L_COUNT + 1);
+    if (st == X0NE_OK) st = x0ne_gpu_sync(e->gpu);
+    if (st == X0NE_OK) st = build_end(e);
+    if (st != X0NE_OK) {
+        delete e;
+        return st;
+    }
+    *out = e;
+    return X0NE_OK;
+}
+
+extern "C" void x0ne_engine_free(x0ne_engine* e) { delete e; }
+
+// ---------------------------------------------------------------------------------------------
+// Sessions (engine.rs:389-452, :1137-1344)
+// ---------------------------------------------------------------------------------------------
+
+extern "C" x0ne_status x0ne_engine_session(x0ne_engine* e, const uint32_t* prompt, size_t n, x0ne_session** out) {
+    if (!e || !out) return fail(X0NE_ERR_FORMAT, "null argument");
+    *out = nullptr;
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    if (e->poisoned) X0NE_TRY(scrub(e));
+    X0NE_TRY(check_ids(e, prompt, n));
+    x0ne_status st = prefill(e, prompt, n);
+    if (st == X0NE_OK) st = pull_logits(e);
+    if (st != X0NE_OK) {
+        scrub(e);
+        return st;
+    }
+    x0ne_session* s = new x0ne_session();
+    s->e = e;
+    s->pos = n;
+    e->session_open = true;
+    *out = s;
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_session_logits(const x0ne_session* s, const float** ptr, size_t* len) {
+    if (!s || !ptr || !len) return fail(X0NE_ERR_FORMAT, "null argument");
+    if (s->failed) {
+        *ptr = nullptr;
+        *len = 0;
+        return X0NE_OK;
+    }
+    *ptr = s->e->host_logits;
+    *len = s->e->c.vocab;
+    return X0NE_OK;
+}
+
+extern "C" size_t x0ne_session_position(const x0ne_session* s) { return s ? s->pos : 0; }
+
+extern "C" x0ne_status x0ne_session_step(x0ne_session* s, uint32_t token) {
+    if (!s) return fail(X0NE_ERR_FORMAT, "null session");
+    if (s->failed) return fail(X0NE_ERR_GPU, "a previous step failed");
+    x0ne_engine* e = s->e;
+    if (token >= e->c.vocab) return fail(X0NE_ERR_FORMAT, "token " + std::to_string(token) + " outside the vocabulary");
+    if (s->pos >= e->max_ctx)
+        return fail(X0NE_ERR_FORMAT, "position " + std::to_string(s->pos) + " at max_ctx " + std::to_string(e->max_ctx));
+    // The token goes up from a pinned word; the step reads it and pos on the device.
+    *e->host_token = token;
+    e->gpu->counts.htod++;
+    hipError_t he = hipMemcpyAsync(e->d(e->tokens), e->host_token, 4, hipMemcpyHostToDevice, e->gpu->stream);
+    x0ne_status st = he == hipSuccess ? X0NE_OK : gpu_fail(he, "token copy");
+    if (st == X0NE_OK) st = run_step(e);
+    if (st == X0NE_OK) st = pull_logits(e);
+    if (st != X0NE_OK) {
+        s->failed = true;
+        return st;
+    }
+    s->pos += 1;
+    return X0NE_OK;
+}
+
+static x0ne_status session_close(x0ne_session* s) {
+    x0ne_status st = X0NE_OK;
+    if (s->open) {
+        s->open = false;
+        st = scrub(s->e);
+    }
+    s->e->session_open = false;
+    return st;
+}
+
+extern "C" x0ne_status x0ne_session_finish(x0ne_session* s) {
+    if (!s) return fail(X0NE_ERR_FORMAT, "null session");
+    x0ne_status st = session_close(s);
+    delete s;
+    return st;
+}
+
+extern "C" void x0ne_session_drop(x0ne_session* s) {
+    if (!s) return;
+    session_close(s);
+    delete s;
+}
+
+namespace {
+
+// Launches steps until `ahead` tokens are in flight or every token asked is launched; step j
+// writes its token into ring word j % RING (engine.rs:1322-1343).
+x0ne_status greedy_fill(x0ne_greedy* g) {
+    x0ne_engine* e = g->s->e;
+    const size_t taken_m1 = g->taken ? g->taken - 1 : 0;
+    while (g->launched + 1 < g->max_tokens && g->launched - taken_m1 < g->ahead) {
+        const size_t j = g->launched + 1;
+        x0ne_status st = run_step(e);
+        if (st == X0NE_OK) st = ring_fetch(e, j);
+        if (st != X0NE_OK) {
+            g->s->failed = true;
+            return st;
+        }
+        g->launched = j;
+        g->s->pos += 1;
+    }
+    return X0NE_OK;
+}
+
+}  // namespace
+
+extern "C" x0ne_status x0ne_session_into_greedy(x0ne_session* s, size_t max_tokens, size_t ahead, x0ne_greedy** out) {
+    if (!s || !out) return fail(X0NE_ERR_FORMAT, "null argument");
+    *out = nullptr;
+    auto refuse = [&](x0ne_status st) {
+        x0ne_session_drop(s);
+        return st;
+    };
+    if (ahead < 1 || ahead > X0NE_GREEDY_AHEAD_MAX)
+        return refuse(fail(X0NE_ERR_FORMAT, std::to_string(ahead) + " greedy steps ahead: 1 to 15"));
+    if (s->failed) return refuse(fail(X0NE_ERR_GPU, "a previous step failed"));
+    if (max_tokens == 0) return refuse(fail(X0NE_ERR_FORMAT, "0 greedy tokens asked"));
+    const size_t room = s->e->max_ctx > s->pos ? s->e->max_ctx - s->pos : 0;
+    if (max_tokens - 1 > room)
+        return refuse(fail(X0NE_ERR_FORMAT, std::to_string(max_tokens) + " greedy tokens at position " +
+                                                std::to_string(s->pos) + " pass max_ctx " + std::to_string(s->e->max_ctx)));
+    x0ne_greedy* g = new x0ne_greedy();
+    g->s = s;
+    g->max_tokens = max_tokens;
+    g->ahead = ahead;
+    // The argmax of the current position is in tokens[0] already (the step wrote it).
+    x0ne_status st = read_token(s->e, &g->first);
+    if (st == X0NE_OK) st = greedy_fill(g);
+    if (st != X0NE_OK) {
+        s->failed = true;
+        x0ne_greedy_drop(g);
+        return st;
+    }
+    *out = g;
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_greedy_next(x0ne_greedy* g, uint32_t* token) {
+    if (!g || !token) return fail(X0NE_ERR_FORMAT, "null argument");
+    if (g->s->failed) return fail(X0NE_ERR_GPU, "a previous step failed");
+    if (g->taken == g->max_tokens)
+        return fail(X0NE_ERR_FORMAT, "all " + std::to_string(g->max_tokens) + " greedy tokens taken");
+    uint32_t t = g->first;
+    if (g->taken > 0) {
+        x0ne_status st = ring_take(g->s->e, g->taken, &t);
+        if (st != X0NE_OK) {
+            g->s->failed = true;
+            return st;
+        }
+    }
+    if (t >= g->s->e->c.vocab) {
+        g->s->failed = true;
+        return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
+    }
+    g->taken += 1;
+    X0NE_TRY(greedy_fill(g));
+    *token = t;
+    return X0NE_OK;
+}
+
+extern "C" size_t x0ne_greedy_taken(const x0ne_greedy* g) { return g ? g->taken : 0; }
+extern "C" size_t x0ne_greedy_position(const x0ne_greedy* g) { return g ? g->s->pos : 0; }
+
+extern "C" x0ne_status x0ne_greedy_finish(x0ne_greedy* g) {
+    if (!g) return fail(X0NE_ERR_FORMAT, "null greedy");
+    x0ne_status st = x0ne_session_finish(g->s);
+    delete g;
+    return st;
+}
+
+extern "C" void x0ne_greedy_drop(x0ne_greedy* g) {
+    if (!g) return;
+    x0ne_session_drop(g->s);
+    delete g;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Greedy passes (engine.rs:1026-1135)
+// ---------------------------------------------------------------------------------------------
+
+namespace {
+
+x0ne_status greedy_inner(x0ne_engine* e, const uint32_t* prompt, size_t np, size_t n, uint32_t* out, double* times) {
+    const auto t0 = std::chrono::steady_clock::now();
+    auto now = [&]() { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); };
+    X0NE_TRY(prefill(e, prompt, np));
+    // The first token comes from the prefill's last step; it is in tokens[0] for the next.
+    X0NE_TRY(read_token(e, &out[0]));
+    if (times) times[0] = now();
+    if (e->mode == X0NE_DECODE_EAGER) {
+        for (size_t i = 1; i < n; ++i) {
+            X0NE_TRY(step_launches(e));
+            X0NE_TRY(read_token(e, &out[i]));
+            if (times) times[i] = now();
+        }
+        return X0NE_OK;
+    }
+    // Per token: one graph launch, one 4-byte copy into a host word, one event; the host runs
+    // up to RING - 1 steps ahead and collects tokens in order.
+    size_t next = 1;
+    auto collect = [&](size_t j) -> x0ne_status {
+        uint32_t t = 0;
+        X0NE_TRY(ring_take(e, j, &t));
+        if (t >= e->c.vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
+        out[j] = t;
+        if (times) times[j] = now();
+        return X0NE_OK;
+    };
+    for (size_t i = 1; i < n; ++i) {
+        X0NE_TRY(run_step(e));
+        X0NE_TRY(ring_fetch(e, i));
+        if (i + 1 - next >= RING - 1) {
+            X0NE_TRY(collect(next));
+            next += 1;
+        }
+    }
+    while (next < n) {
+        X0NE_TRY(collect(next));
+        next += 1;
+    }
+    return X0NE_OK;
+}
+
+x0ne_status greedy_checks(x0ne_engine* e, const uint32_t* prompt, size_t np, size_t n) {
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    if (e->poisoned) X0NE_TRY(scrub(e));
+    X0NE_TRY(check_ids(e, prompt, np));
+    if (n == 0 || np + n - 1 > e->max_ctx)
+        return fail(X0NE_ERR_FORMAT, std::to_string(np) + " + " + std::to_string(n) + " tokens exceed max_ctx " +
+                                         std::to_string(e->max_ctx));
+    return X0NE_OK;
+}
+
+}  // namespace
+
+extern "C" x0ne_status x0ne_engine_greedy_timed(x0ne_engine* e, const uint32_t* prompt, size_t np, size_t n,
+                                                uint32_t* tokens, double* times) {
+    if (!e || !tokens) return fail(X0NE_ERR_FORMAT, "null argument");
+    X0NE_TRY(greedy_checks(e, prompt, np, n));
+    x0ne_status st = greedy_inner(e, prompt, np, n, tokens, times);
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
+extern "C" x0ne_status x0ne_engine_greedy_with_last_logits(x0ne_engine* e, const uint32_t* prompt, size_t np, size_t n,
+                                                           uint32_t* tokens, float* logits) {
+    if (!e || !tokens || !logits) return fail(X0NE_ERR_FORMAT, "null argument");
+    X0NE_TRY(greedy_checks(e, prompt, np, n));
+    x0ne_status st = greedy_inner(e, prompt, np, n, tokens, nullptr);
+    if (st == X0NE_OK) st = x0ne_arena_read(e->arena, e->logits, 0, logits, e->c.vocab * 4);
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
+extern "C" x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids, size_t n, const size_t* positions,
+                                             size_t n_positions, uint32_t route, float* rows) {
+    if (!e || (!rows && n_positions)) return fail(X0NE_ERR_FORMAT, "null argument");
+    if (route != X0NE_ROUTE_PREFILL && route != X0NE_ROUTE_DECODE) return fail(X0NE_ERR_FORMAT, "unknown route");
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    if (e->poisoned) X0NE_TRY(scrub(e));
+    X0NE_TRY(check_ids(e, ids, n));
+    for (size_t k = 0; k < n_positions; ++k)
+        if (positions[k] >= n)
+            return fail(X0NE_ERR_FORMAT, "position " + std::to_string(positions[k]) + " outside " + std::to_string(n) + " tokens");
+    // Both routes feed one position per step here (the prefill route's many-row pass is not
+    // built yet), so they give the same bits.
+    x0ne_status st = put_prompt(e, ids, n);
+    for (size_t p = 0; p < n && st == X0NE_OK; ++p) {
+        st = feed(e, (uint32_t)p);
+        for (size_t k = 0; k < n_positions && st == X0NE_OK; ++k)
+            if (positions[k] == p) st = x0ne_arena_read(e->arena, e->logits, 0, rows + k * e->c.vocab, e->c.vocab * 4);
+    }
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Introspection
+// ---------------------------------------------------------------------------------------------
+
+extern "C" x0ne_status x0ne_engine_set_decode_mode(x0ne_engine* e, uint32_t mode) {
+    if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
+    if (mode != X0NE_DECODE_EAGER && mode != X0NE_DECODE_GRAPH) return fail(X0NE_ERR_FORMAT, "unknown decode mode");
+    if (mode == X0NE_DECODE_GRAPH && !e->graph) return fail(X0NE_ERR_GPU, "no decode graph captured");
+    e->mode = mode;
+    return X0NE_OK;
+}
+
+extern "C" uint32_t x0ne_engine_decode_mode(const x0ne_engine* e) { return e ? e->mode : 0; }
+
+extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, size_t len) {
+    if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
+    char gpu[512];
+    x0ne_gpu_describe(e->gpu, gpu, sizeof gpu);
+    char s[1024];
+    std::snprintf(s, sizeof s,
+                  "%s, arena %llu bytes, decode graph %zu nodes, decode attention split-K P %u (grid %u x %u, %u q "
+                  "heads per block, %u blocks per CU, merge %s), KV pages of %d positions (%llu pages, %s order), "
+                  "GEMV grids qkv %u o %u gate_up %u down %u head %u, feed-forward dense",
+                  gpu, (unsigned long long)e->arena->len, e->graph ? e->graph->nodes : (size_t)0, e->split.splits,
+                  e->split.grid_x, e->split.splits, e->split.group, e->split.per_cu,
+                  e->split.grouped ? "LastBlock" : "Kernel", X0NE_PAGE_C, (unsigned long long)e->pages,
+                  e->page_seed ? "shuffled" : "identity", e->grid_qkv, e->grid_o, e->grid_gu, e->grid_down,
+                  e->grid_head);
+    if (buf && len) {
+        std::strncpy(buf, s, len - 1);
+        buf[len - 1] = 0;
+    }
+    return X0NE_OK;
+}
+
+extern "C" size_t x0ne_engine_graph_nodes(const x0ne_engine* e) { return e && e->graph ? e->graph->nodes : 0; }
+extern "C" uint32_t x0ne_engine_splits(const x0ne_engine* e) { return e ? e->split.splits : 0; }
+extern "C" uint64_t x0ne_engine_max_ctx(const x0ne_engine* e) { return e ? e->max_ctx : 0; }
+extern "C" const x0ne_arena* x0ne_engine_arena(const x0ne_engine* e) { return e ? e->arena : nullptr; }
+
+extern "C" x0ne_status x0ne_engine_counts(const x0ne_engine* e, x0ne_counts* out) {
+    if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
+    return x0ne_gpu_counts(e->gpu, out);
+}
+
+extern "C" x0ne_status x0ne_engine_page(const x0ne_engine* e, uint64_t i, uint32_t* out) {
+    if (!e || !out || i >= e->pages) return fail(X0NE_ERR_FORMAT, "no such page");
+    *out = e->page_of[i];
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_engine_client_data_is_zero(const x0ne_engine* e, int* out) {
+    if (!e || !out) return fail(X0NE_ERR_FORMAT, "null argument");
+    const uint64_t STEP = 64ull << 20;
+    std::vector<uint8_t> buf(STEP);
+    *out = 1;
+    for (const auto& r : e->arena->regions) {
+        if (r.cls != X0NE_CLASS_CLIENT_DATA) continue;
+        for (uint64_t at = 0; at < r.len; at += STEP) {
+            const uint64_t n = r.len - at < STEP ? r.len - at : STEP;
+            X0NE_HIP(hipMemcpy(buf.data(), e->arena->base + r.offset + at, n, hipMemcpyDeviceToHost), "read back");
+            for (uint64_t i = 0; i < n; ++i)
+                if (buf[i]) {
+                    *out = 0;
+                    return X0NE_OK;
+                }
+        }
+    }
+    return X0NE_OK;
+}
+
+extern "C" int x0ne_engine_host_buffers_are_zero(const x0ne_engine* e) {
+    if (!e) return 0;
+    for (uint64_t i = 0; i < e->c.vocab; ++i)
+        if (e->host_logits[i] != 0.0f || std::signbit(e->host_logits[i])) return 0;
+    if (*e->host_token) return 0;
+    for (size_t i = 0; i < RING; ++i)
+        if (e->ring[i]) return 0;
+    return 1;
+}

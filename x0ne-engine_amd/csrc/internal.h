@@ -1,0 +1,85 @@
+// Host-side structures of the runtime, shared by runtime.hip (device, launch API, arena) and
+// engine.hip (the Qwen3 engine).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/x0ne_core.h"
+#include "kernels.h"
+#include "launch.h"
+
+namespace x0ne {
+
+// Sets the calling thread's message and returns the status (the reference's Error variants).
+x0ne_status fail(x0ne_status s, const std::string& msg);
+// X0NE_ERR_GPU with the runtime's error text, for a failed HIP call.
+x0ne_status gpu_fail(hipError_t e, const char* what);
+
+struct Counts {
+    std::atomic<uint64_t> launches{0}, graph_launches{0}, gemms{0}, htod{0}, dtoh{0}, memsets{0}, syncs{0};
+};
+
+}  // namespace x0ne
+
+#define X0NE_HIP(call, what)                                        \
+    do {                                                            \
+        hipError_t e_ = (call);                                     \
+        if (e_ != hipSuccess) return x0ne::gpu_fail(e_, (what));    \
+    } while (0)
+
+#define X0NE_TRY(call)                          \
+    do {                                        \
+        x0ne_status s_ = (call);                \
+        if (s_ != X0NE_OK) return s_;           \
+    } while (0)
+
+struct x0ne_gpu {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name, arch;
+    uint32_t cus = 0;
+    int driver_version = 0, runtime_version = 0;
+    uint64_t total_mem = 0;
+    x0ne::Counts counts;
+    bool capturing = false;
+};
+
+struct x0ne_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    size_t nodes = 0;
+};
+
+struct x0ne_arena {
+    struct Region {
+        std::string label;
+        uint32_t cls;
+        uint64_t offset, len;
+    };
+    uint64_t id = 0;
+    std::vector<Region> regions;
+    uint64_t size = 0;
+    bool frozen = false;
+    x0ne_gpu* gpu = nullptr;  // null: host backing
+    uint8_t* base = nullptr;
+    uint64_t len = 0;
+};
+
+namespace x0ne {
+// Checked offset of `len` bytes at `at` of slice s (arena.rs:229-240).
+x0ne_status arena_check(const x0ne_arena* a, x0ne_slice s, uint64_t at, uint64_t len, uint64_t* off);
+// Device address of a slice (its first byte).
+inline uint8_t* dev(const x0ne_arena* a, x0ne_slice s) { return a->base + s.offset; }
+// Launch of a table kernel by index with checked arguments.
+x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32_t gy, uint32_t block,
+                           const x0ne_arg* args, size_t n);
+// Split plan for a geometry (gpu.rs:958-985), P capped at `cap`.
+x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out);
+x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_block, const void* q, const void* k,
+                            const void* v, const void* pages, void* state, void* counter, void* out, const void* pos,
+                            uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
+}  // namespace x0ne

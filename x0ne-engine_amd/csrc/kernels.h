@@ -1,0 +1,63 @@
+// The kernel ABI of this library (the analogue of x0ne-core/kernels/cuda/x0ne_kernels.h): C
+// linkage, row-major bf16, f32 accumulation, positions and token ids read from device memory,
+// bounds checked without trap. KV planes are paged: [pages][kv_heads][16][128] bf16 with a
+// page table mapping position / 16 to a physical page. Launch shapes are documented at each
+// definition (attention.hip, norm.hip, gemv.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;
+
+extern "C" {
+__global__ void x0ne_probe_iota_u32(uint32_t* out, uint32_t n);
+__global__ void x0ne_embedding_bf16(const bf16_t* table, const uint32_t* tokens, bf16_t* out, uint32_t hidden,
+                                    uint32_t vocab);
+__global__ void x0ne_add_rmsnorm_bf16(float* residual, const bf16_t* x, const bf16_t* w, bf16_t* out,
+                                      uint32_t hidden, float eps);
+__global__ void x0ne_qk_norm_rope_kv_write_bf16(const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm,
+                                                const float* inv_freq, bf16_t* q_out, bf16_t* k_cache,
+                                                bf16_t* v_cache, const uint32_t* pages, const uint32_t* pos0,
+                                                uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float eps);
+__global__ void x0ne_attention_decode_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
+                                           const uint32_t* pages, bf16_t* out, const uint32_t* pos, uint32_t q_heads,
+                                           uint32_t kv_heads, uint32_t max_ctx, float scale);
+__global__ void x0ne_attention_decode_split_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
+                                                 const uint32_t* pages, float* state, const uint32_t* pos,
+                                                 uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx,
+                                                 uint32_t splits, float scale);
+#define X0NE_DECLARE_SPLIT_GROUP(G)                                                                              \
+    __global__ void x0ne_attention_decode_split_g##G##_bf16(                                                    \
+        const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache, const uint32_t* pages, float* state,     \
+        uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, \
+        uint32_t splits, float scale);
+X0NE_DECLARE_SPLIT_GROUP(1)
+X0NE_DECLARE_SPLIT_GROUP(2)
+X0NE_DECLARE_SPLIT_GROUP(4)
+X0NE_DECLARE_SPLIT_GROUP(8)
+#undef X0NE_DECLARE_SPLIT_GROUP
+__global__ void x0ne_attention_merge_bf16(const float* state, bf16_t* out, const uint32_t* pos, uint32_t max_ctx,
+                                          uint32_t splits);
+__global__ void x0ne_attention_prefill_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
+                                            const uint32_t* pages, bf16_t* out, const uint32_t* pos0, uint32_t rows,
+                                            uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
+__global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
+__global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
+__global__ void x0ne_advance_u32(uint32_t* pos);
+__global__ void x0ne_feed_u32(const uint32_t* ids, uint32_t i, uint32_t* tokens, uint32_t* pos);
+__global__ void x0ne_gemv_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
+__global__ void x0ne_gemv_f32(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
+__global__ void x0ne_gemv_any(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols,
+                              uint32_t f32_out);
+}
+
+// The table: name, host stub, parameter kinds (0 pointer, 1 u32, 2 f32), most threads a block
+// may have.
+struct X0neKernel {
+    const char* name;
+    const void* fn;
+    const char* params;  // one character per parameter: 'p', 'u', 'f'
+    uint32_t max_block;
+};
+
+const X0neKernel* x0ne_kernel_table(size_t* n);

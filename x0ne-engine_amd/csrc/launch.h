@@ -1,0 +1,35 @@
+// Typed launchers of the fused kernels, for the runtime (host side of this library).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// One fused GEMV launch (gemv.hip). prologue: 0 x given, 1 add+RMSNorm, 2 embedding+RMSNorm;
+// epilogue: 0 bf16 out, 1 f32 out, 2 SwiGLU over [gate; up], 3 f32 logits + argmax.
+struct X0neGemv {
+    const uint16_t* w;
+    const uint16_t* x;
+    const float* res_in;
+    float* res_out;
+    const uint16_t* delta;
+    const uint16_t* norm_w;
+    const uint16_t* embed;
+    const uint32_t* tokens;
+    void* y;
+    float* partial;
+    uint32_t* counter;
+    uint32_t* token_out;
+    uint32_t* pos;
+    uint32_t rows, cols, vocab, advance;
+    float eps;
+    int prologue, epilogue;
+    uint32_t grid;
+};
+
+hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s);
+uint32_t x0ne_gemv_rows_per_step(uint32_t cols);
+
+// Device weight initialisers (init.hip): n values of N(0, std) bf16 from stream `key`
+// starting at value `first` (even), and a constant fill.
+hipError_t x0ne_launch_init_normal(uint16_t* out, uint64_t n, uint64_t key, uint64_t first, double std_dev,
+                                   hipStream_t s);
+hipError_t x0ne_launch_fill_u16(uint16_t* out, uint64_t n, uint16_t v, hipStream_t s);

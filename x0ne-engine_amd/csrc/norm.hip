@@ -1,0 +1,179 @@
+// The small kernels of the decode step, for gfx950: embedding, residual add + RMSNorm, per-head
+// QK-norm + RoPE + the paged KV write, SwiGLU, greedy argmax, the position advance. Each follows
+// its reference kernel in x0ne-core/kernels/cuda/ (cited per kernel), with 64-lane reductions;
+// the norms, RoPE and SwiGLU compute in f64 like the reference's oracle (oracle/src/lib.rs), so
+// their bf16 results are the oracle's except where an f64 result sits on a rounding boundary.
+#include "device.h"
+
+// Smallest kernel that proves the build path end to end (probe.cu:4-9): out[i] = i.
+// grid (ceil(n / 256)), block 256.
+extern "C" __global__ void __launch_bounds__(256) x0ne_probe_iota_u32(uint32_t* out, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = i;
+}
+
+// out[r] = table[tokens[r]] (embedding.cu:5-17): grid (rows), block 128, hidden % 8 == 0,
+// 16-byte copies. An id >= vocab writes a zero row.
+extern "C" __global__ void __launch_bounds__(128)
+    x0ne_embedding_bf16(const bf16_t* __restrict__ table, const uint32_t* __restrict__ tokens,
+                        bf16_t* __restrict__ out, uint32_t hidden, uint32_t vocab) {
+    const uint32_t row = blockIdx.x;
+    const uint32_t t = tokens[row];
+    uint4* dst = reinterpret_cast<uint4*>(out + (size_t)row * hidden);
+    const uint32_t n = hidden / 8;
+    if (t >= vocab) {
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) dst[i] = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    const uint4* src = reinterpret_cast<const uint4*>(table + (size_t)t * hidden);
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+}
+
+// residual[r] += x[r] (f32, one addition per value); out[r] = bf16(residual / rms * w), the rms
+// and the product in f64 (rmsnorm.cu:5-21; oracle/src/lib.rs:50-67). grid (rows), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_add_rmsnorm_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+                          bf16_t* __restrict__ out, uint32_t hidden, float eps) {
+    __shared__ double sh[16];
+    const size_t base = (size_t)blockIdx.x * hidden;
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) {
+        const float r = residual[base + i] + bf2f(x[base + i]);
+        residual[base + i] = r;
+        ss += (double)r * (double)r;
+    }
+    const double total = block_sum_d(ss, sh);
+    const double scale = 1.0 / sqrt(total / (double)hidden + (double)eps);
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x)
+        out[base + i] = f2bf((float)((double)residual[base + i] * scale * (double)bf2f(w[i])));
+}
+
+// Per-head RMSNorm of q and k, rotate-half RoPE, and the K/V write into the paged cache
+// (rope.cu:7-47; oracle/src/lib.rs:82-120). grid (q_heads + kv_heads, rows), block 64: lane i
+// owns the pair (i, i + 64) of one head. Row r sits at position pos0[0] + r, written at
+// physical page page_table[pos / 16], slot pos % 16 of the layer's K and V planes
+// ([pages][kv_heads][16][128]). A position >= max_ctx writes nothing into the cache. The angle
+// is the f32 product pos * inv_freq[i] (inv_freq computed on the host in f32), its sine and
+// cosine in f64. Blocks of k heads also copy v, bit for bit.
+extern "C" __global__ void __launch_bounds__(64)
+    x0ne_qk_norm_rope_kv_write_bf16(const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm,
+                                    const bf16_t* __restrict__ k_norm, const float* __restrict__ inv_freq,
+                                    bf16_t* __restrict__ q_out, bf16_t* __restrict__ k_cache,
+                                    bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
+                                    const uint32_t* __restrict__ pos0, uint32_t q_heads, uint32_t kv_heads,
+                                    uint32_t max_ctx, float eps) {
+    constexpr uint32_t HD = X0NE_HEAD_DIM, HALF = HD / 2;
+    const uint32_t head = blockIdx.x, row = blockIdx.y, i = threadIdx.x;
+    const uint32_t q_dim = q_heads * HD, kv_dim = kv_heads * HD, qkv_dim = q_dim + 2 * kv_dim;
+    const uint32_t pos = pos0[0] + row;
+    const bool is_q = head < q_heads;
+    const uint32_t kh = is_q ? 0 : head - q_heads;
+    const bf16_t* src = qkv + (size_t)row * qkv_dim + (is_q ? head * HD : q_dim + kh * HD);
+    const bf16_t* nw = is_q ? q_norm : k_norm;
+
+    const float a = bf2f(src[i]), b = bf2f(src[i + HALF]);
+    const double ss = wave_sum_d((double)a * (double)a + (double)b * (double)b);
+    const double scale = 1.0 / sqrt(ss / (double)HD + (double)eps);
+    const double na = (double)a * scale * (double)bf2f(nw[i]);
+    const double nb = (double)b * scale * (double)bf2f(nw[i + HALF]);
+    const double angle = (double)((float)pos * inv_freq[i]);
+    const double s = sin(angle), c = cos(angle);
+    const float ra = (float)(na * c - nb * s);
+    const float rb = (float)(nb * c + na * s);
+
+    if (is_q) {
+        bf16_t* d = q_out + (size_t)row * q_dim + head * HD;
+        d[i] = f2bf(ra);
+        d[i + HALF] = f2bf(rb);
+        return;
+    }
+    if (pos >= max_ctx) return;
+    const uint32_t at = kv_row(pages, pos, kh, kv_heads);
+    k_cache[at + i] = f2bf(ra);
+    k_cache[at + i + HALF] = f2bf(rb);
+    const bf16_t* vs = qkv + (size_t)row * qkv_dim + q_dim + kv_dim + kh * HD;
+    v_cache[at + i] = vs[i];
+    v_cache[at + i + HALF] = vs[i + HALF];
+}
+
+// SwiGLU on the packed [gate; up] row: out[i] = g / (1 + e^-g) * u, in f64 (swiglu.cu:5-11;
+// oracle/src/lib.rs:205-214). grid (ceil(inter / 256), rows), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_swiglu_bf16(const bf16_t* __restrict__ gate_up, bf16_t* __restrict__ out, uint32_t inter) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+    if (i >= inter) return;
+    const bf16_t* row = gate_up + (size_t)r * 2 * inter;
+    const double g = (double)bf2f(row[i]), u = (double)bf2f(row[inter + i]);
+    out[(size_t)r * inter + i] = f2bf((float)(g / (1.0 + exp(-g)) * u));
+}
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// Greedy pick (argmax.cu:11-58): index of the largest logit of each row, lowest index on ties;
+// a row holding any NaN yields 0xFFFFFFFF. grid (rows), block 1024 (16 wavefronts).
+extern "C" __global__ void __launch_bounds__(1024)
+    x0ne_argmax_f32(const float* __restrict__ logits, uint32_t n, uint32_t* __restrict__ out) {
+    __shared__ float sv[16];
+    __shared__ uint32_t si[16];
+    __shared__ int snan;
+    const float* row = logits + (size_t)blockIdx.x * n;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
+    if (t == 0) snan = 0;
+    __syncthreads();
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    bool nan = false;
+    for (uint32_t i = t; i < n; i += blockDim.x) {
+        const float v = row[i];
+        nan |= v != v;
+        if (better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (__any(nan) && lane == 0) atomicOr(&snan, 1);
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float fv = -INFINITY;
+        uint32_t fi = 0xFFFFFFFFu;
+        for (uint32_t w = 0; w < nw; ++w) {
+            if (better(sv[w], si[w], fv, fi)) {
+                fv = sv[w];
+                fi = si[w];
+            }
+        }
+        out[blockIdx.x] = snan ? 0xFFFFFFFFu : fi;
+    }
+}
+
+// Position advance, the last node of the decode step (advance.cu:5-7): pos[0] += 1.
+// grid (1), block 64.
+extern "C" __global__ void __launch_bounds__(64) x0ne_advance_u32(uint32_t* __restrict__ pos) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) pos[0] += 1u;
+}
+
+// Prefill feed (this build's): token ids[i] into tokens[0] and position i into pos[0], so the
+// decode step that reads both on the device runs on prompt token i. grid (1), block 64.
+extern "C" __global__ void __launch_bounds__(64)
+    x0ne_feed_u32(const uint32_t* __restrict__ ids, uint32_t i, uint32_t* __restrict__ tokens,
+                  uint32_t* __restrict__ pos) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        tokens[0] = ids[i];
+        pos[0] = i;
+    }
+}

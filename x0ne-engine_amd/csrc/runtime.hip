@@ -1,0 +1,586 @@
+// The device, the kernel-launch API, graph capture and the arena: the reference's
+// x0ne-core/runtime/src/{gpu,arena,error}.rs, on the HIP runtime for gfx950.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "internal.h"
+
+namespace x0ne {
+
+static thread_local std::string g_last_error;
+
+x0ne_status fail(x0ne_status s, const std::string& msg) {
+    g_last_error = msg;
+    return s;
+}
+
+x0ne_status gpu_fail(hipError_t e, const char* what) {
+    return fail(X0NE_ERR_GPU, std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+}
+
+static std::atomic<uint64_t> g_next_arena{1};
+
+}  // namespace x0ne
+
+using namespace x0ne;
+
+extern "C" size_t x0ne_last_error(char* buf, size_t len) {
+    const std::string& m = g_last_error;
+    if (buf && len) {
+        const size_t n = m.size() < len - 1 ? m.size() : len - 1;
+        std::memcpy(buf, m.data(), n);
+        buf[n] = 0;
+    }
+    return m.size();
+}
+
+#ifndef X0NE_KERNEL_SET
+#define X0NE_KERNEL_SET "unversioned"
+#endif
+
+extern "C" size_t x0ne_kernel_set(char* buf, size_t len) {
+    const std::string s = std::string("kernels ") + X0NE_KERNEL_SET + ", gfx950, " + __VERSION__;
+    if (buf && len) {
+        const size_t n = s.size() < len - 1 ? s.size() : len - 1;
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return s.size();
+}
+
+// ---------------------------------------------------------------------------------------------
+// The device (gpu.rs:750-928)
+// ---------------------------------------------------------------------------------------------
+
+extern "C" x0ne_status x0ne_gpu_new(x0ne_gpu** out) {
+    if (!out) return fail(X0NE_ERR_FORMAT, "x0ne_gpu_new: null out");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return fail(X0NE_ERR_GPU, std::string("no HIP device: ") + (e != hipSuccess ? hipGetErrorString(e) : "0 devices"));
+    X0NE_HIP(hipSetDevice(0), "hipSetDevice(0)");
+    hipDeviceProp_t p;
+    X0NE_HIP(hipGetDeviceProperties(&p, 0), "hipGetDeviceProperties");
+    const std::string arch = p.gcnArchName;
+    if (arch.rfind("gfx950", 0) != 0)
+        return fail(X0NE_ERR_GPU, "device 0 is " + arch + ": the kernels are built for gfx950 only");
+    x0ne_gpu* g = new x0ne_gpu();
+    g->device = 0;
+    g->name = p.name;
+    g->arch = arch;
+    g->cus = (uint32_t)p.multiProcessorCount;
+    g->total_mem = (uint64_t)p.totalGlobalMem;
+    (void)hipDriverGetVersion(&g->driver_version);
+    (void)hipRuntimeGetVersion(&g->runtime_version);
+    // One non-blocking stream at the default priority.
+    e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete g;
+        return gpu_fail(e, "hipStreamCreateWithFlags");
+    }
+    *out = g;
+    return X0NE_OK;
+}
+
+extern "C" void x0ne_gpu_free(x0ne_gpu* g) {
+    if (!g) return;
+    if (g->stream) {
+        (void)hipStreamSynchronize(g->stream);
+        (void)hipStreamDestroy(g->stream);
+    }
+    delete g;
+}
+
+extern "C" x0ne_status x0ne_gpu_sync(x0ne_gpu* g) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    g->counts.syncs++;
+    X0NE_HIP(hipStreamSynchronize(g->stream), "hipStreamSynchronize");
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_gpu_describe(const x0ne_gpu* g, char* buf, size_t len) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    char s[512];
+    std::snprintf(s, sizeof s, "%s (%s, %u CUs, %.1f GiB), HIP driver %d, runtime %d", g->name.c_str(),
+                  g->arch.c_str(), g->cus, (double)g->total_mem / (1ull << 30), g->driver_version,
+                  g->runtime_version);
+    if (buf && len) {
+        std::strncpy(buf, s, len - 1);
+        buf[len - 1] = 0;
+    }
+    return X0NE_OK;
+}
+
+extern "C" uint32_t x0ne_gpu_compute_units(const x0ne_gpu* g) { return g ? g->cus : 0; }
+
+extern "C" x0ne_status x0ne_gpu_mem_info(const x0ne_gpu* g, uint64_t* free_bytes, uint64_t* total_bytes) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    size_t f = 0, t = 0;
+    X0NE_HIP(hipMemGetInfo(&f, &t), "hipMemGetInfo");
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_gpu_counts(const x0ne_gpu* g, x0ne_counts* out) {
+    if (!g || !out) return fail(X0NE_ERR_GPU, "no device");
+    out->launches = g->counts.launches;
+    out->graph_launches = g->counts.graph_launches;
+    out->gemms = g->counts.gemms;
+    out->htod = g->counts.htod;
+    out->dtoh = g->counts.dtoh;
+    out->memsets = g->counts.memsets;
+    out->syncs = g->counts.syncs;
+    return X0NE_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// The kernel table and the checked launch (gpu.rs:281-374, :1031-1086)
+// ---------------------------------------------------------------------------------------------
+
+static const X0neKernel* find_kernel(const char* name) {
+    if (!name) return nullptr;
+    size_t n = 0;
+    const X0neKernel* t = x0ne_kernel_table(&n);
+    for (size_t i = 0; i < n; ++i)
+        if (std::strcmp(t[i].name, name) == 0) return &t[i];
+    return nullptr;
+}
+
+extern "C" size_t x0ne_kernel_count(void) {
+    size_t n = 0;
+    x0ne_kernel_table(&n);
+    return n;
+}
+
+extern "C" const char* x0ne_kernel_name(size_t i) {
+    size_t n = 0;
+    const X0neKernel* t = x0ne_kernel_table(&n);
+    return i < n ? t[i].name : nullptr;
+}
+
+static uint32_t kind_of(char c) { return c == 'p' ? X0NE_PARAM_PTR : c == 'u' ? X0NE_PARAM_U32 : X0NE_PARAM_F32; }
+
+extern "C" size_t x0ne_kernel_params(const char* name, uint32_t* out, size_t cap) {
+    const X0neKernel* k = find_kernel(name);
+    if (!k) return (size_t)-1;
+    const size_t n = std::strlen(k->params);
+    for (size_t i = 0; i < n && i < cap; ++i) out[i] = kind_of(k->params[i]);
+    return n;
+}
+
+static const char* kind_name(uint32_t k) {
+    return k == X0NE_PARAM_PTR ? "a pointer" : k == X0NE_PARAM_U32 ? "a u32" : k == X0NE_PARAM_F32 ? "an f32" : "unknown";
+}
+
+static x0ne_status check_args_of(const X0neKernel& k, const x0ne_arg* args, size_t n) {
+    const size_t want = std::strlen(k.params);
+    if (n != want)
+        return fail(X0NE_ERR_GPU, std::string(k.name) + ": " + std::to_string(n) + " arguments for " +
+                                      std::to_string(want) + " parameters");
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t p = kind_of(k.params[i]);
+        if (args[i].kind != p)
+            return fail(X0NE_ERR_GPU, std::string(k.name) + ": argument " + std::to_string(i) + " is " +
+                                          kind_name(args[i].kind) + ", the parameter " + kind_name(p));
+    }
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_check_args(const char* name, const x0ne_arg* args, size_t n) {
+    const X0neKernel* k = find_kernel(name);
+    if (!k) return fail(X0NE_ERR_GPU, std::string("no kernel ") + (name ? name : "(null)"));
+    return check_args_of(*k, args, n);
+}
+
+namespace x0ne {
+
+x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32_t gy, uint32_t block,
+                           const x0ne_arg* args, size_t n) {
+    X0NE_TRY(check_args_of(k, args, n));
+    if (gx == 0 || gy == 0 || block == 0 || block > k.max_block || block % 64 != 0)
+        return fail(X0NE_ERR_GPU, std::string(k.name) + ": launch shape (" + std::to_string(gx) + ", " +
+                                      std::to_string(gy) + ") x " + std::to_string(block) + " refused");
+    void* ptrs[16];
+    if (n > 16) return fail(X0NE_ERR_GPU, "too many arguments");
+    for (size_t i = 0; i < n; ++i) {
+        switch (args[i].kind) {
+            case X0NE_PARAM_PTR: ptrs[i] = (void*)&args[i].ptr; break;
+            case X0NE_PARAM_U32: ptrs[i] = (void*)&args[i].u32; break;
+            default: ptrs[i] = (void*)&args[i].f32; break;
+        }
+    }
+    g->counts.launches++;
+    X0NE_HIP(hipLaunchKernel(k.fn, dim3(gx, gy), dim3(block), ptrs, 0, g->stream), k.name);
+    return X0NE_OK;
+}
+
+}  // namespace x0ne
+
+extern "C" x0ne_status x0ne_gpu_launch(x0ne_gpu* g, const char* name, uint32_t gx, uint32_t gy, uint32_t block,
+                                       const x0ne_arg* args, size_t n) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    const X0neKernel* k = find_kernel(name);
+    if (!k) return fail(X0NE_ERR_GPU, std::string("no kernel ") + (name ? name : "(null)"));
+    return launch_checked(g, *k, gx, gy, block, args, n);
+}
+
+// Gpu::gemm (gpu.rs:1098-1149) at n = 1 per launch: the bandwidth-bound GEMV of gemv.hip.
+extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n,
+                                     uint64_t y, int out_f32) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    if (rows == 0 || cols == 0 || n == 0 || rows > UINT32_MAX || cols > UINT32_MAX)
+        return fail(X0NE_ERR_FORMAT, "gemv: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
+                                         std::to_string(n));
+    const uint64_t ob = out_f32 ? 4 : 2;
+    for (uint64_t r = 0; r < n; ++r) {
+        const uint16_t* wp = (const uint16_t*)w;
+        const uint16_t* xp = (const uint16_t*)(x + r * cols * 2);
+        void* yp = (void*)(y + r * rows * ob);
+        g->counts.gemms++;
+        const bool fast = cols % 8 == 0 && w % 16 == 0 && (x + r * cols * 2) % 16 == 0 && cols <= 16 * 256 * 8;
+        if (fast) {
+            X0neGemv a = {};
+            a.w = wp;
+            a.x = xp;
+            a.y = yp;
+            a.rows = (uint32_t)rows;
+            a.cols = (uint32_t)cols;
+            a.prologue = 0;
+            a.epilogue = out_f32 ? 1 : 0;
+            const uint32_t rps = x0ne_gemv_rows_per_step((uint32_t)cols);
+            const uint64_t groups = (rows + rps - 1) / rps;
+            const uint64_t cap = (uint64_t)g->cus * 4;
+            a.grid = (uint32_t)(groups < cap ? groups : cap);
+            g->counts.launches++;
+            X0NE_HIP(x0ne_launch_gemv(a, g->stream), "gemv");
+        } else {
+            g->counts.launches++;
+            hipLaunchKernelGGL(x0ne_gemv_any, dim3((uint32_t)rows), dim3(256), 0, g->stream, (const bf16_t*)wp,
+                               (const bf16_t*)xp, yp, (uint32_t)rows, (uint32_t)cols, (uint32_t)(out_f32 ? 1 : 0));
+            X0NE_HIP(hipGetLastError(), "gemv_any");
+        }
+    }
+    return X0NE_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split-K attention (gpu.rs:958-985; ops.rs:80-127)
+// ---------------------------------------------------------------------------------------------
+
+static const void* group_kernel(uint32_t group) {
+    switch (group) {
+        case 1: return (const void*)&x0ne_attention_decode_split_g1_bf16;
+        case 2: return (const void*)&x0ne_attention_decode_split_g2_bf16;
+        case 4: return (const void*)&x0ne_attention_decode_split_g4_bf16;
+        case 8: return (const void*)&x0ne_attention_decode_split_g8_bf16;
+        default: return nullptr;
+    }
+}
+
+// Most slices a merge reads (the merge keeps one weight per slice in LDS).
+static constexpr uint32_t MAX_SPLITS = 1024;
+// P for a decode step: slices of a kv head beyond this add merge work for nothing at the
+// contexts of a decode (a slice of 64-key tiles each).
+static constexpr uint32_t DEFAULT_SPLIT_CAP = 128;
+
+namespace x0ne {
+
+x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out) {
+    if (kv_heads == 0 || q_heads % kv_heads != 0)
+        return fail(X0NE_ERR_GPU, std::to_string(q_heads) + " q heads for " + std::to_string(kv_heads) + " kv heads");
+    const uint32_t group = q_heads / kv_heads;
+    const void* k = group_kernel(group);
+    x0ne_split_plan p = {};
+    p.grouped = k != nullptr;
+    p.group = p.grouped ? group : 1;
+    p.grid_x = p.grouped ? kv_heads : q_heads;
+    if (!k) k = (const void*)&x0ne_attention_decode_split_bf16;
+    int per = 0;
+    X0NE_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, 64, 0), "occupancy of the split kernel");
+    p.per_cu = per > 0 ? (uint32_t)per : 1;
+    uint32_t splits = g->cus * p.per_cu / p.grid_x;
+    if (splits < 1) splits = 1;
+    if (splits > DEFAULT_SPLIT_CAP) splits = DEFAULT_SPLIT_CAP;
+    p.splits = splits;
+    *out = p;
+    return X0NE_OK;
+}
+
+x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_block, const void* q, const void* k,
+                            const void* v, const void* pages, void* state, void* counter, void* out, const void* pos,
+                            uint32_t qh, uint32_t kvh, uint32_t max_ctx, float scale) {
+    const uint32_t p = plan.splits;
+    if (p == 0 || p > MAX_SPLITS) return fail(X0NE_ERR_GPU, "split-K: P " + std::to_string(p) + " outside 1..=1024");
+    if (kvh == 0 || qh % kvh != 0) return fail(X0NE_ERR_GPU, "split-K: heads");
+    if (plan.grouped) {
+        const void* kern = group_kernel(plan.group);
+        if (!kern || plan.group != qh / kvh) return fail(X0NE_ERR_GPU, "split-K: the plan's group differs");
+        void* cnt = last_block ? counter : nullptr;
+        void* o = last_block ? out : nullptr;
+        void* args[] = {(void*)&q, (void*)&k, (void*)&v, (void*)&pages, (void*)&state, (void*)&cnt,
+                        (void*)&o, (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&p, (void*)&scale};
+        g->counts.launches++;
+        X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, p), dim3(64), args, 0, g->stream), "split-K attention");
+        if (last_block) return X0NE_OK;
+    } else {
+        if (last_block) return fail(X0NE_ERR_GPU, "the last-block merge needs a grouped split-K kernel");
+        g->counts.launches++;
+        hipLaunchKernelGGL(x0ne_attention_decode_split_bf16, dim3(qh, p), dim3(64), 0, g->stream,
+                           (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const uint32_t*)pages,
+                           (float*)state, (const uint32_t*)pos, qh, kvh, max_ctx, p, scale);
+        X0NE_HIP(hipGetLastError(), "split-K attention");
+    }
+    g->counts.launches++;
+    hipLaunchKernelGGL(x0ne_attention_merge_bf16, dim3(qh), dim3(64), 0, g->stream, (const float*)state,
+                       (bf16_t*)out, (const uint32_t*)pos, max_ctx, p);
+    X0NE_HIP(hipGetLastError(), "split-K merge");
+    return X0NE_OK;
+}
+
+}  // namespace x0ne
+
+extern "C" x0ne_status x0ne_gpu_split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads,
+                                           x0ne_split_plan* out) {
+    if (!g || !out) return fail(X0NE_ERR_GPU, "no device");
+    return split_plan(g, q_heads, kv_heads, out);
+}
+
+extern "C" x0ne_status x0ne_gpu_attention_split(x0ne_gpu* g, const x0ne_split_plan* plan, int last_block, uint64_t q,
+                                                uint64_t k, uint64_t v, uint64_t page_table, uint64_t state,
+                                                uint64_t counter, uint64_t out, uint64_t pos, uint32_t q_heads,
+                                                uint32_t kv_heads, uint32_t max_ctx, float scale) {
+    if (!g || !plan) return fail(X0NE_ERR_GPU, "no device");
+    return attention_split(g, *plan, last_block, (const void*)q, (const void*)k, (const void*)v,
+                           (const void*)page_table, (void*)state, (void*)counter, (void*)out, (const void*)pos,
+                           q_heads, kv_heads, max_ctx, scale);
+}
+
+extern "C" uint64_t x0ne_split_state_bytes(uint32_t q_heads, uint32_t splits) {
+    return (uint64_t)q_heads * splits * X0NE_SPLIT_STATE_C * 4;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Graph capture (gpu.rs:1170-1238)
+// ---------------------------------------------------------------------------------------------
+
+extern "C" x0ne_status x0ne_gpu_capture_begin(x0ne_gpu* g) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    if (g->capturing) return fail(X0NE_ERR_GPU, "a capture is already open");
+    X0NE_HIP(hipStreamBeginCapture(g->stream, hipStreamCaptureModeGlobal), "hipStreamBeginCapture");
+    g->capturing = true;
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_gpu_capture_end(x0ne_gpu* g, x0ne_graph** out) {
+    if (!g || !out) return fail(X0NE_ERR_GPU, "no device");
+    if (!g->capturing) return fail(X0NE_ERR_GPU, "no capture open");
+    g->capturing = false;
+    hipGraph_t graph = nullptr;
+    X0NE_HIP(hipStreamEndCapture(g->stream, &graph), "hipStreamEndCapture");
+    x0ne_graph* gr = new x0ne_graph();
+    gr->graph = graph;
+    size_t nodes = 0;
+    (void)hipGraphGetNodes(graph, nullptr, &nodes);
+    gr->nodes = nodes;
+    hipError_t e = hipGraphInstantiate(&gr->exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        delete gr;
+        return gpu_fail(e, "hipGraphInstantiate");
+    }
+    *out = gr;
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_gpu_launch_graph(x0ne_gpu* g, const x0ne_graph* graph) {
+    if (!g || !graph) return fail(X0NE_ERR_GPU, "no device or graph");
+    g->counts.graph_launches++;
+    X0NE_HIP(hipGraphLaunch(graph->exec, g->stream), "hipGraphLaunch");
+    return X0NE_OK;
+}
+
+extern "C" size_t x0ne_graph_nodes(const x0ne_graph* graph) { return graph ? graph->nodes : 0; }
+
+extern "C" void x0ne_graph_free(x0ne_graph* graph) {
+    if (!graph) return;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
+// ---------------------------------------------------------------------------------------------
+// The arena (arena.rs)
+// ---------------------------------------------------------------------------------------------
+
+extern "C" x0ne_status x0ne_arena_new(x0ne_arena** out) {
+    if (!out) return fail(X0NE_ERR_ARENA, "null out");
+    x0ne_arena* a = new x0ne_arena();
+    a->id = g_next_arena.fetch_add(1);
+    *out = a;
+    return X0NE_OK;
+}
+
+extern "C" void x0ne_arena_free(x0ne_arena* a) {
+    if (!a) return;
+    if (a->base) {
+        if (a->gpu) {
+            (void)hipStreamSynchronize(a->gpu->stream);
+            (void)hipFree(a->base);
+        } else {
+            std::free(a->base);
+        }
+    }
+    delete a;
+}
+
+extern "C" x0ne_status x0ne_arena_alloc(x0ne_arena* a, const char* label, uint64_t len, uint32_t cls,
+                                        x0ne_slice* out) {
+    if (!a || !out) return fail(X0NE_ERR_ARENA, "null arena");
+    const std::string l = label ? label : "";
+    if (a->frozen) return fail(X0NE_ERR_ARENA, l + ": the arena is frozen, nothing can be added");
+    if (len == 0) return fail(X0NE_ERR_ARENA, l + ": empty region");
+    if (cls != X0NE_CLASS_WEIGHTS && cls != X0NE_CLASS_CLIENT_DATA) return fail(X0NE_ERR_ARENA, l + ": class");
+    const uint64_t A = X0NE_ARENA_ALIGN;
+    if (a->size > UINT64_MAX - (A - 1)) return fail(X0NE_ERR_ARENA, "size overflow");
+    const uint64_t off = (a->size + A - 1) / A * A;
+    if (off > UINT64_MAX - len) return fail(X0NE_ERR_ARENA, "size overflow");
+    a->regions.push_back({l, cls, off, len});
+    a->size = off + len;
+    *out = {a->id, off, len};
+    return X0NE_OK;
+}
+
+extern "C" uint64_t x0ne_arena_planned_bytes(const x0ne_arena* a) { return a ? a->size : 0; }
+
+extern "C" x0ne_status x0ne_arena_freeze(x0ne_arena* a, x0ne_gpu* g) {
+    if (!a) return fail(X0NE_ERR_ARENA, "null arena");
+    if (a->frozen) return fail(X0NE_ERR_ARENA, "already frozen");
+    const uint64_t len = a->size ? a->size : 1;
+    if (g) {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, len);
+        if (e != hipSuccess) return gpu_fail(e, ("hipMalloc of " + std::to_string(len) + " bytes").c_str());
+        a->base = (uint8_t*)p;
+        a->gpu = g;
+    } else {
+        if (len > (uint64_t)SIZE_MAX) return fail(X0NE_ERR_ARENA, "size exceeds host usize");
+        a->base = (uint8_t*)std::malloc(len);
+        if (!a->base) return fail(X0NE_ERR_ARENA, "host allocation of " + std::to_string(len) + " bytes");
+        std::memset(a->base, 0xA5, len);
+    }
+    a->len = len;
+    a->frozen = true;
+    return X0NE_OK;
+}
+
+namespace x0ne {
+x0ne_status arena_check(const x0ne_arena* a, x0ne_slice s, uint64_t at, uint64_t len, uint64_t* off) {
+    if (!a->frozen) return fail(X0NE_ERR_ARENA, "the arena is not frozen");
+    if (s.arena != a->id) return fail(X0NE_ERR_ARENA, "slice from another arena");
+    if (at > UINT64_MAX - len || at + len > s.len)
+        return fail(X0NE_ERR_ARENA, std::to_string(len) + " bytes at " + std::to_string(at) + " exceed a " +
+                                        std::to_string(s.len) + "-byte slice");
+    *off = s.offset + at;
+    return X0NE_OK;
+}
+}  // namespace x0ne
+
+extern "C" x0ne_status x0ne_arena_write(x0ne_arena* a, x0ne_slice s, uint64_t at, const void* data, uint64_t len) {
+    if (!a) return fail(X0NE_ERR_ARENA, "null arena");
+    uint64_t off;
+    X0NE_TRY(arena_check(a, s, at, len, &off));
+    if (len == 0) return X0NE_OK;
+    if (a->gpu) {
+        a->gpu->counts.htod++;
+        X0NE_HIP(hipMemcpyAsync(a->base + off, data, len, hipMemcpyHostToDevice, a->gpu->stream), "arena write");
+        a->gpu->counts.syncs++;
+        X0NE_HIP(hipStreamSynchronize(a->gpu->stream), "arena write");
+    } else {
+        std::memcpy(a->base + off, data, len);
+    }
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_arena_read(const x0ne_arena* a, x0ne_slice s, uint64_t at, void* out, uint64_t len) {
+    if (!a) return fail(X0NE_ERR_ARENA, "null arena");
+    uint64_t off;
+    X0NE_TRY(arena_check(a, s, at, len, &off));
+    if (len == 0) return X0NE_OK;
+    if (a->gpu) {
+        a->gpu->counts.dtoh++;
+        X0NE_HIP(hipMemcpyAsync(out, a->base + off, len, hipMemcpyDeviceToHost, a->gpu->stream), "arena read");
+        a->gpu->counts.syncs++;
+        X0NE_HIP(hipStreamSynchronize(a->gpu->stream), "arena read");
+    } else {
+        std::memcpy(out, a->base + off, len);
+    }
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_arena_addr(const x0ne_arena* a, x0ne_slice s, uint64_t at, uint64_t* out) {
+    if (!a || !out) return fail(X0NE_ERR_ARENA, "null arena");
+    uint64_t off;
+    X0NE_TRY(arena_check(a, s, at, 0, &off));
+    if (at >= s.len)
+        return fail(X0NE_ERR_ARENA, "address " + std::to_string(at) + " past a " + std::to_string(s.len) + "-byte slice");
+    *out = (uint64_t)(uintptr_t)(a->base + off);
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_arena_span(const x0ne_arena* a, x0ne_slice s, uint64_t at, uint64_t len, uint64_t* out) {
+    if (!a || !out) return fail(X0NE_ERR_ARENA, "null arena");
+    if (len == 0) return fail(X0NE_ERR_ARENA, "empty span");
+    uint64_t off;
+    X0NE_TRY(arena_check(a, s, at, len, &off));
+    *out = (uint64_t)(uintptr_t)(a->base + off);
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_arena_scrub(x0ne_arena* a, uint64_t* zeroed) {
+    if (!a) return fail(X0NE_ERR_ARENA, "null arena");
+    if (!a->frozen) return fail(X0NE_ERR_ARENA, "the arena is not frozen");
+    uint64_t total = 0;
+    for (const auto& r : a->regions) {
+        if (r.cls != X0NE_CLASS_CLIENT_DATA) continue;
+        if (a->gpu) {
+            a->gpu->counts.memsets++;
+            X0NE_HIP(hipMemsetAsync(a->base + r.offset, 0, r.len, a->gpu->stream), "scrub");
+        } else {
+            std::memset(a->base + r.offset, 0, r.len);
+        }
+        total += r.len;
+    }
+    if (a->gpu) {
+        a->gpu->counts.syncs++;
+        X0NE_HIP(hipStreamSynchronize(a->gpu->stream), "scrub");
+    }
+    if (zeroed) *zeroed = total;
+    return X0NE_OK;
+}
+
+extern "C" size_t x0ne_arena_region_count(const x0ne_arena* a) { return a ? a->regions.size() : 0; }
+
+extern "C" x0ne_status x0ne_arena_region(const x0ne_arena* a, size_t i, char* label_buf, size_t label_len,
+                                         uint32_t* cls, uint64_t* offset, uint64_t* len) {
+    if (!a || i >= a->regions.size()) return fail(X0NE_ERR_ARENA, "no such region");
+    const auto& r = a->regions[i];
+    if (label_buf && label_len) {
+        std::strncpy(label_buf, r.label.c_str(), label_len - 1);
+        label_buf[label_len - 1] = 0;
+    }
+    if (cls) *cls = r.cls;
+    if (offset) *offset = r.offset;
+    if (len) *len = r.len;
+    return X0NE_OK;
+}
+
+extern "C" x0ne_status x0ne_arena_region_slice(const x0ne_arena* a, size_t i, x0ne_slice* out) {
+    if (!a || !out || i >= a->regions.size()) return fail(X0NE_ERR_ARENA, "no such region");
+    *out = {a->id, a->regions[i].offset, a->regions[i].len};
+    return X0NE_OK;
+}
+
+extern "C" int x0ne_arena_is_frozen(const x0ne_arena* a) { return a && a->frozen ? 1 : 0; }

@@ -1,0 +1,260 @@
+"""The engine (x0ne-core/runtime/src/engine.rs) over the C ABI: Engine, Session, Greedy.
+
+Same names, argument meanings and error behaviour as the reference's Rust API: a Format error
+comes before any device work; one Session at a time per Engine; a Session's logits are valid
+until its next step or finish; a failed step ends the session's steps; finishing, dropping or
+failing zeroes every client byte (device and host)."""
+from __future__ import annotations
+
+import ctypes as C
+import json
+from dataclasses import dataclass
+from enum import IntEnum
+
+import numpy as np
+
+from ._lib import Counts, EngineOptionsC, check, lib
+
+GREEDY_AHEAD = 2  # engine.rs:78
+GREEDY_AHEAD_MAX = 15  # engine.rs:73
+
+
+class Route(IntEnum):
+    PREFILL = 0
+    DECODE = 1
+
+
+class DecodeMode(IntEnum):
+    EAGER = 0
+    GRAPH = 1
+
+
+@dataclass
+class EngineOptions:
+    """EngineOptions (engine.rs:38-40) plus the KV page order (0: identity, else a seeded
+    shuffle)."""
+    max_ctx: int
+    page_seed: int = 0
+
+    def c(self):
+        return EngineOptionsC(self.max_ctx, self.page_seed)
+
+
+def _ids(ids):
+    a = np.ascontiguousarray(ids, dtype=np.uint32)
+    return a, a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+class Engine:
+    def __init__(self, handle, config: dict):
+        self.h = handle
+        self.config = config
+        self._session = None
+
+    @staticmethod
+    def load_from(config_json, files: dict, opts: EngineOptions, index_json=None) -> "Engine":
+        """Engine::load_from (engine.rs:301-309) over in-memory safetensors files {name: bytes}."""
+        if isinstance(config_json, dict):
+            config_json = json.dumps(config_json)
+        names = list(files)
+        blobs = [bytes(files[n]) for n in names]
+        n = len(names)
+        c_names = (C.c_char_p * max(1, n))(*[x.encode() for x in names])
+        keep = [C.create_string_buffer(b, len(b)) for b in blobs]
+        c_data = (C.c_void_p * max(1, n))(*[C.cast(k, C.c_void_p) for k in keep])
+        c_lens = (C.c_uint64 * max(1, n))(*[len(b) for b in blobs])
+        h = C.c_void_p()
+        o = opts.c()
+        idx = index_json.encode() if isinstance(index_json, str) else index_json
+        check(lib().x0ne_engine_load_from(config_json.encode(), n, c_names, c_data, c_lens, idx, C.byref(o),
+                                          C.byref(h)), "Engine::load_from")
+        return Engine(h, json.loads(config_json))
+
+    @staticmethod
+    def load_synthetic(config_json, seed: int, std: float, opts: EngineOptions) -> "Engine":
+        """This build's synthetic checkpoint: projections and embedding N(0, std) bf16 drawn on the
+        device from `seed`, norm weights 1.0."""
+        if isinstance(config_json, dict):
+            config_json = json.dumps(config_json)
+        h = C.c_void_p()
+        o = opts.c()
+        check(lib().x0ne_engine_load_synthetic(config_json.encode(), seed, float(std), C.byref(o), C.byref(h)),
+              "Engine::load_synthetic")
+        return Engine(h, json.loads(config_json))
+
+    def close(self):
+        if getattr(self, "h", None):
+            if self._session is not None:
+                self._session._drop()
+            lib().x0ne_engine_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    # -- requests --
+    def session(self, prompt) -> "Session":
+        """Engine::session (engine.rs:389-406)."""
+        a, p = _ids(prompt)
+        h = C.c_void_p()
+        check(lib().x0ne_engine_session(self.h, p, a.size, C.byref(h)), "session")
+        s = Session(self, h)
+        self._session = s
+        return s
+
+    def greedy_timed(self, prompt, n: int):
+        """Engine::greedy_timed (engine.rs:1026-1038): tokens and per-token host times."""
+        a, p = _ids(prompt)
+        toks = np.zeros(n, np.uint32)
+        times = np.zeros(n, np.float64)
+        check(lib().x0ne_engine_greedy_timed(self.h, p, a.size, n, toks.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                             times.ctypes.data_as(C.POINTER(C.c_double))), "greedy")
+        return toks, times
+
+    def greedy(self, prompt, n: int) -> np.ndarray:
+        return self.greedy_timed(prompt, n)[0]
+
+    def greedy_with_last_logits(self, prompt, n: int):
+        a, p = _ids(prompt)
+        toks = np.zeros(n, np.uint32)
+        logits = np.zeros(self.vocab_size, np.float32)
+        check(lib().x0ne_engine_greedy_with_last_logits(
+            self.h, p, a.size, n, toks.ctypes.data_as(C.POINTER(C.c_uint32)),
+            logits.ctypes.data_as(C.POINTER(C.c_float))), "greedy_with_last_logits")
+        return toks, logits
+
+    def logits_at(self, ids, positions, route: Route = Route.DECODE) -> list:
+        """Engine::logits_at (engine.rs:1012-1020)."""
+        a, p = _ids(ids)
+        pos = np.ascontiguousarray(positions, np.uintp)
+        rows = np.zeros((len(positions), self.vocab_size), np.float32)
+        check(lib().x0ne_engine_logits_at(self.h, p, a.size, pos.ctypes.data_as(C.POINTER(C.c_size_t)), pos.size,
+                                          int(route), rows.ctypes.data_as(C.POINTER(C.c_float))), "logits_at")
+        return [rows[i] for i in range(len(positions))]
+
+    # -- introspection --
+    @property
+    def vocab_size(self) -> int:
+        return int(self.config["vocab_size"])
+
+    def describe(self) -> str:
+        buf = C.create_string_buffer(2048)
+        check(lib().x0ne_engine_describe(self.h, buf, 2048))
+        return buf.value.decode()
+
+    def set_decode_mode(self, mode: DecodeMode):
+        check(lib().x0ne_engine_set_decode_mode(self.h, int(mode)), "set_decode_mode")
+
+    def decode_mode(self) -> DecodeMode:
+        return DecodeMode(lib().x0ne_engine_decode_mode(self.h))
+
+    def graph_nodes(self) -> int:
+        return lib().x0ne_engine_graph_nodes(self.h)
+
+    def splits(self) -> int:
+        return lib().x0ne_engine_splits(self.h)
+
+    def max_ctx(self) -> int:
+        return lib().x0ne_engine_max_ctx(self.h)
+
+    def counts(self) -> dict:
+        c = Counts()
+        check(lib().x0ne_engine_counts(self.h, C.byref(c)))
+        return c.as_dict()
+
+    def client_data_is_zero(self) -> bool:
+        out = C.c_int()
+        check(lib().x0ne_engine_client_data_is_zero(self.h, C.byref(out)))
+        return bool(out.value)
+
+    def host_buffers_are_zero(self) -> bool:
+        return bool(lib().x0ne_engine_host_buffers_are_zero(self.h))
+
+    def arena(self):
+        from .arena import Arena
+        return Arena(lib().x0ne_engine_arena(self.h), owned=False)
+
+    def page(self, i: int) -> int:
+        out = C.c_uint32()
+        check(lib().x0ne_engine_page(self.h, i, C.byref(out)))
+        return out.value
+
+
+class Session:
+    """A request on the engine (engine.rs:1137-1243)."""
+
+    def __init__(self, engine: Engine, handle):
+        self.e, self.h = engine, handle
+
+    def _drop(self):
+        if self.h:
+            lib().x0ne_session_drop(self.h)
+            self.h = None
+            self.e._session = None
+
+    def __del__(self):
+        self._drop()
+
+    def logits(self) -> np.ndarray:
+        """f32 logits of the last position (a copy; empty after a failed step)."""
+        ptr = C.POINTER(C.c_float)()
+        n = C.c_size_t()
+        check(lib().x0ne_session_logits(self.h, C.byref(ptr), C.byref(n)))
+        if not ptr or n.value == 0:
+            return np.zeros(0, np.float32)
+        return np.ctypeslib.as_array(ptr, shape=(n.value,)).copy()
+
+    def position(self) -> int:
+        return lib().x0ne_session_position(self.h)
+
+    def step(self, token: int):
+        check(lib().x0ne_session_step(self.h, int(token) & 0xFFFFFFFF), "step")
+
+    def finish(self):
+        h, self.h = self.h, None
+        self.e._session = None
+        check(lib().x0ne_session_finish(h), "finish")
+
+    def into_greedy(self, max_tokens: int) -> "Greedy":
+        return self.into_greedy_ahead(max_tokens, GREEDY_AHEAD)
+
+    def into_greedy_ahead(self, max_tokens: int, ahead: int) -> "Greedy":
+        h, self.h = self.h, None
+        self.e._session = None
+        out = C.c_void_p()
+        check(lib().x0ne_session_into_greedy(h, max_tokens, ahead, C.byref(out)), "into_greedy")
+        g = Greedy(self.e, out)
+        self.e._session = g
+        return g
+
+
+class Greedy:
+    """A session decoding greedily on the device (engine.rs:1245-1344)."""
+
+    def __init__(self, engine: Engine, handle):
+        self.e, self.h = engine, handle
+
+    def _drop(self):
+        if self.h:
+            lib().x0ne_greedy_drop(self.h)
+            self.h = None
+            self.e._session = None
+
+    def __del__(self):
+        self._drop()
+
+    def next_token(self) -> int:
+        out = C.c_uint32()
+        check(lib().x0ne_greedy_next(self.h, C.byref(out)), "next_token")
+        return out.value
+
+    def taken(self) -> int:
+        return lib().x0ne_greedy_taken(self.h)
+
+    def position(self) -> int:
+        return lib().x0ne_greedy_position(self.h)
+
+    def finish(self):
+        h, self.h = self.h, None
+        self.e._session = None
+        check(lib().x0ne_greedy_finish(h), "finish")

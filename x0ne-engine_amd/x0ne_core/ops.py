@@ -1,0 +1,354 @@
+"""The kernel surface the parity tests call (x0ne-core/runtime/src/ops.rs, `Kernels`): each entry
+point plans an arena for its inputs and outputs, freezes it (the one allocation), uploads, runs
+one kernel on GPU 0 and reads the result back.
+
+Values are numpy arrays: bf16 as uint16 bit patterns, f32 as float32, ids as uint32. K and V
+are given in the reference's logical layout [position][kv_heads][128] and scattered into the
+paged layout [pages][kv_heads][16][128] by `page_of` (logical page -> physical page; identity
+when None); slots past ctx hold a NaN pattern, so a kernel that reads one shows it."""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import FormatError, GpuError
+from .arena import Arena, Class
+from .gpu import Arg, Gpu, SplitPlan, split_state_bytes
+
+HEAD_DIM = 128
+PAGE = 16
+SPLIT_STATE = HEAD_DIM + 4
+NAN_BF16 = 0x7FC0
+
+
+@dataclass(frozen=True)
+class Heads:
+    q_heads: int
+    kv_heads: int
+    head_dim: int = HEAD_DIM
+
+    @property
+    def q_dim(self):
+        return self.q_heads * self.head_dim
+
+    @property
+    def kv_dim(self):
+        return self.kv_heads * self.head_dim
+
+    def check(self):
+        """ops.rs:32-47: head_dim 128, q_heads a multiple of kv_heads."""
+        if self.head_dim != HEAD_DIM:
+            raise FormatError(f"head_dim {self.head_dim} (kernels are built for {HEAD_DIM})")
+        if self.kv_heads == 0 or self.q_heads % self.kv_heads:
+            raise FormatError(f"{self.q_heads} q heads for {self.kv_heads} kv heads")
+
+
+@dataclass(frozen=True)
+class CacheAt:
+    """Where the KV write lands (ops.rs:130-136): layer `layer` of `layers`, position `pos`."""
+    layers: int
+    max_ctx: int
+    layer: int
+    pos: int
+
+
+@dataclass
+class QkvOut:
+    q: np.ndarray
+    k_row: np.ndarray
+    v_row: np.ndarray
+    rest_untouched: bool
+
+
+def inv_freq(head_dim: int, theta: float) -> np.ndarray:
+    """1 / theta^(2i / d) in f32 (ops.rs:210-214), as the host computes it for the device."""
+    t = np.float32(theta)
+    return np.array([np.float32(1.0) / np.float32(t ** (np.float32(2 * i) / np.float32(head_dim)))
+                     for i in range(head_dim // 2)], np.float32)
+
+
+def attn_scale(head_dim: int) -> float:
+    """ops.rs:217-219"""
+    return float(np.float32(1.0 / math.sqrt(head_dim)))
+
+
+def n_pages(ctx: int) -> int:
+    return (ctx + PAGE - 1) // PAGE
+
+
+def to_pages(rows: np.ndarray, kv_heads: int, page_of, pool: int, fill=NAN_BF16) -> np.ndarray:
+    """[ctx][kv_heads * 128] bf16 -> [pool][kv_heads][16][128], row p at page page_of[p // 16]."""
+    ctx = rows.shape[0] if rows.ndim == 2 else rows.size // (kv_heads * HEAD_DIM)
+    rows = rows.reshape(ctx, kv_heads, HEAD_DIM)
+    out = np.full((pool, kv_heads, PAGE, HEAD_DIM), fill, np.uint16)
+    for p in range(ctx):
+        out[page_of[p // PAGE], :, p % PAGE, :] = rows[p]
+    return out
+
+
+class Kernels:
+    """GPU 0 with this library's kernels (ops.rs:229-238)."""
+
+    def __init__(self, gpu: Gpu | None = None):
+        self.gpu = gpu or Gpu()
+
+    def _arena(self):
+        return Arena()
+
+    def _freeze(self, a: Arena) -> Arena:
+        return a.freeze(self.gpu)
+
+    # -- embedding (ops.rs:240-270) --
+    def embedding(self, table: np.ndarray, hidden: int, token: int) -> np.ndarray:
+        if hidden == 0 or hidden % 8 or table.size % hidden:
+            raise FormatError(f"embedding: hidden {hidden}, table of {table.size}")
+        vocab = table.size // hidden
+        a = self._arena()
+        t = a.alloc("table", table.size * 2, Class.WEIGHTS)
+        tok = a.alloc("token", 4, Class.CLIENT_DATA)
+        out = a.alloc("out", hidden * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(t, 0, table.astype(np.uint16))
+        a.write(tok, 0, np.array([token & 0xFFFFFFFF], np.uint32))
+        self.gpu.launch("x0ne_embedding_bf16", 1, 128,
+                        [Arg.ptr(a.ptr(t)), Arg.ptr(a.ptr(tok)), Arg.ptr(a.ptr(out)), Arg.u32(hidden), Arg.u32(vocab)])
+        self.gpu.sync()
+        return a.read_array(out, 0, hidden, np.uint16)
+
+    # -- add_rmsnorm (ops.rs:272-300) --
+    def add_rmsnorm(self, residual, x, w, eps: float):
+        residual = np.ascontiguousarray(residual, np.float32)
+        h = residual.size
+        if h == 0 or x.size != h or w.size != h:
+            raise FormatError("add_rmsnorm: lengths differ")
+        a = self._arena()
+        r = a.alloc("residual", h * 4, Class.CLIENT_DATA)
+        xs = a.alloc("x", h * 2, Class.CLIENT_DATA)
+        ws = a.alloc("w", h * 2, Class.WEIGHTS)
+        out = a.alloc("out", h * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(r, 0, residual)
+        a.write(xs, 0, x.astype(np.uint16))
+        a.write(ws, 0, w.astype(np.uint16))
+        self.gpu.launch("x0ne_add_rmsnorm_bf16", 1, 256,
+                        [Arg.ptr(a.ptr(r)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(out)), Arg.u32(h),
+                         Arg.f32(eps)])
+        self.gpu.sync()
+        return a.read_array(r, 0, h, np.float32), a.read_array(out, 0, h, np.uint16)
+
+    # -- qk_norm_rope_kv_write (ops.rs:302-384), paged --
+    def qk_norm_rope_kv_write(self, qkv, q_norm, k_norm, heads: Heads, theta: float, eps: float, at: CacheAt,
+                              page_of=None, pool=None) -> QkvOut:
+        heads.check()
+        hd, qd, kvd = heads.head_dim, heads.q_dim, heads.kv_dim
+        if qkv.size != qd + 2 * kvd or q_norm.size != hd or k_norm.size != hd:
+            raise FormatError("qk_norm_rope_kv_write: lengths")
+        if at.layer >= at.layers or at.pos >= at.max_ctx:
+            raise FormatError(f"qk_norm_rope_kv_write: {at} out of range")
+        SENTINEL = 0xA5
+        pages = n_pages(at.max_ctx)
+        page_of = list(range(pages)) if page_of is None else list(page_of)
+        pool = pool or pages
+        plane = pool * heads.kv_heads * PAGE * HEAD_DIM * 2
+        cache_bytes = at.layers * 2 * plane
+        a = self._arena()
+        x = a.alloc("qkv", qkv.size * 2, Class.CLIENT_DATA)
+        qn = a.alloc("q_norm", hd * 2, Class.WEIGHTS)
+        kn = a.alloc("k_norm", hd * 2, Class.WEIGHTS)
+        inv = a.alloc("inv_freq", hd // 2 * 4, Class.WEIGHTS)
+        pt = a.alloc("page_table", len(page_of) * 4, Class.WEIGHTS)
+        q = a.alloc("q", qd * 2, Class.CLIENT_DATA)
+        cache = a.alloc("cache", cache_bytes, Class.CLIENT_DATA)
+        pos = a.alloc("pos", 4, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(x, 0, qkv.astype(np.uint16))
+        a.write(qn, 0, q_norm.astype(np.uint16))
+        a.write(kn, 0, k_norm.astype(np.uint16))
+        a.write(inv, 0, inv_freq(hd, theta))
+        a.write(pt, 0, np.array(page_of, np.uint32))
+        a.write(cache, 0, np.full(cache_bytes, SENTINEL, np.uint8))
+        a.write(pos, 0, np.array([at.pos], np.uint32))
+        k_off = at.layer * 2 * plane
+        v_off = k_off + plane
+        self.gpu.launch("x0ne_qk_norm_rope_kv_write_bf16", heads.q_heads + heads.kv_heads, 64,
+                        [Arg.ptr(a.ptr(x)), Arg.ptr(a.ptr(qn)), Arg.ptr(a.ptr(kn)), Arg.ptr(a.ptr(inv)),
+                         Arg.ptr(a.ptr(q)), Arg.ptr(a.addr(cache, k_off)), Arg.ptr(a.addr(cache, v_off)),
+                         Arg.ptr(a.ptr(pt)), Arg.ptr(a.ptr(pos)), Arg.u32(heads.q_heads), Arg.u32(heads.kv_heads),
+                         Arg.u32(at.max_ctx), Arg.f32(eps)])
+        self.gpu.sync()
+        q_out = a.read_array(q, 0, qd, np.uint16)
+        allb = np.frombuffer(a.read(cache, 0, cache_bytes), np.uint8)
+        page = page_of[at.pos // PAGE]
+        written = np.zeros(cache_bytes, bool)
+        k_rows, v_rows = [], []
+        for kh in range(heads.kv_heads):
+            row = ((page * heads.kv_heads + kh) * PAGE + at.pos % PAGE) * HEAD_DIM * 2
+            for base, acc in ((k_off, k_rows), (v_off, v_rows)):
+                s = base + row
+                written[s:s + HEAD_DIM * 2] = True
+                acc.append(allb[s:s + HEAD_DIM * 2].view(np.uint16))
+        rest = bool(np.all(allb[~written] == SENTINEL))
+        return QkvOut(q_out, np.concatenate(k_rows), np.concatenate(v_rows), rest)
+
+    # -- gemv (ops.rs:386-451, the cuBLAS call) --
+    def _gemv(self, w, rows, cols, x, out_f32):
+        if rows == 0 or cols == 0 or w.size != rows * cols or x.size != cols:
+            raise FormatError(f"gemv: W {w.size} for {rows}x{cols}, x {x.size}")
+        ob = 4 if out_f32 else 2
+        a = self._arena()
+        ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
+        xs = a.alloc("x", cols * 2, Class.CLIENT_DATA)
+        ys = a.alloc("y", rows * ob, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ws, 0, w.astype(np.uint16))
+        a.write(xs, 0, x.astype(np.uint16))
+        self.gpu.gemv(a.ptr(ws), rows, cols, a.ptr(xs), 1, a.ptr(ys), out_f32)
+        self.gpu.sync()
+        return a.read_array(ys, 0, rows, np.float32 if out_f32 else np.uint16)
+
+    def gemv_f32_out(self, w, rows, cols, x) -> np.ndarray:
+        return self._gemv(w, rows, cols, x, True)
+
+    def gemv_bf16_out(self, w, rows, cols, x) -> np.ndarray:
+        return self._gemv(w, rows, cols, x, False)
+
+    # -- attention (ops.rs:453-681) --
+    def _kv_arena(self, q, k, v, ctx, h: Heads, page_of, pool, extra):
+        pages = n_pages(ctx)
+        page_of = list(range(pages)) if page_of is None else list(page_of)[:pages]
+        pool = pool or (max(page_of) + 1)
+        kp = to_pages(np.asarray(k, np.uint16)[:ctx * h.kv_dim].reshape(ctx, h.kv_dim), h.kv_heads, page_of, pool)
+        vp = to_pages(np.asarray(v, np.uint16)[:ctx * h.kv_dim].reshape(ctx, h.kv_dim), h.kv_heads, page_of, pool)
+        a = self._arena()
+        sl = {
+            "q": a.alloc("q", q.size * 2, Class.CLIENT_DATA),
+            "k": a.alloc("k", kp.nbytes, Class.CLIENT_DATA),
+            "v": a.alloc("v", vp.nbytes, Class.CLIENT_DATA),
+            "pt": a.alloc("page_table", len(page_of) * 4, Class.WEIGHTS),
+            "pos": a.alloc("pos", 4, Class.CLIENT_DATA),
+        }
+        for name, size in extra:
+            sl[name] = a.alloc(name, size, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.scrub_client_data()
+        a.write(sl["q"], 0, np.asarray(q, np.uint16))
+        a.write(sl["k"], 0, kp)
+        a.write(sl["v"], 0, vp)
+        a.write(sl["pt"], 0, np.array(page_of, np.uint32))
+        return a, sl
+
+    def _check_attention(self, q, k, v, ctx, h: Heads, rows=1):
+        h.check()
+        if ctx == 0 or q.size != rows * h.q_dim or k.size < ctx * h.kv_dim or v.size < ctx * h.kv_dim:
+            raise FormatError("attention: lengths")
+
+    def attention_decode(self, q, k, v, ctx: int, h: Heads, page_of=None, pool=None) -> np.ndarray:
+        """The per-head kernel (the reference's E2 witness)."""
+        self._check_attention(q, k, v, ctx, h)
+        a, s = self._kv_arena(q, k, v, ctx, h, page_of, pool, [("out", h.q_dim * 2)])
+        a.write(s["pos"], 0, np.array([ctx - 1], np.uint32))
+        self.gpu.launch("x0ne_attention_decode_bf16", h.q_heads, 64,
+                        [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
+                         Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])),
+                         Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.f32(attn_scale(h.head_dim))])
+        self.gpu.sync()
+        return a.read_array(s["out"], 0, h.q_dim, np.uint16)
+
+    def split_plan(self, h: Heads) -> SplitPlan:
+        h.check()
+        return self.gpu.split_plan(h.q_heads, h.kv_heads)
+
+    def attention_decode_split(self, q, k, v, ctx: int, h: Heads, last_block=None, splits=None, page_of=None,
+                               pool=None) -> np.ndarray:
+        """Split-K (ops.rs:491-573): the plan's P unless `splits` is given; the merge kernel, or the
+        grouped kernel's last block (last_block True; the default for a grouped plan)."""
+        self._check_attention(q, k, v, ctx, h)
+        plan = self.split_plan(h)
+        if splits is not None:
+            plan.splits = int(splits)
+        if last_block is None:
+            last_block = plan.grouped
+        a, s = self._kv_arena(q, k, v, ctx, h, page_of, pool,
+                              [("out", h.q_dim * 2), ("state", split_state_bytes(h.q_heads, plan.splits)),
+                               ("counter", h.kv_heads * 4)])
+        a.write(s["pos"], 0, np.array([ctx - 1], np.uint32))
+        self.gpu.attention_split(plan, last_block, a.ptr(s["q"]), a.ptr(s["k"]), a.ptr(s["v"]), a.ptr(s["pt"]),
+                                 a.ptr(s["state"]), a.ptr(s["counter"]), a.ptr(s["out"]), a.ptr(s["pos"]),
+                                 h.q_heads, h.kv_heads, ctx, attn_scale(h.head_dim))
+        self.gpu.sync()
+        counts = a.read_array(s["counter"], 0, h.kv_heads, np.uint32)
+        if counts.any():
+            raise GpuError(f"split-K counters not reset: {counts.tolist()}")
+        return a.read_array(s["out"], 0, h.q_dim, np.uint16)
+
+    def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None):
+        """Causal attention for positions pos0..t of a t-position cache in one launch at pos0
+        (ops.rs:724-775); q holds those t - pos0 rows; returns the rows asked for."""
+        h.check()
+        m = t - pos0
+        if m <= 0 or q.size != m * h.q_dim or k.size != t * h.kv_dim or v.size != t * h.kv_dim or \
+                any(r >= m for r in rows):
+            raise FormatError("attention_prefill_at: lengths")
+        a, s = self._kv_arena(q, k, v, t, h, page_of, pool, [("out", m * h.q_dim * 2)])
+        a.write(s["pos"], 0, np.array([pos0], np.uint32))
+        self.gpu.launch("x0ne_attention_prefill_bf16", (h.q_heads, m), 64,
+                        [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
+                         Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(m),
+                         Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(t), Arg.f32(attn_scale(h.head_dim))])
+        self.gpu.sync()
+        out = a.read_array(s["out"], 0, m * h.q_dim, np.uint16).reshape(m, h.q_dim)
+        return [out[r].copy() for r in rows]
+
+    def attention_prefill_rows(self, q, k, v, t: int, h: Heads, rows, page_of=None, pool=None):
+        """ops.rs:683-722: causal attention over t positions, the rows asked for."""
+        if t == 0:
+            raise FormatError("attention_prefill_rows: lengths")
+        return self.attention_prefill_at(q, k, v, t, 0, h, rows, page_of, pool)
+
+    # -- swiglu (ops.rs:777-795, :978-1001) --
+    def swiglu_rows(self, gate_up, rows: int) -> np.ndarray:
+        if rows == 0 or gate_up.size == 0 or gate_up.size % (2 * rows):
+            raise FormatError("swiglu_rows: length is not rows x 2 x inter")
+        inter = gate_up.size // rows // 2
+        a = self._arena()
+        gu = a.alloc("gate_up", gate_up.size * 2, Class.CLIENT_DATA)
+        out = a.alloc("out", rows * inter * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(gu, 0, gate_up.astype(np.uint16))
+        self.gpu.launch("x0ne_swiglu_bf16", ((inter + 255) // 256, rows), 256,
+                        [Arg.ptr(a.ptr(gu)), Arg.ptr(a.ptr(out)), Arg.u32(inter)])
+        self.gpu.sync()
+        return a.read_array(out, 0, rows * inter, np.uint16)
+
+    def swiglu(self, gate_up) -> np.ndarray:
+        if gate_up.size == 0 or gate_up.size % 2:
+            raise FormatError("swiglu: odd length")
+        return self.swiglu_rows(gate_up, 1)
+
+    # -- advance, argmax (ops.rs:925-976) --
+    def advance(self, value: int) -> int:
+        a = self._arena()
+        pos = a.alloc("pos", 4, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(pos, 0, np.array([value & 0xFFFFFFFF], np.uint32))
+        self.gpu.launch("x0ne_advance_u32", 1, 64, [Arg.ptr(a.ptr(pos))])
+        self.gpu.sync()
+        return int(a.read_array(pos, 0, 1, np.uint32)[0])
+
+    def argmax(self, logits) -> int:
+        logits = np.ascontiguousarray(logits, np.float32)
+        if logits.size == 0:
+            raise FormatError("argmax: empty")
+        a = self._arena()
+        ls = a.alloc("logits", logits.size * 4, Class.CLIENT_DATA)
+        out = a.alloc("out", 4, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ls, 0, logits)
+        self.gpu.launch("x0ne_argmax_f32", 1, 1024, [Arg.ptr(a.ptr(ls)), Arg.u32(logits.size), Arg.ptr(a.ptr(out))])
+        self.gpu.sync()
+        v = int(a.read_array(out, 0, 1, np.uint32)[0])
+        if v >= logits.size:
+            raise GpuError("argmax: no finite maximum (NaN row)")
+        return v
