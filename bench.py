@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""Qwen3-8B bf16 batch-1 greedy decode on one MI355X, the metric BASELINE.json names:
+"Qwen3-8B bf16 decode tok/s @batch1; decode HBM GB/s vs 8 TB/s peak".
+
+Workload: Qwen3-8B shape (36 layers, hidden 4096, 32 q / 8 kv heads,
+head_dim 128, intermediate 12288, vocab 151936, untied), random-init bf16 weights N(0, 0.02) drawn
+on the device from seed 0 (norm weights 1.0), a 20-token prompt of uniform random ids
+(splitmix64 seed 0), then greedy decode steps at batch 1, each step one replay of the captured
+HIP graph. A step is one decode step (one token); W untimed steps, then exactly K steps timed
+between two stream synchronisations. value = K / seconds.
+
+Also printed, in the same JSON line:
+- roofline: the dominant kernel (the gate/up GEMV with its fused RMSNorm and SwiGLU, 201 MB of
+  weights per launch) timed alone with HIP events on the engine's stream over every layer's
+  weights; achieved = algorithmic bytes per launch / average launch time, against 8 TB/s.
+- decode_hbm: bytes per step (roofline.rs formula: every weight once + K/V of the attended
+  positions) x steps / s, against 8 TB/s.
+- cpu_baseline: the CPU oracle (oracle/, a C restatement of the reference's Rust oracle, f64
+  inside) on this host's cores, on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "x0ne-engine_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+QWEN3_8B = {
+    "model_type": "qwen3", "dtype": "bfloat16", "hidden_act": "silu", "attention_bias": False,
+    "hidden_size": 4096, "intermediate_size": 12288, "num_hidden_layers": 36, "num_attention_heads": 32,
+    "num_key_value_heads": 8, "head_dim": 128, "vocab_size": 151936, "max_position_embeddings": 40960,
+    "rms_norm_eps": 1e-6, "rope_theta": 1e6, "tie_word_embeddings": False,
+}
+PROMPT = 20
+SEED = 0
+STD = 0.02
+
+
+def splitmix_ids(n: int, vocab: int, seed: int) -> np.ndarray:
+    """Uniform ids from splitmix64 (oracle/tests/common/mod.rs:15-25; core-perf.rs:17-28)."""
+    out, s = [], seed
+    M = (1 << 64) - 1
+    for _ in range(n):
+        s = (s + 0x9E3779B97F4A7C15) & M
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        out.append((z ^ (z >> 31)) % vocab)
+    return np.array(out, np.uint32)
+
+
+def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, prompt_len: int = 4) -> dict:
+    """The CPU oracle on the same shape and weights (drawn by the oracle's generator, the same
+    bits as the device's): a `prompt_len`-token prompt, then `steps` greedy decode steps; tok/s
+    over the decode steps. Also one thread on two steps, the reference oracle being
+    single-threaded."""
+    from oracle import oracle as O
+    c = O.Config(cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"],
+                 cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"], cfg["vocab_size"],
+                 cfg["max_position_embeddings"], eps=cfg["rms_norm_eps"], theta=cfg["rope_theta"],
+                 tied=cfg["tie_word_embeddings"])
+    O.set_threads(threads)
+    m = O.Model(c, weights_bf16=True)
+    t = time.perf_counter()
+    m.init_normal(SEED, STD)
+    init_s = time.perf_counter() - t
+    m.reset()
+    logits = m.extend(prompt[:prompt_len])
+    times = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = O.argmax(logits)
+        logits = m.step(tok)
+        times.append(time.perf_counter() - t0)
+    value = steps / times[-1]
+    O.set_threads(1)
+    t0 = time.perf_counter()
+    logits = m.step(O.argmax(logits))
+    single = 1 / (time.perf_counter() - t0)
+    O.set_threads(threads)
+    return {"value": round(value, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "single_thread_value": round(single, 4),
+            "sample": f"Qwen3-8B shape, the same N(0,{STD}) bf16 weights (seed {SEED}, drawn by the oracle's "
+                      f"generator in {init_s:.1f} s, not timed), {prompt_len}-token prompt, {steps} greedy decode "
+                      f"steps timed on {threads} threads (rows split, f64 sums in the reference's order); "
+                      f"single_thread_value: 1 step on 1 thread"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--runs", type=int, default=3, help="timed runs; the median is reported")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
+    ap.add_argument("--kernel-iters", type=int, default=4)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); every box here has one, "
+              "and no figure at several GPUs is produced. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from x0ne_core import Engine, EngineOptions, roofline
+
+    cfg = QWEN3_8B
+    prompt = splitmix_ids(PROMPT, cfg["vocab_size"], SEED)
+    n_tokens = args.warmup + args.steps + 1
+    t = time.perf_counter()
+    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=PROMPT + n_tokens + 16, page_seed=1))
+    load_s = time.perf_counter() - t
+    print(f"[bench] loaded in {load_s:.1f} s: {e.describe()}", file=sys.stderr, flush=True)
+
+    runs, tokens = [], None
+    for r in range(args.runs):
+        toks, secs = e.decode_timed(prompt, args.warmup, args.steps)
+        if tokens is None:
+            tokens = toks
+        elif not (toks == tokens).all():
+            raise SystemExit("two runs gave different tokens: the measure is not of one computation")
+        runs.append(secs)
+        print(f"[bench] run {r}: {args.steps / secs:.2f} tok/s", file=sys.stderr, flush=True)
+    secs = sorted(runs)[len(runs) // 2]
+    tok_s = args.steps / secs
+
+    shape = roofline.Shape.of(cfg)
+    # Steps w+1..w+K attend prompt + w + 1 .. prompt + w + K positions.
+    mean_ctx = PROMPT + args.warmup + (args.steps + 1) / 2.0
+    step_bytes = roofline.step_bytes(shape, mean_ctx)
+    hbm_gbs = step_bytes * tok_s / 1e9
+
+    # The dominant kernel alone: gate/up GEMV (fused add + RMSNorm in front, SwiGLU behind).
+    h, inter = cfg["hidden_size"], cfg["intermediate_size"]
+    # Weights, the residual read (f32) and written (f32, block 0), delta and the norm weight (bf16),
+    # the SwiGLU output (inter bf16).
+    gu_bytes = 2 * inter * h * 2 + 4 * h + 4 * h + 2 * h + 2 * h + 2 * inter
+    avg_us, launches = e.time_kernel("gate_up", args.kernel_iters)
+    achieved = gu_bytes / (avg_us * 1e-6) / 1e9
+    others = {}
+    for k in ("qkv", "o", "down", "head", "attention"):
+        us, _ = e.time_kernel(k, args.kernel_iters)
+        others[k] = round(us, 2)
+    print(f"[bench] gate_up {avg_us:.2f} us ({achieved:.0f} GB/s); others us {others}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        try:
+            cpu = cpu_baseline(cfg, prompt, threads)
+        except Exception as ex:  # a baseline that cannot run is reported as missing, not as the GPU's failure
+            cpu = {"value": None, "error": str(ex)}
+        print(f"[bench] cpu baseline {cpu}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "Qwen3-8B bf16 decode tok/s @batch1; decode HBM GB/s vs 8 TB/s peak",
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * secs / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init N(0,0.02) bf16 weights (seed 0), uniform random token ids (seed 0)",
+        "config": {"workload": "Qwen3-8B-shape batch-1 greedy decode, 20-token prompt, hipGraph per step",
+                   "layers": 36, "hidden": 4096, "heads": "32q/8kv", "head_dim": 128, "intermediate": 12288,
+                   "vocab": 151936, "prompt": PROMPT, "mean_ctx": mean_ctx, "runs": runs},
+        "decode_hbm": {"achieved": round(hbm_gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                       "frac": round(hbm_gbs / 8000.0, 4), "bytes_per_step": int(step_bytes),
+                       "ceiling_tok_s": round(roofline.ceiling_tok_s(shape, mean_ctx), 2)},
+        "roofline": {"kernel": "gate_up GEMV (add+RMSNorm prologue, SwiGLU epilogue)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(achieved / 8000.0, 4), "traffic": None, "bytes_per_launch": gu_bytes,
+                     "avg_us": round(avg_us, 3), "launches_timed": launches, "other_kernels_us": others},
+        "cpu_baseline": cpu,
+        "tokens_head": tokens[:8].tolist(),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

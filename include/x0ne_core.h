@@ -220,6 +220,13 @@ x0ne_status x0ne_engine_greedy_timed(x0ne_engine* e, const uint32_t* prompt, siz
 x0ne_status x0ne_engine_greedy_with_last_logits(x0ne_engine* e, const uint32_t* prompt, size_t n_prompt, size_t n,
                                                 uint32_t* tokens, float* logits);
 
+/* The bench's decode measure (the method of x0ne-core/oracle/examples/core-perf.rs:77-94, with
+   the timed region bracketed by stream synchronisations): prefill `prompt`, run `warmup` decode
+   steps, synchronise, then time `steps` decode steps to a final synchronisation. tokens receives
+   warmup + steps + 1 greedy tokens; seconds the timed region. Client bytes are zeroed after. */
+x0ne_status x0ne_engine_decode_timed(x0ne_engine* e, const uint32_t* prompt, size_t n_prompt, size_t warmup,
+                                     size_t steps, uint32_t* tokens, double* seconds);
+
 /* Route (engine.rs:44-48) and DecodeMode (engine.rs:51-55). */
 typedef enum { X0NE_ROUTE_PREFILL = 0, X0NE_ROUTE_DECODE = 1 } x0ne_route;
 typedef enum { X0NE_DECODE_EAGER = 0, X0NE_DECODE_GRAPH = 1 } x0ne_decode_mode;
@@ -244,6 +251,21 @@ uint64_t x0ne_engine_max_ctx(const x0ne_engine* e);
 const x0ne_arena* x0ne_engine_arena(const x0ne_engine* e);
 /* Physical page of logical page i (this build's paged KV arena). */
 x0ne_status x0ne_engine_page(const x0ne_engine* e, uint64_t i, uint32_t* out);
+
+/* One kernel of the decode step timed alone with HIP events on the engine's stream (this
+   build's measurement hook, the analogue of ops.rs:585-681 attention_decode_timed): `iters`
+   rounds over every layer's weights (so no cache holds them), after one warm-up round; the
+   average duration of one launch in microseconds. Client bytes are zeroed afterwards. */
+typedef enum {
+    X0NE_KERNEL_QKV = 0,
+    X0NE_KERNEL_ATTENTION = 1,
+    X0NE_KERNEL_O = 2,
+    X0NE_KERNEL_GATE_UP = 3,
+    X0NE_KERNEL_DOWN = 4,
+    X0NE_KERNEL_HEAD = 5,
+} x0ne_step_kernel;
+x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* avg_us,
+                                    uint64_t* launches);
 
 /* The reference's constants (engine.rs:67-79; kernels/src/lib.rs:135-144). */
 #define X0NE_GREEDY_AHEAD 2

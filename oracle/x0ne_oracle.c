@@ -49,7 +49,8 @@ uint16_t xo_bf16_bits(float x) {
 }
 
 /* bf16.rs:5-7 */
-float xo_bf16_value(uint16_t b) { return f32_of((uint32_t)b << 16); }
+static inline float bf16v(uint16_t b) { return f32_of((uint32_t)b << 16); }
+float xo_bf16_value(uint16_t b) { return bf16v(b); }
 
 /* bf16.rs:23-25 */
 float xo_bf16_round(float x) { return xo_bf16_value(xo_bf16_bits(x)); }
@@ -192,8 +193,7 @@ void xo_det_sincos_turn(double u, double* s, double* c) {
 /* Value i of stream `key`: pair k = i / 2 takes splitmix64 outputs 2k and 2k + 1 of a generator
    seeded with `key`; u1 = (r1 >> 11 + 1) 2^-53 in (0, 1], u2 = (r2 >> 11) 2^-53 in [0, 1);
    value 2k = sqrt(-2 ln u1) cos(2 pi u2), value 2k + 1 = sqrt(-2 ln u1) sin(2 pi u2). */
-double xo_normal_at(uint64_t key, uint64_t i) {
-    uint64_t k = i >> 1;
+static void normal_pair(uint64_t key, uint64_t k, double* z0, double* z1) {
     uint64_t r1 = fmix(key + (2 * k + 1) * GOLDEN);
     uint64_t r2 = fmix(key + (2 * k + 2) * GOLDEN);
     double u1 = (double)((r1 >> 11) + 1) * 0x1p-53;
@@ -201,13 +201,28 @@ double xo_normal_at(uint64_t key, uint64_t i) {
     double rad = sqrt(-2.0 * xo_det_log(u1));
     double s, c;
     xo_det_sincos_turn(u2, &s, &c);
-    return (i & 1) ? rad * s : rad * c;
+    *z0 = rad * c;
+    *z1 = rad * s;
+}
+
+double xo_normal_at(uint64_t key, uint64_t i) {
+    double z0, z1;
+    normal_pair(key, i >> 1, &z0, &z1);
+    return (i & 1) ? z1 : z0;
 }
 
 void xo_normal_bf16(uint64_t key, uint64_t first, size_t n, double std_dev, uint16_t* out) {
-    for (size_t j = 0; j < n; ++j) {
-        double z = xo_normal_at(key, first + j);
-        out[j] = xo_bf16_bits((float)(std_dev * z));
+    size_t j = 0;
+    while (j < n) {
+        uint64_t i = first + j;
+        double z0, z1;
+        normal_pair(key, i >> 1, &z0, &z1);
+        if ((i & 1) == 0) {
+            out[j++] = xo_bf16_bits((float)(std_dev * z0));
+            if (j < n) out[j++] = xo_bf16_bits((float)(std_dev * z1));
+        } else {
+            out[j++] = xo_bf16_bits((float)(std_dev * z1));
+        }
     }
 }
 
@@ -244,10 +259,14 @@ static void range_of(int t, int threads, size_t n, size_t* b, size_t* e) {
     if (*e > n) *e = n;
 }
 
+/* A worker starts having seen every task posted before it was created (the round set_threads
+   hands it), so it never runs a finished task's stale arguments. */
+static uint64_t start_round[256];
+
 static void* worker(void* p) {
     int me = (int)(intptr_t)p;
-    uint64_t seen = 0;
     pthread_mutex_lock(&P.mu);
+    uint64_t seen = start_round[me];
     for (;;) {
         while (P.round == seen && !P.stop) pthread_cond_wait(&P.go, &P.mu);
         if (P.stop) break;
@@ -283,6 +302,9 @@ void xo_set_threads(int n) {
     if (n > 256) n = 256;
     if (P.started) pool_stop();
     P.threads = n;
+    pthread_mutex_lock(&P.mu);
+    for (int i = 1; i < n; ++i) start_round[i] = P.round;
+    pthread_mutex_unlock(&P.mu);
     for (int i = 1; i < n; ++i) pthread_create(&P.tid[i], NULL, worker, (void*)(intptr_t)i);
     P.started = n;
     pthread_mutex_unlock(&call_mu);
@@ -398,7 +420,7 @@ typedef struct {
 } gemv_job;
 
 static inline double wval(const gemv_job* j, size_t idx) {
-    if (j->bf16) return (double)xo_bf16_value(((const uint16_t*)j->w)[idx]);
+    if (j->bf16) return (double)bf16v(((const uint16_t*)j->w)[idx]);
     return (double)((const float*)j->w)[idx];
 }
 
@@ -414,10 +436,10 @@ static void gemv_rows(void* p, size_t b, size_t e) {
             const uint16_t* w2 = w1 + cols;
             const uint16_t* w3 = w2 + cols;
             for (size_t c = 0; c < cols; ++c) {
-                s0 += (double)xo_bf16_value(w0[c]) * x[c];
-                s1 += (double)xo_bf16_value(w1[c]) * x[c];
-                s2 += (double)xo_bf16_value(w2[c]) * x[c];
-                s3 += (double)xo_bf16_value(w3[c]) * x[c];
+                s0 += (double)bf16v(w0[c]) * x[c];
+                s1 += (double)bf16v(w1[c]) * x[c];
+                s2 += (double)bf16v(w2[c]) * x[c];
+                s3 += (double)bf16v(w3[c]) * x[c];
             }
         } else {
             const float* w0 = (const float*)j->w + r * cols;

@@ -396,118 +396,148 @@ void plan_grids(x0ne_engine* e) {
     e->grid_head = grid_for(e, groups(c.vocab, x0ne_gemv_rows_per_step((uint32_t)c.hidden)));
 }
 
-// The launches of one decode step at the device's pos on the device's tokens[0]: forward,
-// logits, argmax into tokens[0], pos += 1. No host copy and no synchronisation, so the
-// sequence can be captured (engine.rs:495-501, :718-839).
-x0ne_status step_launches(x0ne_engine* e) {
+// The kernels of one decode step, one helper each. Norm j of the step reads residual buffer
+// j % 2 and writes (j + 1) % 2: layer l's QKV norm is j = 2l, its gate/up norm 2l + 1, the final
+// norm 2L.
+float* residual_buf(const x0ne_engine* e, int k) { return (float*)e->d(e->residual) + (k & 1) * e->c.hidden; }
+
+x0ne_status launch_qkv(x0ne_engine* e, uint64_t l) {
     const Cfg& c = e->c;
-    x0ne_gpu* g = e->gpu;
-    hipStream_t s = g->stream;
-    const uint32_t h = (uint32_t)c.hidden, qd = (uint32_t)c.q_dim(), inter = (uint32_t)c.inter;
-    const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads, maxc = (uint32_t)e->max_ctx;
-    const float eps = (float)c.eps;
+    const LayerW& w = e->L[l];
+    X0neGemv a = {};
+    a.w = (const uint16_t*)e->d(w.qkv);
+    a.res_in = residual_buf(e, 0);
+    a.res_out = residual_buf(e, 1);
+    a.delta = (const uint16_t*)e->d(e->delta);
+    a.norm_w = (const uint16_t*)e->d(w.input_norm);
+    a.embed = (const uint16_t*)e->d(e->embed);
+    a.tokens = (const uint32_t*)e->d(e->tokens);
+    a.vocab = (uint32_t)c.vocab;
+    a.y = e->d(e->qkv);
+    a.rows = (uint32_t)c.qkv_rows();
+    a.cols = (uint32_t)c.hidden;
+    a.eps = (float)c.eps;
+    a.prologue = l == 0 ? 2 : 1;  // layer 0 adds the embedding row to a zero residual
+    a.epilogue = 0;
+    a.grid = e->grid_qkv;
+    e->gpu->counts.launches++;
+    X0NE_HIP(x0ne_launch_gemv(a, e->gpu->stream), "qkv gemv");
+    return X0NE_OK;
+}
+
+x0ne_status launch_rope(x0ne_engine* e, uint64_t l) {
+    const Cfg& c = e->c;
+    const LayerW& w = e->L[l];
+    const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads;
+    e->gpu->counts.launches++;
+    hipLaunchKernelGGL(x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, 1), dim3(64), 0, e->gpu->stream,
+                       (const bf16_t*)e->d(e->qkv), (const bf16_t*)e->d(w.q_norm), (const bf16_t*)e->d(w.k_norm),
+                       (const float*)e->d(e->inv_freq), (bf16_t*)e->d(e->q), (bf16_t*)e->plane(l, 0),
+                       (bf16_t*)e->plane(l, 1), (const uint32_t*)e->d(e->page_table), (const uint32_t*)e->d(e->pos),
+                       qh, kvh, (uint32_t)e->max_ctx, (float)c.eps);
+    X0NE_HIP(hipGetLastError(), "qk_norm_rope_kv_write");
+    return X0NE_OK;
+}
+
+x0ne_status launch_attention(x0ne_engine* e, uint64_t l) {
+    const Cfg& c = e->c;
     const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));  // ops.rs:217-219
-    float* r0 = (float*)e->d(e->residual);
-    float* r1 = r0 + c.hidden;
-    const uint16_t* delta = (const uint16_t*)e->d(e->delta);
-    const uint32_t* tokens = (const uint32_t*)e->d(e->tokens);
-    uint32_t* pos = (uint32_t*)e->d(e->pos);
-    for (uint64_t l = 0; l < c.layers; ++l) {
-        const LayerW& w = e->L[l];
-        // QKV: norm 2l (reads r0, writes r1); layer 0 adds the embedding to a zero residual.
-        X0neGemv a = {};
-        a.w = (const uint16_t*)e->d(w.qkv);
-        a.res_in = r0;
-        a.res_out = r1;
-        a.delta = delta;
-        a.norm_w = (const uint16_t*)e->d(w.input_norm);
-        a.embed = (const uint16_t*)e->d(e->embed);
-        a.tokens = tokens;
-        a.vocab = (uint32_t)c.vocab;
-        a.y = e->d(e->qkv);
-        a.rows = (uint32_t)c.qkv_rows();
-        a.cols = h;
-        a.eps = eps;
-        a.prologue = l == 0 ? 2 : 1;
-        a.epilogue = 0;
-        a.grid = e->grid_qkv;
-        g->counts.launches++;
-        X0NE_HIP(x0ne_launch_gemv(a, s), "qkv gemv");
-        // QK-norm, RoPE, the K/V rows into their page.
-        g->counts.launches++;
-        hipLaunchKernelGGL(x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, 1), dim3(64), 0, s,
-                           (const bf16_t*)e->d(e->qkv), (const bf16_t*)e->d(w.q_norm), (const bf16_t*)e->d(w.k_norm),
-                           (const float*)e->d(e->inv_freq), (bf16_t*)e->d(e->q), (bf16_t*)e->plane(l, 0),
-                           (bf16_t*)e->plane(l, 1), (const uint32_t*)e->d(e->page_table), (const uint32_t*)pos, qh,
-                           kvh, maxc, eps);
-        X0NE_HIP(hipGetLastError(), "qk_norm_rope_kv_write");
-        // Split-K attention, merged by its last block when grouped.
-        X0NE_TRY(attention_split(g, e->split, e->split.grouped ? 1 : 0, e->d(e->q), e->plane(l, 0), e->plane(l, 1),
-                                 e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn), pos,
-                                 qh, kvh, maxc, scale));
-        // O projection.
-        X0neGemv o = {};
-        o.w = (const uint16_t*)e->d(w.o);
-        o.x = (const uint16_t*)e->d(e->attn);
-        o.y = e->d(e->delta);
-        o.rows = h;
-        o.cols = qd;
-        o.prologue = 0;
-        o.epilogue = 0;
-        o.grid = e->grid_o;
-        g->counts.launches++;
-        X0NE_HIP(x0ne_launch_gemv(o, s), "o gemv");
-        // gate/up: norm 2l + 1 (reads r1, writes r0), SwiGLU behind.
-        X0neGemv gu = {};
-        gu.w = (const uint16_t*)e->d(w.gate_up);
-        gu.res_in = r1;
-        gu.res_out = r0;
-        gu.delta = delta;
-        gu.norm_w = (const uint16_t*)e->d(w.post_norm);
-        gu.y = e->d(e->act);
-        gu.rows = 2 * inter;
-        gu.cols = h;
-        gu.eps = eps;
-        gu.prologue = 1;
-        gu.epilogue = 2;
-        gu.grid = e->grid_gu;
-        g->counts.launches++;
-        X0NE_HIP(x0ne_launch_gemv(gu, s), "gate_up gemv");
-        // down projection.
-        X0neGemv dn = {};
-        dn.w = (const uint16_t*)e->d(w.down);
-        dn.x = (const uint16_t*)e->d(e->act);
-        dn.y = e->d(e->delta);
-        dn.rows = h;
-        dn.cols = inter;
-        dn.prologue = 0;
-        dn.epilogue = 0;
-        dn.grid = e->grid_down;
-        g->counts.launches++;
-        X0NE_HIP(x0ne_launch_gemv(dn, s), "down gemv");
-    }
-    // Final norm 2L (reads r0), the LM head, argmax into tokens[0], pos += 1.
+    return attention_split(e->gpu, e->split, e->split.grouped ? 1 : 0, e->d(e->q), e->plane(l, 0), e->plane(l, 1),
+                           e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn),
+                           e->d(e->pos), (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, scale);
+}
+
+x0ne_status launch_o(x0ne_engine* e, uint64_t l) {
+    const Cfg& c = e->c;
+    X0neGemv o = {};
+    o.w = (const uint16_t*)e->d(e->L[l].o);
+    o.x = (const uint16_t*)e->d(e->attn);
+    o.y = e->d(e->delta);
+    o.rows = (uint32_t)c.hidden;
+    o.cols = (uint32_t)c.q_dim();
+    o.prologue = 0;
+    o.epilogue = 0;
+    o.grid = e->grid_o;
+    e->gpu->counts.launches++;
+    X0NE_HIP(x0ne_launch_gemv(o, e->gpu->stream), "o gemv");
+    return X0NE_OK;
+}
+
+x0ne_status launch_gate_up(x0ne_engine* e, uint64_t l) {
+    const Cfg& c = e->c;
+    X0neGemv gu = {};
+    gu.w = (const uint16_t*)e->d(e->L[l].gate_up);
+    gu.res_in = residual_buf(e, 1);
+    gu.res_out = residual_buf(e, 0);
+    gu.delta = (const uint16_t*)e->d(e->delta);
+    gu.norm_w = (const uint16_t*)e->d(e->L[l].post_norm);
+    gu.y = e->d(e->act);
+    gu.rows = (uint32_t)(2 * c.inter);
+    gu.cols = (uint32_t)c.hidden;
+    gu.eps = (float)c.eps;
+    gu.prologue = 1;
+    gu.epilogue = 2;  // SwiGLU over [gate; up]
+    gu.grid = e->grid_gu;
+    e->gpu->counts.launches++;
+    X0NE_HIP(x0ne_launch_gemv(gu, e->gpu->stream), "gate_up gemv");
+    return X0NE_OK;
+}
+
+x0ne_status launch_down(x0ne_engine* e, uint64_t l) {
+    const Cfg& c = e->c;
+    X0neGemv dn = {};
+    dn.w = (const uint16_t*)e->d(e->L[l].down);
+    dn.x = (const uint16_t*)e->d(e->act);
+    dn.y = e->d(e->delta);
+    dn.rows = (uint32_t)c.hidden;
+    dn.cols = (uint32_t)c.inter;
+    dn.prologue = 0;
+    dn.epilogue = 0;
+    dn.grid = e->grid_down;
+    e->gpu->counts.launches++;
+    X0NE_HIP(x0ne_launch_gemv(dn, e->gpu->stream), "down gemv");
+    return X0NE_OK;
+}
+
+// Final norm, the LM head (f32 logits), the argmax into tokens[0] and pos += 1.
+x0ne_status launch_head(x0ne_engine* e) {
+    const Cfg& c = e->c;
     X0neGemv hd = {};
     hd.w = (const uint16_t*)e->d(e->has_lm_head ? e->lm_head : e->embed);
-    hd.res_in = r0;
+    hd.res_in = residual_buf(e, 0);
     hd.res_out = nullptr;
-    hd.delta = delta;
+    hd.delta = (const uint16_t*)e->d(e->delta);
     hd.norm_w = (const uint16_t*)e->d(e->final_norm);
     hd.y = e->d(e->logits);
     hd.partial = (float*)e->d(e->head_partial);
     hd.counter = (uint32_t*)e->d(e->head_counter);
-    hd.token_out = (uint32_t*)tokens;
-    hd.pos = pos;
+    hd.token_out = (uint32_t*)e->d(e->tokens);
+    hd.pos = (uint32_t*)e->d(e->pos);
     hd.advance = 1;
     hd.rows = (uint32_t)c.vocab;
-    hd.cols = h;
-    hd.eps = eps;
+    hd.cols = (uint32_t)c.hidden;
+    hd.eps = (float)c.eps;
     hd.prologue = 1;
     hd.epilogue = 3;
     hd.grid = e->grid_head;
-    g->counts.launches++;
-    X0NE_HIP(x0ne_launch_gemv(hd, s), "lm_head gemv");
+    e->gpu->counts.launches++;
+    X0NE_HIP(x0ne_launch_gemv(hd, e->gpu->stream), "lm_head gemv");
     return X0NE_OK;
+}
+
+// The launches of one decode step at the device's pos on the device's tokens[0]: forward,
+// logits, argmax into tokens[0], pos += 1. No host copy and no synchronisation, so the
+// sequence can be captured (engine.rs:495-501, :718-839).
+x0ne_status step_launches(x0ne_engine* e) {
+    for (uint64_t l = 0; l < e->c.layers; ++l) {
+        X0NE_TRY(launch_qkv(e, l));
+        X0NE_TRY(launch_rope(e, l));
+        X0NE_TRY(launch_attention(e, l));
+        X0NE_TRY(launch_o(e, l));
+        X0NE_TRY(launch_gate_up(e, l));
+        X0NE_TRY(launch_down(e, l));
+    }
+    return launch_head(e);
 }
 
 x0ne_status run_step(x0ne_engine* e) {
@@ -1054,6 +1084,47 @@ extern "C" x0ne_status x0ne_engine_greedy_timed(x0ne_engine* e, const uint32_t* 
     return st != X0NE_OK ? st : sc;
 }
 
+// The bench's decode measure: the prompt, `warmup` decode steps, a stream synchronisation, then
+// `steps` decode steps timed on the host clock between two synchronisations. Per step one
+// graph launch and one 4-byte copy into the host ring, RING - 1 steps in flight, as in
+// greedy_inner. tokens gets warmup + steps + 1 tokens (the first from the prompt).
+extern "C" x0ne_status x0ne_engine_decode_timed(x0ne_engine* e, const uint32_t* prompt, size_t np, size_t warmup,
+                                                size_t steps, uint32_t* tokens, double* seconds) {
+    if (!e || !tokens || !seconds || steps == 0) return fail(X0NE_ERR_FORMAT, "null argument");
+    const size_t n = warmup + steps + 1;
+    X0NE_TRY(greedy_checks(e, prompt, np, n));
+    auto body = [&]() -> x0ne_status {
+        X0NE_TRY(prefill(e, prompt, np));
+        X0NE_TRY(read_token(e, &tokens[0]));
+        size_t next = 1;
+        auto collect = [&](size_t j) -> x0ne_status {
+            uint32_t t = 0;
+            X0NE_TRY(ring_take(e, j, &t));
+            if (t >= e->c.vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
+            tokens[j] = t;
+            return X0NE_OK;
+        };
+        auto run = [&](size_t first, size_t last) -> x0ne_status {
+            for (size_t i = first; i <= last; ++i) {
+                X0NE_TRY(run_step(e));
+                X0NE_TRY(ring_fetch(e, i));
+                if (i + 1 - next >= RING - 1) X0NE_TRY(collect(next++));
+            }
+            while (next <= last) X0NE_TRY(collect(next++));
+            return x0ne_gpu_sync(e->gpu);
+        };
+        if (warmup) X0NE_TRY(run(1, warmup));
+        X0NE_TRY(x0ne_gpu_sync(e->gpu));
+        const auto t0 = std::chrono::steady_clock::now();
+        X0NE_TRY(run(warmup + 1, warmup + steps));
+        *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        return X0NE_OK;
+    };
+    x0ne_status st = body();
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
 extern "C" x0ne_status x0ne_engine_greedy_with_last_logits(x0ne_engine* e, const uint32_t* prompt, size_t np, size_t n,
                                                            uint32_t* tokens, float* logits) {
     if (!e || !tokens || !logits) return fail(X0NE_ERR_FORMAT, "null argument");
@@ -1129,6 +1200,46 @@ extern "C" const x0ne_arena* x0ne_engine_arena(const x0ne_engine* e) { return e 
 extern "C" x0ne_status x0ne_engine_counts(const x0ne_engine* e, x0ne_counts* out) {
     if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
     return x0ne_gpu_counts(e->gpu, out);
+}
+
+extern "C" x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* avg_us,
+                                              uint64_t* launches) {
+    if (!e || !avg_us || iters == 0) return fail(X0NE_ERR_FORMAT, "null argument");
+    if (which > X0NE_KERNEL_HEAD) return fail(X0NE_ERR_FORMAT, "unknown kernel");
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    auto one = [&](uint64_t l) -> x0ne_status {
+        switch (which) {
+            case X0NE_KERNEL_QKV: return launch_qkv(e, e->c.layers > 1 ? l + 1 : 0);
+            case X0NE_KERNEL_ATTENTION: return launch_attention(e, l);
+            case X0NE_KERNEL_O: return launch_o(e, l);
+            case X0NE_KERNEL_GATE_UP: return launch_gate_up(e, l);
+            case X0NE_KERNEL_DOWN: return launch_down(e, l);
+            default: return launch_head(e);
+        }
+    };
+    // Layer 0's QKV kernel also reads the embedding; the others are timed.
+    const uint64_t per = which == X0NE_KERNEL_HEAD ? 1
+                         : which == X0NE_KERNEL_QKV ? (e->c.layers > 1 ? e->c.layers - 1 : 1)
+                                                    : e->c.layers;
+    hipEvent_t a = nullptr, b = nullptr;
+    X0NE_HIP(hipEventCreate(&a), "event");
+    X0NE_HIP(hipEventCreate(&b), "event");
+    x0ne_status st = X0NE_OK;
+    for (uint64_t l = 0; l < per && st == X0NE_OK; ++l) st = one(l);  // warm-up round
+    if (st == X0NE_OK && hipEventRecord(a, e->gpu->stream) != hipSuccess) st = fail(X0NE_ERR_GPU, "event record");
+    for (uint32_t i = 0; i < iters && st == X0NE_OK; ++i)
+        for (uint64_t l = 0; l < per && st == X0NE_OK; ++l) st = one(l);
+    float ms = 0.f;
+    if (st == X0NE_OK && hipEventRecord(b, e->gpu->stream) != hipSuccess) st = fail(X0NE_ERR_GPU, "event record");
+    if (st == X0NE_OK && hipEventSynchronize(b) != hipSuccess) st = fail(X0NE_ERR_GPU, "event wait");
+    if (st == X0NE_OK && hipEventElapsedTime(&ms, a, b) != hipSuccess) st = fail(X0NE_ERR_GPU, "elapsed time");
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    x0ne_status sc = scrub(e);
+    if (st != X0NE_OK) return st;
+    *avg_us = (double)ms * 1000.0 / ((double)iters * (double)per);
+    if (launches) *launches = (uint64_t)iters * per;
+    return sc;
 }
 
 extern "C" x0ne_status x0ne_engine_page(const x0ne_engine* e, uint64_t i, uint32_t* out) {

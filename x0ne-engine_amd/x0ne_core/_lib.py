@@ -133,6 +133,7 @@ SIGNATURES = {
     "x0ne_greedy_drop": ([P], None),
     "x0ne_engine_greedy_timed": ([P, C.POINTER(U32), SZ, SZ, C.POINTER(U32), C.POINTER(F64)], ST),
     "x0ne_engine_greedy_with_last_logits": ([P, C.POINTER(U32), SZ, SZ, C.POINTER(U32), C.POINTER(F32)], ST),
+    "x0ne_engine_decode_timed": ([P, C.POINTER(U32), SZ, SZ, SZ, C.POINTER(U32), C.POINTER(F64)], ST),
     "x0ne_engine_set_decode_mode": ([P, U32], ST),
     "x0ne_engine_decode_mode": ([P], U32),
     "x0ne_engine_logits_at": ([P, C.POINTER(U32), SZ, C.POINTER(SZ), SZ, U32, C.POINTER(F32)], ST),
@@ -145,6 +146,7 @@ SIGNATURES = {
     "x0ne_engine_max_ctx": ([P], U64),
     "x0ne_engine_arena": ([P], P),
     "x0ne_engine_page": ([P, U64, C.POINTER(U32)], ST),
+    "x0ne_engine_time_kernel": ([P, U32, U32, C.POINTER(F64), C.POINTER(U64)], ST),
 }
 
 

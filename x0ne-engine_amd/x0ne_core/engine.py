@@ -111,6 +111,17 @@ class Engine:
                                              times.ctypes.data_as(C.POINTER(C.c_double))), "greedy")
         return toks, times
 
+    def decode_timed(self, prompt, warmup: int, steps: int):
+        """Prefill, `warmup` decode steps, then `steps` decode steps timed between two stream
+        synchronisations: (tokens, seconds of the timed steps)."""
+        a, p = _ids(prompt)
+        toks = np.zeros(warmup + steps + 1, np.uint32)
+        secs = C.c_double()
+        check(lib().x0ne_engine_decode_timed(self.h, p, a.size, warmup, steps,
+                                             toks.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(secs)),
+              "decode_timed")
+        return toks, secs.value
+
     def greedy(self, prompt, n: int) -> np.ndarray:
         return self.greedy_timed(prompt, n)[0]
 
@@ -173,6 +184,16 @@ class Engine:
     def arena(self):
         from .arena import Arena
         return Arena(lib().x0ne_engine_arena(self.h), owned=False)
+
+    KERNELS = {"qkv": 0, "attention": 1, "o": 2, "gate_up": 3, "down": 4, "head": 5}
+
+    def time_kernel(self, which: str, iters: int):
+        """One decode-step kernel alone, `iters` rounds over every layer, HIP events on the
+        engine's stream: (average microseconds per launch, launches timed)."""
+        avg, n = C.c_double(), C.c_uint64()
+        check(lib().x0ne_engine_time_kernel(self.h, self.KERNELS[which], iters, C.byref(avg), C.byref(n)),
+              "time_kernel")
+        return avg.value, n.value
 
     def page(self, i: int) -> int:
         out = C.c_uint32()
