@@ -102,19 +102,26 @@ def main():
     ap.add_argument("--runs", type=int, default=3, help="timed runs; the median is reported")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--kernel-iters", type=int, default=4)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch each step's kernels one by one instead of replaying the captured graph "
+                         "(for kernel-trace profilers; the same kernels and results)")
+    ap.add_argument("--f64-sums", action="store_true", help="f64 accumulation in the GEMVs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); every box here has one, "
               "and no figure at several GPUs is produced. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    from x0ne_core import Engine, EngineOptions, roofline
+    from x0ne_core import DecodeMode, Engine, EngineOptions, roofline
 
     cfg = QWEN3_8B
     prompt = splitmix_ids(PROMPT, cfg["vocab_size"], SEED)
     n_tokens = args.warmup + args.steps + 1
     t = time.perf_counter()
-    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=PROMPT + n_tokens + 16, page_seed=1))
+    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=PROMPT + n_tokens + 16, page_seed=1,
+                                                            f64_sums=args.f64_sums))
+    if args.eager:
+        e.set_decode_mode(DecodeMode.EAGER)
     load_s = time.perf_counter() - t
     print(f"[bench] loaded in {load_s:.1f} s: {e.describe()}", file=sys.stderr, flush=True)
 
@@ -171,7 +178,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: random-init N(0,0.02) bf16 weights (seed 0), uniform random token ids (seed 0)",
-        "config": {"workload": "Qwen3-8B-shape batch-1 greedy decode, 20-token prompt, hipGraph per step",
+        "config": {"workload": "Qwen3-8B-shape batch-1 greedy decode, 20-token prompt, "
+                               + ("eager launches" if args.eager else "hipGraph per step")
+                               + (", f64 GEMV sums" if args.f64_sums else ""),
                    "layers": 36, "hidden": 4096, "heads": "32q/8kv", "head_dim": 128, "intermediate": 12288,
                    "vocab": 151936, "prompt": PROMPT, "mean_ctx": mean_ctx, "runs": runs},
         "decode_hbm": {"achieved": round(hbm_gbs, 1), "peak": 8000.0, "unit": "GB/s",

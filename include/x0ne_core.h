@@ -169,11 +169,19 @@ typedef struct x0ne_engine x0ne_engine;
 typedef struct x0ne_session x0ne_session;
 typedef struct x0ne_greedy x0ne_greedy;
 
-/* EngineOptions (engine.rs:38-40), plus this build's KV-page order: page_seed 0 keeps logical
-   page i at physical page i, another seed shuffles the pages with a seeded permutation. */
+/* EngineOptions (engine.rs:38-40), plus this build's choices:
+   - page_seed: 0 keeps logical KV page i at physical page i, another seed shuffles the pages
+     with a seeded permutation;
+   - f64_sums: 1 selects the exact mode: the projections add their exact bf16 products in f64,
+     and decode attention computes scores, softmax and sums in f64 with the f64 scale
+     1/sqrt(128) (one block per kv head, no split), so every rounding point of the step is the
+     f64 oracle's; 1, 2, 4 or 8 q heads per kv head (X0NE_ERR_NOT_IMPLEMENTED otherwise).
+     0, the default, is the fp32-accumulating decode path. */
 typedef struct {
     uint64_t max_ctx;
     uint64_t page_seed;
+    uint32_t f64_sums;
+    uint32_t reserved;
 } x0ne_engine_options;
 
 /* Engine::load_from (engine.rs:301-309) over safetensors files already in memory (the

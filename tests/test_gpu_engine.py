@@ -237,3 +237,31 @@ def test_synthetic_greedy_against_the_oracle():
     for p, row in zip([19, 40, 82], logits_dev):
         assert_logits(f"synthetic pos {p}", row, full[p])
     assert agree == n or margins[agree] < 2 * LOGITS_ATOL_OF_MAX * float(np.abs(full[19 + agree]).max())
+
+
+def test_qwen3_8b_greedy_is_the_oracle_fixture():
+    """The bench workload itself (Qwen3-8B shape, N(0, 0.02) bf16 weights from seed 0, the
+    20-token splitmix64 prompt): 64 greedy tokens against the CPU oracle's, stored in
+    tests/golden/oracle_greedy_8b.json by tests/golden/make_oracle_greedy.py. With f64 sums in the
+    GEMVs every token must agree (the reference's bar for the 8B model, 64 steps); the default f32
+    sums are reported, and must agree up to the first choice whose margin is below 1e-2."""
+    import os
+    from x0ne_core import Engine, EngineOptions
+    with open(os.path.join(os.path.dirname(__file__), "golden", "oracle_greedy_8b.json")) as fh:
+        fx = json.load(fh)
+    prompt = np.array(fx["prompt"], np.uint32)
+    want = np.array(fx["tokens"], np.uint32)
+    margins = np.array(fx["margins"])
+    n = want.size
+    for f64 in (True, False):
+        e = Engine.load_synthetic(fx["config"], fx["seed"], fx["std"],
+                                  EngineOptions(max_ctx=prompt.size + n + 16, page_seed=1, f64_sums=f64))
+        got = e.greedy(prompt, n)
+        agree = next((i for i in range(n) if got[i] != want[i]), n)
+        print(f"MEASURE Qwen3-8B greedy, {'f64' if f64 else 'f32'} sums: {agree} of {n} tokens equal to the "
+              f"oracle's; first mismatch margin {margins[agree] if agree < n else None}; {e.describe()}")
+        if f64:
+            assert agree == n, f"f64 sums: token {agree} differs (oracle margin {margins[agree]:.3e})"
+        else:
+            assert agree == n or margins[agree] < 1e-2, f"f32 sums: token {agree}, margin {margins[agree]:.3e}"
+        del e

@@ -222,6 +222,77 @@ def test_decode_attention_is_the_oracle_around_every_boundary(kernels, qh, kvh):
                 assert (again == split).all(), f"{what}: split-K is not deterministic"
 
 
+@pytest.mark.parametrize("qh,kvh", [(1, 1), (2, 1), (16, 8), (32, 8), (64, 8)])
+def test_fused_rope_attention_is_the_two_kernel_path_bit_for_bit(kernels, qh, kvh):
+    """The engine's one-launch attention (QK-norm + RoPE + K/V write + split-K) gives the bits of
+    the QK-norm/RoPE kernel followed by split-K on the same P and merge, writes the same K/V row
+    into the page of position ctx - 1, and is the oracle's attention within tolerance."""
+    from x0ne_core.ops import CacheAt, inv_freq
+    h = H(qh, kvh)
+    rng = O.Rng(470 + qh)
+    theta, eps = 1e6, 1e-6
+    for ctx in [1, 2, 16, 17, 64, 65, 255, 256, 257, 700, 2049]:
+        qkv = rng.bf16s(h.q_dim + 2 * h.kv_dim, 3.0)
+        qn, kn = rng.bf16s(128, 1.5), rng.bf16s(128, 1.5)
+        k = rng.bf16s((ctx - 1) * h.kv_dim, 1.0)
+        v = bf16s_with_edges(rng, (ctx - 1) * h.kv_dim, 4.0)
+        pages = (ctx + 15) // 16
+        page_of = [int(p) for p in np.random.default_rng(ctx).permutation(pages + 2)[:pages]]
+        rope = kernels.qk_norm_rope_kv_write(bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), h, theta, eps,
+                                             CacheAt(1, ctx, 0, ctx - 1))
+        kb = np.concatenate([bf16_bits(k), rope.k_row])
+        vb = np.concatenate([bf16_bits(v), rope.v_row])
+        q_o, k_o, v_o = O.qk_norm_rope(qkv, qn, kn, inv_freq(128, theta), qh, kvh, 128, ctx - 1, eps)
+        want = O.attention_decode(bf16_vals(rope.q), bf16_vals(kb), bf16_vals(vb), ctx, qh, kvh)
+        atol = ATTENTION_ATOL_OF_VMAX * max(max_abs(v), max_abs(bf16_vals(rope.v_row)))
+        what = f"fused {qh}/{kvh} ctx {ctx}"
+        for splits in [1, 3, None]:
+            for last_block in [True, False]:
+                out, k_row, v_row = kernels.attention_rope_decode(
+                    bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), eps, theta, bf16_bits(k), bf16_bits(v), ctx, h,
+                    last_block=last_block, splits=splits, page_of=page_of)
+                assert (k_row == rope.k_row).all() and (v_row == rope.v_row).all(), f"{what}: the K/V row"
+                two = kernels.attention_decode_split(rope.q, kb, vb, ctx, h, last_block=last_block, splits=splits,
+                                                     page_of=page_of)
+                assert (out == two).all(), f"{what} P {splits} last_block {last_block}: not the two-kernel bits"
+                assert_close(f"{what} P {splits}", bf16_vals(out), want, atol, 0.0)
+        assert_close(f"{what} k row", bf16_vals(rope.k_row), k_o, ROPE_ATOL_OF_XMAX * max_abs(k_o) + BF16_ATOL,
+                     BF16_RTOL)
+
+
+@pytest.mark.parametrize("qh,kvh", [(1, 1), (2, 1), (16, 8), (32, 8), (64, 8)])
+def test_exact_attention_is_the_f64_oracle_bit_for_bit(kernels, qh, kvh):
+    """The exact mode's fused attention (f64 scores, softmax and sums) gives the bits of the f64
+    oracle's attention rounded f64 -> f32 -> bf16, on the q and K/V row its own QK-norm/RoPE
+    produced (which are the QK-norm/RoPE kernel's bits)."""
+    from x0ne_core.ops import CacheAt
+    h = H(qh, kvh)
+    rng = O.Rng(490 + qh)
+    theta, eps = 1e6, 1e-6
+    total = differ = 0
+    for ctx in [1, 2, 17, 64, 65, 256, 257, 1000, 4097]:
+        qkv = rng.bf16s(h.q_dim + 2 * h.kv_dim, 3.0)
+        qn, kn = rng.bf16s(128, 1.5), rng.bf16s(128, 1.5)
+        k = rng.bf16s((ctx - 1) * h.kv_dim, 1.0)
+        v = bf16s_with_edges(rng, (ctx - 1) * h.kv_dim, 4.0)
+        v[~np.isfinite(v)] = 0.0
+        pages = (ctx + 15) // 16
+        page_of = [int(p) for p in np.random.default_rng(ctx).permutation(pages + 1)[:pages]]
+        rope = kernels.qk_norm_rope_kv_write(bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), h, theta, eps,
+                                             CacheAt(1, ctx, 0, ctx - 1))
+        out, k_row, v_row = kernels.attention_rope_decode(bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), eps, theta,
+                                                          bf16_bits(k), bf16_bits(v), ctx, h, page_of=page_of,
+                                                          exact=True)
+        assert (k_row == rope.k_row).all() and (v_row == rope.v_row).all(), f"ctx {ctx}: the K/V row"
+        kb = np.concatenate([bf16_bits(k), rope.k_row])
+        vb = np.concatenate([bf16_bits(v), rope.v_row])
+        want = bf16_bits(O.attention_decode(bf16_vals(rope.q), bf16_vals(kb), bf16_vals(vb), ctx, qh, kvh))
+        total += want.size
+        differ += int((out != want).sum())
+    print(f"MEASURE exact attention {qh}/{kvh}: {differ} of {total} outputs differ from the f64 oracle's bits")
+    assert differ == 0
+
+
 def test_decode_attention_on_one_key_a_dominant_key_and_equal_keys(kernels):
     h = H(4, 2)
     rng = O.Rng(450)

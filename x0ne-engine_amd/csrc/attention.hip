@@ -3,43 +3,76 @@
 // Semantics follow x0ne-core/kernels/cuda/attention.cu: the query at position pos[0] attends
 // keys 0..pos[0] (ctx = min(pos + 1, max_ctx)); q head h reads kv head h / (q_heads / kv_heads);
 // scores q.k / sqrt(128); softmax with the maximum subtracted; f32 accumulation. Split-K
-// (attention.cu:161-251): keys in tiles at absolute positions, block (kh, y) takes tiles
-// y, y + P, y + 2P, ... below ctx and writes a partial state (m, l, o[128]) per q head at
+// (attention.cu:161-251): the keys are cut in tiles at absolute positions, a block of slice y
+// takes its share of them and writes a partial state (m, l, o[128]) per q head at
 // state[(h * P + y) * 132]; the merge (attention.cu:253-280) combines slices 0..active-1 in that
 // fixed order. The result depends on the inputs, ctx and P only.
 //
 // The layout and the work split are this build's own, shaped for CDNA:
 //  - K and V planes are paged: [pages][kv_heads][16][128] bf16, page_table[pos / 16] the
-//    physical page. A tile is 64 keys (4 pages); one wavefront takes a tile per step.
-//  - Each 16-byte load of a wavefront covers 4 whole rows of one page (1 KiB contiguous). Lane
-//    (r = lane / 16, b = lane % 16) holds dims 8b..8b+7 of rows 4i + r, i = 0..15.
-//  - The partial dot products of a lane (16 rows x G heads) are summed over the 16 lanes of a row
-//    by a transposing butterfly (xor 1, 2, 4, 8; each step halves the vector), so a lane ends
-//    with whole scores without reducing every value separately.
-//  - Scores and softmax weights go through LDS once per tile, so each lane runs the online
-//    softmax for one key and the V accumulation for its own rows, with no further shuffles.
+//    physical page. A tile is 64 keys (4 pages); a block is 4 wavefronts and takes 4 tiles
+//    (256 keys) at a time: block y of P takes block-tiles y, y + P, ..., wavefront w the tile
+//    4 bt + w of each.
+//  - Each 16-byte load of a wavefront covers 4 whole rows of one page (1 KiB contiguous); the K
+//    and V loads of a tile are issued together. Lane (r = lane / 16, b = lane % 16) holds dims
+//    8b..8b+7 of rows 4i + r, i = 0..15.
+//  - The partial dot products of a lane (16 rows x G heads) are summed over the 16 lanes of a
+//    row by a transposing butterfly (xor 1, 2, 4, 8; each step halves the vector), so a lane ends
+//    with whole scores without reducing every value separately. Scores and softmax weights go
+//    through the wavefront's own LDS once per tile: each lane runs the online softmax of one key
+//    and the V accumulation of its own rows, with no further shuffles.
+//  - The 4 wavefronts' states are merged in LDS; a block that covers the whole context (ctx of at
+//    most 256, or P = 1) writes the output directly, without a state, a counter or a second pass.
+//  - The fused variant starts with the QK-norm + RoPE of its G q heads (into LDS) and, in the
+//    block that owns position pos, the K/V write of that position's row (rope.cu:7-47), so a
+//    decode step's attention is one launch.
 #include "device.h"
 
 namespace {
 
+constexpr int WAVES = 4;
+constexpr int BLOCK = 64 * WAVES;
+constexpr uint32_t BLOCK_TILES = WAVES;  // tiles of 64 keys per block-tile
+constexpr uint32_t MERGE_MAX = 256;      // most slices a merge takes (P is capped at this)
+
+// Every LDS write this wavefront issued is done, and no memory access moves across this point.
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// The accumulation type T is float (the decode path) or double (the exact mode, whose sums
+// follow the f64 oracle).
+__device__ __forceinline__ float acc_exp(float x) { return expf(x); }
+__device__ __forceinline__ double acc_exp(double x) { return exp(x); }
+__device__ __forceinline__ float acc_fma(float a, float b, float c) { return fmaf(a, b, c); }
+__device__ __forceinline__ double acc_fma(double a, double b, double c) { return fma(a, b, c); }
+__device__ __forceinline__ float acc_max(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ double acc_max(double a, double b) { return fmax(a, b); }
+__device__ __forceinline__ float acc_wave_sum(float v) { return wave_sum(v); }
+__device__ __forceinline__ double acc_wave_sum(double v) { return wave_sum_d(v); }
+template <class T>
+__device__ __forceinline__ T acc_wave_max(T v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = acc_max(v, (T)__shfl_xor(v, o, 64));
+    return v;
+}
+
 // One step of the transposing butterfly: lanes b and b ^ 2^K exchange halves of an N-vector;
 // the lane whose bit K is 0 keeps the lower half, its partner the upper.
-template <int N, int K>
-__device__ __forceinline__ void butterfly_step(float* a, uint32_t b) {
+template <int N, int K, class T>
+__device__ __forceinline__ void butterfly_step(T* a, uint32_t b) {
     constexpr int H = N >> 1;
     const bool bit = (b >> K) & 1u;
 #pragma unroll
     for (int j = 0; j < H; ++j) {
-        const float send = bit ? a[j] : a[j + H];
-        const float keep = bit ? a[j + H] : a[j];
+        const T send = bit ? a[j] : a[j + H];
+        const T keep = bit ? a[j + H] : a[j];
         a[j] = keep + __shfl_xor(send, 1 << K, 64);
     }
 }
 
 // Sum over the 16 lanes of a row, transposing: lane b (of a row) ends with values
 // (N/16) * rev4(b) + e, e < N/16, of the original vector, in a[0..N/16).
-template <int N>
-__device__ __forceinline__ void butterfly16(float* a, uint32_t b) {
+template <int N, class T>
+__device__ __forceinline__ void butterfly16(T* a, uint32_t b) {
     butterfly_step<N, 0>(a, b);
     butterfly_step<N / 2, 1>(a, b);
     butterfly_step<N / 4, 2>(a, b);
@@ -50,30 +83,30 @@ __device__ __forceinline__ uint32_t rev4(uint32_t b) {
     return ((b & 1u) << 3) | ((b & 2u) << 1) | ((b & 4u) >> 1) | ((b & 8u) >> 3);
 }
 
-// One wavefront: the G q heads at `q` (G x 128 bf16, consecutive) over kv head kh, tiles
-// t0, t0 + tstep, ... below ntiles. Leaves per head the running max m, the sum l (whole, every
-// lane) and o = sum exp(s - m) v for dims 8b..8b+7 (summed over the 4 rows of a lane, valid in
-// every lane). lds: 2 * G * 64 floats.
-template <int G>
-__device__ __forceinline__ void attend_wave(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
-                                            const bf16_t* __restrict__ vc, const uint32_t* __restrict__ pages,
-                                            uint32_t kh, uint32_t kv_heads, uint32_t ctx, uint32_t t0,
-                                            uint32_t tstep, float scale, float* lds, float m[G], float l[G],
-                                            float o[G][8]) {
-    constexpr int HG = G < 4 ? G : 4;  // heads per score pass
+// One wavefront: the G q heads in qs (G x 128 f32, LDS) over kv head kh, tiles t0, t0 + tstep,
+// ... below ntiles. Leaves per head the running max m, the sum l (whole, every lane) and
+// o = sum exp(s - m) v for dims 8b..8b+7 (summed over the 4 rows of a lane, valid in every
+// lane). lds: this wavefront's 2 * G * 64 values. A wavefront without a tile leaves m = -inf.
+template <int G, class T>
+__device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc,
+                                            const uint32_t* __restrict__ pages, uint32_t kh, uint32_t kv_heads,
+                                            uint32_t ctx, uint32_t t0, uint32_t tstep, T scale, T* lds,
+                                            T m[G], T l[G], T o[G][8]) {
+    constexpr int HGMAX = sizeof(T) == 4 ? 4 : 2;  // heads per score pass (registers)
+    constexpr int HG = G < HGMAX ? G : HGMAX;
     constexpr int PASSES = G / HG;
-    float* s_lds = lds;           // [G][64] scores of the tile's keys
-    float* p_lds = lds + G * 64;  // [G][64] their softmax weights
+    T* s_lds = lds;           // [G][64] scores of the tile's keys
+    T* p_lds = lds + G * 64;  // [G][64] their softmax weights
     const uint32_t lane = threadIdx.x & 63, r = lane >> 4, b = lane & 15;
     const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
 
-    float lsum[G];
+    T lsum[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
-        lsum[g] = 0.f;
+        lsum[g] = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[g][j] = 0.f;
+        for (int j = 0; j < 8; ++j) o[g][j] = 0;
     }
 
     for (uint32_t t = t0; t < ntiles; t += tstep) {
@@ -93,74 +126,76 @@ __device__ __forceinline__ void attend_wave(const bf16_t* __restrict__ q, const 
             valid[i] = base + 4 * i + r < ctx;
             off[i] = ((pg[i >> 2] * kv_heads + kh) * X0NE_PAGE + 4 * (i & 3) + r) * X0NE_HEAD_DIM + 8 * b;
         }
-        uint4 kv[16];
+        // K and V rows together (the f64 mode loads V after the scores, for registers); rows
+        // past ctx are zero (their weight is 0, and a zero keeps a value that is not a number
+        // out of the sum).
+        uint4 kv[16], vv[16];
+        auto load_v = [&] {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                vv[i] = valid[i] ? *reinterpret_cast<const uint4*>(vc + off[i]) : make_uint4(0, 0, 0, 0);
+        };
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             kv[i] = valid[i] ? *reinterpret_cast<const uint4*>(kc + off[i]) : make_uint4(0, 0, 0, 0);
+        if constexpr (sizeof(T) == 4) load_v();
 
 #pragma unroll
         for (int pass = 0; pass < PASSES; ++pass) {
-            float qf[HG][8];
+            T qf[HG][8];
 #pragma unroll
             for (int g = 0; g < HG; ++g) {
-                const uint4 u = *reinterpret_cast<const uint4*>(q + (pass * HG + g) * X0NE_HEAD_DIM + 8 * b);
-                qf[g][0] = bf_lo(u.x); qf[g][1] = bf_hi(u.x);
-                qf[g][2] = bf_lo(u.y); qf[g][3] = bf_hi(u.y);
-                qf[g][4] = bf_lo(u.z); qf[g][5] = bf_hi(u.z);
-                qf[g][6] = bf_lo(u.w); qf[g][7] = bf_hi(u.w);
+                const float4 q0 = *reinterpret_cast<const float4*>(qs + (pass * HG + g) * X0NE_HEAD_DIM + 8 * b);
+                const float4 q1 = *reinterpret_cast<const float4*>(qs + (pass * HG + g) * X0NE_HEAD_DIM + 8 * b + 4);
+                qf[g][0] = q0.x; qf[g][1] = q0.y; qf[g][2] = q0.z; qf[g][3] = q0.w;
+                qf[g][4] = q1.x; qf[g][5] = q1.y; qf[g][6] = q1.z; qf[g][7] = q1.w;
             }
-            float part[16 * HG];
+            T part[16 * HG];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float k0 = bf_lo(kv[i].x), k1 = bf_hi(kv[i].x), k2 = bf_lo(kv[i].y), k3 = bf_hi(kv[i].y);
-                const float k4 = bf_lo(kv[i].z), k5 = bf_hi(kv[i].z), k6 = bf_lo(kv[i].w), k7 = bf_hi(kv[i].w);
+                const T k0 = bf_lo(kv[i].x), k1 = bf_hi(kv[i].x), k2 = bf_lo(kv[i].y), k3 = bf_hi(kv[i].y);
+                const T k4 = bf_lo(kv[i].z), k5 = bf_hi(kv[i].z), k6 = bf_lo(kv[i].w), k7 = bf_hi(kv[i].w);
 #pragma unroll
                 for (int g = 0; g < HG; ++g) {
-                    float d = qf[g][0] * k0;
-                    d = fmaf(qf[g][1], k1, d);
-                    d = fmaf(qf[g][2], k2, d);
-                    d = fmaf(qf[g][3], k3, d);
-                    d = fmaf(qf[g][4], k4, d);
-                    d = fmaf(qf[g][5], k5, d);
-                    d = fmaf(qf[g][6], k6, d);
-                    d = fmaf(qf[g][7], k7, d);
+                    T d = qf[g][0] * k0;
+                    d = acc_fma(qf[g][1], k1, d);
+                    d = acc_fma(qf[g][2], k2, d);
+                    d = acc_fma(qf[g][3], k3, d);
+                    d = acc_fma(qf[g][4], k4, d);
+                    d = acc_fma(qf[g][5], k5, d);
+                    d = acc_fma(qf[g][6], k6, d);
+                    d = acc_fma(qf[g][7], k7, d);
                     part[i * HG + g] = d;
                 }
             }
             butterfly16<16 * HG>(part, b);
             // Lane holds values HG * rev4(b) + e: row slot i = v / HG, head g = v % HG.
-            constexpr int VPL = HG;
 #pragma unroll
-            for (int e = 0; e < VPL; ++e) {
-                const uint32_t v = VPL * rev4(b) + e;
+            for (int e = 0; e < HG; ++e) {
+                const uint32_t v = HG * rev4(b) + e;
                 const uint32_t i = v / HG, g = v % HG;
                 const uint32_t row = 4 * i + r;
-                const float s = (base + row < ctx) ? part[e] * scale : -INFINITY;
+                const T s = (base + row < ctx) ? part[e] * scale : (T)-INFINITY;
                 s_lds[(pass * HG + g) * 64 + row] = s;
             }
         }
-        __syncthreads();
+        wave_lds_sync();
+        if constexpr (sizeof(T) == 8) load_v();
 
         // Online softmax, lane = key of the tile.
-        float alpha[G];
+        T alpha[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float s = s_lds[g * 64 + lane];
-            const float mn = fmaxf(m[g], wave_max(s));  // key `base` is below ctx: mn is finite
-            alpha[g] = expf(m[g] - mn);
-            const float p = expf(s - mn);
+            const T s = s_lds[g * 64 + lane];
+            const T mn = acc_max(m[g], acc_wave_max(s));  // key `base` is below ctx: mn is finite
+            alpha[g] = acc_exp(m[g] - mn);
+            const T p = acc_exp(s - mn);
             lsum[g] = lsum[g] * alpha[g] + p;
             m[g] = mn;
             p_lds[g * 64 + lane] = p;
         }
-        __syncthreads();
+        wave_lds_sync();
 
-        // V rows 4i + r, dims 8b..8b+7; rows past ctx are zero (their weight is 0, and a zero
-        // keeps a value that is not a number out of the sum).
-        uint4 vv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            vv[i] = valid[i] ? *reinterpret_cast<const uint4*>(vc + off[i]) : make_uint4(0, 0, 0, 0);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
 #pragma unroll
@@ -168,56 +203,48 @@ __device__ __forceinline__ void attend_wave(const bf16_t* __restrict__ q, const 
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float v0 = bf_lo(vv[i].x), v1 = bf_hi(vv[i].x), v2 = bf_lo(vv[i].y), v3 = bf_hi(vv[i].y);
-            const float v4 = bf_lo(vv[i].z), v5 = bf_hi(vv[i].z), v6 = bf_lo(vv[i].w), v7 = bf_hi(vv[i].w);
+            const T v0 = bf_lo(vv[i].x), v1 = bf_hi(vv[i].x), v2 = bf_lo(vv[i].y), v3 = bf_hi(vv[i].y);
+            const T v4 = bf_lo(vv[i].z), v5 = bf_hi(vv[i].z), v6 = bf_lo(vv[i].w), v7 = bf_hi(vv[i].w);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float p = p_lds[g * 64 + 4 * i + r];
-                o[g][0] = fmaf(p, v0, o[g][0]);
-                o[g][1] = fmaf(p, v1, o[g][1]);
-                o[g][2] = fmaf(p, v2, o[g][2]);
-                o[g][3] = fmaf(p, v3, o[g][3]);
-                o[g][4] = fmaf(p, v4, o[g][4]);
-                o[g][5] = fmaf(p, v5, o[g][5]);
-                o[g][6] = fmaf(p, v6, o[g][6]);
-                o[g][7] = fmaf(p, v7, o[g][7]);
+                const T p = p_lds[g * 64 + 4 * i + r];
+                o[g][0] = acc_fma(p, v0, o[g][0]);
+                o[g][1] = acc_fma(p, v1, o[g][1]);
+                o[g][2] = acc_fma(p, v2, o[g][2]);
+                o[g][3] = acc_fma(p, v3, o[g][3]);
+                o[g][4] = acc_fma(p, v4, o[g][4]);
+                o[g][5] = acc_fma(p, v5, o[g][5]);
+                o[g][6] = acc_fma(p, v6, o[g][6]);
+                o[g][7] = acc_fma(p, v7, o[g][7]);
             }
         }
-        __syncthreads();  // the next tile rewrites s_lds and p_lds
+        wave_lds_sync();  // the next tile rewrites s_lds and p_lds
     }
     // Whole sums: l over the 64 keys' lanes, o over the 4 rows of a lane (lanes b, b+16, ...).
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        l[g] = wave_sum(lsum[g]);
+        l[g] = acc_wave_sum(lsum[g]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            float x = o[g][j];
-            x += __shfl_xor(x, 16, 64);
-            x += __shfl_xor(x, 32, 64);
+            T x = o[g][j];
+            x += (T)__shfl_xor(x, 16, 64);
+            x += (T)__shfl_xor(x, 32, 64);
             o[g][j] = x;
         }
     }
 }
 
-// The state of one (q head, slice): [0] m, [1] l, [4..131] o. Lanes 0..15 write o.
-template <int G>
-__device__ __forceinline__ void write_states(float* __restrict__ state, uint32_t h0, uint32_t splits, uint32_t y,
-                                             const float m[G], const float l[G], const float o[G][8]) {
-    const uint32_t lane = threadIdx.x & 63;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float* st = state + ((size_t)(h0 + g) * splits + y) * X0NE_SPLIT_STATE;
-        if (lane < 16) {
-            float4* d = reinterpret_cast<float4*>(st + 4 + 8 * lane);
-            d[0] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
-            d[1] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
-        }
-        if (lane == 0) {
-            st[0] = m[g];
-            st[1] = l[g];
-        }
-    }
-}
+// The shared memory of one block: q of its heads, each wavefront's exchange area, each
+// wavefront's state for the block merge, each wavefront's slice weights for a global merge.
+template <int G, class T = float>
+struct AttnShared {
+    float qs[G][X0NE_HEAD_DIM];
+    T xch[WAVES][2 * G * 64];
+    T wm[WAVES][G], wl[WAVES][G];
+    T wo[WAVES][G][X0NE_HEAD_DIM];
+    float f[sizeof(T) == 4 ? WAVES : 1][MERGE_MAX];  // the exact mode has no global merge
+    uint32_t last;
+};
 
 __device__ __forceinline__ float ld_agent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -225,78 +252,308 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 
 // Merge of one q head's slices 0..active-1 in that order (FlashInfer's: M = max m_y,
 // f_y = exp(m_y - M), l = sum l_y f_y, o = sum o_y f_y; one rounding, of o / l). One wavefront;
-// lane d owns dims d and d + 64. lds: at least `active` floats. Every active slice saw a key,
-// so each m is finite. States are read with agent-coherent loads: other workgroups wrote them.
-__device__ __forceinline__ void merge_head(const float* __restrict__ s, bf16_t* __restrict__ out_h,
-                                           uint32_t active, float* lds) {
+// lane d owns dims d and d + 64. f: this wavefront's LDS for `active` floats. Every active slice
+// saw a key, so each m is finite. States are read with agent-coherent loads: other workgroups
+// wrote them.
+__device__ __forceinline__ void merge_head(const float* __restrict__ s, bf16_t* __restrict__ out_h, uint32_t active,
+                                           float* f) {
     const uint32_t lane = threadIdx.x & 63;
     float mx = -INFINITY;
-    for (uint32_t y = 0; y < active; ++y)
-        mx = fmaxf(mx, ld_agent(s + (size_t)y * X0NE_SPLIT_STATE));
-    for (uint32_t y = lane; y < active; y += 64)
-        lds[y] = expf(ld_agent(s + (size_t)y * X0NE_SPLIT_STATE) - mx);
-    __syncthreads();
+    for (uint32_t y = 0; y < active; ++y) mx = fmaxf(mx, ld_agent(s + (size_t)y * X0NE_SPLIT_STATE));
+    for (uint32_t y = lane; y < active; y += 64) f[y] = expf(ld_agent(s + (size_t)y * X0NE_SPLIT_STATE) - mx);
+    wave_lds_sync();
     float l = 0.f, o0 = 0.f, o1 = 0.f;
     for (uint32_t y = 0; y < active; ++y) {
         const float* st = s + (size_t)y * X0NE_SPLIT_STATE;
-        const float f = lds[y];
-        l += ld_agent(st + 1) * f;
-        o0 += ld_agent(st + 4 + lane) * f;
-        o1 += ld_agent(st + 4 + 64 + lane) * f;
+        const float fy = f[y];
+        l += ld_agent(st + 1) * fy;
+        o0 += ld_agent(st + 4 + lane) * fy;
+        o1 += ld_agent(st + 4 + 64 + lane) * fy;
     }
     out_h[lane] = f2bf(o0 / l);
     out_h[lane + 64] = f2bf(o1 / l);
-    __syncthreads();
+    wave_lds_sync();
 }
 
-constexpr int MERGE_LDS = 1024;  // most slices a merge takes (P is capped at this)
-
-template <int G>
-__device__ __forceinline__ void split_group(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
-                                            const bf16_t* __restrict__ vc, const uint32_t* __restrict__ pages,
-                                            float* __restrict__ state, uint32_t* __restrict__ counter,
-                                            bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,
-                                            uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale) {
-    __shared__ float lds[2 * G * 64 > MERGE_LDS ? 2 * G * 64 : MERGE_LDS];
-    __shared__ uint32_t last;
-    const uint32_t kh = blockIdx.x, y = blockIdx.y;
-    const uint32_t ctx = min(pos[0] + 1u, max_ctx);
-    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
-    if (y >= ntiles) return;  // block-uniform
-    float m[G], l[G], o[G][8];
-    attend_wave<G>(q + (size_t)kh * G * X0NE_HEAD_DIM, kc, vc, pages, kh, kv_heads, ctx, y, splits, scale, lds, m,
-                   l, o);
-    write_states<G>(state, kh * G, splits, y, m, l, o);
-    if (counter == nullptr) return;  // grid-uniform: the merge kernel follows
-    const uint32_t active = min(splits, ntiles);
-    __threadfence();  // this block's states, visible to the block that merges
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(counter + kh, 1u) == active - 1;
-    __syncthreads();
-    if (!last) return;  // block-uniform
-    __threadfence();
-#pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-        const uint32_t h = kh * G + g;
-        merge_head(state + (size_t)h * splits * X0NE_SPLIT_STATE, out + (size_t)h * X0NE_HEAD_DIM, active, lds);
+// The 4 wavefronts' states of a block merged (in wave order, a wavefront without a key skipped),
+// per head g and dim d. Thread t takes the (g, d) pairs t, t + 256, ...; calls f(g, d, m, l, o).
+template <int G, class T, class F>
+__device__ __forceinline__ void block_merge(const AttnShared<G, T>& sh, F f) {
+    for (uint32_t k = threadIdx.x; k < (uint32_t)G * X0NE_HEAD_DIM; k += BLOCK) {
+        const uint32_t g = k / X0NE_HEAD_DIM, d = k % X0NE_HEAD_DIM;
+        T mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) mx = acc_max(mx, sh.wm[w][g]);
+        T l = 0, o = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            if (sh.wm[w][g] == (T)-INFINITY) continue;  // the wavefront saw no key
+            const T fw = acc_exp(sh.wm[w][g] - mx);
+            l += sh.wl[w][g] * fw;
+            o += sh.wo[w][g][d] * fw;
+        }
+        f(g, d, mx, l, o);
     }
-    if (threadIdx.x == 0) counter[kh] = 0;  // ready for the next step
+}
+
+// QK-norm + RoPE of one head row (oracle/src/lib.rs:95-110; rope.cu:7-47): lane i owns the pair
+// (i, i + 64); RMSNorm and the rotation in f64, the angle the f32 product pos * inv_freq[i].
+// Returns the two rotated values, unrounded.
+__device__ __forceinline__ void rope_pair(const bf16_t* __restrict__ src, const bf16_t* __restrict__ nw,
+                                          const float* __restrict__ inv_freq, uint32_t pos, float eps, float* ra,
+                                          float* rb) {
+    constexpr uint32_t HALF = X0NE_HEAD_DIM / 2;
+    const uint32_t i = threadIdx.x & 63;
+    const float a = bf2f(src[i]), b = bf2f(src[i + HALF]);
+    const double ss = wave_sum_d((double)a * (double)a + (double)b * (double)b);
+    const double scale = 1.0 / sqrt(ss / (double)X0NE_HEAD_DIM + (double)eps);
+    const double na = (double)a * scale * (double)bf2f(nw[i]);
+    const double nb = (double)b * scale * (double)bf2f(nw[i + HALF]);
+    const double angle = (double)((float)pos * inv_freq[i]);
+    const double s = sin(angle), c = cos(angle);
+    *ra = (float)(na * c - nb * s);
+    *rb = (float)(nb * c + na * s);
+}
+
+struct AttnArgs {
+    const bf16_t* q;         // non-fused: [q_heads][128]
+    const bf16_t* qkv;       // fused: the packed [q; k; v] row
+    const bf16_t* q_norm;    // fused
+    const bf16_t* k_norm;    // fused
+    const float* inv_freq;   // fused
+    bf16_t* k_cache;         // written by the fused variant at pos
+    bf16_t* v_cache;
+    const uint32_t* pages;
+    float* state;
+    uint32_t* counter;       // null: the merge kernel follows
+    bf16_t* out;
+    const uint32_t* pos;
+    uint32_t q_heads, kv_heads, max_ctx, splits;
+    float scale, eps;
+};
+
+// A wavefront's state into the block's LDS for the block merge.
+template <int G, class T>
+__device__ __forceinline__ void stash_wave(AttnShared<G, T>& sh, const T m[G], const T l[G], const T o[G][8]) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            sh.wm[wave][g] = m[g];
+            sh.wl[wave][g] = l[g];
+        }
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sh.wo[wave][g][8 * lane + j] = o[g][j];
+        }
+    }
+}
+
+// Block (kv head kh, slice y) of the grouped kernel: q heads kh G .. kh G + G - 1. With
+// T = double (the exact mode) P is 1: the block attends the whole context and writes out.
+template <int G, bool FUSED, class T>
+__device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G, T>& sh) {
+    constexpr bool EXACT = sizeof(T) == 8;
+    const uint32_t kh = blockIdx.x, y = blockIdx.y, P = a.splits;
+    if (EXACT && P != 1) return;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t pos = a.pos[0];
+    const uint32_t ctx = min(pos + 1u, a.max_ctx);
+    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
+    const uint32_t nbt = (ntiles + BLOCK_TILES - 1) / BLOCK_TILES;
+    // Block-uniform exits: a slice past the context, or a launch that does not fit the geometry.
+    if (y >= nbt || y >= P || P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
+    const uint32_t active = min(P, nbt);
+    const uint32_t h0 = kh * G;
+
+    // q of the G heads into LDS (the rotated values, rounded to bf16 as the engine stores q).
+    if (FUSED) {
+        const uint32_t q_dim = a.q_heads * X0NE_HEAD_DIM;
+        for (uint32_t g = wave; g < (uint32_t)G; g += WAVES) {
+            float ra, rb;
+            rope_pair(a.qkv + (h0 + g) * X0NE_HEAD_DIM, a.q_norm, a.inv_freq, pos, a.eps, &ra, &rb);
+            sh.qs[g][lane] = bf_round(ra);
+            sh.qs[g][lane + 64] = bf_round(rb);
+        }
+        // The block owning pos's tile writes that position's K and V rows (its page, its slot).
+        const uint32_t owner = ((pos / X0NE_SPLIT_TILE) / BLOCK_TILES) % P;
+        if (pos < a.max_ctx && y == owner && wave == WAVES - 1) {
+            const uint32_t kv_dim = a.kv_heads * X0NE_HEAD_DIM;
+            float ra, rb;
+            rope_pair(a.qkv + q_dim + kh * X0NE_HEAD_DIM, a.k_norm, a.inv_freq, pos, a.eps, &ra, &rb);
+            const uint32_t at = kv_row(a.pages, pos, kh, a.kv_heads);
+            a.k_cache[at + lane] = f2bf(ra);
+            a.k_cache[at + lane + 64] = f2bf(rb);
+            const bf16_t* vs = a.qkv + q_dim + kv_dim + kh * X0NE_HEAD_DIM;
+            a.v_cache[at + lane] = vs[lane];
+            a.v_cache[at + lane + 64] = vs[lane + 64];
+        }
+    } else {
+        for (uint32_t k = t; k < (uint32_t)G * X0NE_HEAD_DIM; k += BLOCK)
+            sh.qs[k / X0NE_HEAD_DIM][k % X0NE_HEAD_DIM] = bf2f(a.q[(size_t)h0 * X0NE_HEAD_DIM + k]);
+    }
+    __syncthreads();  // q in LDS; the new K/V row in memory for the wavefront that reads it
+
+    // The exact mode scales by 1/sqrt(128) in f64, as the f64 oracle does.
+    const T scale = EXACT ? (T)(1.0 / sqrt((double)X0NE_HEAD_DIM)) : (T)a.scale;
+    T m[G], l[G], o[G][8];
+    attend_wave<G, T>(&sh.qs[0][0], a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, BLOCK_TILES * y + wave,
+                      BLOCK_TILES * P, scale, sh.xch[wave], m, l, o);
+    stash_wave<G, T>(sh, m, l, o);
+    __syncthreads();
+
+    if (active == 1) {  // one block holds the whole context: the output directly
+        block_merge<G, T>(sh, [&](uint32_t g, uint32_t d, T, T lv, T ov) {
+            a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf((float)(ov / lv));
+        });
+        return;
+    }
+    if constexpr (!EXACT) {
+        block_merge<G, T>(sh, [&](uint32_t g, uint32_t d, float mv, float lv, float ov) {
+            float* st = a.state + ((size_t)(h0 + g) * P + y) * X0NE_SPLIT_STATE;
+            st[4 + d] = ov;
+            if (d == 0) {
+                st[0] = mv;
+                st[1] = lv;
+            }
+        });
+        if (a.counter == nullptr) return;  // grid-uniform: the merge kernel follows
+        __threadfence();  // this block's states, visible to the block that merges
+        __syncthreads();
+        if (t == 0) sh.last = atomicAdd(a.counter + kh, 1u) == active - 1;
+        __syncthreads();
+        if (!sh.last) return;  // block-uniform
+        __threadfence();
+        for (uint32_t g = wave; g < (uint32_t)G; g += WAVES)
+            merge_head(a.state + (size_t)(h0 + g) * P * X0NE_SPLIT_STATE, a.out + (size_t)(h0 + g) * X0NE_HEAD_DIM,
+                       active, sh.f[wave]);
+        __syncthreads();
+        if (t == 0) a.counter[kh] = 0;  // ready for the next step
+    }
+}
+
+// One q head per block (group sizes without a grouped kernel, the per-head witness, prefill):
+// q head row q_row over kv head kh, ctx keys, slice y of P; the output directly when the block
+// holds the whole context (and out_h is given), else a state at state_h[y * 132].
+__device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row, const bf16_t* __restrict__ kc,
+                                                const bf16_t* __restrict__ vc, const uint32_t* __restrict__ pages,
+                                                uint32_t kh, uint32_t kv_heads, uint32_t ctx, uint32_t y, uint32_t P,
+                                                float scale, float* state_h, bf16_t* out_h, AttnShared<1>& sh) {
+    const uint32_t t = threadIdx.x, wave = t >> 6;
+    if (t < X0NE_HEAD_DIM) sh.qs[0][t] = bf2f(q_row[t]);
+    __syncthreads();
+    float m[1], l[1], o[1][8];
+    attend_wave<1, float>(&sh.qs[0][0], kc, vc, pages, kh, kv_heads, ctx, BLOCK_TILES * y + wave, BLOCK_TILES * P,
+                          scale, sh.xch[wave], m, l, o);
+    stash_wave<1, float>(sh, m, l, o);
+    __syncthreads();
+    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
+    const uint32_t nbt = (ntiles + BLOCK_TILES - 1) / BLOCK_TILES;
+    if (min(P, nbt) == 1 && out_h != nullptr) {
+        block_merge<1, float>(sh, [&](uint32_t, uint32_t d, float, float lv, float ov) { out_h[d] = f2bf(ov / lv); });
+        return;
+    }
+    block_merge<1, float>(sh, [&](uint32_t, uint32_t d, float mv, float lv, float ov) {
+        float* st = state_h + (size_t)y * X0NE_SPLIT_STATE;
+        st[4 + d] = ov;
+        if (d == 0) {
+            st[0] = mv;
+            st[1] = lv;
+        }
+    });
 }
 
 }  // namespace
 
-// Split-K, one block (one wavefront) per (kv head, slice) serving the G q heads of the group:
-// grid (kv_heads, P), block 64. With counter != 0 the last block of a kv head to finish merges
-// its G heads into out (same code and order as x0ne_attention_merge_bf16, so the same bits)
-// and sets counter[kh] back to 0; with counter == 0, out is unused and the merge kernel follows.
+// Split-K, one block (4 wavefronts) per (kv head, slice) serving the G q heads of the group:
+// grid (kv_heads, P), block 256. With counter != 0 the last block of a kv head to finish merges
+// its G heads into out (same code and order as x0ne_attention_merge_bf16, so the same bits) and
+// sets counter[kh] back to 0; with counter == 0 and more than one active slice, out is unused and
+// the merge kernel follows. With one active slice (ctx <= 256 or P = 1) the block writes out.
+//
+// The fused variant x0ne_attention_rope_decode_g*_bf16 takes the packed qkv row instead of q:
+// it applies QK-norm + RoPE to its q heads and writes the K/V row of position pos into its page
+// (the work of x0ne_qk_norm_rope_kv_write_bf16 for one decode row), then attends.
+//
+// x0ne_attention_rope_decode_exact_g*_bf16 is the fused variant with f64 scores, softmax and
+// sums and the f64 scale 1/sqrt(128), one block per kv head over the whole context (grid
+// (kv_heads, 1), block 256): the exact mode, whose outputs follow the f64 oracle's rounding
+// (oracle/src/lib.rs:112-176) rather than the f32 kernels'.
 #define X0NE_SPLIT_GROUP(G)                                                                                        \
-    extern "C" __global__ void __launch_bounds__(64) x0ne_attention_decode_split_g##G##_bf16(                     \
+    extern "C" __global__ void __launch_bounds__(256) x0ne_attention_decode_split_g##G##_bf16(                    \
         const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
         const uint32_t* __restrict__ pages, float* __restrict__ state, uint32_t* __restrict__ counter,           \
         bf16_t* __restrict__ out, const uint32_t* __restrict__ pos, uint32_t q_heads, uint32_t kv_heads,         \
         uint32_t max_ctx, uint32_t splits, float scale) {                                                         \
-        (void)q_heads;                                                                                             \
-        split_group<G>(q, k_cache, v_cache, pages, state, counter, out, pos, kv_heads, max_ctx, splits, scale);    \
+        __shared__ AttnShared<G> sh;                                                                               \
+        AttnArgs a = {};                                                                                           \
+        a.q = q;                                                                                                   \
+        a.k_cache = const_cast<bf16_t*>(k_cache);                                                                  \
+        a.v_cache = const_cast<bf16_t*>(v_cache);                                                                  \
+        a.pages = pages;                                                                                           \
+        a.state = state;                                                                                           \
+        a.counter = counter;                                                                                       \
+        a.out = out;                                                                                               \
+        a.pos = pos;                                                                                               \
+        a.q_heads = q_heads;                                                                                       \
+        a.kv_heads = kv_heads;                                                                                     \
+        a.max_ctx = max_ctx;                                                                                       \
+        a.splits = splits;                                                                                         \
+        a.scale = scale;                                                                                           \
+        attn_group_block<G, false, float>(a, sh);                                                                         \
+    }                                                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) x0ne_attention_rope_decode_g##G##_bf16(                     \
+        const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm, const bf16_t* __restrict__ k_norm,    \
+        const float* __restrict__ inv_freq, bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,          \
+        const uint32_t* __restrict__ pages, float* __restrict__ state, uint32_t* __restrict__ counter,           \
+        bf16_t* __restrict__ out, const uint32_t* __restrict__ pos, uint32_t q_heads, uint32_t kv_heads,         \
+        uint32_t max_ctx, uint32_t splits, float scale, float eps) {                                              \
+        __shared__ AttnShared<G> sh;                                                                               \
+        AttnArgs a = {};                                                                                           \
+        a.qkv = qkv;                                                                                               \
+        a.q_norm = q_norm;                                                                                         \
+        a.k_norm = k_norm;                                                                                         \
+        a.inv_freq = inv_freq;                                                                                     \
+        a.k_cache = k_cache;                                                                                       \
+        a.v_cache = v_cache;                                                                                       \
+        a.pages = pages;                                                                                           \
+        a.state = state;                                                                                           \
+        a.counter = counter;                                                                                       \
+        a.out = out;                                                                                               \
+        a.pos = pos;                                                                                               \
+        a.q_heads = q_heads;                                                                                       \
+        a.kv_heads = kv_heads;                                                                                     \
+        a.max_ctx = max_ctx;                                                                                       \
+        a.splits = splits;                                                                                         \
+        a.scale = scale;                                                                                           \
+        a.eps = eps;                                                                                               \
+        attn_group_block<G, true, float>(a, sh);                                                                   \
+    }                                                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) x0ne_attention_rope_decode_exact_g##G##_bf16(               \
+        const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm, const bf16_t* __restrict__ k_norm,    \
+        const float* __restrict__ inv_freq, bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,          \
+        const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,           \
+        uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float eps) {                                       \
+        __shared__ AttnShared<G, double> sh;                                                                       \
+        AttnArgs a = {};                                                                                           \
+        a.qkv = qkv;                                                                                               \
+        a.q_norm = q_norm;                                                                                         \
+        a.k_norm = k_norm;                                                                                         \
+        a.inv_freq = inv_freq;                                                                                     \
+        a.k_cache = k_cache;                                                                                       \
+        a.v_cache = v_cache;                                                                                       \
+        a.pages = pages;                                                                                           \
+        a.out = out;                                                                                               \
+        a.pos = pos;                                                                                               \
+        a.q_heads = q_heads;                                                                                       \
+        a.kv_heads = kv_heads;                                                                                     \
+        a.max_ctx = max_ctx;                                                                                       \
+        a.splits = 1;                                                                                              \
+        a.eps = eps;                                                                                               \
+        attn_group_block<G, true, double>(a, sh);                                                                  \
     }
 X0NE_SPLIT_GROUP(1)
 X0NE_SPLIT_GROUP(2)
@@ -304,73 +561,68 @@ X0NE_SPLIT_GROUP(4)
 X0NE_SPLIT_GROUP(8)
 
 // Split-K, one block per (q head, slice), for group sizes without a grouped kernel:
-// grid (q_heads, P), block 64. The merge kernel follows.
-extern "C" __global__ void __launch_bounds__(64)
+// grid (q_heads, P), block 256. The merge kernel follows unless one slice holds the context, in
+// which case the block writes out itself.
+extern "C" __global__ void __launch_bounds__(256)
     x0ne_attention_decode_split_bf16(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
                                      const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
-                                     float* __restrict__ state, const uint32_t* __restrict__ pos, uint32_t q_heads,
-                                     uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale) {
-    __shared__ float lds[2 * 64];
-    const uint32_t h = blockIdx.x, y = blockIdx.y, kh = h / (q_heads / kv_heads);
+                                     float* __restrict__ state, bf16_t* __restrict__ out,
+                                     const uint32_t* __restrict__ pos, uint32_t q_heads, uint32_t kv_heads,
+                                     uint32_t max_ctx, uint32_t splits, float scale) {
+    __shared__ AttnShared<1> sh;
+    const uint32_t h = blockIdx.x, y = blockIdx.y;
+    if (h >= q_heads || y >= splits || kv_heads == 0 || q_heads % kv_heads != 0) return;
+    const uint32_t kh = h / (q_heads / kv_heads);
     const uint32_t ctx = min(pos[0] + 1u, max_ctx);
-    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
-    if (y >= ntiles) return;
-    float m[1], l[1], o[1][8];
-    attend_wave<1>(q + (size_t)h * X0NE_HEAD_DIM, k_cache, v_cache, pages, kh, kv_heads, ctx, y, splits, scale, lds,
-                   m, l, o);
-    write_states<1>(state, h, splits, y, m, l, o);
+    const uint32_t nbt = ((ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE + BLOCK_TILES - 1) / BLOCK_TILES;
+    if (y >= nbt) return;
+    attn_head_block(q + (size_t)h * X0NE_HEAD_DIM, k_cache, v_cache, pages, kh, kv_heads, ctx, y, splits, scale,
+                    state + (size_t)h * splits * X0NE_SPLIT_STATE, out + (size_t)h * X0NE_HEAD_DIM, sh);
 }
 
-// Merge of the split-K states: grid (q_heads), block 64, active = min(P, ceil(ctx / 64)).
+// Merge of the split-K states: grid (q_heads), block 64, active = min(P, ceil(ctx / 256)). With
+// one active slice the split kernel wrote out already and this does nothing.
 extern "C" __global__ void __launch_bounds__(64)
     x0ne_attention_merge_bf16(const float* __restrict__ state, bf16_t* __restrict__ out,
                               const uint32_t* __restrict__ pos, uint32_t max_ctx, uint32_t splits) {
-    __shared__ float lds[MERGE_LDS];
+    __shared__ float f[MERGE_MAX];
     const uint32_t h = blockIdx.x;
     const uint32_t ctx = min(pos[0] + 1u, max_ctx);
-    const uint32_t active = min(splits, (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE);
-    merge_head(state + (size_t)h * splits * X0NE_SPLIT_STATE, out + (size_t)h * X0NE_HEAD_DIM, active, lds);
+    const uint32_t nbt = ((ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE + BLOCK_TILES - 1) / BLOCK_TILES;
+    const uint32_t active = min(splits, nbt);
+    if (active <= 1 || splits > MERGE_MAX) return;
+    merge_head(state + (size_t)h * splits * X0NE_SPLIT_STATE, out + (size_t)h * X0NE_HEAD_DIM, active, f);
 }
 
 // Per-head decode over the whole context in one block (the reference's E2 witness,
-// attention.cu:9-81): grid (q_heads), block 64; one slice, normalised in the block.
-extern "C" __global__ void __launch_bounds__(64)
+// attention.cu:9-81): grid (q_heads), block 256; one slice, normalised in the block.
+extern "C" __global__ void __launch_bounds__(256)
     x0ne_attention_decode_bf16(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
                                const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
                                bf16_t* __restrict__ out, const uint32_t* __restrict__ pos, uint32_t q_heads,
                                uint32_t kv_heads, uint32_t max_ctx, float scale) {
-    __shared__ float lds[2 * 64];
-    const uint32_t h = blockIdx.x, kh = h / (q_heads / kv_heads);
+    __shared__ AttnShared<1> sh;
+    const uint32_t h = blockIdx.x;
+    if (h >= q_heads || kv_heads == 0 || q_heads % kv_heads != 0) return;
+    const uint32_t kh = h / (q_heads / kv_heads);
     const uint32_t ctx = min(pos[0] + 1u, max_ctx);
-    float m[1], l[1], o[1][8];
-    attend_wave<1>(q + (size_t)h * X0NE_HEAD_DIM, k_cache, v_cache, pages, kh, kv_heads, ctx, 0, 1, scale, lds, m,
-                   l, o);
-    const uint32_t lane = threadIdx.x & 63;
-    if (lane < 16) {
-        bf16_t* d = out + (size_t)h * X0NE_HEAD_DIM + 8 * lane;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) d[j] = f2bf(o[0][j] / l[0]);
-    }
+    attn_head_block(q + (size_t)h * X0NE_HEAD_DIM, k_cache, v_cache, pages, kh, kv_heads, ctx, 0, 1, scale, nullptr,
+                    out + (size_t)h * X0NE_HEAD_DIM, sh);
 }
 
 // Causal prefill: rows at positions pos0[0] + r over the cache (already holding their keys).
-// grid (q_heads, rows), block 64: one wavefront per (q head, row), the decode arithmetic over
-// keys 0..min(pos0 + r, max_ctx - 1). q and out are [rows][q_heads][128].
-extern "C" __global__ void __launch_bounds__(64)
+// grid (q_heads, rows), block 256: one block per (q head, row), the decode arithmetic over keys
+// 0..min(pos0 + r, max_ctx - 1). q and out are [rows][q_heads][128].
+extern "C" __global__ void __launch_bounds__(256)
     x0ne_attention_prefill_bf16(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
                                 const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
                                 bf16_t* __restrict__ out, const uint32_t* __restrict__ pos0, uint32_t rows,
                                 uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale) {
-    __shared__ float lds[2 * 64];
-    const uint32_t h = blockIdx.x, row = blockIdx.y, kh = h / (q_heads / kv_heads);
-    if (row >= rows) return;
+    __shared__ AttnShared<1> sh;
+    const uint32_t h = blockIdx.x, row = blockIdx.y;
+    if (row >= rows || h >= q_heads || kv_heads == 0 || q_heads % kv_heads != 0) return;
+    const uint32_t kh = h / (q_heads / kv_heads);
     const uint32_t ctx = min(pos0[0] + row + 1u, max_ctx);
     const size_t at = ((size_t)row * q_heads + h) * X0NE_HEAD_DIM;
-    float m[1], l[1], o[1][8];
-    attend_wave<1>(q + at, k_cache, v_cache, pages, kh, kv_heads, ctx, 0, 1, scale, lds, m, l, o);
-    const uint32_t lane = threadIdx.x & 63;
-    if (lane < 16) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) out[at + 8 * lane + j] = f2bf(o[0][j] / l[0]);
-    }
+    attn_head_block(q + at, k_cache, v_cache, pages, kh, kv_heads, ctx, 0, 1, scale, nullptr, out + at, sh);
 }

@@ -276,6 +276,7 @@ struct LayerW {
 struct x0ne_engine {
     Cfg c;
     uint64_t max_ctx = 0, pages = 0, page_seed = 0;
+    int f64_sums = 0;
     x0ne_gpu* gpu = nullptr;
     x0ne_arena* arena = nullptr;
     // weights
@@ -378,22 +379,27 @@ x0ne_status plan(x0ne_engine* e) {
     return X0NE_OK;
 }
 
-uint32_t grid_for(const x0ne_engine* e, uint64_t groups) {
+// Blocks of a GEMV launch: enough wavefronts for every row group, at most `bpc` blocks per CU
+// (a persistent grid; each wavefront walks its row groups).
+uint32_t grid_for(const x0ne_engine* e, uint64_t rows, uint64_t rows_per_group) {
     static const char* env = std::getenv("X0NE_GEMV_BLOCKS_PER_CU");
-    uint64_t bpc = 2;
+    uint64_t bpc = 4;
     if (env && std::atoi(env) > 0) bpc = (uint64_t)std::atoi(env);
+    const uint64_t groups = (rows + rows_per_group - 1) / rows_per_group;
+    const uint64_t wpb = x0ne_gemv_waves_per_block();
+    const uint64_t blocks = (groups + wpb - 1) / wpb;
     const uint64_t cap = (uint64_t)e->gpu->cus * bpc;
-    return (uint32_t)(groups < cap ? groups : cap);
+    return (uint32_t)(blocks < cap ? blocks : cap);
 }
 
 void plan_grids(x0ne_engine* e) {
     const Cfg& c = e->c;
-    auto groups = [](uint64_t rows, uint32_t rps) { return (rows + rps - 1) / rps; };
-    e->grid_qkv = grid_for(e, groups(c.qkv_rows(), x0ne_gemv_rows_per_step((uint32_t)c.hidden)));
-    e->grid_o = grid_for(e, groups(c.hidden, x0ne_gemv_rows_per_step((uint32_t)c.q_dim())));
-    e->grid_gu = grid_for(e, groups(c.inter, x0ne_gemv_rows_per_step((uint32_t)c.hidden) / 2));
-    e->grid_down = grid_for(e, groups(c.hidden, x0ne_gemv_rows_per_step((uint32_t)c.inter)));
-    e->grid_head = grid_for(e, groups(c.vocab, x0ne_gemv_rows_per_step((uint32_t)c.hidden)));
+    const uint64_t r = x0ne_gemv_rows_per_step(0);
+    e->grid_qkv = grid_for(e, c.qkv_rows(), r);
+    e->grid_o = grid_for(e, c.hidden, r);
+    e->grid_gu = grid_for(e, c.inter, r / 2);
+    e->grid_down = grid_for(e, c.hidden, r);
+    e->grid_head = grid_for(e, c.vocab, r);
 }
 
 // The kernels of one decode step, one helper each. Norm j of the step reads residual buffer
@@ -420,6 +426,7 @@ x0ne_status launch_qkv(x0ne_engine* e, uint64_t l) {
     a.prologue = l == 0 ? 2 : 1;  // layer 0 adds the embedding row to a zero residual
     a.epilogue = 0;
     a.grid = e->grid_qkv;
+    a.f64acc = e->f64_sums;
     e->gpu->counts.launches++;
     X0NE_HIP(x0ne_launch_gemv(a, e->gpu->stream), "qkv gemv");
     return X0NE_OK;
@@ -439,10 +446,27 @@ x0ne_status launch_rope(x0ne_engine* e, uint64_t l) {
     return X0NE_OK;
 }
 
+// A grouped plan: one fused launch (QK-norm + RoPE + K/V write + split-K + last-block merge).
+// Otherwise the QK-norm/RoPE kernel, then split-K and the merge kernel.
 x0ne_status launch_attention(x0ne_engine* e, uint64_t l) {
     const Cfg& c = e->c;
     const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));  // ops.rs:217-219
-    return attention_split(e->gpu, e->split, e->split.grouped ? 1 : 0, e->d(e->q), e->plane(l, 0), e->plane(l, 1),
+    if (e->f64_sums) {  // the exact mode (group size checked at load)
+        const LayerW& w = e->L[l];
+        return attention_rope_exact(e->gpu, e->d(e->qkv), e->d(w.q_norm), e->d(w.k_norm), e->d(e->inv_freq),
+                                    e->plane(l, 0), e->plane(l, 1), e->d(e->page_table), e->d(e->attn), e->d(e->pos),
+                                    (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, (float)c.eps);
+    }
+    if (e->split.grouped) {
+        const LayerW& w = e->L[l];
+        return attention_rope_split(e->gpu, e->split, e->d(e->qkv), e->d(w.q_norm), e->d(w.k_norm),
+                                    e->d(e->inv_freq), e->plane(l, 0), e->plane(l, 1), e->d(e->page_table),
+                                    e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn), e->d(e->pos),
+                                    (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, scale,
+                                    (float)c.eps);
+    }
+    X0NE_TRY(launch_rope(e, l));
+    return attention_split(e->gpu, e->split, 0, e->d(e->q), e->plane(l, 0), e->plane(l, 1),
                            e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn),
                            e->d(e->pos), (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, scale);
 }
@@ -458,6 +482,7 @@ x0ne_status launch_o(x0ne_engine* e, uint64_t l) {
     o.prologue = 0;
     o.epilogue = 0;
     o.grid = e->grid_o;
+    o.f64acc = e->f64_sums;
     e->gpu->counts.launches++;
     X0NE_HIP(x0ne_launch_gemv(o, e->gpu->stream), "o gemv");
     return X0NE_OK;
@@ -478,6 +503,7 @@ x0ne_status launch_gate_up(x0ne_engine* e, uint64_t l) {
     gu.prologue = 1;
     gu.epilogue = 2;  // SwiGLU over [gate; up]
     gu.grid = e->grid_gu;
+    gu.f64acc = e->f64_sums;
     e->gpu->counts.launches++;
     X0NE_HIP(x0ne_launch_gemv(gu, e->gpu->stream), "gate_up gemv");
     return X0NE_OK;
@@ -494,6 +520,7 @@ x0ne_status launch_down(x0ne_engine* e, uint64_t l) {
     dn.prologue = 0;
     dn.epilogue = 0;
     dn.grid = e->grid_down;
+    dn.f64acc = e->f64_sums;
     e->gpu->counts.launches++;
     X0NE_HIP(x0ne_launch_gemv(dn, e->gpu->stream), "down gemv");
     return X0NE_OK;
@@ -520,6 +547,7 @@ x0ne_status launch_head(x0ne_engine* e) {
     hd.prologue = 1;
     hd.epilogue = 3;
     hd.grid = e->grid_head;
+    hd.f64acc = e->f64_sums;
     e->gpu->counts.launches++;
     X0NE_HIP(x0ne_launch_gemv(hd, e->gpu->stream), "lm_head gemv");
     return X0NE_OK;
@@ -531,7 +559,6 @@ x0ne_status launch_head(x0ne_engine* e) {
 x0ne_status step_launches(x0ne_engine* e) {
     for (uint64_t l = 0; l < e->c.layers; ++l) {
         X0NE_TRY(launch_qkv(e, l));
-        X0NE_TRY(launch_rope(e, l));
         X0NE_TRY(launch_attention(e, l));
         X0NE_TRY(launch_o(e, l));
         X0NE_TRY(launch_gate_up(e, l));
@@ -668,6 +695,16 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     e->c = c;
     e->max_ctx = opts->max_ctx;
     e->page_seed = opts->page_seed;
+    e->f64_sums = opts->f64_sums ? 1 : 0;
+    if (e->f64_sums) {
+        const uint64_t grp = c.q_heads / c.kv_heads;
+        if (grp != 1 && grp != 2 && grp != 4 && grp != 8) {
+            delete e;
+            return fail(X0NE_ERR_NOT_IMPLEMENTED,
+                        "f64 sums: the exact attention kernels take 1, 2, 4 or 8 q heads per kv head, not " +
+                            std::to_string(grp));
+        }
+    }
     e->pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
     x0ne_status st = x0ne_gpu_new(&e->gpu);
     if (st != X0NE_OK) {
@@ -1179,12 +1216,12 @@ extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, siz
     std::snprintf(s, sizeof s,
                   "%s, arena %llu bytes, decode graph %zu nodes, decode attention split-K P %u (grid %u x %u, %u q "
                   "heads per block, %u blocks per CU, merge %s), KV pages of %d positions (%llu pages, %s order), "
-                  "GEMV grids qkv %u o %u gate_up %u down %u head %u, feed-forward dense",
+                  "GEMV grids qkv %u o %u gate_up %u down %u head %u (%s sums), feed-forward dense",
                   gpu, (unsigned long long)e->arena->len, e->graph ? e->graph->nodes : (size_t)0, e->split.splits,
                   e->split.grid_x, e->split.splits, e->split.group, e->split.per_cu,
                   e->split.grouped ? "LastBlock" : "Kernel", X0NE_PAGE_C, (unsigned long long)e->pages,
                   e->page_seed ? "shuffled" : "identity", e->grid_qkv, e->grid_o, e->grid_gu, e->grid_down,
-                  e->grid_head);
+                  e->grid_head, e->f64_sums ? "f64" : "f32");
     if (buf && len) {
         std::strncpy(buf, s, len - 1);
         buf[len - 1] = 0;

@@ -1,13 +1,17 @@
-// Bandwidth-bound bf16 GEMV for gfx950: y = W x, W [rows][cols] row-major bf16, x bf16,
-// f32 accumulation. It replaces the reference's cuBLAS call at n = 1 (x0ne-core/runtime/src/
-// gpu.rs:1098-1149: Y[n][rows] = X[n][cols] W^T, bf16 in, f32 compute, bf16 or f32 out).
+// Bandwidth-bound bf16 GEMV for gfx950: y = W x, W [rows][cols] row-major bf16, x bf16. It
+// replaces the reference's cuBLAS call at n = 1 (x0ne-core/runtime/src/gpu.rs:1098-1149:
+// Y[n][rows] = X[n][cols] W^T, bf16 in, f32 compute, bf16 or f32 out).
 //
-// Layout of the work (this build's): a block of 256 threads spans one whole row; thread t holds
-// the 16-byte chunks t, t + 256, ... of it, so the 256 threads of a block read 4 KiB contiguous
-// per load instruction, and thread t's slice of x stays in its registers for every row the
-// block visits. A block takes RPB rows at a time (RPB x chunks loads in flight per thread) and
-// walks the row groups g, g + gridDim.x, ... (a persistent grid of a few blocks per CU), so the
-// prologue below runs once per block, not once per row.
+// Layout of the work (this build's): a block of 256 threads (4 wavefronts) first stages x in LDS
+// (bf16, after the fused prologue below), then each wavefront works alone, with no barrier: it
+// takes R whole rows at a time (row groups w, w + W, ... of a persistent grid of W wavefronts),
+// lane l reading the 16-byte chunks l, l + 64, ... of each row, so one load instruction of a
+// wavefront covers 1 KiB contiguous of one row and R x 8 such loads are in flight per wavefront.
+// The R partial sums of a lane are reduced over the 64 lanes by a transposing butterfly (the R
+// values halve at the first log2(R) steps), so a row costs about one shuffle.
+//
+// Accumulation: `Acc` = float (f32 FMA, products of two bf16 exact in f32) or double (each exact
+// product added in f64, as the oracle sums, oracle/src/lib.rs:123-133).
 //
 // Fused prologue (the engine's; x0ne-core/kernels/cuda/rmsnorm.cu:5-21 and embedding.cu:5-17
 // restated): x = bf16(rmsnorm(residual_in + delta) * w_norm), with the residual add in f32 (one
@@ -17,7 +21,7 @@
 // (a token past the table gives a zero row) to a zero residual.
 //
 // Fused epilogues: bf16 out; f32 out; SwiGLU over the packed [gate; up] rows (gate row i and up
-// row inter + i are summed by the same block, act[i] = bf16(silu(bf16 g) bf16 u) in f64,
+// row inter + i are summed by the same wavefront, act[i] = bf16(silu(bf16 g) bf16 u) in f64,
 // oracle/src/lib.rs:205-214); and f32 logits with the greedy argmax (first largest, any NaN
 // gives 0xFFFFFFFF; kernels/cuda/argmax.cu:11-58) reduced by the last block to finish, which
 // writes the token to device memory and can advance the position (advance.cu:5-7).
@@ -26,6 +30,7 @@
 namespace {
 
 constexpr int BLOCK = 256;
+constexpr int WAVES = BLOCK / 64;
 constexpr uint32_t NO_TOKEN = 0xFFFFFFFFu;
 
 enum Pro : int { PRO_X = 0, PRO_NORM = 1, PRO_EMBED_NORM = 2 };
@@ -56,22 +61,18 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);
 }
 
-// x of this thread: chunk j covers columns 8 (t + 256 j) .. + 7 (as f32 values of bf16).
-template <int KMAX, int PRO>
-__device__ __forceinline__ void prologue(const GemvArgs& a, float xs[KMAX][8], double* sh) {
-    const uint32_t t = threadIdx.x, nch = (a.cols / 8 + BLOCK - 1) / BLOCK, C = a.cols / 8;
+__device__ __forceinline__ uint32_t pack2(bf16_t lo, bf16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
+
+// Stages x (bf16) in LDS: the given x, or bf16(rmsnorm(residual + delta) * w_norm). Block-wide;
+// ends with a barrier.
+template <int PRO>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, uint4* xl, double* sh) {
+    const uint32_t t = threadIdx.x, C = a.cols / 8;
     if (PRO == PRO_X) {
-#pragma unroll
-        for (int j = 0; j < KMAX; ++j) {
-            const uint32_t c = t + BLOCK * j;
-            uint4 u = make_uint4(0, 0, 0, 0);
-            if (j < (int)nch && c < C) u = *reinterpret_cast<const uint4*>(a.x + 8 * (size_t)c);
-            xs[j][0] = bf_lo(u.x); xs[j][1] = bf_hi(u.x); xs[j][2] = bf_lo(u.y); xs[j][3] = bf_hi(u.y);
-            xs[j][4] = bf_lo(u.z); xs[j][5] = bf_hi(u.z); xs[j][6] = bf_lo(u.w); xs[j][7] = bf_hi(u.w);
-        }
+        for (uint32_t c = t; c < C; c += BLOCK) xl[c] = *reinterpret_cast<const uint4*>(a.x + 8 * (size_t)c);
+        __syncthreads();
         return;
     }
-    // r = residual_in + delta (f32), or the embedding row over a zero residual.
     const bf16_t* drow = a.delta;
     bool zero_row = false;
     if (PRO == PRO_EMBED_NORM) {
@@ -79,55 +80,64 @@ __device__ __forceinline__ void prologue(const GemvArgs& a, float xs[KMAX][8], d
         zero_row = tok >= a.vocab;
         drow = a.embed + (size_t)(zero_row ? 0 : tok) * a.cols;
     }
+    // Pass 1: r = residual + delta (f32), its squares summed in f64; r kept in LDS as f32 pairs
+    // would double the LDS, so it is recomputed in pass 2 (the same f32 additions, the same bits).
     double ss = 0.0;
+    for (uint32_t c = t; c < C; c += BLOCK) {
+        uint4 u = *reinterpret_cast<const uint4*>(drow + 8 * (size_t)c);
+        if (zero_row) u = make_uint4(0, 0, 0, 0);
+        const float d[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y), bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
+        float r[8];
+        if (PRO == PRO_NORM) {
+            const float4 r0 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c);
+            const float4 r1 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c + 4);
+            r[0] = r0.x + d[0]; r[1] = r0.y + d[1]; r[2] = r0.z + d[2]; r[3] = r0.w + d[3];
+            r[4] = r1.x + d[4]; r[5] = r1.y + d[5]; r[6] = r1.z + d[6]; r[7] = r1.w + d[7];
+        } else {
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-        const uint32_t c = t + BLOCK * j;
-        float r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (j < (int)nch && c < C) {
-            uint4 u = *reinterpret_cast<const uint4*>(drow + 8 * (size_t)c);
-            if (zero_row) u = make_uint4(0, 0, 0, 0);
-            const float d[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y),
-                                bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
-            if (PRO == PRO_NORM) {
-                const float4 r0 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c);
-                const float4 r1 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c + 4);
-                r[0] = r0.x + d[0]; r[1] = r0.y + d[1]; r[2] = r0.z + d[2]; r[3] = r0.w + d[3];
-                r[4] = r1.x + d[4]; r[5] = r1.y + d[5]; r[6] = r1.z + d[6]; r[7] = r1.w + d[7];
-            } else {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) r[k] = 0.f + d[k];
-            }
-            if (blockIdx.x == 0 && a.res_out != nullptr) {
-                float4* o = reinterpret_cast<float4*>(a.res_out + 8 * (size_t)c);
-                o[0] = make_float4(r[0], r[1], r[2], r[3]);
-                o[1] = make_float4(r[4], r[5], r[6], r[7]);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) ss += (double)r[k] * (double)r[k];
+            for (int k = 0; k < 8; ++k) r[k] = 0.f + d[k];
+        }
+        if (blockIdx.x == 0 && a.res_out != nullptr) {
+            float4* o = reinterpret_cast<float4*>(a.res_out + 8 * (size_t)c);
+            o[0] = make_float4(r[0], r[1], r[2], r[3]);
+            o[1] = make_float4(r[4], r[5], r[6], r[7]);
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) xs[j][k] = r[k];
+        for (int k = 0; k < 8; ++k) ss += (double)r[k] * (double)r[k];
+        // Keep r in LDS as its f32 bits, two chunks' worth per chunk slot would not fit: store
+        // the bf16 result in pass 2 instead.
     }
     const double total = block_sum_d(ss, sh);
     const double scale = 1.0 / sqrt(total / (double)a.cols + (double)a.eps);
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-        const uint32_t c = t + BLOCK * j;
-        if (j < (int)nch && c < C) {
-            const uint4 u = *reinterpret_cast<const uint4*>(a.norm_w + 8 * (size_t)c);
-            const float w[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y),
-                                bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) xs[j][k] = bf_round((float)((double)xs[j][k] * scale * (double)w[k]));
+    for (uint32_t c = t; c < C; c += BLOCK) {
+        uint4 u = *reinterpret_cast<const uint4*>(drow + 8 * (size_t)c);
+        if (zero_row) u = make_uint4(0, 0, 0, 0);
+        const float d[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y), bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
+        float r[8];
+        if (PRO == PRO_NORM) {
+            const float4 r0 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c);
+            const float4 r1 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c + 4);
+            r[0] = r0.x + d[0]; r[1] = r0.y + d[1]; r[2] = r0.z + d[2]; r[3] = r0.w + d[3];
+            r[4] = r1.x + d[4]; r[5] = r1.y + d[5]; r[6] = r1.z + d[6]; r[7] = r1.w + d[7];
         } else {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) xs[j][k] = 0.f;
+            for (int k = 0; k < 8; ++k) r[k] = 0.f + d[k];
         }
+        const uint4 wn = *reinterpret_cast<const uint4*>(a.norm_w + 8 * (size_t)c);
+        const float w[8] = {bf_lo(wn.x), bf_hi(wn.x), bf_lo(wn.y), bf_hi(wn.y), bf_lo(wn.z), bf_hi(wn.z), bf_lo(wn.w), bf_hi(wn.w)};
+        bf16_t o[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = f2bf((float)((double)r[k] * scale * (double)w[k]));
+        xl[c] = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
     }
+    __syncthreads();
 }
 
-__device__ __forceinline__ float dot8(const uint4 w, const float* x, float acc) {
+template <class A>
+__device__ __forceinline__ A dot8(const uint4 w, const float* x, A acc);
+
+template <>
+__device__ __forceinline__ float dot8<float>(const uint4 w, const float* x, float acc) {
     acc = fmaf(bf_lo(w.x), x[0], acc);
     acc = fmaf(bf_hi(w.x), x[1], acc);
     acc = fmaf(bf_lo(w.y), x[2], acc);
@@ -139,81 +149,150 @@ __device__ __forceinline__ float dot8(const uint4 w, const float* x, float acc) 
     return acc;
 }
 
-// RPB rows per step. For EPI_SWIGLU a step is RPB / 2 pairs: gate rows i.. and up rows inter + i..
-template <int KMAX, int RPB, int PRO, int EPI>
-__device__ __forceinline__ void gemv_body(const GemvArgs& a) {
+// Each product of two bf16 is exact in f32; it is added in f64.
+template <>
+__device__ __forceinline__ double dot8<double>(const uint4 w, const float* x, double acc) {
+    acc += (double)(bf_lo(w.x) * x[0]);
+    acc += (double)(bf_hi(w.x) * x[1]);
+    acc += (double)(bf_lo(w.y) * x[2]);
+    acc += (double)(bf_hi(w.y) * x[3]);
+    acc += (double)(bf_lo(w.z) * x[4]);
+    acc += (double)(bf_hi(w.z) * x[5]);
+    acc += (double)(bf_lo(w.w) * x[6]);
+    acc += (double)(bf_hi(w.w) * x[7]);
+    return acc;
+}
+
+// Sum of R values over the 64 lanes. At the first log2(R) steps (lane bits 5, 4, ...) each lane
+// keeps half of its values (bit set: the upper half) and adds its partner's copy of them; the
+// remaining steps are plain butterflies. Lane l ends with the sum of value reduced_row<R>(l).
+template <int N, int K, class A>
+struct RowReduce {
+    static __device__ __forceinline__ void run(A* v, uint32_t lane) {
+        constexpr int H = N >> 1;
+        const bool bit = (lane >> K) & 1u;
+#pragma unroll
+        for (int j = 0; j < H; ++j) {
+            const A send = bit ? v[j] : v[j + H];
+            const A keep = bit ? v[j + H] : v[j];
+            v[j] = keep + __shfl_xor(send, 1 << K, 64);
+        }
+        RowReduce<H, K - 1, A>::run(v, lane);
+    }
+};
+template <int K, class A>
+struct RowReduce<1, K, A> {
+    static __device__ __forceinline__ void run(A* v, uint32_t lane) {
+        v[0] += __shfl_xor(v[0], 1 << K, 64);
+        RowReduce<1, K - 1, A>::run(v, lane);
+    }
+};
+template <class A>
+struct RowReduce<1, -1, A> {
+    static __device__ __forceinline__ void run(A*, uint32_t) {}
+};
+
+template <int R, class A>
+__device__ __forceinline__ A wave_reduce_rows(A* v) {
+    RowReduce<R, 5, A>::run(v, threadIdx.x & 63);
+    return v[0];
+}
+
+template <int R>
+__device__ __forceinline__ uint32_t reduced_row(uint32_t lane) {
+    uint32_t idx = 0;
+    int n = R;
+#pragma unroll
+    for (int k = 5; k >= 0; --k) {
+        if (n > 1) {
+            const int h = n >> 1;
+            if ((lane >> k) & 1u) idx += h;
+            n = h;
+        }
+    }
+    return idx;
+}
+
+// R rows per wavefront step. For EPI_SWIGLU a step is R / 2 pairs: gate rows i.. and up rows
+// inter + i.. . x is staged in dynamic LDS (cols bf16).
+template <int R, int BATCH, int PRO, int EPI, class Acc>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
     __shared__ double sh[16];
-    __shared__ float part[2][BLOCK / 64][RPB];
-    __shared__ float best_v[BLOCK / 64];
-    __shared__ uint32_t best_i[BLOCK / 64];
+    __shared__ float best_v[WAVES];
+    __shared__ uint32_t best_i[WAVES];
+    __shared__ int any_nan;
     __shared__ uint32_t last;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const uint32_t C = a.cols / 8, nch = (C + BLOCK - 1) / BLOCK;
-    float xs[KMAX][8];
-    prologue<KMAX, PRO>(a, xs, sh);
-
-    constexpr int PAIRS = RPB / 2;
+    const uint32_t C = a.cols / 8;
+    const uint32_t CPL = (C + 63) / 64;  // chunks per lane per row
+    constexpr int PAIRS = R / 2;
     const uint32_t inter = a.rows / 2;
-    const uint32_t groups = EPI == EPI_SWIGLU ? (inter + PAIRS - 1) / PAIRS : (a.rows + RPB - 1) / RPB;
+    const uint32_t groups = EPI == EPI_SWIGLU ? (inter + PAIRS - 1) / PAIRS : (a.rows + R - 1) / R;
+    const uint32_t nwaves = gridDim.x * WAVES;
+    if (EPI == EPI_ARGMAX && t == 0) any_nan = 0;
+
+    stage_x<PRO>(a, xl, sh);
+
     float bv = -INFINITY;
     uint32_t bi = NO_TOKEN;
     bool nan = false;
-    int parity = 0;
-    for (uint32_t g = blockIdx.x; g < groups; g += gridDim.x) {
-        uint32_t row[RPB];
+    for (uint32_t g = blockIdx.x * WAVES + wave; g < groups; g += nwaves) {
+        uint32_t row[R];
+        bool in[R];
 #pragma unroll
-        for (int rr = 0; rr < RPB; ++rr) {
-            if (EPI == EPI_SWIGLU)
-                row[rr] = rr < PAIRS ? g * PAIRS + rr : inter + g * PAIRS + (rr - PAIRS);
-            else
-                row[rr] = g * RPB + rr;
-        }
-        bool in[RPB];
-#pragma unroll
-        for (int rr = 0; rr < RPB; ++rr)
-            in[rr] = EPI == EPI_SWIGLU ? (rr < PAIRS ? row[rr] < inter : row[rr] - inter < inter) : row[rr] < a.rows;
-        uint4 wv[RPB][KMAX];
-#pragma unroll
-        for (int rr = 0; rr < RPB; ++rr) {
-            const bf16_t* wr = a.w + (size_t)row[rr] * a.cols;
-#pragma unroll
-            for (int j = 0; j < KMAX; ++j) {
-                const uint32_t c = t + BLOCK * j;
-                wv[rr][j] = (in[rr] && j < (int)nch && c < C) ? *reinterpret_cast<const uint4*>(wr + 8 * (size_t)c)
-                                                                : make_uint4(0, 0, 0, 0);
+        for (int r = 0; r < R; ++r) {
+            if (EPI == EPI_SWIGLU) {
+                const uint32_t i = g * PAIRS + (r % PAIRS);
+                in[r] = i < inter;
+                row[r] = r < PAIRS ? i : inter + i;
+            } else {
+                row[r] = g * R + r;
+                in[r] = row[r] < a.rows;
             }
         }
-        float acc[RPB];
+        Acc acc[R];
 #pragma unroll
-        for (int rr = 0; rr < RPB; ++rr) {
-            float s = 0.f;
+        for (int r = 0; r < R; ++r) acc[r] = (Acc)0;
+        for (uint32_t b0 = 0; b0 < CPL; b0 += BATCH) {
+            uint4 w[R][BATCH];
 #pragma unroll
-            for (int j = 0; j < KMAX; ++j) s = dot8(wv[rr][j], xs[j], s);
-            acc[rr] = wave_sum(s);
-        }
-        if (lane == 0) {
+            for (int r = 0; r < R; ++r) {
+                const bf16_t* wr = a.w + (size_t)row[r] * a.cols;
 #pragma unroll
-            for (int rr = 0; rr < RPB; ++rr) part[parity][wave][rr] = acc[rr];
-        }
-        __syncthreads();
-        if (EPI == EPI_SWIGLU) {
-            const uint32_t i = g * PAIRS + t;
-            if (t < (uint32_t)PAIRS && i < inter) {
-                float gs = 0.f, us = 0.f;
-#pragma unroll
-                for (int w = 0; w < BLOCK / 64; ++w) {
-                    gs += part[parity][w][t];
-                    us += part[parity][w][PAIRS + t];
+                for (int j = 0; j < BATCH; ++j) {
+                    const uint32_t c = lane + 64 * (b0 + j);
+                    w[r][j] = (in[r] && c < C) ? *reinterpret_cast<const uint4*>(wr + 8 * (size_t)c) : make_uint4(0, 0, 0, 0);
                 }
-                const double gd = (double)bf_round(gs), ud = (double)bf_round(us);
-                reinterpret_cast<bf16_t*>(a.y)[i] = f2bf((float)(gd / (1.0 + exp(-gd)) * ud));
             }
-        } else {
-            const uint32_t r = g * RPB + t;
-            if (t < (uint32_t)RPB && r < a.rows) {
-                float s = 0.f;
 #pragma unroll
-                for (int w = 0; w < BLOCK / 64; ++w) s += part[parity][w][t];
+            for (int j = 0; j < BATCH; ++j) {
+                const uint32_t c = lane + 64 * (b0 + j);
+                if (c < C) {
+                    const uint4 u = xl[c];
+                    const float x[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y),
+                                        bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r] = dot8<Acc>(w[r][j], x, acc[r]);
+                }
+            }
+        }
+        const Acc sum = wave_reduce_rows<R, Acc>(acc);
+        const uint32_t k = reduced_row<R>(lane);
+        const bool holder = (lane & (64 / R - 1)) == 0;  // one lane per row holds its sum
+        if (EPI == EPI_SWIGLU) {
+            // Gate k < PAIRS sits in the lower lanes, up k + PAIRS in the upper: bring up down.
+            const Acc up = __shfl_xor(sum, 32, 64);
+            if (holder && k < (uint32_t)PAIRS && in[0]) {
+                const uint32_t i = g * PAIRS + k;
+                if (i < inter) {
+                    const double gd = (double)bf_round((float)sum), ud = (double)bf_round((float)up);
+                    reinterpret_cast<bf16_t*>(a.y)[i] = f2bf((float)(gd / (1.0 + exp(-gd)) * ud));
+                }
+            }
+        } else if (holder) {
+            const uint32_t r = g * R + k;
+            if (r < a.rows) {
+                const float s = (float)sum;
                 if (EPI == EPI_BF16) reinterpret_cast<bf16_t*>(a.y)[r] = f2bf(s);
                 if (EPI == EPI_F32 || EPI == EPI_ARGMAX) reinterpret_cast<float*>(a.y)[r] = s;
                 if (EPI == EPI_ARGMAX) {
@@ -225,27 +304,36 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
                 }
             }
         }
-        parity ^= 1;
     }
     if (EPI != EPI_ARGMAX) return;
 
-    // This block's candidate: lanes 0..RPB-1 of wave 0 hold one each.
-    if (wave == 0) {
+    // This block's candidate: each wave's over its lanes, then the waves' in LDS.
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const uint32_t oi = __shfl_xor(bi, o, 64);
-            if (better(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (__any(nan) && lane == 0) atomicOr(&any_nan, 1);
+    if (lane == 0) {
+        best_v[wave] = bv;
+        best_i[wave] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float fv = -INFINITY;
+        uint32_t fi = NO_TOKEN;
+        for (int w = 0; w < WAVES; ++w)
+            if (better(best_v[w], best_i[w], fv, fi)) {
+                fv = best_v[w];
+                fi = best_i[w];
             }
-        }
-        const bool any_nan = __any(nan);
-        if (lane == 0) {
-            a.partial[3 * blockIdx.x] = bv;
-            a.partial[3 * blockIdx.x + 1] = __uint_as_float(bi);
-            a.partial[3 * blockIdx.x + 2] = any_nan ? 1.f : 0.f;
-        }
+        a.partial[3 * blockIdx.x] = fv;
+        a.partial[3 * blockIdx.x + 1] = __uint_as_float(fi);
+        a.partial[3 * blockIdx.x + 2] = any_nan ? 1.f : 0.f;
     }
     __threadfence();
     __syncthreads();
@@ -277,23 +365,22 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
         }
     }
     const bool wn = __any(n);
+    __syncthreads();
     if (lane == 0) {
-        best_v[wave] = wn ? NAN : v;
-        best_i[wave] = wn ? NO_TOKEN : i;
+        best_v[wave] = v;
+        best_i[wave] = i;
+        if (wn) atomicOr(&any_nan, 2);
     }
     __syncthreads();
     if (t == 0) {
-        bool any = false;
         float fv = -INFINITY;
         uint32_t fi = NO_TOKEN;
-        for (int w = 0; w < BLOCK / 64; ++w) {
-            if (best_i[w] == NO_TOKEN && best_v[w] != best_v[w]) any = true;
+        for (int w = 0; w < WAVES; ++w)
             if (better(best_v[w], best_i[w], fv, fi)) {
                 fv = best_v[w];
                 fi = best_i[w];
             }
-        }
-        a.token_out[0] = any ? NO_TOKEN : fi;
+        a.token_out[0] = (any_nan & 2) ? NO_TOKEN : fi;
         if (a.advance) a.pos[0] += 1u;
         a.counter[0] = 0;  // ready for the next launch
     }
@@ -301,25 +388,27 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
 
 }  // namespace
 
-// ---- host-side dispatch: one kernel per (KMAX, RPB, prologue, epilogue) ----
-
-template <int KMAX, int RPB, int PRO, int EPI>
+template <int R, int BATCH, int PRO, int EPI, class Acc>
 __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
-    gemv_body<KMAX, RPB, PRO, EPI>(a);
+    extern __shared__ uint4 xl[];
+    gemv_body<R, BATCH, PRO, EPI, Acc>(a, xl);
 }
 
-// Plain GEMV for the kernel table and tests: y[rows] = W x, bf16 or f32 out, any cols that is
-// a multiple of 8 up to 16384 (16-byte chunks); grid (blocks), block 256.
+// Plain GEMV for the kernel table and tests: y[rows] = W x, bf16 or f32 out, f32 accumulation,
+// cols a multiple of 8 up to 16384 (x staged in 32 KiB of static LDS); any grid (persistent),
+// block 256.
 #define X0NE_GEMV_PLAIN(NAME, EPI)                                                                                \
     extern "C" __global__ void __launch_bounds__(256) NAME(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, \
                                                           void* __restrict__ y, uint32_t rows, uint32_t cols) {     \
+        __shared__ uint4 xs[16384 / 8];                                                                           \
+        if (cols > 16384 || cols % 8) return;                                                                     \
         GemvArgs a = {};                                                                                          \
         a.w = w;                                                                                                  \
         a.x = x;                                                                                                  \
         a.y = y;                                                                                                  \
         a.rows = rows;                                                                                            \
         a.cols = cols;                                                                                            \
-        gemv_body<8, 2, PRO_X, EPI>(a);                                                                          \
+        gemv_body<4, 4, PRO_X, EPI, float>(a, xs);                                                                   \
     }
 X0NE_GEMV_PLAIN(x0ne_gemv_bf16, EPI_BF16)
 X0NE_GEMV_PLAIN(x0ne_gemv_f32, EPI_F32)
@@ -353,36 +442,26 @@ extern "C" __global__ void __launch_bounds__(256)
 
 namespace {
 
-template <int RPB, int PRO, int EPI>
-hipError_t launch_k(const GemvArgs& a, uint32_t grid, hipStream_t s) {
-    const uint32_t nch = (a.cols / 8 + BLOCK - 1) / BLOCK;
-    if (nch <= 1) return (gemv_kernel<1, RPB * 4 <= 8 ? RPB * 4 : 8, PRO, EPI><<<grid, BLOCK, 0, s>>>(a), hipGetLastError());
-    if (nch <= 2) return (gemv_kernel<2, RPB * 2 <= 8 ? RPB * 2 : 8, PRO, EPI><<<grid, BLOCK, 0, s>>>(a), hipGetLastError());
-    if (nch <= 4) return (gemv_kernel<4, RPB, PRO, EPI><<<grid, BLOCK, 0, s>>>(a), hipGetLastError());
-    if (nch <= 8) return (gemv_kernel<8, RPB / 2 >= 2 ? RPB / 2 : 2, PRO, EPI><<<grid, BLOCK, 0, s>>>(a), hipGetLastError());
-    if (nch <= 16) return (gemv_kernel<16, 2, PRO, EPI><<<grid, BLOCK, 0, s>>>(a), hipGetLastError());
-    return hipErrorInvalidValue;
-}
-
-template <int PRO, int EPI>
-hipError_t launch_pe(const GemvArgs& a, uint32_t grid, hipStream_t s) {
-    return launch_k<2, PRO, EPI>(a, grid, s);
+template <int R, int BATCH, int PRO, int EPI>
+hipError_t launch_pe(const GemvArgs& a, uint32_t grid, int f64acc, hipStream_t s) {
+    const size_t lds = (size_t)a.cols * 2;
+    if (f64acc)
+        gemv_kernel<R, BATCH, PRO, EPI, double><<<grid, BLOCK, lds, s>>>(a);
+    else
+        gemv_kernel<R, BATCH, PRO, EPI, float><<<grid, BLOCK, lds, s>>>(a);
+    return hipGetLastError();
 }
 
 }  // namespace
 
-// Rows per step the launch above picks for cols (EPI_SWIGLU counts rows of both halves).
-uint32_t x0ne_gemv_rows_per_step(uint32_t cols) {
-    const uint32_t nch = (cols / 8 + BLOCK - 1) / BLOCK;
-    if (nch <= 1) return 8;
-    if (nch <= 2) return 4;
-    if (nch <= 4) return 2;
-    return 2;
-}
+// Rows a wavefront takes per step (SwiGLU: both halves counted).
+uint32_t x0ne_gemv_rows_per_step(uint32_t cols) { return (void)cols, 4u; }
+
+// Row groups a launch walks: the grid is cut to cover them with whole wavefronts.
+uint32_t x0ne_gemv_waves_per_block() { return WAVES; }
 
 hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s) {
-    if (g.cols == 0 || g.cols % 8 != 0 || (g.cols / 8 + BLOCK - 1) / BLOCK > 16 || g.rows == 0 || g.grid == 0)
-        return hipErrorInvalidValue;
+    if (g.cols == 0 || g.cols % 8 != 0 || g.cols > 32768 || g.rows == 0 || g.grid == 0) return hipErrorInvalidValue;
     GemvArgs a = {};
     a.w = g.w;
     a.x = g.x;
@@ -404,7 +483,7 @@ hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s) {
     a.eps = g.eps;
     const int pro = g.prologue, epi = g.epilogue;
 #define X0NE_CASE(P, E) \
-    if (pro == P && epi == E) return launch_pe<P, E>(a, g.grid, s);
+    if (pro == P && epi == E) return launch_pe<4, 4, P, E>(a, g.grid, g.f64acc, s);
     X0NE_CASE(PRO_X, EPI_BF16)
     X0NE_CASE(PRO_X, EPI_F32)
     X0NE_CASE(PRO_NORM, EPI_BF16)

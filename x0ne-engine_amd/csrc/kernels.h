@@ -23,14 +23,22 @@ __global__ void x0ne_attention_decode_bf16(const bf16_t* q, const bf16_t* k_cach
                                            const uint32_t* pages, bf16_t* out, const uint32_t* pos, uint32_t q_heads,
                                            uint32_t kv_heads, uint32_t max_ctx, float scale);
 __global__ void x0ne_attention_decode_split_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
-                                                 const uint32_t* pages, float* state, const uint32_t* pos,
+                                                 const uint32_t* pages, float* state, bf16_t* out, const uint32_t* pos,
                                                  uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx,
                                                  uint32_t splits, float scale);
 #define X0NE_DECLARE_SPLIT_GROUP(G)                                                                              \
     __global__ void x0ne_attention_decode_split_g##G##_bf16(                                                    \
         const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache, const uint32_t* pages, float* state,     \
         uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, \
-        uint32_t splits, float scale);
+        uint32_t splits, float scale);                                                                            \
+    __global__ void x0ne_attention_rope_decode_g##G##_bf16(                                                     \
+        const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq, bf16_t* k_cache,  \
+        bf16_t* v_cache, const uint32_t* pages, float* state, uint32_t* counter, bf16_t* out, const uint32_t* pos, \
+        uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale, float eps);     \
+    __global__ void x0ne_attention_rope_decode_exact_g##G##_bf16(                                               \
+        const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq, bf16_t* k_cache,  \
+        bf16_t* v_cache, const uint32_t* pages, bf16_t* out, const uint32_t* pos, uint32_t q_heads,              \
+        uint32_t kv_heads, uint32_t max_ctx, float eps);
 X0NE_DECLARE_SPLIT_GROUP(1)
 X0NE_DECLARE_SPLIT_GROUP(2)
 X0NE_DECLARE_SPLIT_GROUP(4)

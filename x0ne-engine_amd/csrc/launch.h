@@ -23,10 +23,12 @@ struct X0neGemv {
     float eps;
     int prologue, epilogue;
     uint32_t grid;
+    int f64acc;  // 1: products added in f64 (the oracle's sums), 0: f32 FMA
 };
 
 hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s);
 uint32_t x0ne_gemv_rows_per_step(uint32_t cols);
+uint32_t x0ne_gemv_waves_per_block();
 
 // Device weight initialisers (init.hip): n values of N(0, std) bf16 from stream `key`
 // starting at value `first` (even), and a constant fill.

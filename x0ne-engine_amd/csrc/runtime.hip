@@ -203,8 +203,8 @@ x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32
     if (gx == 0 || gy == 0 || block == 0 || block > k.max_block || block % 64 != 0)
         return fail(X0NE_ERR_GPU, std::string(k.name) + ": launch shape (" + std::to_string(gx) + ", " +
                                       std::to_string(gy) + ") x " + std::to_string(block) + " refused");
-    void* ptrs[16];
-    if (n > 16) return fail(X0NE_ERR_GPU, "too many arguments");
+    void* ptrs[24];
+    if (n > 24) return fail(X0NE_ERR_GPU, "too many arguments");
     for (size_t i = 0; i < n; ++i) {
         switch (args[i].kind) {
             case X0NE_PARAM_PTR: ptrs[i] = (void*)&args[i].ptr; break;
@@ -240,7 +240,7 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
         const uint16_t* xp = (const uint16_t*)(x + r * cols * 2);
         void* yp = (void*)(y + r * rows * ob);
         g->counts.gemms++;
-        const bool fast = cols % 8 == 0 && w % 16 == 0 && (x + r * cols * 2) % 16 == 0 && cols <= 16 * 256 * 8;
+        const bool fast = cols % 8 == 0 && w % 16 == 0 && (x + r * cols * 2) % 16 == 0 && cols <= 32768;
         if (fast) {
             X0neGemv a = {};
             a.w = wp;
@@ -252,8 +252,9 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
             a.epilogue = out_f32 ? 1 : 0;
             const uint32_t rps = x0ne_gemv_rows_per_step((uint32_t)cols);
             const uint64_t groups = (rows + rps - 1) / rps;
+            const uint64_t blocks = (groups + x0ne_gemv_waves_per_block() - 1) / x0ne_gemv_waves_per_block();
             const uint64_t cap = (uint64_t)g->cus * 4;
-            a.grid = (uint32_t)(groups < cap ? groups : cap);
+            a.grid = (uint32_t)(blocks < cap ? blocks : cap);
             g->counts.launches++;
             X0NE_HIP(x0ne_launch_gemv(a, g->stream), "gemv");
         } else {
@@ -280,8 +281,28 @@ static const void* group_kernel(uint32_t group) {
     }
 }
 
+static const void* rope_group_kernel(uint32_t group) {
+    switch (group) {
+        case 1: return (const void*)&x0ne_attention_rope_decode_g1_bf16;
+        case 2: return (const void*)&x0ne_attention_rope_decode_g2_bf16;
+        case 4: return (const void*)&x0ne_attention_rope_decode_g4_bf16;
+        case 8: return (const void*)&x0ne_attention_rope_decode_g8_bf16;
+        default: return nullptr;
+    }
+}
+
+static const void* exact_group_kernel(uint32_t group) {
+    switch (group) {
+        case 1: return (const void*)&x0ne_attention_rope_decode_exact_g1_bf16;
+        case 2: return (const void*)&x0ne_attention_rope_decode_exact_g2_bf16;
+        case 4: return (const void*)&x0ne_attention_rope_decode_exact_g4_bf16;
+        case 8: return (const void*)&x0ne_attention_rope_decode_exact_g8_bf16;
+        default: return nullptr;
+    }
+}
+
 // Most slices a merge reads (the merge keeps one weight per slice in LDS).
-static constexpr uint32_t MAX_SPLITS = 1024;
+static constexpr uint32_t MAX_SPLITS = 256;
 // P for a decode step: slices of a kv head beyond this add merge work for nothing at the
 // contexts of a decode (a slice of 64-key tiles each).
 static constexpr uint32_t DEFAULT_SPLIT_CAP = 128;
@@ -299,7 +320,7 @@ x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x
     p.grid_x = p.grouped ? kv_heads : q_heads;
     if (!k) k = (const void*)&x0ne_attention_decode_split_bf16;
     int per = 0;
-    X0NE_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, 64, 0), "occupancy of the split kernel");
+    X0NE_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, 256, 0), "occupancy of the split kernel");
     p.per_cu = per > 0 ? (uint32_t)per : 1;
     uint32_t splits = g->cus * p.per_cu / p.grid_x;
     if (splits < 1) splits = 1;
@@ -313,30 +334,63 @@ x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_b
                             const void* v, const void* pages, void* state, void* counter, void* out, const void* pos,
                             uint32_t qh, uint32_t kvh, uint32_t max_ctx, float scale) {
     const uint32_t p = plan.splits;
-    if (p == 0 || p > MAX_SPLITS) return fail(X0NE_ERR_GPU, "split-K: P " + std::to_string(p) + " outside 1..=1024");
+    if (p == 0 || p > MAX_SPLITS) return fail(X0NE_ERR_GPU, "split-K: P " + std::to_string(p) + " outside 1..=256");
     if (kvh == 0 || qh % kvh != 0) return fail(X0NE_ERR_GPU, "split-K: heads");
     if (plan.grouped) {
         const void* kern = group_kernel(plan.group);
         if (!kern || plan.group != qh / kvh) return fail(X0NE_ERR_GPU, "split-K: the plan's group differs");
+        // Without the counter the merge kernel below follows; either way a block writes out
+        // itself when one slice holds the whole context (and the merge then returns at once).
         void* cnt = last_block ? counter : nullptr;
-        void* o = last_block ? out : nullptr;
         void* args[] = {(void*)&q, (void*)&k, (void*)&v, (void*)&pages, (void*)&state, (void*)&cnt,
-                        (void*)&o, (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&p, (void*)&scale};
+                        (void*)&out, (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&p, (void*)&scale};
         g->counts.launches++;
-        X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, p), dim3(64), args, 0, g->stream), "split-K attention");
+        X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "split-K attention");
         if (last_block) return X0NE_OK;
     } else {
         if (last_block) return fail(X0NE_ERR_GPU, "the last-block merge needs a grouped split-K kernel");
         g->counts.launches++;
-        hipLaunchKernelGGL(x0ne_attention_decode_split_bf16, dim3(qh, p), dim3(64), 0, g->stream,
+        hipLaunchKernelGGL(x0ne_attention_decode_split_bf16, dim3(qh, p), dim3(256), 0, g->stream,
                            (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const uint32_t*)pages,
-                           (float*)state, (const uint32_t*)pos, qh, kvh, max_ctx, p, scale);
+                           (float*)state, (bf16_t*)out, (const uint32_t*)pos, qh, kvh, max_ctx, p, scale);
         X0NE_HIP(hipGetLastError(), "split-K attention");
     }
     g->counts.launches++;
     hipLaunchKernelGGL(x0ne_attention_merge_bf16, dim3(qh), dim3(64), 0, g->stream, (const float*)state,
                        (bf16_t*)out, (const uint32_t*)pos, max_ctx, p);
     X0NE_HIP(hipGetLastError(), "split-K merge");
+    return X0NE_OK;
+}
+
+x0ne_status attention_rope_split(x0ne_gpu* g, const x0ne_split_plan& plan, const void* qkv, const void* q_norm,
+                                 const void* k_norm, const void* inv_freq, void* k, void* v, const void* pages,
+                                 void* state, void* counter, void* out, const void* pos, uint32_t qh, uint32_t kvh,
+                                 uint32_t max_ctx, float scale, float eps) {
+    const uint32_t p = plan.splits;
+    if (p == 0 || p > MAX_SPLITS) return fail(X0NE_ERR_GPU, "split-K: P " + std::to_string(p) + " outside 1..=256");
+    if (!plan.grouped || kvh == 0 || qh % kvh != 0 || plan.group != qh / kvh)
+        return fail(X0NE_ERR_GPU, "fused attention needs a grouped plan of this geometry");
+    const void* kern = rope_group_kernel(plan.group);
+    if (!kern) return fail(X0NE_ERR_GPU, "fused attention: no kernel for this group size");
+    void* args[] = {(void*)&qkv,   (void*)&q_norm, (void*)&k_norm, (void*)&inv_freq, (void*)&k,
+                    (void*)&v,     (void*)&pages,  (void*)&state,  (void*)&counter,  (void*)&out,
+                    (void*)&pos,   (void*)&qh,     (void*)&kvh,    (void*)&max_ctx,  (void*)&p,
+                    (void*)&scale, (void*)&eps};
+    g->counts.launches++;
+    X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "fused decode attention");
+    return X0NE_OK;
+}
+
+x0ne_status attention_rope_exact(x0ne_gpu* g, const void* qkv, const void* q_norm, const void* k_norm,
+                                 const void* inv_freq, void* k, void* v, const void* pages, void* out, const void* pos,
+                                 uint32_t qh, uint32_t kvh, uint32_t max_ctx, float eps) {
+    if (kvh == 0 || qh % kvh != 0) return fail(X0NE_ERR_GPU, "exact attention: heads");
+    const void* kern = exact_group_kernel(qh / kvh);
+    if (!kern) return fail(X0NE_ERR_GPU, "exact attention: no kernel for group " + std::to_string(qh / kvh));
+    void* args[] = {(void*)&qkv, (void*)&q_norm, (void*)&k_norm, (void*)&inv_freq, (void*)&k, (void*)&v,
+                    (void*)&pages, (void*)&out, (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
+    g->counts.launches++;
+    X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, 1), dim3(256), args, 0, g->stream), "exact decode attention");
     return X0NE_OK;
 }
 

@@ -8,14 +8,22 @@ static const X0neKernel TABLE[] = {
     {"x0ne_embedding_bf16", (const void*)&x0ne_embedding_bf16, "pppuu", 128},
     {"x0ne_add_rmsnorm_bf16", (const void*)&x0ne_add_rmsnorm_bf16, "ppppuf", 256},
     {"x0ne_qk_norm_rope_kv_write_bf16", (const void*)&x0ne_qk_norm_rope_kv_write_bf16, "pppppppppuuuf", 64},
-    {"x0ne_attention_decode_bf16", (const void*)&x0ne_attention_decode_bf16, "ppppppuuuf", 64},
-    {"x0ne_attention_decode_split_bf16", (const void*)&x0ne_attention_decode_split_bf16, "ppppppuuuuf", 64},
-    {"x0ne_attention_decode_split_g1_bf16", (const void*)&x0ne_attention_decode_split_g1_bf16, "ppppppppuuuuf", 64},
-    {"x0ne_attention_decode_split_g2_bf16", (const void*)&x0ne_attention_decode_split_g2_bf16, "ppppppppuuuuf", 64},
-    {"x0ne_attention_decode_split_g4_bf16", (const void*)&x0ne_attention_decode_split_g4_bf16, "ppppppppuuuuf", 64},
-    {"x0ne_attention_decode_split_g8_bf16", (const void*)&x0ne_attention_decode_split_g8_bf16, "ppppppppuuuuf", 64},
+    {"x0ne_attention_decode_bf16", (const void*)&x0ne_attention_decode_bf16, "ppppppuuuf", 256},
+    {"x0ne_attention_decode_split_bf16", (const void*)&x0ne_attention_decode_split_bf16, "pppppppuuuuf", 256},
+    {"x0ne_attention_decode_split_g1_bf16", (const void*)&x0ne_attention_decode_split_g1_bf16, "ppppppppuuuuf", 256},
+    {"x0ne_attention_decode_split_g2_bf16", (const void*)&x0ne_attention_decode_split_g2_bf16, "ppppppppuuuuf", 256},
+    {"x0ne_attention_decode_split_g4_bf16", (const void*)&x0ne_attention_decode_split_g4_bf16, "ppppppppuuuuf", 256},
+    {"x0ne_attention_decode_split_g8_bf16", (const void*)&x0ne_attention_decode_split_g8_bf16, "ppppppppuuuuf", 256},
+    {"x0ne_attention_rope_decode_g1_bf16", (const void*)&x0ne_attention_rope_decode_g1_bf16, "pppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_g2_bf16", (const void*)&x0ne_attention_rope_decode_g2_bf16, "pppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_g4_bf16", (const void*)&x0ne_attention_rope_decode_g4_bf16, "pppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_g8_bf16", (const void*)&x0ne_attention_rope_decode_g8_bf16, "pppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_exact_g1_bf16", (const void*)&x0ne_attention_rope_decode_exact_g1_bf16, "pppppppppuuuf", 256},
+    {"x0ne_attention_rope_decode_exact_g2_bf16", (const void*)&x0ne_attention_rope_decode_exact_g2_bf16, "pppppppppuuuf", 256},
+    {"x0ne_attention_rope_decode_exact_g4_bf16", (const void*)&x0ne_attention_rope_decode_exact_g4_bf16, "pppppppppuuuf", 256},
+    {"x0ne_attention_rope_decode_exact_g8_bf16", (const void*)&x0ne_attention_rope_decode_exact_g8_bf16, "pppppppppuuuf", 256},
     {"x0ne_attention_merge_bf16", (const void*)&x0ne_attention_merge_bf16, "pppuu", 64},
-    {"x0ne_attention_prefill_bf16", (const void*)&x0ne_attention_prefill_bf16, "ppppppuuuuf", 64},
+    {"x0ne_attention_prefill_bf16", (const void*)&x0ne_attention_prefill_bf16, "ppppppuuuuf", 256},
     {"x0ne_swiglu_bf16", (const void*)&x0ne_swiglu_bf16, "ppu", 256},
     {"x0ne_argmax_f32", (const void*)&x0ne_argmax_f32, "pup", 1024},
     {"x0ne_advance_u32", (const void*)&x0ne_advance_u32, "p", 64},

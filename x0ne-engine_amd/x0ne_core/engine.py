@@ -32,12 +32,13 @@ class DecodeMode(IntEnum):
 @dataclass
 class EngineOptions:
     """EngineOptions (engine.rs:38-40) plus the KV page order (0: identity, else a seeded
-    shuffle)."""
+    shuffle) and the projections' summation (f32 FMA, or each exact product added in f64)."""
     max_ctx: int
     page_seed: int = 0
+    f64_sums: bool = False
 
     def c(self):
-        return EngineOptionsC(self.max_ctx, self.page_seed)
+        return EngineOptionsC(self.max_ctx, self.page_seed, int(self.f64_sums), 0)
 
 
 def _ids(ids):

@@ -249,7 +249,7 @@ class Kernels:
         self._check_attention(q, k, v, ctx, h)
         a, s = self._kv_arena(q, k, v, ctx, h, page_of, pool, [("out", h.q_dim * 2)])
         a.write(s["pos"], 0, np.array([ctx - 1], np.uint32))
-        self.gpu.launch("x0ne_attention_decode_bf16", h.q_heads, 64,
+        self.gpu.launch("x0ne_attention_decode_bf16", h.q_heads, 256,
                         [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
                          Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])),
                          Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.f32(attn_scale(h.head_dim))])
@@ -283,6 +283,69 @@ class Kernels:
             raise GpuError(f"split-K counters not reset: {counts.tolist()}")
         return a.read_array(s["out"], 0, h.q_dim, np.uint16)
 
+    def attention_rope_decode(self, qkv, q_norm, k_norm, eps: float, theta: float, k, v, ctx: int, h: Heads,
+                              last_block=True, splits=None, page_of=None, pool=None, exact=False):
+        """The engine's fused decode attention (one launch per layer): QK-norm + RoPE of the q
+        heads of the packed qkv row at position ctx - 1, that position's K/V row written into its
+        page, then split-K attention over keys 0..ctx-1 (k, v hold rows 0..ctx-2). last_block
+        False runs the merge kernel after it. Returns (out, k_row, v_row) with the K/V row read
+        back from the cache (the composition of ops.rs:138-208 and ops.rs:491-573). exact: the
+        exact mode's kernel (f64 scores, softmax and sums; one block per kv head, no split)."""
+        h.check()
+        qd, kvd = h.q_dim, h.kv_dim
+        if ctx == 0 or qkv.size != qd + 2 * kvd or k.size < (ctx - 1) * kvd or v.size < (ctx - 1) * kvd:
+            raise FormatError("attention_rope_decode: lengths")
+        plan = self.split_plan(h)
+        if not plan.grouped:
+            raise FormatError(f"attention_rope_decode: no grouped kernel for group {h.q_heads // h.kv_heads}")
+        if splits is not None:
+            plan.splits = int(splits)
+        nan_row = np.full(kvd, NAN_BF16, np.uint16)
+        kf = np.concatenate([np.asarray(k, np.uint16)[:(ctx - 1) * kvd], nan_row])
+        vf = np.concatenate([np.asarray(v, np.uint16)[:(ctx - 1) * kvd], nan_row])
+        hd = h.head_dim
+        a, s = self._kv_arena(np.asarray(qkv, np.uint16), kf, vf, ctx, h, page_of, pool,
+                              [("out", qd * 2), ("state", split_state_bytes(h.q_heads, plan.splits)),
+                               ("counter", h.kv_heads * 4), ("q_norm", hd * 2), ("k_norm", hd * 2),
+                               ("inv_freq", hd // 2 * 4)])
+        a.write(s["pos"], 0, np.array([ctx - 1], np.uint32))
+        a.write(s["q_norm"], 0, np.asarray(q_norm, np.uint16))
+        a.write(s["k_norm"], 0, np.asarray(k_norm, np.uint16))
+        a.write(s["inv_freq"], 0, inv_freq(hd, theta))
+        counter = a.ptr(s["counter"]) if last_block else 0
+        if exact:
+            self.gpu.launch(f"x0ne_attention_rope_decode_exact_g{plan.group}_bf16", (h.kv_heads, 1), 256,
+                            [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["q_norm"])), Arg.ptr(a.ptr(s["k_norm"])),
+                             Arg.ptr(a.ptr(s["inv_freq"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
+                             Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])),
+                             Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.f32(eps)])
+            last_block = True
+        else:
+            self.gpu.launch(f"x0ne_attention_rope_decode_g{plan.group}_bf16", (h.kv_heads, plan.splits), 256,
+                            [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["q_norm"])), Arg.ptr(a.ptr(s["k_norm"])),
+                             Arg.ptr(a.ptr(s["inv_freq"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
+                             Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["state"])), Arg.ptr(counter),
+                             Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(h.q_heads),
+                             Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.u32(plan.splits),
+                             Arg.f32(attn_scale(hd)), Arg.f32(eps)])
+        if not last_block:
+            self.gpu.launch("x0ne_attention_merge_bf16", h.q_heads, 64,
+                            [Arg.ptr(a.ptr(s["state"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])),
+                             Arg.u32(ctx), Arg.u32(plan.splits)])
+        self.gpu.sync()
+        counts = a.read_array(s["counter"], 0, h.kv_heads, np.uint32)
+        if counts.any():
+            raise GpuError(f"split-K counters not reset: {counts.tolist()}")
+        pages = n_pages(ctx)
+        page_of = list(range(pages)) if page_of is None else list(page_of)
+        pg, slot = page_of[(ctx - 1) // PAGE], (ctx - 1) % PAGE
+        k_rows, v_rows = [], []
+        for kh in range(h.kv_heads):
+            at = ((pg * h.kv_heads + kh) * PAGE + slot) * HEAD_DIM
+            k_rows.append(a.read_array(s["k"], at * 2, HEAD_DIM, np.uint16))
+            v_rows.append(a.read_array(s["v"], at * 2, HEAD_DIM, np.uint16))
+        return a.read_array(s["out"], 0, qd, np.uint16), np.concatenate(k_rows), np.concatenate(v_rows)
+
     def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None):
         """Causal attention for positions pos0..t of a t-position cache in one launch at pos0
         (ops.rs:724-775); q holds those t - pos0 rows; returns the rows asked for."""
@@ -293,7 +356,7 @@ class Kernels:
             raise FormatError("attention_prefill_at: lengths")
         a, s = self._kv_arena(q, k, v, t, h, page_of, pool, [("out", m * h.q_dim * 2)])
         a.write(s["pos"], 0, np.array([pos0], np.uint32))
-        self.gpu.launch("x0ne_attention_prefill_bf16", (h.q_heads, m), 64,
+        self.gpu.launch("x0ne_attention_prefill_bf16", (h.q_heads, m), 256,
                         [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
                          Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(m),
                          Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(t), Arg.f32(attn_scale(h.head_dim))])
