@@ -106,6 +106,9 @@ def main():
                     help="launch each step's kernels one by one instead of replaying the captured graph "
                          "(for kernel-trace profilers; the same kernels and results)")
     ap.add_argument("--f64-sums", action="store_true", help="f64 accumulation in the GEMVs")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run one device-to-device copy of MIB MiB (a plain copy kernel of known size, "
+                         "for scaling hardware byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); every box here has one, "
@@ -148,13 +151,25 @@ def main():
     # Weights, the residual read (f32) and written (f32, block 0), delta and the norm weight (bf16),
     # the SwiGLU output (inter bf16).
     gu_bytes = 2 * inter * h * 2 + 4 * h + 4 * h + 2 * h + 2 * h + 2 * inter
-    avg_us, launches = e.time_kernel("gate_up", args.kernel_iters)
+    avg_us, wall_us, launches = e.time_kernel("gate_up", args.kernel_iters)
     achieved = gu_bytes / (avg_us * 1e-6) / 1e9
     others = {}
-    for k in ("qkv", "o", "down", "head", "attention"):
-        us, _ = e.time_kernel(k, args.kernel_iters)
-        others[k] = round(us, 2)
-    print(f"[bench] gate_up {avg_us:.2f} us ({achieved:.0f} GB/s); others us {others}", file=sys.stderr, flush=True)
+    for k in ("qkv", "attention", "o", "down", "head"):
+        kus, wus, _ = e.time_kernel(k, args.kernel_iters)
+        others[k] = {"kernel_us": round(kus, 2), "wall_us": round(wus, 2)}
+    print(f"[bench] gate_up {avg_us:.2f} us ({achieved:.0f} GB/s), {wall_us:.2f} us per launch with gaps; "
+          f"others {others}", file=sys.stderr, flush=True)
+
+    if args.calibrate_copy:
+        import torch
+        n = args.calibrate_copy << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
@@ -189,7 +204,9 @@ def main():
         "roofline": {"kernel": "gate_up GEMV (add+RMSNorm prologue, SwiGLU epilogue)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(achieved / 8000.0, 4), "traffic": None, "bytes_per_launch": gu_bytes,
-                     "avg_us": round(avg_us, 3), "launches_timed": launches, "other_kernels_us": others},
+                     "avg_us": round(avg_us, 3), "wall_us_per_launch": round(wall_us, 3),
+                     "launches_timed": launches, "timing": "hipExtLaunchKernel start/stop events per launch",
+                     "other_kernels": others},
         "cpu_baseline": cpu,
         "tokens_head": tokens[:8].tolist(),
     }

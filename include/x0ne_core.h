@@ -262,8 +262,12 @@ x0ne_status x0ne_engine_page(const x0ne_engine* e, uint64_t i, uint32_t* out);
 
 /* One kernel of the decode step timed alone with HIP events on the engine's stream (this
    build's measurement hook, the analogue of ops.rs:585-681 attention_decode_timed): `iters`
-   rounds over every layer's weights (so no cache holds them), after one warm-up round; the
-   average duration of one launch in microseconds. Client bytes are zeroed afterwards. */
+   rounds over every layer's weights (so no cache holds them), launched back to back after one
+   warm-up round. kernel_us: the average duration of one launch's kernels, from the start and
+   stop events hipExtLaunchKernel records at the kernel's own begin and end (the figure a kernel
+   trace reports); wall_us: the average time per launch between events around the whole run,
+   gaps between launches included (either pointer may be NULL). Client bytes are zeroed
+   afterwards. */
 typedef enum {
     X0NE_KERNEL_QKV = 0,
     X0NE_KERNEL_ATTENTION = 1,
@@ -272,8 +276,8 @@ typedef enum {
     X0NE_KERNEL_DOWN = 4,
     X0NE_KERNEL_HEAD = 5,
 } x0ne_step_kernel;
-x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* avg_us,
-                                    uint64_t* launches);
+x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* kernel_us,
+                                    double* wall_us, uint64_t* launches);
 
 /* The reference's constants (engine.rs:67-79; kernels/src/lib.rs:135-144). */
 #define X0NE_GREEDY_AHEAD 2

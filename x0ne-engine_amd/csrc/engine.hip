@@ -21,6 +21,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <vector>
 
 #include "internal.h"
 #include "json.h"
@@ -379,27 +380,29 @@ x0ne_status plan(x0ne_engine* e) {
     return X0NE_OK;
 }
 
-// Blocks of a GEMV launch: enough wavefronts for every row group, at most `bpc` blocks per CU
-// (a persistent grid; each wavefront walks its row groups).
-uint32_t grid_for(const x0ne_engine* e, uint64_t rows, uint64_t rows_per_group) {
-    static const char* env = std::getenv("X0NE_GEMV_BLOCKS_PER_CU");
-    uint64_t bpc = 4;
-    if (env && std::atoi(env) > 0) bpc = (uint64_t)std::atoi(env);
-    const uint64_t groups = (rows + rows_per_group - 1) / rows_per_group;
-    const uint64_t wpb = x0ne_gemv_waves_per_block();
-    const uint64_t blocks = (groups + wpb - 1) / wpb;
-    const uint64_t cap = (uint64_t)e->gpu->cus * bpc;
-    return (uint32_t)(blocks < cap ? blocks : cap);
-}
-
-void plan_grids(x0ne_engine* e) {
+// The GEMV grids of a decode step: the kernel's occupancy on this device, the row groups split
+// evenly over the resident wavefronts (x0ne_gemv_grid). X0NE_GEMV_BLOCKS_PER_CU caps the blocks
+// per CU (a tuning knob; unset, the occupancy decides).
+x0ne_status plan_grids(x0ne_engine* e) {
     const Cfg& c = e->c;
-    const uint64_t r = x0ne_gemv_rows_per_step(0);
-    e->grid_qkv = grid_for(e, c.qkv_rows(), r);
-    e->grid_o = grid_for(e, c.hidden, r);
-    e->grid_gu = grid_for(e, c.inter, r / 2);
-    e->grid_down = grid_for(e, c.hidden, r);
-    e->grid_head = grid_for(e, c.vocab, r);
+    static const char* env = std::getenv("X0NE_GEMV_BLOCKS_PER_CU");
+    const uint32_t cap = env && std::atoi(env) > 0 ? (uint32_t)std::atoi(env) : 0;
+    auto grid = [&](uint64_t rows, uint64_t cols, int pro, int epi, uint32_t* out) -> x0ne_status {
+        X0neGemv a = {};
+        a.rows = (uint32_t)rows;
+        a.cols = (uint32_t)cols;
+        a.prologue = pro;
+        a.epilogue = epi;
+        a.f64acc = e->f64_sums;
+        *out = x0ne_gemv_grid(a, e->gpu->cus, cap);
+        if (*out == 0) return fail(X0NE_ERR_FORMAT, "a projection shape the GEMV refuses");
+        return X0NE_OK;
+    };
+    X0NE_TRY(grid(c.qkv_rows(), c.hidden, 1, 0, &e->grid_qkv));
+    X0NE_TRY(grid(c.hidden, c.q_dim(), 0, 0, &e->grid_o));
+    X0NE_TRY(grid(2 * c.inter, c.hidden, 1, 2, &e->grid_gu));
+    X0NE_TRY(grid(c.hidden, c.inter, 0, 0, &e->grid_down));
+    return grid(c.vocab, c.hidden, 1, 3, &e->grid_head);
 }
 
 // The kernels of one decode step, one helper each. Norm j of the step reads residual buffer
@@ -437,12 +440,22 @@ x0ne_status launch_rope(x0ne_engine* e, uint64_t l) {
     const LayerW& w = e->L[l];
     const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads;
     e->gpu->counts.launches++;
-    hipLaunchKernelGGL(x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, 1), dim3(64), 0, e->gpu->stream,
-                       (const bf16_t*)e->d(e->qkv), (const bf16_t*)e->d(w.q_norm), (const bf16_t*)e->d(w.k_norm),
-                       (const float*)e->d(e->inv_freq), (bf16_t*)e->d(e->q), (bf16_t*)e->plane(l, 0),
-                       (bf16_t*)e->plane(l, 1), (const uint32_t*)e->d(e->page_table), (const uint32_t*)e->d(e->pos),
-                       qh, kvh, (uint32_t)e->max_ctx, (float)c.eps);
-    X0NE_HIP(hipGetLastError(), "qk_norm_rope_kv_write");
+    const void* qkv = e->d(e->qkv);
+    const void* qn = e->d(w.q_norm);
+    const void* kn = e->d(w.k_norm);
+    const void* inv = e->d(e->inv_freq);
+    void* q = e->d(e->q);
+    void* kc = e->plane(l, 0);
+    void* vc = e->plane(l, 1);
+    const void* pt = e->d(e->page_table);
+    const void* pos = e->d(e->pos);
+    uint32_t max_ctx = (uint32_t)e->max_ctx;
+    float eps = (float)c.eps;
+    void* args[] = {(void*)&qkv, (void*)&qn, (void*)&kn,      (void*)&inv, (void*)&q,   (void*)&kc,  (void*)&vc,
+                    (void*)&pt,  (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
+    X0NE_HIP(x0ne_launch((const void*)&x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, 1), dim3(64), args, 0,
+                         e->gpu->stream),
+             "qk_norm_rope_kv_write");
     return X0NE_OK;
 }
 
@@ -716,7 +729,7 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
         return s;
     };
     if ((st = split_plan(e->gpu, (uint32_t)c.q_heads, (uint32_t)c.kv_heads, &e->split)) != X0NE_OK) return bail(st);
-    plan_grids(e);
+    if ((st = plan_grids(e)) != X0NE_OK) return bail(st);
     if ((st = x0ne_arena_new(&e->arena)) != X0NE_OK) return bail(st);
     if ((st = plan(e)) != X0NE_OK) return bail(st);
     if ((st = x0ne_arena_freeze(e->arena, e->gpu)) != X0NE_OK) return bail(st);
@@ -1239,9 +1252,9 @@ extern "C" x0ne_status x0ne_engine_counts(const x0ne_engine* e, x0ne_counts* out
     return x0ne_gpu_counts(e->gpu, out);
 }
 
-extern "C" x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* avg_us,
-                                              uint64_t* launches) {
-    if (!e || !avg_us || iters == 0) return fail(X0NE_ERR_FORMAT, "null argument");
+extern "C" x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* kernel_us,
+                                              double* wall_us, uint64_t* launches) {
+    if (!e || iters == 0) return fail(X0NE_ERR_FORMAT, "null argument");
     if (which > X0NE_KERNEL_HEAD) return fail(X0NE_ERR_FORMAT, "unknown kernel");
     if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
     auto one = [&](uint64_t l) -> x0ne_status {
@@ -1258,24 +1271,38 @@ extern "C" x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, u
     const uint64_t per = which == X0NE_KERNEL_HEAD ? 1
                          : which == X0NE_KERNEL_QKV ? (e->c.layers > 1 ? e->c.layers - 1 : 1)
                                                     : e->c.layers;
-    hipEvent_t a = nullptr, b = nullptr;
-    X0NE_HIP(hipEventCreate(&a), "event");
-    X0NE_HIP(hipEventCreate(&b), "event");
+    const uint64_t n = (uint64_t)iters * per;
+    std::vector<hipEvent_t> ev(2 * n + 2, nullptr);
     x0ne_status st = X0NE_OK;
+    for (auto& x : ev)
+        if (st == X0NE_OK && hipEventCreate(&x) != hipSuccess) st = fail(X0NE_ERR_GPU, "event create");
     for (uint64_t l = 0; l < per && st == X0NE_OK; ++l) st = one(l);  // warm-up round
-    if (st == X0NE_OK && hipEventRecord(a, e->gpu->stream) != hipSuccess) st = fail(X0NE_ERR_GPU, "event record");
-    for (uint32_t i = 0; i < iters && st == X0NE_OK; ++i)
-        for (uint64_t l = 0; l < per && st == X0NE_OK; ++l) st = one(l);
-    float ms = 0.f;
-    if (st == X0NE_OK && hipEventRecord(b, e->gpu->stream) != hipSuccess) st = fail(X0NE_ERR_GPU, "event record");
-    if (st == X0NE_OK && hipEventSynchronize(b) != hipSuccess) st = fail(X0NE_ERR_GPU, "event wait");
-    if (st == X0NE_OK && hipEventElapsedTime(&ms, a, b) != hipSuccess) st = fail(X0NE_ERR_GPU, "elapsed time");
-    (void)hipEventDestroy(a);
-    (void)hipEventDestroy(b);
+    if (st == X0NE_OK && hipEventRecord(ev[2 * n], e->gpu->stream) != hipSuccess) st = fail(X0NE_ERR_GPU, "event");
+    std::vector<X0neTimer> timers(n);
+    for (uint64_t i = 0; i < n && st == X0NE_OK; ++i) {
+        timers[i] = X0neTimer{ev[2 * i], ev[2 * i + 1], false};
+        x0ne_timer = &timers[i];
+        st = one(i % per);
+        x0ne_timer = nullptr;
+    }
+    if (st == X0NE_OK && hipEventRecord(ev[2 * n + 1], e->gpu->stream) != hipSuccess) st = fail(X0NE_ERR_GPU, "event");
+    if (st == X0NE_OK && hipEventSynchronize(ev[2 * n + 1]) != hipSuccess) st = fail(X0NE_ERR_GPU, "event wait");
+    double kern_ms = 0.0;
+    float wall_ms = 0.f;
+    for (uint64_t i = 0; i < n && st == X0NE_OK; ++i) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) st = fail(X0NE_ERR_GPU, "elapsed time");
+        kern_ms += ms;
+    }
+    if (st == X0NE_OK && hipEventElapsedTime(&wall_ms, ev[2 * n], ev[2 * n + 1]) != hipSuccess)
+        st = fail(X0NE_ERR_GPU, "elapsed time");
+    for (auto& x : ev)
+        if (x) (void)hipEventDestroy(x);
     x0ne_status sc = scrub(e);
     if (st != X0NE_OK) return st;
-    *avg_us = (double)ms * 1000.0 / ((double)iters * (double)per);
-    if (launches) *launches = (uint64_t)iters * per;
+    if (kernel_us) *kernel_us = kern_ms * 1000.0 / (double)n;
+    if (wall_us) *wall_us = (double)wall_ms * 1000.0 / (double)n;
+    if (launches) *launches = n;
     return sc;
 }
 

@@ -64,9 +64,12 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 __device__ __forceinline__ uint32_t pack2(bf16_t lo, bf16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
 // Stages x (bf16) in LDS: the given x, or bf16(rmsnorm(residual + delta) * w_norm). Block-wide;
-// ends with a barrier.
+// ends with a barrier. The residual sums of a thread's first KEEP chunks stay in registers between
+// the two passes (hidden sizes up to 256 x 8 x KEEP need no second read); later chunks are read
+// again and recomputed (the same f32 additions, the same bits).
 template <int PRO>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, uint4* xl, double* sh) {
+    constexpr uint32_t KEEP = 2;
     const uint32_t t = threadIdx.x, C = a.cols / 8;
     if (PRO == PRO_X) {
         for (uint32_t c = t; c < C; c += BLOCK) xl[c] = *reinterpret_cast<const uint4*>(a.x + 8 * (size_t)c);
@@ -80,14 +83,10 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, uint4* xl, double* sh
         zero_row = tok >= a.vocab;
         drow = a.embed + (size_t)(zero_row ? 0 : tok) * a.cols;
     }
-    // Pass 1: r = residual + delta (f32), its squares summed in f64; r kept in LDS as f32 pairs
-    // would double the LDS, so it is recomputed in pass 2 (the same f32 additions, the same bits).
-    double ss = 0.0;
-    for (uint32_t c = t; c < C; c += BLOCK) {
+    auto residual = [&](uint32_t c, float* r) {
         uint4 u = *reinterpret_cast<const uint4*>(drow + 8 * (size_t)c);
         if (zero_row) u = make_uint4(0, 0, 0, 0);
         const float d[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y), bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
-        float r[8];
         if (PRO == PRO_NORM) {
             const float4 r0 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c);
             const float4 r1 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c + 4);
@@ -97,6 +96,14 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, uint4* xl, double* sh
 #pragma unroll
             for (int k = 0; k < 8; ++k) r[k] = 0.f + d[k];
         }
+    };
+    // Pass 1: r = residual + delta (f32), block 0 writes it out, squares summed in f64.
+    float keep[KEEP][8];
+    double ss = 0.0;
+    uint32_t it = 0;
+    for (uint32_t c = t; c < C; c += BLOCK, ++it) {
+        float r[8];
+        residual(c, r);
         if (blockIdx.x == 0 && a.res_out != nullptr) {
             float4* o = reinterpret_cast<float4*>(a.res_out + 8 * (size_t)c);
             o[0] = make_float4(r[0], r[1], r[2], r[3]);
@@ -104,24 +111,28 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, uint4* xl, double* sh
         }
 #pragma unroll
         for (int k = 0; k < 8; ++k) ss += (double)r[k] * (double)r[k];
-        // Keep r in LDS as its f32 bits, two chunks' worth per chunk slot would not fit: store
-        // the bf16 result in pass 2 instead.
+#pragma unroll
+        for (uint32_t q = 0; q < KEEP; ++q)
+            if (it == q) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) keep[q][k] = r[k];
+            }
     }
     const double total = block_sum_d(ss, sh);
     const double scale = 1.0 / sqrt(total / (double)a.cols + (double)a.eps);
-    for (uint32_t c = t; c < C; c += BLOCK) {
-        uint4 u = *reinterpret_cast<const uint4*>(drow + 8 * (size_t)c);
-        if (zero_row) u = make_uint4(0, 0, 0, 0);
-        const float d[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y), bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
+    // Pass 2: x = bf16(r * scale * w) in f64.
+    it = 0;
+    for (uint32_t c = t; c < C; c += BLOCK, ++it) {
         float r[8];
-        if (PRO == PRO_NORM) {
-            const float4 r0 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c);
-            const float4 r1 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c + 4);
-            r[0] = r0.x + d[0]; r[1] = r0.y + d[1]; r[2] = r0.z + d[2]; r[3] = r0.w + d[3];
-            r[4] = r1.x + d[4]; r[5] = r1.y + d[5]; r[6] = r1.z + d[6]; r[7] = r1.w + d[7];
-        } else {
+        if (it < KEEP) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) r[k] = 0.f + d[k];
+            for (uint32_t q = 0; q < KEEP; ++q)
+                if (it == q) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) r[k] = keep[q][k];
+                }
+        } else {
+            residual(c, r);
         }
         const uint4 wn = *reinterpret_cast<const uint4*>(a.norm_w + 8 * (size_t)c);
         const float w[8] = {bf_lo(wn.x), bf_hi(wn.x), bf_lo(wn.y), bf_hi(wn.y), bf_lo(wn.z), bf_hi(wn.z), bf_lo(wn.w), bf_hi(wn.w)};
@@ -213,8 +224,15 @@ __device__ __forceinline__ uint32_t reduced_row(uint32_t lane) {
     return idx;
 }
 
-// R rows per wavefront step. For EPI_SWIGLU a step is R / 2 pairs: gate rows i.. and up rows
-// inter + i.. . x is staged in dynamic LDS (cols bf16).
+// A wavefront's work is a sequence of tiles: row group g (R rows; for EPI_SWIGLU R / 2 gate rows
+// i.. and the up rows inter + i..) times batch b (chunks 64 BATCH b + lane + 64 j, j < BATCH, of
+// each row). Tiles are double-buffered in registers: while one is summed the next is in flight,
+// and the first two are requested before the prologue, so the weights' latency overlaps the
+// staging of x. A group's sums are reduced over the wavefront after its last batch.
+struct TilePos {
+    uint32_t g, b;
+};
+
 template <int R, int BATCH, int PRO, int EPI, class Acc>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
     __shared__ double sh[16];
@@ -224,73 +242,94 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
     __shared__ uint32_t last;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t C = a.cols / 8;
-    const uint32_t CPL = (C + 63) / 64;  // chunks per lane per row
+    const uint32_t NB = (C + 64 * BATCH - 1) / (64 * BATCH);  // batches per row group
     constexpr int PAIRS = R / 2;
     const uint32_t inter = a.rows / 2;
     const uint32_t groups = EPI == EPI_SWIGLU ? (inter + PAIRS - 1) / PAIRS : (a.rows + R - 1) / R;
-    const uint32_t nwaves = gridDim.x * WAVES;
+    const uint32_t gw = blockIdx.x * WAVES + wave, nw = gridDim.x * WAVES;
+    const uint32_t my_groups = gw < groups ? (groups - gw + nw - 1) / nw : 0;
+    const uint32_t T = my_groups * NB;  // wavefront-uniform
     if (EPI == EPI_ARGMAX && t == 0) any_nan = 0;
+
+    auto row_of = [&](uint32_t g, int r, bool& in) -> uint32_t {
+        if (EPI == EPI_SWIGLU) {
+            const uint32_t i = g * PAIRS + (r % PAIRS);
+            in = i < inter;
+            return r < PAIRS ? i : inter + i;
+        }
+        const uint32_t row = g * R + r;
+        in = row < a.rows;
+        return row;
+    };
+    auto load = [&](uint4 (&w)[R][BATCH], TilePos p) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            bool in;
+            const uint32_t row = row_of(p.g, r, in);
+            const bf16_t* wr = a.w + (size_t)row * a.cols;
+#pragma unroll
+            for (int j = 0; j < BATCH; ++j) {
+                const uint32_t c = lane + 64 * (BATCH * p.b + j);
+                w[r][j] = (in && c < C) ? *reinterpret_cast<const uint4*>(wr + 8 * (size_t)c) : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto advance = [&](TilePos& p) {
+        if (++p.b == NB) {
+            p.b = 0;
+            p.g += nw;
+        }
+    };
+
+    uint4 w0[R][BATCH], w1[R][BATCH];
+    TilePos lp = {gw, 0};  // next tile to request
+    if (T > 0) {
+        load(w0, lp);
+        advance(lp);
+    }
+    if (T > 1) {
+        load(w1, lp);
+        advance(lp);
+    }
 
     stage_x<PRO>(a, xl, sh);
 
     float bv = -INFINITY;
     uint32_t bi = NO_TOKEN;
     bool nan = false;
-    for (uint32_t g = blockIdx.x * WAVES + wave; g < groups; g += nwaves) {
-        uint32_t row[R];
-        bool in[R];
+    Acc acc[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (EPI == EPI_SWIGLU) {
-                const uint32_t i = g * PAIRS + (r % PAIRS);
-                in[r] = i < inter;
-                row[r] = r < PAIRS ? i : inter + i;
-            } else {
-                row[r] = g * R + r;
-                in[r] = row[r] < a.rows;
+    for (int r = 0; r < R; ++r) acc[r] = (Acc)0;
+
+    auto consume = [&](const uint4 (&w)[R][BATCH], TilePos p) {
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+            const uint32_t c = lane + 64 * (BATCH * p.b + j);
+            if (c < C) {
+                const uint4 u = xl[c];
+                const float x[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y),
+                                    bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] = dot8<Acc>(w[r][j], x, acc[r]);
             }
         }
-        Acc acc[R];
+        if (p.b + 1 != NB) return;
+        // The group's last batch: reduce and write.
+        const Acc sum = wave_reduce_rows<R, Acc>(acc);
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = (Acc)0;
-        for (uint32_t b0 = 0; b0 < CPL; b0 += BATCH) {
-            uint4 w[R][BATCH];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const bf16_t* wr = a.w + (size_t)row[r] * a.cols;
-#pragma unroll
-                for (int j = 0; j < BATCH; ++j) {
-                    const uint32_t c = lane + 64 * (b0 + j);
-                    w[r][j] = (in[r] && c < C) ? *reinterpret_cast<const uint4*>(wr + 8 * (size_t)c) : make_uint4(0, 0, 0, 0);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < BATCH; ++j) {
-                const uint32_t c = lane + 64 * (b0 + j);
-                if (c < C) {
-                    const uint4 u = xl[c];
-                    const float x[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y),
-                                        bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
-#pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] = dot8<Acc>(w[r][j], x, acc[r]);
-                }
-            }
-        }
-        const Acc sum = wave_reduce_rows<R, Acc>(acc);
         const uint32_t k = reduced_row<R>(lane);
         const bool holder = (lane & (64 / R - 1)) == 0;  // one lane per row holds its sum
         if (EPI == EPI_SWIGLU) {
             // Gate k < PAIRS sits in the lower lanes, up k + PAIRS in the upper: bring up down.
             const Acc up = __shfl_xor(sum, 32, 64);
-            if (holder && k < (uint32_t)PAIRS && in[0]) {
-                const uint32_t i = g * PAIRS + k;
-                if (i < inter) {
-                    const double gd = (double)bf_round((float)sum), ud = (double)bf_round((float)up);
-                    reinterpret_cast<bf16_t*>(a.y)[i] = f2bf((float)(gd / (1.0 + exp(-gd)) * ud));
-                }
+            const uint32_t i = p.g * PAIRS + k;
+            if (holder && k < (uint32_t)PAIRS && i < inter) {
+                const double gd = (double)bf_round((float)sum), ud = (double)bf_round((float)up);
+                reinterpret_cast<bf16_t*>(a.y)[i] = f2bf((float)(gd / (1.0 + exp(-gd)) * ud));
             }
         } else if (holder) {
-            const uint32_t r = g * R + k;
+            const uint32_t r = p.g * R + k;
             if (r < a.rows) {
                 const float s = (float)sum;
                 if (EPI == EPI_BF16) reinterpret_cast<bf16_t*>(a.y)[r] = f2bf(s);
@@ -303,6 +342,23 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
                     }
                 }
             }
+        }
+    };
+
+    TilePos cp = {gw, 0};  // next tile to sum
+    for (uint32_t i = 0; i < T; i += 2) {
+        consume(w0, cp);
+        advance(cp);
+        if (i + 2 < T) {
+            load(w0, lp);
+            advance(lp);
+        }
+        if (i + 1 >= T) break;
+        consume(w1, cp);
+        advance(cp);
+        if (i + 3 < T) {
+            load(w1, lp);
+            advance(lp);
         }
     }
     if (EPI != EPI_ARGMAX) return;
@@ -442,26 +498,61 @@ extern "C" __global__ void __launch_bounds__(256)
 
 namespace {
 
-template <int R, int BATCH, int PRO, int EPI>
-hipError_t launch_pe(const GemvArgs& a, uint32_t grid, int f64acc, hipStream_t s) {
-    const size_t lds = (size_t)a.cols * 2;
-    if (f64acc)
-        gemv_kernel<R, BATCH, PRO, EPI, double><<<grid, BLOCK, lds, s>>>(a);
-    else
-        gemv_kernel<R, BATCH, PRO, EPI, float><<<grid, BLOCK, lds, s>>>(a);
-    return hipGetLastError();
+constexpr int TILE_R = 4;      // rows per row group
+constexpr int TILE_BATCH = 4;  // 16-byte chunks per lane per row in one tile
+
+template <int P, int E>
+const void* instance(int f64acc) {
+    return f64acc ? (const void*)&gemv_kernel<TILE_R, TILE_BATCH, P, E, double>
+                  : (const void*)&gemv_kernel<TILE_R, TILE_BATCH, P, E, float>;
+}
+
+const void* pick(int pro, int epi, int f64acc) {
+#define X0NE_CASE(P, E) \
+    if (pro == P && epi == E) return instance<P, E>(f64acc);
+    X0NE_CASE(PRO_X, EPI_BF16)
+    X0NE_CASE(PRO_X, EPI_F32)
+    X0NE_CASE(PRO_NORM, EPI_BF16)
+    X0NE_CASE(PRO_NORM, EPI_SWIGLU)
+    X0NE_CASE(PRO_NORM, EPI_ARGMAX)
+    X0NE_CASE(PRO_NORM, EPI_F32)
+    X0NE_CASE(PRO_EMBED_NORM, EPI_BF16)
+#undef X0NE_CASE
+    return nullptr;
+}
+
+bool shape_ok(const X0neGemv& g) {
+    return g.cols != 0 && g.cols % 8 == 0 && g.cols <= 32768 && g.rows != 0 &&
+           (g.epilogue != EPI_SWIGLU || g.rows % 2 == 0);
 }
 
 }  // namespace
 
-// Rows a wavefront takes per step (SwiGLU: both halves counted).
-uint32_t x0ne_gemv_rows_per_step(uint32_t cols) { return (void)cols, 4u; }
-
-// Row groups a launch walks: the grid is cut to cover them with whole wavefronts.
-uint32_t x0ne_gemv_waves_per_block() { return WAVES; }
+// The grid of a launch: as many wavefronts as can be resident at once (the kernel's occupancy
+// on `cus` CUs, capped at `max_blocks_per_cu` blocks per CU when that is not 0), then cut so the
+// row groups divide as evenly as they can: each wavefront takes ceil(groups / waves) of them,
+// and no more wavefronts are launched than that split needs.
+uint32_t x0ne_gemv_grid(const X0neGemv& g, uint32_t cus, uint32_t max_blocks_per_cu) {
+    if (!shape_ok(g) || cus == 0) return 0;
+    const void* fn = pick(g.prologue, g.epilogue, g.f64acc);
+    if (!fn) return 0;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, BLOCK, (size_t)g.cols * 2) != hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    if (max_blocks_per_cu != 0 && (uint32_t)per_cu > max_blocks_per_cu) per_cu = (int)max_blocks_per_cu;
+    const uint64_t groups = g.epilogue == EPI_SWIGLU ? ((uint64_t)g.rows / 2 + TILE_R / 2 - 1) / (TILE_R / 2)
+                                                     : ((uint64_t)g.rows + TILE_R - 1) / TILE_R;
+    const uint64_t waves_max = (uint64_t)cus * (uint64_t)per_cu * WAVES;
+    const uint64_t per_wave = (groups + waves_max - 1) / waves_max;
+    const uint64_t waves = (groups + per_wave - 1) / per_wave;
+    return (uint32_t)((waves + WAVES - 1) / WAVES);
+}
 
 hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s) {
-    if (g.cols == 0 || g.cols % 8 != 0 || g.cols > 32768 || g.rows == 0 || g.grid == 0) return hipErrorInvalidValue;
+    if (!shape_ok(g) || g.grid == 0) return hipErrorInvalidValue;
+    const void* fn = pick(g.prologue, g.epilogue, g.f64acc);
+    if (!fn) return hipErrorInvalidValue;
     GemvArgs a = {};
     a.w = g.w;
     a.x = g.x;
@@ -481,16 +572,6 @@ hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s) {
     a.vocab = g.vocab;
     a.advance = g.advance;
     a.eps = g.eps;
-    const int pro = g.prologue, epi = g.epilogue;
-#define X0NE_CASE(P, E) \
-    if (pro == P && epi == E) return launch_pe<4, 4, P, E>(a, g.grid, g.f64acc, s);
-    X0NE_CASE(PRO_X, EPI_BF16)
-    X0NE_CASE(PRO_X, EPI_F32)
-    X0NE_CASE(PRO_NORM, EPI_BF16)
-    X0NE_CASE(PRO_NORM, EPI_SWIGLU)
-    X0NE_CASE(PRO_NORM, EPI_ARGMAX)
-    X0NE_CASE(PRO_NORM, EPI_F32)
-    X0NE_CASE(PRO_EMBED_NORM, EPI_BF16)
-#undef X0NE_CASE
-    return hipErrorInvalidValue;
+    void* args[] = {(void*)&a};
+    return x0ne_launch(fn, dim3(g.grid), dim3(BLOCK), args, (size_t)g.cols * 2, s);
 }

@@ -26,9 +26,23 @@ struct X0neGemv {
     int f64acc;  // 1: products added in f64 (the oracle's sums), 0: f32 FMA
 };
 
+// Kernel-time measurement. While x0ne_timer is set (this thread only), x0ne_launch records
+// `start` at the start of the first kernel it launches and `stop` at the end of each one
+// (hipExtLaunchKernel's events carry the kernel's own begin and end), so the pair brackets the
+// kernels of one operation and not the gaps before it.
+struct X0neTimer {
+    hipEvent_t start;
+    hipEvent_t stop;
+    bool started;
+};
+extern thread_local X0neTimer* x0ne_timer;
+// Every kernel of the decode step is launched through this.
+hipError_t x0ne_launch(const void* fn, dim3 grid, dim3 block, void** args, size_t lds, hipStream_t s);
+
 hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s);
-uint32_t x0ne_gemv_rows_per_step(uint32_t cols);
-uint32_t x0ne_gemv_waves_per_block();
+// Blocks for a launch of this shape, prologue, epilogue and accumulation on `cus` CUs (0 for a
+// shape the kernel refuses); max_blocks_per_cu 0 means the kernel's occupancy.
+uint32_t x0ne_gemv_grid(const X0neGemv& g, uint32_t cus, uint32_t max_blocks_per_cu);
 
 // Device weight initialisers (init.hip): n values of N(0, std) bf16 from stream `key`
 // starting at value `first` (even), and a constant fill.

@@ -197,6 +197,20 @@ extern "C" x0ne_status x0ne_check_args(const char* name, const x0ne_arg* args, s
 
 namespace x0ne {
 
+}  // namespace x0ne
+
+thread_local X0neTimer* x0ne_timer = nullptr;
+
+hipError_t x0ne_launch(const void* fn, dim3 grid, dim3 block, void** args, size_t lds, hipStream_t s) {
+    X0neTimer* t = x0ne_timer;
+    if (!t) return hipLaunchKernel(fn, grid, block, args, lds, s);
+    hipEvent_t start = t->started ? nullptr : t->start;
+    t->started = true;
+    return hipExtLaunchKernel(fn, grid, block, args, lds, s, start, t->stop, 0);
+}
+
+namespace x0ne {
+
 x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32_t gy, uint32_t block,
                            const x0ne_arg* args, size_t n) {
     X0NE_TRY(check_args_of(k, args, n));
@@ -250,11 +264,7 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
             a.cols = (uint32_t)cols;
             a.prologue = 0;
             a.epilogue = out_f32 ? 1 : 0;
-            const uint32_t rps = x0ne_gemv_rows_per_step((uint32_t)cols);
-            const uint64_t groups = (rows + rps - 1) / rps;
-            const uint64_t blocks = (groups + x0ne_gemv_waves_per_block() - 1) / x0ne_gemv_waves_per_block();
-            const uint64_t cap = (uint64_t)g->cus * 4;
-            a.grid = (uint32_t)(blocks < cap ? blocks : cap);
+            a.grid = x0ne_gemv_grid(a, g->cus, 0);
             g->counts.launches++;
             X0NE_HIP(x0ne_launch_gemv(a, g->stream), "gemv");
         } else {
@@ -345,20 +355,21 @@ x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_b
         void* args[] = {(void*)&q, (void*)&k, (void*)&v, (void*)&pages, (void*)&state, (void*)&cnt,
                         (void*)&out, (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&p, (void*)&scale};
         g->counts.launches++;
-        X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "split-K attention");
+        X0NE_HIP(x0ne_launch(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "split-K attention");
         if (last_block) return X0NE_OK;
     } else {
         if (last_block) return fail(X0NE_ERR_GPU, "the last-block merge needs a grouped split-K kernel");
         g->counts.launches++;
-        hipLaunchKernelGGL(x0ne_attention_decode_split_bf16, dim3(qh, p), dim3(256), 0, g->stream,
-                           (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, (const uint32_t*)pages,
-                           (float*)state, (bf16_t*)out, (const uint32_t*)pos, qh, kvh, max_ctx, p, scale);
-        X0NE_HIP(hipGetLastError(), "split-K attention");
+        void* args[] = {(void*)&q,   (void*)&k,   (void*)&v,       (void*)&pages, (void*)&state, (void*)&out,
+                        (void*)&pos, (void*)&qh,  (void*)&kvh, (void*)&max_ctx, (void*)&p, (void*)&scale};
+        X0NE_HIP(x0ne_launch((const void*)&x0ne_attention_decode_split_bf16, dim3(qh, p), dim3(256), args, 0,
+                             g->stream),
+                 "split-K attention");
     }
     g->counts.launches++;
-    hipLaunchKernelGGL(x0ne_attention_merge_bf16, dim3(qh), dim3(64), 0, g->stream, (const float*)state,
-                       (bf16_t*)out, (const uint32_t*)pos, max_ctx, p);
-    X0NE_HIP(hipGetLastError(), "split-K merge");
+    void* margs[] = {(void*)&state, (void*)&out, (void*)&pos, (void*)&max_ctx, (void*)&p};
+    X0NE_HIP(x0ne_launch((const void*)&x0ne_attention_merge_bf16, dim3(qh), dim3(64), margs, 0, g->stream),
+             "split-K merge");
     return X0NE_OK;
 }
 
@@ -377,7 +388,7 @@ x0ne_status attention_rope_split(x0ne_gpu* g, const x0ne_split_plan& plan, const
                     (void*)&pos,   (void*)&qh,     (void*)&kvh,    (void*)&max_ctx,  (void*)&p,
                     (void*)&scale, (void*)&eps};
     g->counts.launches++;
-    X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "fused decode attention");
+    X0NE_HIP(x0ne_launch(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "fused decode attention");
     return X0NE_OK;
 }
 
@@ -390,7 +401,7 @@ x0ne_status attention_rope_exact(x0ne_gpu* g, const void* qkv, const void* q_nor
     void* args[] = {(void*)&qkv, (void*)&q_norm, (void*)&k_norm, (void*)&inv_freq, (void*)&k, (void*)&v,
                     (void*)&pages, (void*)&out, (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
     g->counts.launches++;
-    X0NE_HIP(hipLaunchKernel(kern, dim3(kvh, 1), dim3(256), args, 0, g->stream), "exact decode attention");
+    X0NE_HIP(x0ne_launch(kern, dim3(kvh, 1), dim3(256), args, 0, g->stream), "exact decode attention");
     return X0NE_OK;
 }
 

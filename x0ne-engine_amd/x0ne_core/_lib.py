@@ -147,7 +147,7 @@ SIGNATURES = {
     "x0ne_engine_max_ctx": ([P], U64),
     "x0ne_engine_arena": ([P], P),
     "x0ne_engine_page": ([P, U64, C.POINTER(U32)], ST),
-    "x0ne_engine_time_kernel": ([P, U32, U32, C.POINTER(F64), C.POINTER(U64)], ST),
+    "x0ne_engine_time_kernel": ([P, U32, U32, C.POINTER(F64), C.POINTER(F64), C.POINTER(U64)], ST),
 }
 
 

@@ -189,12 +189,13 @@ class Engine:
     KERNELS = {"qkv": 0, "attention": 1, "o": 2, "gate_up": 3, "down": 4, "head": 5}
 
     def time_kernel(self, which: str, iters: int):
-        """One decode-step kernel alone, `iters` rounds over every layer, HIP events on the
-        engine's stream: (average microseconds per launch, launches timed)."""
-        avg, n = C.c_double(), C.c_uint64()
-        check(lib().x0ne_engine_time_kernel(self.h, self.KERNELS[which], iters, C.byref(avg), C.byref(n)),
-              "time_kernel")
-        return avg.value, n.value
+        """One decode-step kernel alone, `iters` rounds over every layer, launched back to back on
+        the engine's stream: (average kernel duration in microseconds from the start/stop events
+        hipExtLaunchKernel records, average wall time per launch with the gaps, launches)."""
+        kern, wall, n = C.c_double(), C.c_double(), C.c_uint64()
+        check(lib().x0ne_engine_time_kernel(self.h, self.KERNELS[which], iters, C.byref(kern), C.byref(wall),
+                                            C.byref(n)), "time_kernel")
+        return kern.value, wall.value, n.value
 
     def page(self, i: int) -> int:
         out = C.c_uint32()
