@@ -94,6 +94,41 @@ def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, pr
                       f"single_thread_value: 1 step on 1 thread"}
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qwen3-8b-decode_hbm-bytes.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 byte-counter summary
+    (FETCH_SIZE and WRITE_SIZE runs, scaled by a copy of known size), or None."""
+    import re
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            m = re.search(rf"^traffic_bytes_per_launch {kernel} = (\d+)$", fh.read(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(n: int):
+    """One device-to-device hipMemcpy of n bytes (the runtime's plain copy kernel): a known
+    number of bytes read and written, for scaling the hardware's byte counters."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    src, dst = C.c_void_p(), C.c_void_p()
+    for p in (src, dst):
+        if hip.hipMalloc(C.byref(p), C.c_size_t(n)) != 0:
+            raise SystemExit("calibration copy: hipMalloc failed")
+    try:
+        if hip.hipMemset(src, 1, C.c_size_t(n)) != 0 or hip.hipDeviceSynchronize() != 0:
+            raise SystemExit("calibration copy: hipMemset failed")
+        if hip.hipMemcpy(dst, src, C.c_size_t(n), 3) != 0 or hip.hipDeviceSynchronize() != 0:  # device to device
+            raise SystemExit("calibration copy: hipMemcpy failed")
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+    print(f"[bench] calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,15 +196,7 @@ def main():
           f"others {others}", file=sys.stderr, flush=True)
 
     if args.calibrate_copy:
-        import torch
-        n = args.calibrate_copy << 20
-        src = torch.empty(n, dtype=torch.uint8, device="cuda:0")
-        dst = torch.empty_like(src)
-        src.fill_(1)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        print(f"[bench] calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
+        copy_calibration(args.calibrate_copy << 20)
 
     cpu = None
     if not args.no_cpu:
@@ -203,7 +230,8 @@ def main():
                        "ceiling_tok_s": round(roofline.ceiling_tok_s(shape, mean_ctx), 2)},
         "roofline": {"kernel": "gate_up GEMV (add+RMSNorm prologue, SwiGLU epilogue)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(achieved / 8000.0, 4), "traffic": None, "bytes_per_launch": gu_bytes,
+                     "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic("gate_up"),
+                     "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT), "bytes_per_launch": gu_bytes,
                      "avg_us": round(avg_us, 3), "wall_us_per_launch": round(wall_us, 3),
                      "launches_timed": launches, "timing": "hipExtLaunchKernel start/stop events per launch",
                      "other_kernels": others},
