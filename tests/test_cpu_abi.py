@@ -1,0 +1,129 @@
+"""The C-ABI library without a GPU: it loads, it exports every function include/x0ne_core.h
+declares (and the Python mirror binds each with the header's arity), the kernel table matches the
+kernel declarations of kernels.h parameter for parameter, and every call that needs a device says
+so with X0NE_ERR_GPU instead of failing another way (the drop-in boundary, a line each of
+x0ne-core/runtime/src/{gpu.rs, arena.rs, engine.rs} re-exported in C)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from common import ROOT
+
+HEADER = os.path.join(ROOT, "include", "x0ne_core.h")
+KERNELS_H = os.path.join(ROOT, "x0ne-engine_amd", "csrc", "kernels.h")
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^[A-Za-z_][A-Za-z_0-9 \*]*?\b(x0ne_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, re.M | re.S):
+        args = m.group(2).strip()
+        n = 0 if args in ("", "void") else args.count(",") + 1
+        decls[m.group(1)] = n
+    return decls
+
+
+def test_the_header_declares_the_boundary_the_reference_binds():
+    decls = header_functions()
+    # The entry points a Rust wrapper of x0ne-core/runtime needs (engine.rs, gpu.rs, arena.rs).
+    for name in ["x0ne_engine_load_from", "x0ne_engine_session", "x0ne_session_logits", "x0ne_session_step",
+                 "x0ne_session_finish", "x0ne_session_into_greedy", "x0ne_greedy_next", "x0ne_greedy_finish",
+                 "x0ne_engine_greedy_timed", "x0ne_engine_describe", "x0ne_engine_free", "x0ne_arena_new",
+                 "x0ne_arena_alloc", "x0ne_arena_freeze", "x0ne_arena_write", "x0ne_arena_read", "x0ne_arena_addr",
+                 "x0ne_arena_scrub", "x0ne_gpu_launch", "x0ne_gpu_gemv", "x0ne_gpu_capture_begin",
+                 "x0ne_gpu_capture_end", "x0ne_gpu_launch_graph", "x0ne_gpu_split_plan", "x0ne_last_error"]:
+        assert name in decls, name
+    assert len(decls) >= 60
+
+
+def test_the_library_exports_every_declared_function():
+    from x0ne_core._lib import lib
+    L = lib()
+    missing = [n for n in header_functions() if not hasattr(L, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_the_python_mirror_binds_every_function_with_the_headers_arity():
+    from x0ne_core._lib import SIGNATURES
+    decls = header_functions()
+    for name, n in decls.items():
+        assert name in SIGNATURES, f"{name} has no binding"
+        assert len(SIGNATURES[name][0]) == n, f"{name}: {len(SIGNATURES[name][0])} arguments bound, header has {n}"
+
+
+def kernel_declarations():
+    """Parameter kinds of each kernel in kernels.h, with the group macro expanded."""
+    text = open(KERNELS_H).read()
+    kinds = {}
+
+    def kind(p):
+        p = p.strip()
+        if "*" in p:
+            return "p"
+        if p.startswith("float"):
+            return "f"
+        if p.startswith("uint32_t"):
+            return "u"
+        raise AssertionError(f"parameter {p!r}")
+
+    macro = re.search(r"#define X0NE_DECLARE_SPLIT_GROUP\(G\)(.*?)\n(?!.*\\\n)X0NE_DECLARE", text, re.S)
+    body = macro.group(1).replace("\\\n", "\n")
+    groups = re.findall(r"^X0NE_DECLARE_SPLIT_GROUP\((\d+)\)", text, re.M)
+    expanded = "\n".join(body.replace("##G##", g) for g in groups)
+    plain = text.replace(macro.group(0), "X0NE_DECLARE")
+    for src in (plain, expanded):
+        for m in re.finditer(r"__global__ void (x0ne_\w+)\s*\(([^)]*)\)", src, re.S):
+            kinds[m.group(1)] = "".join(kind(p) for p in m.group(2).split(","))
+    return kinds
+
+
+def test_the_kernel_table_is_the_kernel_declarations():
+    from x0ne_core import gpu
+    decl = kernel_declarations()
+    names = gpu.kernel_names()
+    assert sorted(names) == sorted(decl), "the table lists exactly the declared kernels"
+    for n in names:
+        got = "".join({0: "p", 1: "u", 2: "f"}[int(p)] for p in gpu.params_of(n))
+        assert got == decl[n], f"{n}: table {got}, declaration {decl[n]}"
+
+
+def test_a_launch_is_checked_against_the_table_before_any_device():
+    from x0ne_core import gpu
+    from x0ne_core.gpu import Arg
+    with pytest.raises(Exception):
+        gpu.check_args("x0ne_advance_u32", [Arg.u32(1)])  # a pointer is expected
+    with pytest.raises(Exception):
+        gpu.check_args("x0ne_advance_u32", [])
+    with pytest.raises(Exception):
+        gpu.check_args("no_such_kernel", [])
+    gpu.check_args("x0ne_advance_u32", [Arg.ptr(0)])
+
+
+def test_without_a_gpu_device_calls_fail_with_the_gpu_error():
+    from x0ne_core import Engine, EngineOptions, GpuError
+    from x0ne_core.gpu import Gpu
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(GpuError):
+        Gpu()
+    cfg = {"model_type": "qwen3", "dtype": "bfloat16", "hidden_act": "silu", "attention_bias": False,
+           "hidden_size": 64, "intermediate_size": 96, "num_hidden_layers": 1, "num_attention_heads": 2,
+           "num_key_value_heads": 1, "head_dim": 128, "vocab_size": 100, "max_position_embeddings": 256,
+           "rms_norm_eps": 1e-6, "rope_theta": 1e6, "tie_word_embeddings": True}
+    with pytest.raises(GpuError):
+        Engine.load_synthetic(cfg, 0, 0.02, EngineOptions(max_ctx=64))
+
+
+def test_the_error_codes_are_the_references_variants():
+    from x0ne_core import _lib
+    L = _lib.lib()
+    # x0ne_status values are fixed by the header: OK 0, IO 1, FORMAT 2, ARENA 3, NOT_IMPLEMENTED 4, GPU 5.
+    text = open(HEADER).read()
+    for name, v in [("X0NE_OK", 0), ("X0NE_ERR_IO", 1), ("X0NE_ERR_FORMAT", 2), ("X0NE_ERR_ARENA", 3),
+                    ("X0NE_ERR_NOT_IMPLEMENTED", 4), ("X0NE_ERR_GPU", 5)]:
+        assert re.search(rf"\b{name}\s*=\s*{v}\b", text), name
+    buf = C.create_string_buffer(256)
+    L.x0ne_last_error(buf, 256)  # callable without a device

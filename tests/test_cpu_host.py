@@ -1,0 +1,52 @@
+"""Host-side logic without a GPU: the roofline formula against the reference's published ceiling,
+the bench's workload generator against the oracle's, and the host metrics against the oracle's."""
+import sys
+
+import numpy as np
+
+from common import O, ROOT
+
+
+def test_the_roofline_reproduces_the_references_h100_ceiling_and_the_mi355x_targets():
+    """roofline.rs:55-102; the published 221.13 tok/s H100 ceiling of Qwen3-8B at prompt 20 and
+    256 generated (3,352 GB/s), and the 8 TB/s targets of the decode configs."""
+    from x0ne_core import roofline
+    from bench import QWEN3_8B
+    s = roofline.Shape.of(QWEN3_8B)
+    # 2 [36 (4096 * 6144 + 4096 * 4096 + 3 * 4096 * 12288 + 2 * 4096 + 2 * 128) + 4096 + 151936 * 4096 + 4096]
+    assert roofline.weight_bytes_per_token(s) == 2 * (36 * 192946432 + 622338048) == 15136819200
+    assert roofline.kv_bytes_per_position(s) == 147456
+    ctx = roofline.mean_decode_ctx(20, 256)
+    assert abs(roofline.ceiling_tok_s(s, ctx, bandwidth_gbs=3352.0) - 221.13) < 0.01
+    assert abs(roofline.ceiling_tok_s(s, ctx) - 527.8) < 0.05
+    assert abs(roofline.ceiling_tok_s(s, roofline.mean_decode_ctx(8192, 512)) - 488.3) < 0.05
+    assert abs(roofline.ceiling_tok_s(s, roofline.mean_decode_ctx(8192, 512), batch=8) - 2549.5) < 0.1
+    s32 = roofline.Shape(5120, 25600, 64, 64, 8, 128, 151936)
+    assert abs(roofline.ceiling_tok_s(s32, roofline.mean_decode_ctx(512, 256)) - 124.7) < 0.05
+
+
+def test_the_bench_prompt_is_the_oracles_splitmix_stream():
+    import bench
+    assert (bench.splitmix_ids(20, 151936, 0) == O.synthetic_ids(20, 151936, 0)).all()
+    # The reference's known answer (bench_tests.rs:1072-1081).
+    assert bench.splitmix_ids(6, 151936, 0x0C0E5EED).tolist() == [126819, 135692, 59481, 30850, 145817, 72711]
+
+
+def test_the_bench_refuses_more_than_one_gpu():
+    import subprocess
+    r = subprocess.run([sys.executable, f"{ROOT}/bench.py", "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode != 0 and "one GPU" in r.stderr
+
+
+def test_host_metrics_are_the_oracles():
+    from x0ne_core import metrics
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        p = rng.normal(0, 3, 1000).astype(np.float32)
+        q = (p + rng.normal(0, 0.1, 1000)).astype(np.float32)
+        assert metrics.argmax(p) == O.argmax(p)
+        assert abs(metrics.logsumexp(p) - O.logsumexp(p)) < 1e-12 * abs(O.logsumexp(p))
+        assert abs(metrics.kl(p, q) - O.kl(p, q)) < 1e-12
+    assert metrics.argmax([1.0, float("nan")]) is None and O.argmax([1.0, float("nan")]) is None
+    assert metrics.argmax([2.0, 2.0]) == 0

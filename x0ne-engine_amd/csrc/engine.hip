@@ -772,12 +772,21 @@ extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_f
     Cfg c;
     X0NE_TRY(parse_config(config_json, &c));
     X0NE_TRY(check_config(c, opts->max_ctx));
-    // Every format check before the device is touched.
+    // Every format check before the device is touched. The files and the index agree exactly
+    // (st.rs:216-277): without an index, one file; with one, every file it names given once,
+    // no other file, each listed tensor in the shard it names, and every tensor listed.
+    if (n_files == 0) return fail(X0NE_ERR_FORMAT, "no checkpoint file");
+    if (!index_json && n_files != 1)
+        return fail(X0NE_ERR_FORMAT, std::to_string(n_files) + " files without an index");
     std::map<std::string, TensorView> tensors;
     std::map<std::string, std::string> file_of;
+    std::map<std::string, size_t> seen_files;
     for (size_t i = 0; i < n_files; ++i) {
         std::map<std::string, TensorView> one;
         const std::string fname = names && names[i] ? names[i] : ("file" + std::to_string(i));
+        if (seen_files.count(fname)) return fail(X0NE_ERR_FORMAT, fname + ": given twice");
+        seen_files[fname] = i;
+        if (!data || (!data[i] && lens[i] != 0)) return fail(X0NE_ERR_FORMAT, fname + ": no bytes");
         X0NE_TRY(parse_safetensors(fname, data[i], lens[i], &one));
         for (auto& kv : one) {
             if (tensors.count(kv.first)) return fail(X0NE_ERR_FORMAT, kv.first + ": in two files");
@@ -792,14 +801,23 @@ extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_f
         } catch (const std::exception& ex) {
             return fail(X0NE_ERR_FORMAT, std::string("index: ") + ex.what());
         }
+        if (idx.kind != Json::Object) return fail(X0NE_ERR_FORMAT, "index: not an object");
         const Json* wm = idx.get("weight_map");
         if (!wm || wm->kind != Json::Object) return fail(X0NE_ERR_FORMAT, "index: no weight_map");
+        std::map<std::string, int> named;
         for (const auto& f : wm->fields) {
             if (f.second.kind != Json::String) return fail(X0NE_ERR_FORMAT, "index: " + f.first + ": file is not a string");
+            named[f.second.text] = 1;
             auto it = file_of.find(f.first);
             if (it == file_of.end() || it->second != f.second.text)
                 return fail(X0NE_ERR_FORMAT, f.first + ": not in " + f.second.text);
         }
+        for (const auto& kv : file_of)
+            if (!wm->get(kv.first)) return fail(X0NE_ERR_FORMAT, kv.first + ": in " + kv.second + " but not in the index");
+        for (const auto& f : seen_files)
+            if (!named.count(f.first)) return fail(X0NE_ERR_FORMAT, f.first + ": a file the index does not name");
+        for (const auto& f : named)
+            if (!seen_files.count(f.first)) return fail(X0NE_ERR_FORMAT, f.first + ": named by the index, not given");
     }
     X0NE_TRY(check_tensors(c, tensors));
     x0ne_engine* e = nullptr;

@@ -532,7 +532,8 @@ extern "C" x0ne_status x0ne_arena_freeze(x0ne_arena* a, x0ne_gpu* g) {
         a->gpu = g;
     } else {
         if (len > (uint64_t)SIZE_MAX) return fail(X0NE_ERR_ARENA, "size exceeds host usize");
-        a->base = (uint8_t*)std::malloc(len);
+        void* p = nullptr;  // aligned like a device allocation, so a slice's address is aligned too
+        a->base = posix_memalign(&p, X0NE_ARENA_ALIGN, (size_t)len) == 0 ? (uint8_t*)p : nullptr;
         if (!a->base) return fail(X0NE_ERR_ARENA, "host allocation of " + std::to_string(len) + " bytes");
         std::memset(a->base, 0xA5, len);
     }
