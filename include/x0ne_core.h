@@ -4,8 +4,8 @@
  * This is the drop-in boundary for the reference's x0ne-core runtime crate
  * (x0ne-core/runtime/src/, Rust): every entry point below names the Rust item it replaces,
  * file:line in the reference. Plain pointers and sizes only. A Rust FFI crate binds these
- * functions one to one (see INTEGRATION.md for the extern block and the safe wrappers that give
- * back the reference's Engine / Session / Greedy / Gpu / Arena types).
+ * functions one to one, and safe wrappers over them give back the reference's Engine / Session /
+ * Greedy / Gpu / Arena types.
  *
  * Conventions:
  *  - Every call returns an x0ne_status; X0NE_OK is 0. The other codes are the variants of the
