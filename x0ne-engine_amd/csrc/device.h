@@ -56,6 +56,27 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // Sum over a block of `blockDim.x` threads (a multiple of 64, at most 1024); every thread gets
 // it. `sh` holds 16 doubles. Wave sums, then the wave sums in wave order.
+// A barrier for data exchanged through LDS only: this wavefront's LDS operations are complete,
+// then all wavefronts meet. Unlike __syncthreads() it does not wait for outstanding global loads
+// (the workgroup fence does), so loads requested before it stay in flight across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Sum over a block of WAVES wavefronts in f64, exchanged through LDS `sh` (one double per
+// wavefront) with LDS-only barriers. The block size is a compile-time constant: reading
+// blockDim is a memory load, and waiting for it would wait for every load issued before.
+template <int WAVES>
+__device__ __forceinline__ double block_sum_lds(double v, double* sh) {
+    v = wave_sum_d(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    lds_barrier();
+    if (lane == 0) sh[wave] = v;
+    lds_barrier();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) t += sh[w];
+    return t;
+}
+
 __device__ __forceinline__ double block_sum_d(double v, double* sh) {
     v = wave_sum_d(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;

@@ -138,8 +138,11 @@ x0ne_status check_config(const Cfg& c, uint64_t max_ctx) {
     const uint64_t pages = (max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
     for (uint64_t s : {c.vocab, c.hidden, 2 * c.inter, c.qkv_rows(), max_ctx * c.kv_dim(), pages * X0NE_PAGE_C * c.kv_dim()})
         if (s > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "a dimension exceeds u32");
-    for (uint64_t cols : {c.hidden, c.q_dim(), c.inter})
-        if (cols > 16 * 256 * 8) return fail(X0NE_ERR_FORMAT, "a GEMV width exceeds 32768 columns");
+    // GEMV widths: x is staged whole in LDS; a normed x (hidden) is at most 16384, an
+    // attention output or activation (q_dim, intermediate) at most 32768.
+    if (c.hidden > 16384) return fail(X0NE_ERR_FORMAT, "hidden_size exceeds 16384");
+    for (uint64_t cols : {c.q_dim(), c.inter})
+        if (cols > 32768) return fail(X0NE_ERR_FORMAT, "a GEMV width exceeds 32768 columns");
     return X0NE_OK;
 }
 

@@ -63,85 +63,119 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 
 __device__ __forceinline__ uint32_t pack2(bf16_t lo, bf16_t hi) { return (uint32_t)lo | ((uint32_t)hi << 16); }
 
-// Stages x (bf16) in LDS: the given x, or bf16(rmsnorm(residual + delta) * w_norm). Block-wide;
-// ends with a barrier. The residual sums of a thread's first KEEP chunks stay in registers between
-// the two passes (hidden sizes up to 256 x 8 x KEEP need no second read); later chunks are read
-// again and recomputed (the same f32 additions, the same bits).
-template <int PRO>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, uint4* xl, double* sh) {
-    constexpr uint32_t KEEP = 2;
-    const uint32_t t = threadIdx.x, C = a.cols / 8;
+// ---- branch-free loads ----
+// A raw buffer resource over `bytes` bytes at `base` (gfx9 word 3: 32-bit data format). A load
+// whose 16 bytes are not all inside gives zeros and touches no memory, so a row past the matrix,
+// a chunk past the row or a prefetch past the last tile needs no branch: every load of the
+// pipeline is an instruction the compiler can count, and its waits cover only what is needed.
+constexpr int RSRC_WORD3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, RSRC_WORD3);
+}
+
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+
+// The prologue's inputs, XC 16-byte chunks per thread (chunk t + 256 i): requested first, used
+// after the first weight tiles are in flight.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 load16f(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+template <int PRO, int XC>
+struct XIn {
+    uint4 d[XC];                // x (PRO_X) or delta / the embedding row (norm prologues)
+    f32x4 r0[XC], r1[XC];       // the f32 residual (PRO_NORM)
+    uint4 w[XC];                // the norm weight (norm prologues)
+};
+
+template <int PRO, int XC>
+__device__ __forceinline__ void x_request(const GemvArgs& a, XIn<PRO, XC>& in) {
+    const uint32_t t = threadIdx.x;
     if (PRO == PRO_X) {
-        for (uint32_t c = t; c < C; c += BLOCK) xl[c] = *reinterpret_cast<const uint4*>(a.x + 8 * (size_t)c);
-        __syncthreads();
+        const auto xr = rsrc(a.x, a.cols * 2);
+#pragma unroll
+        for (int i = 0; i < XC; ++i) in.d[i] = load16(xr, (t + BLOCK * i) * 16);
         return;
     }
-    const bf16_t* drow = a.delta;
-    bool zero_row = false;
+    __amdgpu_buffer_rsrc_t dr;
     if (PRO == PRO_EMBED_NORM) {
         const uint32_t tok = a.tokens[0];
-        zero_row = tok >= a.vocab;
-        drow = a.embed + (size_t)(zero_row ? 0 : tok) * a.cols;
+        // A token past the table gives a zero row (embedding.cu:5-17).
+        dr = rsrc(a.embed + (size_t)(tok < a.vocab ? tok : 0) * a.cols, tok < a.vocab ? a.cols * 2 : 0);
+    } else {
+        dr = rsrc(a.delta, a.cols * 2);
     }
-    auto residual = [&](uint32_t c, float* r) {
-        uint4 u = *reinterpret_cast<const uint4*>(drow + 8 * (size_t)c);
-        if (zero_row) u = make_uint4(0, 0, 0, 0);
+    const auto nr = rsrc(a.norm_w, a.cols * 2);
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const uint32_t c = t + BLOCK * i;
+        in.d[i] = load16(dr, c * 16);
+        in.w[i] = load16(nr, c * 16);
+        if (PRO == PRO_NORM) {
+            const auto rr = rsrc(a.res_in, a.cols * 4);
+            in.r0[i] = load16f(rr, c * 32);
+            in.r1[i] = load16f(rr, c * 32 + 16);
+        }
+    }
+}
+
+// Stages x (bf16) in LDS from the requested inputs: the given x, or bf16(rmsnorm(residual +
+// delta) * w_norm) with the residual add in f32 and the norm in f64; block 0 writes the new
+// residual. Block-wide; ends with a barrier.
+template <int PRO, int XC>
+__device__ __forceinline__ void x_stage(const GemvArgs& a, const XIn<PRO, XC>& in, uint4* xl, double* sh) {
+    const uint32_t t = threadIdx.x, C = a.cols / 8;
+    if (PRO == PRO_X) {
+#pragma unroll
+        for (int i = 0; i < XC; ++i)
+            if (t + BLOCK * i < C) xl[t + BLOCK * i] = in.d[i];
+        lds_barrier();
+        return;
+    }
+    float r[XC][8];
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const uint4 u = in.d[i];
         const float d[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y), bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
         if (PRO == PRO_NORM) {
-            const float4 r0 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c);
-            const float4 r1 = *reinterpret_cast<const float4*>(a.res_in + 8 * (size_t)c + 4);
-            r[0] = r0.x + d[0]; r[1] = r0.y + d[1]; r[2] = r0.z + d[2]; r[3] = r0.w + d[3];
-            r[4] = r1.x + d[4]; r[5] = r1.y + d[5]; r[6] = r1.z + d[6]; r[7] = r1.w + d[7];
-        } else {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) r[k] = 0.f + d[k];
-        }
-    };
-    // Pass 1: r = residual + delta (f32), block 0 writes it out, squares summed in f64.
-    float keep[KEEP][8];
-    double ss = 0.0;
-    uint32_t it = 0;
-    for (uint32_t c = t; c < C; c += BLOCK, ++it) {
-        float r[8];
-        residual(c, r);
-        if (blockIdx.x == 0 && a.res_out != nullptr) {
-            float4* o = reinterpret_cast<float4*>(a.res_out + 8 * (size_t)c);
-            o[0] = make_float4(r[0], r[1], r[2], r[3]);
-            o[1] = make_float4(r[4], r[5], r[6], r[7]);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ss += (double)r[k] * (double)r[k];
-#pragma unroll
-        for (uint32_t q = 0; q < KEEP; ++q)
-            if (it == q) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) keep[q][k] = r[k];
+            for (int k = 0; k < 4; ++k) {
+                r[i][k] = in.r0[i][k] + d[k];
+                r[i][k + 4] = in.r1[i][k] + d[k + 4];
             }
-    }
-    const double total = block_sum_d(ss, sh);
-    const double scale = 1.0 / sqrt(total / (double)a.cols + (double)a.eps);
-    // Pass 2: x = bf16(r * scale * w) in f64.
-    it = 0;
-    for (uint32_t c = t; c < C; c += BLOCK, ++it) {
-        float r[8];
-        if (it < KEEP) {
-#pragma unroll
-            for (uint32_t q = 0; q < KEEP; ++q)
-                if (it == q) {
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) r[k] = keep[q][k];
-                }
         } else {
-            residual(c, r);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) r[i][k] = 0.f + d[k];
         }
-        const uint4 wn = *reinterpret_cast<const uint4*>(a.norm_w + 8 * (size_t)c);
+        const uint32_t c = t + BLOCK * i;
+        if (blockIdx.x == 0 && a.res_out != nullptr && c < C) {
+            float4* o = reinterpret_cast<float4*>(a.res_out + 8 * (size_t)c);
+            o[0] = make_float4(r[i][0], r[i][1], r[i][2], r[i][3]);
+            o[1] = make_float4(r[i][4], r[i][5], r[i][6], r[i][7]);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss += (double)r[i][k] * (double)r[i][k];  // chunks past C are 0
+    }
+    const double total = block_sum_lds<WAVES>(ss, sh);
+    const double scale = 1.0 / sqrt(total / (double)a.cols + (double)a.eps);
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const uint32_t c = t + BLOCK * i;
+        const uint4 wn = in.w[i];
         const float w[8] = {bf_lo(wn.x), bf_hi(wn.x), bf_lo(wn.y), bf_hi(wn.y), bf_lo(wn.z), bf_hi(wn.z), bf_lo(wn.w), bf_hi(wn.w)};
         bf16_t o[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o[k] = f2bf((float)((double)r[k] * scale * (double)w[k]));
-        xl[c] = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+        for (int k = 0; k < 8; ++k) o[k] = f2bf((float)((double)r[i][k] * scale * (double)w[k]));
+        if (c < C) xl[c] = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 template <class A>
@@ -227,30 +261,61 @@ __device__ __forceinline__ uint32_t reduced_row(uint32_t lane) {
 // A wavefront's work is a sequence of tiles: row group g (R rows; for EPI_SWIGLU R / 2 gate rows
 // i.. and the up rows inter + i..) times batch b (chunks 64 BATCH b + lane + 64 j, j < BATCH, of
 // each row). Tiles are double-buffered in registers: while one is summed the next is in flight,
-// and the first two are requested before the prologue, so the weights' latency overlaps the
-// staging of x. A group's sums are reduced over the wavefront after its last batch.
+// and the first is requested right after the prologue's inputs, so waiting for x leaves it in
+// flight (the prologue's barriers wait for LDS only). Every load is unconditional (buffer resources bound rows and chunks), so
+// the compiler's waits before a tile cover that tile only. A group's sums are reduced over the
+// wavefront after its last batch.
 struct TilePos {
     uint32_t g, b;
 };
 
-template <int R, int BATCH, int PRO, int EPI, class Acc>
+// Work mapping (MAP bits). MAP_CONTIGUOUS: wavefront w takes row groups [w per, w per + per)
+// instead of w, w + W, ... MAP_XCD: launch ids alternate between the 8 XCDs (each with its own
+// L2), so block id (b % 8) (grid / 8) + b / 8 gives each XCD a contiguous range of blocks (the
+// grid is then a multiple of 8).
+constexpr int MAP_CONTIGUOUS = 1;
+constexpr int MAP_XCD = 2;
+// MAP_SPREAD: batch b of a row takes chunks lane + 64 (b + NB j), spread over the whole row,
+// instead of a contiguous run. MAP_STAGGER: wavefront w starts each row group at batch w % NB,
+// so wavefronts in step do not all read the same part of their rows.
+constexpr int MAP_SPREAD = 4;
+constexpr int MAP_STAGGER = 8;
+
+template <int R, int BATCH, int PRO, int EPI, class Acc, int XC, int MAP>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
     __shared__ double sh[16];
     __shared__ float best_v[WAVES];
     __shared__ uint32_t best_i[WAVES];
     __shared__ int any_nan;
     __shared__ uint32_t last;
-    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t t = threadIdx.x, lane = t & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: row resources in SGPRs
     const uint32_t C = a.cols / 8;
     const uint32_t NB = (C + 64 * BATCH - 1) / (64 * BATCH);  // batches per row group
     constexpr int PAIRS = R / 2;
     const uint32_t inter = a.rows / 2;
     const uint32_t groups = EPI == EPI_SWIGLU ? (inter + PAIRS - 1) / PAIRS : (a.rows + R - 1) / R;
-    const uint32_t gw = blockIdx.x * WAVES + wave, nw = gridDim.x * WAVES;
-    const uint32_t my_groups = gw < groups ? (groups - gw + nw - 1) / nw : 0;
+    const uint32_t bid = (MAP & MAP_XCD) ? (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const uint32_t gw = bid * WAVES + wave, nw = gridDim.x * WAVES;
+    uint32_t g0, gstep, my_groups;
+    if (MAP & MAP_CONTIGUOUS) {
+        const uint32_t per = (groups + nw - 1) / nw;
+        g0 = gw * per;
+        gstep = 1;
+        my_groups = g0 < groups ? min(per, groups - g0) : 0;
+    } else {
+        g0 = gw;
+        gstep = nw;
+        my_groups = gw < groups ? (groups - gw + nw - 1) / nw : 0;
+    }
     const uint32_t T = my_groups * NB;  // wavefront-uniform
     if (EPI == EPI_ARGMAX && t == 0) any_nan = 0;
 
+    // Chunk j of batch b.
+    auto chunk = [&](uint32_t b, int j) -> uint32_t {
+        return (MAP & MAP_SPREAD) ? lane + 64 * (b + NB * j) : lane + 64 * (BATCH * b + j);
+    };
+    const uint32_t b0 = (MAP & MAP_STAGGER) ? gw % NB : 0;  // first batch of each row group
     auto row_of = [&](uint32_t g, int r, bool& in) -> uint32_t {
         if (EPI == EPI_SWIGLU) {
             const uint32_t i = g * PAIRS + (r % PAIRS);
@@ -261,38 +326,36 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
         in = row < a.rows;
         return row;
     };
-    auto load = [&](uint4 (&w)[R][BATCH], TilePos p) {
+    // live = false: a prefetch past the wavefront's last tile (reads nothing).
+    auto load = [&](uint4 (&w)[R][BATCH], TilePos p, bool live) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             bool in;
             const uint32_t row = row_of(p.g, r, in);
-            const bf16_t* wr = a.w + (size_t)row * a.cols;
+            const auto rs = rsrc(a.w + (size_t)(in && live ? row : 0) * a.cols, in && live ? a.cols * 2 : 0);
 #pragma unroll
-            for (int j = 0; j < BATCH; ++j) {
-                const uint32_t c = lane + 64 * (BATCH * p.b + j);
-                w[r][j] = (in && c < C) ? *reinterpret_cast<const uint4*>(wr + 8 * (size_t)c) : make_uint4(0, 0, 0, 0);
-            }
+            for (int j = 0; j < BATCH; ++j) w[r][j] = load16(rs, chunk(p.b, j) * 16);
         }
     };
+    // Batches of a group run b0, b0 + 1, ..., NB - 1, 0, ..., b0 - 1; the group ends at its last.
     auto advance = [&](TilePos& p) {
-        if (++p.b == NB) {
-            p.b = 0;
-            p.g += nw;
-        }
+        if (++p.b == NB) p.b = 0;
+        if (p.b == b0) p.g += gstep;
     };
 
     uint4 w0[R][BATCH], w1[R][BATCH];
-    TilePos lp = {gw, 0};  // next tile to request
-    if (T > 0) {
-        load(w0, lp);
+    TilePos lp = {g0, b0};  // next tile to request
+    {
+        XIn<PRO, XC> xin;
+        x_request<PRO, XC>(a, xin);
+        __builtin_amdgcn_sched_barrier(0);  // keep the request order: x first, then the weights
+        load(w0, lp, T > 0);
         advance(lp);
+        __builtin_amdgcn_sched_barrier(0);
+        x_stage<PRO, XC>(a, xin, xl, sh);
     }
-    if (T > 1) {
-        load(w1, lp);
-        advance(lp);
-    }
-
-    stage_x<PRO>(a, xl, sh);
+    load(w1, lp, T > 1);
+    advance(lp);
 
     float bv = -INFINITY;
     uint32_t bi = NO_TOKEN;
@@ -304,16 +367,18 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
     auto consume = [&](const uint4 (&w)[R][BATCH], TilePos p) {
 #pragma unroll
         for (int j = 0; j < BATCH; ++j) {
-            const uint32_t c = lane + 64 * (BATCH * p.b + j);
-            if (c < C) {
-                const uint4 u = xl[c];
-                const float x[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y),
-                                    bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
+            const uint32_t c = chunk(p.b, j);
+            const bool ok = c < C;
+            const uint4 u = xl[ok ? c : 0];
+            // A chunk past the row: its weights are zeros, and so is x (0 times a value that is
+            // not finite would not be 0).
+            const float x[8] = {ok ? bf_lo(u.x) : 0.f, ok ? bf_hi(u.x) : 0.f, ok ? bf_lo(u.y) : 0.f,
+                                ok ? bf_hi(u.y) : 0.f, ok ? bf_lo(u.z) : 0.f, ok ? bf_hi(u.z) : 0.f,
+                                ok ? bf_lo(u.w) : 0.f, ok ? bf_hi(u.w) : 0.f};
 #pragma unroll
-                for (int r = 0; r < R; ++r) acc[r] = dot8<Acc>(w[r][j], x, acc[r]);
-            }
+            for (int r = 0; r < R; ++r) acc[r] = dot8<Acc>(w[r][j], x, acc[r]);
         }
-        if (p.b + 1 != NB) return;
+        if ((p.b + 1 == NB ? 0 : p.b + 1) != b0) return;
         // The group's last batch: reduce and write.
         const Acc sum = wave_reduce_rows<R, Acc>(acc);
 #pragma unroll
@@ -345,21 +410,17 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
         }
     };
 
-    TilePos cp = {gw, 0};  // next tile to sum
+    TilePos cp = {g0, b0};  // next tile to sum
     for (uint32_t i = 0; i < T; i += 2) {
         consume(w0, cp);
         advance(cp);
-        if (i + 2 < T) {
-            load(w0, lp);
-            advance(lp);
-        }
+        load(w0, lp, i + 2 < T);
+        advance(lp);
         if (i + 1 >= T) break;
         consume(w1, cp);
         advance(cp);
-        if (i + 3 < T) {
-            load(w1, lp);
-            advance(lp);
-        }
+        load(w1, lp, i + 3 < T);
+        advance(lp);
     }
     if (EPI != EPI_ARGMAX) return;
 
@@ -444,10 +505,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
 
 }  // namespace
 
-template <int R, int BATCH, int PRO, int EPI, class Acc>
+template <int R, int BATCH, int PRO, int EPI, class Acc, int XC, int MAP>
 __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
     extern __shared__ uint4 xl[];
-    gemv_body<R, BATCH, PRO, EPI, Acc>(a, xl);
+    gemv_body<R, BATCH, PRO, EPI, Acc, XC, MAP>(a, xl);
 }
 
 // Plain GEMV for the kernel table and tests: y[rows] = W x, bf16 or f32 out, f32 accumulation,
@@ -464,7 +525,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
         a.y = y;                                                                                                  \
         a.rows = rows;                                                                                            \
         a.cols = cols;                                                                                            \
-        gemv_body<4, 4, PRO_X, EPI, float>(a, xs);                                                                   \
+        gemv_body<4, 4, PRO_X, EPI, float, 8, 0>(a, xs);                                                             \
     }
 X0NE_GEMV_PLAIN(x0ne_gemv_bf16, EPI_BF16)
 X0NE_GEMV_PLAIN(x0ne_gemv_f32, EPI_F32)
@@ -498,18 +559,54 @@ extern "C" __global__ void __launch_bounds__(256)
 
 namespace {
 
-constexpr int TILE_R = 4;      // rows per row group
-constexpr int TILE_BATCH = 4;  // 16-byte chunks per lane per row in one tile
+// Tile shape and residency per epilogue, measured on MI355X over 36 distinct matrices of each
+// Qwen3-8B projection: narrow tiles (2 rows x 4 chunks) at one block per CU for the plain and
+// normed projections, 4 x 4 tiles at the kernel's occupancy for gate/up (both rows of a SwiGLU
+// pair in one wavefront), and whole-row 4 x 8 tiles at one block per CU for the LM head. More
+// resident wavefronts than that (more rows streamed at once) lowered the achieved bandwidth.
+template <int E>
+struct Tile {
+    static constexpr int R = 2, BATCH = 4, BLOCKS_PER_CU = 1;
+};
+template <>
+struct Tile<EPI_SWIGLU> {
+    static constexpr int R = 4, BATCH = 4, BLOCKS_PER_CU = 0;  // 0: the occupancy
+};
+template <>
+struct Tile<EPI_ARGMAX> {
+    static constexpr int R = 4, BATCH = 8, BLOCKS_PER_CU = 1;
+};
+constexpr int TILE_MAP = 0;  // strided row groups, launch order
 
-template <int P, int E>
-const void* instance(int f64acc) {
-    return f64acc ? (const void*)&gemv_kernel<TILE_R, TILE_BATCH, P, E, double>
-                  : (const void*)&gemv_kernel<TILE_R, TILE_BATCH, P, E, float>;
+// 16-byte chunks of x per thread the prologue requests: the smallest of 2, 4, 8, 16 that covers
+// cols / 8 over 256 threads (the norm prologues keep four registers per chunk and stop at 8).
+int x_chunks(uint32_t cols) {
+    const uint32_t per = (cols / 8 + BLOCK - 1) / BLOCK;
+    return per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
 }
 
-const void* pick(int pro, int epi, int f64acc) {
+template <int P, int E, int XC>
+const void* instance(int f64acc) {
+    constexpr int R = Tile<E>::R, B = Tile<E>::BATCH;
+    return f64acc ? (const void*)&gemv_kernel<R, B, P, E, double, XC, TILE_MAP>
+                  : (const void*)&gemv_kernel<R, B, P, E, float, XC, TILE_MAP>;
+}
+
+template <int P, int E>
+const void* instance_x(int f64acc, int xc) {
+    if (xc == 2) return instance<P, E, 2>(f64acc);
+    if (xc == 4) return instance<P, E, 4>(f64acc);
+    if (xc == 8) return instance<P, E, 8>(f64acc);
+    if constexpr (P == PRO_X) {
+        if (xc == 16) return instance<P, E, 16>(f64acc);
+    }
+    return nullptr;
+}
+
+const void* pick(int pro, int epi, int f64acc, uint32_t cols) {
+    const int xc = x_chunks(cols);
 #define X0NE_CASE(P, E) \
-    if (pro == P && epi == E) return instance<P, E>(f64acc);
+    if (pro == P && epi == E) return instance_x<P, E>(f64acc, xc);
     X0NE_CASE(PRO_X, EPI_BF16)
     X0NE_CASE(PRO_X, EPI_F32)
     X0NE_CASE(PRO_NORM, EPI_BF16)
@@ -521,28 +618,45 @@ const void* pick(int pro, int epi, int f64acc) {
     return nullptr;
 }
 
+// Rows per row group and the default blocks-per-CU cap of an epilogue's tile.
+void tile_of(int epi, uint32_t* rows, uint32_t* blocks_per_cu) {
+    if (epi == EPI_SWIGLU) {
+        *rows = Tile<EPI_SWIGLU>::R;
+        *blocks_per_cu = Tile<EPI_SWIGLU>::BLOCKS_PER_CU;
+    } else if (epi == EPI_ARGMAX) {
+        *rows = Tile<EPI_ARGMAX>::R;
+        *blocks_per_cu = Tile<EPI_ARGMAX>::BLOCKS_PER_CU;
+    } else {
+        *rows = Tile<EPI_BF16>::R;
+        *blocks_per_cu = Tile<EPI_BF16>::BLOCKS_PER_CU;
+    }
+}
+
 bool shape_ok(const X0neGemv& g) {
-    return g.cols != 0 && g.cols % 8 == 0 && g.cols <= 32768 && g.rows != 0 &&
+    return g.cols != 0 && g.cols % 8 == 0 && g.cols <= (g.prologue == PRO_X ? 32768u : 16384u) && g.rows != 0 &&
            (g.epilogue != EPI_SWIGLU || g.rows % 2 == 0);
 }
 
 }  // namespace
 
-// The grid of a launch: as many wavefronts as can be resident at once (the kernel's occupancy
-// on `cus` CUs, capped at `max_blocks_per_cu` blocks per CU when that is not 0), then cut so the
-// row groups divide as evenly as they can: each wavefront takes ceil(groups / waves) of them,
-// and no more wavefronts are launched than that split needs.
+// The grid of a launch: as many wavefronts as the epilogue's tile keeps resident (its
+// blocks-per-CU cap, or the kernel's occupancy; `max_blocks_per_cu`, when not 0, overrides
+// both), then cut so the row groups divide as evenly as they can: each wavefront takes
+// ceil(groups / waves) of them, and no more wavefronts are launched than that split needs.
 uint32_t x0ne_gemv_grid(const X0neGemv& g, uint32_t cus, uint32_t max_blocks_per_cu) {
     if (!shape_ok(g) || cus == 0) return 0;
-    const void* fn = pick(g.prologue, g.epilogue, g.f64acc);
+    const void* fn = pick(g.prologue, g.epilogue, g.f64acc, g.cols);
     if (!fn) return 0;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, BLOCK, (size_t)g.cols * 2) != hipSuccess ||
         per_cu <= 0)
         per_cu = 1;
-    if (max_blocks_per_cu != 0 && (uint32_t)per_cu > max_blocks_per_cu) per_cu = (int)max_blocks_per_cu;
-    const uint64_t groups = g.epilogue == EPI_SWIGLU ? ((uint64_t)g.rows / 2 + TILE_R / 2 - 1) / (TILE_R / 2)
-                                                     : ((uint64_t)g.rows + TILE_R - 1) / TILE_R;
+    uint32_t rows = 0, cap = 0;
+    tile_of(g.epilogue, &rows, &cap);
+    if (max_blocks_per_cu != 0) cap = max_blocks_per_cu;
+    if (cap != 0 && (uint32_t)per_cu > cap) per_cu = (int)cap;
+    const uint64_t groups = g.epilogue == EPI_SWIGLU ? ((uint64_t)g.rows / 2 + rows / 2 - 1) / (rows / 2)
+                                                     : ((uint64_t)g.rows + rows - 1) / rows;
     const uint64_t waves_max = (uint64_t)cus * (uint64_t)per_cu * WAVES;
     const uint64_t per_wave = (groups + waves_max - 1) / waves_max;
     const uint64_t waves = (groups + per_wave - 1) / per_wave;
@@ -551,7 +665,7 @@ uint32_t x0ne_gemv_grid(const X0neGemv& g, uint32_t cus, uint32_t max_blocks_per
 
 hipError_t x0ne_launch_gemv(const X0neGemv& g, hipStream_t s) {
     if (!shape_ok(g) || g.grid == 0) return hipErrorInvalidValue;
-    const void* fn = pick(g.prologue, g.epilogue, g.f64acc);
+    const void* fn = pick(g.prologue, g.epilogue, g.f64acc, g.cols);
     if (!fn) return hipErrorInvalidValue;
     GemvArgs a = {};
     a.w = g.w;
