@@ -85,13 +85,13 @@ __device__ __forceinline__ uint32_t rev4(uint32_t b) {
 
 // One wavefront: the G q heads in qs (G x 128 f32, LDS) over kv head kh, tiles t0, t0 + tstep,
 // ... below ntiles. Leaves per head the running max m, the sum l (whole, every lane) and
-// o = sum exp(s - m) v for dims 8b..8b+7 (summed over the 4 rows of a lane, valid in every
-// lane). lds: this wavefront's 2 * G * 64 values. A wavefront without a tile leaves m = -inf.
+// o = sum exp(s - m) v for dims lane and lane + 64. lds: this wavefront's 2 * G * 64 values. A
+// wavefront without a tile leaves m = -inf.
 template <int G, class T>
 __device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc,
                                             const uint32_t* __restrict__ pages, uint32_t kh, uint32_t kv_heads,
                                             uint32_t ctx, uint32_t t0, uint32_t tstep, T scale, T* lds,
-                                            T m[G], T l[G], T o[G][8]) {
+                                            T m[G], T l[G], T o[G][2]) {
     constexpr int HGMAX = sizeof(T) == 4 ? 4 : 2;  // heads per score pass (registers)
     constexpr int HG = G < HGMAX ? G : HGMAX;
     constexpr int PASSES = G / HG;
@@ -105,8 +105,8 @@ __device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __res
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         lsum[g] = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[g][j] = 0;
+        o[g][0] = 0;
+        o[g][1] = 0;
     }
 
     for (uint32_t t = t0; t < ntiles; t += tstep) {
@@ -126,14 +126,24 @@ __device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __res
             valid[i] = base + 4 * i + r < ctx;
             off[i] = ((pg[i >> 2] * kv_heads + kh) * X0NE_PAGE + 4 * (i & 3) + r) * X0NE_HEAD_DIM + 8 * b;
         }
-        // K and V rows together (the f64 mode loads V after the scores, for registers); rows
-        // past ctx are zero (their weight is 0, and a zero keeps a value that is not a number
-        // out of the sum).
+        // K and V together (the f64 mode loads V after the scores, for registers). K: rows 4i + r,
+        // dims 8b..8b+7. V (dim-major pages): vv[4 pp + 2 dh + kk] holds keys 16 pp + 8 kk ..
+        // + 7 of the tile at dim lane + 64 dh. Rows past ctx are zero (their weight is 0, and a
+        // zero keeps a value that is not a number out of the sum).
         uint4 kv[16], vv[16];
         auto load_v = [&] {
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                vv[i] = valid[i] ? *reinterpret_cast<const uint4*>(vc + off[i]) : make_uint4(0, 0, 0, 0);
+            for (int pp = 0; pp < 4; ++pp) {
+                const bool live = base + X0NE_PAGE * pp < ctx;
+                const bf16_t* vp = vc + (size_t)(pg[pp] * kv_heads + kh) * X0NE_HEAD_DIM * X0NE_PAGE;
+#pragma unroll
+                for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk)
+                        vv[4 * pp + 2 * dh + kk] =
+                            live ? *reinterpret_cast<const uint4*>(vp + (lane + 64 * dh) * X0NE_PAGE + 8 * kk)
+                                 : make_uint4(0, 0, 0, 0);
+            }
         };
 #pragma unroll
         for (int i = 0; i < 16; ++i)
@@ -198,40 +208,35 @@ __device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __res
 
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[g][j] *= alpha[g];
+            o[g][0] *= alpha[g];
+            o[g][1] *= alpha[g];
         }
+        // Keys past ctx inside a live page hold anything: their values are taken as 0.
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const T v0 = bf_lo(vv[i].x), v1 = bf_hi(vv[i].x), v2 = bf_lo(vv[i].y), v3 = bf_hi(vv[i].y);
-            const T v4 = bf_lo(vv[i].z), v5 = bf_hi(vv[i].z), v6 = bf_lo(vv[i].w), v7 = bf_hi(vv[i].w);
+        for (int pp = 0; pp < 4; ++pp)
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const T p = p_lds[g * 64 + 4 * i + r];
-                o[g][0] = acc_fma(p, v0, o[g][0]);
-                o[g][1] = acc_fma(p, v1, o[g][1]);
-                o[g][2] = acc_fma(p, v2, o[g][2]);
-                o[g][3] = acc_fma(p, v3, o[g][3]);
-                o[g][4] = acc_fma(p, v4, o[g][4]);
-                o[g][5] = acc_fma(p, v5, o[g][5]);
-                o[g][6] = acc_fma(p, v6, o[g][6]);
-                o[g][7] = acc_fma(p, v7, o[g][7]);
+            for (int kk = 0; kk < 2; ++kk) {
+                const uint4 w0 = vv[4 * pp + kk], w1 = vv[4 * pp + 2 + kk];
+                const uint32_t u0[4] = {w0.x, w0.y, w0.z, w0.w}, u1[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t key = X0NE_PAGE * pp + 8 * kk + e;
+                    const bool ok = base + key < ctx;
+                    const T v0 = ok ? (T)((e & 1) ? bf_hi(u0[e >> 1]) : bf_lo(u0[e >> 1])) : (T)0;
+                    const T v1 = ok ? (T)((e & 1) ? bf_hi(u1[e >> 1]) : bf_lo(u1[e >> 1])) : (T)0;
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const T p = p_lds[g * 64 + key];
+                        o[g][0] = acc_fma(p, v0, o[g][0]);
+                        o[g][1] = acc_fma(p, v1, o[g][1]);
+                    }
+                }
             }
-        }
         wave_lds_sync();  // the next tile rewrites s_lds and p_lds
     }
-    // Whole sums: l over the 64 keys' lanes, o over the 4 rows of a lane (lanes b, b+16, ...).
+    // Whole sums: l over the 64 keys' lanes (o is whole in each lane already).
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        l[g] = acc_wave_sum(lsum[g]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            T x = o[g][j];
-            x += (T)__shfl_xor(x, 16, 64);
-            x += (T)__shfl_xor(x, 32, 64);
-            o[g][j] = x;
-        }
-    }
+    for (int g = 0; g < G; ++g) l[g] = acc_wave_sum(lsum[g]);
 }
 
 // The shared memory of one block: q of its heads, each wavefront's exchange area, each
@@ -334,7 +339,7 @@ struct AttnArgs {
 
 // A wavefront's state into the block's LDS for the block merge.
 template <int G, class T>
-__device__ __forceinline__ void stash_wave(AttnShared<G, T>& sh, const T m[G], const T l[G], const T o[G][8]) {
+__device__ __forceinline__ void stash_wave(AttnShared<G, T>& sh, const T m[G], const T l[G], const T o[G][2]) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) {
 #pragma unroll
@@ -343,12 +348,10 @@ __device__ __forceinline__ void stash_wave(AttnShared<G, T>& sh, const T m[G], c
             sh.wl[wave][g] = l[g];
         }
     }
-    if (lane < 16) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sh.wo[wave][g][8 * lane + j] = o[g][j];
-        }
+    for (int g = 0; g < G; ++g) {
+        sh.wo[wave][g][lane] = o[g][0];
+        sh.wo[wave][g][lane + 64] = o[g][1];
     }
 }
 
@@ -388,8 +391,9 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
             a.k_cache[at + lane] = f2bf(ra);
             a.k_cache[at + lane + 64] = f2bf(rb);
             const bf16_t* vs = a.qkv + q_dim + kv_dim + kh * X0NE_HEAD_DIM;
-            a.v_cache[at + lane] = vs[lane];
-            a.v_cache[at + lane + 64] = vs[lane + 64];
+            const uint32_t vat = v_slot(a.pages, pos, kh, a.kv_heads);
+            a.v_cache[vat + lane * X0NE_PAGE] = vs[lane];
+            a.v_cache[vat + (lane + 64) * X0NE_PAGE] = vs[lane + 64];
         }
     } else {
         for (uint32_t k = t; k < (uint32_t)G * X0NE_HEAD_DIM; k += BLOCK)
@@ -399,7 +403,7 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
 
     // The exact mode scales by 1/sqrt(128) in f64, as the f64 oracle does.
     const T scale = EXACT ? (T)(1.0 / sqrt((double)X0NE_HEAD_DIM)) : (T)a.scale;
-    T m[G], l[G], o[G][8];
+    T m[G], l[G], o[G][2];
     attend_wave<G, T>(&sh.qs[0][0], a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, BLOCK_TILES * y + wave,
                       BLOCK_TILES * P, scale, sh.xch[wave], m, l, o);
     stash_wave<G, T>(sh, m, l, o);
@@ -445,7 +449,7 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
     const uint32_t t = threadIdx.x, wave = t >> 6;
     if (t < X0NE_HEAD_DIM) sh.qs[0][t] = bf2f(q_row[t]);
     __syncthreads();
-    float m[1], l[1], o[1][8];
+    float m[1], l[1], o[1][2];
     attend_wave<1, float>(&sh.qs[0][0], kc, vc, pages, kh, kv_heads, ctx, BLOCK_TILES * y + wave, BLOCK_TILES * P,
                           scale, sh.xch[wave], m, l, o);
     stash_wave<1, float>(sh, m, l, o);

@@ -89,10 +89,19 @@ __device__ __forceinline__ double block_sum_d(double v, double* sh) {
 }
 
 // ---- KV pages ----
-// A layer's K (or V) plane is [pages][kv_heads][16][128] bf16; page_table maps a sequence's
+// A layer's K plane is [pages][kv_heads][16][128] bf16 (a key row of 128 dims contiguous); its
+// V plane is [pages][kv_heads][128][16] (dim-major within a page: the 16 positions of one dim
+// contiguous, the operand layout of the matrix-core P·V product). page_table maps a sequence's
 // logical page (position / 16) to its physical page.
 __device__ __forceinline__ uint32_t kv_row(const uint32_t* __restrict__ pages, uint32_t pos, uint32_t kh,
                                          uint32_t kv_heads) {
     const uint32_t page = pages[pos / X0NE_PAGE];
     return ((page * kv_heads + kh) * X0NE_PAGE + (pos % X0NE_PAGE)) * X0NE_HEAD_DIM;
+}
+
+// Element (pos, dim 0) of a V plane; dim d is at + d * 16.
+__device__ __forceinline__ uint32_t v_slot(const uint32_t* __restrict__ pages, uint32_t pos, uint32_t kh,
+                                         uint32_t kv_heads) {
+    const uint32_t page = pages[pos / X0NE_PAGE];
+    return (page * kv_heads + kh) * X0NE_HEAD_DIM * X0NE_PAGE + (pos % X0NE_PAGE);
 }

@@ -51,8 +51,9 @@ extern "C" __global__ void __launch_bounds__(256)
 // Per-head RMSNorm of q and k, rotate-half RoPE, and the K/V write into the paged cache
 // (rope.cu:7-47; oracle/src/lib.rs:82-120). grid (q_heads + kv_heads, rows), block 64: lane i
 // owns the pair (i, i + 64) of one head. Row r sits at position pos0[0] + r, written at
-// physical page page_table[pos / 16], slot pos % 16 of the layer's K and V planes
-// ([pages][kv_heads][16][128]). A position >= max_ctx writes nothing into the cache. The angle
+// physical page page_table[pos / 16], slot pos % 16 of the layer's K plane
+// ([pages][kv_heads][16][128]) and V plane ([pages][kv_heads][128][16]). A position >= max_ctx
+// writes nothing into the cache. The angle
 // is the f32 product pos * inv_freq[i] (inv_freq computed on the host in f32), its sine and
 // cosine in f64. Blocks of k heads also copy v, bit for bit.
 extern "C" __global__ void __launch_bounds__(64)
@@ -92,8 +93,9 @@ extern "C" __global__ void __launch_bounds__(64)
     k_cache[at + i] = f2bf(ra);
     k_cache[at + i + HALF] = f2bf(rb);
     const bf16_t* vs = qkv + (size_t)row * qkv_dim + q_dim + kv_dim + kh * HD;
-    v_cache[at + i] = vs[i];
-    v_cache[at + i + HALF] = vs[i + HALF];
+    const uint32_t vat = v_slot(pages, pos, kh, kv_heads);
+    v_cache[vat + i * X0NE_PAGE] = vs[i];
+    v_cache[vat + (i + HALF) * X0NE_PAGE] = vs[i + HALF];
 }
 
 // SwiGLU on the packed [gate; up] row: out[i] = g / (1 + e^-g) * u, in f64 (swiglu.cu:5-11;

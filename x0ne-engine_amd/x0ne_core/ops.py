@@ -78,14 +78,20 @@ def n_pages(ctx: int) -> int:
     return (ctx + PAGE - 1) // PAGE
 
 
-def to_pages(rows: np.ndarray, kv_heads: int, page_of, pool: int, fill=NAN_BF16) -> np.ndarray:
-    """[ctx][kv_heads * 128] bf16 -> [pool][kv_heads][16][128], row p at page page_of[p // 16]."""
+def to_pages(rows: np.ndarray, kv_heads: int, page_of, pool: int, fill=NAN_BF16, dim_major=False) -> np.ndarray:
+    """[ctx][kv_heads * 128] bf16 -> K pages [pool][kv_heads][16][128], or V pages
+    [pool][kv_heads][128][16] when dim_major; row p at page page_of[p // 16], slot p % 16."""
     ctx = rows.shape[0] if rows.ndim == 2 else rows.size // (kv_heads * HEAD_DIM)
     rows = rows.reshape(ctx, kv_heads, HEAD_DIM)
     out = np.full((pool, kv_heads, PAGE, HEAD_DIM), fill, np.uint16)
     for p in range(ctx):
         out[page_of[p // PAGE], :, p % PAGE, :] = rows[p]
-    return out
+    return np.ascontiguousarray(out.transpose(0, 1, 3, 2)) if dim_major else out
+
+
+def v_offset(page: int, kv_heads: int, kh: int, slot: int, dim: int) -> int:
+    """Element index of (slot, dim) of kv head kh in V page `page` (dim-major pages)."""
+    return ((page * kv_heads + kh) * HEAD_DIM + dim) * PAGE + slot
 
 
 class Kernels:
@@ -184,11 +190,14 @@ class Kernels:
         written = np.zeros(cache_bytes, bool)
         k_rows, v_rows = [], []
         for kh in range(heads.kv_heads):
-            row = ((page * heads.kv_heads + kh) * PAGE + at.pos % PAGE) * HEAD_DIM * 2
-            for base, acc in ((k_off, k_rows), (v_off, v_rows)):
-                s = base + row
-                written[s:s + HEAD_DIM * 2] = True
-                acc.append(allb[s:s + HEAD_DIM * 2].view(np.uint16))
+            s = k_off + ((page * heads.kv_heads + kh) * PAGE + at.pos % PAGE) * HEAD_DIM * 2
+            written[s:s + HEAD_DIM * 2] = True
+            k_rows.append(allb[s:s + HEAD_DIM * 2].view(np.uint16))
+            # V pages are dim-major: the row is 128 elements 16 apart.
+            idx = np.array([v_offset(page, heads.kv_heads, kh, at.pos % PAGE, d) for d in range(HEAD_DIM)])
+            for b in (0, 1):
+                written[v_off + 2 * idx + b] = True
+            v_rows.append(allb.view(np.uint16)[(v_off // 2) + idx].copy())
         rest = bool(np.all(allb[~written] == SENTINEL))
         return QkvOut(q_out, np.concatenate(k_rows), np.concatenate(v_rows), rest)
 
@@ -220,7 +229,8 @@ class Kernels:
         page_of = list(range(pages)) if page_of is None else list(page_of)[:pages]
         pool = pool or (max(page_of) + 1)
         kp = to_pages(np.asarray(k, np.uint16)[:ctx * h.kv_dim].reshape(ctx, h.kv_dim), h.kv_heads, page_of, pool)
-        vp = to_pages(np.asarray(v, np.uint16)[:ctx * h.kv_dim].reshape(ctx, h.kv_dim), h.kv_heads, page_of, pool)
+        vp = to_pages(np.asarray(v, np.uint16)[:ctx * h.kv_dim].reshape(ctx, h.kv_dim), h.kv_heads, page_of, pool,
+                      dim_major=True)
         a = self._arena()
         sl = {
             "q": a.alloc("q", q.size * 2, Class.CLIENT_DATA),
@@ -340,10 +350,13 @@ class Kernels:
         page_of = list(range(pages)) if page_of is None else list(page_of)
         pg, slot = page_of[(ctx - 1) // PAGE], (ctx - 1) % PAGE
         k_rows, v_rows = [], []
+        v_all = None
         for kh in range(h.kv_heads):
             at = ((pg * h.kv_heads + kh) * PAGE + slot) * HEAD_DIM
             k_rows.append(a.read_array(s["k"], at * 2, HEAD_DIM, np.uint16))
-            v_rows.append(a.read_array(s["v"], at * 2, HEAD_DIM, np.uint16))
+            if v_all is None:
+                v_all = a.read_array(s["v"], 0, s["v"].len // 2, np.uint16)
+            v_rows.append(v_all[[v_offset(pg, h.kv_heads, kh, slot, d) for d in range(HEAD_DIM)]])
         return a.read_array(s["out"], 0, qd, np.uint16), np.concatenate(k_rows), np.concatenate(v_rows)
 
     def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None):
