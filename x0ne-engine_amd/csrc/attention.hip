@@ -9,18 +9,20 @@
 // fixed order. The result depends on the inputs, ctx and P only.
 //
 // The layout and the work split are this build's own, shaped for CDNA:
-//  - K and V planes are paged: [pages][kv_heads][16][128] bf16, page_table[pos / 16] the
-//    physical page. A tile is 64 keys (4 pages); a block is 4 wavefronts and takes 4 tiles
-//    (256 keys) at a time: block y of P takes block-tiles y, y + P, ..., wavefront w the tile
-//    4 bt + w of each.
-//  - Each 16-byte load of a wavefront covers 4 whole rows of one page (1 KiB contiguous); the K
-//    and V loads of a tile are issued together. Lane (r = lane / 16, b = lane % 16) holds dims
-//    8b..8b+7 of rows 4i + r, i = 0..15.
-//  - The partial dot products of a lane (16 rows x G heads) are summed over the 16 lanes of a
-//    row by a transposing butterfly (xor 1, 2, 4, 8; each step halves the vector), so a lane ends
-//    with whole scores without reducing every value separately. Scores and softmax weights go
-//    through the wavefront's own LDS once per tile: each lane runs the online softmax of one key
-//    and the V accumulation of its own rows, with no further shuffles.
+//  - K planes are paged [pages][kv_heads][16][128] bf16 (key rows), V planes
+//    [pages][kv_heads][128][16] (dim-major: the operand layout of the matrix-core P V),
+//    page_table[pos / 16] the physical page. A tile is 64 keys (4 pages); a block is 4
+//    wavefronts. Slice y of P takes a contiguous run of tiles (a multiple of 4), its wavefront w
+//    the tiles w, w + 4, ... of the run, so a block reads 256 consecutive keys at a time.
+//  - The fp32 kernels run on the matrix cores (attend_wave_mfma): S^T = K Q^T and O = P V as
+//    16x16x32 bf16 products with fp32 accumulation, the G q heads of a kv head padded to 16, the
+//    tiles of a wavefront pipelined (the next tile's K and V requested while the current one is
+//    computed) through branch-free buffer loads.
+//  - The f64 (exact) mode and the per-head kernels run on the vector units (attend_wave): lane
+//    (r = lane / 16, b = lane % 16) holds dims 8b..8b+7 of key rows 4i + r; its partial dot
+//    products are summed over the 16 lanes of a row by a transposing butterfly (each step halves
+//    the vector), scores and weights pass once through LDS, and lane d accumulates dims d and
+//    d + 64 over the tile's keys.
 //  - The 4 wavefronts' states are merged in LDS; a block that covers the whole context (ctx of at
 //    most 256, or P = 1) writes the output directly, without a state, a counter or a second pass.
 //  - The fused variant starts with the QK-norm + RoPE of its G q heads (into LDS) and, in the
@@ -34,6 +36,22 @@ constexpr int WAVES = 4;
 constexpr int BLOCK = 64 * WAVES;
 constexpr uint32_t BLOCK_TILES = WAVES;  // tiles of 64 keys per block-tile
 constexpr uint32_t MERGE_MAX = 256;      // most slices a merge takes (P is capped at this)
+
+// The split of ctx keys over P slices: tiles of 64 keys, each slice a contiguous run of `per`
+// tiles (a multiple of the 4 a block takes at a time), `active` slices holding at least one.
+// Slice y takes tiles [y per, min((y + 1) per, ntiles)); wavefront w of its block the tiles
+// y per + w, + 4, ..., so the block reads 256 consecutive keys at a time.
+struct Split {
+    uint32_t ntiles, per, active;
+};
+__device__ __forceinline__ Split split_of(uint32_t ctx, uint32_t P) {
+    Split s;
+    s.ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
+    const uint32_t groups = (s.ntiles + BLOCK_TILES - 1) / BLOCK_TILES;  // 4-tile groups
+    s.per = BLOCK_TILES * ((groups + P - 1) / P);
+    s.active = (s.ntiles + s.per - 1) / s.per;
+    return s;
+}
 
 // Every LDS write this wavefront issued is done, and no memory access moves across this point.
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -90,8 +108,8 @@ __device__ __forceinline__ uint32_t rev4(uint32_t b) {
 template <int G, class T>
 __device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc,
                                             const uint32_t* __restrict__ pages, uint32_t kh, uint32_t kv_heads,
-                                            uint32_t ctx, uint32_t t0, uint32_t tstep, T scale, T* lds,
-                                            T m[G], T l[G], T o[G][2]) {
+                                            uint32_t ctx, uint32_t t0, uint32_t tstep, uint32_t t_end, T scale,
+                                            T* lds, T m[G], T l[G], T o[G][2]) {
     constexpr int HGMAX = sizeof(T) == 4 ? 4 : 2;  // heads per score pass (registers)
     constexpr int HG = G < HGMAX ? G : HGMAX;
     constexpr int PASSES = G / HG;
@@ -109,7 +127,8 @@ __device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __res
         o[g][1] = 0;
     }
 
-    for (uint32_t t = t0; t < ntiles; t += tstep) {
+    const uint32_t tend = min(t_end, ntiles);
+    for (uint32_t t = t0; t < tend; t += tstep) {
         const uint32_t base = t * X0NE_SPLIT_TILE;
         // Rows 4i + r of the tile: page base/16 + i/4, slot 4 (i % 4) + r. A page is looked up
         // only when its first key is below ctx (the table holds ceil(ctx / 16) pages at least).
@@ -239,6 +258,206 @@ __device__ __forceinline__ void attend_wave(const float* qs, const bf16_t* __res
     for (int g = 0; g < G; ++g) l[g] = acc_wave_sum(lsum[g]);
 }
 
+// ---- the matrix-core path (fp32 accumulation) ----
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// Raw buffer resources (gfx9 word 3): a load whose bytes are not all below `bytes` gives zeros
+// and touches no memory, so a key past the context or a prefetch past the last tile needs no
+// branch, and the compiler's waits before a use cover only the loads that use needs.
+constexpr int RSRC_WORD3 = 0x00020000;
+constexpr uint32_t OFF_NONE = 0xFFFFFFF0u;  // an offset past any plane: the load gives zeros
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, RSRC_WORD3);
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+
+// One wavefront on the matrix cores (v_mfma_f32_16x16x32_bf16; lane l: row or column l % 16,
+// k = 8 (l / 16) .. + 7 of a 32-wide step; result rows 4 (l / 16) .. + 3, column l % 16). The
+// G q heads are the 16 columns of S^T = K Q^T (heads past G are zero) and the 16 rows of
+// O = P V. For a tile of 64 keys: four 16-key blocks X0, Y0, X1, Y1 of S^T (block (kp, h)
+// row m is key 32 kp + 8 (m / 4) + 4 h + m % 4, so lane l ends with keys 32 kp + 8 (l / 16) +
+// 0..7 of its head: the k = 8 (l / 16) .. + 7 slice of P's 32-key step kp, in registers), four
+// 32-dim steps each; then P V over two 32-key steps and 8 blocks of 16 dims, V read from the
+// dim-major pages (8 consecutive keys of one dim = 16 bytes). P enters as bf16 hi + lo (two
+// products), so its rounding is about 2^-16 relative, below the fp32 accumulation's own.
+//
+// The tiles of a wavefront are pipelined: tile t + 1's K is requested right after tile t's
+// S^T, its V right after tile t's P V, and the page-table entries a tile ahead of that, so a
+// load is in flight while the matrix cores work. The planes are addressed by 32-bit byte
+// offsets (a plane below 4 GiB - 16 bytes); only OFF_NONE falls outside their resources.
+// qb[s]: the B operand of Q^T for step s. Leaves m (running max) and l (sum) of head l % 16 in
+// lane l, and o[nb][i] = O[head 4 (l / 16) + i][dim 16 nb + l % 16].
+__device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t* __restrict__ kc,
+                                                 const bf16_t* __restrict__ vc, const uint32_t* __restrict__ pages, uint32_t kh, uint32_t kv_heads,
+                                                 uint32_t ctx, uint32_t t0, uint32_t tstep, uint32_t t_end,
+                                                 float scale, float& m_out, float& l_out, f32x4 o[8]) {
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, q4 = lane >> 4;
+    const uint32_t ntiles = min(t_end, (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE);  // this wavefront's end
+    const auto kr = plane_rsrc(kc, OFF_NONE), vr = plane_rsrc(vc, OFF_NONE);
+    float m_run = -INFINITY, lsum = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t head_b = kh * X0NE_PAGE * X0NE_HEAD_DIM * 2;             // kv head's block in a page, bytes
+    const uint32_t page_b = kv_heads * X0NE_PAGE * X0NE_HEAD_DIM * 2;       // one page of one plane, bytes
+
+    // Page-table entries of a tile (0 for pages past the context; their loads read nothing).
+    auto tile_pages = [&](uint32_t t, uint32_t pg[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t first = t * X0NE_SPLIT_TILE + X0NE_PAGE * i;
+            pg[i] = (t < ntiles && first < ctx) ? pages[first / X0NE_PAGE] : 0u;
+        }
+    };
+    auto load_k = [&](uint32_t t, const uint32_t pg[4], uint4 (&ka)[2][2][4]) {
+        const uint32_t base = t * X0NE_SPLIT_TILE;
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t key = 32 * kp + 8 * (n >> 2) + 4 * h + (n & 3);
+                const bool ok = t < ntiles && base + key < ctx;
+                const uint32_t row = pg[key / X0NE_PAGE] * page_b + head_b + (key % X0NE_PAGE) * X0NE_HEAD_DIM * 2 + 16 * q4;
+#pragma unroll
+                for (int st = 0; st < 4; ++st) ka[kp][h][st] = bload16(kr, ok ? row + 64 * st : OFF_NONE);
+            }
+    };
+    auto load_v = [&](uint32_t t, const uint32_t pg[4], uint4 (&vb)[2][8]) {
+        const uint32_t base = t * X0NE_SPLIT_TILE;
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const uint32_t pp = 2 * kp + (q4 >> 1);
+            const bool live = t < ntiles && base + X0NE_PAGE * pp < ctx;
+            const uint32_t col = pg[pp] * page_b + head_b + 16 * (q4 & 1);
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb)
+                vb[kp][nb] = bload16(vr, live ? col + (16 * nb + n) * X0NE_PAGE * 2 : OFF_NONE);
+        }
+    };
+
+    uint32_t pg[4], pg_next[4];
+    uint4 ka[2][2][4], vb[2][8];
+    tile_pages(t0, pg);
+    load_k(t0, pg, ka);
+    load_v(t0, pg, vb);
+    tile_pages(t0 + tstep, pg_next);
+
+    for (uint32_t t = t0; t < ntiles; t += tstep) {
+        const uint32_t base = t * X0NE_SPLIT_TILE;
+        // S^T = K Q^T, then tile t + 1's K.
+        f32x4 sacc[2][2];
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) acc = mfma16x16x32(ka[kp][h][st], qb[st], acc);
+                sacc[kp][h] = acc;
+            }
+        load_k(t + tstep, pg_next, ka);
+        // Scale, mask, and the online softmax of head n over the lane's 16 keys and the 3 other
+        // lanes of the head (l ^ 16, l ^ 32).
+        float sc[2][2][4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t key = 32 * kp + 8 * q4 + 4 * h + i;
+                    sc[kp][h][i] = base + key < ctx ? sacc[kp][h][i] * scale : -INFINITY;
+                    mx = fmaxf(mx, sc[kp][h][i]);
+                }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m_run, mx);  // key `base` is below ctx: mn is finite
+        const float alpha = expf(m_run - mn);
+        m_run = mn;
+        float psum = 0.f;
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    sc[kp][h][i] = expf(sc[kp][h][i] - mn);
+                    psum += sc[kp][h][i];
+                }
+        lsum = lsum * alpha + psum;
+        // O rows are heads 4 q4 + i: their factors come from lanes 4 q4 + i.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * q4 + i, 64);
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) o[nb][i] *= ai;
+        }
+        // Keys past ctx in a live page hold anything: their V values are taken as 0 (their weight
+        // is 0, and 0 times a value that is not a number would not be).
+        if (base + X0NE_SPLIT_TILE > ctx) {
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                const uint32_t k0 = base + 32 * kp + 8 * q4;
+                const uint32_t valid = k0 >= ctx ? 0u : min(ctx - k0, 8u);  // keys kept, from the first
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) {
+                    uint32_t w[4] = {vb[kp][nb].x, vb[kp][nb].y, vb[kp][nb].z, vb[kp][nb].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t keep = (2 * e + 1 < valid ? 0xFFFF0000u : 0u) | (2 * e < valid ? 0xFFFFu : 0u);
+                        w[e] &= keep;
+                    }
+                    vb[kp][nb] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+        }
+        // O += P V, P as bf16 hi + lo; then tile t + 1's V and the pages of tile t + 2.
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            float pv[8], lo[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pv[i] = sc[kp][0][i];
+                pv[4 + i] = sc[kp][1][i];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) lo[j] = pv[j] - bf_round(pv[j]);
+            const uint4 ahi = make_uint4(pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]), pack_bf16(pv[4], pv[5]),
+                                         pack_bf16(pv[6], pv[7]));
+            const uint4 alo = make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]), pack_bf16(lo[4], lo[5]),
+                                         pack_bf16(lo[6], lo[7]));
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) {
+                o[nb] = mfma16x16x32(ahi, vb[kp][nb], o[nb]);
+                o[nb] = mfma16x16x32(alo, vb[kp][nb], o[nb]);
+            }
+        }
+        load_v(t + tstep, pg_next, vb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pg[i] = pg_next[i];
+        tile_pages(t + 2 * tstep, pg_next);
+    }
+    float l = lsum + __shfl_xor(lsum, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    m_out = m_run;
+    l_out = l;
+}
+
 // The shared memory of one block: q of its heads, each wavefront's exchange area, each
 // wavefront's state for the block merge, each wavefront's slice weights for a global merge.
 template <int G, class T = float>
@@ -251,29 +470,47 @@ struct AttnShared {
     uint32_t last;
 };
 
-__device__ __forceinline__ float ld_agent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
-// Merge of one q head's slices 0..active-1 in that order (FlashInfer's: M = max m_y,
-// f_y = exp(m_y - M), l = sum l_y f_y, o = sum o_y f_y; one rounding, of o / l). One wavefront;
-// lane d owns dims d and d + 64. f: this wavefront's LDS for `active` floats. Every active slice
-// saw a key, so each m is finite. States are read with agent-coherent loads: other workgroups
-// wrote them.
+// Merge of one q head's slices 0..active-1 (FlashInfer's: M = max m_y, f_y = exp(m_y - M),
+// l = sum l_y f_y, o = sum o_y f_y; one rounding, of o / l), the sums in a fixed order so the
+// result depends on the states only. One wavefront; lane y reads slice y's (m, l) (and y + 64,
+// ...), lane d owns dims d and d + 64 of o, whose loads are issued 8 slices at a time. f: this
+// wavefront's LDS for `active` floats. Every active slice saw a key, so each m is finite. The
+// caller has made other workgroups' states visible (their release, its acquire): plain loads.
 __device__ __forceinline__ void merge_head(const float* __restrict__ s, bf16_t* __restrict__ out_h, uint32_t active,
                                            float* f) {
     const uint32_t lane = threadIdx.x & 63;
     float mx = -INFINITY;
-    for (uint32_t y = 0; y < active; ++y) mx = fmaxf(mx, ld_agent(s + (size_t)y * X0NE_SPLIT_STATE));
-    for (uint32_t y = lane; y < active; y += 64) f[y] = expf(ld_agent(s + (size_t)y * X0NE_SPLIT_STATE) - mx);
+    for (uint32_t y = lane; y < active; y += 64) mx = fmaxf(mx, s[(size_t)y * X0NE_SPLIT_STATE]);
+    mx = wave_max(mx);
+    float lp = 0.f;
+    for (uint32_t y = lane; y < active; y += 64) {
+        const float fy = expf(s[(size_t)y * X0NE_SPLIT_STATE] - mx);
+        f[y] = fy;
+        lp += s[(size_t)y * X0NE_SPLIT_STATE + 1] * fy;
+    }
+    const float l = wave_sum(lp);
     wave_lds_sync();
-    float l = 0.f, o0 = 0.f, o1 = 0.f;
-    for (uint32_t y = 0; y < active; ++y) {
-        const float* st = s + (size_t)y * X0NE_SPLIT_STATE;
-        const float fy = f[y];
-        l += ld_agent(st + 1) * fy;
-        o0 += ld_agent(st + 4 + lane) * fy;
-        o1 += ld_agent(st + 4 + 64 + lane) * fy;
+    float o0 = 0.f, o1 = 0.f;
+    uint32_t y = 0;
+    for (; y + 8 <= active; y += 8) {
+        float a[8], b[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float* st = s + (size_t)(y + k) * X0NE_SPLIT_STATE + 4;
+            a[k] = st[lane];
+            b[k] = st[lane + 64];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            o0 = fmaf(a[k], f[y + k], o0);
+            o1 = fmaf(b[k], f[y + k], o1);
+        }
+    }
+    for (; y < active; ++y) {
+        const float* st = s + (size_t)y * X0NE_SPLIT_STATE + 4;
+        o0 = fmaf(st[lane], f[y], o0);
+        o1 = fmaf(st[lane + 64], f[y], o1);
     }
     out_h[lane] = f2bf(o0 / l);
     out_h[lane + 64] = f2bf(o1 / l);
@@ -365,11 +602,11 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t pos = a.pos[0];
     const uint32_t ctx = min(pos + 1u, a.max_ctx);
-    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
-    const uint32_t nbt = (ntiles + BLOCK_TILES - 1) / BLOCK_TILES;
+    const Split sp = split_of(ctx, P);
     // Block-uniform exits: a slice past the context, or a launch that does not fit the geometry.
-    if (y >= nbt || y >= P || P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
-    const uint32_t active = min(P, nbt);
+    if (y >= sp.active || y >= P || P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
+    const uint32_t active = sp.active;
+    const uint32_t t_begin = y * sp.per + wave, t_end = (y + 1) * sp.per;
     const uint32_t h0 = kh * G;
 
     // q of the G heads into LDS (the rotated values, rounded to bf16 as the engine stores q).
@@ -382,7 +619,7 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
             sh.qs[g][lane + 64] = bf_round(rb);
         }
         // The block owning pos's tile writes that position's K and V rows (its page, its slot).
-        const uint32_t owner = ((pos / X0NE_SPLIT_TILE) / BLOCK_TILES) % P;
+        const uint32_t owner = (pos / X0NE_SPLIT_TILE) / sp.per;
         if (pos < a.max_ctx && y == owner && wave == WAVES - 1) {
             const uint32_t kv_dim = a.kv_heads * X0NE_HEAD_DIM;
             float ra, rb;
@@ -401,12 +638,43 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
     }
     __syncthreads();  // q in LDS; the new K/V row in memory for the wavefront that reads it
 
-    // The exact mode scales by 1/sqrt(128) in f64, as the f64 oracle does.
-    const T scale = EXACT ? (T)(1.0 / sqrt((double)X0NE_HEAD_DIM)) : (T)a.scale;
-    T m[G], l[G], o[G][2];
-    attend_wave<G, T>(&sh.qs[0][0], a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, BLOCK_TILES * y + wave,
-                      BLOCK_TILES * P, scale, sh.xch[wave], m, l, o);
-    stash_wave<G, T>(sh, m, l, o);
+    if constexpr (EXACT) {
+        // The exact mode: scalar f64 sums, scaled by 1/sqrt(128) in f64 as the f64 oracle does.
+        const T scale = (T)(1.0 / sqrt((double)X0NE_HEAD_DIM));
+        T m[G], l[G], o[G][2];
+        attend_wave<G, T>(&sh.qs[0][0], a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, t_begin, BLOCK_TILES,
+                          t_end, scale, sh.xch[wave], m, l, o);
+        stash_wave<G, T>(sh, m, l, o);
+    } else {
+        // The matrix cores: Q^T as the B operand (head lane % 16, dims 32 st + 8 (lane / 16) ..),
+        // heads past G zero. The q values in LDS are bf16 already: the conversion is exact.
+        const uint32_t n = lane & 15, q4 = lane >> 4;
+        uint4 qb[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = n < (uint32_t)G ? sh.qs[n < (uint32_t)G ? n : 0][32 * st + 8 * q4 + j] : 0.f;
+            qb[st] = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
+                                pack_bf16(v[6], v[7]));
+        }
+        float mw, lw;
+        f32x4 ow[8];
+        attend_wave_mfma(qb, a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, t_begin, BLOCK_TILES, t_end, a.scale,
+                         mw, lw, ow);
+        if (q4 == 0 && n < (uint32_t)G) {
+            sh.wm[wave][n] = mw;
+            sh.wl[wave][n] = lw;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t h = 4 * q4 + i;
+            if (h < (uint32_t)G) {
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) sh.wo[wave][h][16 * nb + n] = ow[nb][i];
+            }
+        }
+    }
     __syncthreads();
 
     if (active == 1) {  // one block holds the whole context: the output directly
@@ -450,13 +718,12 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
     if (t < X0NE_HEAD_DIM) sh.qs[0][t] = bf2f(q_row[t]);
     __syncthreads();
     float m[1], l[1], o[1][2];
-    attend_wave<1, float>(&sh.qs[0][0], kc, vc, pages, kh, kv_heads, ctx, BLOCK_TILES * y + wave, BLOCK_TILES * P,
+    const Split sp = split_of(ctx, P);
+    attend_wave<1, float>(&sh.qs[0][0], kc, vc, pages, kh, kv_heads, ctx, y * sp.per + wave, BLOCK_TILES, (y + 1) * sp.per,
                           scale, sh.xch[wave], m, l, o);
     stash_wave<1, float>(sh, m, l, o);
     __syncthreads();
-    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
-    const uint32_t nbt = (ntiles + BLOCK_TILES - 1) / BLOCK_TILES;
-    if (min(P, nbt) == 1 && out_h != nullptr) {
+    if (sp.active == 1 && out_h != nullptr) {
         block_merge<1, float>(sh, [&](uint32_t, uint32_t d, float, float lv, float ov) { out_h[d] = f2bf(ov / lv); });
         return;
     }
@@ -578,8 +845,7 @@ extern "C" __global__ void __launch_bounds__(256)
     if (h >= q_heads || y >= splits || kv_heads == 0 || q_heads % kv_heads != 0) return;
     const uint32_t kh = h / (q_heads / kv_heads);
     const uint32_t ctx = min(pos[0] + 1u, max_ctx);
-    const uint32_t nbt = ((ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE + BLOCK_TILES - 1) / BLOCK_TILES;
-    if (y >= nbt) return;
+    if (y >= split_of(ctx, splits).active) return;
     attn_head_block(q + (size_t)h * X0NE_HEAD_DIM, k_cache, v_cache, pages, kh, kv_heads, ctx, y, splits, scale,
                     state + (size_t)h * splits * X0NE_SPLIT_STATE, out + (size_t)h * X0NE_HEAD_DIM, sh);
 }
@@ -592,8 +858,7 @@ extern "C" __global__ void __launch_bounds__(64)
     __shared__ float f[MERGE_MAX];
     const uint32_t h = blockIdx.x;
     const uint32_t ctx = min(pos[0] + 1u, max_ctx);
-    const uint32_t nbt = ((ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE + BLOCK_TILES - 1) / BLOCK_TILES;
-    const uint32_t active = min(splits, nbt);
+    const uint32_t active = split_of(ctx, splits).active;
     if (active <= 1 || splits > MERGE_MAX) return;
     merge_head(state + (size_t)h * splits * X0NE_SPLIT_STATE, out + (size_t)h * X0NE_HEAD_DIM, active, f);
 }
