@@ -142,6 +142,23 @@ def test_rope_far_into_a_long_context(kernels):
         assert out.rest_untouched
 
 
+def test_rope_table_is_the_cosine_and_sine_of_the_f32_angle(kernels):
+    """The fused attention's table: for each position and pair, cos and sin in f64 of the f32
+    product p * inv_freq[i], within 2 ulp of numpy's (the rotation kernels' own functions give
+    the table's bits: the fused-vs-two-kernel test compares the K rows they write bit for bit)."""
+    from x0ne_core.ops import inv_freq
+    n = 4096
+    t = kernels.rope_table(128, 1e6, n)
+    inv = inv_freq(128, 1e6)
+    angle = (np.arange(n, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float64)
+    assert angle.dtype == np.float64 and np.all(angle[1] == inv.astype(np.float64))
+    for k, f in [(0, np.cos), (1, np.sin)]:
+        want = f(angle)
+        err = np.abs(t[:, :, k] - want)
+        assert (err <= 2 * np.spacing(np.maximum(np.abs(want), 1e-300))).all(), f"{f.__name__}: {err.max()}"
+    assert (t[0, :, 0] == 1.0).all() and (t[0, :, 1] == 0.0).all()
+
+
 def assert_gemv(what, got, want, magnitude, rounded):
     bound = F32_RTOL * magnitude + (BF16_RTOL * np.abs(want).astype(np.float64) + BF16_ATOL if rounded else 1e-30)
     r = np.abs(got.astype(np.float64) - want.astype(np.float64)) / bound

@@ -267,9 +267,17 @@ __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
                                                    0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two finite values to bf16, nearest-even, in one word (v_cvt_pk_bf16_f32): the matrix-core
+// operands built from softmax weights, which are finite.
+__device__ __forceinline__ uint32_t pack_bf16_finite(float lo, float hi) {
+    const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
 
 // Raw buffer resources (gfx9 word 3): a load whose bytes are not all below `bytes` gives zeros
 // and touches no memory, so a key past the context or a prefetch past the last tile needs no
@@ -300,15 +308,29 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // S^T, its V right after tile t's P V, and the page-table entries a tile ahead of that, so a
 // load is in flight while the matrix cores work. The planes are addressed by 32-bit byte
 // offsets (a plane below 4 GiB - 16 bytes); only OFF_NONE falls outside their resources.
-// qb[s]: the B operand of Q^T for step s. Leaves m (running max) and l (sum) of head l % 16 in
-// lane l, and o[nb][i] = O[head 4 (l / 16) + i][dim 16 nb + l % 16].
-__device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t* __restrict__ kc,
+// prologue(qb) runs once the first tile's loads are issued and fills qb[s], the B operand of Q^T
+// for step s (every wavefront of the block calls it: it may hold a barrier). fx names the key
+// whose K and V rows come from LDS rather than from the loads. Leaves m (running max) and l (sum)
+// of head l % 16 in lane l, and o[nb][i] = O[head 4 (l / 16) + i][dim 16 nb + l % 16].
+//
+// The K and V rows of position pos as the block that writes them holds them in LDS: the
+// wavefront whose tile holds pos takes them from there, since its loads may be served before the
+// block's own write of that row lands (tile = ~0u: no such key).
+struct NewRow {
+    uint32_t tile, key;  // pos / 64 and pos % 64
+    const bf16_t* k;     // LDS, 128 bf16: the rotated K row (16-byte aligned)
+    const bf16_t* v;     // LDS, 128 bf16: the V row
+};
+template <class Prologue>
+__device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewRow& fx, const bf16_t* __restrict__ kc,
                                                  const bf16_t* __restrict__ vc, const uint32_t* __restrict__ pages, uint32_t kh, uint32_t kv_heads,
                                                  uint32_t ctx, uint32_t t0, uint32_t tstep, uint32_t t_end,
                                                  float scale, float& m_out, float& l_out, f32x4 o[8]) {
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, q4 = lane >> 4;
     const uint32_t ntiles = min(t_end, (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE);  // this wavefront's end
     const auto kr = plane_rsrc(kc, OFF_NONE), vr = plane_rsrc(vc, OFF_NONE);
+    // Scores in units of log2 (scale log2 e folded in), so each weight is one exp2.
+    const float scale2 = scale * LOG2E;
     float m_run = -INFINITY, lsum = 0.f;
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -351,13 +373,33 @@ __device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t
 
     uint32_t pg[4], pg_next[4];
     uint4 ka[2][2][4], vb[2][8];
+    // Loads only for tiles that exist (wavefront-uniform branches): a load past the last tile
+    // would still cost its address cycles in the CU's memory pipeline.
     tile_pages(t0, pg);
-    load_k(t0, pg, ka);
-    load_v(t0, pg, vb);
+    if (t0 < ntiles) {
+        load_k(t0, pg, ka);
+        load_v(t0, pg, vb);
+    }
     tile_pages(t0 + tstep, pg_next);
+    uint4 qb[4];
+    prologue(qb);  // while the first tile is in flight
 
     for (uint32_t t = t0; t < ntiles; t += tstep) {
         const uint32_t base = t * X0NE_SPLIT_TILE;
+        if (t == fx.tile) {  // wavefront-uniform: key fx.key of this tile is the new row
+            const uint32_t r = fx.key & 31, ksel = fx.key >> 5, hsel = (r >> 2) & 1u;
+            if (n == 4 * (r >> 3) + (r & 3)) {
+#pragma unroll
+                for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        if (kp == (int)ksel && h == (int)hsel) {
+#pragma unroll
+                            for (int st = 0; st < 4; ++st)
+                                ka[kp][h][st] = *reinterpret_cast<const uint4*>(fx.k + 32 * st + 8 * q4);
+                        }
+            }
+        }
         // S^T = K Q^T, then tile t + 1's K.
         f32x4 sacc[2][2];
 #pragma unroll
@@ -369,7 +411,7 @@ __device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t
                 for (int st = 0; st < 4; ++st) acc = mfma16x16x32(ka[kp][h][st], qb[st], acc);
                 sacc[kp][h] = acc;
             }
-        load_k(t + tstep, pg_next, ka);
+        if (t + tstep < ntiles) load_k(t + tstep, pg_next, ka);
         // Scale, mask, and the online softmax of head n over the lane's 16 keys and the 3 other
         // lanes of the head (l ^ 16, l ^ 32).
         float sc[2][2][4];
@@ -381,13 +423,13 @@ __device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t key = 32 * kp + 8 * q4 + 4 * h + i;
-                    sc[kp][h][i] = base + key < ctx ? sacc[kp][h][i] * scale : -INFINITY;
+                    sc[kp][h][i] = base + key < ctx ? sacc[kp][h][i] * scale2 : -INFINITY;
                     mx = fmaxf(mx, sc[kp][h][i]);
                 }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mn = fmaxf(m_run, mx);  // key `base` is below ctx: mn is finite
-        const float alpha = expf(m_run - mn);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
         m_run = mn;
         float psum = 0.f;
 #pragma unroll
@@ -396,7 +438,7 @@ __device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    sc[kp][h][i] = expf(sc[kp][h][i] - mn);
+                    sc[kp][h][i] = __builtin_amdgcn_exp2f(sc[kp][h][i] - mn);
                     psum += sc[kp][h][i];
                 }
         lsum = lsum * alpha + psum;
@@ -426,6 +468,23 @@ __device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t
                 }
             }
         }
+        if (t == fx.tile && q4 == ((fx.key >> 3) & 3u)) {  // the new row's V: key fx.key % 8 of the lane's 8
+            const uint32_t vsel = fx.key >> 5, e = fx.key & 7u;
+            const uint32_t shift = 16 * (e & 1u), keep = shift ? 0x0000FFFFu : 0xFFFF0000u;
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp)
+                if (kp == (int)vsel) {
+#pragma unroll
+                    for (int nb = 0; nb < 8; ++nb) {
+                        uint32_t w[4] = {vb[kp][nb].x, vb[kp][nb].y, vb[kp][nb].z, vb[kp][nb].w};
+                        const uint32_t val = (uint32_t)fx.v[16 * nb + n] << shift;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            if (j == (int)(e >> 1)) w[j] = (w[j] & keep) | val;
+                        vb[kp][nb] = make_uint4(w[0], w[1], w[2], w[3]);
+                    }
+                }
+        }
         // O += P V, P as bf16 hi + lo; then tile t + 1's V and the pages of tile t + 2.
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
@@ -435,26 +494,30 @@ __device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t
                 pv[i] = sc[kp][0][i];
                 pv[4 + i] = sc[kp][1][i];
             }
+            uint32_t hw[4], lw[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) lo[j] = pv[j] - bf_round(pv[j]);
-            const uint4 ahi = make_uint4(pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]), pack_bf16(pv[4], pv[5]),
-                                         pack_bf16(pv[6], pv[7]));
-            const uint4 alo = make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]), pack_bf16(lo[4], lo[5]),
-                                         pack_bf16(lo[6], lo[7]));
+            for (int j = 0; j < 4; ++j) {
+                hw[j] = pack_bf16_finite(pv[2 * j], pv[2 * j + 1]);
+                lo[2 * j] = pv[2 * j] - bf_lo(hw[j]);  // exact
+                lo[2 * j + 1] = pv[2 * j + 1] - bf_hi(hw[j]);
+                lw[j] = pack_bf16_finite(lo[2 * j], lo[2 * j + 1]);
+            }
+            const uint4 ahi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            const uint4 alo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
 #pragma unroll
             for (int nb = 0; nb < 8; ++nb) {
                 o[nb] = mfma16x16x32(ahi, vb[kp][nb], o[nb]);
                 o[nb] = mfma16x16x32(alo, vb[kp][nb], o[nb]);
             }
         }
-        load_v(t + tstep, pg_next, vb);
+        if (t + tstep < ntiles) load_v(t + tstep, pg_next, vb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) pg[i] = pg_next[i];
         tile_pages(t + 2 * tstep, pg_next);
     }
     float l = lsum + __shfl_xor(lsum, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    m_out = m_run;
+    m_out = m_run * LN2;  // back to natural units for the merges
     l_out = l;
 }
 
@@ -462,10 +525,13 @@ __device__ __forceinline__ void attend_wave_mfma(const uint4 qb[4], const bf16_t
 // wavefront's state for the block merge, each wavefront's slice weights for a global merge.
 template <int G, class T = float>
 struct AttnShared {
-    float qs[G][X0NE_HEAD_DIM];
+    float qs[G][X0NE_HEAD_DIM];                      // the vector-unit paths' q
+    alignas(16) bf16_t qh[G][X0NE_HEAD_DIM];         // the matrix-core path's q (bf16)
+    alignas(16) bf16_t knew[X0NE_HEAD_DIM], vnew[X0NE_HEAD_DIM];  // the fused variant's new K/V row
     T xch[WAVES][2 * G * 64];
     T wm[WAVES][G], wl[WAVES][G];
     T wo[WAVES][G][X0NE_HEAD_DIM];
+    T wf[WAVES][G], mh[G], lh[G];  // the block merge's factors, maximum and sum per head
     float f[sizeof(T) == 4 ? WAVES : 1][MERGE_MAX];  // the exact mode has no global merge
     uint32_t last;
 };
@@ -518,43 +584,72 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ s, bf16_t* 
 }
 
 // The 4 wavefronts' states of a block merged (in wave order, a wavefront without a key skipped),
-// per head g and dim d. Thread t takes the (g, d) pairs t, t + 256, ...; calls f(g, d, m, l, o).
+// per head g and dim d: threads 0..G-1 first take each head's maximum, factors and sum into LDS;
+// then thread t takes the (g, d) pairs t, t + 256, ... and calls f(g, d, m, l, o). Every thread
+// of the block calls it (it holds a barrier), after the wavefronts' states are in LDS.
 template <int G, class T, class F>
-__device__ __forceinline__ void block_merge(const AttnShared<G, T>& sh, F f) {
-    for (uint32_t k = threadIdx.x; k < (uint32_t)G * X0NE_HEAD_DIM; k += BLOCK) {
-        const uint32_t g = k / X0NE_HEAD_DIM, d = k % X0NE_HEAD_DIM;
+__device__ __forceinline__ void block_merge(AttnShared<G, T>& sh, F f) {
+    const uint32_t t = threadIdx.x;
+    if (t < (uint32_t)G) {
         T mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) mx = acc_max(mx, sh.wm[w][g]);
-        T l = 0, o = 0;
+        for (int w = 0; w < WAVES; ++w) mx = acc_max(mx, sh.wm[w][t]);
+        T l = 0;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) {
-            if (sh.wm[w][g] == (T)-INFINITY) continue;  // the wavefront saw no key
-            const T fw = acc_exp(sh.wm[w][g] - mx);
-            l += sh.wl[w][g] * fw;
-            o += sh.wo[w][g][d] * fw;
+            const bool seen = sh.wm[w][t] != (T)-INFINITY;  // the wavefront saw a key
+            const T fw = seen ? acc_exp(sh.wm[w][t] - mx) : (T)0;
+            sh.wf[w][t] = fw;
+            if (seen) l += sh.wl[w][t] * fw;
         }
-        f(g, d, mx, l, o);
+        sh.mh[t] = mx;
+        sh.lh[t] = l;
+    }
+    lds_barrier();
+    for (uint32_t k = t; k < (uint32_t)G * X0NE_HEAD_DIM; k += BLOCK) {
+        const uint32_t g = k / X0NE_HEAD_DIM, d = k % X0NE_HEAD_DIM;
+        T o = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w)
+            if (sh.wm[w][g] != (T)-INFINITY) o += sh.wo[w][g][d] * sh.wf[w][g];
+        f(g, d, sh.mh[g], sh.lh[g], o);
     }
 }
 
+// One head row's pair (lane i: elements i and i + 64) and its norm weights, as loaded.
+struct RopeIn {
+    float a, b, wa, wb;
+};
+__device__ __forceinline__ RopeIn rope_in(const bf16_t* __restrict__ src, const bf16_t* __restrict__ nw) {
+    constexpr uint32_t HALF = X0NE_HEAD_DIM / 2;
+    const uint32_t i = threadIdx.x & 63;
+    return {bf2f(src[i]), bf2f(src[i + HALF]), bf2f(nw[i]), bf2f(nw[i + HALF])};
+}
+
 // QK-norm + RoPE of one head row (oracle/src/lib.rs:95-110; rope.cu:7-47): lane i owns the pair
-// (i, i + 64); RMSNorm and the rotation in f64, the angle the f32 product pos * inv_freq[i].
+// (i, i + 64); RMSNorm and the rotation in f64 by the angle whose cosine and sine are c and s.
 // Returns the two rotated values, unrounded.
+__device__ __forceinline__ void rope_rotate_cs(const RopeIn& r, double c, double s, float eps, float* ra,
+                                               float* rb) {
+    const double ss = wave_sum_d((double)r.a * (double)r.a + (double)r.b * (double)r.b);
+    const double scale = 1.0 / sqrt(ss / (double)X0NE_HEAD_DIM + (double)eps);
+    const double na = (double)r.a * scale * (double)r.wa;
+    const double nb = (double)r.b * scale * (double)r.wb;
+    *ra = (float)(na * c - nb * s);
+    *rb = (float)(nb * c + na * s);
+}
+
+// The angle of lane i is the f32 product pos * inv_freq[i] (invf), its sine and cosine in f64.
+__device__ __forceinline__ void rope_rotate(const RopeIn& r, float invf, uint32_t pos, float eps, float* ra,
+                                            float* rb) {
+    const double angle = (double)((float)pos * invf);
+    rope_rotate_cs(r, cos(angle), sin(angle), eps, ra, rb);
+}
+
 __device__ __forceinline__ void rope_pair(const bf16_t* __restrict__ src, const bf16_t* __restrict__ nw,
                                           const float* __restrict__ inv_freq, uint32_t pos, float eps, float* ra,
                                           float* rb) {
-    constexpr uint32_t HALF = X0NE_HEAD_DIM / 2;
-    const uint32_t i = threadIdx.x & 63;
-    const float a = bf2f(src[i]), b = bf2f(src[i + HALF]);
-    const double ss = wave_sum_d((double)a * (double)a + (double)b * (double)b);
-    const double scale = 1.0 / sqrt(ss / (double)X0NE_HEAD_DIM + (double)eps);
-    const double na = (double)a * scale * (double)bf2f(nw[i]);
-    const double nb = (double)b * scale * (double)bf2f(nw[i + HALF]);
-    const double angle = (double)((float)pos * inv_freq[i]);
-    const double s = sin(angle), c = cos(angle);
-    *ra = (float)(na * c - nb * s);
-    *rb = (float)(nb * c + na * s);
+    rope_rotate(rope_in(src, nw), inv_freq[threadIdx.x & 63], pos, eps, ra, rb);
 }
 
 struct AttnArgs {
@@ -563,6 +658,7 @@ struct AttnArgs {
     const bf16_t* q_norm;    // fused
     const bf16_t* k_norm;    // fused
     const float* inv_freq;   // fused
+    const double* rope_cs;   // fused: cos and sin per position below max_ctx and lane (x0ne_rope_table_f64)
     bf16_t* k_cache;         // written by the fused variant at pos
     bf16_t* v_cache;
     const uint32_t* pages;
@@ -592,76 +688,161 @@ __device__ __forceinline__ void stash_wave(AttnShared<G, T>& sh, const T m[G], c
     }
 }
 
-// Block (kv head kh, slice y) of the grouped kernel: q heads kh G .. kh G + G - 1. With
-// T = double (the exact mode) P is 1: the block attends the whole context and writes out.
-template <int G, bool FUSED, class T>
-__device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G, T>& sh) {
-    constexpr bool EXACT = sizeof(T) == 8;
+// The exact mode's block (kv head kh, the whole context, P = 1): QK-norm + RoPE of the G q heads
+// and the K/V write of position pos, then scalar f64 scores, softmax and sums, scaled by
+// 1/sqrt(128) in f64 as the f64 oracle does, and the output.
+template <int G>
+__device__ __forceinline__ void attn_group_block_exact(const AttnArgs& a, AttnShared<G, double>& sh) {
+    const uint32_t kh = blockIdx.x;
+    if (a.splits != 1 || blockIdx.y != 0 || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t pos = a.pos[0];
+    const uint32_t ctx = min(pos + 1u, a.max_ctx);
+    const uint32_t h0 = kh * G, q_dim = a.q_heads * X0NE_HEAD_DIM;
+    for (uint32_t g = wave; g < (uint32_t)G; g += WAVES) {
+        float ra, rb;
+        rope_pair(a.qkv + (h0 + g) * X0NE_HEAD_DIM, a.q_norm, a.inv_freq, pos, a.eps, &ra, &rb);
+        sh.qs[g][lane] = bf_round(ra);
+        sh.qs[g][lane + 64] = bf_round(rb);
+    }
+    if (pos < a.max_ctx && wave == WAVES - 1) {
+        const uint32_t kv_dim = a.kv_heads * X0NE_HEAD_DIM;
+        float ra, rb;
+        rope_pair(a.qkv + q_dim + kh * X0NE_HEAD_DIM, a.k_norm, a.inv_freq, pos, a.eps, &ra, &rb);
+        const uint32_t at = kv_row(a.pages, pos, kh, a.kv_heads);
+        a.k_cache[at + lane] = f2bf(ra);
+        a.k_cache[at + lane + 64] = f2bf(rb);
+        const bf16_t* vs = a.qkv + q_dim + kv_dim + kh * X0NE_HEAD_DIM;
+        const uint32_t vat = v_slot(a.pages, pos, kh, a.kv_heads);
+        a.v_cache[vat + lane * X0NE_PAGE] = vs[lane];
+        a.v_cache[vat + (lane + 64) * X0NE_PAGE] = vs[lane + 64];
+    }
+    __syncthreads();  // q in LDS; the new K/V row in memory for the wavefront that reads it
+    const double scale = 1.0 / sqrt((double)X0NE_HEAD_DIM);
+    double m[G], l[G], o[G][2];
+    attend_wave<G, double>(&sh.qs[0][0], a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, wave, BLOCK_TILES,
+                           ~0u, scale, sh.xch[wave], m, l, o);
+    stash_wave<G, double>(sh, m, l, o);
+    lds_barrier();
+    block_merge<G, double>(sh, [&](uint32_t g, uint32_t d, double, double lv, double ov) {
+        a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf((float)(ov / lv));
+    });
+}
+
+// Block (kv head kh, slice y) of the grouped kernel on the matrix cores: q heads kh G .. kh G +
+// G - 1. The loads that do not depend on pos (the q rows, or the packed qkv rows and norm
+// weights of the fused variant) are issued first, the first tile's page-table entries and K/V as
+// soon as pos is known, and the QK-norm + RoPE runs while those are in flight. In the fused
+// variant the block owning pos's tile writes that position's K and V rows to their page and
+// keeps them in LDS for its wavefront that attends them, so no wavefront waits for that write.
+template <int G, bool FUSED>
+__device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G>& sh) {
     const uint32_t kh = blockIdx.x, y = blockIdx.y, P = a.splits;
-    if (EXACT && P != 1) return;
-    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // Block-uniform exits for a launch that does not fit the geometry, before any load.
+    if (P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t h0 = kh * G, q_dim = a.q_heads * X0NE_HEAD_DIM, kv_dim = a.kv_heads * X0NE_HEAD_DIM;
+
+    // Requested before pos: the fused variant's q rows wave, wave + 4, ... of the group (and in
+    // the last wavefront kv head kh's K and V rows), or the plain variant's q values.
+    constexpr int QPW = (G + WAVES - 1) / WAVES;             // q heads a wavefront ropes
+    constexpr int QV = (G * X0NE_HEAD_DIM + BLOCK - 1) / BLOCK;  // plain: q values per thread
+    RopeIn qin[QPW], kin{};
+    bf16_t vrow[2] = {0, 0}, qv[QV];
+    float invf = 0.f;
+    if (FUSED) {
+#pragma unroll
+        for (int j = 0; j < QPW; ++j) {
+            const uint32_t g = wave + WAVES * j;
+            qin[j] = g < (uint32_t)G ? rope_in(a.qkv + (h0 + g) * X0NE_HEAD_DIM, a.q_norm) : RopeIn{};
+        }
+        invf = a.inv_freq[lane];
+        if (wave == WAVES - 1) {
+            kin = rope_in(a.qkv + q_dim + kh * X0NE_HEAD_DIM, a.k_norm);
+            const bf16_t* vs = a.qkv + q_dim + kv_dim + kh * X0NE_HEAD_DIM;
+            vrow[0] = vs[lane];
+            vrow[1] = vs[lane + 64];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < QV; ++j) {
+            const uint32_t k = t + BLOCK * j;
+            qv[j] = k < (uint32_t)G * X0NE_HEAD_DIM ? a.q[(size_t)h0 * X0NE_HEAD_DIM + k] : (bf16_t)0;
+        }
+    }
+
     const uint32_t pos = a.pos[0];
     const uint32_t ctx = min(pos + 1u, a.max_ctx);
     const Split sp = split_of(ctx, P);
-    // Block-uniform exits: a slice past the context, or a launch that does not fit the geometry.
-    if (y >= sp.active || y >= P || P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
+    if (y >= sp.active) return;  // block-uniform: a slice past the context
     const uint32_t active = sp.active;
     const uint32_t t_begin = y * sp.per + wave, t_end = (y + 1) * sp.per;
-    const uint32_t h0 = kh * G;
-
-    // q of the G heads into LDS (the rotated values, rounded to bf16 as the engine stores q).
+    const bool owner = FUSED && pos < a.max_ctx && y == (pos / X0NE_SPLIT_TILE) / sp.per;
+    // This lane's cosine and sine at pos: the table's below max_ctx, else computed alike.
+    double rc = 0.0, rs = 0.0;
     if (FUSED) {
-        const uint32_t q_dim = a.q_heads * X0NE_HEAD_DIM;
-        for (uint32_t g = wave; g < (uint32_t)G; g += WAVES) {
-            float ra, rb;
-            rope_pair(a.qkv + (h0 + g) * X0NE_HEAD_DIM, a.q_norm, a.inv_freq, pos, a.eps, &ra, &rb);
-            sh.qs[g][lane] = bf_round(ra);
-            sh.qs[g][lane + 64] = bf_round(rb);
+        if (pos < a.max_ctx) {
+            const double2 v = *reinterpret_cast<const double2*>(a.rope_cs + 2 * ((size_t)pos * (X0NE_HEAD_DIM / 2) + lane));
+            rc = v.x;
+            rs = v.y;
+        } else {
+            const double angle = (double)((float)pos * invf);
+            rc = cos(angle);
+            rs = sin(angle);
         }
-        // The block owning pos's tile writes that position's K and V rows (its page, its slot).
-        const uint32_t owner = (pos / X0NE_SPLIT_TILE) / sp.per;
-        if (pos < a.max_ctx && y == owner && wave == WAVES - 1) {
-            const uint32_t kv_dim = a.kv_heads * X0NE_HEAD_DIM;
-            float ra, rb;
-            rope_pair(a.qkv + q_dim + kh * X0NE_HEAD_DIM, a.k_norm, a.inv_freq, pos, a.eps, &ra, &rb);
-            const uint32_t at = kv_row(a.pages, pos, kh, a.kv_heads);
-            a.k_cache[at + lane] = f2bf(ra);
-            a.k_cache[at + lane + 64] = f2bf(rb);
-            const bf16_t* vs = a.qkv + q_dim + kv_dim + kh * X0NE_HEAD_DIM;
-            const uint32_t vat = v_slot(a.pages, pos, kh, a.kv_heads);
-            a.v_cache[vat + lane * X0NE_PAGE] = vs[lane];
-            a.v_cache[vat + (lane + 64) * X0NE_PAGE] = vs[lane + 64];
-        }
-    } else {
-        for (uint32_t k = t; k < (uint32_t)G * X0NE_HEAD_DIM; k += BLOCK)
-            sh.qs[k / X0NE_HEAD_DIM][k % X0NE_HEAD_DIM] = bf2f(a.q[(size_t)h0 * X0NE_HEAD_DIM + k]);
     }
-    __syncthreads();  // q in LDS; the new K/V row in memory for the wavefront that reads it
+    const NewRow fx = {owner ? pos / X0NE_SPLIT_TILE : ~0u, pos % X0NE_SPLIT_TILE, sh.knew, sh.vnew};
 
-    if constexpr (EXACT) {
-        // The exact mode: scalar f64 sums, scaled by 1/sqrt(128) in f64 as the f64 oracle does.
-        const T scale = (T)(1.0 / sqrt((double)X0NE_HEAD_DIM));
-        T m[G], l[G], o[G][2];
-        attend_wave<G, T>(&sh.qs[0][0], a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, t_begin, BLOCK_TILES,
-                          t_end, scale, sh.xch[wave], m, l, o);
-        stash_wave<G, T>(sh, m, l, o);
-    } else {
-        // The matrix cores: Q^T as the B operand (head lane % 16, dims 32 st + 8 (lane / 16) ..),
-        // heads past G zero. The q values in LDS are bf16 already: the conversion is exact.
+    // q into LDS as bf16 (the rotated values rounded, as the engine stores q), then the B operand
+    // of Q^T: head lane % 16, dims 32 st + 8 (lane / 16) .., heads past G zero.
+    auto prologue = [&](uint4 qb[4]) {
+        if (FUSED) {
+#pragma unroll
+            for (int j = 0; j < QPW; ++j) {
+                const uint32_t g = wave + WAVES * j;
+                if (g < (uint32_t)G) {
+                    float ra, rb;
+                    rope_rotate_cs(qin[j], rc, rs, a.eps, &ra, &rb);
+                    sh.qh[g][lane] = f2bf(ra);
+                    sh.qh[g][lane + 64] = f2bf(rb);
+                }
+            }
+            if (owner && wave == WAVES - 1) {  // the K/V write of position pos, and its LDS copy
+                float ra, rb;
+                rope_rotate_cs(kin, rc, rs, a.eps, &ra, &rb);
+                const bf16_t k0 = f2bf(ra), k1 = f2bf(rb);
+                const uint32_t at = kv_row(a.pages, pos, kh, a.kv_heads);
+                a.k_cache[at + lane] = k0;
+                a.k_cache[at + lane + 64] = k1;
+                const uint32_t vat = v_slot(a.pages, pos, kh, a.kv_heads);
+                a.v_cache[vat + lane * X0NE_PAGE] = vrow[0];
+                a.v_cache[vat + (lane + 64) * X0NE_PAGE] = vrow[1];
+                sh.knew[lane] = k0;
+                sh.knew[lane + 64] = k1;
+                sh.vnew[lane] = vrow[0];
+                sh.vnew[lane + 64] = vrow[1];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < QV; ++j) {
+                const uint32_t k = t + BLOCK * j;
+                if (k < (uint32_t)G * X0NE_HEAD_DIM) sh.qh[k / X0NE_HEAD_DIM][k % X0NE_HEAD_DIM] = qv[j];
+            }
+        }
+        lds_barrier();  // q and the new row in LDS; the loads in flight stay in flight
         const uint32_t n = lane & 15, q4 = lane >> 4;
-        uint4 qb[4];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = n < (uint32_t)G ? sh.qs[n < (uint32_t)G ? n : 0][32 * st + 8 * q4 + j] : 0.f;
-            qb[st] = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
-                                pack_bf16(v[6], v[7]));
+            const uint4 v = *reinterpret_cast<const uint4*>(&sh.qh[n < (uint32_t)G ? n : 0][32 * st + 8 * q4]);
+            qb[st] = n < (uint32_t)G ? v : make_uint4(0, 0, 0, 0);
         }
-        float mw, lw;
-        f32x4 ow[8];
-        attend_wave_mfma(qb, a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, t_begin, BLOCK_TILES, t_end, a.scale,
-                         mw, lw, ow);
+    };
+    float mw, lw;
+    f32x4 ow[8];
+    attend_wave_mfma(prologue, fx, a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, t_begin, BLOCK_TILES, t_end,
+                     a.scale, mw, lw, ow);
+    {
+        const uint32_t n = lane & 15, q4 = lane >> 4;
         if (q4 == 0 && n < (uint32_t)G) {
             sh.wm[wave][n] = mw;
             sh.wl[wave][n] = lw;
@@ -675,36 +856,34 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     if (active == 1) {  // one block holds the whole context: the output directly
-        block_merge<G, T>(sh, [&](uint32_t g, uint32_t d, T, T lv, T ov) {
-            a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf((float)(ov / lv));
+        block_merge<G, float>(sh, [&](uint32_t g, uint32_t d, float, float lv, float ov) {
+            a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf(ov / lv);
         });
         return;
     }
-    if constexpr (!EXACT) {
-        block_merge<G, T>(sh, [&](uint32_t g, uint32_t d, float mv, float lv, float ov) {
-            float* st = a.state + ((size_t)(h0 + g) * P + y) * X0NE_SPLIT_STATE;
-            st[4 + d] = ov;
-            if (d == 0) {
-                st[0] = mv;
-                st[1] = lv;
-            }
-        });
-        if (a.counter == nullptr) return;  // grid-uniform: the merge kernel follows
-        __threadfence();  // this block's states, visible to the block that merges
-        __syncthreads();
-        if (t == 0) sh.last = atomicAdd(a.counter + kh, 1u) == active - 1;
-        __syncthreads();
-        if (!sh.last) return;  // block-uniform
-        __threadfence();
-        for (uint32_t g = wave; g < (uint32_t)G; g += WAVES)
-            merge_head(a.state + (size_t)(h0 + g) * P * X0NE_SPLIT_STATE, a.out + (size_t)(h0 + g) * X0NE_HEAD_DIM,
-                       active, sh.f[wave]);
-        __syncthreads();
-        if (t == 0) a.counter[kh] = 0;  // ready for the next step
-    }
+    block_merge<G, float>(sh, [&](uint32_t g, uint32_t d, float mv, float lv, float ov) {
+        float* st = a.state + ((size_t)(h0 + g) * P + y) * X0NE_SPLIT_STATE;
+        st[4 + d] = ov;
+        if (d == 0) {
+            st[0] = mv;
+            st[1] = lv;
+        }
+    });
+    if (a.counter == nullptr) return;  // grid-uniform: the merge kernel follows
+    __threadfence();  // this block's states, visible to the block that merges
+    __syncthreads();
+    if (t == 0) sh.last = atomicAdd(a.counter + kh, 1u) == active - 1;
+    __syncthreads();
+    if (!sh.last) return;  // block-uniform
+    __threadfence();
+    for (uint32_t g = wave; g < (uint32_t)G; g += WAVES)
+        merge_head(a.state + (size_t)(h0 + g) * P * X0NE_SPLIT_STATE, a.out + (size_t)(h0 + g) * X0NE_HEAD_DIM,
+                   active, sh.f[wave]);
+    __syncthreads();
+    if (t == 0) a.counter[kh] = 0;  // ready for the next step
 }
 
 // One q head per block (group sizes without a grouped kernel, the per-head witness, prefill):
@@ -774,20 +953,21 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         a.max_ctx = max_ctx;                                                                                       \
         a.splits = splits;                                                                                         \
         a.scale = scale;                                                                                           \
-        attn_group_block<G, false, float>(a, sh);                                                                         \
+        attn_group_block<G, false>(a, sh);                                                                         \
     }                                                                                                              \
     extern "C" __global__ void __launch_bounds__(256) x0ne_attention_rope_decode_g##G##_bf16(                     \
         const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm, const bf16_t* __restrict__ k_norm,    \
-        const float* __restrict__ inv_freq, bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,          \
-        const uint32_t* __restrict__ pages, float* __restrict__ state, uint32_t* __restrict__ counter,           \
-        bf16_t* __restrict__ out, const uint32_t* __restrict__ pos, uint32_t q_heads, uint32_t kv_heads,         \
-        uint32_t max_ctx, uint32_t splits, float scale, float eps) {                                              \
+        const float* __restrict__ inv_freq, const double* __restrict__ rope_cs, bf16_t* __restrict__ k_cache,    \
+        bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages, float* __restrict__ state,             \
+        uint32_t* __restrict__ counter, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,              \
+        uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale, float eps) {         \
         __shared__ AttnShared<G> sh;                                                                               \
         AttnArgs a = {};                                                                                           \
         a.qkv = qkv;                                                                                               \
         a.q_norm = q_norm;                                                                                         \
         a.k_norm = k_norm;                                                                                         \
         a.inv_freq = inv_freq;                                                                                     \
+        a.rope_cs = rope_cs;                                                                                       \
         a.k_cache = k_cache;                                                                                       \
         a.v_cache = v_cache;                                                                                       \
         a.pages = pages;                                                                                           \
@@ -801,7 +981,7 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         a.splits = splits;                                                                                         \
         a.scale = scale;                                                                                           \
         a.eps = eps;                                                                                               \
-        attn_group_block<G, true, float>(a, sh);                                                                   \
+        attn_group_block<G, true>(a, sh);                                                                          \
     }                                                                                                              \
     extern "C" __global__ void __launch_bounds__(256) x0ne_attention_rope_decode_exact_g##G##_bf16(               \
         const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm, const bf16_t* __restrict__ k_norm,    \
@@ -824,7 +1004,7 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         a.max_ctx = max_ctx;                                                                                       \
         a.splits = 1;                                                                                              \
         a.eps = eps;                                                                                               \
-        attn_group_block<G, true, double>(a, sh);                                                                  \
+        attn_group_block_exact<G>(a, sh);                                                                          \
     }
 X0NE_SPLIT_GROUP(1)
 X0NE_SPLIT_GROUP(2)

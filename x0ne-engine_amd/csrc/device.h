@@ -23,13 +23,13 @@ __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w <<
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 // Nearest bf16, ties to even; a NaN keeps its sign and gets the quiet bit (the reference's
-// rounding, x0ne-core/oracle/src/bf16.rs:11-20).
+// rounding, x0ne-core/oracle/src/bf16.rs:11-20). Branch-free: adding 0x7FFF plus the kept
+// part's lowest bit carries into the kept part exactly when the dropped half is above 0x8000,
+// or equal to it with that bit odd; a NaN's sum is discarded by the select.
 __device__ __forceinline__ bf16_t f2bf(float x) {
-    uint32_t b = __float_as_uint(x);
-    if (x != x) return (bf16_t)((b >> 16) | 0x0040u);
-    uint32_t lo = b & 0xFFFFu, hi = b >> 16;
-    uint32_t up = (lo > 0x8000u) | ((lo == 0x8000u) & (hi & 1u));
-    return (bf16_t)(hi + up);
+    const uint32_t b = __float_as_uint(x);
+    const uint32_t rounded = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+    return (bf16_t)(x != x ? ((b >> 16) | 0x0040u) : rounded);
 }
 
 __device__ __forceinline__ float bf_round(float x) { return bf2f(f2bf(x)); }

@@ -288,7 +288,7 @@ struct x0ne_engine {
     bool has_lm_head = false;
     std::vector<LayerW> L;
     // buffers
-    x0ne_slice inv_freq{}, page_table{}, kv{}, prompt{}, tokens{}, pos{}, residual{}, delta{}, qkv{}, q{}, attn{},
+    x0ne_slice inv_freq{}, rope_cs{}, page_table{}, kv{}, prompt{}, tokens{}, pos{}, residual{}, delta{}, qkv{}, q{}, attn{},
         act{}, logits{}, head_partial{}, head_counter{}, attn_state{}, attn_counter{};
     std::vector<uint32_t> page_of;
     x0ne_split_plan split{};
@@ -362,6 +362,7 @@ x0ne_status plan(x0ne_engine* e) {
     if (e->has_lm_head) X0NE_TRY(al("lm_head", c.vocab * c.hidden * 2, W, &e->lm_head));
     // Engine tables, not client data: the host's f32 inverse frequencies and the page order.
     X0NE_TRY(al("inv_freq", c.head_dim / 2 * 4, W, &e->inv_freq));
+    X0NE_TRY(al("rope_cs", e->max_ctx * (c.head_dim / 2) * 16, W, &e->rope_cs));
     X0NE_TRY(al("page_table", e->pages * 4, W, &e->page_table));
     // Client data.
     X0NE_TRY(al("kv_cache", 2 * c.layers * e->plane_bytes(), CD, &e->kv));
@@ -476,8 +477,9 @@ x0ne_status launch_attention(x0ne_engine* e, uint64_t l) {
     if (e->split.grouped) {
         const LayerW& w = e->L[l];
         return attention_rope_split(e->gpu, e->split, e->d(e->qkv), e->d(w.q_norm), e->d(w.k_norm),
-                                    e->d(e->inv_freq), e->plane(l, 0), e->plane(l, 1), e->d(e->page_table),
-                                    e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn), e->d(e->pos),
+                                    e->d(e->inv_freq), e->d(e->rope_cs), e->plane(l, 0), e->plane(l, 1),
+                                    e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn),
+                                    e->d(e->pos),
                                     (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, scale,
                                     (float)c.eps);
     }
@@ -748,8 +750,23 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     return X0NE_OK;
 }
 
+// The fused decode attention's RoPE table: cos and sin per position below max_ctx and pair, from
+// inv_freq, on the device (the functions the rotation kernels call, so the same bits).
+x0ne_status fill_rope_table(x0ne_engine* e) {
+    const void* inv = e->d(e->inv_freq);
+    void* cs = e->d(e->rope_cs);
+    uint32_t positions = (uint32_t)e->max_ctx;
+    void* args[] = {(void*)&inv, (void*)&cs, (void*)&positions};
+    const uint32_t blocks = (uint32_t)((e->max_ctx * (e->c.head_dim / 2) + 255) / 256);
+    X0NE_HIP(x0ne_launch((const void*)&x0ne_rope_table_f64, dim3(blocks), dim3(256), args, 0, e->gpu->stream),
+             "rope table");
+    X0NE_HIP(hipStreamSynchronize(e->gpu->stream), "rope table");
+    return X0NE_OK;
+}
+
 x0ne_status build_end(x0ne_engine* e) {
     X0NE_TRY(x0ne_arena_scrub(e->arena, nullptr));
+    X0NE_TRY(fill_rope_table(e));
     X0NE_HIP(hipHostMalloc((void**)&e->ring, RING * 4, hipHostMallocDefault), "pinned ring");
     X0NE_HIP(hipHostMalloc((void**)&e->host_logits, e->c.vocab * 4, hipHostMallocDefault), "pinned logits");
     X0NE_HIP(hipHostMalloc((void**)&e->host_token, 4, hipHostMallocDefault), "pinned token");

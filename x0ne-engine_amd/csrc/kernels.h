@@ -32,9 +32,10 @@ __global__ void x0ne_attention_decode_split_bf16(const bf16_t* q, const bf16_t* 
         uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, \
         uint32_t splits, float scale);                                                                            \
     __global__ void x0ne_attention_rope_decode_g##G##_bf16(                                                     \
-        const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq, bf16_t* k_cache,  \
-        bf16_t* v_cache, const uint32_t* pages, float* state, uint32_t* counter, bf16_t* out, const uint32_t* pos, \
-        uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale, float eps);     \
+        const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq,                    \
+        const double* rope_cs, bf16_t* k_cache, bf16_t* v_cache, const uint32_t* pages, float* state,           \
+        uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads,                \
+        uint32_t max_ctx, uint32_t splits, float scale, float eps);                                              \
     __global__ void x0ne_attention_rope_decode_exact_g##G##_bf16(                                               \
         const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq, bf16_t* k_cache,  \
         bf16_t* v_cache, const uint32_t* pages, bf16_t* out, const uint32_t* pos, uint32_t q_heads,              \
@@ -49,6 +50,7 @@ __global__ void x0ne_attention_merge_bf16(const float* state, bf16_t* out, const
 __global__ void x0ne_attention_prefill_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
                                             const uint32_t* pages, bf16_t* out, const uint32_t* pos0, uint32_t rows,
                                             uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
+__global__ void x0ne_rope_table_f64(const float* inv_freq, double* cs, uint32_t positions);
 __global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
 __global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
 __global__ void x0ne_advance_u32(uint32_t* pos);

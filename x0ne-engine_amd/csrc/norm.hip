@@ -98,6 +98,20 @@ extern "C" __global__ void __launch_bounds__(64)
     v_cache[vat + (i + HALF) * X0NE_PAGE] = vs[i + HALF];
 }
 
+// The RoPE table of the fused decode attention: cs[2 (p 64 + i)] = cos and cs[2 (p 64 + i) + 1] =
+// sin of the f64 angle (double)((float)p * inv_freq[i]), positions p < positions: the values the
+// rotation above computes, so a kernel that reads them rotates to the same bits. grid
+// (ceil(positions * 64 / 256)), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_rope_table_f64(const float* __restrict__ inv_freq, double* __restrict__ cs, uint32_t positions) {
+    const uint64_t k = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (k >= (uint64_t)positions * (X0NE_HEAD_DIM / 2)) return;
+    const uint32_t p = (uint32_t)(k / (X0NE_HEAD_DIM / 2)), i = (uint32_t)(k % (X0NE_HEAD_DIM / 2));
+    const double angle = (double)((float)p * inv_freq[i]);
+    cs[2 * k] = cos(angle);
+    cs[2 * k + 1] = sin(angle);
+}
+
 // SwiGLU on the packed [gate; up] row: out[i] = g / (1 + e^-g) * u, in f64 (swiglu.cu:5-11;
 // oracle/src/lib.rs:205-214). grid (ceil(inter / 256), rows), block 256.
 extern "C" __global__ void __launch_bounds__(256)

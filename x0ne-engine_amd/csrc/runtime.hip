@@ -374,7 +374,8 @@ x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_b
 }
 
 x0ne_status attention_rope_split(x0ne_gpu* g, const x0ne_split_plan& plan, const void* qkv, const void* q_norm,
-                                 const void* k_norm, const void* inv_freq, void* k, void* v, const void* pages,
+                                 const void* k_norm, const void* inv_freq, const void* rope_cs, void* k, void* v,
+                                 const void* pages,
                                  void* state, void* counter, void* out, const void* pos, uint32_t qh, uint32_t kvh,
                                  uint32_t max_ctx, float scale, float eps) {
     const uint32_t p = plan.splits;
@@ -383,10 +384,10 @@ x0ne_status attention_rope_split(x0ne_gpu* g, const x0ne_split_plan& plan, const
         return fail(X0NE_ERR_GPU, "fused attention needs a grouped plan of this geometry");
     const void* kern = rope_group_kernel(plan.group);
     if (!kern) return fail(X0NE_ERR_GPU, "fused attention: no kernel for this group size");
-    void* args[] = {(void*)&qkv,   (void*)&q_norm, (void*)&k_norm, (void*)&inv_freq, (void*)&k,
-                    (void*)&v,     (void*)&pages,  (void*)&state,  (void*)&counter,  (void*)&out,
-                    (void*)&pos,   (void*)&qh,     (void*)&kvh,    (void*)&max_ctx,  (void*)&p,
-                    (void*)&scale, (void*)&eps};
+    void* args[] = {(void*)&qkv,     (void*)&q_norm, (void*)&k_norm, (void*)&inv_freq, (void*)&rope_cs,
+                    (void*)&k,       (void*)&v,      (void*)&pages,  (void*)&state,    (void*)&counter,
+                    (void*)&out,     (void*)&pos,    (void*)&qh,     (void*)&kvh,      (void*)&max_ctx,
+                    (void*)&p,       (void*)&scale,  (void*)&eps};
     g->counts.launches++;
     X0NE_HIP(x0ne_launch(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "fused decode attention");
     return X0NE_OK;

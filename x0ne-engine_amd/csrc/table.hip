@@ -7,6 +7,7 @@ static const X0neKernel TABLE[] = {
     {"x0ne_probe_iota_u32", (const void*)&x0ne_probe_iota_u32, "pu", 256},
     {"x0ne_embedding_bf16", (const void*)&x0ne_embedding_bf16, "pppuu", 128},
     {"x0ne_add_rmsnorm_bf16", (const void*)&x0ne_add_rmsnorm_bf16, "ppppuf", 256},
+    {"x0ne_rope_table_f64", (const void*)&x0ne_rope_table_f64, "ppu", 256},
     {"x0ne_qk_norm_rope_kv_write_bf16", (const void*)&x0ne_qk_norm_rope_kv_write_bf16, "pppppppppuuuf", 64},
     {"x0ne_attention_decode_bf16", (const void*)&x0ne_attention_decode_bf16, "ppppppuuuf", 256},
     {"x0ne_attention_decode_split_bf16", (const void*)&x0ne_attention_decode_split_bf16, "pppppppuuuuf", 256},
@@ -14,10 +15,10 @@ static const X0neKernel TABLE[] = {
     {"x0ne_attention_decode_split_g2_bf16", (const void*)&x0ne_attention_decode_split_g2_bf16, "ppppppppuuuuf", 256},
     {"x0ne_attention_decode_split_g4_bf16", (const void*)&x0ne_attention_decode_split_g4_bf16, "ppppppppuuuuf", 256},
     {"x0ne_attention_decode_split_g8_bf16", (const void*)&x0ne_attention_decode_split_g8_bf16, "ppppppppuuuuf", 256},
-    {"x0ne_attention_rope_decode_g1_bf16", (const void*)&x0ne_attention_rope_decode_g1_bf16, "pppppppppppuuuuff", 256},
-    {"x0ne_attention_rope_decode_g2_bf16", (const void*)&x0ne_attention_rope_decode_g2_bf16, "pppppppppppuuuuff", 256},
-    {"x0ne_attention_rope_decode_g4_bf16", (const void*)&x0ne_attention_rope_decode_g4_bf16, "pppppppppppuuuuff", 256},
-    {"x0ne_attention_rope_decode_g8_bf16", (const void*)&x0ne_attention_rope_decode_g8_bf16, "pppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_g1_bf16", (const void*)&x0ne_attention_rope_decode_g1_bf16, "ppppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_g2_bf16", (const void*)&x0ne_attention_rope_decode_g2_bf16, "ppppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_g4_bf16", (const void*)&x0ne_attention_rope_decode_g4_bf16, "ppppppppppppuuuuff", 256},
+    {"x0ne_attention_rope_decode_g8_bf16", (const void*)&x0ne_attention_rope_decode_g8_bf16, "ppppppppppppuuuuff", 256},
     {"x0ne_attention_rope_decode_exact_g1_bf16", (const void*)&x0ne_attention_rope_decode_exact_g1_bf16, "pppppppppuuuf", 256},
     {"x0ne_attention_rope_decode_exact_g2_bf16", (const void*)&x0ne_attention_rope_decode_exact_g2_bf16, "pppppppppuuuf", 256},
     {"x0ne_attention_rope_decode_exact_g4_bf16", (const void*)&x0ne_attention_rope_decode_exact_g4_bf16, "pppppppppuuuf", 256},

@@ -224,6 +224,25 @@ class Kernels:
         return self._gemv(w, rows, cols, x, False)
 
     # -- attention (ops.rs:453-681) --
+    def _rope_table(self, inv_ptr: int, cs_ptr: int, positions: int, head_dim: int):
+        self.gpu.launch("x0ne_rope_table_f64", (positions * (head_dim // 2) + 255) // 256, 256,
+                        [Arg.ptr(inv_ptr), Arg.ptr(cs_ptr), Arg.u32(positions)])
+
+    def rope_table(self, head_dim: int, theta: float, positions: int) -> np.ndarray:
+        """The fused decode attention's RoPE table, [positions][head_dim / 2][cos, sin] in f64: the
+        cosine and sine of (double)((float)p * inv_freq[i]) (the angle of rope.cu:7-47)."""
+        if positions == 0:
+            raise FormatError("rope_table: no positions")
+        a = self._arena()
+        inv = a.alloc("inv_freq", head_dim // 2 * 4, Class.WEIGHTS)
+        cs = a.alloc("rope_cs", positions * (head_dim // 2) * 16, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(inv, 0, inv_freq(head_dim, theta))
+        self._rope_table(a.ptr(inv), a.ptr(cs), positions, head_dim)
+        self.gpu.sync()
+        raw = a.read(cs, 0, positions * (head_dim // 2) * 16)
+        return np.frombuffer(raw, np.float64).reshape(positions, head_dim // 2, 2).copy()
+
     def _kv_arena(self, q, k, v, ctx, h: Heads, page_of, pool, extra):
         pages = n_pages(ctx)
         page_of = list(range(pages)) if page_of is None else list(page_of)[:pages]
@@ -317,11 +336,12 @@ class Kernels:
         a, s = self._kv_arena(np.asarray(qkv, np.uint16), kf, vf, ctx, h, page_of, pool,
                               [("out", qd * 2), ("state", split_state_bytes(h.q_heads, plan.splits)),
                                ("counter", h.kv_heads * 4), ("q_norm", hd * 2), ("k_norm", hd * 2),
-                               ("inv_freq", hd // 2 * 4)])
+                               ("inv_freq", hd // 2 * 4), ("rope_cs", ctx * (hd // 2) * 16)])
         a.write(s["pos"], 0, np.array([ctx - 1], np.uint32))
         a.write(s["q_norm"], 0, np.asarray(q_norm, np.uint16))
         a.write(s["k_norm"], 0, np.asarray(k_norm, np.uint16))
         a.write(s["inv_freq"], 0, inv_freq(hd, theta))
+        self._rope_table(a.ptr(s["inv_freq"]), a.ptr(s["rope_cs"]), ctx, hd)
         counter = a.ptr(s["counter"]) if last_block else 0
         if exact:
             self.gpu.launch(f"x0ne_attention_rope_decode_exact_g{plan.group}_bf16", (h.kv_heads, 1), 256,
@@ -333,7 +353,8 @@ class Kernels:
         else:
             self.gpu.launch(f"x0ne_attention_rope_decode_g{plan.group}_bf16", (h.kv_heads, plan.splits), 256,
                             [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["q_norm"])), Arg.ptr(a.ptr(s["k_norm"])),
-                             Arg.ptr(a.ptr(s["inv_freq"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
+                             Arg.ptr(a.ptr(s["inv_freq"])), Arg.ptr(a.ptr(s["rope_cs"])), Arg.ptr(a.ptr(s["k"])),
+                             Arg.ptr(a.ptr(s["v"])),
                              Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["state"])), Arg.ptr(counter),
                              Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(h.q_heads),
                              Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.u32(plan.splits),
