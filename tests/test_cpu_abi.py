@@ -54,7 +54,7 @@ def test_the_python_mirror_binds_every_function_with_the_headers_arity():
 
 
 def kernel_declarations():
-    """Parameter kinds of each kernel in kernels.h, with the group macro expanded."""
+    """Parameter kinds of each kernel in kernels.h, with the declaration macros expanded."""
     text = open(KERNELS_H).read()
     kinds = {}
 
@@ -68,12 +68,19 @@ def kernel_declarations():
             return "u"
         raise AssertionError(f"parameter {p!r}")
 
-    macro = re.search(r"#define X0NE_DECLARE_SPLIT_GROUP\(G\)(.*?)\n(?!.*\\\n)X0NE_DECLARE", text, re.S)
-    body = macro.group(1).replace("\\\n", "\n")
-    groups = re.findall(r"^X0NE_DECLARE_SPLIT_GROUP\((\d+)\)", text, re.M)
-    expanded = "\n".join(body.replace("##G##", g) for g in groups)
-    plain = text.replace(macro.group(0), "X0NE_DECLARE")
-    for src in (plain, expanded):
+    # Each #define X0NE_DECLARE_NAME(params) with a continued body, expanded at its uses.
+    plain, expanded = text, []
+    for m in re.finditer(r"#define (X0NE_DECLARE_\w+)\(([^)]*)\)((?:.*\\\n)+.*\n)", text):
+        name, params = m.group(1), [q.strip() for q in m.group(2).split(",")]
+        body = m.group(3).replace("\\\n", "\n")
+        plain = plain.replace(m.group(0), "")
+        for use in re.finditer(r"^" + name + r"\(([^)]*)\)", text, re.M):
+            b = body
+            for q, v in zip(params, [x.strip() for x in use.group(1).split(",")]):
+                b = b.replace("##" + q + "##", v).replace("##" + q, v)
+            expanded.append(b)
+        assert re.search(r"^" + name + r"\(", text, re.M), f"{name} is never used"
+    for src in [plain] + expanded:
         for m in re.finditer(r"__global__ void (x0ne_\w+)\s*\(([^)]*)\)", src, re.S):
             kinds[m.group(1)] = "".join(kind(p) for p in m.group(2).split(","))
     return kinds

@@ -38,6 +38,25 @@ def test_probe_and_launch_checks(kernels):
     print("MEASURE", kernels.gpu.describe())
 
 
+def test_the_hardware_bf16_rounding_is_the_references_on_every_f32(kernels):
+    """The kernels round with v_cvt_pk_bf16_f32. On the device it is compared with the rounding
+    stated on the bits for all 2^32 f32 values; on the host, with the oracle's encoder
+    (bf16.rs:11-20), over ranges holding zeros, denormals, ties around 1, the largest finite
+    values, infinities and NaNs of both signs."""
+    step = 1 << 28
+    for base in range(0, 1 << 32, step):
+        differ, _ = kernels.probe_bf16_round(base, step)
+        assert differ == 0, f"{differ} values from {base:#010x} round differently"
+    for base in [0x00000000, 0x007F8000, 0x3F7F8000, 0x3F800000, 0x7F7F0000, 0x7FBF8000, 0x80000000, 0xFF7F0000,
+                 0xFFBF8000, 0xFFFF0000]:
+        n = 1 << 16
+        _, bits = kernels.probe_bf16_round(base, n, read=True)
+        vals = (np.arange(n, dtype=np.uint64) + base).astype(np.uint32).view(np.float32)
+        want = O.bf16_bits(vals)
+        bad = np.flatnonzero(bits != want)
+        assert bad.size == 0, f"{base + int(bad[0]):#010x}: {int(bits[bad[0]]):#06x} vs {int(want[bad[0]]):#06x}"
+
+
 def test_embedding_copies_the_row_bit_for_bit_and_zeroes_a_token_outside(kernels):
     rng = O.Rng(1)
     for hidden in [8, 16, 64, 1024, 4096]:

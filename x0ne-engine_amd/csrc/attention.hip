@@ -269,9 +269,8 @@ __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// Two finite values to bf16, nearest-even, in one word (v_cvt_pk_bf16_f32): the matrix-core
-// operands built from softmax weights, which are finite.
-__device__ __forceinline__ uint32_t pack_bf16_finite(float lo, float hi) {
+// Two values to bf16 (f2bf's rounding), in one word: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     const bf16x2 v = {(__bf16)lo, (__bf16)hi};
     return __builtin_bit_cast(uint32_t, v);
 }
@@ -497,10 +496,10 @@ __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewR
             uint32_t hw[4], lw[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                hw[j] = pack_bf16_finite(pv[2 * j], pv[2 * j + 1]);
+                hw[j] = pack_bf16(pv[2 * j], pv[2 * j + 1]);
                 lo[2 * j] = pv[2 * j] - bf_lo(hw[j]);  // exact
                 lo[2 * j + 1] = pv[2 * j + 1] - bf_hi(hw[j]);
-                lw[j] = pack_bf16_finite(lo[2 * j], lo[2 * j + 1]);
+                lw[j] = pack_bf16(lo[2 * j], lo[2 * j + 1]);
             }
             const uint4 ahi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
             const uint4 alo = make_uint4(lw[0], lw[1], lw[2], lw[3]);

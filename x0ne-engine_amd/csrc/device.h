@@ -22,15 +22,19 @@ __device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// Nearest bf16, ties to even; a NaN keeps its sign and gets the quiet bit (the reference's
-// rounding, x0ne-core/oracle/src/bf16.rs:11-20). Branch-free: adding 0x7FFF plus the kept
-// part's lowest bit carries into the kept part exactly when the dropped half is above 0x8000,
-// or equal to it with that bit odd; a NaN's sum is discarded by the select.
-__device__ __forceinline__ bf16_t f2bf(float x) {
+// Nearest bf16, ties to even; a NaN keeps its sign and the high bits of its payload and gets the
+// quiet bit (the reference's rounding, x0ne-core/oracle/src/bf16.rs:11-20), stated on the bits:
+// adding 0x7FFF plus the kept part's lowest bit carries into the kept part exactly when the
+// dropped half is above 0x8000, or equal to it with that bit odd.
+__device__ __forceinline__ bf16_t f2bf_bits(float x) {
     const uint32_t b = __float_as_uint(x);
     const uint32_t rounded = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
     return (bf16_t)(x != x ? ((b >> 16) | 0x0040u) : rounded);
 }
+
+// The same rounding by the hardware (v_cvt_pk_bf16_f32, nearest-even mode, f32 denormals kept):
+// x0ne_probe_bf16_round checks it against f2bf_bits on all 2^32 inputs.
+__device__ __forceinline__ bf16_t f2bf(float x) { return __builtin_bit_cast(bf16_t, (__bf16)x); }
 
 __device__ __forceinline__ float bf_round(float x) { return bf2f(f2bf(x)); }
 
@@ -54,8 +58,6 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Sum over a block of `blockDim.x` threads (a multiple of 64, at most 1024); every thread gets
-// it. `sh` holds 16 doubles. Wave sums, then the wave sums in wave order.
 // A barrier for data exchanged through LDS only: this wavefront's LDS operations are complete,
 // then all wavefronts meet. Unlike __syncthreads() it does not wait for outstanding global loads
 // (the workgroup fence does), so loads requested before it stay in flight across it.
@@ -77,6 +79,8 @@ __device__ __forceinline__ double block_sum_lds(double v, double* sh) {
     return t;
 }
 
+// Sum over a block of `blockDim.x` threads (a multiple of 64, at most 1024); every thread gets
+// it. `sh` holds 16 doubles. Wave sums, then the wave sums in wave order.
 __device__ __forceinline__ double block_sum_d(double v, double* sh) {
     v = wave_sum_d(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;

@@ -23,11 +23,6 @@ struct Counts {
     std::atomic<uint64_t> launches{0}, graph_launches{0}, gemms{0}, htod{0}, dtoh{0}, memsets{0}, syncs{0};
 };
 
-// The exact mode's decode attention: the fused work of attention_rope_split with f64 sums, one
-// block per kv head over the whole context, for group sizes 1, 2, 4 and 8.
-x0ne_status attention_rope_exact(x0ne_gpu* g, const void* qkv, const void* q_norm, const void* k_norm,
-                                 const void* inv_freq, void* k, void* v, const void* pages, void* out, const void* pos,
-                                 uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float eps);
 }  // namespace x0ne
 
 #define X0NE_HIP(call, what)                                        \

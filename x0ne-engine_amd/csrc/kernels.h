@@ -11,6 +11,7 @@ typedef uint16_t bf16_t;
 
 extern "C" {
 __global__ void x0ne_probe_iota_u32(uint32_t* out, uint32_t n);
+__global__ void x0ne_probe_bf16_round(uint32_t base, uint32_t n, bf16_t* out, uint32_t* counter);
 __global__ void x0ne_embedding_bf16(const bf16_t* table, const uint32_t* tokens, bf16_t* out, uint32_t hidden,
                                     uint32_t vocab);
 __global__ void x0ne_add_rmsnorm_bf16(float* residual, const bf16_t* x, const bf16_t* w, bf16_t* out,

@@ -12,6 +12,21 @@ extern "C" __global__ void __launch_bounds__(256) x0ne_probe_iota_u32(uint32_t* 
     if (i < n) out[i] = i;
 }
 
+// Probe of the bf16 rounding: for the f32 values whose bits are base + i, i < n, out[i] = f2bf
+// (when out is given) and counter[0] += how many differ from f2bf_bits. Any grid of 256-thread
+// blocks (grid-stride).
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_probe_bf16_round(uint32_t base, uint32_t n, bf16_t* __restrict__ out, uint32_t* __restrict__ counter) {
+    uint32_t differ = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const float x = __uint_as_float(base + (uint32_t)i);
+        const bf16_t h = f2bf(x);
+        differ += h != f2bf_bits(x);
+        if (out) out[i] = h;
+    }
+    if (differ) atomicAdd(counter, differ);
+}
+
 // out[r] = table[tokens[r]] (embedding.cu:5-17): grid (rows), block 128, hidden % 8 == 0,
 // 16-byte copies. An id >= vocab writes a zero row.
 extern "C" __global__ void __launch_bounds__(128)

@@ -224,6 +224,23 @@ class Kernels:
         return self._gemv(w, rows, cols, x, False)
 
     # -- attention (ops.rs:453-681) --
+    def probe_bf16_round(self, base: int, n: int, read: bool = False):
+        """The device's bf16 rounding of the f32 values whose bits are base .. base + n - 1: how many
+        differ from the rounding stated on the bits, and (read) the rounded bits."""
+        if n == 0 or base + n > 1 << 32:
+            raise FormatError("probe_bf16_round: range")
+        a = self._arena()
+        cnt = a.alloc("counter", 4, Class.CLIENT_DATA)
+        out = a.alloc("out", n * 2, Class.CLIENT_DATA) if read else None
+        self._freeze(a)
+        a.scrub_client_data()
+        self.gpu.launch("x0ne_probe_bf16_round", min((n + 255) // 256, 8192), 256,
+                        [Arg.u32(base), Arg.u32(n), Arg.ptr(a.ptr(out) if read else 0), Arg.ptr(a.ptr(cnt))])
+        self.gpu.sync()
+        differ = int(np.frombuffer(a.read(cnt, 0, 4), np.uint32)[0])
+        bits = np.frombuffer(a.read(out, 0, n * 2), np.uint16).copy() if read else None
+        return differ, bits
+
     def _rope_table(self, inv_ptr: int, cs_ptr: int, positions: int, head_dim: int):
         self.gpu.launch("x0ne_rope_table_f64", (positions * (head_dim // 2) + 255) // 256, 256,
                         [Arg.ptr(inv_ptr), Arg.ptr(cs_ptr), Arg.u32(positions)])
