@@ -97,7 +97,9 @@ x0ne_status x0ne_gpu_launch(x0ne_gpu* g, const char* name, uint32_t gx, uint32_t
 
 /* Gpu::gemm (gpu.rs:1098-1149), the projection the reference hands cuBLAS: Y[n][rows] =
    X[n][cols] W^T, W [rows][cols] row-major bf16, X bf16, f32 accumulation; out_f32 = 0 gives
-   bf16 Y, 1 f32 Y. Device addresses. Hand-written bandwidth-bound GEMV, one launch per row of X. */
+   bf16 Y, 1 f32 Y. Device addresses. From 4 rows of X on (cols a multiple of 8, W and X each
+   below 4 GiB) one hand-written matrix-core GEMM launch (x0ne_gemm_bf16); below that the
+   bandwidth-bound GEMV, one launch per row of X. */
 x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n, uint64_t y,
                           int out_f32);
 

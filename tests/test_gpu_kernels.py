@@ -204,6 +204,30 @@ def test_gemv_is_the_oracle_on_random_shapes(kernels, seed):
     assert (b == bf16_bits(f)).all(), what
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
+    """Gpu::gemm over many rows (the matrix-core GEMM from 4 rows on): every row of Y is the
+    oracle's GEMV of that row of X within the GEMV tolerance (gpu_kernels.rs:331-393), at tile
+    edges of both sides and K tails; the bf16 output is the f32 output rounded."""
+    rng = O.Rng(700 + seed)
+    n = rng.pick([4, 5, 31, 128, 129, 257])
+    rows = rng.pick([1, 15, 128, 129, 384, 1000])
+    cols = rng.pick([8, 64, 72, 1000, 4096])
+    scale = rng.pick([1e-2, 1.0, 50.0])
+    w = bf16s_with_edges(rng, rows * cols, scale)
+    x = bf16s_with_edges(rng, n * cols, scale)
+    f = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True)
+    b = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, False)
+    what = f"gemm seed {seed} {n}x{rows}x{cols}"
+    for r in range(n):
+        xr = x[r * cols:(r + 1) * cols]
+        want = O.gemv(w, rows, cols, xr)
+        mag = O.gemv_magnitude(w, rows, cols, xr)
+        assert_gemv(f"{what} row {r} f32", f[r], want, mag, False)
+        assert_gemv(f"{what} row {r} bf16", bf16_vals(b[r]), want, mag, True)
+    assert (b == bf16_bits(f).reshape(b.shape)).all(), what
+
+
 def test_gemv_carries_non_finite_values_to_the_rows_that_read_them(kernels):
     rows, cols = 16, 64
     rng = O.Rng(399)

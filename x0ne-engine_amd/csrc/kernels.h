@@ -56,6 +56,8 @@ __global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t in
 __global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
 __global__ void x0ne_advance_u32(uint32_t* pos);
 __global__ void x0ne_feed_u32(const uint32_t* ids, uint32_t i, uint32_t* tokens, uint32_t* pos);
+__global__ void x0ne_gemm_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, uint32_t n,
+                               uint32_t out_f32);
 __global__ void x0ne_gemv_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_f32(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_any(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols,

@@ -242,6 +242,11 @@ extern "C" x0ne_status x0ne_gpu_launch(x0ne_gpu* g, const char* name, uint32_t g
 }
 
 // Gpu::gemm (gpu.rs:1098-1149) at n = 1 per launch: the bandwidth-bound GEMV of gemv.hip.
+// From this many rows of X on, x0ne_gpu_gemv is one matrix-core GEMM (gemm.hip) rather than a
+// GEMV per row; its buffer offsets are 32-bit.
+static constexpr uint64_t GEMM_MIN_ROWS = 4;
+static constexpr uint64_t GEMM_MAX_BYTES = 0xFFFFFFF0ull;
+
 extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n,
                                      uint64_t y, int out_f32) {
     if (!g) return fail(X0NE_ERR_GPU, "no device");
@@ -249,6 +254,20 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
         return fail(X0NE_ERR_FORMAT, "gemv: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
                                          std::to_string(n));
     const uint64_t ob = out_f32 ? 4 : 2;
+    // Several rows: one matrix-core GEMM launch, the weights read once.
+    if (n >= GEMM_MIN_ROWS && cols % 8 == 0 && n <= UINT32_MAX && rows * cols * 2 <= GEMM_MAX_BYTES &&
+        n * cols * 2 <= GEMM_MAX_BYTES) {
+        g->counts.gemms++;
+        g->counts.launches++;
+        const bf16_t* wp = (const bf16_t*)w;
+        const bf16_t* xp = (const bf16_t*)x;
+        void* yp = (void*)y;
+        uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, f32 = out_f32 ? 1u : 0u;
+        void* args[] = {(void*)&wp, (void*)&xp, (void*)&yp, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&f32};
+        const uint32_t tiles = (uint32_t)(((rows + 127) / 128) * ((n + 127) / 128));
+        X0NE_HIP(x0ne_launch((const void*)&x0ne_gemm_bf16, dim3(tiles), dim3(256), args, 0, g->stream), "gemm");
+        return X0NE_OK;
+    }
     for (uint64_t r = 0; r < n; ++r) {
         const uint16_t* wp = (const uint16_t*)w;
         const uint16_t* xp = (const uint16_t*)(x + r * cols * 2);

@@ -5,6 +5,7 @@
 
 static const X0neKernel TABLE[] = {
     {"x0ne_probe_iota_u32", (const void*)&x0ne_probe_iota_u32, "pu", 256},
+    {"x0ne_gemm_bf16", (const void*)&x0ne_gemm_bf16, "pppuuuu", 256},
     {"x0ne_probe_bf16_round", (const void*)&x0ne_probe_bf16_round, "uupp", 256},
     {"x0ne_embedding_bf16", (const void*)&x0ne_embedding_bf16, "pppuu", 128},
     {"x0ne_add_rmsnorm_bf16", (const void*)&x0ne_add_rmsnorm_bf16, "ppppuf", 256},

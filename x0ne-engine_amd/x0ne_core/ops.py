@@ -217,6 +217,23 @@ class Kernels:
         self.gpu.sync()
         return a.read_array(ys, 0, rows, np.float32 if out_f32 else np.uint16)
 
+    def gemm(self, w, rows, cols, x, n, out_f32) -> np.ndarray:
+        """Gpu::gemm over n rows of X (gpu.rs:1098-1149): Y[n][rows] = X[n][cols] W^T, the
+        matrix-core GEMM from 4 rows on; returns Y (f32, or bf16 bits)."""
+        if rows == 0 or cols == 0 or n == 0 or w.size != rows * cols or x.size != n * cols:
+            raise FormatError(f"gemm: W {w.size} for {rows}x{cols}, X {x.size} for {n} rows")
+        ob = 4 if out_f32 else 2
+        a = self._arena()
+        ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
+        xs = a.alloc("x", x.size * 2, Class.CLIENT_DATA)
+        ys = a.alloc("y", n * rows * ob, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ws, 0, w.astype(np.uint16))
+        a.write(xs, 0, x.astype(np.uint16))
+        self.gpu.gemv(a.ptr(ws), rows, cols, a.ptr(xs), n, a.ptr(ys), out_f32)
+        self.gpu.sync()
+        return a.read_array(ys, 0, n * rows, np.float32 if out_f32 else np.uint16).reshape(n, rows)
+
     def gemv_f32_out(self, w, rows, cols, x) -> np.ndarray:
         return self._gemv(w, rows, cols, x, True)
 
