@@ -178,12 +178,15 @@ typedef struct x0ne_greedy x0ne_greedy;
      and decode attention computes scores, softmax and sums in f64 with the f64 scale
      1/sqrt(128) (one block per kv head, no split), so every rounding point of the step is the
      f64 oracle's; 1, 2, 4 or 8 q heads per kv head (X0NE_ERR_NOT_IMPLEMENTED otherwise).
-     0, the default, is the fp32-accumulating decode path. */
+     0, the default, is the fp32-accumulating decode path.
+   - prefill_chunk: prompt rows per prefill pass (engine.rs:67, PREFILL_CHUNK); 0 takes
+     min(2048, max_ctx). A pass runs every layer over its rows with matrix-core GEMMs and the
+     causal prefill attention; the exact mode feeds a prompt one decode step per token. */
 typedef struct {
     uint64_t max_ctx;
     uint64_t page_seed;
     uint32_t f64_sums;
-    uint32_t reserved;
+    uint32_t prefill_chunk;
 } x0ne_engine_options;
 
 /* Engine::load_from (engine.rs:301-309) over safetensors files already in memory (the

@@ -71,11 +71,41 @@ def test_every_route_gives_the_oracle_logits_at_every_position(name, make):
             for p in positions:
                 assert_logits(f"{name} {mode.name} {route.name} pos {p}", got[p], want[p])
             assert e.client_data_is_zero() and e.host_buffers_are_zero()
+    # Graph and eager replay the same decode launches: the same bits (gpu_engine.rs:155-158). The
+    # prefill passes (GEMMs over many rows) agree with them within the model tolerance.
     base = rows[(DecodeMode.GRAPH, Route.DECODE)]
-    for key, got in rows.items():
-        for p in positions:
-            assert (got[p].view(np.uint32) == base[p].view(np.uint32)).all(), f"{name} {key} pos {p}: graph = eager"
+    for p in positions:
+        eager = rows[(DecodeMode.EAGER, Route.DECODE)][p]
+        assert (eager.view(np.uint32) == base[p].view(np.uint32)).all(), f"{name} pos {p}: graph = eager"
+        for mode in [DecodeMode.GRAPH, DecodeMode.EAGER]:
+            assert_logits(f"{name} prefill against decode pos {p}", rows[(mode, Route.PREFILL)][p], base[p])
+        assert (rows[(DecodeMode.GRAPH, Route.PREFILL)][p].view(np.uint32) ==
+                rows[(DecodeMode.EAGER, Route.PREFILL)][p].view(np.uint32)).all(), f"{name} pos {p}: prefill twice"
     print(f"MEASURE {name}: {e.describe()}")
+
+
+@pytest.mark.parametrize("chunk", [1 << 30, 16, 7])
+def test_prefill_passes_across_chunk_boundaries_give_the_oracle_logits(chunk):
+    """A prompt cut in passes of `chunk` rows (gpu_engine.rs:229-302): the logits at and around
+    every boundary are the oracle's, and the first pass's rows equal those of that pass alone."""
+    from x0ne_core import Engine, EngineOptions, Route
+    f = Fixture(wide(), 6)
+    e = Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
+                         EngineOptions(max_ctx=96, page_seed=5, prefill_chunk=min(chunk, 96)))
+    c = min(chunk, 96)
+    assert f"prefill passes of {c} rows" in e.describe(), e.describe()
+    ids = f.tokens(14, 50)
+    want = f.model.logits(ids)
+    keep = sorted(set(p for b in range(0, 50, c) for p in (b - 1, b, b + 1) if 0 <= p < 50) | {0, 49})
+    got = e.logits_at(ids, keep, Route.PREFILL)
+    for row, p in zip(got, keep):
+        assert_logits(f"chunk {c} position {p}", row, want[p])
+    first = [p for p in keep if p < min(c, 50)]
+    alone = e.logits_at(ids[:min(c, 50)], first, Route.PREFILL)
+    for row, one, p in zip(got, alone, first):
+        assert (row.view(np.uint32) == one.view(np.uint32)).all(), f"chunk {c} position {p}: the first pass alone"
+    g = e.greedy(ids[:45], 6)
+    assert g.size == 6 and e.client_data_is_zero()
 
 
 def test_the_same_request_twice_gives_the_same_bits():

@@ -383,29 +383,33 @@ def test_decode_attention_on_one_key_a_dominant_key_and_equal_keys(kernels):
         kernels.attention_decode(bf16_bits(q), bf16_bits(kk), bf16_bits(v), 301, h)
 
 
-@pytest.mark.parametrize("qh,kvh", [(2, 1), (4, 2), (16, 8)])
+@pytest.mark.parametrize("qh,kvh", [(2, 1), (4, 2), (16, 8), (32, 8), (8, 8), (16, 2)])
 def test_prefill_attention_is_the_oracle_whole_and_from_a_chunk_boundary(kernels, qh, kvh):
+    """Both prefill kernels (per q head and row on the vector units; the matrix-core kernel per
+    group of rows and heads), whole and from a chunk boundary, against the oracle's causal rows."""
     h = H(qh, kvh)
     rng = O.Rng(500 + qh)
-    for t in [1, 2, 63, 64, 65, 511, 513, 1025]:
+    for t in [1, 2, 15, 16, 17, 63, 64, 65, 511, 513, 1025]:
         q = rng.bf16s(t * h.q_dim, 0.3 * np.sqrt(128))
         k = rng.bf16s(t * h.kv_dim, 0.3 * np.sqrt(128))
         v = bf16s_with_edges(rng, t * h.kv_dim, 4.0)
         atol = ATTENTION_ATOL_OF_VMAX * max_abs(v)
         rows = sorted(set([0, t - 1, t // 2, rng.below(t)]))
         want = O.attention_rows(q, k, v, 0, qh, kvh, 128, rows)
-        got = kernels.attention_prefill_rows(bf16_bits(q), bf16_bits(k), bf16_bits(v), t, h, rows)
-        for r, g, w in zip(rows, got, want):
-            assert_close(f"prefill {qh}/{kvh} t {t} row {r}", bf16_vals(g), w, atol, 0.0)
+        for grouped in [False, True]:
+            got = kernels.attention_prefill_rows(bf16_bits(q), bf16_bits(k), bf16_bits(v), t, h, rows, grouped=grouped)
+            for r, g, w in zip(rows, got, want):
+                assert_close(f"prefill {qh}/{kvh} t {t} row {r} grouped {grouped}", bf16_vals(g), w, atol, 0.0)
         for pos0 in sorted(set([0, 1, t // 2, t - 1])):
             if pos0 >= t:
                 continue
             tail = list(range(0, t - pos0, max(1, (t - pos0) // 5)))
-            got = kernels.attention_prefill_at(bf16_bits(q[pos0 * h.q_dim:]), bf16_bits(k), bf16_bits(v), t, pos0,
-                                               h, tail)
             want = O.attention_rows(q[pos0 * h.q_dim:], k, v, pos0, qh, kvh, 128, tail)
-            for r, g, w in zip(tail, got, want):
-                assert_close(f"prefill at {pos0} t {t} row {r}", bf16_vals(g), w, atol, 0.0)
+            for grouped in [False, True]:
+                got = kernels.attention_prefill_at(bf16_bits(q[pos0 * h.q_dim:]), bf16_bits(k), bf16_bits(v), t,
+                                                   pos0, h, tail, grouped=grouped)
+                for r, g, w in zip(tail, got, want):
+                    assert_close(f"prefill at {pos0} t {t} row {r} grouped {grouped}", bf16_vals(g), w, atol, 0.0)
 
 
 @pytest.mark.parametrize("seed", range(20))

@@ -309,7 +309,10 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // offsets (a plane below 4 GiB - 16 bytes); only OFF_NONE falls outside their resources.
 // prologue(qb) runs once the first tile's loads are issued and fills qb[s], the B operand of Q^T
 // for step s (every wavefront of the block calls it: it may hold a barrier). fx names the key
-// whose K and V rows come from LDS rather than from the loads. Leaves m (running max) and l (sum)
+// whose K and V rows come from LDS rather than from the loads. ctx bounds the keys the
+// wavefront reads (ctx rows exist in the cache); ctx_col, at most ctx, those its lane's column
+// attends (a causal prefill row's own position + 1; the decode query's is ctx). The first tile
+// a wavefront takes holds a key below every column's ctx_col. Leaves m (running max) and l (sum)
 // of head l % 16 in lane l, and o[nb][i] = O[head 4 (l / 16) + i][dim 16 nb + l % 16].
 //
 // The K and V rows of position pos as the block that writes them holds them in LDS: the
@@ -323,8 +326,8 @@ struct NewRow {
 template <class Prologue>
 __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewRow& fx, const bf16_t* __restrict__ kc,
                                                  const bf16_t* __restrict__ vc, const uint32_t* __restrict__ pages, uint32_t kh, uint32_t kv_heads,
-                                                 uint32_t ctx, uint32_t t0, uint32_t tstep, uint32_t t_end,
-                                                 float scale, float& m_out, float& l_out, f32x4 o[8]) {
+                                                 uint32_t ctx, uint32_t ctx_col, uint32_t t0, uint32_t tstep,
+                                                 uint32_t t_end, float scale, float& m_out, float& l_out, f32x4 o[8]) {
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, q4 = lane >> 4;
     const uint32_t ntiles = min(t_end, (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE);  // this wavefront's end
     const auto kr = plane_rsrc(kc, OFF_NONE), vr = plane_rsrc(vc, OFF_NONE);
@@ -422,7 +425,7 @@ __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewR
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const uint32_t key = 32 * kp + 8 * q4 + 4 * h + i;
-                    sc[kp][h][i] = base + key < ctx ? sacc[kp][h][i] * scale2 : -INFINITY;
+                    sc[kp][h][i] = base + key < ctx_col ? sacc[kp][h][i] * scale2 : -INFINITY;
                     mx = fmaxf(mx, sc[kp][h][i]);
                 }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -838,7 +841,7 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
     };
     float mw, lw;
     f32x4 ow[8];
-    attend_wave_mfma(prologue, fx, a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, t_begin, BLOCK_TILES, t_end,
+    attend_wave_mfma(prologue, fx, a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, ctx, t_begin, BLOCK_TILES, t_end,
                      a.scale, mw, lw, ow);
     {
         const uint32_t n = lane & 15, q4 = lane >> 4;
@@ -884,6 +887,70 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
     __syncthreads();
     if (t == 0) a.counter[kh] = 0;  // ready for the next step
 }
+
+// Causal prefill on the matrix cores, for G q heads per kv head: rows r of q ([rows][q_heads][128]
+// bf16) at positions pos0 + r, over the cache (which already holds their keys). Wavefront w of
+// block (kh, y) takes the R = 16 / G rows 4 R y + R w .. and the G q heads of kv head kh: the 16
+// columns of its products (column c: row c / G, head c % G), each over keys 0 .. min(pos0 + row,
+// max_ctx - 1), in one pass over the tiles up to its last row's; its output goes straight to
+// out ([rows][q_heads][128]). The wavefronts of a block do not wait for each other.
+template <int G>
+__device__ __forceinline__ void prefill_wave(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
+                                             const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
+                                             bf16_t* __restrict__ out, uint32_t p0, uint32_t rows, uint32_t q_heads,
+                                             uint32_t kv_heads, uint32_t max_ctx, float scale) {
+    constexpr uint32_t R = 16 / G;
+    const uint32_t kh = blockIdx.x, lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t r0 = (4 * blockIdx.y + wave) * R;  // the wavefront's first row
+    if (kh >= kv_heads || q_heads != G * kv_heads || r0 >= rows || max_ctx == 0) return;  // wavefront-uniform
+    const uint32_t n = lane & 15, q4 = lane >> 4;
+    const uint32_t r = r0 + n / G, h = kh * G + n % G;
+    const bool col = r < rows;
+    const uint32_t ctx_col = col ? min(p0 + r + 1, max_ctx) : 1u;
+    const uint32_t ctx = min(p0 + min(r0 + R, rows), max_ctx);  // through the wavefront's last row
+    const bf16_t* qr = q + ((size_t)(col ? r : 0) * q_heads + h) * X0NE_HEAD_DIM + 8 * q4;
+    auto prologue = [&](uint4 qb[4]) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+            qb[st] = col ? *reinterpret_cast<const uint4*>(qr + 32 * st) : make_uint4(0, 0, 0, 0);
+    };
+    const NewRow none = {~0u, 0, nullptr, nullptr};
+    float mw, lw;
+    f32x4 ow[8];
+    attend_wave_mfma(prologue, none, k_cache, v_cache, pages, kh, kv_heads, ctx, ctx_col, 0, 1, ~0u, scale, mw, lw, ow);
+    // ow[nb][i] = O[column 4 q4 + i][dim 16 nb + n]; lane c < 16 holds column c's sum.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t c = 4 * q4 + i;
+        const float l = __shfl(lw, (int)c, 64);
+        const uint32_t rc = r0 + c / G;
+        if (rc < rows) {
+            bf16_t* o = out + ((size_t)rc * q_heads + kh * G + c % G) * X0NE_HEAD_DIM;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) o[16 * nb + n] = f2bf(ow[nb][i] / l);
+        }
+    }
+}
+
+}  // namespace
+
+// x0ne_attention_prefill_g{G}_bf16: the causal prefill of x0ne_attention_prefill_bf16 (same
+// arguments and semantics) on the matrix cores for G q heads per kv head; grid (kv_heads,
+// ceil(rows / (64 / G))), block 256.
+#define X0NE_PREFILL_GROUP(G)                                                                                      \
+    extern "C" __global__ void __launch_bounds__(256) x0ne_attention_prefill_g##G##_bf16(                          \
+        const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
+        const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos0,          \
+        uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale) {                       \
+        prefill_wave<G>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx, scale);       \
+    }
+X0NE_PREFILL_GROUP(1)
+X0NE_PREFILL_GROUP(2)
+X0NE_PREFILL_GROUP(4)
+X0NE_PREFILL_GROUP(8)
+
+namespace {
 
 // One q head per block (group sizes without a grouped kernel, the per-head witness, prefill):
 // q head row q_row over kv head kh, ctx keys, slice y of P; the output directly when the block

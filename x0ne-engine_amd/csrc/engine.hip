@@ -31,6 +31,9 @@ using namespace x0ne;
 namespace {
 
 constexpr size_t RING = 16;  // engine.rs:70
+// Prompt rows per prefill pass by default (engine.rs:67 has 512; the matrix-core GEMM's tiles are
+// 128 rows, and 2048 rows keep it compute-bound).
+constexpr uint64_t PREFILL_CHUNK = 2048;
 
 struct Cfg {
     uint64_t hidden = 0, inter = 0, layers = 0, q_heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, max_pos = 0;
@@ -280,6 +283,7 @@ struct LayerW {
 struct x0ne_engine {
     Cfg c;
     uint64_t max_ctx = 0, pages = 0, page_seed = 0;
+    uint64_t chunk = 1;  // prompt rows per prefill pass; 1: one decode step per token
     int f64_sums = 0;
     x0ne_gpu* gpu = nullptr;
     x0ne_arena* arena = nullptr;
@@ -290,6 +294,8 @@ struct x0ne_engine {
     // buffers
     x0ne_slice inv_freq{}, rope_cs{}, page_table{}, kv{}, prompt{}, tokens{}, pos{}, residual{}, delta{}, qkv{}, q{}, attn{},
         act{}, logits{}, head_partial{}, head_counter{}, attn_state{}, attn_counter{};
+    // A prefill pass's rows: f32 residual, bf16 delta, normed x, qkv, q, attention, [gate; up], act.
+    x0ne_slice p_res{}, p_delta{}, p_x{}, p_qkv{}, p_q{}, p_attn{}, p_gu{}, p_act{};
     std::vector<uint32_t> page_of;
     x0ne_split_plan split{};
     uint32_t grid_qkv = 0, grid_o = 0, grid_gu = 0, grid_down = 0, grid_head = 0;
@@ -381,6 +387,17 @@ x0ne_status plan(x0ne_engine* e) {
     X0NE_TRY(al("attention_split_state", x0ne_split_state_bytes((uint32_t)c.q_heads, e->split.splits), CD,
                 &e->attn_state));
     X0NE_TRY(al("attention_split_counter", c.kv_heads * 4, CD, &e->attn_counter));
+    if (e->chunk > 1) {
+        const uint64_t n = e->chunk;
+        X0NE_TRY(al("prefill_residual", n * c.hidden * 4, CD, &e->p_res));
+        X0NE_TRY(al("prefill_delta", n * c.hidden * 2, CD, &e->p_delta));
+        X0NE_TRY(al("prefill_normed", n * c.hidden * 2, CD, &e->p_x));
+        X0NE_TRY(al("prefill_qkv", n * c.qkv_rows() * 2, CD, &e->p_qkv));
+        X0NE_TRY(al("prefill_q", n * c.q_dim() * 2, CD, &e->p_q));
+        X0NE_TRY(al("prefill_attn", n * c.q_dim() * 2, CD, &e->p_attn));
+        X0NE_TRY(al("prefill_gate_up", n * 2 * c.inter * 2, CD, &e->p_gu));
+        X0NE_TRY(al("prefill_act", n * c.inter * 2, CD, &e->p_act));
+    }
     return X0NE_OK;
 }
 
@@ -606,6 +623,143 @@ x0ne_status put_prompt(x0ne_engine* e, const uint32_t* ids, size_t n) {
     return x0ne_arena_write(e->arena, e->prompt, 0, ids, n * 4);
 }
 
+// tokens[0] = prompt[i], pos = i, without a step.
+x0ne_status set_position(x0ne_engine* e, uint64_t i) {
+    e->gpu->counts.launches++;
+    hipLaunchKernelGGL(x0ne_feed_u32, dim3(1), dim3(64), 0, e->gpu->stream, (const uint32_t*)e->d(e->prompt),
+                       (uint32_t)i, (uint32_t*)e->d(e->tokens), (uint32_t*)e->d(e->pos));
+    X0NE_HIP(hipGetLastError(), "position");
+    return X0NE_OK;
+}
+
+x0ne_status launch_rows(x0ne_engine* e, const void* fn, dim3 grid, dim3 block, void** args, const char* what) {
+    e->gpu->counts.launches++;
+    X0NE_HIP(x0ne_launch(fn, grid, block, args, 0, e->gpu->stream), what);
+    return X0NE_OK;
+}
+
+// Y[n][rows] = X[n][cols] W^T on arena slices (Gpu::gemm, bf16 out).
+x0ne_status gemm(x0ne_engine* e, x0ne_slice w, uint64_t rows, uint64_t cols, x0ne_slice x, uint64_t n, x0ne_slice y) {
+    return x0ne_gpu_gemv(e->gpu, (uint64_t)(uintptr_t)e->d(w), rows, cols, (uint64_t)(uintptr_t)e->d(x), n,
+                         (uint64_t)(uintptr_t)e->d(y), 0);
+}
+
+// Prompt rows pos0 .. pos0 + n - 1 through every layer (engine.rs:729-839 with n rows): the
+// embedding into delta and a zero residual, then per layer add + RMSNorm, the QKV GEMM, QK-norm
+// + RoPE with the K/V rows written at their positions, the causal attention (matrix-core kernel
+// for 1, 2, 4 or 8 q heads per kv head), the O GEMM, add + RMSNorm, the gate/up GEMM, SwiGLU,
+// the down GEMM. Leaves the rows' residual and last delta for the final norm.
+x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n) {
+    const Cfg& c = e->c;
+    if (e->chunk < 2 || n == 0 || n > e->chunk || pos0 + n > e->max_ctx)
+        return fail(X0NE_ERR_FORMAT, "prefill: " + std::to_string(n) + " rows at " + std::to_string(pos0));
+    X0NE_TRY(set_position(e, pos0));
+    const uint32_t rows = (uint32_t)n, h = (uint32_t)c.hidden, vocab = (uint32_t)c.vocab, inter = (uint32_t)c.inter;
+    const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads, max_ctx = (uint32_t)e->max_ctx;
+    const float eps = (float)c.eps, scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+    {
+        const void* table = e->d(e->embed);
+        const void* toks = (const uint32_t*)e->d(e->prompt) + pos0;
+        void* out = e->d(e->p_delta);
+        void* args[] = {(void*)&table, (void*)&toks, (void*)&out, (void*)&h, (void*)&vocab};
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_embedding_bf16, dim3(rows), dim3(128), args, "embedding"));
+    }
+    e->gpu->counts.memsets++;
+    X0NE_HIP(hipMemsetAsync(e->d(e->p_res), 0, n * c.hidden * 4, e->gpu->stream), "residual");
+    void* res = e->d(e->p_res);
+    void* dl = e->d(e->p_delta);
+    void* xn = e->d(e->p_x);
+    auto norm = [&](x0ne_slice w) {
+        const void* wp = e->d(w);
+        void* args[] = {(void*)&res, (void*)&dl, (void*)&wp, (void*)&xn, (void*)&h, (void*)&eps};
+        return launch_rows(e, (const void*)&x0ne_add_rmsnorm_bf16, dim3(rows), dim3(256), args, "add_rmsnorm");
+    };
+    const uint32_t group = qh / kvh;
+    const void* grouped = group == 1   ? (const void*)&x0ne_attention_prefill_g1_bf16
+                          : group == 2 ? (const void*)&x0ne_attention_prefill_g2_bf16
+                          : group == 4 ? (const void*)&x0ne_attention_prefill_g4_bf16
+                          : group == 8 ? (const void*)&x0ne_attention_prefill_g8_bf16
+                                       : nullptr;
+    for (uint64_t l = 0; l < c.layers; ++l) {
+        const LayerW& w = e->L[l];
+        X0NE_TRY(norm(w.input_norm));
+        X0NE_TRY(gemm(e, w.qkv, c.qkv_rows(), c.hidden, e->p_x, n, e->p_qkv));
+        {
+            const void* qkv = e->d(e->p_qkv);
+            const void* qn = e->d(w.q_norm);
+            const void* kn = e->d(w.k_norm);
+            const void* inv = e->d(e->inv_freq);
+            void* q = e->d(e->p_q);
+            void* kc = e->plane(l, 0);
+            void* vc = e->plane(l, 1);
+            const void* pt = e->d(e->page_table);
+            const void* pos = e->d(e->pos);
+            void* args[] = {(void*)&qkv, (void*)&qn, (void*)&kn, (void*)&inv, (void*)&q,       (void*)&kc, (void*)&vc,
+                            (void*)&pt,  (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
+            X0NE_TRY(launch_rows(e, (const void*)&x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, rows), dim3(64), args,
+                                 "qk_norm_rope_kv_write"));
+        }
+        {
+            const void* q = e->d(e->p_q);
+            const void* kc = e->plane(l, 0);
+            const void* vc = e->plane(l, 1);
+            const void* pt = e->d(e->page_table);
+            void* out = e->d(e->p_attn);
+            const void* pos = e->d(e->pos);
+            void* args[] = {(void*)&q,    (void*)&kc, (void*)&vc,  (void*)&pt,      (void*)&out, (void*)&pos,
+                            (void*)&rows, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&scale};
+            if (grouped) {
+                const uint32_t per = 64 / group;  // rows per block
+                X0NE_TRY(launch_rows(e, grouped, dim3(kvh, (rows + per - 1) / per), dim3(256), args, "prefill attention"));
+            } else {
+                X0NE_TRY(launch_rows(e, (const void*)&x0ne_attention_prefill_bf16, dim3(qh, rows), dim3(256), args,
+                                     "prefill attention"));
+            }
+        }
+        X0NE_TRY(gemm(e, w.o, c.hidden, c.q_dim(), e->p_attn, n, e->p_delta));
+        X0NE_TRY(norm(w.post_norm));
+        X0NE_TRY(gemm(e, w.gate_up, 2 * c.inter, c.hidden, e->p_x, n, e->p_gu));
+        {
+            const void* gu = e->d(e->p_gu);
+            void* act = e->d(e->p_act);
+            void* args[] = {(void*)&gu, (void*)&act, (void*)&inter};
+            X0NE_TRY(launch_rows(e, (const void*)&x0ne_swiglu_bf16, dim3((inter + 255) / 256, rows), dim3(256), args,
+                                 "swiglu"));
+        }
+        X0NE_TRY(gemm(e, w.down, c.hidden, c.inter, e->p_act, n, e->p_delta));
+    }
+    return X0NE_OK;
+}
+
+// The final norm and the LM head on row r of the last pass, at position p: f32 logits, the argmax
+// into tokens[0] and, with advance, pos = p + 1 for the decode step that follows.
+x0ne_status prefill_head(x0ne_engine* e, uint64_t r, uint64_t p, bool advance) {
+    const Cfg& c = e->c;
+    X0NE_TRY(set_position(e, p));
+    X0neGemv hd = {};
+    hd.w = (const uint16_t*)e->d(e->has_lm_head ? e->lm_head : e->embed);
+    hd.res_in = (const float*)e->d(e->p_res) + r * c.hidden;
+    hd.res_out = nullptr;
+    hd.delta = (const uint16_t*)e->d(e->p_delta) + r * c.hidden;
+    hd.norm_w = (const uint16_t*)e->d(e->final_norm);
+    hd.y = e->d(e->logits);
+    hd.partial = (float*)e->d(e->head_partial);
+    hd.counter = (uint32_t*)e->d(e->head_counter);
+    hd.token_out = (uint32_t*)e->d(e->tokens);
+    hd.pos = (uint32_t*)e->d(e->pos);
+    hd.advance = advance ? 1 : 0;
+    hd.rows = (uint32_t)c.vocab;
+    hd.cols = (uint32_t)c.hidden;
+    hd.eps = (float)c.eps;
+    hd.prologue = 1;
+    hd.epilogue = 3;
+    hd.grid = e->grid_head;
+    hd.f64acc = e->f64_sums;
+    e->gpu->counts.launches++;
+    X0NE_HIP(x0ne_launch_gemv(hd, e->gpu->stream), "prefill lm_head gemv");
+    return X0NE_OK;
+}
+
 // The ids of a request: 1..=max_ctx of them, each inside the vocabulary (engine.rs:637-645).
 x0ne_status check_ids(const x0ne_engine* e, const uint32_t* ids, size_t n) {
     if (n == 0 || n > e->max_ctx)
@@ -661,10 +815,22 @@ x0ne_status read_token(x0ne_engine* e, uint32_t* out) {
     return X0NE_OK;
 }
 
+// A prompt into the cache: passes of up to `chunk` rows, then the last row's logits and argmax
+// (engine.rs:408-425); tokens[0] holds the first generated token and pos the prompt's length.
+// With chunk 1 (the exact mode) one decode step per token.
 x0ne_status prefill(x0ne_engine* e, const uint32_t* ids, size_t n) {
     X0NE_TRY(put_prompt(e, ids, n));
-    for (size_t i = 0; i < n; ++i) X0NE_TRY(feed(e, (uint32_t)i));
-    return X0NE_OK;
+    if (e->chunk < 2) {
+        for (size_t i = 0; i < n; ++i) X0NE_TRY(feed(e, (uint32_t)i));
+        return X0NE_OK;
+    }
+    size_t start = 0;
+    for (;;) {
+        const size_t len = std::min<size_t>(e->chunk, n - start);
+        X0NE_TRY(prefill_pass(e, start, len));
+        if (start + len == n) return prefill_head(e, len - 1, n - 1, true);
+        start += len;
+    }
 }
 
 x0ne_status capture(x0ne_engine* e) {
@@ -714,6 +880,10 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     e->max_ctx = opts->max_ctx;
     e->page_seed = opts->page_seed;
     e->f64_sums = opts->f64_sums ? 1 : 0;
+    // The exact mode's sums are the decode GEMV's (f64): its prompts go one step per token.
+    e->chunk = e->f64_sums ? 1
+                           : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK, opts->max_ctx);
+    if (e->chunk == 0) e->chunk = 1;
     if (e->f64_sums) {
         const uint64_t grp = c.q_heads / c.kv_heads;
         if (grp != 1 && grp != 2 && grp != 4 && grp != 8) {
@@ -1233,13 +1403,32 @@ extern "C" x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids
     for (size_t k = 0; k < n_positions; ++k)
         if (positions[k] >= n)
             return fail(X0NE_ERR_FORMAT, "position " + std::to_string(positions[k]) + " outside " + std::to_string(n) + " tokens");
-    // Both routes feed one position per step here (the prefill route's many-row pass is not
-    // built yet), so they give the same bits.
+    // The decode route feeds one position per step (graph or eager); the prefill route runs
+    // passes of up to `chunk` rows and the LM head on each kept row (engine.rs:946-1016).
     x0ne_status st = put_prompt(e, ids, n);
-    for (size_t p = 0; p < n && st == X0NE_OK; ++p) {
-        st = feed(e, (uint32_t)p);
-        for (size_t k = 0; k < n_positions && st == X0NE_OK; ++k)
-            if (positions[k] == p) st = x0ne_arena_read(e->arena, e->logits, 0, rows + k * e->c.vocab, e->c.vocab * 4);
+    auto take = [&](size_t p) -> x0ne_status {
+        for (size_t k = 0; k < n_positions; ++k)
+            if (positions[k] == p) X0NE_TRY(x0ne_arena_read(e->arena, e->logits, 0, rows + k * e->c.vocab, e->c.vocab * 4));
+        return X0NE_OK;
+    };
+    if (route == X0NE_ROUTE_PREFILL && e->chunk > 1) {
+        for (size_t start = 0; start < n && st == X0NE_OK;) {
+            const size_t len = std::min<size_t>(e->chunk, n - start);
+            st = prefill_pass(e, start, len);
+            for (size_t p = start; p < start + len && st == X0NE_OK; ++p) {
+                bool kept = false;
+                for (size_t k = 0; k < n_positions; ++k) kept |= positions[k] == p;
+                if (!kept) continue;
+                st = prefill_head(e, p - start, p, false);
+                if (st == X0NE_OK) st = take(p);
+            }
+            start += len;
+        }
+    } else {
+        for (size_t p = 0; p < n && st == X0NE_OK; ++p) {
+            st = feed(e, (uint32_t)p);
+            if (st == X0NE_OK) st = take(p);
+        }
     }
     x0ne_status sc = scrub(e);
     return st != X0NE_OK ? st : sc;
@@ -1267,12 +1456,13 @@ extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, siz
     std::snprintf(s, sizeof s,
                   "%s, arena %llu bytes, decode graph %zu nodes, decode attention split-K P %u (grid %u x %u, %u q "
                   "heads per block, %u blocks per CU, merge %s), KV pages of %d positions (%llu pages, %s order), "
-                  "GEMV grids qkv %u o %u gate_up %u down %u head %u (%s sums), feed-forward dense",
+                  "GEMV grids qkv %u o %u gate_up %u down %u head %u (%s sums), prefill passes of %llu rows, "
+                  "feed-forward dense",
                   gpu, (unsigned long long)e->arena->len, e->graph ? e->graph->nodes : (size_t)0, e->split.splits,
                   e->split.grid_x, e->split.splits, e->split.group, e->split.per_cu,
                   e->split.grouped ? "LastBlock" : "Kernel", X0NE_PAGE_C, (unsigned long long)e->pages,
                   e->page_seed ? "shuffled" : "identity", e->grid_qkv, e->grid_o, e->grid_gu, e->grid_down,
-                  e->grid_head, e->f64_sums ? "f64" : "f32");
+                  e->grid_head, e->f64_sums ? "f64" : "f32", (unsigned long long)e->chunk);
     if (buf && len) {
         std::strncpy(buf, s, len - 1);
         buf[len - 1] = 0;

@@ -26,6 +26,10 @@ static const X0neKernel TABLE[] = {
     {"x0ne_attention_rope_decode_exact_g4_bf16", (const void*)&x0ne_attention_rope_decode_exact_g4_bf16, "pppppppppuuuf", 256},
     {"x0ne_attention_rope_decode_exact_g8_bf16", (const void*)&x0ne_attention_rope_decode_exact_g8_bf16, "pppppppppuuuf", 256},
     {"x0ne_attention_merge_bf16", (const void*)&x0ne_attention_merge_bf16, "pppuu", 64},
+    {"x0ne_attention_prefill_g1_bf16", (const void*)&x0ne_attention_prefill_g1_bf16, "ppppppuuuuf", 256},
+    {"x0ne_attention_prefill_g2_bf16", (const void*)&x0ne_attention_prefill_g2_bf16, "ppppppuuuuf", 256},
+    {"x0ne_attention_prefill_g4_bf16", (const void*)&x0ne_attention_prefill_g4_bf16, "ppppppuuuuf", 256},
+    {"x0ne_attention_prefill_g8_bf16", (const void*)&x0ne_attention_prefill_g8_bf16, "ppppppuuuuf", 256},
     {"x0ne_attention_prefill_bf16", (const void*)&x0ne_attention_prefill_bf16, "ppppppuuuuf", 256},
     {"x0ne_swiglu_bf16", (const void*)&x0ne_swiglu_bf16, "ppu", 256},
     {"x0ne_argmax_f32", (const void*)&x0ne_argmax_f32, "pup", 1024},

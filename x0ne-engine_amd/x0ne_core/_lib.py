@@ -68,7 +68,7 @@ class SplitPlanC(C.Structure):
 
 class EngineOptionsC(C.Structure):
     _fields_ = [("max_ctx", C.c_uint64), ("page_seed", C.c_uint64), ("f64_sums", C.c_uint32),
-                ("reserved", C.c_uint32)]
+                ("prefill_chunk", C.c_uint32)]
 
 
 _lib = None

@@ -32,13 +32,15 @@ class DecodeMode(IntEnum):
 @dataclass
 class EngineOptions:
     """EngineOptions (engine.rs:38-40) plus the KV page order (0: identity, else a seeded
-    shuffle) and the projections' summation (f32 FMA, or each exact product added in f64)."""
+    shuffle), the projections' summation (f32 FMA, or each exact product added in f64) and the
+    prompt rows per prefill pass (0: min(2048, max_ctx))."""
     max_ctx: int
     page_seed: int = 0
     f64_sums: bool = False
+    prefill_chunk: int = 0
 
     def c(self):
-        return EngineOptionsC(self.max_ctx, self.page_seed, int(self.f64_sums), 0)
+        return EngineOptionsC(self.max_ctx, self.page_seed, int(self.f64_sums), int(self.prefill_chunk))
 
 
 def _ids(ids):

@@ -414,9 +414,11 @@ class Kernels:
             v_rows.append(v_all[[v_offset(pg, h.kv_heads, kh, slot, d) for d in range(HEAD_DIM)]])
         return a.read_array(s["out"], 0, qd, np.uint16), np.concatenate(k_rows), np.concatenate(v_rows)
 
-    def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None):
+    def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None,
+                             grouped=False):
         """Causal attention for positions pos0..t of a t-position cache in one launch at pos0
-        (ops.rs:724-775); q holds those t - pos0 rows; returns the rows asked for."""
+        (ops.rs:724-775); q holds those t - pos0 rows; returns the rows asked for. grouped: the
+        matrix-core kernel for the geometry's group size (x0ne_attention_prefill_g*_bf16)."""
         h.check()
         m = t - pos0
         if m <= 0 or q.size != m * h.q_dim or k.size != t * h.kv_dim or v.size != t * h.kv_dim or \
@@ -424,7 +426,12 @@ class Kernels:
             raise FormatError("attention_prefill_at: lengths")
         a, s = self._kv_arena(q, k, v, t, h, page_of, pool, [("out", m * h.q_dim * 2)])
         a.write(s["pos"], 0, np.array([pos0], np.uint32))
-        self.gpu.launch("x0ne_attention_prefill_bf16", (h.q_heads, m), 256,
+        g = h.q_heads // h.kv_heads
+        if grouped and g not in (1, 2, 4, 8):
+            raise FormatError(f"attention_prefill_at: no grouped kernel for group {g}")
+        name, grid = ((f"x0ne_attention_prefill_g{g}_bf16", (h.kv_heads, (m + 64 // g - 1) // (64 // g))) if grouped
+                      else ("x0ne_attention_prefill_bf16", (h.q_heads, m)))
+        self.gpu.launch(name, grid, 256,
                         [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
                          Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(m),
                          Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(t), Arg.f32(attn_scale(h.head_dim))])
@@ -432,11 +439,11 @@ class Kernels:
         out = a.read_array(s["out"], 0, m * h.q_dim, np.uint16).reshape(m, h.q_dim)
         return [out[r].copy() for r in rows]
 
-    def attention_prefill_rows(self, q, k, v, t: int, h: Heads, rows, page_of=None, pool=None):
+    def attention_prefill_rows(self, q, k, v, t: int, h: Heads, rows, page_of=None, pool=None, grouped=False):
         """ops.rs:683-722: causal attention over t positions, the rows asked for."""
         if t == 0:
             raise FormatError("attention_prefill_rows: lengths")
-        return self.attention_prefill_at(q, k, v, t, 0, h, rows, page_of, pool)
+        return self.attention_prefill_at(q, k, v, t, 0, h, rows, page_of, pool, grouped)
 
     # -- swiglu (ops.rs:777-795, :978-1001) --
     def swiglu_rows(self, gate_up, rows: int) -> np.ndarray:
