@@ -17,6 +17,11 @@ Also printed, in the same JSON line:
   positions) x steps / s, against 8 TB/s.
 - cpu_baseline: the CPU oracle (oracle/, a C restatement of the reference's Rust oracle, f64
   inside) on this host's cores, on a bounded sample of the same workload.
+- prefill: the prompt's time to the first token (greedy_timed's first host time: the prompt in
+  passes of up to 2048 rows through matrix-core GEMMs and the causal prefill attention, then the
+  LM head on the last row), as tok/s and TFLOP/s against the 2.5 PFLOP/s dense bf16 peak.
+
+--prompt 8192 --steps 512 is BASELINE.json config 4 (8B, 8192-token prompt, 512 decode steps).
 """
 from __future__ import annotations
 
@@ -141,6 +146,7 @@ def main():
                     help="launch each step's kernels one by one instead of replaying the captured graph "
                          "(for kernel-trace profilers; the same kernels and results)")
     ap.add_argument("--f64-sums", action="store_true", help="f64 accumulation in the GEMVs")
+    ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt tokens (config 4: 8192)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel of known size, "
                          "for scaling hardware byte counters)")
@@ -153,10 +159,10 @@ def main():
     from x0ne_core import DecodeMode, Engine, EngineOptions, roofline
 
     cfg = QWEN3_8B
-    prompt = splitmix_ids(PROMPT, cfg["vocab_size"], SEED)
+    prompt = splitmix_ids(args.prompt, cfg["vocab_size"], SEED)
     n_tokens = args.warmup + args.steps + 1
     t = time.perf_counter()
-    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=PROMPT + n_tokens + 16, page_seed=1,
+    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=args.prompt + n_tokens + 16, page_seed=1,
                                                             f64_sums=args.f64_sums))
     if args.eager:
         e.set_decode_mode(DecodeMode.EAGER)
@@ -175,14 +181,29 @@ def main():
     secs = sorted(runs)[len(runs) // 2]
     tok_s = args.steps / secs
 
+    # The prompt to its first token, twice (the first also loads code): the second is reported.
+    for _ in range(2):
+        _, ptimes = e.greedy_timed(prompt, 1)
+    pre_s = float(ptimes[0])
+    h, inter, L, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"], cfg["vocab_size"]
+    qd, kvd = cfg["num_attention_heads"] * 128, cfg["num_key_value_heads"] * 128
+    P = args.prompt
+    pre_flops = 2 * P * L * (h * (qd + 2 * kvd) + qd * h + 3 * h * inter) + 2 * V * h \
+        + 4 * cfg["num_attention_heads"] * 128 * L * (P * (P + 1) // 2)
+    prefill = {"tokens": P, "seconds": round(pre_s, 6), "tok_s": round(P / pre_s, 1),
+               "tflops": round(pre_flops / pre_s / 1e12, 2), "peak_tflops": 2500.0,
+               "frac": round(pre_flops / pre_s / 1e12 / 2500.0, 4), "flops": pre_flops,
+               "timing": "greedy_timed: host time from the call to the first token on the host"}
+    print(f"[bench] prefill {P} tokens: {pre_s * 1e3:.2f} ms, {prefill['tok_s']} tok/s, {prefill['tflops']} TFLOP/s",
+          file=sys.stderr, flush=True)
+
     shape = roofline.Shape.of(cfg)
     # Steps w+1..w+K attend prompt + w + 1 .. prompt + w + K positions.
-    mean_ctx = PROMPT + args.warmup + (args.steps + 1) / 2.0
+    mean_ctx = args.prompt + args.warmup + (args.steps + 1) / 2.0
     step_bytes = roofline.step_bytes(shape, mean_ctx)
     hbm_gbs = step_bytes * tok_s / 1e9
 
     # The dominant kernel alone: gate/up GEMV (fused add + RMSNorm in front, SwiGLU behind).
-    h, inter = cfg["hidden_size"], cfg["intermediate_size"]
     # Weights, the residual read (f32) and written (f32, block 0), delta and the norm weight (bf16),
     # the SwiGLU output (inter bf16).
     gu_bytes = 2 * inter * h * 2 + 4 * h + 4 * h + 2 * h + 2 * h + 2 * inter
@@ -220,11 +241,11 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: random-init N(0,0.02) bf16 weights (seed 0), uniform random token ids (seed 0)",
-        "config": {"workload": "Qwen3-8B-shape batch-1 greedy decode, 20-token prompt, "
+        "config": {"workload": f"Qwen3-8B-shape batch-1 greedy decode, {args.prompt}-token prompt, "
                                + ("eager launches" if args.eager else "hipGraph per step")
                                + (", f64 GEMV sums" if args.f64_sums else ""),
                    "layers": 36, "hidden": 4096, "heads": "32q/8kv", "head_dim": 128, "intermediate": 12288,
-                   "vocab": 151936, "prompt": PROMPT, "mean_ctx": mean_ctx, "runs": runs},
+                   "vocab": 151936, "prompt": args.prompt, "mean_ctx": mean_ctx, "runs": runs},
         "decode_hbm": {"achieved": round(hbm_gbs, 1), "peak": 8000.0, "unit": "GB/s",
                        "frac": round(hbm_gbs / 8000.0, 4), "bytes_per_step": int(step_bytes),
                        "ceiling_tok_s": round(roofline.ceiling_tok_s(shape, mean_ctx), 2)},
@@ -236,6 +257,7 @@ def main():
                      "launches_timed": launches, "timing": "hipExtLaunchKernel start/stop events per launch",
                      "other_kernels": others},
         "cpu_baseline": cpu,
+        "prefill": prefill,
         "tokens_head": tokens[:8].tolist(),
     }
     print(json.dumps(line))
