@@ -21,7 +21,8 @@ Also printed, in the same JSON line:
   passes of up to 2048 rows through matrix-core GEMMs and the causal prefill attention, then the
   LM head on the last row), as tok/s and TFLOP/s against the 2.5 PFLOP/s dense bf16 peak.
 
---prompt 8192 --steps 512 is BASELINE.json config 4 (8B, 8192-token prompt, 512 decode steps).
+--prompt 8192 --steps 512 is BASELINE.json config 4 (8B, 8192-token prompt, 512 decode steps);
+--model 32b --prompt 512 is config 5's batch-1 case; --model 0.6b --steps 64 config 1's.
 """
 from __future__ import annotations
 
@@ -44,6 +45,11 @@ QWEN3_8B = {
     "num_key_value_heads": 8, "head_dim": 128, "vocab_size": 151936, "max_position_embeddings": 40960,
     "rms_norm_eps": 1e-6, "rope_theta": 1e6, "tie_word_embeddings": False,
 }
+QWEN3_32B = dict(QWEN3_8B, hidden_size=5120, intermediate_size=25600, num_hidden_layers=64,
+                 num_attention_heads=64, num_key_value_heads=8)
+QWEN3_0_6B = dict(QWEN3_8B, hidden_size=1024, intermediate_size=3072, num_hidden_layers=28, num_attention_heads=16,
+                  num_key_value_heads=8, tie_word_embeddings=True)
+MODELS = {"8b": ("Qwen3-8B", QWEN3_8B), "32b": ("Qwen3-32B", QWEN3_32B), "0.6b": ("Qwen3-0.6B", QWEN3_0_6B)}
 PROMPT = 20
 SEED = 0
 STD = 0.02
@@ -62,7 +68,8 @@ def splitmix_ids(n: int, vocab: int, seed: int) -> np.ndarray:
     return np.array(out, np.uint32)
 
 
-def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, prompt_len: int = 4) -> dict:
+def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, prompt_len: int = 4,
+                 name: str = "Qwen3-8B") -> dict:
     """The CPU oracle on the same shape and weights (drawn by the oracle's generator, the same
     bits as the device's): a `prompt_len`-token prompt, then `steps` greedy decode steps; tok/s
     over the decode steps. Also one thread on two steps, the reference oracle being
@@ -93,7 +100,7 @@ def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, pr
     O.set_threads(threads)
     return {"value": round(value, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "single_thread_value": round(single, 4),
-            "sample": f"Qwen3-8B shape, the same N(0,{STD}) bf16 weights (seed {SEED}, drawn by the oracle's "
+            "sample": f"{name} shape, the same N(0,{STD}) bf16 weights (seed {SEED}, drawn by the oracle's "
                       f"generator in {init_s:.1f} s, not timed), {prompt_len}-token prompt, {steps} greedy decode "
                       f"steps timed on {threads} threads (rows split, f64 sums in the reference's order); "
                       f"single_thread_value: 1 step on 1 thread"}
@@ -147,6 +154,7 @@ def main():
                          "(for kernel-trace profilers; the same kernels and results)")
     ap.add_argument("--f64-sums", action="store_true", help="f64 accumulation in the GEMVs")
     ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt tokens (config 4: 8192)")
+    ap.add_argument("--model", choices=sorted(MODELS), default="8b", help="the Qwen3 shape (default 8b)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel of known size, "
                          "for scaling hardware byte counters)")
@@ -158,7 +166,7 @@ def main():
 
     from x0ne_core import DecodeMode, Engine, EngineOptions, roofline
 
-    cfg = QWEN3_8B
+    model_name, cfg = MODELS[args.model]
     prompt = splitmix_ids(args.prompt, cfg["vocab_size"], SEED)
     n_tokens = args.warmup + args.steps + 1
     t = time.perf_counter()
@@ -223,13 +231,13 @@ def main():
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
         try:
-            cpu = cpu_baseline(cfg, prompt, threads)
+            cpu = cpu_baseline(cfg, prompt, threads, name=model_name)
         except Exception as ex:  # a baseline that cannot run is reported as missing, not as the GPU's failure
             cpu = {"value": None, "error": str(ex)}
         print(f"[bench] cpu baseline {cpu}", file=sys.stderr, flush=True)
 
     line = {
-        "metric": "Qwen3-8B bf16 decode tok/s @batch1; decode HBM GB/s vs 8 TB/s peak",
+        "metric": f"{model_name} bf16 decode tok/s @batch1; decode HBM GB/s vs 8 TB/s peak",
         "value": round(tok_s, 3),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -241,17 +249,19 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: random-init N(0,0.02) bf16 weights (seed 0), uniform random token ids (seed 0)",
-        "config": {"workload": f"Qwen3-8B-shape batch-1 greedy decode, {args.prompt}-token prompt, "
+        "config": {"workload": f"{model_name}-shape batch-1 greedy decode, {args.prompt}-token prompt, "
                                + ("eager launches" if args.eager else "hipGraph per step")
                                + (", f64 GEMV sums" if args.f64_sums else ""),
-                   "layers": 36, "hidden": 4096, "heads": "32q/8kv", "head_dim": 128, "intermediate": 12288,
-                   "vocab": 151936, "prompt": args.prompt, "mean_ctx": mean_ctx, "runs": runs},
+                   "layers": cfg["num_hidden_layers"], "hidden": cfg["hidden_size"],
+                   "heads": f"{cfg['num_attention_heads']}q/{cfg['num_key_value_heads']}kv", "head_dim": 128,
+                   "intermediate": cfg["intermediate_size"], "vocab": cfg["vocab_size"],
+                   "tied": cfg["tie_word_embeddings"], "prompt": args.prompt, "mean_ctx": mean_ctx, "runs": runs},
         "decode_hbm": {"achieved": round(hbm_gbs, 1), "peak": 8000.0, "unit": "GB/s",
                        "frac": round(hbm_gbs / 8000.0, 4), "bytes_per_step": int(step_bytes),
                        "ceiling_tok_s": round(roofline.ceiling_tok_s(shape, mean_ctx), 2)},
         "roofline": {"kernel": "gate_up GEMV (add+RMSNorm prologue, SwiGLU epilogue)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic("gate_up"),
+                     "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic("gate_up") if args.model == "8b" else None,
                      "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT), "bytes_per_launch": gu_bytes,
                      "avg_us": round(avg_us, 3), "wall_us_per_launch": round(wall_us, 3),
                      "launches_timed": launches, "timing": "hipExtLaunchKernel start/stop events per launch",
