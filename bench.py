@@ -141,6 +141,38 @@ def copy_calibration(n: int):
     print(f"[bench] calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
 
 
+def attention_line(args) -> dict:
+    """the isolated decode attention (Qwen3-8B geometry, 32 q / 8 kv heads)
+    at ctx 1k / 8k / 32k and P in {1, 4, 16}, each launch over distinct K/V planes (more than
+    512 MiB rotated); bytes per launch 2 ctx 8 128 2 (K + V) + Q + out + the split states."""
+    from x0ne_core.gpu import Gpu
+    g = Gpu()
+    qh, kvh = 32, 8
+    rows = []
+    for ctx in (1024, 8192, 32768):
+        for P in (1, 4, 16):
+            us, planes = g.time_attention(qh, kvh, ctx, P, args.attention_iters, SEED)
+            nbytes = 2 * ctx * kvh * 128 * 2 + qh * 128 * 2 * 2 + (qh * P * 132 * 4 if P > 1 else 0)
+            rows.append({"ctx": ctx, "splits": P, "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+                         "frac": round(nbytes / us / 1e3 / 8000.0, 4), "bytes": nbytes, "planes": planes})
+            print(f"[bench] attention ctx {ctx} P {P}: {us:.2f} us, {nbytes / us / 1e3:.1f} GB/s ({planes} planes)",
+                  file=sys.stderr, flush=True)
+    best = max((r for r in rows if r["ctx"] == 32768), key=lambda r: r["gbs"])
+    return {
+        "metric": "Qwen3-8B decode attention GB/s (BASELINE.json config 2) vs 8 TB/s peak",
+        "value": best["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.attention_iters, "warmup": 0,
+        "ms_per_step": round(best["us"] / 1e3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: Q, K, V N(0,1) bf16 (seed 0), pages in a seeded permutation",
+        "config": {"workload": "isolated split-K decode attention, 32q/8kv heads, head_dim 128, last-block merge; "
+                               "value at ctx 32768 with the fastest P", "ctx": best["ctx"], "splits": best["splits"],
+                   "table": rows},
+        "roofline": {"kernel": "x0ne_attention_decode_split_g4_bf16", "bound": "hbm", "achieved": best["gbs"],
+                     "peak": 8000.0, "unit": "GB/s", "frac": best["frac"], "traffic": None,
+                     "bytes_per_launch": best["bytes"], "avg_us": best["us"],
+                     "timing": "hipExtLaunchKernel start/stop events per launch"},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,6 +187,9 @@ def main():
     ap.add_argument("--f64-sums", action="store_true", help="f64 accumulation in the GEMVs")
     ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt tokens (config 4: 8192)")
     ap.add_argument("--model", choices=sorted(MODELS), default="8b", help="the Qwen3 shape (default 8b)")
+    ap.add_argument("--attention", action="store_true",
+                    help="BASELINE.json config 2 instead: the isolated decode attention at ctx 1k/8k/32k, P 1/4/16")
+    ap.add_argument("--attention-iters", type=int, default=64)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel of known size, "
                          "for scaling hardware byte counters)")
@@ -164,6 +199,9 @@ def main():
               "and no figure at several GPUs is produced. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    if args.attention:
+        print(json.dumps(attention_line(args)))
+        return
     from x0ne_core import DecodeMode, Engine, EngineOptions, roofline
 
     model_name, cfg = MODELS[args.model]

@@ -118,6 +118,13 @@ x0ne_status x0ne_gpu_attention_split(x0ne_gpu* g, const x0ne_split_plan* plan, i
                                      uint32_t max_ctx, float scale);
 /* split_state_bytes (ops.rs:125-127) */
 uint64_t x0ne_split_state_bytes(uint32_t q_heads, uint32_t splits);
+/* BASELINE.json config 2, the isolated decode attention of ops.rs:585-681: the grouped split-K
+   kernel (P = splits, last-block merge) at position ctx - 1 over ctx keys, Q, K and V N(0, 1) bf16
+   drawn from `seed`, pages in a seeded permutation, each launch on the next of *planes_out
+   distinct K/V plane pairs (together more than 512 MiB, so the 256 MiB Infinity Cache serves
+   none of them). *us: the mean kernel time of `iters` launches (events around each kernel). */
+x0ne_status x0ne_gpu_time_attention(x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, uint32_t ctx, uint32_t splits,
+                                    uint32_t iters, uint64_t seed, double* us, uint32_t* planes_out);
 
 /* Graph capture (gpu.rs:1170-1238): every launch between begin and end is recorded, then
    replayed by x0ne_gpu_launch_graph. */

@@ -412,6 +412,15 @@ def test_prefill_attention_is_the_oracle_whole_and_from_a_chunk_boundary(kernels
                     assert_close(f"prefill at {pos0} t {t} row {r} grouped {grouped}", bf16_vals(g), w, atol, 0.0)
 
 
+def test_the_isolated_attention_timing_rotates_distinct_planes(kernels):
+    """BASELINE.json config 2's harness (x0ne_gpu_time_attention): it runs the grouped split-K
+    kernel over more than 512 MiB of distinct K/V planes and reports a positive kernel time."""
+    for ctx, p in [(64, 1), (1024, 4)]:
+        us, planes = kernels.gpu.time_attention(32, 8, ctx, p, 4, 0)
+        plane = (ctx + 15) // 16 * 8 * 16 * 128 * 2
+        assert us > 0 and planes >= 2 and 2 * plane * planes > 512 << 20, (ctx, p, us, planes)
+
+
 @pytest.mark.parametrize("seed", range(20))
 def test_swiglu_is_the_oracle(kernels, seed):
     rng = O.Rng(600 + seed)

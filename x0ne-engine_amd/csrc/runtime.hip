@@ -445,6 +445,89 @@ extern "C" x0ne_status x0ne_gpu_attention_split(x0ne_gpu* g, const x0ne_split_pl
                            q_heads, kv_heads, max_ctx, scale);
 }
 
+extern "C" x0ne_status x0ne_gpu_time_attention(x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, uint32_t ctx,
+                                               uint32_t splits, uint32_t iters, uint64_t seed, double* us,
+                                               uint32_t* planes_out) {
+    if (!g || !us) return fail(X0NE_ERR_GPU, "no device");
+    if (ctx == 0 || iters == 0 || kv_heads == 0 || q_heads % kv_heads != 0 || splits == 0 || splits > MAX_SPLITS)
+        return fail(X0NE_ERR_FORMAT, "time_attention: geometry");
+    x0ne_split_plan plan = {};
+    X0NE_TRY(split_plan(g, q_heads, kv_heads, &plan));
+    if (!plan.grouped) return fail(X0NE_ERR_NOT_IMPLEMENTED, "time_attention: no grouped kernel for this group");
+    plan.splits = splits;
+    const uint64_t pages = (ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
+    const uint64_t plane = pages * kv_heads * X0NE_PAGE_C * X0NE_HEAD_DIM_C * 2;
+    // Enough distinct K/V planes to exceed twice the 256 MiB Infinity Cache, at least 2.
+    const uint64_t n_planes = std::max<uint64_t>(2, (512ull << 20) / (2 * plane) + 1);
+    std::vector<void*> kv(2 * n_planes, nullptr);
+    void *q = nullptr, *out = nullptr, *state = nullptr, *counter = nullptr, *pt = nullptr, *posp = nullptr;
+    std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
+    x0ne_status st = X0NE_OK;
+    auto hip = [&](hipError_t e, const char* what) {
+        if (st == X0NE_OK && e != hipSuccess) st = gpu_fail(e, what);
+    };
+    for (auto& p : kv) hip(hipMalloc(&p, plane), "time_attention: planes");
+    hip(hipMalloc(&q, (size_t)q_heads * X0NE_HEAD_DIM_C * 2), "time_attention: q");
+    hip(hipMalloc(&out, (size_t)q_heads * X0NE_HEAD_DIM_C * 2), "time_attention: out");
+    hip(hipMalloc(&state, x0ne_split_state_bytes(q_heads, splits)), "time_attention: state");
+    hip(hipMalloc(&counter, kv_heads * 4), "time_attention: counter");
+    hip(hipMalloc(&pt, pages * 4), "time_attention: page table");
+    hip(hipMalloc(&posp, 4), "time_attention: pos");
+    // Q, K and V N(0, 1) bf16 from the seed; pages in a splitmix64 Fisher-Yates order.
+    for (size_t i = 0; i < kv.size() && st == X0NE_OK; ++i)
+        hip(x0ne_launch_init_normal((uint16_t*)kv[i], plane / 2, seed + 1 + i, 0, 1.0, g->stream), "time_attention: K/V");
+    if (st == X0NE_OK)
+        hip(x0ne_launch_init_normal((uint16_t*)q, (uint64_t)q_heads * X0NE_HEAD_DIM_C, seed, 0, 1.0, g->stream),
+            "time_attention: q");
+    std::vector<uint32_t> order(pages);
+    for (uint64_t i = 0; i < pages; ++i) order[i] = (uint32_t)i;
+    uint64_t sm = seed;
+    for (uint64_t i = pages; i > 1; --i) {
+        sm += 0x9E3779B97F4A7C15ull;
+        uint64_t z = sm;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        std::swap(order[i - 1], order[z % i]);
+    }
+    const uint32_t pos = ctx - 1;
+    hip(hipMemcpy(pt, order.data(), pages * 4, hipMemcpyHostToDevice), "time_attention: page table");
+    hip(hipMemcpy(posp, &pos, 4, hipMemcpyHostToDevice), "time_attention: pos");
+    hip(hipMemset(counter, 0, kv_heads * 4), "time_attention: counter");
+    for (auto& x : ev) hip(hipEventCreate(&x), "time_attention: event");
+    const float scale = (float)(1.0 / std::sqrt((double)X0NE_HEAD_DIM_C));
+    auto launch = [&](uint64_t i) {
+        if (st == X0NE_OK)
+            st = attention_split(g, plan, 1, q, kv[2 * (i % n_planes)], kv[2 * (i % n_planes) + 1], pt, state, counter,
+                                 out, posp, q_heads, kv_heads, ctx, scale);
+    };
+    for (uint64_t i = 0; i < n_planes; ++i) launch(i);  // warm-up: every plane once
+    std::vector<X0neTimer> timers(iters);
+    for (uint32_t i = 0; i < iters && st == X0NE_OK; ++i) {
+        timers[i] = X0neTimer{ev[2 * i], ev[2 * i + 1], false};
+        x0ne_timer = &timers[i];
+        launch(n_planes + i);
+        x0ne_timer = nullptr;
+    }
+    if (st == X0NE_OK) hip(hipStreamSynchronize(g->stream), "time_attention: sync");
+    double total = 0.0;
+    for (uint32_t i = 0; i < iters && st == X0NE_OK; ++i) {
+        float ms = 0.f;
+        hip(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]), "time_attention: elapsed");
+        total += ms;
+    }
+    for (auto& x : ev)
+        if (x) (void)hipEventDestroy(x);
+    for (void* p : kv)
+        if (p) (void)hipFree(p);
+    for (void* p : {q, out, state, counter, pt, posp})
+        if (p) (void)hipFree(p);
+    if (st != X0NE_OK) return st;
+    *us = total * 1000.0 / iters;
+    if (planes_out) *planes_out = (uint32_t)n_planes;
+    return X0NE_OK;
+}
+
 extern "C" uint64_t x0ne_split_state_bytes(uint32_t q_heads, uint32_t splits) {
     return (uint64_t)q_heads * splits * X0NE_SPLIT_STATE_C * 4;
 }

@@ -97,6 +97,7 @@ SIGNATURES = {
     "x0ne_gpu_attention_split": ([P, C.POINTER(SplitPlanC), I32, U64, U64, U64, U64, U64, U64, U64, U64,
                                   U32, U32, U32, F32], ST),
     "x0ne_split_state_bytes": ([U32, U32], U64),
+    "x0ne_gpu_time_attention": ([P, U32, U32, U32, U32, U32, U64, C.POINTER(F64), C.POINTER(U32)], ST),
     "x0ne_gpu_capture_begin": ([P], ST),
     "x0ne_gpu_capture_end": ([P, C.POINTER(P)], ST),
     "x0ne_gpu_launch_graph": ([P, P], ST),

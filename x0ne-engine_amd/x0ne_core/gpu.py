@@ -176,6 +176,14 @@ class Gpu:
         check(lib().x0ne_gpu_attention_split(self.h, C.byref(pc), int(last_block), q, k, v, pages, state, counter,
                                               out, pos, q_heads, kv_heads, max_ctx, scale), "split-K attention")
 
+    def time_attention(self, q_heads: int, kv_heads: int, ctx: int, splits: int, iters: int, seed: int = 0):
+        """the isolated split-K decode attention over more than 512 MiB of
+        rotating K/V planes; (mean kernel µs per launch, planes rotated)."""
+        us, planes = C.c_double(), C.c_uint32()
+        check(lib().x0ne_gpu_time_attention(self.h, q_heads, kv_heads, ctx, splits, iters, seed, C.byref(us),
+                                            C.byref(planes)), "time_attention")
+        return us.value, planes.value
+
     def capture(self, launches) -> Graph:
         """Gpu::capture (gpu.rs:1170-1217): records the launches `launches()` makes."""
         check(lib().x0ne_gpu_capture_begin(self.h), "capture")
