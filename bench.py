@@ -23,6 +23,11 @@ Also printed, in the same JSON line:
 
 --prompt 8192 --steps 512 is BASELINE.json config 4 (8B, 8192-token prompt, 512 decode steps);
 --model 32b --prompt 512 is config 5's batch-1 case; --model 0.6b --steps 64 config 1's.
+--batch B decodes B independent prompts (splitmix64 seeds 0 .. B - 1; sequence 0's is the batch-1
+prompt) together, each step one replay of the batched step's graph: config 4 at batch 8 is
+--prompt 8192 --steps 512 --batch 8, config 5 at batch 16 --model 32b --prompt 512 --batch 16.
+value is then B x K / seconds (tokens of all sequences), the roofline kernel the batched gate/up
+projection (the few-row matrix-core GEMM with SwiGLU behind).
 """
 from __future__ import annotations
 
@@ -173,6 +178,99 @@ def attention_line(args) -> dict:
     }
 
 
+def batch_line(args, model_name: str, cfg: dict) -> dict:
+    """--batch B: B independent prompts decoded together (the batched step)."""
+    from x0ne_core import DecodeMode, Engine, EngineOptions, roofline
+    B = args.batch
+    prompts = np.stack([splitmix_ids(args.prompt, cfg["vocab_size"], SEED + b) for b in range(B)])
+    n_tokens = args.warmup + args.steps + 1
+    t = time.perf_counter()
+    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=args.prompt + n_tokens + 16, page_seed=1,
+                                                            max_batch=B))
+    if args.eager:
+        e.set_decode_mode(DecodeMode.EAGER)
+    print(f"[bench] loaded in {time.perf_counter() - t:.1f} s: {e.describe()}", file=sys.stderr, flush=True)
+    runs, tokens = [], None
+    for r in range(args.runs):
+        toks, secs = e.decode_batch_timed(prompts, args.warmup, args.steps)
+        if tokens is None:
+            tokens = toks
+        elif not (toks == tokens).all():
+            raise SystemExit("two runs gave different tokens: the measure is not of one computation")
+        runs.append(secs)
+        print(f"[bench] run {r}: {B * args.steps / secs:.2f} tok/s ({1e3 * secs / args.steps:.3f} ms per step)",
+              file=sys.stderr, flush=True)
+    secs = sorted(runs)[len(runs) // 2]
+    tok_s = B * args.steps / secs
+
+    # The B prompts to their first tokens (one after the other), twice; the second is reported.
+    for _ in range(2):
+        _, ptimes = e.greedy_batch(prompts, 1)
+    pre_s = float(ptimes[0])
+    h, inter, L, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"], cfg["vocab_size"]
+    qd, kvd = cfg["num_attention_heads"] * 128, cfg["num_key_value_heads"] * 128
+    P = args.prompt
+    pre_flops = B * (2 * P * L * (h * (qd + 2 * kvd) + qd * h + 3 * h * inter) + 2 * V * h
+                     + 4 * cfg["num_attention_heads"] * 128 * L * (P * (P + 1) // 2))
+    prefill = {"tokens": B * P, "seconds": round(pre_s, 6), "tok_s": round(B * P / pre_s, 1),
+               "tflops": round(pre_flops / pre_s / 1e12, 2), "peak_tflops": 2500.0,
+               "frac": round(pre_flops / pre_s / 1e12 / 2500.0, 4), "flops": pre_flops,
+               "timing": "greedy_batch: host time from the call to the first tokens of all sequences"}
+    print(f"[bench] prefill {B} x {P} tokens: {pre_s * 1e3:.2f} ms", file=sys.stderr, flush=True)
+
+    shape = roofline.Shape.of(cfg)
+    mean_ctx = args.prompt + args.warmup + (args.steps + 1) / 2.0
+    step_bytes = roofline.step_bytes(shape, mean_ctx, B)
+    hbm_gbs = step_bytes * (args.steps / secs) / 1e9
+    # The dominant kernel alone: the batched gate/up projection with SwiGLU behind (weights, the B
+    # normed rows in, the B activation rows out).
+    gu_bytes = 2 * inter * h * 2 + B * h * 2 + B * inter * 2
+    avg_us, wall_us, launches = e.time_kernel("gate_up", args.kernel_iters, batch=B)
+    achieved = gu_bytes / (avg_us * 1e-6) / 1e9
+    others = {}
+    for k in ("qkv", "attention", "o", "down", "head"):
+        kus, wus, _ = e.time_kernel(k, args.kernel_iters, batch=B)
+        others[k] = {"kernel_us": round(kus, 2), "wall_us": round(wus, 2)}
+    print(f"[bench] batched gate_up {avg_us:.2f} us ({achieved:.0f} GB/s), {wall_us:.2f} us per launch with gaps; "
+          f"others {others}", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        try:
+            cpu = cpu_baseline(cfg, prompts[0], threads, name=model_name)
+            cpu["sample"] += "; the oracle decodes one sequence at a time (its tok/s is per sequence)"
+        except Exception as ex:
+            cpu = {"value": None, "error": str(ex)}
+        print(f"[bench] cpu baseline {cpu}", file=sys.stderr, flush=True)
+    return {
+        "metric": f"{model_name} bf16 decode tok/s @batch{B}; decode HBM GB/s vs 8 TB/s peak",
+        "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(1e3 * secs / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": f"synthetic: random-init N(0,0.02) bf16 weights (seed 0), {B} prompts of uniform random token ids "
+                f"(seeds 0..{B - 1})",
+        "config": {"workload": f"{model_name}-shape batch-{B} greedy decode of independent prompts, "
+                               f"{args.prompt}-token prompts, "
+                               + ("eager launches" if args.eager else "hipGraph per batched step"),
+                   "batch": B, "layers": L, "hidden": h,
+                   "heads": f"{cfg['num_attention_heads']}q/{cfg['num_key_value_heads']}kv", "head_dim": 128,
+                   "intermediate": inter, "vocab": V, "tied": cfg["tie_word_embeddings"], "prompt": args.prompt,
+                   "mean_ctx": mean_ctx, "runs": runs},
+        "decode_hbm": {"achieved": round(hbm_gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                       "frac": round(hbm_gbs / 8000.0, 4), "bytes_per_step": int(step_bytes),
+                       "ceiling_tok_s": round(roofline.ceiling_tok_s(shape, mean_ctx, B), 2)},
+        "roofline": {"kernel": "batched gate_up few-row GEMM (SwiGLU epilogue)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(achieved / 8000.0, 4), "traffic": None, "bytes_per_launch": gu_bytes,
+                     "avg_us": round(avg_us, 3), "wall_us_per_launch": round(wall_us, 3),
+                     "launches_timed": launches, "timing": "hipExtLaunchKernel start/stop events per launch",
+                     "other_kernels": others},
+        "cpu_baseline": cpu,
+        "prefill": prefill,
+        "tokens_head": tokens[:, :4].tolist(),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -187,6 +285,8 @@ def main():
     ap.add_argument("--f64-sums", action="store_true", help="f64 accumulation in the GEMVs")
     ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt tokens (config 4: 8192)")
     ap.add_argument("--model", choices=sorted(MODELS), default="8b", help="the Qwen3 shape (default 8b)")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="independent sequences decoded together (config 4: 8, config 5: 16)")
     ap.add_argument("--attention", action="store_true",
                     help="BASELINE.json config 2 instead: the isolated decode attention at ctx 1k/8k/32k, P 1/4/16")
     ap.add_argument("--attention-iters", type=int, default=64)
@@ -205,6 +305,9 @@ def main():
     from x0ne_core import DecodeMode, Engine, EngineOptions, roofline
 
     model_name, cfg = MODELS[args.model]
+    if args.batch > 1:
+        print(json.dumps(batch_line(args, model_name, cfg)))
+        return
     prompt = splitmix_ids(args.prompt, cfg["vocab_size"], SEED)
     n_tokens = args.warmup + args.steps + 1
     t = time.perf_counter()

@@ -94,6 +94,11 @@ x0ne_status x0ne_check_args(const char* name, const x0ne_arg* args, size_t n);
    (gx, gy), `block` threads, the arguments checked against the table first. Not synchronised. */
 x0ne_status x0ne_gpu_launch(x0ne_gpu* g, const char* name, uint32_t gx, uint32_t gy, uint32_t block,
                             const x0ne_arg* args, size_t n);
+/* x0ne_gpu_launch with a third grid dimension, for the kernels that take one sequence per
+   blockIdx.z (x0ne_attention_rope_decode_batch_g*_bf16); no counterpart in the reference, whose
+   launch grids are two-dimensional (gpu.rs:1031-1086). */
+x0ne_status x0ne_gpu_launch_3d(x0ne_gpu* g, const char* name, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t block,
+                               const x0ne_arg* args, size_t n);
 
 /* Gpu::gemm (gpu.rs:1098-1149), the projection the reference hands cuBLAS: Y[n][rows] =
    X[n][cols] W^T, W [rows][cols] row-major bf16, X bf16, f32 accumulation; out_f32 = 0 gives
@@ -188,12 +193,19 @@ typedef struct x0ne_greedy x0ne_greedy;
      0, the default, is the fp32-accumulating decode path.
    - prefill_chunk: prompt rows per prefill pass (engine.rs:67, PREFILL_CHUNK); 0 takes
      min(2048, max_ctx). A pass runs every layer over its rows with matrix-core GEMMs and the
-     causal prefill attention; the exact mode feeds a prompt one decode step per token. */
+     causal prefill attention; the exact mode feeds a prompt one decode step per token.
+   - max_batch: independent sequences the batched greedy entry points serve (0 or 1: the
+     single-sequence engine). Each sequence has its own max_ctx positions of KV pages (the page
+     table holds max_batch runs of ceil(max_ctx / 16) pages) and its own position; the batched
+     step's projections read every weight once for all sequences. 1 to 64; the f32 path only
+     (X0NE_ERR_NOT_IMPLEMENTED with f64_sums or a group size without a grouped kernel). */
 typedef struct {
     uint64_t max_ctx;
     uint64_t page_seed;
     uint32_t f64_sums;
     uint32_t prefill_chunk;
+    uint32_t max_batch;
+    uint32_t reserved; /* 0 */
 } x0ne_engine_options;
 
 /* Engine::load_from (engine.rs:301-309) over safetensors files already in memory (the
@@ -247,6 +259,23 @@ x0ne_status x0ne_engine_greedy_with_last_logits(x0ne_engine* e, const uint32_t* 
 x0ne_status x0ne_engine_decode_timed(x0ne_engine* e, const uint32_t* prompt, size_t n_prompt, size_t warmup,
                                      size_t steps, uint32_t* tokens, double* seconds);
 
+/* Batched greedy decoding of `batch` independent sequences (1 <= batch <= max_batch): no
+   counterpart in the reference, whose engine serves one sequence at a time (engine.rs:389-406);
+   it is Engine::greedy_timed applied to each of `batch` prompts at once. prompts holds
+   batch rows of n_prompt ids. Each prompt is prefilled into its own KV pages (passes of
+   prefill_chunk rows), then every decode step advances all sequences: one graph launch (or the
+   eager launches) and one copy of `batch` token words. tokens receives batch rows of n tokens;
+   times (may be NULL) the wall time of each step's tokens, seconds from the call; last_logits
+   (may be NULL) batch rows of vocab_size floats, the logits of each sequence's last token.
+   A sequence's tokens and logits do not depend on the other sequences of the batch: the same
+   bits alone or beside any others. Client bytes are zeroed after. */
+x0ne_status x0ne_engine_greedy_batch(x0ne_engine* e, const uint32_t* prompts, size_t n_prompt, size_t batch, size_t n,
+                                     uint32_t* tokens, double* times, float* last_logits);
+/* The bench's batched decode measure: as x0ne_engine_decode_timed for `batch` sequences (tokens:
+   batch rows of warmup + steps + 1 tokens). */
+x0ne_status x0ne_engine_decode_batch_timed(x0ne_engine* e, const uint32_t* prompts, size_t n_prompt, size_t batch,
+                                           size_t warmup, size_t steps, uint32_t* tokens, double* seconds);
+
 /* Route (engine.rs:44-48) and DecodeMode (engine.rs:51-55). */
 typedef enum { X0NE_ROUTE_PREFILL = 0, X0NE_ROUTE_DECODE = 1 } x0ne_route;
 typedef enum { X0NE_DECODE_EAGER = 0, X0NE_DECODE_GRAPH = 1 } x0ne_decode_mode;
@@ -290,6 +319,11 @@ typedef enum {
 } x0ne_step_kernel;
 x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* kernel_us,
                                     double* wall_us, uint64_t* launches);
+/* The same measurement for the batched step's kernel at `batch` sequences (1 <= batch <=
+   max_batch of an engine loaded with max_batch > 1): the few-row GEMM projections, the batched
+   attention, the LM head with the per-sequence argmax. No counterpart in the reference. */
+x0ne_status x0ne_engine_time_batch_kernel(x0ne_engine* e, uint32_t which, uint32_t batch, uint32_t iters,
+                                          double* kernel_us, double* wall_us, uint64_t* launches);
 
 /* The reference's constants (engine.rs:67-79; kernels/src/lib.rs:135-144). */
 #define X0NE_GREEDY_AHEAD 2

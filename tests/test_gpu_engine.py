@@ -169,6 +169,79 @@ def test_greedy_on_the_device_is_greedy_on_the_host(which):
         print(f"MEASURE greedy prompt {prompt_len}: compared {compared} of {n} tokens with the oracle")
 
 
+@pytest.mark.parametrize("which", [0, 1])
+def test_batched_greedy_is_each_sequence_alone_and_the_oracle(which):
+    """B independent prompts decoded together (the batched step: few-row GEMMs, one attention
+    launch over every sequence's own pages): each sequence's tokens and last logits are the bits
+    it gets alone or in another batch order, graph and eager alike; they are the oracle's greedy
+    tokens until the oracle's top-2 margin is within the tolerance, and its logits within the
+    model tolerance; and the client bytes are zeroed after."""
+    from x0ne_core import DecodeMode, Engine, EngineOptions
+    f = [Fixture(tiny(2, 4, 2, False), 21), Fixture(wide(), 22)][which]
+    e = Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
+                         EngineOptions(max_ctx=96, page_seed=9, prefill_chunk=16, max_batch=4))
+    B, np_, n = 4, 21, 30
+    prompts = np.stack([f.tokens(300 + b, np_) for b in range(B)])
+    toks, times, logits = e.greedy_batch(prompts, n, logits=True)
+    assert toks.shape == (B, n) and (np.diff(times) >= 0).all()
+    assert e.client_data_is_zero() and e.host_buffers_are_zero()
+    order = [2, 0, 3, 1]
+    t2, _, l2 = e.greedy_batch(prompts[order], n, logits=True)
+    for i, b in enumerate(order):
+        assert (t2[i] == toks[b]).all(), f"sequence {b} in another order"
+        assert (l2[i].view(np.uint32) == logits[b].view(np.uint32)).all(), f"sequence {b} logits in another order"
+    for b in [0, 3]:
+        t1, _, l1 = e.greedy_batch(prompts[b:b + 1], n, logits=True)
+        assert (t1[0] == toks[b]).all() and (l1[0].view(np.uint32) == logits[b].view(np.uint32)).all(), \
+            f"sequence {b} alone"
+    e.set_decode_mode(DecodeMode.EAGER)
+    te, _, le = e.greedy_batch(prompts, n, logits=True)
+    e.set_decode_mode(DecodeMode.GRAPH)
+    assert (te == toks).all() and (le.view(np.uint32) == logits.view(np.uint32)).all(), "eager = graph"
+    for b in range(B):
+        f.model.reset()
+        ol = f.model.extend(prompts[b])
+        compared = 0
+        for i in range(n):
+            scale = float(np.abs(ol).max())
+            first, second = top_two(ol)
+            if first - second <= 2 * LOGITS_ATOL_OF_MAX * scale:
+                break
+            assert toks[b, i] == O.argmax(ol), f"sequence {b} token {i} against the oracle"
+            compared += 1
+            if i + 1 < n:
+                ol = f.model.step(int(toks[b, i]))
+        print(f"MEASURE batched greedy sequence {b}: compared {compared} of {n} tokens with the oracle")
+        f.model.reset()
+        want = f.model.logits(np.concatenate([prompts[b], toks[b, :-1]]))[-1]
+        assert_logits(f"batched sequence {b} last logits", logits[b], want)
+    assert e.client_data_is_zero() and e.host_buffers_are_zero()
+
+
+def test_batched_greedy_refusals():
+    from x0ne_core import Engine, EngineOptions, FormatError, NotImplementedFeature
+    f = Fixture(tiny(1, 2, 1, False), 23)
+    single = f.engine(64)
+    with pytest.raises(NotImplementedFeature):
+        single.greedy_batch(np.zeros((1, 3), np.uint32), 2)
+    e = Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
+                         EngineOptions(max_ctx=64, page_seed=2, max_batch=2))
+    with pytest.raises(FormatError):
+        e.greedy_batch(np.zeros((3, 3), np.uint32), 2)  # above max_batch
+    with pytest.raises(FormatError):
+        e.greedy_batch(np.full((2, 3), f.cfg.vocab, np.uint32), 2)  # outside the vocabulary
+    with pytest.raises(FormatError):
+        e.greedy_batch(np.zeros((2, 60), np.uint32), 6)  # 60 + 6 - 1 > 64
+    assert e.greedy_batch(np.zeros((2, 60), np.uint32), 5)[0].shape == (2, 5)
+    with pytest.raises(NotImplementedFeature):
+        Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
+                         EngineOptions(max_ctx=64, f64_sums=True, max_batch=2))
+    assert e.client_data_is_zero() and e.host_buffers_are_zero()
+    # The single-sequence paths still run on a batched engine (sequence 0's pages).
+    g = e.greedy(f.tokens(5, 9), 7)
+    assert (g == single.greedy(f.tokens(5, 9), 7)).all()
+
+
 def test_session_refusals_and_scrub():
     from x0ne_core import FormatError
     f = Fixture(tiny(1, 2, 1, False), 5)

@@ -210,7 +210,7 @@ def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
     oracle's GEMV of that row of X within the GEMV tolerance (gpu_kernels.rs:331-393), at tile
     edges of both sides and K tails; the bf16 output is the f32 output rounded."""
     rng = O.Rng(700 + seed)
-    n = rng.pick([4, 5, 31, 128, 129, 257])
+    n = rng.pick([2, 3, 4, 5, 16, 17, 31, 33, 64, 65, 128, 129, 257])
     rows = rng.pick([1, 15, 128, 129, 384, 1000])
     cols = rng.pick([8, 64, 72, 1000, 4096])
     scale = rng.pick([1e-2, 1.0, 50.0])
@@ -226,6 +226,37 @@ def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
         assert_gemv(f"{what} row {r} f32", f[r], want, mag, False)
         assert_gemv(f"{what} row {r} bf16", bf16_vals(b[r]), want, mag, True)
     assert (b == bf16_bits(f).reshape(b.shape)).all(), what
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_few_row_gemm_is_the_oracle_and_its_swiglu_the_swiglu_kernel(kernels, seed):
+    """The batched step's projection kernel (2 to 64 rows of X, each W row read once) at every
+    block size it runs with: every row of Y is the oracle's GEMV within the GEMV tolerance, the
+    bf16 output is the f32 output rounded, and the fused SwiGLU (mode 2) over a packed
+    [gate; up] W gives the bits of the SwiGLU kernel applied to the bf16 projection (the same
+    products in the same order), which is the oracle's SwiGLU of the rounded gate and up."""
+    rng = O.Rng(800 + seed)
+    n = rng.pick([1, 2, 7, 16, 17, 32, 33, 64])
+    rows = rng.pick([1, 16, 17, 100, 256, 1000])
+    cols = rng.pick([8, 32, 40, 200, 1024, 4096])
+    block = rng.pick([256, 512])
+    scale = rng.pick([1e-2, 1.0, 20.0])
+    w = bf16s_with_edges(rng, 2 * rows * cols, scale)
+    x = bf16s_with_edges(rng, n * cols, scale)
+    what = f"few-row gemm seed {seed} {n}x{rows}x{cols} block {block}"
+    f = kernels.gemm_few(bf16_bits(w[:rows * cols]), rows, cols, bf16_bits(x), n, 1, block)
+    b = kernels.gemm_few(bf16_bits(w[:rows * cols]), rows, cols, bf16_bits(x), n, 0, block)
+    for r in range(n):
+        xr = x[r * cols:(r + 1) * cols]
+        want = O.gemv(w[:rows * cols], rows, cols, xr)
+        mag = O.gemv_magnitude(w[:rows * cols], rows, cols, xr)
+        assert_gemv(f"{what} row {r} f32", f[r], want, mag, False)
+    assert (b == bf16_bits(f).reshape(b.shape)).all(), f"{what}: bf16 is the f32 rounded"
+    gu = kernels.gemm_few(bf16_bits(w), 2 * rows, cols, bf16_bits(x), n, 0, block)
+    act = kernels.gemm_few(bf16_bits(w), rows, cols, bf16_bits(x), n, 2, block)
+    for r in range(n):
+        assert (act[r] == kernels.swiglu(gu[r])).all(), f"{what} row {r}: fused SwiGLU"
+        assert_close(f"{what} row {r} swiglu", bf16_vals(act[r]), O.swiglu(bf16_vals(gu[r])), BF16_ATOL, BF16_RTOL)
 
 
 def test_gemv_carries_non_finite_values_to_the_rows_that_read_them(kernels):
@@ -318,6 +349,42 @@ def test_fused_rope_attention_is_the_two_kernel_path_bit_for_bit(kernels, qh, kv
                 assert_close(f"{what} P {splits}", bf16_vals(out), want, atol, 0.0)
         assert_close(f"{what} k row", bf16_vals(rope.k_row), k_o, ROPE_ATOL_OF_XMAX * max_abs(k_o) + BF16_ATOL,
                      BF16_RTOL)
+
+
+@pytest.mark.parametrize("qh,kvh", [(1, 1), (2, 1), (4, 2), (16, 8), (32, 8), (64, 8)])
+def test_batched_attention_is_each_sequence_alone_bit_for_bit(kernels, qh, kvh):
+    """The batched step's attention (grid (kv_heads, P, B)): sequences at ragged positions, each
+    in its own run of a shuffled page table over shared planes, get the bits the single-sequence
+    fused kernel gives each alone on the same P, write the same K/V rows, and are the oracle's
+    attention within tolerance."""
+    from x0ne_core.ops import CacheAt
+    h = H(qh, kvh)
+    rng = O.Rng(490 + qh)
+    theta, eps, max_ctx = 1e6, 1e-6, 1100
+    ctxs = [1, 17, 256, 257, 1000]
+    B = len(ctxs)
+    qkv = [rng.bf16s(h.q_dim + 2 * h.kv_dim, 3.0) for _ in range(B)]
+    qn, kn = rng.bf16s(128, 1.5), rng.bf16s(128, 1.5)
+    ks = [rng.bf16s((c - 1) * h.kv_dim, 1.0) for c in ctxs]
+    vs = [bf16s_with_edges(rng, (c - 1) * h.kv_dim, 4.0) for c in ctxs]
+    for splits in [1, 4]:
+        out, k_rows, v_rows = kernels.attention_rope_decode_batch(
+            np.concatenate([bf16_bits(q) for q in qkv]), bf16_bits(qn), bf16_bits(kn), eps, theta,
+            [bf16_bits(k) for k in ks], [bf16_bits(v) for v in vs], ctxs, h, splits, max_ctx, page_seed=5 + splits)
+        for b, ctx in enumerate(ctxs):
+            what = f"batched {qh}/{kvh} P {splits} sequence {b} ctx {ctx}"
+            one, k_row, v_row = kernels.attention_rope_decode(
+                bf16_bits(qkv[b]), bf16_bits(qn), bf16_bits(kn), eps, theta, bf16_bits(ks[b]), bf16_bits(vs[b]), ctx,
+                h, last_block=True, splits=splits)
+            assert (out[b] == one).all(), f"{what}: not the single-sequence bits"
+            assert (k_rows[b] == k_row).all() and (v_rows[b] == v_row).all(), f"{what}: the K/V row"
+            rope = kernels.qk_norm_rope_kv_write(bf16_bits(qkv[b]), bf16_bits(qn), bf16_bits(kn), h, theta, eps,
+                                                 CacheAt(1, ctx, 0, ctx - 1))
+            assert (rope.k_row == k_row).all() and (rope.v_row == v_row).all(), f"{what}: the rope kernel's row"
+            kb = np.concatenate([ks[b], bf16_vals(k_row)])
+            vb = np.concatenate([vs[b], bf16_vals(v_row)])
+            want = O.attention_decode(bf16_vals(rope.q), kb, vb, ctx, qh, kvh)
+            assert_close(what, bf16_vals(out[b]), want, ATTENTION_ATOL_OF_VMAX * max_abs(vb), 0.0)
 
 
 @pytest.mark.parametrize("qh,kvh", [(1, 1), (2, 1), (16, 8), (32, 8), (64, 8)])

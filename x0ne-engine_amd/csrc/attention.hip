@@ -1007,6 +1007,12 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
 // it applies QK-norm + RoPE to its q heads and writes the K/V row of position pos into its page
 // (the work of x0ne_qk_norm_rope_kv_write_bf16 for one decode row), then attends.
 //
+// x0ne_attention_rope_decode_batch_g*_bf16 is the fused variant for B independent sequences,
+// grid (kv_heads, P, B): sequence b = blockIdx.z has its packed qkv row at qkv + b (q_heads + 2
+// kv_heads) 128, its page table at pages + b seq_pages (its own pages of the shared K/V planes),
+// its position at pos[b], its split state and counters after b (q_heads P) states and b kv_heads
+// counters, and its output at out + b q_heads 128.
+//
 // x0ne_attention_rope_decode_exact_g*_bf16 is the fused variant with f64 scores, softmax and
 // sums and the f64 scale 1/sqrt(128), one block per kv head over the whole context (grid
 // (kv_heads, 1), block 256): the exact mode, whose outputs follow the f64 oracle's rounding
@@ -1054,6 +1060,36 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         a.counter = counter;                                                                                       \
         a.out = out;                                                                                               \
         a.pos = pos;                                                                                               \
+        a.q_heads = q_heads;                                                                                       \
+        a.kv_heads = kv_heads;                                                                                     \
+        a.max_ctx = max_ctx;                                                                                       \
+        a.splits = splits;                                                                                         \
+        a.scale = scale;                                                                                           \
+        a.eps = eps;                                                                                               \
+        attn_group_block<G, true>(a, sh);                                                                          \
+    }                                                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) x0ne_attention_rope_decode_batch_g##G##_bf16(               \
+        const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm, const bf16_t* __restrict__ k_norm,    \
+        const float* __restrict__ inv_freq, const double* __restrict__ rope_cs, bf16_t* __restrict__ k_cache,    \
+        bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages, float* __restrict__ state,             \
+        uint32_t* __restrict__ counter, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,              \
+        uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale, float eps,          \
+        uint32_t seq_pages) {                                                                                      \
+        __shared__ AttnShared<G> sh;                                                                               \
+        const size_t b = blockIdx.z;                                                                               \
+        AttnArgs a = {};                                                                                           \
+        a.qkv = qkv + b * (q_heads + 2 * kv_heads) * X0NE_HEAD_DIM;                                                \
+        a.q_norm = q_norm;                                                                                         \
+        a.k_norm = k_norm;                                                                                         \
+        a.inv_freq = inv_freq;                                                                                     \
+        a.rope_cs = rope_cs;                                                                                       \
+        a.k_cache = k_cache;                                                                                       \
+        a.v_cache = v_cache;                                                                                       \
+        a.pages = pages + b * seq_pages;                                                                           \
+        a.state = state + b * q_heads * splits * X0NE_SPLIT_STATE;                                                 \
+        a.counter = counter + b * kv_heads;                                                                        \
+        a.out = out + b * q_heads * X0NE_HEAD_DIM;                                                                 \
+        a.pos = pos + b;                                                                                           \
         a.q_heads = q_heads;                                                                                       \
         a.kv_heads = kv_heads;                                                                                     \
         a.max_ctx = max_ctx;                                                                                       \

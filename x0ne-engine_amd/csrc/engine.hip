@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <vector>
 
@@ -34,6 +35,7 @@ constexpr size_t RING = 16;  // engine.rs:70
 // Prompt rows per prefill pass by default (engine.rs:67 has 512; the matrix-core GEMM's tiles are
 // 128 rows, and 2048 rows keep it compute-bound).
 constexpr uint64_t PREFILL_CHUNK = 2048;
+constexpr uint64_t MAX_BATCH = 64;  // the few-row GEMM's most rows
 
 struct Cfg {
     uint64_t hidden = 0, inter = 0, layers = 0, q_heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, max_pos = 0;
@@ -284,6 +286,7 @@ struct x0ne_engine {
     Cfg c;
     uint64_t max_ctx = 0, pages = 0, page_seed = 0;
     uint64_t chunk = 1;  // prompt rows per prefill pass; 1: one decode step per token
+    uint64_t max_batch = 1, seq_pages = 0;  // sequences of the batched step; pages per sequence
     int f64_sums = 0;
     x0ne_gpu* gpu = nullptr;
     x0ne_arena* arena = nullptr;
@@ -296,13 +299,19 @@ struct x0ne_engine {
         act{}, logits{}, head_partial{}, head_counter{}, attn_state{}, attn_counter{};
     // A prefill pass's rows: f32 residual, bf16 delta, normed x, qkv, q, attention, [gate; up], act.
     x0ne_slice p_res{}, p_delta{}, p_x{}, p_qkv{}, p_q{}, p_attn{}, p_gu{}, p_act{};
+    // The batched step's rows ([max_batch][...]): f32 residual, bf16 delta, normed x, qkv,
+    // attention, SwiGLU activation, f32 logits; its split-K state and counters.
+    x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{};
     std::vector<uint32_t> page_of;
-    x0ne_split_plan split{};
+    x0ne_split_plan split{}, bsplit{};
     uint32_t grid_qkv = 0, grid_o = 0, grid_gu = 0, grid_down = 0, grid_head = 0;
     x0ne_graph* graph = nullptr;
+    x0ne_graph* bgraph = nullptr;  // the batched step for bgraph_batch sequences
+    uint64_t bgraph_batch = 0;
     uint32_t mode = X0NE_DECODE_GRAPH;
     // host side (pinned)
     uint32_t* ring = nullptr;
+    uint32_t* bring = nullptr;  // RING slots of max_batch token words
     hipEvent_t ring_ev[RING] = {};
     float* host_logits = nullptr;
     hipEvent_t logits_ev = nullptr;
@@ -312,11 +321,13 @@ struct x0ne_engine {
 
     ~x0ne_engine() {
         if (graph) x0ne_graph_free(graph);
+        if (bgraph) x0ne_graph_free(bgraph);
         if (gpu && gpu->stream) (void)hipStreamSynchronize(gpu->stream);
         for (auto& ev : ring_ev)
             if (ev) (void)hipEventDestroy(ev);
         if (logits_ev) (void)hipEventDestroy(logits_ev);
         if (ring) (void)hipHostFree(ring);
+        if (bring) (void)hipHostFree(bring);
         if (host_logits) (void)hipHostFree(host_logits);
         if (host_token) (void)hipHostFree(host_token);
         if (arena) x0ne_arena_free(arena);
@@ -326,6 +337,11 @@ struct x0ne_engine {
     uint64_t plane_bytes() const { return pages * X0NE_PAGE_C * c.kv_dim() * 2; }
     // K (kv = 0) or V (kv = 1) plane of layer l.
     uint8_t* plane(uint64_t l, int kvsel) const { return d(kv) + (2 * l + kvsel) * plane_bytes(); }
+    // Sequence b's page table, position, token and prompt row (b = 0: the single-sequence ones).
+    const uint32_t* pages_of(uint64_t b) const { return (const uint32_t*)d(page_table) + b * seq_pages; }
+    uint32_t* pos_of(uint64_t b) const { return (uint32_t*)d(pos) + b; }
+    uint32_t* token_of(uint64_t b) const { return (uint32_t*)d(tokens) + b; }
+    const uint32_t* prompt_of(uint64_t b) const { return (const uint32_t*)d(prompt) + b * max_ctx; }
 };
 
 struct x0ne_session {
@@ -372,9 +388,9 @@ x0ne_status plan(x0ne_engine* e) {
     X0NE_TRY(al("page_table", e->pages * 4, W, &e->page_table));
     // Client data.
     X0NE_TRY(al("kv_cache", 2 * c.layers * e->plane_bytes(), CD, &e->kv));
-    X0NE_TRY(al("prompt", e->max_ctx * 4, CD, &e->prompt));
-    X0NE_TRY(al("tokens", 4, CD, &e->tokens));
-    X0NE_TRY(al("pos", 4, CD, &e->pos));
+    X0NE_TRY(al("prompt", e->max_batch * e->max_ctx * 4, CD, &e->prompt));
+    X0NE_TRY(al("tokens", e->max_batch * 4, CD, &e->tokens));
+    X0NE_TRY(al("pos", e->max_batch * 4, CD, &e->pos));
     X0NE_TRY(al("residual", 2 * c.hidden * 4, CD, &e->residual));
     X0NE_TRY(al("delta", c.hidden * 2, CD, &e->delta));
     X0NE_TRY(al("qkv_out", c.qkv_rows() * 2, CD, &e->qkv));
@@ -397,6 +413,19 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("prefill_attn", n * c.q_dim() * 2, CD, &e->p_attn));
         X0NE_TRY(al("prefill_gate_up", n * 2 * c.inter * 2, CD, &e->p_gu));
         X0NE_TRY(al("prefill_act", n * c.inter * 2, CD, &e->p_act));
+    }
+    if (e->max_batch > 1) {
+        const uint64_t b = e->max_batch;
+        X0NE_TRY(al("batch_residual", b * c.hidden * 4, CD, &e->b_res));
+        X0NE_TRY(al("batch_delta", b * c.hidden * 2, CD, &e->b_delta));
+        X0NE_TRY(al("batch_normed", b * c.hidden * 2, CD, &e->b_x));
+        X0NE_TRY(al("batch_qkv", b * c.qkv_rows() * 2, CD, &e->b_qkv));
+        X0NE_TRY(al("batch_attn", b * c.q_dim() * 2, CD, &e->b_attn));
+        X0NE_TRY(al("batch_act", b * c.inter * 2, CD, &e->b_act));
+        X0NE_TRY(al("batch_logits", b * c.vocab * 4, CD, &e->b_logits));
+        X0NE_TRY(al("batch_split_state", b * x0ne_split_state_bytes((uint32_t)c.q_heads, e->bsplit.splits), CD,
+                    &e->b_state));
+        X0NE_TRY(al("batch_split_counter", b * c.kv_heads * 4, CD, &e->b_counter));
     }
     return X0NE_OK;
 }
@@ -623,11 +652,11 @@ x0ne_status put_prompt(x0ne_engine* e, const uint32_t* ids, size_t n) {
     return x0ne_arena_write(e->arena, e->prompt, 0, ids, n * 4);
 }
 
-// tokens[0] = prompt[i], pos = i, without a step.
-x0ne_status set_position(x0ne_engine* e, uint64_t i) {
+// Sequence b's token = its prompt[i], its position = i, without a step.
+x0ne_status set_position(x0ne_engine* e, uint64_t i, uint64_t b = 0) {
     e->gpu->counts.launches++;
-    hipLaunchKernelGGL(x0ne_feed_u32, dim3(1), dim3(64), 0, e->gpu->stream, (const uint32_t*)e->d(e->prompt),
-                       (uint32_t)i, (uint32_t*)e->d(e->tokens), (uint32_t*)e->d(e->pos));
+    hipLaunchKernelGGL(x0ne_feed_u32, dim3(1), dim3(64), 0, e->gpu->stream, e->prompt_of(b), (uint32_t)i,
+                       e->token_of(b), e->pos_of(b));
     X0NE_HIP(hipGetLastError(), "position");
     return X0NE_OK;
 }
@@ -648,18 +677,19 @@ x0ne_status gemm(x0ne_engine* e, x0ne_slice w, uint64_t rows, uint64_t cols, x0n
 // embedding into delta and a zero residual, then per layer add + RMSNorm, the QKV GEMM, QK-norm
 // + RoPE with the K/V rows written at their positions, the causal attention (matrix-core kernel
 // for 1, 2, 4 or 8 q heads per kv head), the O GEMM, add + RMSNorm, the gate/up GEMM, SwiGLU,
-// the down GEMM. Leaves the rows' residual and last delta for the final norm.
-x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n) {
+// the down GEMM. Leaves the rows' residual and last delta for the final norm. Sequence b: its
+// prompt row, position and KV pages.
+x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b = 0) {
     const Cfg& c = e->c;
-    if (e->chunk < 2 || n == 0 || n > e->chunk || pos0 + n > e->max_ctx)
+    if (e->chunk < 2 || n == 0 || n > e->chunk || pos0 + n > e->max_ctx || b >= e->max_batch)
         return fail(X0NE_ERR_FORMAT, "prefill: " + std::to_string(n) + " rows at " + std::to_string(pos0));
-    X0NE_TRY(set_position(e, pos0));
+    X0NE_TRY(set_position(e, pos0, b));
     const uint32_t rows = (uint32_t)n, h = (uint32_t)c.hidden, vocab = (uint32_t)c.vocab, inter = (uint32_t)c.inter;
     const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads, max_ctx = (uint32_t)e->max_ctx;
     const float eps = (float)c.eps, scale = (float)(1.0 / std::sqrt((double)c.head_dim));
     {
         const void* table = e->d(e->embed);
-        const void* toks = (const uint32_t*)e->d(e->prompt) + pos0;
+        const void* toks = e->prompt_of(b) + pos0;
         void* out = e->d(e->p_delta);
         void* args[] = {(void*)&table, (void*)&toks, (void*)&out, (void*)&h, (void*)&vocab};
         X0NE_TRY(launch_rows(e, (const void*)&x0ne_embedding_bf16, dim3(rows), dim3(128), args, "embedding"));
@@ -692,8 +722,8 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n) {
             void* q = e->d(e->p_q);
             void* kc = e->plane(l, 0);
             void* vc = e->plane(l, 1);
-            const void* pt = e->d(e->page_table);
-            const void* pos = e->d(e->pos);
+            const void* pt = e->pages_of(b);
+            const void* pos = e->pos_of(b);
             void* args[] = {(void*)&qkv, (void*)&qn, (void*)&kn, (void*)&inv, (void*)&q,       (void*)&kc, (void*)&vc,
                             (void*)&pt,  (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
             X0NE_TRY(launch_rows(e, (const void*)&x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, rows), dim3(64), args,
@@ -703,9 +733,9 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n) {
             const void* q = e->d(e->p_q);
             const void* kc = e->plane(l, 0);
             const void* vc = e->plane(l, 1);
-            const void* pt = e->d(e->page_table);
+            const void* pt = e->pages_of(b);
             void* out = e->d(e->p_attn);
-            const void* pos = e->d(e->pos);
+            const void* pos = e->pos_of(b);
             void* args[] = {(void*)&q,    (void*)&kc, (void*)&vc,  (void*)&pt,      (void*)&out, (void*)&pos,
                             (void*)&rows, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&scale};
             if (grouped) {
@@ -732,10 +762,11 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n) {
 }
 
 // The final norm and the LM head on row r of the last pass, at position p: f32 logits, the argmax
-// into tokens[0] and, with advance, pos = p + 1 for the decode step that follows.
-x0ne_status prefill_head(x0ne_engine* e, uint64_t r, uint64_t p, bool advance) {
+// into tokens[0] and, with advance, pos = p + 1 for the decode step that follows (sequence b's
+// token and position).
+x0ne_status prefill_head(x0ne_engine* e, uint64_t r, uint64_t p, bool advance, uint64_t b = 0) {
     const Cfg& c = e->c;
-    X0NE_TRY(set_position(e, p));
+    X0NE_TRY(set_position(e, p, b));
     X0neGemv hd = {};
     hd.w = (const uint16_t*)e->d(e->has_lm_head ? e->lm_head : e->embed);
     hd.res_in = (const float*)e->d(e->p_res) + r * c.hidden;
@@ -745,8 +776,8 @@ x0ne_status prefill_head(x0ne_engine* e, uint64_t r, uint64_t p, bool advance) {
     hd.y = e->d(e->logits);
     hd.partial = (float*)e->d(e->head_partial);
     hd.counter = (uint32_t*)e->d(e->head_counter);
-    hd.token_out = (uint32_t*)e->d(e->tokens);
-    hd.pos = (uint32_t*)e->d(e->pos);
+    hd.token_out = e->token_of(b);
+    hd.pos = e->pos_of(b);
     hd.advance = advance ? 1 : 0;
     hd.rows = (uint32_t)c.vocab;
     hd.cols = (uint32_t)c.hidden;
@@ -777,6 +808,7 @@ x0ne_status scrub(x0ne_engine* e) {
     if (e->host_logits) std::memset(e->host_logits, 0, e->c.vocab * 4);
     if (e->host_token) *e->host_token = 0;
     if (e->ring) std::memset(e->ring, 0, RING * 4);
+    if (e->bring) std::memset(e->bring, 0, RING * e->max_batch * 4);
     e->poisoned = false;
     return X0NE_OK;
 }
@@ -818,19 +850,24 @@ x0ne_status read_token(x0ne_engine* e, uint32_t* out) {
 // A prompt into the cache: passes of up to `chunk` rows, then the last row's logits and argmax
 // (engine.rs:408-425); tokens[0] holds the first generated token and pos the prompt's length.
 // With chunk 1 (the exact mode) one decode step per token.
+// The passes of sequence b's prompt (n ids, already in its prompt row) and its first token.
+x0ne_status prefill_passes(x0ne_engine* e, size_t n, uint64_t b) {
+    size_t start = 0;
+    for (;;) {
+        const size_t len = std::min<size_t>(e->chunk, n - start);
+        X0NE_TRY(prefill_pass(e, start, len, b));
+        if (start + len == n) return prefill_head(e, len - 1, n - 1, true, b);
+        start += len;
+    }
+}
+
 x0ne_status prefill(x0ne_engine* e, const uint32_t* ids, size_t n) {
     X0NE_TRY(put_prompt(e, ids, n));
     if (e->chunk < 2) {
         for (size_t i = 0; i < n; ++i) X0NE_TRY(feed(e, (uint32_t)i));
         return X0NE_OK;
     }
-    size_t start = 0;
-    for (;;) {
-        const size_t len = std::min<size_t>(e->chunk, n - start);
-        X0NE_TRY(prefill_pass(e, start, len));
-        if (start + len == n) return prefill_head(e, len - 1, n - 1, true);
-        start += len;
-    }
+    return prefill_passes(e, n, 0);
 }
 
 x0ne_status capture(x0ne_engine* e) {
@@ -893,7 +930,17 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
                             std::to_string(grp));
         }
     }
-    e->pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
+    e->max_batch = opts->max_batch ? opts->max_batch : 1;
+    if (e->max_batch > MAX_BATCH) {
+        delete e;
+        return fail(X0NE_ERR_FORMAT, "max_batch " + std::to_string(e->max_batch) + " above " + std::to_string(MAX_BATCH));
+    }
+    if (e->max_batch > 1 && e->f64_sums) {
+        delete e;
+        return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding with f64 sums");
+    }
+    e->seq_pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
+    e->pages = e->max_batch * e->seq_pages;
     x0ne_status st = x0ne_gpu_new(&e->gpu);
     if (st != X0NE_OK) {
         delete e;
@@ -904,6 +951,14 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
         return s;
     };
     if ((st = split_plan(e->gpu, (uint32_t)c.q_heads, (uint32_t)c.kv_heads, &e->split)) != X0NE_OK) return bail(st);
+    if (e->max_batch > 1) {
+        if (!e->split.grouped)
+            return bail(fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding needs 1, 2, 4 or 8 q heads per kv head"));
+        // The batched step's attention grid is max_batch times wider: fewer slices per sequence.
+        e->bsplit = e->split;
+        const uint64_t p = (uint64_t)e->gpu->cus * e->split.per_cu / (2 * e->split.grid_x * e->max_batch);
+        e->bsplit.splits = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(p, e->split.splits));
+    }
     if ((st = plan_grids(e)) != X0NE_OK) return bail(st);
     if ((st = x0ne_arena_new(&e->arena)) != X0NE_OK) return bail(st);
     if ((st = plan(e)) != X0NE_OK) return bail(st);
@@ -941,6 +996,10 @@ x0ne_status build_end(x0ne_engine* e) {
     X0NE_HIP(hipHostMalloc((void**)&e->host_logits, e->c.vocab * 4, hipHostMallocDefault), "pinned logits");
     X0NE_HIP(hipHostMalloc((void**)&e->host_token, 4, hipHostMallocDefault), "pinned token");
     std::memset(e->ring, 0, RING * 4);
+    if (e->max_batch > 1) {
+        X0NE_HIP(hipHostMalloc((void**)&e->bring, RING * e->max_batch * 4, hipHostMallocDefault), "pinned batch ring");
+        std::memset(e->bring, 0, RING * e->max_batch * 4);
+    }
     std::memset(e->host_logits, 0, e->c.vocab * 4);
     *e->host_token = 0;
     for (auto& ev : e->ring_ev) X0NE_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming), "ring event");
@@ -1321,6 +1380,240 @@ x0ne_status greedy_inner(x0ne_engine* e, const uint32_t* prompt, size_t np, size
     return X0NE_OK;
 }
 
+// ---- the batched step: B independent sequences, each weight read once for all of them ----
+
+// The launches of one batched decode step on sequences 0 .. B - 1, each at its own position with
+// its own token and KV pages: per layer add + RMSNorm (layer 0: the embedding row on a zero
+// residual), the QKV projection, the fused QK-norm + RoPE + K/V write + split-K attention over
+// each sequence's pages, the O projection, add + RMSNorm, the gate/up projection with SwiGLU
+// behind, the down projection; then the final norm, the f32 LM head and per sequence the
+// argmax into its token and its position + 1. The projections are the few-row GEMM (each weight
+// row read once for all B rows); the rounding points are those of the single-sequence step.
+// Add + RMSNorm of the B rows (residual += delta, normed x out).
+x0ne_status batch_norm(x0ne_engine* e, uint32_t B, x0ne_slice w) {
+    const uint32_t h = (uint32_t)e->c.hidden;
+    const float eps = (float)e->c.eps;
+    void* res = e->d(e->b_res);
+    const void* dl = e->d(e->b_delta);
+    const void* wp = e->d(w);
+    void* xn = e->d(e->b_x);
+    void* args[] = {(void*)&res, (void*)&dl, (void*)&wp, (void*)&xn, (void*)&h, (void*)&eps};
+    return launch_rows(e, (const void*)&x0ne_add_rmsnorm_bf16, dim3(B), dim3(256), args, "batch add_rmsnorm");
+}
+
+// Layer 0's norm: each sequence's embedding row on a zero residual.
+x0ne_status batch_embed_norm(x0ne_engine* e, uint32_t B) {
+    const uint32_t h = (uint32_t)e->c.hidden, vocab = (uint32_t)e->c.vocab;
+    const float eps = (float)e->c.eps;
+    const void* table = e->d(e->embed);
+    const void* toks = e->token_of(0);
+    void* res = e->d(e->b_res);
+    const void* wp = e->d(e->L[0].input_norm);
+    void* xn = e->d(e->b_x);
+    void* args[] = {(void*)&table, (void*)&toks, (void*)&res, (void*)&wp, (void*)&xn, (void*)&h, (void*)&vocab,
+                    (void*)&eps};
+    return launch_rows(e, (const void*)&x0ne_embed_rmsnorm_bf16, dim3(B), dim3(256), args, "batch embedding");
+}
+
+x0ne_status batch_qkv(x0ne_engine* e, uint32_t B, uint64_t l) {
+    const Cfg& c = e->c;
+    return skinny(e->gpu, e->d(e->L[l].qkv), c.qkv_rows(), c.hidden, e->d(e->b_x), B, e->d(e->b_qkv), 0);
+}
+
+x0ne_status batch_attention(x0ne_engine* e, uint32_t B, uint64_t l) {
+    const Cfg& c = e->c;
+    const void* kern = nullptr;
+    switch (e->bsplit.group) {
+        case 1: kern = (const void*)&x0ne_attention_rope_decode_batch_g1_bf16; break;
+        case 2: kern = (const void*)&x0ne_attention_rope_decode_batch_g2_bf16; break;
+        case 4: kern = (const void*)&x0ne_attention_rope_decode_batch_g4_bf16; break;
+        case 8: kern = (const void*)&x0ne_attention_rope_decode_batch_g8_bf16; break;
+        default: return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched attention for this group size");
+    }
+    const LayerW& w = e->L[l];
+    const void* qkv = e->d(e->b_qkv);
+    const void* qn = e->d(w.q_norm);
+    const void* kn = e->d(w.k_norm);
+    const void* inv = e->d(e->inv_freq);
+    const void* cs = e->d(e->rope_cs);
+    void* kc = e->plane(l, 0);
+    void* vc = e->plane(l, 1);
+    const void* pt = e->d(e->page_table);
+    void* st = e->d(e->b_state);
+    void* cnt = e->d(e->b_counter);
+    void* out = e->d(e->b_attn);
+    const void* pos = e->d(e->pos);
+    uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads, max_ctx = (uint32_t)e->max_ctx;
+    uint32_t P = e->bsplit.splits, sp = (uint32_t)e->seq_pages;
+    float scale = (float)(1.0 / std::sqrt((double)c.head_dim)), eps = (float)c.eps;
+    void* args[] = {(void*)&qkv, (void*)&qn,  (void*)&kn,      (void*)&inv, (void*)&cs,    (void*)&kc, (void*)&vc,
+                    (void*)&pt,  (void*)&st,  (void*)&cnt,     (void*)&out, (void*)&pos,   (void*)&qh, (void*)&kvh,
+                    (void*)&max_ctx, (void*)&P, (void*)&scale, (void*)&eps, (void*)&sp};
+    return launch_rows(e, kern, dim3(kvh, P, B), dim3(256), args, "batch attention");
+}
+
+x0ne_status batch_o(x0ne_engine* e, uint32_t B, uint64_t l) {
+    const Cfg& c = e->c;
+    return skinny(e->gpu, e->d(e->L[l].o), c.hidden, c.q_dim(), e->d(e->b_attn), B, e->d(e->b_delta), 0);
+}
+
+x0ne_status batch_gate_up(x0ne_engine* e, uint32_t B, uint64_t l) {
+    const Cfg& c = e->c;
+    return skinny(e->gpu, e->d(e->L[l].gate_up), c.inter, c.hidden, e->d(e->b_x), B, e->d(e->b_act), 2);
+}
+
+x0ne_status batch_down(x0ne_engine* e, uint32_t B, uint64_t l) {
+    const Cfg& c = e->c;
+    return skinny(e->gpu, e->d(e->L[l].down), c.hidden, c.inter, e->d(e->b_act), B, e->d(e->b_delta), 0);
+}
+
+// The f32 LM head over the B normed rows, then each row's argmax into its token, position + 1.
+x0ne_status batch_head(x0ne_engine* e, uint32_t B) {
+    const Cfg& c = e->c;
+    X0NE_TRY(skinny(e->gpu, e->d(e->has_lm_head ? e->lm_head : e->embed), c.vocab, c.hidden, e->d(e->b_x), B,
+                    e->d(e->b_logits), 1));
+    const void* lg = e->d(e->b_logits);
+    uint32_t vocab = (uint32_t)c.vocab;
+    void* toks = e->token_of(0);
+    void* pos = e->pos_of(0);
+    void* args[] = {(void*)&lg, (void*)&vocab, (void*)&toks, (void*)&pos};
+    return launch_rows(e, (const void*)&x0ne_argmax_advance_f32, dim3(B), dim3(1024), args, "batch argmax");
+}
+
+// The launches of one batched decode step on sequences 0 .. B - 1, each at its own position with
+// its own token and KV pages: per layer add + RMSNorm (layer 0: the embedding row on a zero
+// residual), the QKV projection, the fused QK-norm + RoPE + K/V write + split-K attention over
+// each sequence's pages, the O projection, add + RMSNorm, the gate/up projection with SwiGLU
+// behind, the down projection; then the final norm, the f32 LM head and per sequence the
+// argmax into its token and its position + 1. The projections are the few-row GEMM (each weight
+// row read once for all B rows); the rounding points are those of the single-sequence step.
+x0ne_status batch_step_launches(x0ne_engine* e, uint32_t B) {
+    for (uint64_t l = 0; l < e->c.layers; ++l) {
+        X0NE_TRY(l == 0 ? batch_embed_norm(e, B) : batch_norm(e, B, e->L[l].input_norm));
+        X0NE_TRY(batch_qkv(e, B, l));
+        X0NE_TRY(batch_attention(e, B, l));
+        X0NE_TRY(batch_o(e, B, l));
+        X0NE_TRY(batch_norm(e, B, e->L[l].post_norm));
+        X0NE_TRY(batch_gate_up(e, B, l));
+        X0NE_TRY(batch_down(e, B, l));
+    }
+    X0NE_TRY(batch_norm(e, B, e->final_norm));
+    return batch_head(e, B);
+}
+
+// The batched step's graph for B sequences, captured as the single-sequence one is (an eager
+// step on zeroed client buffers first); the client bytes are zeroed after, so this runs before
+// any sequence is prefilled.
+x0ne_status batch_capture(x0ne_engine* e, uint32_t B) {
+    if (e->bgraph && e->bgraph_batch == B) return X0NE_OK;
+    X0NE_TRY(batch_step_launches(e, B));
+    X0NE_TRY(x0ne_gpu_sync(e->gpu));
+    if (e->bgraph) {
+        x0ne_graph_free(e->bgraph);
+        e->bgraph = nullptr;
+        e->bgraph_batch = 0;
+    }
+    X0NE_TRY(x0ne_gpu_capture_begin(e->gpu));
+    x0ne_status st = batch_step_launches(e, B);
+    x0ne_graph* gr = nullptr;
+    x0ne_status st2 = x0ne_gpu_capture_end(e->gpu, &gr);
+    if (st != X0NE_OK) {
+        if (gr) x0ne_graph_free(gr);
+        return st;
+    }
+    X0NE_TRY(st2);
+    e->bgraph = gr;
+    e->bgraph_batch = B;
+    return x0ne_arena_scrub(e->arena, nullptr);
+}
+
+// The B token words into ring slot j % RING, then its event.
+x0ne_status batch_ring_fetch(x0ne_engine* e, size_t j, uint32_t B) {
+    e->gpu->counts.dtoh++;
+    X0NE_HIP(hipMemcpyAsync(e->bring + (j % RING) * e->max_batch, e->token_of(0), B * 4, hipMemcpyDeviceToHost,
+                            e->gpu->stream),
+             "batch ring copy");
+    X0NE_HIP(hipEventRecord(e->ring_ev[j % RING], e->gpu->stream), "ring event");
+    return X0NE_OK;
+}
+
+// Step j's tokens out of the ring into column j of the [B][n] token rows.
+x0ne_status batch_ring_take(x0ne_engine* e, size_t j, uint32_t B, size_t n, uint32_t* out) {
+    X0NE_HIP(hipEventSynchronize(e->ring_ev[j % RING]), "ring wait");
+    for (uint32_t b = 0; b < B; ++b) {
+        const uint32_t t = e->bring[(j % RING) * e->max_batch + b];
+        if (t >= e->c.vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
+        out[b * n + j] = t;
+    }
+    return X0NE_OK;
+}
+
+x0ne_status batch_checks(x0ne_engine* e, const uint32_t* prompts, size_t np, size_t B, size_t n) {
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    if (e->poisoned) X0NE_TRY(scrub(e));
+    if (B == 0 || B > e->max_batch)
+        return fail(X0NE_ERR_FORMAT, "batch " + std::to_string(B) + " for max_batch " + std::to_string(e->max_batch));
+    if (e->chunk < 2 || e->max_batch < 2)
+        return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding needs an engine loaded with max_batch > 1");
+    if (!prompts) return fail(X0NE_ERR_FORMAT, "null argument");
+    for (size_t b = 0; b < B; ++b) X0NE_TRY(check_ids(e, prompts + b * np, np));
+    if (n == 0 || np + n - 1 > e->max_ctx)
+        return fail(X0NE_ERR_FORMAT, std::to_string(np) + " + " + std::to_string(n) + " tokens exceed max_ctx " +
+                                         std::to_string(e->max_ctx));
+    return X0NE_OK;
+}
+
+// The batch's graph (or nothing in eager mode), the prompts into their rows and their passes,
+// and each sequence's first token into column 0 of tokens ([B][n]).
+x0ne_status batch_prefill(x0ne_engine* e, const uint32_t* prompts, size_t np, uint32_t B, size_t n, uint32_t* tokens) {
+    if (e->mode == X0NE_DECODE_GRAPH) X0NE_TRY(batch_capture(e, B));
+    for (uint32_t b = 0; b < B; ++b)
+        X0NE_TRY(x0ne_arena_write(e->arena, e->prompt, (uint64_t)b * e->max_ctx * 4, prompts + (size_t)b * np, np * 4));
+    for (uint32_t b = 0; b < B; ++b) {
+        X0NE_TRY(prefill_passes(e, np, b));
+        // Its logits row where the batched step leaves the others' (the last token's logits of a
+        // one-token request).
+        X0NE_HIP(hipMemcpyAsync(e->d(e->b_logits) + (uint64_t)b * e->c.vocab * 4, e->d(e->logits), e->c.vocab * 4,
+                                hipMemcpyDeviceToDevice, e->gpu->stream),
+                 "first logits");
+    }
+    std::vector<uint32_t> first(B);
+    X0NE_TRY(x0ne_arena_read(e->arena, e->tokens, 0, first.data(), B * 4));
+    for (uint32_t b = 0; b < B; ++b) {
+        if (first[b] >= e->c.vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
+        tokens[b * n] = first[b];
+    }
+    return X0NE_OK;
+}
+
+x0ne_status batch_run_step(x0ne_engine* e, uint32_t B) {
+    if (e->mode == X0NE_DECODE_GRAPH) {
+        if (!e->bgraph || e->bgraph_batch != B) return fail(X0NE_ERR_GPU, "no batched decode graph captured");
+        return x0ne_gpu_launch_graph(e->gpu, e->bgraph);
+    }
+    return batch_step_launches(e, B);
+}
+
+// Decode steps first .. last (each one launch and one copy of B words, up to RING - 1 in
+// flight), collecting column j of tokens ([B][n]) as step j's words arrive.
+x0ne_status batch_steps(x0ne_engine* e, uint32_t B, size_t first, size_t last, size_t n, uint32_t* tokens,
+                        const std::function<void(size_t)>& arrived) {
+    size_t next = first;
+    for (size_t i = first; i <= last; ++i) {
+        X0NE_TRY(batch_run_step(e, B));
+        X0NE_TRY(batch_ring_fetch(e, i, B));
+        if (i + 1 - next >= RING - 1) {
+            X0NE_TRY(batch_ring_take(e, next, B, n, tokens));
+            arrived(next++);
+        }
+    }
+    while (next <= last) {
+        X0NE_TRY(batch_ring_take(e, next, B, n, tokens));
+        arrived(next++);
+    }
+    return X0NE_OK;
+}
+
 x0ne_status greedy_checks(x0ne_engine* e, const uint32_t* prompt, size_t np, size_t n) {
     if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
     if (e->poisoned) X0NE_TRY(scrub(e));
@@ -1375,6 +1668,50 @@ extern "C" x0ne_status x0ne_engine_decode_timed(x0ne_engine* e, const uint32_t* 
         X0NE_TRY(x0ne_gpu_sync(e->gpu));
         const auto t0 = std::chrono::steady_clock::now();
         X0NE_TRY(run(warmup + 1, warmup + steps));
+        *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        return X0NE_OK;
+    };
+    x0ne_status st = body();
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
+extern "C" x0ne_status x0ne_engine_greedy_batch(x0ne_engine* e, const uint32_t* prompts, size_t np, size_t batch,
+                                                size_t n, uint32_t* tokens, double* times, float* last_logits) {
+    if (!e || !tokens) return fail(X0NE_ERR_FORMAT, "null argument");
+    X0NE_TRY(batch_checks(e, prompts, np, batch, n));
+    const uint32_t B = (uint32_t)batch;
+    const auto t0 = std::chrono::steady_clock::now();
+    auto now = [&]() { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); };
+    auto body = [&]() -> x0ne_status {
+        X0NE_TRY(batch_prefill(e, prompts, np, B, n, tokens));
+        if (times) times[0] = now();
+        if (n > 1)
+            X0NE_TRY(batch_steps(e, B, 1, n - 1, n, tokens, [&](size_t j) {
+                if (times) times[j] = now();
+            }));
+        if (!last_logits) return X0NE_OK;
+        return x0ne_arena_read(e->arena, e->b_logits, 0, last_logits, (uint64_t)B * e->c.vocab * 4);
+    };
+    x0ne_status st = body();
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
+extern "C" x0ne_status x0ne_engine_decode_batch_timed(x0ne_engine* e, const uint32_t* prompts, size_t np, size_t batch,
+                                                      size_t warmup, size_t steps, uint32_t* tokens, double* seconds) {
+    if (!e || !tokens || !seconds || steps == 0) return fail(X0NE_ERR_FORMAT, "null argument");
+    const size_t n = warmup + steps + 1;
+    X0NE_TRY(batch_checks(e, prompts, np, batch, n));
+    const uint32_t B = (uint32_t)batch;
+    auto body = [&]() -> x0ne_status {
+        X0NE_TRY(batch_prefill(e, prompts, np, B, n, tokens));
+        auto none = [](size_t) {};
+        if (warmup) X0NE_TRY(batch_steps(e, B, 1, warmup, n, tokens, none));
+        X0NE_TRY(x0ne_gpu_sync(e->gpu));
+        const auto t0 = std::chrono::steady_clock::now();
+        X0NE_TRY(batch_steps(e, B, warmup + 1, warmup + steps, n, tokens, none));
+        X0NE_TRY(x0ne_gpu_sync(e->gpu));
         *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
         return X0NE_OK;
     };
@@ -1480,12 +1817,26 @@ extern "C" x0ne_status x0ne_engine_counts(const x0ne_engine* e, x0ne_counts* out
     return x0ne_gpu_counts(e->gpu, out);
 }
 
-extern "C" x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* kernel_us,
-                                              double* wall_us, uint64_t* launches) {
+namespace {
+
+x0ne_status time_kernel(x0ne_engine* e, uint32_t which, uint32_t batch, uint32_t iters, double* kernel_us,
+                        double* wall_us, uint64_t* launches) {
     if (!e || iters == 0) return fail(X0NE_ERR_FORMAT, "null argument");
     if (which > X0NE_KERNEL_HEAD) return fail(X0NE_ERR_FORMAT, "unknown kernel");
     if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    if (batch > 0 && (batch > e->max_batch || e->max_batch < 2))
+        return fail(X0NE_ERR_FORMAT, "batch " + std::to_string(batch) + " for max_batch " + std::to_string(e->max_batch));
     auto one = [&](uint64_t l) -> x0ne_status {
+        if (batch > 0) {
+            switch (which) {
+                case X0NE_KERNEL_QKV: return batch_qkv(e, batch, l);
+                case X0NE_KERNEL_ATTENTION: return batch_attention(e, batch, l);
+                case X0NE_KERNEL_O: return batch_o(e, batch, l);
+                case X0NE_KERNEL_GATE_UP: return batch_gate_up(e, batch, l);
+                case X0NE_KERNEL_DOWN: return batch_down(e, batch, l);
+                default: return batch_head(e, batch);
+            }
+        }
         switch (which) {
             case X0NE_KERNEL_QKV: return launch_qkv(e, e->c.layers > 1 ? l + 1 : 0);
             case X0NE_KERNEL_ATTENTION: return launch_attention(e, l);
@@ -1534,6 +1885,19 @@ extern "C" x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, u
     return sc;
 }
 
+}  // namespace
+
+extern "C" x0ne_status x0ne_engine_time_kernel(x0ne_engine* e, uint32_t which, uint32_t iters, double* kernel_us,
+                                              double* wall_us, uint64_t* launches) {
+    return time_kernel(e, which, 0, iters, kernel_us, wall_us, launches);
+}
+
+extern "C" x0ne_status x0ne_engine_time_batch_kernel(x0ne_engine* e, uint32_t which, uint32_t batch, uint32_t iters,
+                                                    double* kernel_us, double* wall_us, uint64_t* launches) {
+    if (batch == 0) return fail(X0NE_ERR_FORMAT, "batch 0");
+    return time_kernel(e, which, batch, iters, kernel_us, wall_us, launches);
+}
+
 extern "C" x0ne_status x0ne_engine_page(const x0ne_engine* e, uint64_t i, uint32_t* out) {
     if (!e || !out || i >= e->pages) return fail(X0NE_ERR_FORMAT, "no such page");
     *out = e->page_of[i];
@@ -1567,5 +1931,7 @@ extern "C" int x0ne_engine_host_buffers_are_zero(const x0ne_engine* e) {
     if (*e->host_token) return 0;
     for (size_t i = 0; i < RING; ++i)
         if (e->ring[i]) return 0;
+    for (size_t i = 0; e->bring && i < RING * e->max_batch; ++i)
+        if (e->bring[i]) return 0;
     return 1;
 }

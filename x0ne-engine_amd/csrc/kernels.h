@@ -37,6 +37,11 @@ __global__ void x0ne_attention_decode_split_bf16(const bf16_t* q, const bf16_t* 
         const double* rope_cs, bf16_t* k_cache, bf16_t* v_cache, const uint32_t* pages, float* state,           \
         uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads,                \
         uint32_t max_ctx, uint32_t splits, float scale, float eps);                                              \
+    __global__ void x0ne_attention_rope_decode_batch_g##G##_bf16(                                               \
+        const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq,                    \
+        const double* rope_cs, bf16_t* k_cache, bf16_t* v_cache, const uint32_t* pages, float* state,           \
+        uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads,                \
+        uint32_t max_ctx, uint32_t splits, float scale, float eps, uint32_t seq_pages);                          \
     __global__ void x0ne_attention_rope_decode_exact_g##G##_bf16(                                               \
         const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq, bf16_t* k_cache,  \
         bf16_t* v_cache, const uint32_t* pages, bf16_t* out, const uint32_t* pos, uint32_t q_heads,              \
@@ -64,10 +69,20 @@ X0NE_DECLARE_PREFILL_GROUP(8)
 #undef X0NE_DECLARE_PREFILL_GROUP
 __global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
 __global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
+__global__ void x0ne_argmax_advance_f32(const float* logits, uint32_t n, uint32_t* tokens, uint32_t* pos);
+__global__ void x0ne_embed_rmsnorm_bf16(const bf16_t* table, const uint32_t* tokens, float* residual,
+                                        const bf16_t* w, bf16_t* out, uint32_t hidden, uint32_t vocab, float eps);
 __global__ void x0ne_advance_u32(uint32_t* pos);
 __global__ void x0ne_feed_u32(const uint32_t* ids, uint32_t i, uint32_t* tokens, uint32_t* pos);
 __global__ void x0ne_gemm_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, uint32_t n,
                                uint32_t out_f32);
+#define X0NE_DECLARE_SKINNY(N)                                                                                   \
+    __global__ void x0ne_gemm_skinny##N##_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows,         \
+                                               uint32_t cols, uint32_t n, uint32_t mode);
+X0NE_DECLARE_SKINNY(16)
+X0NE_DECLARE_SKINNY(32)
+X0NE_DECLARE_SKINNY(64)
+#undef X0NE_DECLARE_SKINNY
 __global__ void x0ne_gemv_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_f32(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_any(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols,

@@ -63,6 +63,29 @@ extern "C" __global__ void __launch_bounds__(256)
         out[base + i] = f2bf((float)((double)residual[base + i] * scale * (double)bf2f(w[i])));
 }
 
+// The first norm of a batched step: residual[r] = 0 + table[tokens[r]] (f32; an id >= vocab gives
+// a zero row) and out[r] its RMSNorm, the bits x0ne_embedding_bf16 followed by
+// x0ne_add_rmsnorm_bf16 on a zero residual give. grid (rows), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_embed_rmsnorm_bf16(const bf16_t* __restrict__ table, const uint32_t* __restrict__ tokens,
+                            float* __restrict__ residual, const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
+                            uint32_t hidden, uint32_t vocab, float eps) {
+    __shared__ double sh[16];
+    const size_t base = (size_t)blockIdx.x * hidden;
+    const uint32_t tok = tokens[blockIdx.x];
+    const bf16_t* src = table + (size_t)(tok < vocab ? tok : 0) * hidden;
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) {
+        const float r = 0.0f + (tok < vocab ? bf2f(src[i]) : 0.0f);
+        residual[base + i] = r;
+        ss += (double)r * (double)r;
+    }
+    const double total = block_sum_d(ss, sh);
+    const double scale = 1.0 / sqrt(total / (double)hidden + (double)eps);
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x)
+        out[base + i] = f2bf((float)((double)residual[base + i] * scale * (double)bf2f(w[i])));
+}
+
 // Per-head RMSNorm of q and k, rotate-half RoPE, and the K/V write into the paged cache
 // (rope.cu:7-47; oracle/src/lib.rs:82-120). grid (q_heads + kv_heads, rows), block 64: lane i
 // owns the pair (i, i + 64) of one head. Row r sits at position pos0[0] + r, written at
@@ -142,14 +165,12 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);
 }
 
-// Greedy pick (argmax.cu:11-58): index of the largest logit of each row, lowest index on ties;
-// a row holding any NaN yields 0xFFFFFFFF. grid (rows), block 1024 (16 wavefronts).
-extern "C" __global__ void __launch_bounds__(1024)
-    x0ne_argmax_f32(const float* __restrict__ logits, uint32_t n, uint32_t* __restrict__ out) {
+// The first largest value's index of row[0 .. n), or 0xFFFFFFFF when the row holds a NaN, for
+// thread 0 of a block of whole wavefronts (at most 16).
+__device__ __forceinline__ uint32_t argmax_row(const float* __restrict__ row, uint32_t n) {
     __shared__ float sv[16];
     __shared__ uint32_t si[16];
     __shared__ int snan;
-    const float* row = logits + (size_t)blockIdx.x * n;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
     if (t == 0) snan = 0;
     __syncthreads();
@@ -179,16 +200,36 @@ extern "C" __global__ void __launch_bounds__(1024)
         si[wave] = bi;
     }
     __syncthreads();
+    float fv = -INFINITY;
+    uint32_t fi = 0xFFFFFFFFu;
     if (t == 0) {
-        float fv = -INFINITY;
-        uint32_t fi = 0xFFFFFFFFu;
         for (uint32_t w = 0; w < nw; ++w) {
             if (better(sv[w], si[w], fv, fi)) {
                 fv = sv[w];
                 fi = si[w];
             }
         }
-        out[blockIdx.x] = snan ? 0xFFFFFFFFu : fi;
+    }
+    return snan ? 0xFFFFFFFFu : fi;
+}
+
+// Greedy pick (argmax.cu:11-58): index of the largest logit of each row, lowest index on ties;
+// a row holding any NaN yields 0xFFFFFFFF. grid (rows), block 1024 (16 wavefronts).
+extern "C" __global__ void __launch_bounds__(1024)
+    x0ne_argmax_f32(const float* __restrict__ logits, uint32_t n, uint32_t* __restrict__ out) {
+    const uint32_t i = argmax_row(logits + (size_t)blockIdx.x * n, n);
+    if (threadIdx.x == 0) out[blockIdx.x] = i;
+}
+
+// The batched step's pick and advance: tokens[r] = the argmax of logits row r (as
+// x0ne_argmax_f32), pos[r] += 1. grid (rows), block 1024.
+extern "C" __global__ void __launch_bounds__(1024)
+    x0ne_argmax_advance_f32(const float* __restrict__ logits, uint32_t n, uint32_t* __restrict__ tokens,
+                            uint32_t* __restrict__ pos) {
+    const uint32_t i = argmax_row(logits + (size_t)blockIdx.x * n, n);
+    if (threadIdx.x == 0) {
+        tokens[blockIdx.x] = i;
+        pos[blockIdx.x] += 1u;
     }
 }
 

@@ -212,11 +212,12 @@ hipError_t x0ne_launch(const void* fn, dim3 grid, dim3 block, void** args, size_
 namespace x0ne {
 
 x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32_t gy, uint32_t block,
-                           const x0ne_arg* args, size_t n) {
+                           const x0ne_arg* args, size_t n, uint32_t gz) {
     X0NE_TRY(check_args_of(k, args, n));
-    if (gx == 0 || gy == 0 || block == 0 || block > k.max_block || block % 64 != 0)
+    if (gx == 0 || gy == 0 || gz == 0 || block == 0 || block > k.max_block || block % 64 != 0)
         return fail(X0NE_ERR_GPU, std::string(k.name) + ": launch shape (" + std::to_string(gx) + ", " +
-                                      std::to_string(gy) + ") x " + std::to_string(block) + " refused");
+                                      std::to_string(gy) + ", " + std::to_string(gz) + ") x " + std::to_string(block) +
+                                      " refused");
     void* ptrs[24];
     if (n > 24) return fail(X0NE_ERR_GPU, "too many arguments");
     for (size_t i = 0; i < n; ++i) {
@@ -227,7 +228,7 @@ x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32
         }
     }
     g->counts.launches++;
-    X0NE_HIP(hipLaunchKernel(k.fn, dim3(gx, gy), dim3(block), ptrs, 0, g->stream), k.name);
+    X0NE_HIP(hipLaunchKernel(k.fn, dim3(gx, gy, gz), dim3(block), ptrs, 0, g->stream), k.name);
     return X0NE_OK;
 }
 
@@ -241,11 +242,45 @@ extern "C" x0ne_status x0ne_gpu_launch(x0ne_gpu* g, const char* name, uint32_t g
     return launch_checked(g, *k, gx, gy, block, args, n);
 }
 
-// Gpu::gemm (gpu.rs:1098-1149) at n = 1 per launch: the bandwidth-bound GEMV of gemv.hip.
-// From this many rows of X on, x0ne_gpu_gemv is one matrix-core GEMM (gemm.hip) rather than a
-// GEMV per row; its buffer offsets are 32-bit.
-static constexpr uint64_t GEMM_MIN_ROWS = 4;
+extern "C" x0ne_status x0ne_gpu_launch_3d(x0ne_gpu* g, const char* name, uint32_t gx, uint32_t gy, uint32_t gz,
+                                          uint32_t block, const x0ne_arg* args, size_t n) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    const X0neKernel* k = find_kernel(name);
+    if (!k) return fail(X0NE_ERR_GPU, std::string("no kernel ") + (name ? name : "(null)"));
+    return launch_checked(g, *k, gx, gy, block, args, n, gz);
+}
+
+// Gpu::gemm (gpu.rs:1098-1149). One row: the bandwidth-bound GEMV of gemv.hip. Two to 64 rows:
+// the few-row kernel of gemm.hip, still bandwidth-bound (each W row read once). More: the tiled
+// matrix-core GEMM. The kernels of gemm.hip take 32-bit buffer offsets.
+static constexpr uint64_t SKINNY_MAX_ROWS = 64;
 static constexpr uint64_t GEMM_MAX_BYTES = 0xFFFFFFF0ull;
+
+namespace x0ne {
+
+x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
+                   uint32_t mode) {
+    const uint64_t wrows = mode == 2 ? 2 * rows : rows;
+    if (n == 0 || n > SKINNY_MAX_ROWS || rows == 0 || cols == 0 || cols % 8 != 0 || mode > 2 ||
+        wrows * cols * 2 > GEMM_MAX_BYTES || n * cols * 2 > GEMM_MAX_BYTES || (uintptr_t)w % 16 != 0 ||
+        (uintptr_t)x % 16 != 0)
+        return fail(X0NE_ERR_FORMAT, "few-row gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
+                                         std::to_string(n) + ", mode " + std::to_string(mode));
+    const uint32_t blocks = (uint32_t)((rows + 15) / 16);
+    // Eight wavefronts per block while the launch would hold fewer than 12 per CU at four.
+    const uint32_t waves = (uint64_t)blocks * 4 < 12ull * g->cus ? 8 : 4;
+    const void* fn = n <= 16 ? (const void*)&x0ne_gemm_skinny16_bf16
+                     : n <= 32 ? (const void*)&x0ne_gemm_skinny32_bf16
+                               : (const void*)&x0ne_gemm_skinny64_bf16;
+    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n;
+    void* args[] = {(void*)&w, (void*)&x, (void*)&y, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&mode};
+    g->counts.gemms++;
+    g->counts.launches++;
+    X0NE_HIP(x0ne_launch(fn, dim3(blocks), dim3(64 * waves), args, 0, g->stream), "few-row gemm");
+    return X0NE_OK;
+}
+
+}  // namespace x0ne
 
 extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n,
                                      uint64_t y, int out_f32) {
@@ -254,8 +289,11 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
         return fail(X0NE_ERR_FORMAT, "gemv: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
                                          std::to_string(n));
     const uint64_t ob = out_f32 ? 4 : 2;
-    // Several rows: one matrix-core GEMM launch, the weights read once.
-    if (n >= GEMM_MIN_ROWS && cols % 8 == 0 && n <= UINT32_MAX && rows * cols * 2 <= GEMM_MAX_BYTES &&
+    if (n >= 2 && n <= SKINNY_MAX_ROWS && cols % 8 == 0 && rows * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 &&
+        x % 16 == 0)
+        return x0ne::skinny(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 ? 1 : 0);
+    // Many rows: one matrix-core GEMM launch, the weights read once.
+    if (n > SKINNY_MAX_ROWS && cols % 8 == 0 && n <= UINT32_MAX && rows * cols * 2 <= GEMM_MAX_BYTES &&
         n * cols * 2 <= GEMM_MAX_BYTES) {
         g->counts.gemms++;
         g->counts.launches++;

@@ -68,7 +68,7 @@ class SplitPlanC(C.Structure):
 
 class EngineOptionsC(C.Structure):
     _fields_ = [("max_ctx", C.c_uint64), ("page_seed", C.c_uint64), ("f64_sums", C.c_uint32),
-                ("prefill_chunk", C.c_uint32)]
+                ("prefill_chunk", C.c_uint32), ("max_batch", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 _lib = None
@@ -92,6 +92,7 @@ SIGNATURES = {
     "x0ne_kernel_params": ([C.c_char_p, C.POINTER(U32), SZ], SZ),
     "x0ne_check_args": ([C.c_char_p, C.POINTER(ArgC), SZ], ST),
     "x0ne_gpu_launch": ([P, C.c_char_p, U32, U32, U32, C.POINTER(ArgC), SZ], ST),
+    "x0ne_gpu_launch_3d": ([P, C.c_char_p, U32, U32, U32, U32, C.POINTER(ArgC), SZ], ST),
     "x0ne_gpu_gemv": ([P, U64, U64, U64, U64, U64, U64, I32], ST),
     "x0ne_gpu_split_plan": ([P, U32, U32, C.POINTER(SplitPlanC)], ST),
     "x0ne_gpu_attention_split": ([P, C.POINTER(SplitPlanC), I32, U64, U64, U64, U64, U64, U64, U64, U64,
@@ -136,6 +137,8 @@ SIGNATURES = {
     "x0ne_engine_greedy_timed": ([P, C.POINTER(U32), SZ, SZ, C.POINTER(U32), C.POINTER(F64)], ST),
     "x0ne_engine_greedy_with_last_logits": ([P, C.POINTER(U32), SZ, SZ, C.POINTER(U32), C.POINTER(F32)], ST),
     "x0ne_engine_decode_timed": ([P, C.POINTER(U32), SZ, SZ, SZ, C.POINTER(U32), C.POINTER(F64)], ST),
+    "x0ne_engine_greedy_batch": ([P, C.POINTER(U32), SZ, SZ, SZ, C.POINTER(U32), C.POINTER(F64), C.POINTER(F32)], ST),
+    "x0ne_engine_decode_batch_timed": ([P, C.POINTER(U32), SZ, SZ, SZ, SZ, C.POINTER(U32), C.POINTER(F64)], ST),
     "x0ne_engine_set_decode_mode": ([P, U32], ST),
     "x0ne_engine_decode_mode": ([P], U32),
     "x0ne_engine_logits_at": ([P, C.POINTER(U32), SZ, C.POINTER(SZ), SZ, U32, C.POINTER(F32)], ST),
@@ -149,6 +152,7 @@ SIGNATURES = {
     "x0ne_engine_arena": ([P], P),
     "x0ne_engine_page": ([P, U64, C.POINTER(U32)], ST),
     "x0ne_engine_time_kernel": ([P, U32, U32, C.POINTER(F64), C.POINTER(F64), C.POINTER(U64)], ST),
+    "x0ne_engine_time_batch_kernel": ([P, U32, U32, U32, C.POINTER(F64), C.POINTER(F64), C.POINTER(U64)], ST),
 }
 
 

@@ -13,7 +13,7 @@ from enum import IntEnum
 
 import numpy as np
 
-from ._lib import Counts, EngineOptionsC, check, lib
+from ._lib import Counts, EngineOptionsC, FormatError, check, lib
 
 GREEDY_AHEAD = 2  # engine.rs:78
 GREEDY_AHEAD_MAX = 15  # engine.rs:73
@@ -32,15 +32,18 @@ class DecodeMode(IntEnum):
 @dataclass
 class EngineOptions:
     """EngineOptions (engine.rs:38-40) plus the KV page order (0: identity, else a seeded
-    shuffle), the projections' summation (f32 FMA, or each exact product added in f64) and the
-    prompt rows per prefill pass (0: min(2048, max_ctx))."""
+    shuffle), the projections' summation (f32 FMA, or each exact product added in f64), the
+    prompt rows per prefill pass (0: min(2048, max_ctx)) and the sequences the batched greedy
+    entry points serve (0 or 1: one)."""
     max_ctx: int
     page_seed: int = 0
     f64_sums: bool = False
     prefill_chunk: int = 0
+    max_batch: int = 0
 
     def c(self):
-        return EngineOptionsC(self.max_ctx, self.page_seed, int(self.f64_sums), int(self.prefill_chunk))
+        return EngineOptionsC(self.max_ctx, self.page_seed, int(self.f64_sums), int(self.prefill_chunk),
+                              int(self.max_batch), 0)
 
 
 def _ids(ids):
@@ -128,6 +131,34 @@ class Engine:
     def greedy(self, prompt, n: int) -> np.ndarray:
         return self.greedy_timed(prompt, n)[0]
 
+    def greedy_batch(self, prompts, n: int, logits: bool = False):
+        """Greedy decoding of independent prompts (rows of equal length) at once: tokens
+        [batch][n], per-step host times, and with `logits` each sequence's last logits row."""
+        a = np.ascontiguousarray(prompts, dtype=np.uint32)
+        if a.ndim != 2:
+            raise FormatError("prompts: one row per sequence")
+        b, np_ = a.shape
+        toks = np.zeros((b, n), np.uint32)
+        times = np.zeros(n, np.float64)
+        rows = np.zeros((b, self.vocab_size), np.float32) if logits else None
+        check(lib().x0ne_engine_greedy_batch(
+            self.h, a.ctypes.data_as(C.POINTER(C.c_uint32)), np_, b, n, toks.ctypes.data_as(C.POINTER(C.c_uint32)),
+            times.ctypes.data_as(C.POINTER(C.c_double)),
+            rows.ctypes.data_as(C.POINTER(C.c_float)) if logits else None), "greedy_batch")
+        return (toks, times, rows) if logits else (toks, times)
+
+    def decode_batch_timed(self, prompts, warmup: int, steps: int):
+        """decode_timed for independent prompts at once: (tokens [batch][warmup + steps + 1],
+        seconds of the timed steps)."""
+        a = np.ascontiguousarray(prompts, dtype=np.uint32)
+        b, np_ = a.shape
+        toks = np.zeros((b, warmup + steps + 1), np.uint32)
+        secs = C.c_double()
+        check(lib().x0ne_engine_decode_batch_timed(self.h, a.ctypes.data_as(C.POINTER(C.c_uint32)), np_, b, warmup,
+                                                   steps, toks.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                                   C.byref(secs)), "decode_batch_timed")
+        return toks, secs.value
+
     def greedy_with_last_logits(self, prompt, n: int):
         a, p = _ids(prompt)
         toks = np.zeros(n, np.uint32)
@@ -190,13 +221,18 @@ class Engine:
 
     KERNELS = {"qkv": 0, "attention": 1, "o": 2, "gate_up": 3, "down": 4, "head": 5}
 
-    def time_kernel(self, which: str, iters: int):
+    def time_kernel(self, which: str, iters: int, batch: int = 0):
         """One decode-step kernel alone, `iters` rounds over every layer, launched back to back on
         the engine's stream: (average kernel duration in microseconds from the start/stop events
-        hipExtLaunchKernel records, average wall time per launch with the gaps, launches)."""
+        hipExtLaunchKernel records, average wall time per launch with the gaps, launches).
+        batch > 0: the batched step's kernel at that many sequences."""
         kern, wall, n = C.c_double(), C.c_double(), C.c_uint64()
-        check(lib().x0ne_engine_time_kernel(self.h, self.KERNELS[which], iters, C.byref(kern), C.byref(wall),
-                                            C.byref(n)), "time_kernel")
+        if batch:
+            check(lib().x0ne_engine_time_batch_kernel(self.h, self.KERNELS[which], batch, iters, C.byref(kern),
+                                                      C.byref(wall), C.byref(n)), "time_batch_kernel")
+        else:
+            check(lib().x0ne_engine_time_kernel(self.h, self.KERNELS[which], iters, C.byref(kern), C.byref(wall),
+                                                C.byref(n)), "time_kernel")
         return kern.value, wall.value, n.value
 
     def page(self, i: int) -> int:

@@ -158,7 +158,12 @@ class Gpu:
 
     def launch(self, name: str, grid, block: int, args):
         """Gpu::launch (gpu.rs:1031-1086): checked against the kernel table, not synchronised."""
-        gx, gy = (grid, 1) if isinstance(grid, int) else grid
+        if isinstance(grid, int):
+            grid = (grid, 1)
+        if len(grid) == 3:
+            check(lib().x0ne_gpu_launch_3d(self.h, name.encode(), *grid, block, _args(args), len(args)), name)
+            return
+        gx, gy = grid
         check(lib().x0ne_gpu_launch(self.h, name.encode(), gx, gy, block, _args(args), len(args)), name)
 
     def gemv(self, w: int, rows: int, cols: int, x: int, n: int, y: int, out_f32: bool):

@@ -414,6 +414,99 @@ class Kernels:
             v_rows.append(v_all[[v_offset(pg, h.kv_heads, kh, slot, d) for d in range(HEAD_DIM)]])
         return a.read_array(s["out"], 0, qd, np.uint16), np.concatenate(k_rows), np.concatenate(v_rows)
 
+    def attention_rope_decode_batch(self, qkv, q_norm, k_norm, eps: float, theta: float, ks, vs, ctxs, h: Heads,
+                                    splits: int, max_ctx: int, page_seed: int = 0):
+        """The batched step's fused decode attention for B independent sequences in one launch
+        (grid (kv_heads, P, B)): sequence b's packed qkv row qkv[b] at position ctxs[b] - 1 over
+        its keys 0..ctxs[b]-1 (ks[b], vs[b] hold its rows 0..ctxs[b]-2), each sequence in its
+        own run of ceil(max_ctx / 16) entries of one shuffled page table over shared K/V planes.
+        Returns out [B][q_dim] and the K/V rows written at each sequence's position."""
+        h.check()
+        qd, kvd, hd = h.q_dim, h.kv_dim, h.head_dim
+        B = len(ctxs)
+        qkv = np.asarray(qkv, np.uint16).reshape(B, qd + 2 * kvd)
+        if B == 0 or len(ks) != B or len(vs) != B or any(c == 0 or c > max_ctx for c in ctxs):
+            raise FormatError("attention_rope_decode_batch: lengths")
+        plan = self.split_plan(h)
+        if not plan.grouped:
+            raise FormatError(f"attention_rope_decode_batch: no grouped kernel for group {h.q_heads // h.kv_heads}")
+        plan.splits = int(splits)
+        sp = n_pages(max_ctx)
+        pool = B * sp
+        order = np.arange(pool, dtype=np.uint32)
+        if page_seed:
+            np.random.default_rng(page_seed).shuffle(order)
+        kp = np.full((pool, h.kv_heads, PAGE, HEAD_DIM), NAN_BF16, np.uint16)
+        vp = np.full((pool, h.kv_heads, PAGE, HEAD_DIM), NAN_BF16, np.uint16)
+        for b, c in enumerate(ctxs):
+            rk = np.asarray(ks[b], np.uint16)[:(c - 1) * kvd].reshape(c - 1, h.kv_heads, HEAD_DIM)
+            rv = np.asarray(vs[b], np.uint16)[:(c - 1) * kvd].reshape(c - 1, h.kv_heads, HEAD_DIM)
+            for p in range(c - 1):
+                kp[order[b * sp + p // PAGE], :, p % PAGE, :] = rk[p]
+                vp[order[b * sp + p // PAGE], :, p % PAGE, :] = rv[p]
+        vp = np.ascontiguousarray(vp.transpose(0, 1, 3, 2))
+        a = self._arena()
+        sl = {name: a.alloc(name, size, cls) for name, size, cls in [
+            ("qkv", qkv.nbytes, Class.CLIENT_DATA), ("k", kp.nbytes, Class.CLIENT_DATA),
+            ("v", vp.nbytes, Class.CLIENT_DATA), ("pt", pool * 4, Class.WEIGHTS), ("pos", B * 4, Class.CLIENT_DATA),
+            ("out", B * qd * 2, Class.CLIENT_DATA),
+            ("state", B * split_state_bytes(h.q_heads, plan.splits), Class.CLIENT_DATA),
+            ("counter", B * h.kv_heads * 4, Class.CLIENT_DATA), ("q_norm", hd * 2, Class.WEIGHTS),
+            ("k_norm", hd * 2, Class.WEIGHTS), ("inv_freq", hd // 2 * 4, Class.WEIGHTS),
+            ("rope_cs", max_ctx * (hd // 2) * 16, Class.WEIGHTS)]}
+        self._freeze(a)
+        a.scrub_client_data()
+        a.write(sl["qkv"], 0, qkv)
+        a.write(sl["k"], 0, kp)
+        a.write(sl["v"], 0, vp)
+        a.write(sl["pt"], 0, order)
+        a.write(sl["pos"], 0, np.array([c - 1 for c in ctxs], np.uint32))
+        a.write(sl["q_norm"], 0, np.asarray(q_norm, np.uint16))
+        a.write(sl["k_norm"], 0, np.asarray(k_norm, np.uint16))
+        a.write(sl["inv_freq"], 0, inv_freq(hd, theta))
+        self._rope_table(a.ptr(sl["inv_freq"]), a.ptr(sl["rope_cs"]), max_ctx, hd)
+        self.gpu.launch(f"x0ne_attention_rope_decode_batch_g{plan.group}_bf16", (h.kv_heads, plan.splits, B), 256,
+                        [Arg.ptr(a.ptr(sl["qkv"])), Arg.ptr(a.ptr(sl["q_norm"])), Arg.ptr(a.ptr(sl["k_norm"])),
+                         Arg.ptr(a.ptr(sl["inv_freq"])), Arg.ptr(a.ptr(sl["rope_cs"])), Arg.ptr(a.ptr(sl["k"])),
+                         Arg.ptr(a.ptr(sl["v"])), Arg.ptr(a.ptr(sl["pt"])), Arg.ptr(a.ptr(sl["state"])),
+                         Arg.ptr(a.ptr(sl["counter"])), Arg.ptr(a.ptr(sl["out"])), Arg.ptr(a.ptr(sl["pos"])),
+                         Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(max_ctx), Arg.u32(plan.splits),
+                         Arg.f32(attn_scale(hd)), Arg.f32(eps), Arg.u32(sp)])
+        self.gpu.sync()
+        counts = a.read_array(sl["counter"], 0, B * h.kv_heads, np.uint32)
+        if counts.any():
+            raise GpuError(f"split-K counters not reset: {counts.tolist()}")
+        out = a.read_array(sl["out"], 0, B * qd, np.uint16).reshape(B, qd)
+        k_all = a.read_array(sl["k"], 0, kp.size, np.uint16).reshape(kp.shape)
+        v_all = a.read_array(sl["v"], 0, vp.size, np.uint16).reshape(vp.shape)
+        k_rows, v_rows = [], []
+        for b, c in enumerate(ctxs):
+            pg, slot = order[b * sp + (c - 1) // PAGE], (c - 1) % PAGE
+            k_rows.append(k_all[pg, :, slot, :].reshape(-1).copy())
+            v_rows.append(v_all[pg, :, :, slot].reshape(-1).copy())
+        return out, k_rows, v_rows
+
+    def gemm_few(self, w, rows, cols, x, n, mode: int, block: int = 256) -> np.ndarray:
+        """The few-row GEMM kernel itself (x0ne_gemm_skinny{16,32,64}_bf16 by n): mode 0 bf16 Y,
+        1 f32 Y, 2 SwiGLU over the packed [gate; up] W of 2 rows rows (act [n][rows] bf16)."""
+        wrows = 2 * rows if mode == 2 else rows
+        if w.size != wrows * cols or x.size != n * cols or not 1 <= n <= 64 or cols % 8:
+            raise FormatError("gemm_few: lengths")
+        name = f"x0ne_gemm_skinny{16 if n <= 16 else 32 if n <= 32 else 64}_bf16"
+        ob = 4 if mode == 1 else 2
+        a = self._arena()
+        ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
+        xs = a.alloc("x", x.size * 2, Class.CLIENT_DATA)
+        ys = a.alloc("y", n * rows * ob, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ws, 0, np.asarray(w, np.uint16))
+        a.write(xs, 0, np.asarray(x, np.uint16))
+        self.gpu.launch(name, (rows + 15) // 16, block,
+                        [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(cols),
+                         Arg.u32(n), Arg.u32(mode)])
+        self.gpu.sync()
+        return a.read_array(ys, 0, n * rows, np.float32 if mode == 1 else np.uint16).reshape(n, rows)
+
     def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None,
                              grouped=False):
         """Causal attention for positions pos0..t of a t-position cache in one launch at pos0
