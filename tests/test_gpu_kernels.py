@@ -228,7 +228,7 @@ def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
     assert (b == bf16_bits(f).reshape(b.shape)).all(), what
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(24))
 def test_few_row_gemm_is_the_oracle_and_its_swiglu_the_swiglu_kernel(kernels, seed):
     """The batched step's projection kernel (2 to 64 rows of X, each W row read once) at every
     block size it runs with: every row of Y is the oracle's GEMV within the GEMV tolerance, the
@@ -240,20 +240,23 @@ def test_few_row_gemm_is_the_oracle_and_its_swiglu_the_swiglu_kernel(kernels, se
     rows = rng.pick([1, 16, 17, 100, 256, 1000])
     cols = rng.pick([8, 32, 40, 200, 1024, 4096])
     block = rng.pick([256, 512])
+    tt = 1 if n <= 16 else 2 if n <= 32 else 4
+    rg = rng.pick([g for (t, g) in kernels.FEW_KERNELS if t == tt])
+    rg_glu = rng.pick([g for (t, g) in kernels.FEW_SWIGLU if t == tt])
     scale = rng.pick([1e-2, 1.0, 20.0])
     w = bf16s_with_edges(rng, 2 * rows * cols, scale)
     x = bf16s_with_edges(rng, n * cols, scale)
-    what = f"few-row gemm seed {seed} {n}x{rows}x{cols} block {block}"
-    f = kernels.gemm_few(bf16_bits(w[:rows * cols]), rows, cols, bf16_bits(x), n, 1, block)
-    b = kernels.gemm_few(bf16_bits(w[:rows * cols]), rows, cols, bf16_bits(x), n, 0, block)
+    what = f"few-row gemm seed {seed} {n}x{rows}x{cols} block {block} row groups {rg}/{rg_glu}"
+    f = kernels.gemm_few(bf16_bits(w[:rows * cols]), rows, cols, bf16_bits(x), n, 1, block, rg)
+    b = kernels.gemm_few(bf16_bits(w[:rows * cols]), rows, cols, bf16_bits(x), n, 0, block, rg)
     for r in range(n):
         xr = x[r * cols:(r + 1) * cols]
         want = O.gemv(w[:rows * cols], rows, cols, xr)
         mag = O.gemv_magnitude(w[:rows * cols], rows, cols, xr)
         assert_gemv(f"{what} row {r} f32", f[r], want, mag, False)
     assert (b == bf16_bits(f).reshape(b.shape)).all(), f"{what}: bf16 is the f32 rounded"
-    gu = kernels.gemm_few(bf16_bits(w), 2 * rows, cols, bf16_bits(x), n, 0, block)
-    act = kernels.gemm_few(bf16_bits(w), rows, cols, bf16_bits(x), n, 2, block)
+    gu = kernels.gemm_few(bf16_bits(w), 2 * rows, cols, bf16_bits(x), n, 0, block, rg_glu)
+    act = kernels.gemm_few(bf16_bits(w), rows, cols, bf16_bits(x), n, 2, block, rg_glu)
     for r in range(n):
         assert (act[r] == kernels.swiglu(gu[r])).all(), f"{what} row {r}: fused SwiGLU"
         assert_close(f"{what} row {r} swiglu", bf16_vals(act[r]), O.swiglu(bf16_vals(gu[r])), BF16_ATOL, BF16_RTOL)
@@ -540,6 +543,33 @@ def test_argmax_is_the_first_largest_and_a_nan_row_has_none(kernels):
     assert kernels.argmax(np.array([-0.0, 0.0], np.float32)) == 0
     with pytest.raises(FormatError):
         kernels.argmax(np.zeros(0, np.float32))
+
+
+def test_sliced_argmax_picks_what_the_one_block_argmax_picks(kernels):
+    """The batched step's argmax (rows cut in slices, then a pick over the slices) against the
+    oracle's first largest, with ties straddling slice boundaries, infinities, a NaN row, a row
+    of -inf, and slices past the row's end; every position advances by one."""
+    rng = O.Rng(710)
+    for n, slices in [(151936, 64), (1000, 64), (65, 64), (7, 64), (4096, 3), (1, 1)]:
+        rows = []
+        for r in range(6):
+            row = rng.f32s(n, 30.0) if r % 2 else np.array([rng.below(3) - 1.0 for _ in range(n)], np.float32)
+            rows.append(row)
+        per = -(-n // slices)
+        if n > 2 * per:
+            rows[2][[per - 1, per]] = np.float32(1e30)  # a tie across a slice boundary: the first wins
+        rows[3][n - 1] = np.inf
+        rows[4][:] = -np.inf
+        nan_row = rng.f32s(n, 1.0)
+        nan_row[rng.below(n)] = np.nan
+        rows.append(nan_row)
+        logits = np.stack(rows)
+        pos = np.arange(len(rows), dtype=np.uint32) * 1000 + 5
+        toks, after = kernels.argmax_rows_sliced(logits, slices, pos)
+        for r in range(len(rows) - 1):
+            assert toks[r] == O.argmax(logits[r]), f"n {n} slices {slices} row {r}"
+        assert toks[-1] == 0xFFFFFFFF, "a NaN row has no pick"
+        assert (after == pos + 1).all()
 
 
 def test_advance_adds_one(kernels):

@@ -36,6 +36,7 @@ constexpr size_t RING = 16;  // engine.rs:70
 // 128 rows, and 2048 rows keep it compute-bound).
 constexpr uint64_t PREFILL_CHUNK = 2048;
 constexpr uint64_t MAX_BATCH = 64;  // the few-row GEMM's most rows
+constexpr uint32_t ARGMAX_SLICES = 64;  // blocks per logits row of the batched step's argmax
 
 struct Cfg {
     uint64_t hidden = 0, inter = 0, layers = 0, q_heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, max_pos = 0;
@@ -301,7 +302,7 @@ struct x0ne_engine {
     x0ne_slice p_res{}, p_delta{}, p_x{}, p_qkv{}, p_q{}, p_attn{}, p_gu{}, p_act{};
     // The batched step's rows ([max_batch][...]): f32 residual, bf16 delta, normed x, qkv,
     // attention, SwiGLU activation, f32 logits; its split-K state and counters.
-    x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{};
+    x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{}, b_argmax{};
     std::vector<uint32_t> page_of;
     x0ne_split_plan split{}, bsplit{};
     uint32_t grid_qkv = 0, grid_o = 0, grid_gu = 0, grid_down = 0, grid_head = 0;
@@ -426,6 +427,7 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("batch_split_state", b * x0ne_split_state_bytes((uint32_t)c.q_heads, e->bsplit.splits), CD,
                     &e->b_state));
         X0NE_TRY(al("batch_split_counter", b * c.kv_heads * 4, CD, &e->b_counter));
+        X0NE_TRY(al("batch_argmax", b * ARGMAX_SLICES * 3 * 4, CD, &e->b_argmax));
     }
     return X0NE_OK;
 }
@@ -954,10 +956,14 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     if (e->max_batch > 1) {
         if (!e->split.grouped)
             return bail(fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding needs 1, 2, 4 or 8 q heads per kv head"));
-        // The batched step's attention grid is max_batch times wider: fewer slices per sequence.
+        // The batched step's attention grid is max_batch times wider: fewer slices per sequence,
+        // about one block per CU in all (measured at 8 and 16 sequences of 8 kv heads, 640 and
+        // 8.7k positions: P 4 and 2 beat half and twice as many blocks).
         e->bsplit = e->split;
-        const uint64_t p = (uint64_t)e->gpu->cus * e->split.per_cu / (2 * e->split.grid_x * e->max_batch);
+        const uint64_t p = (uint64_t)e->gpu->cus * e->split.per_cu / (e->split.grid_x * e->max_batch);
         e->bsplit.splits = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(p, e->split.splits));
+        static const char* env = std::getenv("X0NE_BATCH_SPLITS");  // a tuning knob
+        if (env && std::atoi(env) > 0) e->bsplit.splits = (uint32_t)std::min(std::atoi(env), 256);
     }
     if ((st = plan_grids(e)) != X0NE_OK) return bail(st);
     if ((st = x0ne_arena_new(&e->arena)) != X0NE_OK) return bail(st);
@@ -1473,11 +1479,14 @@ x0ne_status batch_head(x0ne_engine* e, uint32_t B) {
     X0NE_TRY(skinny(e->gpu, e->d(e->has_lm_head ? e->lm_head : e->embed), c.vocab, c.hidden, e->d(e->b_x), B,
                     e->d(e->b_logits), 1));
     const void* lg = e->d(e->b_logits);
-    uint32_t vocab = (uint32_t)c.vocab;
+    uint32_t vocab = (uint32_t)c.vocab, slices = ARGMAX_SLICES;
+    void* part = e->d(e->b_argmax);
+    void* args[] = {(void*)&lg, (void*)&vocab, (void*)&slices, (void*)&part};
+    X0NE_TRY(launch_rows(e, (const void*)&x0ne_argmax_slices_f32, dim3(B, slices), dim3(256), args, "batch argmax"));
     void* toks = e->token_of(0);
     void* pos = e->pos_of(0);
-    void* args[] = {(void*)&lg, (void*)&vocab, (void*)&toks, (void*)&pos};
-    return launch_rows(e, (const void*)&x0ne_argmax_advance_f32, dim3(B), dim3(1024), args, "batch argmax");
+    void* args2[] = {(void*)&part, (void*)&slices, (void*)&toks, (void*)&pos};
+    return launch_rows(e, (const void*)&x0ne_argmax_pick_advance, dim3(B), dim3(64), args2, "batch argmax pick");
 }
 
 // The launches of one batched decode step on sequences 0 .. B - 1, each at its own position with

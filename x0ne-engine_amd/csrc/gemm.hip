@@ -140,20 +140,21 @@ extern "C" __global__ void __launch_bounds__(256)
 // ---- a few rows: Y[n][rows] = X[n][cols] W^T for n <= 64, bandwidth-bound ----
 // The batched decode step's projections and a short prompt's. Every W row is read once, so the
 // kernel streams W at the HBM rate and the few-row matrix-core products cost nothing beside it:
-//  - Block b takes W rows 16 b .. 16 b + 15 over all of K; its V wavefronts (V = blockDim / 64:
-//    4 or 8, chosen by the host so the launch holds enough loads in flight) take V contiguous
-//    runs of K, in whole steps of 32 columns.
-//  - A step is TT 16 x 16 x 32 products (TT = 1, 2 or 4 tiles of 16 tokens) whose A operand is
-//    X (row = token, zero past n) and B operand W (column = W row): lane l loads 16 bytes,
-//    columns k0 + 8 (l / 16) .. + 7, of W row 16 b + l % 16 and of X row 16 tt + l % 16; the 4
-//    lane groups cover 64 contiguous bytes of each row.
+//  - Block b takes the RG row groups of 16 W rows 16 RG b .. 16 RG b + 16 RG - 1 over all of K;
+//    its V wavefronts (V = blockDim / 64, chosen by the host with RG so the launch holds enough
+//    loads in flight) take V contiguous runs of K, in whole steps of 32 columns.
+//  - A step is TT x RG 16 x 16 x 32 products (TT tiles of 16 tokens, RG row groups) whose A
+//    operand is X (row = token, zero past n) and B operand W (column = W row): lane l loads
+//    16 bytes, columns k0 + 8 (l / 16) .. + 7, of W row 16 (RG b + g) + l % 16 and of X row
+//    16 tt + l % 16; the 4 lane groups cover 64 contiguous bytes of each row. One X piece
+//    serves the RG row groups, so X (read from the L2 by every block) costs TT / RG of W's loads.
 //  - U steps are in flight per wavefront: the slot a product has consumed is refilled at once
 //    with the step U ahead, so U - 1 steps stay in flight while one multiplies. A piece past K
 //    (or a token past n, a W row past rows) is a raw buffer load at an offset past the buffer,
 //    which returns zeros without touching memory.
 //  - The wavefronts' partial tiles are summed in LDS in wavefront order (deterministic).
-// mode 0: Y bf16. mode 1: Y f32. mode 2: SwiGLU over the packed [gate; up] W of 2 rows rows:
-// block b also takes the up rows rows + 16 b .., and writes act[t][r] = bf16(g / (1 + e^-g) u)
+// out_f32 0: Y bf16, 1: Y f32. GLU: SwiGLU over the packed [gate; up] W of 2 rows rows: the block
+// also takes the up rows rows + 16 (RG b + g) .., and writes act[t][r] = bf16(g / (1 + e^-g) u)
 // of the bf16-rounded g and u, in f64 (x0ne_swiglu_bf16 of the bf16 projection).
 namespace {
 
@@ -162,32 +163,40 @@ __device__ __forceinline__ uint32_t sk_off(bool in, uint32_t r, uint32_t cols, u
     return in ? (r * cols + k) * 2 : OFF_NONE;
 }
 
-template <int TT, int U>
-__device__ __forceinline__ void skinny(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y,
-                                       uint32_t rows, uint32_t cols, uint32_t n, uint32_t mode, f32x4* part) {
-    constexpr int MAXV = 8;
+template <int TT, int RG, int U, bool GLU, int MAXV>
+__device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
+                                         void* __restrict__ y, uint32_t rows, uint32_t cols, uint32_t n,
+                                         uint32_t out_f32, f32x4* part) {
+    constexpr int KINDS = GLU ? 2 : 1;
     const uint32_t b = blockIdx.x, V = blockDim.x >> 6;
-    if (b * 16 >= rows || n == 0 || n > 16 * TT || cols % 8 != 0 || mode > 2 || V > MAXV) return;  // grid-uniform
+    // Grid-uniform exits for a launch that does not fit.
+    if (b * 16 * RG >= rows || n == 0 || n > 16 * TT || cols % 8 != 0 || V > MAXV || (GLU && out_f32)) return;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool glu = mode == 2;
     const uint32_t r = lane & 15, q4 = lane >> 4;
-    const bool row_in = b * 16 + r < rows;
-    const uint32_t wrow = b * 16 + r, urow = rows + b * 16 + r;
     const auto xr = rsrc(x, (uint64_t)n * cols * 2);
-    const auto wr = rsrc(w, (uint64_t)(glu ? 2 : 1) * rows * cols * 2);
+    const auto wr = rsrc(w, (uint64_t)KINDS * rows * cols * 2);
     const uint32_t steps = (cols + 31) / 32, per = (steps + V - 1) / V;
     const uint32_t s_begin = min(wave * per, steps), s_end = min(s_begin + per, steps);
-    f32x4 acc[TT], accu[TT];
+    f32x4 acc[KINDS][RG][TT];
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) acc[tt] = accu[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    uint4 xa[U][TT], wb[U], wu[U];
+    for (int kd = 0; kd < KINDS; ++kd)
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) acc[kd][g][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 xa[U][TT], wb[U][KINDS][RG];
     auto request = [&](int u, uint32_t s) {
         const uint32_t k = 32 * s + 8 * q4;
         const bool in = s < s_end && k < cols;  // a K tail: pieces past the row read zeros
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) xa[u][tt] = bload(xr, sk_off(in && 16 * tt + r < n, 16 * tt + r, cols, k));
-        wb[u] = bload(wr, sk_off(in && row_in, wrow, cols, k));
-        if (glu) wu[u] = bload(wr, sk_off(in && row_in, urow, cols, k));
+#pragma unroll
+        for (int kd = 0; kd < KINDS; ++kd)
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+                const uint32_t row = 16 * (RG * b + g) + r;
+                wb[u][kd][g] = bload(wr, sk_off(in && row < rows, kd * rows + row, cols, k));
+            }
     };
 #pragma unroll
     for (int u = 0; u < U; ++u) request(u, s_begin + u);
@@ -195,41 +204,48 @@ __device__ __forceinline__ void skinny(const bf16_t* __restrict__ w, const bf16_
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
-            for (int tt = 0; tt < TT; ++tt) {
-                acc[tt] = mfma(xa[u][tt], wb[u], acc[tt]);
-                if (glu) accu[tt] = mfma(xa[u][tt], wu[u], accu[tt]);
-            }
+            for (int kd = 0; kd < KINDS; ++kd)
+#pragma unroll
+                for (int g = 0; g < RG; ++g)
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt) acc[kd][g][tt] = mfma(xa[u][tt], wb[u][kd][g], acc[kd][g][tt]);
             request(u, s0 + U + u);
         }
     }
-    // part[((kind V + wave) TT + tt) 64 + lane]
+    // part[(((kd V + wave) RG + g) TT + tt) 64 + lane]
+    auto at = [&](uint32_t kd, uint32_t v, uint32_t g, uint32_t tt) { return (((kd * V + v) * RG + g) * TT + tt) * 64 + lane; };
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-        part[(wave * TT + tt) * 64 + lane] = acc[tt];
-        if (glu) part[((V + wave) * TT + tt) * 64 + lane] = accu[tt];
-    }
+    for (int kd = 0; kd < KINDS; ++kd)
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) part[at(kd, wave, g, tt)] = acc[kd][g][tt];
     lds_barrier();
-    if (wave != 0 || !row_in) return;
+    // Wavefront w sums row groups w, w + V, ..: the V partials of each in wavefront order.
+    for (uint32_t g = wave; g < (uint32_t)RG; g += V) {
+        const uint32_t wrow = 16 * (RG * b + g) + r;
+        if (wrow >= rows) continue;
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-        f32x4 sg = part[tt * 64 + lane], su = glu ? part[(V * TT + tt) * 64 + lane] : f32x4{0.f, 0.f, 0.f, 0.f};
-        for (uint32_t v = 1; v < V; ++v) {
-            sg += part[(v * TT + tt) * 64 + lane];
-            if (glu) su += part[((V + v) * TT + tt) * 64 + lane];
-        }
-        // sg[i]: token 16 tt + 4 (lane / 16) + i, W row 16 b + lane % 16.
+        for (int tt = 0; tt < TT; ++tt) {
+            f32x4 sg = part[at(0, 0, g, tt)], su = GLU ? part[at(1, 0, g, tt)] : f32x4{0.f, 0.f, 0.f, 0.f};
+            for (uint32_t v = 1; v < V; ++v) {
+                sg += part[at(0, v, g, tt)];
+                if (GLU) su += part[at(1, v, g, tt)];
+            }
+            // sg[i]: token 16 tt + 4 (lane / 16) + i, W row wrow.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t t = 16 * tt + 4 * q4 + i;
-            if (t >= n) continue;
-            const size_t at = (size_t)t * rows + wrow;
-            if (mode == 1) {
-                static_cast<float*>(y)[at] = sg[i];
-            } else if (mode == 0) {
-                static_cast<bf16_t*>(y)[at] = f2bf(sg[i]);
-            } else {
-                const double g = (double)bf2f(f2bf(sg[i])), u = (double)bf2f(f2bf(su[i]));
-                static_cast<bf16_t*>(y)[at] = f2bf((float)(g / (1.0 + exp(-g)) * u));
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t = 16 * tt + 4 * q4 + i;
+                if (t >= n) continue;
+                const size_t o = (size_t)t * rows + wrow;
+                if (GLU) {
+                    const double gv = (double)bf2f(f2bf(sg[i])), uv = (double)bf2f(f2bf(su[i]));
+                    static_cast<bf16_t*>(y)[o] = f2bf((float)(gv / (1.0 + exp(-gv)) * uv));
+                } else if (out_f32) {
+                    static_cast<float*>(y)[o] = sg[i];
+                } else {
+                    static_cast<bf16_t*>(y)[o] = f2bf(sg[i]);
+                }
             }
         }
     }
@@ -237,16 +253,26 @@ __device__ __forceinline__ void skinny(const bf16_t* __restrict__ w, const bf16_
 
 }  // namespace
 
-// grid (ceil(rows / 16)), block 256 or 512; n in 1..16, 1..32, 1..64 for the 16, 32 and 64
-// kernels; cols a multiple of 8; X, W below 4 GiB - 16 bytes.
-#define X0NE_SKINNY(N, TT, U)                                                                                     \
-    extern "C" __global__ void __launch_bounds__(512)                                                             \
-        x0ne_gemm_skinny##N##_bf16(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, \
-                                   uint32_t rows, uint32_t cols, uint32_t n, uint32_t mode) {                     \
-        __shared__ f32x4 part[2 * 8 * TT * 64];                                                                   \
-        skinny<TT, U>(w, x, y, rows, cols, n, mode, part);                                                         \
+// x0ne_gemm_few_t{TT}_r{RG}[_swiglu]_bf16: grid (ceil(rows / (16 RG))), block 64 V threads
+// (V <= MAXV); n in 1 .. 16 TT; cols a multiple of 8; X, W below 4 GiB - 16 bytes. The
+// SwiGLU variants write bf16 (out_f32 must be 0).
+#define X0NE_FEW(NAME, TT, RG, U, GLU, MAXV)                                                                     \
+    extern "C" __global__ void __launch_bounds__(64 * MAXV)                                                       \
+        NAME(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, uint32_t rows,     \
+             uint32_t cols, uint32_t n, uint32_t out_f32) {                                                       \
+        __shared__ f32x4 part[(GLU ? 2 : 1) * MAXV * RG * TT * 64];                                               \
+        few_rows<TT, RG, U, GLU, MAXV>(w, x, y, rows, cols, n, out_f32, part);                                    \
     }
-X0NE_SKINNY(16, 1, 8)
-X0NE_SKINNY(32, 2, 8)
-X0NE_SKINNY(64, 4, 4)
-#undef X0NE_SKINNY
+#ifndef X0NE_FEW_NO_TABLE
+X0NE_FEW(x0ne_gemm_few_t1_r1_bf16, 1, 1, 12, false, 8)
+X0NE_FEW(x0ne_gemm_few_t1_r2_bf16, 1, 2, 4, false, 8)
+X0NE_FEW(x0ne_gemm_few_t1_r4_bf16, 1, 4, 8, false, 8)
+X0NE_FEW(x0ne_gemm_few_t1_r8_bf16, 1, 8, 4, false, 8)
+X0NE_FEW(x0ne_gemm_few_t1_r1_swiglu_bf16, 1, 1, 4, true, 8)
+X0NE_FEW(x0ne_gemm_few_t1_r2_swiglu_bf16, 1, 2, 4, true, 8)
+X0NE_FEW(x0ne_gemm_few_t2_r1_bf16, 2, 1, 8, false, 8)
+X0NE_FEW(x0ne_gemm_few_t2_r2_bf16, 2, 2, 4, false, 8)
+X0NE_FEW(x0ne_gemm_few_t2_r1_swiglu_bf16, 2, 1, 4, true, 8)
+X0NE_FEW(x0ne_gemm_few_t4_r1_bf16, 4, 1, 4, false, 8)
+X0NE_FEW(x0ne_gemm_few_t4_r1_swiglu_bf16, 4, 1, 4, true, 8)
+#endif

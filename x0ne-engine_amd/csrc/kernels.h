@@ -69,20 +69,29 @@ X0NE_DECLARE_PREFILL_GROUP(8)
 #undef X0NE_DECLARE_PREFILL_GROUP
 __global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
 __global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
-__global__ void x0ne_argmax_advance_f32(const float* logits, uint32_t n, uint32_t* tokens, uint32_t* pos);
+__global__ void x0ne_argmax_slices_f32(const float* logits, uint32_t n, uint32_t slices, uint32_t* partial);
+__global__ void x0ne_argmax_pick_advance(const uint32_t* partial, uint32_t slices, uint32_t* tokens, uint32_t* pos);
 __global__ void x0ne_embed_rmsnorm_bf16(const bf16_t* table, const uint32_t* tokens, float* residual,
                                         const bf16_t* w, bf16_t* out, uint32_t hidden, uint32_t vocab, float eps);
 __global__ void x0ne_advance_u32(uint32_t* pos);
 __global__ void x0ne_feed_u32(const uint32_t* ids, uint32_t i, uint32_t* tokens, uint32_t* pos);
 __global__ void x0ne_gemm_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, uint32_t n,
                                uint32_t out_f32);
-#define X0NE_DECLARE_SKINNY(N)                                                                                   \
-    __global__ void x0ne_gemm_skinny##N##_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows,         \
-                                               uint32_t cols, uint32_t n, uint32_t mode);
-X0NE_DECLARE_SKINNY(16)
-X0NE_DECLARE_SKINNY(32)
-X0NE_DECLARE_SKINNY(64)
-#undef X0NE_DECLARE_SKINNY
+#define X0NE_DECLARE_FEW(V)                                                                                      \
+    __global__ void x0ne_gemm_few_##V##_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, \
+                                             uint32_t n, uint32_t out_f32);
+X0NE_DECLARE_FEW(t1_r1)
+X0NE_DECLARE_FEW(t1_r2)
+X0NE_DECLARE_FEW(t1_r4)
+X0NE_DECLARE_FEW(t1_r8)
+X0NE_DECLARE_FEW(t1_r1_swiglu)
+X0NE_DECLARE_FEW(t1_r2_swiglu)
+X0NE_DECLARE_FEW(t2_r1)
+X0NE_DECLARE_FEW(t2_r2)
+X0NE_DECLARE_FEW(t2_r1_swiglu)
+X0NE_DECLARE_FEW(t4_r1)
+X0NE_DECLARE_FEW(t4_r1_swiglu)
+#undef X0NE_DECLARE_FEW
 __global__ void x0ne_gemv_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_f32(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_any(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols,

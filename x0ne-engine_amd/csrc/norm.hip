@@ -46,21 +46,57 @@ extern "C" __global__ void __launch_bounds__(128)
 
 // residual[r] += x[r] (f32, one addition per value); out[r] = bf16(residual / rms * w), the rms
 // and the product in f64 (rmsnorm.cu:5-21; oracle/src/lib.rs:50-67). grid (rows), block 256.
-extern "C" __global__ void __launch_bounds__(256)
-    x0ne_add_rmsnorm_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
-                          bf16_t* __restrict__ out, uint32_t hidden, float eps) {
+// Thread t owns values t, t + 256, ..; up to NORM_HELD of them are loaded into registers at once
+// (every load in flight together, one memory round trip per row), the rest of a wider row in a
+// loop. Each thread sums its squares in that order, then the block (block_sum_d).
+constexpr uint32_t NORM_HELD = 32;  // values per thread kept in registers: hidden <= 8192 at 256
+
+template <class Src>
+__device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& src, const bf16_t* __restrict__ w,
+                                            bf16_t* __restrict__ out, uint32_t hidden, float eps) {
     __shared__ double sh[16];
-    const size_t base = (size_t)blockIdx.x * hidden;
+    const uint32_t t = threadIdx.x, step = blockDim.x;
+    float r[NORM_HELD];
     double ss = 0.0;
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) {
-        const float r = residual[base + i] + bf2f(x[base + i]);
-        residual[base + i] = r;
-        ss += (double)r * (double)r;
+    // Loads of a clamped index, selected after: no branch between them, so all are in flight at
+    // once.
+#pragma unroll
+    for (uint32_t c = 0; c < NORM_HELD; ++c) {
+        const uint32_t i = t + c * step;
+        const float v = src(i < hidden ? i : 0u);
+        r[c] = i < hidden ? v : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < NORM_HELD; ++c) {
+        const uint32_t i = t + c * step;
+        if (i < hidden) {
+            residual[i] = r[c];
+            ss += (double)r[c] * (double)r[c];
+        }
+    }
+    for (uint32_t i = t + NORM_HELD * step; i < hidden; i += step) {  // rows wider than held
+        const float v = src(i);
+        residual[i] = v;
+        ss += (double)v * (double)v;
     }
     const double total = block_sum_d(ss, sh);
     const double scale = 1.0 / sqrt(total / (double)hidden + (double)eps);
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x)
-        out[base + i] = f2bf((float)((double)residual[base + i] * scale * (double)bf2f(w[i])));
+#pragma unroll
+    for (uint32_t c = 0; c < NORM_HELD; ++c) {
+        const uint32_t i = t + c * step;
+        if (i < hidden) out[i] = f2bf((float)((double)r[c] * scale * (double)bf2f(w[i])));
+    }
+    for (uint32_t i = t + NORM_HELD * step; i < hidden; i += step)
+        out[i] = f2bf((float)((double)residual[i] * scale * (double)bf2f(w[i])));
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_add_rmsnorm_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+                          bf16_t* __restrict__ out, uint32_t hidden, float eps) {
+    const size_t base = (size_t)blockIdx.x * hidden;
+    float* res = residual + base;
+    const bf16_t* xr = x + base;
+    rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w, out + base, hidden, eps);
 }
 
 // The first norm of a batched step: residual[r] = 0 + table[tokens[r]] (f32; an id >= vocab gives
@@ -70,20 +106,14 @@ extern "C" __global__ void __launch_bounds__(256)
     x0ne_embed_rmsnorm_bf16(const bf16_t* __restrict__ table, const uint32_t* __restrict__ tokens,
                             float* __restrict__ residual, const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
                             uint32_t hidden, uint32_t vocab, float eps) {
-    __shared__ double sh[16];
     const size_t base = (size_t)blockIdx.x * hidden;
     const uint32_t tok = tokens[blockIdx.x];
     const bf16_t* src = table + (size_t)(tok < vocab ? tok : 0) * hidden;
-    double ss = 0.0;
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x) {
-        const float r = 0.0f + (tok < vocab ? bf2f(src[i]) : 0.0f);
-        residual[base + i] = r;
-        ss += (double)r * (double)r;
-    }
-    const double total = block_sum_d(ss, sh);
-    const double scale = 1.0 / sqrt(total / (double)hidden + (double)eps);
-    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x)
-        out[base + i] = f2bf((float)((double)residual[base + i] * scale * (double)bf2f(w[i])));
+    const bool in = tok < vocab;
+    rmsnorm_row(residual + base, [&](uint32_t i) {
+        const float v = bf2f(src[i]);  // row 0 for an id past the table, then not used
+        return 0.0f + (in ? v : 0.0f);
+    }, w, out + base, hidden, eps);
 }
 
 // Per-head RMSNorm of q and k, rotate-half RoPE, and the K/V write into the paged cache
@@ -165,9 +195,15 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);
 }
 
-// The first largest value's index of row[0 .. n), or 0xFFFFFFFF when the row holds a NaN, for
-// thread 0 of a block of whole wavefronts (at most 16).
-__device__ __forceinline__ uint32_t argmax_row(const float* __restrict__ row, uint32_t n) {
+// The first largest value of row[0 .. n) with its index (0xFFFFFFFF and -inf for an empty
+// row) and whether the row holds a NaN, for thread 0 of a block of whole wavefronts (at most 16).
+struct ArgBest {
+    float v;
+    uint32_t i;
+    bool nan;
+};
+
+__device__ __forceinline__ ArgBest argmax_block(const float* __restrict__ row, uint32_t n) {
     __shared__ float sv[16];
     __shared__ uint32_t si[16];
     __shared__ int snan;
@@ -200,36 +236,75 @@ __device__ __forceinline__ uint32_t argmax_row(const float* __restrict__ row, ui
         si[wave] = bi;
     }
     __syncthreads();
-    float fv = -INFINITY;
-    uint32_t fi = 0xFFFFFFFFu;
+    ArgBest best = {-INFINITY, 0xFFFFFFFFu, snan != 0};
     if (t == 0) {
         for (uint32_t w = 0; w < nw; ++w) {
-            if (better(sv[w], si[w], fv, fi)) {
-                fv = sv[w];
-                fi = si[w];
+            if (better(sv[w], si[w], best.v, best.i)) {
+                best.v = sv[w];
+                best.i = si[w];
             }
         }
     }
-    return snan ? 0xFFFFFFFFu : fi;
+    return best;
 }
 
 // Greedy pick (argmax.cu:11-58): index of the largest logit of each row, lowest index on ties;
 // a row holding any NaN yields 0xFFFFFFFF. grid (rows), block 1024 (16 wavefronts).
 extern "C" __global__ void __launch_bounds__(1024)
     x0ne_argmax_f32(const float* __restrict__ logits, uint32_t n, uint32_t* __restrict__ out) {
-    const uint32_t i = argmax_row(logits + (size_t)blockIdx.x * n, n);
-    if (threadIdx.x == 0) out[blockIdx.x] = i;
+    const ArgBest b = argmax_block(logits + (size_t)blockIdx.x * n, n);
+    if (threadIdx.x == 0) out[blockIdx.x] = b.nan ? 0xFFFFFFFFu : b.i;
 }
 
-// The batched step's pick and advance: tokens[r] = the argmax of logits row r (as
-// x0ne_argmax_f32), pos[r] += 1. grid (rows), block 1024.
-extern "C" __global__ void __launch_bounds__(1024)
-    x0ne_argmax_advance_f32(const float* __restrict__ logits, uint32_t n, uint32_t* __restrict__ tokens,
-                            uint32_t* __restrict__ pos) {
-    const uint32_t i = argmax_row(logits + (size_t)blockIdx.x * n, n);
+// The batched step's pick in two launches, so many blocks share a row: slice s of row r (grid
+// (rows, slices), block 256) takes values s per .. (s + 1) per - 1, per = ceil(n / slices), and
+// writes its first largest value, that value's index in the row and its NaN flag into
+// partial[3 (r slices + s) ..]; then x0ne_argmax_pick_advance (grid (rows), block 64) takes the
+// first largest over the slices in slice order (so the lowest index on ties, as x0ne_argmax_f32),
+// 0xFFFFFFFF when any slice saw a NaN, into tokens[r], and advances pos[r].
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_argmax_slices_f32(const float* __restrict__ logits, uint32_t n, uint32_t slices,
+                           uint32_t* __restrict__ partial) {
+    const uint32_t r = blockIdx.x, s = blockIdx.y;
+    const uint32_t per = (n + slices - 1) / slices, begin = min(s * per, n), len = min(per, n - begin);
+    const ArgBest b = argmax_block(logits + (size_t)r * n + begin, len);
     if (threadIdx.x == 0) {
-        tokens[blockIdx.x] = i;
-        pos[blockIdx.x] += 1u;
+        uint32_t* p = partial + 3 * ((size_t)r * slices + s);
+        p[0] = __float_as_uint(b.v);
+        p[1] = b.i == 0xFFFFFFFFu ? 0xFFFFFFFFu : begin + b.i;
+        p[2] = b.nan ? 1u : 0u;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(64)
+    x0ne_argmax_pick_advance(const uint32_t* __restrict__ partial, uint32_t slices, uint32_t* __restrict__ tokens,
+                             uint32_t* __restrict__ pos) {
+    const uint32_t r = blockIdx.x, lane = threadIdx.x;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    bool nan = false;
+    for (uint32_t s = lane; s < slices; s += 64) {  // lane order = slice order within a lane
+        const uint32_t* p = partial + 3 * ((size_t)r * slices + s);
+        const float v = __uint_as_float(p[0]);
+        nan |= p[2] != 0;
+        if (better(v, p[1], bv, bi)) {
+            bv = v;
+            bi = p[1];
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    nan = __any(nan);
+    if (lane == 0) {
+        tokens[r] = nan ? 0xFFFFFFFFu : bi;
+        pos[r] += 1u;
     }
 }
 

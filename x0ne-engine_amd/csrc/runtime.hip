@@ -266,17 +266,43 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
         (uintptr_t)x % 16 != 0)
         return fail(X0NE_ERR_FORMAT, "few-row gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
                                          std::to_string(n) + ", mode " + std::to_string(mode));
-    const uint32_t blocks = (uint32_t)((rows + 15) / 16);
-    // Eight wavefronts per block while the launch would hold fewer than 12 per CU at four.
-    const uint32_t waves = (uint64_t)blocks * 4 < 12ull * g->cus ? 8 : 4;
-    const void* fn = n <= 16 ? (const void*)&x0ne_gemm_skinny16_bf16
-                     : n <= 32 ? (const void*)&x0ne_gemm_skinny32_bf16
-                               : (const void*)&x0ne_gemm_skinny64_bf16;
-    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n;
-    void* args[] = {(void*)&w, (void*)&x, (void*)&y, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&mode};
+    // Row groups per block (each X piece serves RG W pieces) and wavefronts per block, from a
+    // sweep on MI355X over the decode shapes: at most 8 rows of X the L2 serves X cheaply and
+    // more blocks win (RG 2 while 192 blocks remain); at 9 to 16 rows X costs as much as W per
+    // piece, and RG grows while 160 blocks remain.
+    const bool glu = mode == 2;
+    auto blocks_of = [&](uint32_t rg) { return (uint32_t)((rows + 16 * rg - 1) / (16 * rg)); };
+    uint32_t rg = 1, waves = 4;
+    const void* fn = nullptr;
+    if (n <= 16) {
+        if (glu) {
+            rg = n > 8 && blocks_of(2) >= 1024 ? 2 : 1;
+            fn = rg == 2 ? (const void*)&x0ne_gemm_few_t1_r2_swiglu_bf16 : (const void*)&x0ne_gemm_few_t1_r1_swiglu_bf16;
+            waves = blocks_of(rg) >= 1024 ? 8 : 4;
+        } else {
+            const uint32_t min_blocks = n <= 8 ? 192 : 160, max_rg = n <= 8 ? 2 : 8;
+            for (uint32_t c = 2; c <= max_rg; c *= 2)
+                if (blocks_of(c) >= min_blocks) rg = c;
+            fn = rg == 1   ? (const void*)&x0ne_gemm_few_t1_r1_bf16
+                 : rg == 2 ? (const void*)&x0ne_gemm_few_t1_r2_bf16
+                 : rg == 4 ? (const void*)&x0ne_gemm_few_t1_r4_bf16
+                           : (const void*)&x0ne_gemm_few_t1_r8_bf16;
+        }
+    } else if (n <= 32) {
+        if (glu) {
+            fn = (const void*)&x0ne_gemm_few_t2_r1_swiglu_bf16;
+        } else {
+            rg = blocks_of(2) >= 160 ? 2 : 1;
+            fn = rg == 2 ? (const void*)&x0ne_gemm_few_t2_r2_bf16 : (const void*)&x0ne_gemm_few_t2_r1_bf16;
+        }
+    } else {
+        fn = glu ? (const void*)&x0ne_gemm_few_t4_r1_swiglu_bf16 : (const void*)&x0ne_gemm_few_t4_r1_bf16;
+    }
+    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, f32 = mode == 1 ? 1u : 0u;
+    void* args[] = {(void*)&w, (void*)&x, (void*)&y, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&f32};
     g->counts.gemms++;
     g->counts.launches++;
-    X0NE_HIP(x0ne_launch(fn, dim3(blocks), dim3(64 * waves), args, 0, g->stream), "few-row gemm");
+    X0NE_HIP(x0ne_launch(fn, dim3(blocks_of(rg)), dim3(64 * waves), args, 0, g->stream), "few-row gemm");
     return X0NE_OK;
 }
 

@@ -6,9 +6,17 @@
 static const X0neKernel TABLE[] = {
     {"x0ne_probe_iota_u32", (const void*)&x0ne_probe_iota_u32, "pu", 256},
     {"x0ne_gemm_bf16", (const void*)&x0ne_gemm_bf16, "pppuuuu", 256},
-    {"x0ne_gemm_skinny16_bf16", (const void*)&x0ne_gemm_skinny16_bf16, "pppuuuu", 512},
-    {"x0ne_gemm_skinny32_bf16", (const void*)&x0ne_gemm_skinny32_bf16, "pppuuuu", 512},
-    {"x0ne_gemm_skinny64_bf16", (const void*)&x0ne_gemm_skinny64_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t1_r1_bf16", (const void*)&x0ne_gemm_few_t1_r1_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t1_r2_bf16", (const void*)&x0ne_gemm_few_t1_r2_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t1_r4_bf16", (const void*)&x0ne_gemm_few_t1_r4_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t1_r8_bf16", (const void*)&x0ne_gemm_few_t1_r8_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t1_r1_swiglu_bf16", (const void*)&x0ne_gemm_few_t1_r1_swiglu_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t1_r2_swiglu_bf16", (const void*)&x0ne_gemm_few_t1_r2_swiglu_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t2_r1_bf16", (const void*)&x0ne_gemm_few_t2_r1_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t2_r2_bf16", (const void*)&x0ne_gemm_few_t2_r2_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t2_r1_swiglu_bf16", (const void*)&x0ne_gemm_few_t2_r1_swiglu_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t4_r1_bf16", (const void*)&x0ne_gemm_few_t4_r1_bf16, "pppuuuu", 512},
+    {"x0ne_gemm_few_t4_r1_swiglu_bf16", (const void*)&x0ne_gemm_few_t4_r1_swiglu_bf16, "pppuuuu", 512},
     {"x0ne_probe_bf16_round", (const void*)&x0ne_probe_bf16_round, "uupp", 256},
     {"x0ne_embedding_bf16", (const void*)&x0ne_embedding_bf16, "pppuu", 128},
     {"x0ne_add_rmsnorm_bf16", (const void*)&x0ne_add_rmsnorm_bf16, "ppppuf", 256},
@@ -40,7 +48,8 @@ static const X0neKernel TABLE[] = {
     {"x0ne_attention_prefill_bf16", (const void*)&x0ne_attention_prefill_bf16, "ppppppuuuuf", 256},
     {"x0ne_swiglu_bf16", (const void*)&x0ne_swiglu_bf16, "ppu", 256},
     {"x0ne_argmax_f32", (const void*)&x0ne_argmax_f32, "pup", 1024},
-    {"x0ne_argmax_advance_f32", (const void*)&x0ne_argmax_advance_f32, "pupp", 1024},
+    {"x0ne_argmax_slices_f32", (const void*)&x0ne_argmax_slices_f32, "puup", 256},
+    {"x0ne_argmax_pick_advance", (const void*)&x0ne_argmax_pick_advance, "pupp", 64},
     {"x0ne_embed_rmsnorm_bf16", (const void*)&x0ne_embed_rmsnorm_bf16, "pppppuuf", 256},
     {"x0ne_advance_u32", (const void*)&x0ne_advance_u32, "p", 64},
     {"x0ne_feed_u32", (const void*)&x0ne_feed_u32, "pupp", 64},

@@ -486,13 +486,20 @@ class Kernels:
             v_rows.append(v_all[pg, :, :, slot].reshape(-1).copy())
         return out, k_rows, v_rows
 
-    def gemm_few(self, w, rows, cols, x, n, mode: int, block: int = 256) -> np.ndarray:
-        """The few-row GEMM kernel itself (x0ne_gemm_skinny{16,32,64}_bf16 by n): mode 0 bf16 Y,
-        1 f32 Y, 2 SwiGLU over the packed [gate; up] W of 2 rows rows (act [n][rows] bf16)."""
+    FEW_KERNELS = {(1, 1): 8, (1, 2): 8, (1, 4): 8, (1, 8): 8, (2, 1): 8, (2, 2): 8, (4, 1): 8}
+    FEW_SWIGLU = {(1, 1), (1, 2), (2, 1), (4, 1)}
+
+    def gemm_few(self, w, rows, cols, x, n, mode: int, block: int = 256, rg: int = 1) -> np.ndarray:
+        """One few-row GEMM kernel itself (x0ne_gemm_few_t{TT}_r{RG}[_swiglu]_bf16, TT = 1, 2
+        or 4 tiles of 16 rows of X by n): mode 0 bf16 Y, 1 f32 Y, 2 SwiGLU over the packed
+        [gate; up] W of 2 rows rows (act [n][rows] bf16); `rg` row groups of 16 per block."""
         wrows = 2 * rows if mode == 2 else rows
-        if w.size != wrows * cols or x.size != n * cols or not 1 <= n <= 64 or cols % 8:
-            raise FormatError("gemm_few: lengths")
-        name = f"x0ne_gemm_skinny{16 if n <= 16 else 32 if n <= 32 else 64}_bf16"
+        tt = 1 if n <= 16 else 2 if n <= 32 else 4
+        if w.size != wrows * cols or x.size != n * cols or not 1 <= n <= 64 or cols % 8 or \
+                (tt, rg) not in self.FEW_KERNELS or (mode == 2 and (tt, rg) not in self.FEW_SWIGLU) or \
+                block // 64 > self.FEW_KERNELS[(tt, rg)]:
+            raise FormatError("gemm_few: lengths or variant")
+        name = f"x0ne_gemm_few_t{tt}_r{rg}{'_swiglu' if mode == 2 else ''}_bf16"
         ob = 4 if mode == 1 else 2
         a = self._arena()
         ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
@@ -501,9 +508,9 @@ class Kernels:
         self._freeze(a)
         a.write(ws, 0, np.asarray(w, np.uint16))
         a.write(xs, 0, np.asarray(x, np.uint16))
-        self.gpu.launch(name, (rows + 15) // 16, block,
+        self.gpu.launch(name, (rows + 16 * rg - 1) // (16 * rg), block,
                         [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(cols),
-                         Arg.u32(n), Arg.u32(mode)])
+                         Arg.u32(n), Arg.u32(1 if mode == 1 else 0)])
         self.gpu.sync()
         return a.read_array(ys, 0, n * rows, np.float32 if mode == 1 else np.uint16).reshape(n, rows)
 
@@ -567,6 +574,27 @@ class Kernels:
         self.gpu.launch("x0ne_advance_u32", 1, 64, [Arg.ptr(a.ptr(pos))])
         self.gpu.sync()
         return int(a.read_array(pos, 0, 1, np.uint32)[0])
+
+    def argmax_rows_sliced(self, logits, slices: int, pos):
+        """The batched step's two-launch pick over rows of logits ([rows][n] f32): each row cut
+        in `slices` blocks, then the pick and the advance; returns (tokens, positions after).
+        A token 0xFFFFFFFF marks a row holding a NaN."""
+        logits = np.ascontiguousarray(logits, np.float32)
+        rows, n = logits.shape
+        a = self._arena()
+        ls = a.alloc("logits", logits.nbytes, Class.CLIENT_DATA)
+        part = a.alloc("partial", rows * slices * 12, Class.CLIENT_DATA)
+        toks = a.alloc("tokens", rows * 4, Class.CLIENT_DATA)
+        ps = a.alloc("pos", rows * 4, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ls, 0, logits)
+        a.write(ps, 0, np.asarray(pos, np.uint32))
+        self.gpu.launch("x0ne_argmax_slices_f32", (rows, slices), 256,
+                        [Arg.ptr(a.ptr(ls)), Arg.u32(n), Arg.u32(slices), Arg.ptr(a.ptr(part))])
+        self.gpu.launch("x0ne_argmax_pick_advance", rows, 64,
+                        [Arg.ptr(a.ptr(part)), Arg.u32(slices), Arg.ptr(a.ptr(toks)), Arg.ptr(a.ptr(ps))])
+        self.gpu.sync()
+        return a.read_array(toks, 0, rows, np.uint32), a.read_array(ps, 0, rows, np.uint32)
 
     def argmax(self, logits) -> int:
         logits = np.ascontiguousarray(logits, np.float32)
