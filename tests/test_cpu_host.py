@@ -50,3 +50,17 @@ def test_host_metrics_are_the_oracles():
         assert abs(metrics.kl(p, q) - O.kl(p, q)) < 1e-12
     assert metrics.argmax([1.0, float("nan")]) is None and O.argmax([1.0, float("nan")]) is None
     assert metrics.argmax([2.0, 2.0]) == 0
+
+
+def test_panel_layout_round_trips_and_places_each_element():
+    """The batched step's X layout (ops.to_panels): element (t, k) of [n][cols] at
+    ((t / 16 * cols / 8 + k / 8) * 16 + t % 16) * 8 + k % 8, rows past n zero."""
+    import numpy as np
+    from x0ne_core.ops import from_panels, to_panels
+    for n, cols in [(1, 8), (16, 8), (17, 24), (40, 4096)]:
+        m = np.arange(n * cols, dtype=np.uint32).reshape(n, cols) + 1
+        p = to_panels(m)
+        assert p.size == -(-n // 16) * 16 * cols and (p != 0).sum() == n * cols
+        for t, k in [(0, 0), (n - 1, cols - 1), (n // 2, cols // 3)]:
+            assert p[(((t // 16) * (cols // 8) + k // 8) * 16 + t % 16) * 8 + k % 8] == m[t, k]
+        assert (from_panels(p, n, cols) == m).all()

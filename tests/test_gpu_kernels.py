@@ -96,6 +96,21 @@ def test_add_rmsnorm_is_the_oracle_on_random_rows(kernels, seed):
     print(f"MEASURE add_rmsnorm seed {seed}: {same:.6f} of the values bit-equal to the rounded oracle")
 
 
+@pytest.mark.parametrize("h", [8, 256, 1024, 4096, 5120, 8192, 9000])
+def test_panel_norm_is_the_row_norm_bit_for_bit(kernels, h):
+    """The batched step's norm (several rows, out in panels) gives each row the bits of
+    x0ne_add_rmsnorm_bf16, past the values a thread keeps in registers too (h > 8192)."""
+    rng = O.Rng(130 + h)
+    n = 19
+    residual = np.stack([rng.f32s(h, 3.0) for _ in range(n)])
+    x = np.stack([bf16_bits(bf16s_with_edges(rng, h, 3.0)) for _ in range(n)])
+    w = bf16_bits(rng.bf16s(h, 2.0))
+    r, out = kernels.add_rmsnorm_panel(residual, x, w, 1e-6)
+    for t in range(n):
+        r1, o1 = kernels.add_rmsnorm(residual[t], x[t], w, 1e-6)
+        assert (bits_f32(r[t]) == bits_f32(r1)).all() and (out[t] == o1).all(), f"h {h} row {t}"
+
+
 def test_add_rmsnorm_on_zero_denormal_and_non_finite_rows(kernels):
     h = 64
     w = np.ones(h, np.float32)
@@ -260,6 +275,12 @@ def test_few_row_gemm_is_the_oracle_and_its_swiglu_the_swiglu_kernel(kernels, se
     for r in range(n):
         assert (act[r] == kernels.swiglu(gu[r])).all(), f"{what} row {r}: fused SwiGLU"
         assert_close(f"{what} row {r} swiglu", bf16_vals(act[r]), O.swiglu(bf16_vals(gu[r])), BF16_ATOL, BF16_RTOL)
+    # The panel layouts move the same values: the same bits.
+    fp = kernels.gemm_few(bf16_bits(w[:rows * cols]), rows, cols, bf16_bits(x), n, 1, block, rg, x_panel=True)
+    assert (fp.view(np.uint32) == f.view(np.uint32)).all(), f"{what}: X in panels"
+    if rows % 8 == 0:
+        ap = kernels.gemm_few(bf16_bits(w), rows, cols, bf16_bits(x), n, 2, block, rg_glu, x_panel=True, y_panel=True)
+        assert (ap == act).all(), f"{what}: SwiGLU with X and Y in panels"
 
 
 def test_gemv_carries_non_finite_values_to_the_rows_that_read_them(kernels):

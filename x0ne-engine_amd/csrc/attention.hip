@@ -556,8 +556,8 @@ __device__ __forceinline__ float state_get(const float* p) {
 // ...), lane d owns dims d and d + 64 of o, whose loads are issued 8 slices at a time. f: this
 // wavefront's LDS for `active` floats. Every active slice saw a key, so each m is finite. The
 // caller has made other workgroups' states visible (their release, its acquire): plain loads.
-__device__ __forceinline__ void merge_head(const float* __restrict__ s, bf16_t* __restrict__ out_h, uint32_t active,
-                                           float* f) {
+template <class Store>
+__device__ __forceinline__ void merge_head(const float* __restrict__ s, Store&& store, uint32_t active, float* f) {
     const uint32_t lane = threadIdx.x & 63;
     float mx = -INFINITY;
     for (uint32_t y = lane; y < active; y += 64) mx = fmaxf(mx, state_get(s + (size_t)y * X0NE_SPLIT_STATE));
@@ -591,8 +591,8 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ s, bf16_t* 
         o0 = fmaf(state_get(st + lane), f[y], o0);
         o1 = fmaf(state_get(st + lane + 64), f[y], o1);
     }
-    out_h[lane] = f2bf(o0 / l);
-    out_h[lane + 64] = f2bf(o1 / l);
+    store(lane, f2bf(o0 / l));
+    store(lane + 64, f2bf(o1 / l));
     wave_lds_sync();
 }
 
@@ -681,7 +681,15 @@ struct AttnArgs {
     const uint32_t* pos;
     uint32_t q_heads, kv_heads, max_ctx, splits;
     float scale, eps;
+    uint32_t out_panel;      // 0: out row-major [q_heads][128]; t + 1: row t of out in panels
 };
+
+// Where dim d of q head h goes: out row-major, or row t = out_panel - 1 of a [..][q_heads 128]
+// matrix in panels (the batched step's X layout, device.h).
+__device__ __forceinline__ size_t out_index(const AttnArgs& a, uint32_t h, uint32_t d) {
+    const uint32_t k = h * X0NE_HEAD_DIM + d;
+    return a.out_panel ? panel_index(a.out_panel - 1, k, a.q_heads * X0NE_HEAD_DIM) : (size_t)k;
+}
 
 // A wavefront's state into the block's LDS for the block merge.
 template <int G, class T>
@@ -873,7 +881,7 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
 
     if (active == 1) {  // one block holds the whole context: the output directly
         block_merge<G, float>(sh, [&](uint32_t g, uint32_t d, float, float lv, float ov) {
-            a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf(ov / lv);
+            a.out[out_index(a, h0 + g, d)] = f2bf(ov / lv);
         });
         return;
     }
@@ -895,8 +903,8 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
     __syncthreads();
     if (!sh.last) return;  // block-uniform
     for (uint32_t g = wave; g < (uint32_t)G; g += WAVES)
-        merge_head(a.state + (size_t)(h0 + g) * P * X0NE_SPLIT_STATE, a.out + (size_t)(h0 + g) * X0NE_HEAD_DIM,
-                   active, sh.f[wave]);
+        merge_head(a.state + (size_t)(h0 + g) * P * X0NE_SPLIT_STATE,
+                   [&](uint32_t d, bf16_t v) { a.out[out_index(a, h0 + g, d)] = v; }, active, sh.f[wave]);
     __syncthreads();
     if (t == 0) __hip_atomic_store(a.counter + kh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next step
 }
@@ -1011,7 +1019,8 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
 // grid (kv_heads, P, B): sequence b = blockIdx.z has its packed qkv row at qkv + b (q_heads + 2
 // kv_heads) 128, its page table at pages + b seq_pages (its own pages of the shared K/V planes),
 // its position at pos[b], its split state and counters after b (q_heads P) states and b kv_heads
-// counters, and its output at out + b q_heads 128.
+// counters, and its output is row b of out, a [B][q_heads 128] matrix in panels (device.h): the
+// X operand of the batched O projection.
 //
 // x0ne_attention_rope_decode_exact_g*_bf16 is the fused variant with f64 scores, softmax and
 // sums and the f64 scale 1/sqrt(128), one block per kv head over the whole context (grid
@@ -1088,7 +1097,8 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         a.pages = pages + b * seq_pages;                                                                           \
         a.state = state + b * q_heads * splits * X0NE_SPLIT_STATE;                                                 \
         a.counter = counter + b * kv_heads;                                                                        \
-        a.out = out + b * q_heads * X0NE_HEAD_DIM;                                                                 \
+        a.out = out;                                                                                               \
+        a.out_panel = (uint32_t)b + 1;                                                                             \
         a.pos = pos + b;                                                                                           \
         a.q_heads = q_heads;                                                                                       \
         a.kv_heads = kv_heads;                                                                                     \
@@ -1155,7 +1165,8 @@ extern "C" __global__ void __launch_bounds__(64)
     const uint32_t ctx = min(pos[0] + 1u, max_ctx);
     const uint32_t active = split_of(ctx, splits).active;
     if (active <= 1 || splits > MERGE_MAX) return;
-    merge_head(state + (size_t)h * splits * X0NE_SPLIT_STATE, out + (size_t)h * X0NE_HEAD_DIM, active, f);
+    bf16_t* out_h = out + (size_t)h * X0NE_HEAD_DIM;
+    merge_head(state + (size_t)h * splits * X0NE_SPLIT_STATE, [&](uint32_t d, bf16_t v) { out_h[d] = v; }, active, f);
 }
 
 // Per-head decode over the whole context in one block (the reference's E2 witness,

@@ -92,6 +92,15 @@ __device__ __forceinline__ double block_sum_d(double v, double* sh) {
     return t;
 }
 
+// ---- panels ----
+// A [rows][cols] bf16 matrix (cols a multiple of 8) kept as ceil(rows / 16) panels of
+// [cols / 8][16][8]: element (t, k) at ((t / 16 cols / 8 + k / 8) 16 + t % 16) 8 + k % 8. The
+// 16 rows' pieces of 8 columns sit together, so the few-row GEMM (gemm.hip) reads one step of
+// its X operand as one contiguous KiB; the batched step's producers of X write this layout.
+__device__ __forceinline__ size_t panel_index(uint32_t t, uint32_t k, uint32_t cols) {
+    return ((size_t)((t >> 4) * (cols >> 3) + (k >> 3)) * 16 + (t & 15)) * 8 + (k & 7);
+}
+
 // ---- KV pages ----
 // A layer's K plane is [pages][kv_heads][16][128] bf16 (a key row of 128 dims contiguous); its
 // V plane is [pages][kv_heads][128][16] (dim-major within a page: the 16 positions of one dim

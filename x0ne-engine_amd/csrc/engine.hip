@@ -416,13 +416,13 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("prefill_act", n * c.inter * 2, CD, &e->p_act));
     }
     if (e->max_batch > 1) {
-        const uint64_t b = e->max_batch;
+        const uint64_t b = e->max_batch, bp = (b + 15) / 16 * 16;  // panels hold whole tiles of 16 rows
         X0NE_TRY(al("batch_residual", b * c.hidden * 4, CD, &e->b_res));
         X0NE_TRY(al("batch_delta", b * c.hidden * 2, CD, &e->b_delta));
-        X0NE_TRY(al("batch_normed", b * c.hidden * 2, CD, &e->b_x));
+        X0NE_TRY(al("batch_normed", bp * c.hidden * 2, CD, &e->b_x));
         X0NE_TRY(al("batch_qkv", b * c.qkv_rows() * 2, CD, &e->b_qkv));
-        X0NE_TRY(al("batch_attn", b * c.q_dim() * 2, CD, &e->b_attn));
-        X0NE_TRY(al("batch_act", b * c.inter * 2, CD, &e->b_act));
+        X0NE_TRY(al("batch_attn", bp * c.q_dim() * 2, CD, &e->b_attn));
+        X0NE_TRY(al("batch_act", bp * c.inter * 2, CD, &e->b_act));
         X0NE_TRY(al("batch_logits", b * c.vocab * 4, CD, &e->b_logits));
         X0NE_TRY(al("batch_split_state", b * x0ne_split_state_bytes((uint32_t)c.q_heads, e->bsplit.splits), CD,
                     &e->b_state));
@@ -1404,7 +1404,7 @@ x0ne_status batch_norm(x0ne_engine* e, uint32_t B, x0ne_slice w) {
     const void* wp = e->d(w);
     void* xn = e->d(e->b_x);
     void* args[] = {(void*)&res, (void*)&dl, (void*)&wp, (void*)&xn, (void*)&h, (void*)&eps};
-    return launch_rows(e, (const void*)&x0ne_add_rmsnorm_bf16, dim3(B), dim3(256), args, "batch add_rmsnorm");
+    return launch_rows(e, (const void*)&x0ne_add_rmsnorm_panel_bf16, dim3(B), dim3(256), args, "batch add_rmsnorm");
 }
 
 // Layer 0's norm: each sequence's embedding row on a zero residual.
@@ -1418,12 +1418,12 @@ x0ne_status batch_embed_norm(x0ne_engine* e, uint32_t B) {
     void* xn = e->d(e->b_x);
     void* args[] = {(void*)&table, (void*)&toks, (void*)&res, (void*)&wp, (void*)&xn, (void*)&h, (void*)&vocab,
                     (void*)&eps};
-    return launch_rows(e, (const void*)&x0ne_embed_rmsnorm_bf16, dim3(B), dim3(256), args, "batch embedding");
+    return launch_rows(e, (const void*)&x0ne_embed_rmsnorm_panel_bf16, dim3(B), dim3(256), args, "batch embedding");
 }
 
 x0ne_status batch_qkv(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].qkv), c.qkv_rows(), c.hidden, e->d(e->b_x), B, e->d(e->b_qkv), 0);
+    return skinny(e->gpu, e->d(e->L[l].qkv), c.qkv_rows(), c.hidden, e->d(e->b_x), B, e->d(e->b_qkv), 0, PANEL_X);
 }
 
 x0ne_status batch_attention(x0ne_engine* e, uint32_t B, uint64_t l) {
@@ -1460,24 +1460,25 @@ x0ne_status batch_attention(x0ne_engine* e, uint32_t B, uint64_t l) {
 
 x0ne_status batch_o(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].o), c.hidden, c.q_dim(), e->d(e->b_attn), B, e->d(e->b_delta), 0);
+    return skinny(e->gpu, e->d(e->L[l].o), c.hidden, c.q_dim(), e->d(e->b_attn), B, e->d(e->b_delta), 0, PANEL_X);
 }
 
 x0ne_status batch_gate_up(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].gate_up), c.inter, c.hidden, e->d(e->b_x), B, e->d(e->b_act), 2);
+    return skinny(e->gpu, e->d(e->L[l].gate_up), c.inter, c.hidden, e->d(e->b_x), B, e->d(e->b_act), 2,
+                  PANEL_X | PANEL_Y);
 }
 
 x0ne_status batch_down(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].down), c.hidden, c.inter, e->d(e->b_act), B, e->d(e->b_delta), 0);
+    return skinny(e->gpu, e->d(e->L[l].down), c.hidden, c.inter, e->d(e->b_act), B, e->d(e->b_delta), 0, PANEL_X);
 }
 
 // The f32 LM head over the B normed rows, then each row's argmax into its token, position + 1.
 x0ne_status batch_head(x0ne_engine* e, uint32_t B) {
     const Cfg& c = e->c;
     X0NE_TRY(skinny(e->gpu, e->d(e->has_lm_head ? e->lm_head : e->embed), c.vocab, c.hidden, e->d(e->b_x), B,
-                    e->d(e->b_logits), 1));
+                    e->d(e->b_logits), 1, PANEL_X));
     const void* lg = e->d(e->b_logits);
     uint32_t vocab = (uint32_t)c.vocab, slices = ARGMAX_SLICES;
     void* part = e->d(e->b_argmax);

@@ -153,10 +153,18 @@ extern "C" __global__ void __launch_bounds__(256)
 //    (or a token past n, a W row past rows) is a raw buffer load at an offset past the buffer,
 //    which returns zeros without touching memory.
 //  - The wavefronts' partial tiles are summed in LDS in wavefront order (deterministic).
-// out_f32 0: Y bf16, 1: Y f32. GLU: SwiGLU over the packed [gate; up] W of 2 rows rows: the block
-// also takes the up rows rows + 16 (RG b + g) .., and writes act[t][r] = bf16(g / (1 + e^-g) u)
-// of the bf16-rounded g and u, in f64 (x0ne_swiglu_bf16 of the bf16 projection).
+// flags: FEW_F32 Y f32 (else bf16); FEW_X_PANEL X in panels (below); FEW_Y_PANEL Y in panels
+// (bf16). GLU: SwiGLU over the packed [gate; up] W of 2 rows rows: the block also takes the up
+// rows rows + 16 (RG b + g) .., and writes act[t][r] = bf16(g / (1 + e^-g) u) of the
+// bf16-rounded g and u, in f64 (x0ne_swiglu_bf16 of the bf16 projection).
+//
+// Panels: a [n][cols] bf16 matrix stored as ceil(n / 16) panels of [cols / 8][16][8]: element
+// (t, k) at ((t / 16 * cols / 8 + k / 8) 16 + t % 16) 8 + k % 8. One step's X operand is then one
+// contiguous KiB; row-major, its 16 rows lie cols apart and meet in the same L2 channels, which
+// costs the W stream up to a fifth of its rate at 16 rows (measured on MI355X).
 namespace {
+
+constexpr uint32_t FEW_F32 = 1, FEW_X_PANEL = 2, FEW_Y_PANEL = 4;
 
 // Byte offset of columns k .. k + 7 of row r, or past every buffer.
 __device__ __forceinline__ uint32_t sk_off(bool in, uint32_t r, uint32_t cols, uint32_t k) {
@@ -166,14 +174,18 @@ __device__ __forceinline__ uint32_t sk_off(bool in, uint32_t r, uint32_t cols, u
 template <int TT, int RG, int U, bool GLU, int MAXV>
 __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
                                          void* __restrict__ y, uint32_t rows, uint32_t cols, uint32_t n,
-                                         uint32_t out_f32, f32x4* part) {
+                                         uint32_t flags, f32x4* part) {
     constexpr int KINDS = GLU ? 2 : 1;
     const uint32_t b = blockIdx.x, V = blockDim.x >> 6;
+    const bool out_f32 = flags & FEW_F32, x_panel = flags & FEW_X_PANEL, y_panel = flags & FEW_Y_PANEL;
     // Grid-uniform exits for a launch that does not fit.
-    if (b * 16 * RG >= rows || n == 0 || n > 16 * TT || cols % 8 != 0 || V > MAXV || (GLU && out_f32)) return;
+    if (b * 16 * RG >= rows || n == 0 || n > 16 * TT || cols % 8 != 0 || V > MAXV || flags > 7 ||
+        (out_f32 && (GLU || y_panel)) || (y_panel && rows % 8 != 0))
+        return;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t r = lane & 15, q4 = lane >> 4;
-    const auto xr = rsrc(x, (uint64_t)n * cols * 2);
+    // Panels hold whole tiles of 16 rows.
+    const auto xr = rsrc(x, (uint64_t)(x_panel ? (n + 15) / 16 * 16 : n) * cols * 2);
     const auto wr = rsrc(w, (uint64_t)KINDS * rows * cols * 2);
     const uint32_t steps = (cols + 31) / 32, per = (steps + V - 1) / V;
     const uint32_t s_begin = min(wave * per, steps), s_end = min(s_begin + per, steps);
@@ -189,7 +201,11 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
         const uint32_t k = 32 * s + 8 * q4;
         const bool in = s < s_end && k < cols;  // a K tail: pieces past the row read zeros
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) xa[u][tt] = bload(xr, sk_off(in && 16 * tt + r < n, 16 * tt + r, cols, k));
+        for (int tt = 0; tt < TT; ++tt) {
+            const uint32_t t = 16 * tt + r;
+            const uint32_t off = x_panel ? (uint32_t)panel_index(t, k, cols) * 2 : (t * cols + k) * 2;
+            xa[u][tt] = bload(xr, in && t < n ? off : OFF_NONE);
+        }
 #pragma unroll
         for (int kd = 0; kd < KINDS; ++kd)
 #pragma unroll
@@ -237,7 +253,7 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
             for (int i = 0; i < 4; ++i) {
                 const uint32_t t = 16 * tt + 4 * q4 + i;
                 if (t >= n) continue;
-                const size_t o = (size_t)t * rows + wrow;
+                const size_t o = y_panel ? panel_index(t, wrow, rows) : (size_t)t * rows + wrow;
                 if (GLU) {
                     const double gv = (double)bf2f(f2bf(sg[i])), uv = (double)bf2f(f2bf(su[i]));
                     static_cast<bf16_t*>(y)[o] = f2bf((float)(gv / (1.0 + exp(-gv)) * uv));
@@ -254,14 +270,14 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
 }  // namespace
 
 // x0ne_gemm_few_t{TT}_r{RG}[_swiglu]_bf16: grid (ceil(rows / (16 RG))), block 64 V threads
-// (V <= MAXV); n in 1 .. 16 TT; cols a multiple of 8; X, W below 4 GiB - 16 bytes. The
-// SwiGLU variants write bf16 (out_f32 must be 0).
+// (V <= MAXV); n in 1 .. 16 TT; cols a multiple of 8 (of 8 and rows of 8 for a Y panel); X, W
+// below 4 GiB - 16 bytes; flags as above (FEW_F32 = 1 not with SwiGLU or a Y panel).
 #define X0NE_FEW(NAME, TT, RG, U, GLU, MAXV)                                                                     \
     extern "C" __global__ void __launch_bounds__(64 * MAXV)                                                       \
         NAME(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, uint32_t rows,     \
-             uint32_t cols, uint32_t n, uint32_t out_f32) {                                                       \
+             uint32_t cols, uint32_t n, uint32_t flags) {                                                         \
         __shared__ f32x4 part[(GLU ? 2 : 1) * MAXV * RG * TT * 64];                                               \
-        few_rows<TT, RG, U, GLU, MAXV>(w, x, y, rows, cols, n, out_f32, part);                                    \
+        few_rows<TT, RG, U, GLU, MAXV>(w, x, y, rows, cols, n, flags, part);                                      \
     }
 #ifndef X0NE_FEW_NO_TABLE
 X0NE_FEW(x0ne_gemm_few_t1_r1_bf16, 1, 1, 12, false, 8)

@@ -71,8 +71,11 @@ __global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t in
 __global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
 __global__ void x0ne_argmax_slices_f32(const float* logits, uint32_t n, uint32_t slices, uint32_t* partial);
 __global__ void x0ne_argmax_pick_advance(const uint32_t* partial, uint32_t slices, uint32_t* tokens, uint32_t* pos);
-__global__ void x0ne_embed_rmsnorm_bf16(const bf16_t* table, const uint32_t* tokens, float* residual,
-                                        const bf16_t* w, bf16_t* out, uint32_t hidden, uint32_t vocab, float eps);
+__global__ void x0ne_embed_rmsnorm_panel_bf16(const bf16_t* table, const uint32_t* tokens, float* residual,
+                                              const bf16_t* w, bf16_t* out, uint32_t hidden, uint32_t vocab,
+                                              float eps);
+__global__ void x0ne_add_rmsnorm_panel_bf16(float* residual, const bf16_t* x, const bf16_t* w, bf16_t* out,
+                                            uint32_t hidden, float eps);
 __global__ void x0ne_advance_u32(uint32_t* pos);
 __global__ void x0ne_feed_u32(const uint32_t* ids, uint32_t i, uint32_t* tokens, uint32_t* pos);
 __global__ void x0ne_gemm_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, uint32_t n,

@@ -51,9 +51,9 @@ extern "C" __global__ void __launch_bounds__(128)
 // loop. Each thread sums its squares in that order, then the block (block_sum_d).
 constexpr uint32_t NORM_HELD = 32;  // values per thread kept in registers: hidden <= 8192 at 256
 
-template <class Src>
+template <class Src, class Dst>
 __device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& src, const bf16_t* __restrict__ w,
-                                            bf16_t* __restrict__ out, uint32_t hidden, float eps) {
+                                            Dst&& out, uint32_t hidden, float eps) {
     __shared__ double sh[16];
     const uint32_t t = threadIdx.x, step = blockDim.x;
     float r[NORM_HELD];
@@ -84,10 +84,10 @@ __device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& 
 #pragma unroll
     for (uint32_t c = 0; c < NORM_HELD; ++c) {
         const uint32_t i = t + c * step;
-        if (i < hidden) out[i] = f2bf((float)((double)r[c] * scale * (double)bf2f(w[i])));
+        if (i < hidden) out(i) = f2bf((float)((double)r[c] * scale * (double)bf2f(w[i])));
     }
     for (uint32_t i = t + NORM_HELD * step; i < hidden; i += step)
-        out[i] = f2bf((float)((double)residual[i] * scale * (double)bf2f(w[i])));
+        out(i) = f2bf((float)((double)residual[i] * scale * (double)bf2f(w[i])));
 }
 
 extern "C" __global__ void __launch_bounds__(256)
@@ -96,24 +96,43 @@ extern "C" __global__ void __launch_bounds__(256)
     const size_t base = (size_t)blockIdx.x * hidden;
     float* res = residual + base;
     const bf16_t* xr = x + base;
-    rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w, out + base, hidden, eps);
+    bf16_t* o = out + base;
+    rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w, [&](uint32_t i) -> bf16_t& { return o[i]; },
+                hidden, eps);
+}
+
+// x0ne_add_rmsnorm_bf16 with out in panels (hidden a multiple of 8): the batched step's norms,
+// whose rows feed the few-row GEMM. The same bits at the panel positions. grid (rows), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_add_rmsnorm_panel_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x,
+                                const bf16_t* __restrict__ w, bf16_t* __restrict__ out, uint32_t hidden, float eps) {
+    const uint32_t row = blockIdx.x;
+    const size_t base = (size_t)row * hidden;
+    float* res = residual + base;
+    const bf16_t* xr = x + base;
+    if (hidden % 8 != 0) return;
+    rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w,
+                [&](uint32_t i) -> bf16_t& { return out[panel_index(row, i, hidden)]; }, hidden, eps);
 }
 
 // The first norm of a batched step: residual[r] = 0 + table[tokens[r]] (f32; an id >= vocab gives
-// a zero row) and out[r] its RMSNorm, the bits x0ne_embedding_bf16 followed by
-// x0ne_add_rmsnorm_bf16 on a zero residual give. grid (rows), block 256.
+// a zero row) and row r of out (in panels, hidden a multiple of 8) its RMSNorm: the bits
+// x0ne_embedding_bf16 followed by x0ne_add_rmsnorm_bf16 on a zero residual give. grid (rows),
+// block 256.
 extern "C" __global__ void __launch_bounds__(256)
-    x0ne_embed_rmsnorm_bf16(const bf16_t* __restrict__ table, const uint32_t* __restrict__ tokens,
-                            float* __restrict__ residual, const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
-                            uint32_t hidden, uint32_t vocab, float eps) {
-    const size_t base = (size_t)blockIdx.x * hidden;
+    x0ne_embed_rmsnorm_panel_bf16(const bf16_t* __restrict__ table, const uint32_t* __restrict__ tokens,
+                                  float* __restrict__ residual, const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
+                                  uint32_t hidden, uint32_t vocab, float eps) {
+    const uint32_t row = blockIdx.x;
+    if (hidden % 8 != 0) return;
+    const size_t base = (size_t)row * hidden;
     const uint32_t tok = tokens[blockIdx.x];
     const bf16_t* src = table + (size_t)(tok < vocab ? tok : 0) * hidden;
     const bool in = tok < vocab;
     rmsnorm_row(residual + base, [&](uint32_t i) {
         const float v = bf2f(src[i]);  // row 0 for an id past the table, then not used
         return 0.0f + (in ? v : 0.0f);
-    }, w, out + base, hidden, eps);
+    }, w, [&](uint32_t i) -> bf16_t& { return out[panel_index(row, i, hidden)]; }, hidden, eps);
 }
 
 // Per-head RMSNorm of q and k, rotate-half RoPE, and the K/V write into the paged cache

@@ -259,30 +259,35 @@ static constexpr uint64_t GEMM_MAX_BYTES = 0xFFFFFFF0ull;
 namespace x0ne {
 
 x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
-                   uint32_t mode) {
+                   uint32_t mode, uint32_t panels) {
     const uint64_t wrows = mode == 2 ? 2 * rows : rows;
-    if (n == 0 || n > SKINNY_MAX_ROWS || rows == 0 || cols == 0 || cols % 8 != 0 || mode > 2 ||
+    if (n == 0 || n > SKINNY_MAX_ROWS || rows == 0 || cols == 0 || cols % 8 != 0 || mode > 2 || (panels & ~6u) ||
+        ((panels & 4) && (mode == 1 || rows % 8 != 0)) ||
         wrows * cols * 2 > GEMM_MAX_BYTES || n * cols * 2 > GEMM_MAX_BYTES || (uintptr_t)w % 16 != 0 ||
         (uintptr_t)x % 16 != 0)
         return fail(X0NE_ERR_FORMAT, "few-row gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
                                          std::to_string(n) + ", mode " + std::to_string(mode));
-    // Row groups per block (each X piece serves RG W pieces) and wavefronts per block, from a
-    // sweep on MI355X over the decode shapes: at most 8 rows of X the L2 serves X cheaply and
-    // more blocks win (RG 2 while 192 blocks remain); at 9 to 16 rows X costs as much as W per
-    // piece, and RG grows while 160 blocks remain.
+    // Row groups per block (each X piece serves RG W pieces) and wavefronts per block, from sweeps
+    // on MI355X over the decode shapes (X in panels, 8 and 16 rows): a CU streams a few hundred
+    // KiB of a launch fastest alone, so a launch of up to two blocks per CU takes RG so that at
+    // most one block lands on each CU (a CU with two finishes last); large launches (the LM
+    // head) take RG 2 at up to 8 rows of X and 8 beyond, where each X piece costs as much as a
+    // W piece; SwiGLU launches, two W pieces per X piece already, keep RG 1.
     const bool glu = mode == 2;
     auto blocks_of = [&](uint32_t rg) { return (uint32_t)((rows + 16 * rg - 1) / (16 * rg)); };
     uint32_t rg = 1, waves = 4;
     const void* fn = nullptr;
     if (n <= 16) {
         if (glu) {
-            rg = n > 8 && blocks_of(2) >= 1024 ? 2 : 1;
-            fn = rg == 2 ? (const void*)&x0ne_gemm_few_t1_r2_swiglu_bf16 : (const void*)&x0ne_gemm_few_t1_r1_swiglu_bf16;
-            waves = blocks_of(rg) >= 1024 ? 8 : 4;
+            fn = (const void*)&x0ne_gemm_few_t1_r1_swiglu_bf16;
+            waves = blocks_of(1) >= 4 * g->cus ? 8 : 4;
         } else {
-            const uint32_t min_blocks = n <= 8 ? 192 : 160, max_rg = n <= 8 ? 2 : 8;
-            for (uint32_t c = 2; c <= max_rg; c *= 2)
-                if (blocks_of(c) >= min_blocks) rg = c;
+            if (blocks_of(1) <= g->cus)
+                rg = 1;
+            else if (blocks_of(2) <= g->cus)
+                rg = 2;
+            else if (blocks_of(1) >= 8 * g->cus)
+                rg = n <= 8 ? 2 : 8;
             fn = rg == 1   ? (const void*)&x0ne_gemm_few_t1_r1_bf16
                  : rg == 2 ? (const void*)&x0ne_gemm_few_t1_r2_bf16
                  : rg == 4 ? (const void*)&x0ne_gemm_few_t1_r4_bf16
@@ -298,8 +303,8 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
     } else {
         fn = glu ? (const void*)&x0ne_gemm_few_t4_r1_swiglu_bf16 : (const void*)&x0ne_gemm_few_t4_r1_bf16;
     }
-    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, f32 = mode == 1 ? 1u : 0u;
-    void* args[] = {(void*)&w, (void*)&x, (void*)&y, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&f32};
+    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, flags = (mode == 1 ? 1u : 0u) | panels;
+    void* args[] = {(void*)&w, (void*)&x, (void*)&y, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&flags};
     g->counts.gemms++;
     g->counts.launches++;
     X0NE_HIP(x0ne_launch(fn, dim3(blocks_of(rg)), dim3(64 * waves), args, 0, g->stream), "few-row gemm");
@@ -317,7 +322,7 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
     const uint64_t ob = out_f32 ? 4 : 2;
     if (n >= 2 && n <= SKINNY_MAX_ROWS && cols % 8 == 0 && rows * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 &&
         x % 16 == 0)
-        return x0ne::skinny(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 ? 1 : 0);
+        return x0ne::skinny(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 ? 1 : 0, 0);
     // Many rows: one matrix-core GEMM launch, the weights read once.
     if (n > SKINNY_MAX_ROWS && cols % 8 == 0 && n <= UINT32_MAX && rows * cols * 2 <= GEMM_MAX_BYTES &&
         n * cols * 2 <= GEMM_MAX_BYTES) {

@@ -89,6 +89,24 @@ def to_pages(rows: np.ndarray, kv_heads: int, page_of, pool: int, fill=NAN_BF16,
     return np.ascontiguousarray(out.transpose(0, 1, 3, 2)) if dim_major else out
 
 
+def to_panels(m) -> np.ndarray:
+    """[n][cols] (cols a multiple of 8) -> the panel layout of the batched step (ceil(n / 16)
+    panels of [cols / 8][16][8], rows past n zero), flattened."""
+    m = np.asarray(m)
+    n, cols = m.shape
+    tiles = -(-n // 16)
+    full = np.zeros((tiles * 16, cols), m.dtype)
+    full[:n] = m
+    return np.ascontiguousarray(full.reshape(tiles, 16, cols // 8, 8).transpose(0, 2, 1, 3)).reshape(-1)
+
+
+def from_panels(flat, n: int, cols: int) -> np.ndarray:
+    """The inverse of to_panels: rows 0 .. n - 1 of [n][cols]."""
+    tiles = -(-n // 16)
+    p = np.asarray(flat)[:tiles * 16 * cols].reshape(tiles, cols // 8, 16, 8).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(p.reshape(tiles * 16, cols)[:n])
+
+
 def v_offset(page: int, kv_heads: int, kh: int, slot: int, dim: int) -> int:
     """Element index of (slot, dim) of kv head kh in V page `page` (dim-major pages)."""
     return ((page * kv_heads + kh) * HEAD_DIM + dim) * PAGE + slot
@@ -124,6 +142,29 @@ class Kernels:
         return a.read_array(out, 0, hidden, np.uint16)
 
     # -- add_rmsnorm (ops.rs:272-300) --
+    def add_rmsnorm_panel(self, residual, x, w, eps: float):
+        """The batched step's norm over rows ([n][h] residual f32 and x bf16 bits, one launch):
+        (residual after, out [n][h] read back from its panels)."""
+        residual = np.ascontiguousarray(residual, np.float32)
+        n, h = residual.shape
+        tiles = -(-n // 16)
+        a = self._arena()
+        r = a.alloc("residual", residual.nbytes, Class.CLIENT_DATA)
+        xs = a.alloc("x", n * h * 2, Class.CLIENT_DATA)
+        ws = a.alloc("w", h * 2, Class.WEIGHTS)
+        out = a.alloc("out", tiles * 16 * h * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.scrub_client_data()
+        a.write(r, 0, residual)
+        a.write(xs, 0, np.asarray(x, np.uint16))
+        a.write(ws, 0, np.asarray(w, np.uint16))
+        self.gpu.launch("x0ne_add_rmsnorm_panel_bf16", n, 256,
+                        [Arg.ptr(a.ptr(r)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(out)), Arg.u32(h),
+                         Arg.f32(eps)])
+        self.gpu.sync()
+        return (a.read_array(r, 0, n * h, np.float32).reshape(n, h),
+                from_panels(a.read_array(out, 0, tiles * 16 * h, np.uint16), n, h))
+
     def add_rmsnorm(self, residual, x, w, eps: float):
         residual = np.ascontiguousarray(residual, np.float32)
         h = residual.size
@@ -420,7 +461,8 @@ class Kernels:
         (grid (kv_heads, P, B)): sequence b's packed qkv row qkv[b] at position ctxs[b] - 1 over
         its keys 0..ctxs[b]-1 (ks[b], vs[b] hold its rows 0..ctxs[b]-2), each sequence in its
         own run of ceil(max_ctx / 16) entries of one shuffled page table over shared K/V planes.
-        Returns out [B][q_dim] and the K/V rows written at each sequence's position."""
+        Returns out [B][q_dim] (the kernel writes it in panels) and the K/V rows written at each
+        sequence's position."""
         h.check()
         qd, kvd, hd = h.q_dim, h.kv_dim, h.head_dim
         B = len(ctxs)
@@ -449,7 +491,7 @@ class Kernels:
         sl = {name: a.alloc(name, size, cls) for name, size, cls in [
             ("qkv", qkv.nbytes, Class.CLIENT_DATA), ("k", kp.nbytes, Class.CLIENT_DATA),
             ("v", vp.nbytes, Class.CLIENT_DATA), ("pt", pool * 4, Class.WEIGHTS), ("pos", B * 4, Class.CLIENT_DATA),
-            ("out", B * qd * 2, Class.CLIENT_DATA),
+            ("out", -(-B // 16) * 16 * qd * 2, Class.CLIENT_DATA),
             ("state", B * split_state_bytes(h.q_heads, plan.splits), Class.CLIENT_DATA),
             ("counter", B * h.kv_heads * 4, Class.CLIENT_DATA), ("q_norm", hd * 2, Class.WEIGHTS),
             ("k_norm", hd * 2, Class.WEIGHTS), ("inv_freq", hd // 2 * 4, Class.WEIGHTS),
@@ -476,7 +518,7 @@ class Kernels:
         counts = a.read_array(sl["counter"], 0, B * h.kv_heads, np.uint32)
         if counts.any():
             raise GpuError(f"split-K counters not reset: {counts.tolist()}")
-        out = a.read_array(sl["out"], 0, B * qd, np.uint16).reshape(B, qd)
+        out = from_panels(a.read_array(sl["out"], 0, sl["out"].len // 2, np.uint16), B, qd)
         k_all = a.read_array(sl["k"], 0, kp.size, np.uint16).reshape(kp.shape)
         v_all = a.read_array(sl["v"], 0, vp.size, np.uint16).reshape(vp.shape)
         k_rows, v_rows = [], []
@@ -489,30 +531,40 @@ class Kernels:
     FEW_KERNELS = {(1, 1): 8, (1, 2): 8, (1, 4): 8, (1, 8): 8, (2, 1): 8, (2, 2): 8, (4, 1): 8}
     FEW_SWIGLU = {(1, 1), (1, 2), (2, 1), (4, 1)}
 
-    def gemm_few(self, w, rows, cols, x, n, mode: int, block: int = 256, rg: int = 1) -> np.ndarray:
+    def gemm_few(self, w, rows, cols, x, n, mode: int, block: int = 256, rg: int = 1, x_panel: bool = False,
+                 y_panel: bool = False) -> np.ndarray:
         """One few-row GEMM kernel itself (x0ne_gemm_few_t{TT}_r{RG}[_swiglu]_bf16, TT = 1, 2
         or 4 tiles of 16 rows of X by n): mode 0 bf16 Y, 1 f32 Y, 2 SwiGLU over the packed
-        [gate; up] W of 2 rows rows (act [n][rows] bf16); `rg` row groups of 16 per block."""
+        [gate; up] W of 2 rows rows (act [n][rows] bf16); `rg` row groups of 16 per block;
+        x_panel / y_panel: X handed over, Y read back, in the panel layout (returned
+        row-major either way)."""
         wrows = 2 * rows if mode == 2 else rows
         tt = 1 if n <= 16 else 2 if n <= 32 else 4
         if w.size != wrows * cols or x.size != n * cols or not 1 <= n <= 64 or cols % 8 or \
                 (tt, rg) not in self.FEW_KERNELS or (mode == 2 and (tt, rg) not in self.FEW_SWIGLU) or \
                 block // 64 > self.FEW_KERNELS[(tt, rg)]:
             raise FormatError("gemm_few: lengths or variant")
+        if y_panel and (mode == 1 or rows % 8):
+            raise FormatError("gemm_few: a Y panel is bf16 with rows a multiple of 8")
         name = f"x0ne_gemm_few_t{tt}_r{rg}{'_swiglu' if mode == 2 else ''}_bf16"
         ob = 4 if mode == 1 else 2
+        xin = to_panels(np.asarray(x, np.uint16).reshape(n, cols)) if x_panel else np.asarray(x, np.uint16)
+        yrows = -(-n // 16) * 16 if y_panel else n
         a = self._arena()
         ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
-        xs = a.alloc("x", x.size * 2, Class.CLIENT_DATA)
-        ys = a.alloc("y", n * rows * ob, Class.CLIENT_DATA)
+        xs = a.alloc("x", xin.size * 2, Class.CLIENT_DATA)
+        ys = a.alloc("y", yrows * rows * ob, Class.CLIENT_DATA)
         self._freeze(a)
+        a.scrub_client_data()
         a.write(ws, 0, np.asarray(w, np.uint16))
-        a.write(xs, 0, np.asarray(x, np.uint16))
+        a.write(xs, 0, xin)
+        flags = (1 if mode == 1 else 0) | (2 if x_panel else 0) | (4 if y_panel else 0)
         self.gpu.launch(name, (rows + 16 * rg - 1) // (16 * rg), block,
                         [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(cols),
-                         Arg.u32(n), Arg.u32(1 if mode == 1 else 0)])
+                         Arg.u32(n), Arg.u32(flags)])
         self.gpu.sync()
-        return a.read_array(ys, 0, n * rows, np.float32 if mode == 1 else np.uint16).reshape(n, rows)
+        y = a.read_array(ys, 0, yrows * rows, np.float32 if mode == 1 else np.uint16)
+        return from_panels(y, n, rows) if y_panel else y.reshape(n, rows)
 
     def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None,
                              grouped=False):
