@@ -37,6 +37,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)n, RSRC_WORD3);
 }
 
+// The default cache policy throughout: a non-temporal hint on the few-row GEMM's weight stream
+// (which speeds the decode GEMV's, gemv.hip) made its launches 5-15 % slower on MI355X.
 __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);

@@ -74,8 +74,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, RSRC_WORD3);
 }
 
+// Cache policy of the weight stream: non-temporal (each weight byte is read once per step, so
+// keeping it in the L2 or the Infinity Cache only evicts what is reused). Measured on MI355X: a
+// streaming read of the LM head's 1.25 GB takes 201 µs with it, 218 µs without.
+constexpr int CPOL_NT = 2;
+
+template <int CPOL = 0>
 __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL);
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
 
@@ -334,7 +340,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
             const uint32_t row = row_of(p.g, r, in);
             const auto rs = rsrc(a.w + (size_t)(in && live ? row : 0) * a.cols, in && live ? a.cols * 2 : 0);
 #pragma unroll
-            for (int j = 0; j < BATCH; ++j) w[r][j] = load16(rs, chunk(p.b, j) * 16);
+            for (int j = 0; j < BATCH; ++j) w[r][j] = load16<CPOL_NT>(rs, chunk(p.b, j) * 16);
         }
     };
     // Batches of a group run b0, b0 + 1, ..., NB - 1, 0, ..., b0 - 1; the group ends at its last.
