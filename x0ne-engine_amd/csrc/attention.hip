@@ -325,11 +325,13 @@ struct NewRow {
     const bf16_t* k;     // LDS, 128 bf16: the rotated K row (16-byte aligned)
     const bf16_t* v;     // LDS, 128 bf16: the V row
 };
+// first_pages, when given, holds tile t0's four page-table entries, read before ctx was known.
 template <class Prologue>
 __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewRow& fx, const bf16_t* __restrict__ kc,
                                                  const bf16_t* __restrict__ vc, const uint32_t* __restrict__ pages, uint32_t kh, uint32_t kv_heads,
                                                  uint32_t ctx, uint32_t ctx_col, uint32_t t0, uint32_t tstep,
-                                                 uint32_t t_end, float scale, float& m_out, float& l_out, f32x4 o[8]) {
+                                                 uint32_t t_end, float scale, float& m_out, float& l_out, f32x4 o[8],
+                                                 const uint32_t* first_pages = nullptr) {
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, q4 = lane >> 4;
     const uint32_t ntiles = min(t_end, (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE);  // this wavefront's end
     const auto kr = plane_rsrc(kc, OFF_NONE), vr = plane_rsrc(vc, OFF_NONE);
@@ -379,7 +381,13 @@ __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewR
     uint4 ka[2][2][4], vb[2][8];
     // Loads only for tiles that exist (wavefront-uniform branches): a load past the last tile
     // would still cost its address cycles in the CU's memory pipeline.
-    tile_pages(t0, pg);
+    if (first_pages) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            pg[i] = (t0 < ntiles && t0 * X0NE_SPLIT_TILE + X0NE_PAGE * i < ctx) ? first_pages[i] : 0u;
+    } else {
+        tile_pages(t0, pg);
+    }
     if (t0 < ntiles) {
         load_k(t0, pg, ka);
         load_v(t0, pg, vb);
@@ -794,6 +802,15 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
         }
     }
 
+    // Slice 0's wavefront w starts at tile w whatever the context: its page-table entries are
+    // requested with pos rather than after it (clamped below max_ctx, unused past ctx).
+    uint32_t first_pages[4] = {0u, 0u, 0u, 0u};
+    if (y == 0) {
+        const uint32_t last_page = (a.max_ctx + X0NE_PAGE - 1) / X0NE_PAGE - 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) first_pages[i] = a.pages[min(4 * wave + i, last_page)];
+    }
+
     const uint32_t pos = a.pos[0];
     const uint32_t ctx = min(pos + 1u, a.max_ctx);
     const Split sp = split_of(ctx, P);
@@ -863,7 +880,7 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
     float mw, lw;
     f32x4 ow[8];
     attend_wave_mfma(prologue, fx, a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, ctx, t_begin, BLOCK_TILES, t_end,
-                     a.scale, mw, lw, ow);
+                     a.scale, mw, lw, ow, y == 0 ? first_pages : nullptr);
     {
         const uint32_t n = lane & 15, q4 = lane >> 4;
         if (q4 == 0 && n < (uint32_t)G) {
