@@ -148,14 +148,15 @@ def copy_calibration(n: int):
 
 def attention_line(args) -> dict:
     """the isolated decode attention (Qwen3-8B geometry, 32 q / 8 kv heads)
-    at ctx 1k / 8k / 32k and P in {1, 4, 16}, each launch over distinct K/V planes (more than
+    at ctx 1k / 8k / 32k and P in {1, 4, 16} (the configuration's) and 32 (the engine's), each
+    launch over distinct K/V planes (more than
     512 MiB rotated); bytes per launch 2 ctx 8 128 2 (K + V) + Q + out + the split states."""
     from x0ne_core.gpu import Gpu
     g = Gpu()
     qh, kvh = 32, 8
     rows = []
     for ctx in (1024, 8192, 32768):
-        for P in (1, 4, 16):
+        for P in (1, 4, 16, 32):
             us, planes = g.time_attention(qh, kvh, ctx, P, args.attention_iters, SEED)
             nbytes = 2 * ctx * kvh * 128 * 2 + qh * 128 * 2 * 2 + (qh * P * 132 * 4 if P > 1 else 0)
             rows.append({"ctx": ctx, "splits": P, "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
