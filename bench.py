@@ -114,12 +114,15 @@ def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, pr
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qwen3-8b-decode_hbm-bytes.md")
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 byte-counter summary
+BATCH8_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qwen3-8b-decode-batch8_hbm-bytes.md")
+
+
+def measured_traffic(kernel: str, profile: str = TRAFFIC_PROFILE):
+    """HBM bytes per launch of `kernel` from a committed rocprofv3 byte-counter summary
     (FETCH_SIZE and WRITE_SIZE runs, scaled by a copy of known size), or None."""
     import re
     try:
-        with open(TRAFFIC_PROFILE) as fh:
+        with open(profile) as fh:
             m = re.search(rf"^traffic_bytes_per_launch {kernel} = (\d+)$", fh.read(), re.M)
     except OSError:
         return None
@@ -234,6 +237,8 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
         others[k] = {"kernel_us": round(kus, 2), "wall_us": round(wus, 2)}
     print(f"[bench] batched gate_up {avg_us:.2f} us ({achieved:.0f} GB/s), {wall_us:.2f} us per launch with gaps; "
           f"others {others}", file=sys.stderr, flush=True)
+    if args.calibrate_copy:
+        copy_calibration(args.calibrate_copy << 20)
     cpu = None
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
@@ -262,7 +267,10 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
                        "ceiling_tok_s": round(roofline.ceiling_tok_s(shape, mean_ctx, B), 2)},
         "roofline": {"kernel": "batched gate_up few-row GEMM (SwiGLU epilogue)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(achieved / 8000.0, 4), "traffic": None, "bytes_per_launch": gu_bytes,
+                     "frac": round(achieved / 8000.0, 4),
+                     "traffic": measured_traffic("batch8 gate_up", BATCH8_TRAFFIC_PROFILE)
+                     if (args.model, B) == ("8b", 8) else None,
+                     "traffic_source": os.path.relpath(BATCH8_TRAFFIC_PROFILE, ROOT), "bytes_per_launch": gu_bytes,
                      "avg_us": round(avg_us, 3), "wall_us_per_launch": round(wall_us, 3),
                      "launches_timed": launches, "timing": "hipExtLaunchKernel start/stop events per launch",
                      "other_kernels": others},
