@@ -56,14 +56,16 @@ __device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& 
                                             Dst&& out, uint32_t hidden, float eps) {
     __shared__ double sh[16];
     const uint32_t t = threadIdx.x, step = blockDim.x;
-    float r[NORM_HELD];
+    float r[NORM_HELD], wv[NORM_HELD];
     double ss = 0.0;
-    // Loads of a clamped index, selected after: no branch between them, so all are in flight at
-    // once.
+    // Loads of a clamped index, selected after: no branch between them, so all (the row's values
+    // and the norm weights) are in flight at once.
 #pragma unroll
     for (uint32_t c = 0; c < NORM_HELD; ++c) {
         const uint32_t i = t + c * step;
-        const float v = src(i < hidden ? i : 0u);
+        const uint32_t j = i < hidden ? i : 0u;
+        const float v = src(j);
+        wv[c] = bf2f(w[j]);
         r[c] = i < hidden ? v : 0.0f;
     }
 #pragma unroll
@@ -84,7 +86,7 @@ __device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& 
 #pragma unroll
     for (uint32_t c = 0; c < NORM_HELD; ++c) {
         const uint32_t i = t + c * step;
-        if (i < hidden) out(i) = f2bf((float)((double)r[c] * scale * (double)bf2f(w[i])));
+        if (i < hidden) out(i) = f2bf((float)((double)r[c] * scale * (double)wv[c]));
     }
     for (uint32_t i = t + NORM_HELD * step; i < hidden; i += step)
         out(i) = f2bf((float)((double)residual[i] * scale * (double)bf2f(w[i])));
