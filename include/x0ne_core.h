@@ -215,6 +215,12 @@ typedef struct {
 x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_files, const char* const* names,
                                   const uint8_t* const* data, const uint64_t* lens, const char* index_json,
                                   const x0ne_engine_options* opts, x0ne_engine** out);
+/* Engine::load (engine.rs:292-297) with Safetensors::open_dir (st.rs:158-181): model_dir's
+   config.json (X0NE_ERR_IO when it cannot be read), then model.safetensors or the shards named
+   by model.safetensors.index.json, mapped read-only, each at most 64 GiB (st.rs:11, :55-67); both
+   present or neither is X0NE_ERR_FORMAT, a shard that cannot be opened X0NE_ERR_IO. The files then
+   pass x0ne_engine_load_from's checks. */
+x0ne_status x0ne_engine_load(const char* model_dir, const x0ne_engine_options* opts, x0ne_engine** out);
 /* This build's synthetic load: the checkpoint of `config_json` drawn on the device, every
    projection and the embedding N(0, std) bf16 from `seed` (tensor i of the checkpoint order,
    oracle/src/model.rs:63-89, takes stream key splitmix64 output i of `seed`), norm weights 1.0. */

@@ -292,3 +292,106 @@ def test_an_index_and_its_shards_must_agree():
     # Without an index: exactly one file.
     with pytest.raises(FormatError):
         Engine.load_from(json.dumps(dense()), files, EngineOptions(max_ctx=64))
+
+
+def load_dir(path, max_ctx=64):
+    from x0ne_core import Engine, EngineOptions
+    return Engine.load(str(path), EngineOptions(max_ctx=max_ctx))
+
+
+def dir_passed_the_checks(path, max_ctx=64):
+    from x0ne_core import GpuError
+    try:
+        e = load_dir(path, max_ctx)
+    except GpuError:
+        return
+    e.close()
+
+
+def test_a_model_directory_is_refused_on_what_it_lacks(checkpoint, tmp_path):
+    """cpu_config.rs:569-612: Engine::load on a directory, the refusals of the in-memory load read
+    from disk; no config.json is an I/O error."""
+    from x0ne_core import FormatError, IoError
+    with pytest.raises(IoError):
+        load_dir(tmp_path)
+    with pytest.raises(IoError):
+        load_dir(tmp_path / "absent")
+    (tmp_path / "config.json").write_text("{")
+    with pytest.raises(FormatError):
+        load_dir(tmp_path)
+    (tmp_path / "config.json").write_text(json.dumps(dense()))
+    with pytest.raises(FormatError):  # no weights
+        load_dir(tmp_path)
+    (tmp_path / "model.safetensors").write_bytes(checkpoint[: len(checkpoint) // 2])
+    with pytest.raises(FormatError):
+        load_dir(tmp_path)
+    (tmp_path / "model.safetensors").write_bytes(checkpoint)
+    with pytest.raises(FormatError):
+        load_dir(tmp_path, max_ctx=0)
+    dir_passed_the_checks(tmp_path)
+
+
+def test_a_model_directory_is_one_file_or_an_index(checkpoint, tmp_path):
+    """cpu_safetensors.rs:691-758 (Safetensors::open_dir): one file or an index, never both, never
+    neither; every truncation on disk refused, the empty file included; an index's shard read
+    like the single file. The 64 GiB per-file cap itself is not exercised here."""
+    from x0ne_core import Error, FormatError
+    (tmp_path / "config.json").write_text(json.dumps(dense()))
+    single = tmp_path / "model.safetensors"
+    single.write_bytes(checkpoint)
+    dir_passed_the_checks(tmp_path)
+    (tmp_path / "model.safetensors.index.json").write_text('{"weight_map":{}}')
+    with pytest.raises(FormatError):  # both present
+        load_dir(tmp_path)
+    (tmp_path / "model.safetensors.index.json").unlink()
+    for cut in [0, 1, 7, 8, 9, len(checkpoint) // 2, len(checkpoint) - 1]:
+        single.write_bytes(checkpoint[:cut])
+        with pytest.raises(FormatError):
+            load_dir(tmp_path)
+    single.unlink()
+    (tmp_path / "s.safetensors").write_bytes(checkpoint)
+    header_len = int.from_bytes(checkpoint[:8], "little")
+    names = [k for k in json.loads(checkpoint[8:8 + header_len]) if k != "__metadata__"]
+    (tmp_path / "model.safetensors.index.json").write_text(
+        json.dumps({"weight_map": {n: "s.safetensors" for n in names}}))
+    dir_passed_the_checks(tmp_path)
+    (tmp_path / "s.safetensors").write_bytes(b"")
+    with pytest.raises(Error):
+        load_dir(tmp_path)
+
+
+def test_a_shard_name_is_a_plain_file_name(checkpoint, tmp_path):
+    """cpu_safetensors.rs:616-689 (st.rs:83-87): an index naming a path, a parent, a hidden file or
+    a directory part is a format error, on disk and in memory; plain names that are not a
+    readable shard are an error of the file system or of the format, never a crash."""
+    from x0ne_core import Engine, EngineOptions, Error, FormatError
+    model = tmp_path / "model"
+    outside = tmp_path / "outside"
+    model.mkdir()
+    outside.mkdir()
+    (model / "config.json").write_text(json.dumps(dense()))
+    (model / "inside.safetensors").write_bytes(checkpoint)
+    (outside / "secret.safetensors").write_bytes(checkpoint)
+    (model / "sub").mkdir()
+    (model / "sub" / "deep.safetensors").write_bytes(checkpoint)
+    header_len = int.from_bytes(checkpoint[:8], "little")
+    names = [k for k in json.loads(checkpoint[8:8 + header_len]) if k != "__metadata__"]
+
+    def write_index(shard):
+        text = json.dumps({"weight_map": {n: shard for n in names}})
+        (model / "model.safetensors.index.json").write_text(text)
+        return text
+
+    write_index("inside.safetensors")
+    dir_passed_the_checks(model)
+    for name in [str(outside / "secret.safetensors"), "../outside/secret.safetensors", "sub/deep.safetensors",
+                 "sub\\deep.safetensors", "./inside.safetensors", ".hidden.safetensors", "..", ".", "/etc/hostname"]:
+        text = write_index(name)
+        with pytest.raises(FormatError):
+            load_dir(model)
+        with pytest.raises(FormatError):
+            Engine.load_from(json.dumps(dense()), {name: checkpoint}, EngineOptions(max_ctx=64), text)
+    for name in ["", "absent.safetensors", "sub", "inside.safetensors\0x"]:
+        write_index(name)
+        with pytest.raises(Error):
+            load_dir(model)

@@ -371,3 +371,40 @@ def test_qwen3_8b_greedy_is_the_oracle_fixture():
             tol = 2 * LOGITS_ATOL_OF_MAX * 6.0  # row scale of this model's logits is about 6
             assert agree == n or margins[agree] < tol, f"f32 sums: token {agree}, margin {margins[agree]:.3e}"
         del e
+
+
+def test_a_model_directory_loads_as_its_files_in_memory(tmp_path):
+    """Engine::load (engine.rs:292-297) from a directory, single file and sharded over an index,
+    gives the in-memory load's tokens and logits bit for bit."""
+    from x0ne_core import Engine, EngineOptions, Route
+    f = Fixture(wide(), 9)
+    ids = f.tokens(21, 12)
+    opts = EngineOptions(max_ctx=64, page_seed=3)
+    e = f.engine(64, page_seed=3)
+    want_tokens = e.greedy(ids, 8)
+    want_logits = e.logits_at(ids, [11], Route.PREFILL)[0]
+    e.close()
+    single = tmp_path / "single"
+    single.mkdir()
+    (single / "config.json").write_text(json.dumps(f.cfg.to_json()))
+    (single / "model.safetensors").write_bytes(f.file)
+    names = list(f.tensors)
+    half = len(names) // 2
+    shards = tmp_path / "shards"
+    shards.mkdir()
+    (shards / "config.json").write_text(json.dumps(f.cfg.to_json()))
+    (shards / "model-00001-of-00002.safetensors").write_bytes(
+        safetensors_bytes({k: f.tensors[k] for k in names[:half]}))
+    (shards / "model-00002-of-00002.safetensors").write_bytes(
+        safetensors_bytes({k: f.tensors[k] for k in names[half:]}))
+    wm = {k: ("model-00001-of-00002.safetensors" if i < half else "model-00002-of-00002.safetensors")
+          for i, k in enumerate(names)}
+    (shards / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": wm}))
+    for d in (single, shards):
+        e = Engine.load(str(d), opts)
+        assert e.config["hidden_size"] == f.cfg.hidden
+        got_tokens = e.greedy(ids, 8)
+        got_logits = e.logits_at(ids, [11], Route.PREFILL)[0]
+        e.close()
+        assert list(got_tokens) == list(want_tokens), d.name
+        assert (got_logits.view(np.uint32) == want_logits.view(np.uint32)).all(), d.name

@@ -6,16 +6,23 @@
 // tokens[0] and pos + 1, so it is captured once into a HIP graph and replayed per token; the
 // host receives 4 bytes per token (engine.rs:1-14, :484-501, :718-839).
 //
-// Per layer the step is 6 launches (the reference's is 10 plus cuBLAS nodes): the QKV GEMV with
-// the residual add + RMSNorm fused in front (layer 0: the embedding too), QK-norm + RoPE + the
-// paged KV write, split-K attention whose last block merges, the O GEMV, the gate/up GEMV with
-// the add + RMSNorm in front and SwiGLU behind, the down GEMV. Then the LM-head GEMV with the
-// final norm in front and the greedy argmax + position advance behind. The residual stream is
-// two f32 buffers used in turn (norm j reads buffer j % 2 and writes j + 1 % 2), so no block of
-// a GEMV reads a residual another block has already advanced.
+// Per layer the step is 5 launches (the reference's is 10 plus cuBLAS nodes): the QKV GEMV with
+// the residual add + RMSNorm fused in front (layer 0: the embedding too); one attention launch
+// doing QK-norm + RoPE, the paged KV write and split-K attention whose last block merges; the O
+// GEMV; the gate/up GEMV with the add + RMSNorm in front and SwiGLU behind; the down GEMV. Then
+// the LM-head GEMV with the final norm in front and the greedy argmax + position advance behind.
+// The residual stream is two f32 buffers used in turn (norm j reads buffer j % 2 and writes
+// j + 1 % 2), so no block of a GEMV reads a residual another block has already advanced.
 //
-// A prompt is fed through the same step, one position at a time (a feed kernel puts ids[i] and
-// i where the step reads them); a prefill of many rows through MFMA GEMMs is not built yet.
+// A prompt is prefilled in passes of up to `chunk` rows through the MFMA GEMMs and the causal
+// matrix-core attention (prefill_pass); with chunk 1 (the exact mode) it is fed through the
+// decode step one position at a time (a feed kernel puts ids[i] and i where the step reads them).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cerrno>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -1019,6 +1026,13 @@ x0ne_status build_end(x0ne_engine* e) {
 // Load
 // ---------------------------------------------------------------------------------------------
 
+namespace {
+// A shard name an index may give (st.rs:83-87): no directory part and not hidden.
+bool plain_shard_name(const std::string& f) {
+    return f.find('/') == std::string::npos && f.find('\\') == std::string::npos && (f.empty() || f[0] != '.');
+}
+}  // namespace
+
 extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_files, const char* const* names,
                                              const uint8_t* const* data, const uint64_t* lens, const char* index_json,
                                              const x0ne_engine_options* opts, x0ne_engine** out) {
@@ -1062,6 +1076,8 @@ extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_f
         std::map<std::string, int> named;
         for (const auto& f : wm->fields) {
             if (f.second.kind != Json::String) return fail(X0NE_ERR_FORMAT, "index: " + f.first + ": file is not a string");
+            if (!plain_shard_name(f.second.text))
+                return fail(X0NE_ERR_FORMAT, "index: shard name \"" + f.second.text + "\" is not a plain file name");
             named[f.second.text] = 1;
             auto it = file_of.find(f.first);
             if (it == file_of.end() || it->second != f.second.text)
@@ -1108,6 +1124,133 @@ extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_f
     }
     *out = e;
     return X0NE_OK;
+}
+
+namespace {
+
+// Per-file size cap of a directory load (st.rs:11, DEFAULT_FILE_CAP).
+constexpr uint64_t FILE_CAP = 64ull << 30;
+
+// A read-only mapping of one checkpoint file (st.rs:55-67), released when it goes out of scope.
+struct MappedFile {
+    void* p = nullptr;
+    size_t n = 0;
+    MappedFile() = default;
+    MappedFile(const MappedFile&) = delete;
+    MappedFile& operator=(const MappedFile&) = delete;
+    ~MappedFile() {
+        if (p) munmap(p, n);
+    }
+};
+
+x0ne_status io_fail(const std::string& path) {
+    return fail(X0NE_ERR_IO, path + ": " + std::strerror(errno));
+}
+
+x0ne_status map_capped(const std::string& path, uint64_t cap, MappedFile* m) {
+    if (path.find('\0') != std::string::npos) return fail(X0NE_ERR_IO, "a path with a NUL byte");
+    const int fd = open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return io_fail(path);
+    struct stat sb;
+    if (fstat(fd, &sb) != 0) {
+        const x0ne_status s = io_fail(path);
+        close(fd);
+        return s;
+    }
+    if (!S_ISREG(sb.st_mode)) {
+        close(fd);
+        return fail(X0NE_ERR_IO, path + ": not a regular file");
+    }
+    const uint64_t len = (uint64_t)sb.st_size;
+    if (len > cap) {
+        close(fd);
+        return fail(X0NE_ERR_FORMAT, path + ": " + std::to_string(len) + " bytes exceeds the " + std::to_string(cap) +
+                                         "-byte cap");
+    }
+    if (len != 0) {  // an empty file stays unmapped: the header check refuses it
+        void* p = mmap(nullptr, (size_t)len, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (p == MAP_FAILED) {
+            const x0ne_status s = io_fail(path);
+            close(fd);
+            return s;
+        }
+        m->p = p;
+        m->n = (size_t)len;
+    }
+    close(fd);
+    return X0NE_OK;
+}
+
+x0ne_status read_text(const std::string& path, std::string* out) {
+    MappedFile m;
+    X0NE_TRY(map_capped(path, FILE_CAP, &m));
+    out->assign(static_cast<const char*>(m.p ? m.p : ""), m.n);
+    return X0NE_OK;
+}
+
+bool file_exists(const std::string& path) {
+    struct stat sb;
+    return stat(path.c_str(), &sb) == 0;
+}
+
+}  // namespace
+
+// Engine::load (engine.rs:292-297) with Safetensors::open_dir (st.rs:158-181): config.json is
+// read and checked first; then model.safetensors, or the shards model.safetensors.index.json
+// names (in first-seen order), each mapped read-only under the per-file cap; both present, or
+// neither, is a format error. The mapped files go through x0ne_engine_load_from's checks.
+extern "C" x0ne_status x0ne_engine_load(const char* model_dir, const x0ne_engine_options* opts, x0ne_engine** out) {
+    if (!out || !opts || !model_dir) return fail(X0NE_ERR_FORMAT, "null argument");
+    *out = nullptr;
+    const std::string dir = model_dir;
+    auto at = [&](const std::string& f) { return dir + "/" + f; };
+    std::string config;
+    X0NE_TRY(read_text(at("config.json"), &config));
+    {
+        Cfg c;
+        X0NE_TRY(parse_config(config.c_str(), &c));
+        X0NE_TRY(check_config(c, opts->max_ctx));
+    }
+    const std::string single = at("model.safetensors"), index = at("model.safetensors.index.json");
+    const bool has_single = file_exists(single), has_index = file_exists(index);
+    if (has_single && has_index) return fail(X0NE_ERR_FORMAT, dir + ": both model.safetensors and its index");
+    if (!has_single && !has_index) return fail(X0NE_ERR_FORMAT, dir + ": no safetensors file");
+    std::vector<std::string> files;
+    std::string index_text;
+    if (has_single) {
+        files.push_back("model.safetensors");
+    } else {
+        X0NE_TRY(read_text(index, &index_text));
+        Json idx;
+        try {
+            idx = parse_json(index_text);
+        } catch (const std::exception& ex) {
+            return fail(X0NE_ERR_FORMAT, std::string("index: ") + ex.what());
+        }
+        const Json* wm = idx.kind == Json::Object ? idx.get("weight_map") : nullptr;
+        if (!wm || wm->kind != Json::Object) return fail(X0NE_ERR_FORMAT, "index: no weight_map");
+        for (const auto& f : wm->fields) {
+            if (f.second.kind != Json::String)
+                return fail(X0NE_ERR_FORMAT, "index: " + f.first + ": file is not a string");
+            if (!plain_shard_name(f.second.text))
+                return fail(X0NE_ERR_FORMAT, "index: shard name \"" + f.second.text + "\" is not a plain file name");
+            bool seen = false;
+            for (const auto& g : files) seen = seen || g == f.second.text;
+            if (!seen) files.push_back(f.second.text);
+        }
+    }
+    std::vector<MappedFile> maps(files.size());
+    std::vector<const char*> names;
+    std::vector<const uint8_t*> data;
+    std::vector<uint64_t> lens;
+    for (size_t i = 0; i < files.size(); ++i) {
+        X0NE_TRY(map_capped(at(files[i]), FILE_CAP, &maps[i]));
+        names.push_back(files[i].c_str());
+        data.push_back(static_cast<const uint8_t*>(maps[i].p));
+        lens.push_back(maps[i].n);
+    }
+    return x0ne_engine_load_from(config.c_str(), files.size(), names.data(), data.data(), lens.data(),
+                                 has_index ? index_text.c_str() : nullptr, opts, out);
 }
 
 extern "C" x0ne_status x0ne_engine_load_synthetic(const char* config_json, uint64_t seed, double std_dev,

@@ -121,6 +121,7 @@ SIGNATURES = {
     "x0ne_engine_load_from": ([C.c_char_p, SZ, C.POINTER(C.c_char_p), C.POINTER(P), C.POINTER(U64),
                                C.c_char_p, C.POINTER(EngineOptionsC), C.POINTER(P)], ST),
     "x0ne_engine_load_synthetic": ([C.c_char_p, U64, F64, C.POINTER(EngineOptionsC), C.POINTER(P)], ST),
+    "x0ne_engine_load": ([C.c_char_p, C.POINTER(EngineOptionsC), C.POINTER(P)], ST),
     "x0ne_engine_free": ([P], None),
     "x0ne_engine_session": ([P, C.POINTER(U32), SZ, C.POINTER(P)], ST),
     "x0ne_session_logits": ([P, C.POINTER(C.POINTER(F32)), C.POINTER(SZ)], ST),

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import json
+import os
 from dataclasses import dataclass
 from enum import IntEnum
 
@@ -75,6 +76,18 @@ class Engine:
         check(lib().x0ne_engine_load_from(config_json.encode(), n, c_names, c_data, c_lens, idx, C.byref(o),
                                           C.byref(h)), "Engine::load_from")
         return Engine(h, json.loads(config_json))
+
+    @staticmethod
+    def load(model_dir, opts: EngineOptions) -> "Engine":
+        """Engine::load (engine.rs:292-297): model_dir's config.json, then model.safetensors or the
+        shards its model.safetensors.index.json names (Safetensors::open_dir, st.rs:158-181)."""
+        h = C.c_void_p()
+        o = opts.c()
+        check(lib().x0ne_engine_load(os.fsencode(model_dir), C.byref(o), C.byref(h)), "Engine::load")
+        e = Engine(h, {})  # freed on any error below
+        with open(os.path.join(model_dir, "config.json"), encoding="utf-8") as f:
+            e.config = json.loads(f.read())
+        return e
 
     @staticmethod
     def load_synthetic(config_json, seed: int, std: float, opts: EngineOptions) -> "Engine":
