@@ -408,3 +408,35 @@ def test_a_model_directory_loads_as_its_files_in_memory(tmp_path):
         e.close()
         assert list(got_tokens) == list(want_tokens), d.name
         assert (got_logits.view(np.uint32) == want_logits.view(np.uint32)).all(), d.name
+
+
+def test_a_batched_engine_holds_its_weights_in_panels_too():
+    """An engine for batches (max_batch > 1) keeps a second copy of every projection and of the
+    LM head in 16-row panels, filled at load from the row-major copy: each is the host's panel
+    layout of the row-major bits (gemm.hip, FEW_W_PANEL); an engine of one sequence has none."""
+    from x0ne_core import Engine, EngineOptions
+    from x0ne_core.ops import to_panels
+    cfg = synthetic_config(vocab=1024, tied=True)
+    e = Engine.load_synthetic(cfg.to_json(), 5, 0.02, EngineOptions(max_ctx=64, max_batch=2))
+    assert "in 16-row panels" in e.describe(), e.describe()
+    a = e.arena()
+    slices = {}
+    for label, _, sl in a.slices():
+        slices.setdefault(label, []).append(sl)
+
+    def read(label, k):
+        sl = slices[label][k]
+        return a.read_array(sl, 0, sl.len // 2, np.uint16)
+
+    h, qkv_rows = cfg.hidden, (cfg.q_heads + 2 * cfg.kv_heads) * cfg.head_dim
+    shapes = {"qkv": (qkv_rows, h), "o": (h, cfg.q_heads * cfg.head_dim), "gate_up": (2 * cfg.inter, h),
+              "down": (h, cfg.inter)}
+    for l in range(cfg.layers):
+        for name, (rows, cols) in shapes.items():
+            want = to_panels(read(name, l).reshape(rows, cols))
+            assert (read(name + "_panel", l) == want).all(), f"layer {l} {name}"
+    assert (read("lm_head_panel", 0) == to_panels(read("embed", 0).reshape(cfg.vocab, h))).all(), "tied head"
+    e.close()
+    one = Engine.load_synthetic(cfg.to_json(), 5, 0.02, EngineOptions(max_ctx=64))
+    assert not any(label.endswith("_panel") for label, _, _ in one.arena().slices())
+

@@ -283,6 +283,51 @@ def test_few_row_gemm_is_the_oracle_and_its_swiglu_the_swiglu_kernel(kernels, se
         assert (ap == act).all(), f"{what}: SwiGLU with X and Y in panels"
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_few_row_gemm_reads_w_in_panels_bit_for_bit(kernels, seed):
+    """W in 16-row panels (FEW_W_PANEL, the batched engine's copy) moves the same values into the
+    same products in the same order: Y is bit-equal to the row-major W's, for the f32, bf16 and
+    SwiGLU outputs, with X and Y in panels or not, at K tails and every block size."""
+    rng = O.Rng(900 + seed)
+    n = rng.pick([1, 2, 7, 16, 17, 32, 33, 64])
+    rows = rng.pick([16, 32, 48, 256, 1024])
+    cols = rng.pick([8, 40, 200, 1024, 4096])
+    block = rng.pick([256, 512])
+    tt = 1 if n <= 16 else 2 if n <= 32 else 4
+    rg = rng.pick([g for (t, g) in kernels.FEW_KERNELS if t == tt])
+    rg_glu = rng.pick([g for (t, g) in kernels.FEW_SWIGLU if t == tt])
+    xp = rng.pick([False, True])
+    w = bf16_bits(bf16s_with_edges(rng, 2 * rows * cols, 1.0))
+    x = bf16_bits(bf16s_with_edges(rng, n * cols, 1.0))
+    what = f"W panel seed {seed} {n}x{rows}x{cols} block {block} row groups {rg}/{rg_glu} X panel {xp}"
+    for mode in (0, 1):
+        want = kernels.gemm_few(w[:rows * cols], rows, cols, x, n, mode, block, rg, x_panel=xp)
+        got = kernels.gemm_few(w[:rows * cols], rows, cols, x, n, mode, block, rg, x_panel=xp, w_panel=True)
+        assert (np.asarray(got).view(np.uint16) == np.asarray(want).view(np.uint16)).all(), f"{what} mode {mode}"
+    want = kernels.gemm_few(w, rows, cols, x, n, 2, block, rg_glu, x_panel=xp, y_panel=xp)
+    got = kernels.gemm_few(w, rows, cols, x, n, 2, block, rg_glu, x_panel=xp, y_panel=xp, w_panel=True)
+    assert (got == want).all(), f"{what}: SwiGLU"
+    from x0ne_core import FormatError
+    with pytest.raises(FormatError):
+        kernels.gemm_few(w[:(rows + 8) * 8], rows + 8, 8, x[:n * 8], n, 0, w_panel=True)
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 8), (48, 40), (32, 1000), (1024, 4096), (17, 8), (16, 12)])
+def test_panel_copy_is_the_panel_layout(kernels, rows, cols):
+    """x0ne_panel_bf16 (the load-time copy of a batched engine's weights) writes the host's panel
+    layout of the matrix; a shape it does not take (rows not a multiple of 16, cols not of 8)
+    leaves the destination untouched."""
+    m = O.Rng(rows * 7 + cols).bf16s(rows * cols, 1.0)
+    got = kernels.panel(bf16_bits(m), rows, cols)
+    if rows % 16 or cols % 8:
+        assert (got == 0xFFFF).all()
+        return
+    from x0ne_core.ops import from_panels, to_panels
+    want = to_panels(bf16_bits(m).reshape(rows, cols))
+    assert (got == want).all()
+    assert (from_panels(got, rows, cols).reshape(-1) == bf16_bits(m)).all()
+
+
 def test_gemv_carries_non_finite_values_to_the_rows_that_read_them(kernels):
     rows, cols = 16, 64
     rng = O.Rng(399)

@@ -288,6 +288,7 @@ uint64_t tensor_key(uint64_t seed, uint64_t index) {
 
 struct LayerW {
     x0ne_slice input_norm, qkv, q_norm, k_norm, o, post_norm, gate_up, down;
+    x0ne_slice qkv_p{}, o_p{}, gate_up_p{}, down_p{};  // the batched step's copies in 16-row panels
 };
 
 struct x0ne_engine {
@@ -300,7 +301,9 @@ struct x0ne_engine {
     x0ne_arena* arena = nullptr;
     // weights
     x0ne_slice embed{}, final_norm{}, lm_head{};
+    x0ne_slice head_p{};  // the LM head (or tied embedding) in 16-row panels
     bool has_lm_head = false;
+    bool wpanel = false;  // the batched step reads the panel copies
     std::vector<LayerW> L;
     // buffers
     x0ne_slice inv_freq{}, rope_cs{}, page_table{}, kv{}, prompt{}, tokens{}, pos{}, residual{}, delta{}, qkv{}, q{}, attn{},
@@ -390,6 +393,21 @@ x0ne_status plan(x0ne_engine* e) {
     X0NE_TRY(al("final_norm", c.hidden * 2, W, &e->final_norm));
     e->has_lm_head = !c.tied;
     if (e->has_lm_head) X0NE_TRY(al("lm_head", c.vocab * c.hidden * 2, W, &e->lm_head));
+    // A batched engine's second copy of the projections and the LM head in 16-row panels
+    // (gemm.hip, FEW_W_PANEL), filled from the row-major copy at load: the few-row GEMM then reads
+    // one contiguous KiB of W per step instead of 64 bytes of 16 rows.
+    e->wpanel = e->max_batch > 1 && c.qkv_rows() % 16 == 0 && c.hidden % 16 == 0 && c.inter % 16 == 0 &&
+                c.vocab % 16 == 0;
+    if (e->wpanel) {
+        for (uint64_t l = 0; l < c.layers; ++l) {
+            LayerW& w = e->L[l];
+            X0NE_TRY(al("qkv_panel", c.qkv_rows() * c.hidden * 2, W, &w.qkv_p));
+            X0NE_TRY(al("o_panel", c.hidden * c.q_dim() * 2, W, &w.o_p));
+            X0NE_TRY(al("gate_up_panel", 2 * c.inter * c.hidden * 2, W, &w.gate_up_p));
+            X0NE_TRY(al("down_panel", c.hidden * c.inter * 2, W, &w.down_p));
+        }
+        X0NE_TRY(al("lm_head_panel", c.vocab * c.hidden * 2, W, &e->head_p));
+    }
     // Engine tables, not client data: the host's f32 inverse frequencies and the page order.
     X0NE_TRY(al("inv_freq", c.head_dim / 2 * 4, W, &e->inv_freq));
     X0NE_TRY(al("rope_cs", e->max_ctx * (c.head_dim / 2) * 16, W, &e->rope_cs));
@@ -1002,9 +1020,40 @@ x0ne_status fill_rope_table(x0ne_engine* e) {
     return X0NE_OK;
 }
 
+// The panel copies of a batched engine's weights (x0ne_panel_bf16), from the row-major ones.
+x0ne_status fill_panels(x0ne_engine* e) {
+    if (!e->wpanel) return X0NE_OK;
+    const Cfg& c = e->c;
+    auto panel = [&](x0ne_slice src, x0ne_slice dst, uint64_t rows, uint64_t cols) -> x0ne_status {
+        if (rows % 16 != 0 || cols % 8 != 0 || src.len != rows * cols * 2 || dst.len != src.len ||
+            rows * cols / 8 > (uint64_t)UINT32_MAX * 256)
+            return fail(X0NE_ERR_FORMAT, "panel copy of a " + std::to_string(rows) + "x" + std::to_string(cols) +
+                                             " matrix");
+        const void* sp = e->d(src);
+        void* dp = e->d(dst);
+        uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols;
+        void* args[] = {(void*)&sp, (void*)&dp, (void*)&r32, (void*)&c32};
+        const uint32_t blocks = (uint32_t)((rows * cols / 8 + 255) / 256);
+        X0NE_HIP(x0ne_launch((const void*)&x0ne_panel_bf16, dim3(blocks), dim3(256), args, 0, e->gpu->stream),
+                 "panel copy");
+        return X0NE_OK;
+    };
+    for (uint64_t l = 0; l < c.layers; ++l) {
+        const LayerW& w = e->L[l];
+        X0NE_TRY(panel(w.qkv, w.qkv_p, c.qkv_rows(), c.hidden));
+        X0NE_TRY(panel(w.o, w.o_p, c.hidden, c.q_dim()));
+        X0NE_TRY(panel(w.gate_up, w.gate_up_p, 2 * c.inter, c.hidden));
+        X0NE_TRY(panel(w.down, w.down_p, c.hidden, c.inter));
+    }
+    X0NE_TRY(panel(e->has_lm_head ? e->lm_head : e->embed, e->head_p, c.vocab, c.hidden));
+    X0NE_HIP(hipStreamSynchronize(e->gpu->stream), "panel copies");
+    return X0NE_OK;
+}
+
 x0ne_status build_end(x0ne_engine* e) {
     X0NE_TRY(x0ne_arena_scrub(e->arena, nullptr));
     X0NE_TRY(fill_rope_table(e));
+    X0NE_TRY(fill_panels(e));
     X0NE_HIP(hipHostMalloc((void**)&e->ring, RING * 4, hipHostMallocDefault), "pinned ring");
     X0NE_HIP(hipHostMalloc((void**)&e->host_logits, e->c.vocab * 4, hipHostMallocDefault), "pinned logits");
     X0NE_HIP(hipHostMalloc((void**)&e->host_token, 4, hipHostMallocDefault), "pinned token");
@@ -1564,9 +1613,13 @@ x0ne_status batch_embed_norm(x0ne_engine* e, uint32_t B) {
     return launch_rows(e, (const void*)&x0ne_embed_rmsnorm_panel_bf16, dim3(B), dim3(256), args, "batch embedding");
 }
 
+uint32_t wpanel_bit(const x0ne_engine* e) { return e->wpanel ? PANEL_W : 0u; }
+
 x0ne_status batch_qkv(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].qkv), c.qkv_rows(), c.hidden, e->d(e->b_x), B, e->d(e->b_qkv), 0, PANEL_X);
+    const LayerW& w = e->L[l];
+    return skinny(e->gpu, e->d(e->wpanel ? w.qkv_p : w.qkv), c.qkv_rows(), c.hidden, e->d(e->b_x), B, e->d(e->b_qkv),
+                  0, PANEL_X | wpanel_bit(e));
 }
 
 x0ne_status batch_attention(x0ne_engine* e, uint32_t B, uint64_t l) {
@@ -1603,25 +1656,31 @@ x0ne_status batch_attention(x0ne_engine* e, uint32_t B, uint64_t l) {
 
 x0ne_status batch_o(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].o), c.hidden, c.q_dim(), e->d(e->b_attn), B, e->d(e->b_delta), 0, PANEL_X);
+    const LayerW& w = e->L[l];
+    return skinny(e->gpu, e->d(e->wpanel ? w.o_p : w.o), c.hidden, c.q_dim(), e->d(e->b_attn), B, e->d(e->b_delta), 0,
+                  PANEL_X | wpanel_bit(e));
 }
 
 x0ne_status batch_gate_up(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].gate_up), c.inter, c.hidden, e->d(e->b_x), B, e->d(e->b_act), 2,
-                  PANEL_X | PANEL_Y);
+    const LayerW& w = e->L[l];
+    return skinny(e->gpu, e->d(e->wpanel ? w.gate_up_p : w.gate_up), c.inter, c.hidden, e->d(e->b_x), B,
+                  e->d(e->b_act), 2, PANEL_X | PANEL_Y | wpanel_bit(e));
 }
 
 x0ne_status batch_down(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
-    return skinny(e->gpu, e->d(e->L[l].down), c.hidden, c.inter, e->d(e->b_act), B, e->d(e->b_delta), 0, PANEL_X);
+    const LayerW& w = e->L[l];
+    return skinny(e->gpu, e->d(e->wpanel ? w.down_p : w.down), c.hidden, c.inter, e->d(e->b_act), B, e->d(e->b_delta),
+                  0, PANEL_X | wpanel_bit(e));
 }
 
 // The f32 LM head over the B normed rows, then each row's argmax into its token, position + 1.
 x0ne_status batch_head(x0ne_engine* e, uint32_t B) {
     const Cfg& c = e->c;
-    X0NE_TRY(skinny(e->gpu, e->d(e->has_lm_head ? e->lm_head : e->embed), c.vocab, c.hidden, e->d(e->b_x), B,
-                    e->d(e->b_logits), 1, PANEL_X));
+    const x0ne_slice head = e->wpanel ? e->head_p : e->has_lm_head ? e->lm_head : e->embed;
+    X0NE_TRY(skinny(e->gpu, e->d(head), c.vocab, c.hidden, e->d(e->b_x), B, e->d(e->b_logits), 1,
+                    PANEL_X | wpanel_bit(e)));
     const void* lg = e->d(e->b_logits);
     uint32_t vocab = (uint32_t)c.vocab, slices = ARGMAX_SLICES;
     void* part = e->d(e->b_argmax);
@@ -1947,12 +2006,13 @@ extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, siz
                   "%s, arena %llu bytes, decode graph %zu nodes, decode attention split-K P %u (grid %u x %u, %u q "
                   "heads per block, %u blocks per CU, merge %s), KV pages of %d positions (%llu pages, %s order), "
                   "GEMV grids qkv %u o %u gate_up %u down %u head %u (%s sums), prefill passes of %llu rows, "
-                  "feed-forward dense",
+                  "batch %llu (weights %s), feed-forward dense",
                   gpu, (unsigned long long)e->arena->len, e->graph ? e->graph->nodes : (size_t)0, e->split.splits,
                   e->split.grid_x, e->split.splits, e->split.group, e->split.per_cu,
                   e->split.grouped ? "LastBlock" : "Kernel", X0NE_PAGE_C, (unsigned long long)e->pages,
                   e->page_seed ? "shuffled" : "identity", e->grid_qkv, e->grid_o, e->grid_gu, e->grid_down,
-                  e->grid_head, e->f64_sums ? "f64" : "f32", (unsigned long long)e->chunk);
+                  e->grid_head, e->f64_sums ? "f64" : "f32", (unsigned long long)e->chunk,
+                  (unsigned long long)e->max_batch, e->wpanel ? "row-major and in 16-row panels" : "row-major");
     if (buf && len) {
         std::strncpy(buf, s, len - 1);
         buf[len - 1] = 0;

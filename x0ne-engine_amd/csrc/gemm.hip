@@ -156,22 +156,21 @@ extern "C" __global__ void __launch_bounds__(256)
 //    which returns zeros without touching memory.
 //  - The wavefronts' partial tiles are summed in LDS in wavefront order (deterministic).
 // flags: FEW_F32 Y f32 (else bf16); FEW_X_PANEL X in panels (below); FEW_Y_PANEL Y in panels
-// (bf16). GLU: SwiGLU over the packed [gate; up] W of 2 rows rows: the block also takes the up
+// (bf16); FEW_W_PANEL W in panels (rows a multiple of 16; with SwiGLU the [gate; up] matrix of
+// 2 rows rows in panels, so gate and up panels do not mix). GLU: SwiGLU over the packed [gate; up] W of 2 rows rows: the block also takes the up
 // rows rows + 16 (RG b + g) .., and writes act[t][r] = bf16(g / (1 + e^-g) u) of the
 // bf16-rounded g and u, in f64 (x0ne_swiglu_bf16 of the bf16 projection).
 //
 // Panels: a [n][cols] bf16 matrix stored as ceil(n / 16) panels of [cols / 8][16][8]: element
 // (t, k) at ((t / 16 * cols / 8 + k / 8) 16 + t % 16) 8 + k % 8. One step's X operand is then one
 // contiguous KiB; row-major, its 16 rows lie cols apart and meet in the same L2 channels, which
-// costs the W stream up to a fifth of its rate at 16 rows (measured on MI355X).
+// costs the W stream up to a fifth of its rate at 16 rows (measured on MI355X). W is laid out the
+// same way for the same reason: row-major, each step reads 64 bytes of 16 rows cols apart, and
+// the W stream of the Qwen3 decode shapes runs at 3.1-5.1 TB/s; in panels each step reads one
+// contiguous KiB and a wavefront's steps run through its panel in order, 3.7-5.9 TB/s (MI355X).
 namespace {
 
-constexpr uint32_t FEW_F32 = 1, FEW_X_PANEL = 2, FEW_Y_PANEL = 4;
-
-// Byte offset of columns k .. k + 7 of row r, or past every buffer.
-__device__ __forceinline__ uint32_t sk_off(bool in, uint32_t r, uint32_t cols, uint32_t k) {
-    return in ? (r * cols + k) * 2 : OFF_NONE;
-}
+constexpr uint32_t FEW_F32 = 1, FEW_X_PANEL = 2, FEW_Y_PANEL = 4, FEW_W_PANEL = 8;
 
 template <int TT, int RG, int U, bool GLU, int MAXV>
 __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
@@ -180,9 +179,10 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
     constexpr int KINDS = GLU ? 2 : 1;
     const uint32_t b = blockIdx.x, V = blockDim.x >> 6;
     const bool out_f32 = flags & FEW_F32, x_panel = flags & FEW_X_PANEL, y_panel = flags & FEW_Y_PANEL;
+    const bool w_panel = flags & FEW_W_PANEL;
     // Grid-uniform exits for a launch that does not fit.
-    if (b * 16 * RG >= rows || n == 0 || n > 16 * TT || cols % 8 != 0 || V > MAXV || flags > 7 ||
-        (out_f32 && (GLU || y_panel)) || (y_panel && rows % 8 != 0))
+    if (b * 16 * RG >= rows || n == 0 || n > 16 * TT || cols % 8 != 0 || V > MAXV || flags > 15 ||
+        (out_f32 && (GLU || y_panel)) || (y_panel && rows % 8 != 0) || (w_panel && rows % 16 != 0))
         return;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t r = lane & 15, q4 = lane >> 4;
@@ -213,7 +213,10 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
 #pragma unroll
             for (int g = 0; g < RG; ++g) {
                 const uint32_t row = 16 * (RG * b + g) + r;
-                wb[u][kd][g] = bload(wr, sk_off(in && row < rows, kd * rows + row, cols, k));
+                const uint32_t wrow = kd * rows + row;
+                wb[u][kd][g] = bload(wr, !(in && row < rows) ? OFF_NONE
+                                         : w_panel ? (uint32_t)panel_index(wrow, k, cols) * 2
+                                                   : (wrow * cols + k) * 2);
             }
     };
 #pragma unroll
@@ -294,3 +297,16 @@ X0NE_FEW(x0ne_gemm_few_t2_r1_swiglu_bf16, 2, 1, 4, true, 8)
 X0NE_FEW(x0ne_gemm_few_t4_r1_bf16, 4, 1, 4, false, 8)
 X0NE_FEW(x0ne_gemm_few_t4_r1_swiglu_bf16, 4, 1, 4, true, 8)
 #endif
+
+// x0ne_panel_bf16: a row-major [rows][cols] bf16 matrix copied into 16-row panels (element (r, k)
+// at panel_index(r, k, cols)), one 16-byte chunk per thread in destination order, so the writes
+// are contiguous; grid ceil(rows cols / 8 / 256), block 256. rows a multiple of 16 and cols of 8,
+// else nothing is written. The source and destination must not overlap.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_panel_bf16(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst, uint32_t rows, uint32_t cols) {
+    if (rows % 16 != 0 || cols % 8 != 0) return;  // grid-uniform
+    const uint64_t c8 = cols / 8, j = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // destination chunk
+    if (j >= (uint64_t)rows * c8) return;
+    const uint64_t r = j / (16 * c8) * 16 + j % 16, k8 = j / 16 % c8;
+    reinterpret_cast<uint4*>(dst)[j] = reinterpret_cast<const uint4*>(src)[r * c8 + k8];
+}

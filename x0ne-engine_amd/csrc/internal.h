@@ -79,8 +79,8 @@ x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32
                            const x0ne_arg* args, size_t n, uint32_t gz = 1);
 // Y[n][rows] = X[n][cols] W^T for 1 <= n <= 64 rows of X with the few-row kernels of gemm.hip
 // (mode 0 bf16 Y, 1 f32 Y, 2 SwiGLU over a packed [gate; up] W of 2 rows rows); panels: 2 X in
-// panels, 4 Y in panels (bf16 Y), the layout of device.h.
-constexpr uint32_t PANEL_X = 2, PANEL_Y = 4;
+// panels, 4 Y in panels (bf16 Y), 8 W in panels (rows a multiple of 16), the layout of device.h.
+constexpr uint32_t PANEL_X = 2, PANEL_Y = 4, PANEL_W = 8;
 x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
                    uint32_t mode, uint32_t panels);
 // Split plan for a geometry (gpu.rs:958-985), P capped at `cap`.

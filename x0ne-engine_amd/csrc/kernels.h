@@ -95,6 +95,7 @@ X0NE_DECLARE_FEW(t2_r1_swiglu)
 X0NE_DECLARE_FEW(t4_r1)
 X0NE_DECLARE_FEW(t4_r1_swiglu)
 #undef X0NE_DECLARE_FEW
+__global__ void x0ne_panel_bf16(const bf16_t* src, bf16_t* dst, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_f32(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_any(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols,

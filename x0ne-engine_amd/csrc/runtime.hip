@@ -261,8 +261,8 @@ namespace x0ne {
 x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
                    uint32_t mode, uint32_t panels) {
     const uint64_t wrows = mode == 2 ? 2 * rows : rows;
-    if (n == 0 || n > SKINNY_MAX_ROWS || rows == 0 || cols == 0 || cols % 8 != 0 || mode > 2 || (panels & ~6u) ||
-        ((panels & 4) && (mode == 1 || rows % 8 != 0)) ||
+    if (n == 0 || n > SKINNY_MAX_ROWS || rows == 0 || cols == 0 || cols % 8 != 0 || mode > 2 || (panels & ~14u) ||
+        ((panels & 4) && (mode == 1 || rows % 8 != 0)) || ((panels & 8) && rows % 16 != 0) ||
         wrows * cols * 2 > GEMM_MAX_BYTES || n * cols * 2 > GEMM_MAX_BYTES || (uintptr_t)w % 16 != 0 ||
         (uintptr_t)x % 16 != 0)
         return fail(X0NE_ERR_FORMAT, "few-row gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
@@ -272,8 +272,10 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
     // KiB of a launch fastest alone, so a launch of up to two blocks per CU takes RG so that at
     // most one block lands on each CU (a CU with two finishes last); large launches (the LM
     // head) take RG 2 at up to 8 rows of X and 8 beyond, where each X piece costs as much as a
-    // W piece; SwiGLU launches, two W pieces per X piece already, keep RG 1.
-    const bool glu = mode == 2;
+    // W piece; SwiGLU launches, two W pieces per X piece already, keep RG 1. With W in panels
+    // (PANEL_W) the one-block-per-CU rule extends to RG 4, and a large launch takes RG 2 over 8
+    // wavefronts at every n up to 16.
+    const bool glu = mode == 2, wpan = panels & PANEL_W;
     auto blocks_of = [&](uint32_t rg) { return (uint32_t)((rows + 16 * rg - 1) / (16 * rg)); };
     uint32_t rg = 1, waves = 4;
     const void* fn = nullptr;
@@ -281,6 +283,18 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
         if (glu) {
             fn = (const void*)&x0ne_gemm_few_t1_r1_swiglu_bf16;
             waves = blocks_of(1) >= 4 * g->cus ? 8 : 4;
+        } else if (wpan) {
+            if (blocks_of(1) <= g->cus)
+                rg = 1;
+            else if (blocks_of(2) <= g->cus)
+                rg = 2;
+            else if (blocks_of(4) <= g->cus)
+                rg = 4;
+            else if (blocks_of(1) >= 8 * g->cus)
+                rg = 2, waves = 8;
+            fn = rg == 1   ? (const void*)&x0ne_gemm_few_t1_r1_bf16
+                 : rg == 2 ? (const void*)&x0ne_gemm_few_t1_r2_bf16
+                           : (const void*)&x0ne_gemm_few_t1_r4_bf16;
         } else {
             if (blocks_of(1) <= g->cus)
                 rg = 1;

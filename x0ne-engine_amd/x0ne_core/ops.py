@@ -532,12 +532,12 @@ class Kernels:
     FEW_SWIGLU = {(1, 1), (1, 2), (2, 1), (4, 1)}
 
     def gemm_few(self, w, rows, cols, x, n, mode: int, block: int = 256, rg: int = 1, x_panel: bool = False,
-                 y_panel: bool = False) -> np.ndarray:
+                 y_panel: bool = False, w_panel: bool = False) -> np.ndarray:
         """One few-row GEMM kernel itself (x0ne_gemm_few_t{TT}_r{RG}[_swiglu]_bf16, TT = 1, 2
         or 4 tiles of 16 rows of X by n): mode 0 bf16 Y, 1 f32 Y, 2 SwiGLU over the packed
         [gate; up] W of 2 rows rows (act [n][rows] bf16); `rg` row groups of 16 per block;
-        x_panel / y_panel: X handed over, Y read back, in the panel layout (returned
-        row-major either way)."""
+        x_panel / y_panel / w_panel: X and W handed over, Y read back, in the panel layout
+        (returned row-major either way; a W panel needs rows a multiple of 16)."""
         wrows = 2 * rows if mode == 2 else rows
         tt = 1 if n <= 16 else 2 if n <= 32 else 4
         if w.size != wrows * cols or x.size != n * cols or not 1 <= n <= 64 or cols % 8 or \
@@ -546,6 +546,8 @@ class Kernels:
             raise FormatError("gemm_few: lengths or variant")
         if y_panel and (mode == 1 or rows % 8):
             raise FormatError("gemm_few: a Y panel is bf16 with rows a multiple of 8")
+        if w_panel and rows % 16:
+            raise FormatError("gemm_few: a W panel needs rows a multiple of 16")
         name = f"x0ne_gemm_few_t{tt}_r{rg}{'_swiglu' if mode == 2 else ''}_bf16"
         ob = 4 if mode == 1 else 2
         xin = to_panels(np.asarray(x, np.uint16).reshape(n, cols)) if x_panel else np.asarray(x, np.uint16)
@@ -556,15 +558,34 @@ class Kernels:
         ys = a.alloc("y", yrows * rows * ob, Class.CLIENT_DATA)
         self._freeze(a)
         a.scrub_client_data()
-        a.write(ws, 0, np.asarray(w, np.uint16))
+        win = np.asarray(w, np.uint16)
+        a.write(ws, 0, to_panels(win.reshape(wrows, cols)) if w_panel else win)
         a.write(xs, 0, xin)
-        flags = (1 if mode == 1 else 0) | (2 if x_panel else 0) | (4 if y_panel else 0)
+        flags = (1 if mode == 1 else 0) | (2 if x_panel else 0) | (4 if y_panel else 0) | (8 if w_panel else 0)
         self.gpu.launch(name, (rows + 16 * rg - 1) // (16 * rg), block,
                         [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(cols),
                          Arg.u32(n), Arg.u32(flags)])
         self.gpu.sync()
         y = a.read_array(ys, 0, yrows * rows, np.float32 if mode == 1 else np.uint16)
         return from_panels(y, n, rows) if y_panel else y.reshape(n, rows)
+
+    def panel(self, m, rows: int, cols: int) -> np.ndarray:
+        """x0ne_panel_bf16: the [rows][cols] bf16 matrix m copied into 16-row panels on the device
+        (flat, rows x cols values; left as the destination held it, 0xFFFF here, when rows is not a
+        multiple of 16 or cols of 8)."""
+        m = np.asarray(m, np.uint16).reshape(-1)
+        if m.size != rows * cols or rows == 0 or cols == 0:
+            raise FormatError("panel: lengths")
+        a = self._arena()
+        src = a.alloc("src", m.size * 2, Class.WEIGHTS)
+        dst = a.alloc("dst", m.size * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(src, 0, m)
+        a.write(dst, 0, np.full(m.size, 0xFFFF, np.uint16))
+        self.gpu.launch("x0ne_panel_bf16", (rows * cols // 8 + 255) // 256 or 1, 256,
+                        [Arg.ptr(a.ptr(src)), Arg.ptr(a.ptr(dst)), Arg.u32(rows), Arg.u32(cols)])
+        self.gpu.sync()
+        return a.read_array(dst, 0, m.size, np.uint16)
 
     def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None,
                              grouped=False):
