@@ -102,9 +102,9 @@ x0ne_status x0ne_gpu_launch_3d(x0ne_gpu* g, const char* name, uint32_t gx, uint3
 
 /* Gpu::gemm (gpu.rs:1098-1149), the projection the reference hands cuBLAS: Y[n][rows] =
    X[n][cols] W^T, W [rows][cols] row-major bf16, X bf16, f32 accumulation; out_f32 = 0 gives
-   bf16 Y, 1 f32 Y. Device addresses. From 4 rows of X on (cols a multiple of 8, W and X each
-   below 4 GiB) one hand-written matrix-core GEMM launch (x0ne_gemm_bf16); below that the
-   bandwidth-bound GEMV, one launch per row of X. */
+   bf16 Y, 1 f32 Y. Device addresses. One row of X: the bandwidth-bound GEMV; 2 to 64 rows (cols
+   a multiple of 8, W and X each below 4 GiB): one few-row matrix-core launch that reads each W
+   row once (x0ne_gemm_few_*); more rows: one tiled matrix-core GEMM launch (x0ne_gemm_bf16). */
 x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n, uint64_t y,
                           int out_f32);
 
@@ -292,6 +292,19 @@ uint32_t x0ne_engine_decode_mode(const x0ne_engine* e);
    rows[k * vocab ..] for positions[k]. */
 x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids, size_t n, const size_t* positions,
                                   size_t n_positions, uint32_t route, float* rows);
+
+/* PosStats (engine.rs:60-64) and Engine::run (engine.rs:928-1006): the teacher-forced pass of
+   x0ne_engine_logits_at with, for each of the n positions, stats[p] (the device's argmax of the
+   row, 0xFFFFFFFF when it holds a NaN; the row's logsumexp, metrics.rs:4-7; the log-probability
+   of ids[p + 1], NaN at the last position), and the f32 rows at keep[k] in rows[k * vocab ..]
+   (the bits x0ne_engine_logits_at gives). Engine::stats is this with n_keep 0. */
+typedef struct {
+    uint32_t argmax;
+    float logsumexp;
+    float next_logprob;
+} x0ne_pos_stats;
+x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t route, const size_t* keep,
+                            size_t n_keep, x0ne_pos_stats* stats, float* rows);
 
 /* Engine::describe, graph_nodes, splits, counts, client_data_is_zero, host_buffers_are_zero
    (engine.rs:563-670). */

@@ -440,3 +440,34 @@ def test_a_batched_engine_holds_its_weights_in_panels_too():
     one = Engine.load_synthetic(cfg.to_json(), 5, 0.02, EngineOptions(max_ctx=64))
     assert not any(label.endswith("_panel") for label, _, _ in one.arena().slices())
 
+
+
+@pytest.mark.parametrize("route_name", ["PREFILL", "DECODE"])
+def test_the_statistics_of_a_pass_are_those_of_its_logits_rows(route_name):
+    """Engine::run / stats (engine.rs:928-1006, gpu_engine.rs:159-182): per position the argmax of
+    the row (metrics::argmax), its log-sum-exp within 1e-4 relative and the next id's
+    log-probability within 1e-3 (NaN at the last position); the rows run keeps are the bits
+    logits_at gives; the client bytes are zero after; a kept position outside the ids is refused."""
+    from x0ne_core import FormatError, Route
+    f = Fixture(wide(), 31)
+    e = f.engine(64, page_seed=4)
+    route = getattr(Route, route_name)
+    ids = f.tokens(41, 24)
+    every = list(range(len(ids)))
+    rows = e.logits_at(ids, every, route)
+    stats, kept = e.run(ids, route, keep=[0, 7, 23])
+    for k, p in enumerate([0, 7, 23]):
+        assert (kept[k].view(np.uint32) == rows[p].view(np.uint32)).all(), f"run row {p}"
+    assert np.array_equal(e.stats(ids, route).view(np.uint32), stats.view(np.uint32)), "stats is run without rows"
+    for p, s in enumerate(stats):
+        row = rows[p].astype(np.float64)
+        assert int(s["argmax"]) == O.argmax(rows[p]), f"argmax at {p}"
+        lse = O.logsumexp(rows[p])
+        assert abs(float(s["logsumexp"]) - lse) <= 1e-4 * max(abs(lse), 1.0), f"log-sum-exp at {p}"
+        if p + 1 < len(ids):
+            assert abs(float(s["next_logprob"]) - (row[ids[p + 1]] - lse)) <= 1e-3, f"log-probability at {p}"
+        else:
+            assert np.isnan(s["next_logprob"])
+    assert e.client_data_is_zero()
+    with pytest.raises(FormatError):
+        e.run(ids, route, keep=[len(ids)])

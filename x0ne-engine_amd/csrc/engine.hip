@@ -1983,6 +1983,71 @@ extern "C" x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids
     return st != X0NE_OK ? st : sc;
 }
 
+namespace {
+
+// metrics::logsumexp (metrics.rs:4-7): the f32 maximum (NaN values skipped, as f32::max does),
+// then m + ln of the f64 sum, in order, of e^(v - m).
+double logsumexp_row(const float* x, size_t n) {
+    float m = -INFINITY;
+    for (size_t i = 0; i < n; ++i) m = std::fmax(m, x[i]);
+    double sum = 0.0;
+    for (size_t i = 0; i < n; ++i) sum += std::exp((double)x[i] - (double)m);
+    return (double)m + std::log(sum);
+}
+
+}  // namespace
+
+// Engine::run (engine.rs:928-1006): a teacher-forced pass over ids by `route`; for every
+// position its PosStats (engine.rs:60-64: the device's argmax of the row, the row's logsumexp,
+// the log-probability of the next id, NaN at the last position) and the full f32 rows at
+// `keep`. The rows come from the launches x0ne_engine_logits_at makes for each position (per
+// row the LM head with the final norm, or the decode step), so both give the same bits; the
+// client bytes are scrubbed after, on success and on failure.
+extern "C" x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t route,
+                                       const size_t* keep, size_t n_keep, x0ne_pos_stats* stats, float* rows) {
+    if (!e || !ids || !stats || (!rows && n_keep) || (!keep && n_keep)) return fail(X0NE_ERR_FORMAT, "null argument");
+    if (route != X0NE_ROUTE_PREFILL && route != X0NE_ROUTE_DECODE) return fail(X0NE_ERR_FORMAT, "unknown route");
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    if (e->poisoned) X0NE_TRY(scrub(e));
+    X0NE_TRY(check_ids(e, ids, n));
+    for (size_t k = 0; k < n_keep; ++k)
+        if (keep[k] >= n)
+            return fail(X0NE_ERR_FORMAT, "position " + std::to_string(keep[k]) + " outside " + std::to_string(n) + " tokens");
+    const size_t vocab = e->c.vocab;
+    std::vector<float> row(vocab);
+    auto collect = [&](size_t p) -> x0ne_status {
+        uint32_t am = 0;
+        X0NE_TRY(x0ne_arena_read(e->arena, e->logits, 0, row.data(), vocab * 4));
+        X0NE_TRY(x0ne_arena_read(e->arena, e->tokens, 0, &am, 4));
+        const double lse = logsumexp_row(row.data(), vocab);
+        stats[p].argmax = am;
+        stats[p].logsumexp = (float)lse;
+        stats[p].next_logprob = p + 1 < n ? (float)((double)row[ids[p + 1]] - lse) : NAN;
+        for (size_t k = 0; k < n_keep; ++k)
+            if (keep[k] == p) std::memcpy(rows + k * vocab, row.data(), vocab * 4);
+        return X0NE_OK;
+    };
+    x0ne_status st = put_prompt(e, ids, n);
+    if (route == X0NE_ROUTE_PREFILL && e->chunk > 1) {
+        for (size_t start = 0; start < n && st == X0NE_OK;) {
+            const size_t len = std::min<size_t>(e->chunk, n - start);
+            st = prefill_pass(e, start, len);
+            for (size_t p = start; p < start + len && st == X0NE_OK; ++p) {
+                st = prefill_head(e, p - start, p, false);
+                if (st == X0NE_OK) st = collect(p);
+            }
+            start += len;
+        }
+    } else {
+        for (size_t p = 0; p < n && st == X0NE_OK; ++p) {
+            st = feed(e, (uint32_t)p);
+            if (st == X0NE_OK) st = collect(p);
+        }
+    }
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Introspection
 // ---------------------------------------------------------------------------------------------

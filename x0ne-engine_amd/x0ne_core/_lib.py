@@ -66,6 +66,11 @@ class SplitPlanC(C.Structure):
                 ("grouped", C.c_uint32), ("per_cu", C.c_uint32)]
 
 
+class PosStatsC(C.Structure):
+    """x0ne_pos_stats: PosStats (engine.rs:60-64)."""
+    _fields_ = [("argmax", C.c_uint32), ("logsumexp", C.c_float), ("next_logprob", C.c_float)]
+
+
 class EngineOptionsC(C.Structure):
     _fields_ = [("max_ctx", C.c_uint64), ("page_seed", C.c_uint64), ("f64_sums", C.c_uint32),
                 ("prefill_chunk", C.c_uint32), ("max_batch", C.c_uint32), ("reserved", C.c_uint32)]
@@ -143,6 +148,7 @@ SIGNATURES = {
     "x0ne_engine_set_decode_mode": ([P, U32], ST),
     "x0ne_engine_decode_mode": ([P], U32),
     "x0ne_engine_logits_at": ([P, C.POINTER(U32), SZ, C.POINTER(SZ), SZ, U32, C.POINTER(F32)], ST),
+    "x0ne_engine_run": ([P, C.POINTER(U32), SZ, U32, C.POINTER(SZ), SZ, C.POINTER(PosStatsC), C.POINTER(F32)], ST),
     "x0ne_engine_describe": ([P, C.c_char_p, SZ], ST),
     "x0ne_engine_graph_nodes": ([P], SZ),
     "x0ne_engine_splits": ([P], U32),

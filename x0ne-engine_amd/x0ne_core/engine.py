@@ -14,7 +14,7 @@ from enum import IntEnum
 
 import numpy as np
 
-from ._lib import Counts, EngineOptionsC, FormatError, check, lib
+from ._lib import Counts, EngineOptionsC, FormatError, PosStatsC, check, lib
 
 GREEDY_AHEAD = 2  # engine.rs:78
 GREEDY_AHEAD_MAX = 15  # engine.rs:73
@@ -50,6 +50,10 @@ class EngineOptions:
 def _ids(ids):
     a = np.ascontiguousarray(ids, dtype=np.uint32)
     return a, a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+# PosStats (engine.rs:60-64).
+POS_STATS = np.dtype([("argmax", np.uint32), ("logsumexp", np.float32), ("next_logprob", np.float32)])
 
 
 class Engine:
@@ -189,6 +193,24 @@ class Engine:
         check(lib().x0ne_engine_logits_at(self.h, p, a.size, pos.ctypes.data_as(C.POINTER(C.c_size_t)), pos.size,
                                           int(route), rows.ctypes.data_as(C.POINTER(C.c_float))), "logits_at")
         return [rows[i] for i in range(len(positions))]
+
+    def run(self, ids, route: Route = Route.DECODE, keep=()):
+        """Engine::run (engine.rs:928-1006): per position (argmax, logsumexp, next_logprob) as a
+        structured array, and the f32 logits rows at `keep`."""
+        a, p = _ids(ids)
+        kp = np.ascontiguousarray(keep, np.uintp)
+        stats = (PosStatsC * max(1, a.size))()
+        rows = np.zeros((kp.size, self.vocab_size), np.float32)
+        check(lib().x0ne_engine_run(self.h, p, a.size, int(route), kp.ctypes.data_as(C.POINTER(C.c_size_t)), kp.size,
+                                    stats, rows.ctypes.data_as(C.POINTER(C.c_float))), "run")
+        out = np.zeros(a.size, POS_STATS)
+        for i in range(a.size):
+            out[i] = (stats[i].argmax, stats[i].logsumexp, stats[i].next_logprob)
+        return out, [rows[i] for i in range(kp.size)]
+
+    def stats(self, ids, route: Route = Route.DECODE):
+        """Engine::stats (engine.rs:1003-1006)."""
+        return self.run(ids, route)[0]
 
     # -- introspection --
     @property
