@@ -100,6 +100,9 @@ def _declare(L):
     L.xo_gemv_magnitude.argtypes = [F32P, S, S, F32P, F64P]
     L.xo_attention_decode.argtypes = [F32P, F32P, F32P, S, S, S, S, F32P]
     L.xo_swiglu.argtypes = [F32P, S, F32P]
+    L.xo_moe_route.argtypes = [F32P, S, S, S, U32P, F32P]
+    L.xo_moe_gemv.argtypes = [F32P, S, S, S, U32P, S, F32P, S, F32P]
+    L.xo_moe_combine.argtypes = [F32P, F32P, S, S, S, F32P]
     L.xo_argmax.argtypes = [F32P, S]
     L.xo_argmax.restype = C.c_int64
     L.xo_logsumexp.argtypes = [F32P, S]
@@ -287,6 +290,40 @@ def qk_norm_rope(qkv, q_norm, k_norm, inv_freq, q_heads, kv_heads, head_dim, pos
     v = np.empty(kv_heads * head_dim, np.float32)
     lib().xo_qk_norm_rope(qkv, qn, kn, inv, q_heads, kv_heads, head_dim, pos, eps, q, k, v)
     return q, k, v
+
+
+MOE_NO_EXPERT = 0xFFFFFFFF
+
+
+def moe_route(logits, experts: int, top_k: int):
+    """lib.rs:254-282: (ids [rows][top_k] u32, weights [rows][top_k] f32), flattened."""
+    lg = f32(logits).ravel()
+    assert experts > 0 and 0 < top_k <= experts and top_k <= 64 and lg.size % experts == 0
+    rows = lg.size // experts
+    ids = np.empty(rows * top_k, np.uint32)
+    w = np.empty(rows * top_k, np.float32)
+    lib().xo_moe_route(lg, rows, experts, top_k, ids, w)
+    return ids, w
+
+
+def moe_gemv(w, experts: int, rows: int, cols: int, ids, x, x_group: int) -> np.ndarray:
+    """lib.rs:284-312: [slots][rows] f32, flattened."""
+    wf, xf = f32(w).ravel(), f32(x).ravel()
+    ids = np.ascontiguousarray(ids, np.uint32)
+    assert wf.size == experts * rows * cols and x_group > 0 and xf.size == ids.size // x_group * cols
+    y = np.empty(ids.size * rows, np.float32)
+    lib().xo_moe_gemv(wf, experts, rows, cols, ids, ids.size, xf, x_group, y)
+    return y
+
+
+def moe_combine(y, weights, hidden: int, top_k: int) -> np.ndarray:
+    """lib.rs:314-329: [rows][hidden] f32, flattened."""
+    yf, wf = f32(y).ravel(), f32(weights).ravel()
+    assert wf.size % top_k == 0 and yf.size == wf.size * hidden
+    rows = wf.size // top_k
+    out = np.empty(rows * hidden, np.float32)
+    lib().xo_moe_combine(yf, wf, rows, hidden, top_k, out)
+    return out
 
 
 def gemv(w: np.ndarray, rows: int, cols: int, x) -> np.ndarray:

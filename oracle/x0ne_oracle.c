@@ -539,6 +539,69 @@ void xo_swiglu(const float* gate_up, size_t inter, float* out) {
     }
 }
 
+/* lib.rs:254-282: routing of `rows` rows of `experts` router logits: per row the top_k experts,
+   larger logit first then the smaller index (-0.0 equals 0.0), and exp(l_e - l_max) renormalised
+   over the chosen in f64, rounded once to f32; a row with a non-finite logit gets
+   XO_MOE_NO_EXPERT and NaN. The selection is a stable order of the indices by decreasing logit
+   (the reference sorts stably), done here by repeated extraction of the best remaining. */
+void xo_moe_route(const float* logits, size_t rows, size_t experts, size_t top_k, uint32_t* ids, float* weights) {
+    unsigned char* taken = (unsigned char*)calloc(experts ? experts : 1, 1);
+    for (size_t r = 0; r < rows; ++r) {
+        const float* row = logits + r * experts;
+        uint32_t* ri = ids + r * top_k;
+        float* rw = weights + r * top_k;
+        int bad = 0;
+        for (size_t i = 0; i < experts; ++i) bad |= !isfinite(row[i]);
+        if (bad) {
+            for (size_t s = 0; s < top_k; ++s) {
+                ri[s] = XO_MOE_NO_EXPERT;
+                rw[s] = NAN;
+            }
+            continue;
+        }
+        memset(taken, 0, experts);
+        for (size_t s = 0; s < top_k; ++s) {
+            size_t best = experts;
+            for (size_t i = 0; i < experts; ++i)
+                if (!taken[i] && (best == experts || row[i] > row[best])) best = i;
+            taken[best] = 1;
+            ri[s] = (uint32_t)best;
+        }
+        const double m = (double)row[ri[0]];
+        double e[64], sum = 0.0;
+        for (size_t s = 0; s < top_k; ++s) {
+            e[s] = exp((double)row[ri[s]] - m);
+            sum += e[s];
+        }
+        for (size_t s = 0; s < top_k; ++s) rw[s] = (float)(e[s] / sum);
+    }
+    free(taken);
+}
+
+/* lib.rs:284-312: y[s] = W[ids[s]] x[s / x_group] for W [experts][rows][cols] (bf16 values as
+   f32) and x [slots / x_group][cols]; an id outside the experts gives a NaN row. */
+void xo_moe_gemv(const float* w, size_t experts, size_t rows, size_t cols, const uint32_t* ids, size_t slots,
+                 const float* x, size_t x_group, float* y) {
+    for (size_t s = 0; s < slots; ++s) {
+        float* ys = y + s * rows;
+        if ((size_t)ids[s] >= experts) {
+            for (size_t r = 0; r < rows; ++r) ys[r] = NAN;
+            continue;
+        }
+        gemv_any(w + (size_t)ids[s] * rows * cols, 0, rows, cols, x + (s / x_group) * cols, ys);
+    }
+}
+
+/* lib.rs:314-329: out[r][i] = sum_s weights[r][s] y[r][s][i] in f64, in slot order, rounded once. */
+void xo_moe_combine(const float* y, const float* weights, size_t rows, size_t hidden, size_t top_k, float* out) {
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t i = 0; i < hidden; ++i) {
+            double acc = 0.0;
+            for (size_t s = 0; s < top_k; ++s) acc += (double)weights[r * top_k + s] * (double)y[(r * top_k + s) * hidden + i];
+            out[r * hidden + i] = (float)acc;
+        }
+}
+
 /* lib.rs:218-230: the first index of the largest value; none for an empty row or a NaN. */
 int64_t xo_argmax(const float* x, size_t n) {
     int64_t best = -1;

@@ -75,6 +75,12 @@ void xo_gemv_magnitude(const float* w, size_t rows, size_t cols, const float* x,
 void xo_attention_decode(const float* q, const float* k, const float* v, size_t ctx,
                          size_t q_heads, size_t kv_heads, size_t head_dim, float* out);
 void xo_swiglu(const float* gate_up, size_t inter, float* out);
+/* GM1, Qwen3-MoE (lib.rs:254-329). */
+#define XO_MOE_NO_EXPERT 0xFFFFFFFFu
+void xo_moe_route(const float* logits, size_t rows, size_t experts, size_t top_k, uint32_t* ids, float* weights);
+void xo_moe_gemv(const float* w, size_t experts, size_t rows, size_t cols, const uint32_t* ids, size_t slots,
+                 const float* x, size_t x_group, float* y);
+void xo_moe_combine(const float* y, const float* weights, size_t rows, size_t hidden, size_t top_k, float* out);
 int64_t xo_argmax(const float* x, size_t n); /* -1: empty or a NaN */
 double xo_logsumexp(const float* x, size_t n);
 double xo_kl(const float* p, const float* q, size_t n);

@@ -641,3 +641,47 @@ def test_sliced_argmax_picks_what_the_one_block_argmax_picks(kernels):
 def test_advance_adds_one(kernels):
     for v in [0, 1, 511, 512, 131071, 2**32 - 2]:
         assert kernels.advance(v) == v + 1
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_moe_kernels_are_the_reference(kernels, seed):
+    """gpu_kernels.rs:841-914: the routing (ids exact, weights within 1e-6 + 1e-5 relative) over
+    1 to 1024 experts with ties and a non-finite logit now and then; the expert GEMVs through
+    the routed ids (an undefined row included) in f32 and bf16; the weighted combination."""
+    rng = O.Rng(800 + seed)
+    experts = rng.pick([1, 2, 8, 128, 1024])
+    top_k = rng.range(1, min(experts, 32))
+    rows = rng.range(1, 9)
+    if rng.chance(3):
+        logits = np.array([float(rng.below(3)) for _ in range(rows * experts)], np.float32)
+    else:
+        logits = np.asarray(rng.f32s(rows * experts, 6.0), np.float32)
+    if rng.chance(3):
+        logits[rng.below(rows * experts)] = rng.pick([np.nan, np.inf, -np.inf])
+    ids, w = kernels.moe_route(logits, experts, top_k)
+    want_ids, want_w = O.moe_route(logits, experts, top_k)
+    what = f"seed {seed}: {experts} experts, top {top_k}, {rows} rows"
+    assert (ids == want_ids).all(), what
+    assert_close(f"moe weights {what}", w, want_w, 1e-6, 1e-5)
+    r, cols = rng.pick([1, 8, 24]), 8 * rng.range(1, 8)
+    small = min(experts, 8)
+    ids = np.array([i if i == O.MOE_NO_EXPERT or i < small else i % small for i in ids.tolist()], np.uint32)
+    wt = np.asarray(rng.bf16s(small * r * cols, 1.0), np.float32)
+    x = np.asarray(rng.bf16s(rows * cols, 2.0), np.float32)
+    want = O.moe_gemv(wt, small, r, cols, ids, x, top_k)
+    for f32_out in (True, False):
+        got = kernels.moe_gemv(bf16_bits(wt), small, r, cols, ids, bf16_bits(x), top_k, f32_out)
+        assert_close(f"moe gemv {what} f32 {f32_out}", got, want, 1e-4, 1e-4 if f32_out else BF16_RTOL)
+    hidden = 8 * rng.range(1, 16)
+    y = np.asarray(rng.f32s(rows * top_k * hidden, 3.0), np.float32)
+    wts = np.asarray(rng.f32s(rows * top_k, 1.0), np.float32)
+    got = bf16_vals(kernels.moe_combine(y, wts, hidden, top_k))
+    assert_close(f"moe combine {what}", got, O.moe_combine(y, wts, hidden, top_k), 1e-4, BF16_RTOL)
+
+
+def test_moe_routing_refuses_what_the_kernel_does_not_take(kernels):
+    """gpu_kernels.rs:915-930."""
+    from x0ne_core import FormatError
+    for experts, top_k, n in [(0, 1, 8), (1025, 1, 1025), (8, 0, 8), (8, 9, 8), (64, 33, 64), (8, 2, 7), (8, 2, 0)]:
+        with pytest.raises(FormatError):
+            kernels.moe_route(np.zeros(n, np.float32), experts, top_k)

@@ -280,3 +280,47 @@ def test_greedy_is_argmax_of_the_logits_it_stepped():
     assert [O.argmax(r) for r in rows] == toks.tolist()
     s = np.sort(rows, axis=1)
     assert np.allclose(s[:, -1] - s[:, -2], margins)
+
+
+def test_the_reference_routing_chooses_the_largest_and_normalises():
+    """cpu_oracle.rs:449-498: per row the chosen experts are the largest, in order (larger logit,
+    then the smaller index), distinct, none left out larger than the last; the weights a
+    decreasing distribution; a row with a non-finite logit has no expert and NaN weights; an
+    expert outside the table gives a NaN row and the others are their GEMV; the combination by
+    hand."""
+    rng = O.Rng(9)
+    for _ in range(2000):
+        experts = rng.range(1, 24)
+        top_k = rng.range(1, experts)
+        row = (np.array([float(rng.below(3)) for _ in range(experts)], np.float32) if rng.chance(3)
+               else np.asarray(rng.f32s(experts, 8.0), np.float32))
+        poisoned = rng.chance(8)
+        if poisoned:
+            row[rng.below(experts)] = rng.pick([np.nan, np.inf, -np.inf])
+        ids, w = O.moe_route(row, experts, top_k)
+        assert ids.size == top_k and w.size == top_k
+        if poisoned:
+            assert (ids == O.MOE_NO_EXPERT).all() and np.isnan(w).all()
+            continue
+        for a, b in zip(ids[:-1], ids[1:]):
+            assert row[a] > row[b] or (row[a] == row[b] and a < b), (row, ids)
+        assert len(set(ids.tolist())) == top_k
+        least = row[ids[-1]]
+        assert all(row[i] <= least for i in range(experts) if i not in set(ids.tolist()))
+        assert abs(float(np.sum(w.astype(np.float64))) - 1.0) < 1e-6
+        assert (w[:-1] >= w[1:]).all() and ((w > 0).all() or top_k > 1)
+    w = np.asarray(rng.bf16s(3 * 4 * 8, 1.0), np.float32)
+    x = np.asarray(rng.bf16s(2 * 8, 1.0), np.float32)
+    y = O.moe_gemv(w, 3, 4, 8, [2, 3, O.MOE_NO_EXPERT, 0], x, 2)
+    assert (y[:4] == O.gemv(w[2 * 32:], 4, 8, x[:8])).all()
+    assert np.isnan(y[4:12]).all()
+    assert (y[12:] == O.gemv(w[:32], 4, 8, x[8:])).all()
+    assert O.moe_combine([1.0, 2.0, 3.0, 4.0], [0.25, 0.75], 2, 2).tolist() == [2.5, 3.5]
+
+
+def test_routing_ties_keep_the_smaller_index_and_signed_zeros_are_equal():
+    """The stable order of the reference (lib.rs:268-270): equal logits, -0.0 and 0.0 among them,
+    keep the smaller index first; the weights of equal logits are equal."""
+    ids, w = O.moe_route(np.array([0.0, -0.0, 1.0, 1.0, -0.0], np.float32), 5, 4)
+    assert ids.tolist() == [2, 3, 0, 1]
+    assert w[0] == w[1] and w[2] == w[3] and w[0] > w[2]

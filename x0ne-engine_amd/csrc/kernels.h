@@ -95,6 +95,14 @@ X0NE_DECLARE_FEW(t2_r1_swiglu)
 X0NE_DECLARE_FEW(t4_r1)
 X0NE_DECLARE_FEW(t4_r1_swiglu)
 #undef X0NE_DECLARE_FEW
+__global__ void x0ne_moe_route_f32(const float* logits, uint32_t experts, uint32_t top_k, uint32_t* ids,
+                                   float* weights);
+__global__ void x0ne_moe_gemv_bf16(const bf16_t* w, const uint32_t* ids, const bf16_t* x, bf16_t* y, uint32_t rows,
+                                   uint32_t cols, uint32_t experts, uint32_t x_group, uint32_t x_stride);
+__global__ void x0ne_moe_gemv_f32(const bf16_t* w, const uint32_t* ids, const bf16_t* x, float* y, uint32_t rows,
+                                  uint32_t cols, uint32_t experts, uint32_t x_group, uint32_t x_stride);
+__global__ void x0ne_moe_combine_bf16(const float* y, const float* weights, bf16_t* out, uint32_t hidden,
+                                      uint32_t top_k);
 __global__ void x0ne_panel_bf16(const bf16_t* src, bf16_t* dst, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_f32(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);

@@ -638,6 +638,80 @@ class Kernels:
             raise FormatError("swiglu: odd length")
         return self.swiglu_rows(gate_up, 1)
 
+    # -- the MoE block (ops.rs:796-920) --
+    MOE_MAX_EXPERTS = 1024
+    MOE_NO_EXPERT = 0xFFFFFFFF
+
+    def moe_route(self, logits, experts: int, top_k: int):
+        """x0ne_moe_route_f32 over rows of `experts` f32 router logits: (ids, weights), each
+        [rows][top_k] flattened (ops.rs:796-842, the same refusals)."""
+        lg = np.ascontiguousarray(logits, np.float32).ravel()
+        if experts == 0 or experts > self.MOE_MAX_EXPERTS or top_k == 0 or top_k > 32 or top_k > experts or \
+                lg.size == 0 or lg.size % experts:
+            raise FormatError(f"moe_route: {lg.size} logits, {experts} experts, top {top_k}")
+        rows = lg.size // experts
+        a = self._arena()
+        ls = a.alloc("logits", lg.size * 4, Class.CLIENT_DATA)
+        ids = a.alloc("ids", rows * top_k * 4, Class.CLIENT_DATA)
+        ws = a.alloc("weights", rows * top_k * 4, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ls, 0, lg)
+        self.gpu.launch("x0ne_moe_route_f32", rows, 128,
+                        [Arg.ptr(a.ptr(ls)), Arg.u32(experts), Arg.u32(top_k), Arg.ptr(a.ptr(ids)),
+                         Arg.ptr(a.ptr(ws))])
+        self.gpu.sync()
+        return a.read_array(ids, 0, rows * top_k, np.uint32), a.read_array(ws, 0, rows * top_k, np.float32)
+
+    def moe_gemv(self, w, experts: int, rows: int, cols: int, ids, x, x_group: int, f32_out: bool) -> np.ndarray:
+        """x0ne_moe_gemv_{bf16,f32}: y[s] = W[ids[s]] x[s / x_group] for bf16 bits W
+        [experts][rows][cols] and x [slots / x_group][cols]; [slots][rows] as f32 values
+        (ops.rs:844-907, the same refusals)."""
+        w = np.ascontiguousarray(w, np.uint16).ravel()
+        x = np.ascontiguousarray(x, np.uint16).ravel()
+        ids = np.ascontiguousarray(ids, np.uint32).ravel()
+        slots = ids.size
+        if experts == 0 or rows == 0 or cols == 0 or cols % 8 or w.size != experts * rows * cols or slots == 0 or \
+                x_group == 0 or slots % x_group or x.size != slots // x_group * cols:
+            raise FormatError(f"moe_gemv: W {w.size} for {experts}x{rows}x{cols}, {slots} slots, x {x.size}")
+        ob = 4 if f32_out else 2
+        a = self._arena()
+        ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
+        is_ = a.alloc("ids", slots * 4, Class.CLIENT_DATA)
+        xs = a.alloc("x", x.size * 2, Class.CLIENT_DATA)
+        ys = a.alloc("y", slots * rows * ob, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ws, 0, w)
+        a.write(is_, 0, ids)
+        a.write(xs, 0, x)
+        self.gpu.launch("x0ne_moe_gemv_f32" if f32_out else "x0ne_moe_gemv_bf16", ((rows + 3) // 4, slots), 256,
+                        [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(is_)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)),
+                         Arg.u32(rows), Arg.u32(cols), Arg.u32(experts), Arg.u32(x_group), Arg.u32(cols)])
+        self.gpu.sync()
+        if f32_out:
+            return a.read_array(ys, 0, slots * rows, np.float32)
+        y = a.read_array(ys, 0, slots * rows, np.uint16)
+        return (y.astype(np.uint32) << 16).view(np.float32)
+
+    def moe_combine(self, y, weights, hidden: int, top_k: int) -> np.ndarray:
+        """x0ne_moe_combine_bf16: out[r] = bf16(sum_s weights[r][s] y[r][s]) for y
+        [rows][top_k][hidden] f32; bf16 bits [rows][hidden] (ops.rs:909-920)."""
+        y = np.ascontiguousarray(y, np.float32).ravel()
+        wt = np.ascontiguousarray(weights, np.float32).ravel()
+        if hidden == 0 or top_k == 0 or wt.size == 0 or wt.size % top_k or y.size != wt.size * hidden:
+            raise FormatError(f"moe_combine: y {y.size}, weights {wt.size}, hidden {hidden}, top {top_k}")
+        rows = wt.size // top_k
+        a = self._arena()
+        ys = a.alloc("y", y.size * 4, Class.CLIENT_DATA)
+        ws = a.alloc("weights", wt.size * 4, Class.CLIENT_DATA)
+        out = a.alloc("out", rows * hidden * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ys, 0, y)
+        a.write(ws, 0, wt)
+        self.gpu.launch("x0ne_moe_combine_bf16", ((hidden + 255) // 256, rows), 256,
+                        [Arg.ptr(a.ptr(ys)), Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(out)), Arg.u32(hidden), Arg.u32(top_k)])
+        self.gpu.sync()
+        return a.read_array(out, 0, rows * hidden, np.uint16)
+
     # -- advance, argmax (ops.rs:925-976) --
     def advance(self, value: int) -> int:
         a = self._arena()
