@@ -306,6 +306,13 @@ typedef struct {
 x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t route, const size_t* keep,
                             size_t n_keep, x0ne_pos_stats* stats, float* rows);
 
+/* Engine::moe_routing (engine.rs:612-640): the experts every layer of a Qwen3-MoE engine chose
+   at each position of ids (fed one per step through the decode route), [position][layer][top_k]
+   into out (room for cap entries; X0NE_ERR_FORMAT when short); *written their count, 0 for a
+   dense engine. */
+x0ne_status x0ne_engine_moe_routing(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t* out, size_t cap,
+                                    size_t* written);
+
 /* Engine::describe, graph_nodes, splits, counts, client_data_is_zero, host_buffers_are_zero
    (engine.rs:563-670). */
 x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, size_t len);

@@ -28,7 +28,7 @@ def header_functions():
 def test_the_header_declares_the_boundary_the_reference_binds():
     decls = header_functions()
     # The entry points a Rust wrapper of x0ne-core/runtime needs (engine.rs, gpu.rs, arena.rs).
-    for name in ["x0ne_engine_load_from", "x0ne_engine_load", "x0ne_engine_run", "x0ne_engine_session", "x0ne_session_logits", "x0ne_session_step",
+    for name in ["x0ne_engine_load_from", "x0ne_engine_load", "x0ne_engine_run", "x0ne_engine_moe_routing", "x0ne_engine_session", "x0ne_session_logits", "x0ne_session_step",
                  "x0ne_session_finish", "x0ne_session_into_greedy", "x0ne_greedy_next", "x0ne_greedy_finish",
                  "x0ne_engine_greedy_timed", "x0ne_engine_describe", "x0ne_engine_free", "x0ne_arena_new",
                  "x0ne_arena_alloc", "x0ne_arena_freeze", "x0ne_arena_write", "x0ne_arena_read", "x0ne_arena_addr",

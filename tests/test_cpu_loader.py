@@ -395,3 +395,78 @@ def test_a_shard_name_is_a_plain_file_name(checkpoint, tmp_path):
         write_index(name)
         with pytest.raises(Error):
             load_dir(model)
+
+
+def moe_config(base=None) -> dict:
+    """cpu_config.rs:37-46"""
+    v = dict(base or dense())
+    v.update({"model_type": "qwen3_moe", "decoder_sparse_step": 1, "norm_topk_prob": True, "num_experts": 8,
+              "num_experts_per_tok": 2, "moe_intermediate_size": 16, "mlp_only_layers": []})
+    return v
+
+
+def moe_checkpoint(cfg_json: dict, seed: int = 5) -> bytes:
+    """A Qwen3-MoE checkpoint of cfg_json's shapes: the dense model's attention, norms and
+    vocabulary, and per layer the router and every expert's gate, up and down projections."""
+    c = cfg_json
+    h, layers, experts, mi = c["hidden_size"], c["num_hidden_layers"], c["num_experts"], c["moe_intermediate_size"]
+    base = reference_tensors(tiny(layers, c["num_attention_heads"], c["num_key_value_heads"], False), seed)
+    out = {k: v for k, v in base.items() if ".mlp." not in k}
+    g = np.random.default_rng(seed)
+
+    def bits(*shape):
+        return shape, (g.integers(0, 1 << 14, size=int(np.prod(shape))) | 0x3C00).astype(np.uint16)
+
+    for l in range(layers):
+        out[f"model.layers.{l}.mlp.gate.weight"] = bits(experts, h)
+        for e in range(experts):
+            out[f"model.layers.{l}.mlp.experts.{e}.gate_proj.weight"] = bits(mi, h)
+            out[f"model.layers.{l}.mlp.experts.{e}.up_proj.weight"] = bits(mi, h)
+            out[f"model.layers.{l}.mlp.experts.{e}.down_proj.weight"] = bits(h, mi)
+    return safetensors_bytes(out)
+
+
+@pytest.fixture(scope="module")
+def moe_file():
+    return moe_checkpoint(moe_config())
+
+
+def test_a_qwen3_moe_config_reads_strictly(moe_file):
+    """cpu_config.rs:362-453 through Engine::load_from: the config itself passes the checks; every
+    value the reader refuses (shared experts, a sparse step other than 1, dense layers, top-k not
+    renormalised, sizes that are not positive integers, more experts per token than experts) is a
+    format error, and so is each required key missing; the optional keys may be null or absent."""
+    passed_the_checks("the MoE config", moe_config(), moe_file)
+    for key, values in [("shared_expert_intermediate_size", [64, 0, False]), ("n_shared_experts", [1, 0]),
+                        ("decoder_sparse_step", [2, 0, None, "1"]), ("mlp_only_layers", [[0], 0, {}, False]),
+                        ("norm_topk_prob", [False, None, 1, "true"]),
+                        ("num_experts", [0, 1, -8, 8.5, 1 << 32, None]), ("num_experts_per_tok", [0, 9, -1, "2"]),
+                        ("moe_intermediate_size", [0, -16, 16.5, None])]:
+        for value in values:
+            refused(f"{key} = {value}", with_(key, value, moe_config()), moe_file)
+    for key in ["decoder_sparse_step", "norm_topk_prob", "num_experts", "num_experts_per_tok",
+                "moe_intermediate_size"]:
+        v = moe_config()
+        del v[key]
+        refused(f"{key} missing", v, moe_file)
+    for key in ["mlp_only_layers", "shared_expert_intermediate_size", "n_shared_experts"]:
+        passed_the_checks(f"{key} null", with_(key, None, moe_config()), moe_file)
+        v = moe_config()
+        v.pop(key, None)
+        passed_the_checks(f"{key} absent", v, moe_file)
+
+
+def test_read_any_tells_dense_from_moe_and_refuses_the_rest(checkpoint, moe_file):
+    """cpu_config.rs:455-475 and :548-565: other model types are refused; a MoE config without its
+    fields, a MoE config over dense weights, a dense config over MoE weights, and the kernels'
+    limits (1025 experts, 33 per token, a width that is not a multiple of 8) are format errors."""
+    for model_type in ["qwen2", "qwen2_moe", "llama", "", "qwen3_moe "]:
+        refused(model_type, with_("model_type", model_type, moe_config()), moe_file)
+    refused("a MoE without its fields", with_("model_type", "qwen3_moe"), checkpoint)
+    refused("a MoE config over dense weights", moe_config(), checkpoint)
+    refused("a dense config over MoE weights", dense(), moe_file)
+    for key, value in [("num_experts", 1025), ("num_experts_per_tok", 33), ("moe_intermediate_size", 12)]:
+        big = with_("num_experts", 1024, moe_config())
+        refused(f"{key} = {value}", with_(key, value, big), moe_file)
+    for bad in ["", "[]"]:
+        refused(f"config {bad!r}", bad, moe_file)

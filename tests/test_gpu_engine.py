@@ -471,3 +471,103 @@ def test_the_statistics_of_a_pass_are_those_of_its_logits_rows(route_name):
     assert e.client_data_is_zero()
     with pytest.raises(FormatError):
         e.run(ids, route, keep=[len(ids)])
+
+
+def moe_of_dense(f, experts: int, top_k: int, router_bits=None):
+    """The Qwen3-MoE checkpoint and config whose every expert is the dense fixture's MLP: the same
+    attention, norms and vocabulary, mlp.experts.e.* = mlp.*, the router `router_bits` (zeros:
+    every logit equal, so the routing takes experts 0 .. top_k - 1 at equal weights)."""
+    cfg = f.cfg.to_json()
+    cfg.update({"model_type": "qwen3_moe", "decoder_sparse_step": 1, "norm_topk_prob": True,
+                "num_experts": experts, "num_experts_per_tok": top_k, "moe_intermediate_size": f.cfg.inter,
+                "mlp_only_layers": []})
+    out = {k: v for k, v in f.tensors.items() if ".mlp." not in k}
+    h = f.cfg.hidden
+    for l in range(f.cfg.layers):
+        p = f"model.layers.{l}.mlp."
+        out[p + "gate.weight"] = ((experts, h), np.zeros(experts * h, np.uint16) if router_bits is None
+                                  else router_bits[l])
+        for e in range(experts):
+            for leaf in ("gate_proj", "up_proj", "down_proj"):
+                out[f"{p}experts.{e}.{leaf}.weight"] = f.tensors[p + leaf + ".weight"]
+    return json.dumps(cfg), safetensors_bytes(out)
+
+
+@pytest.mark.parametrize("experts,top_k", [(1, 1), (2, 2)])
+def test_a_moe_of_identical_experts_is_the_dense_model(experts, top_k):
+    """A Qwen3-MoE engine (router GEMV, routing, expert GEMVs through the device-held ids, SwiGLU,
+    f32 down rows, weighted combination) whose experts all equal the dense MLP: top-1 weighs its
+    expert exactly 1, and two experts with equal router logits route to [0, 1] at 0.5 each, so
+    the combination is exact; the logits are the dense oracle's within the model tolerance
+    (gpu_engine.rs:29-32) at every position, graph and eager give the same bits, the routing
+    diagnostic reads [0 .. top_k) at every layer and position, and the client bytes are zeroed."""
+    from x0ne_core import DecodeMode, Engine, EngineOptions, Route
+    f = Fixture(wide(), 41)
+    text, file = moe_of_dense(f, experts, top_k)
+    e = Engine.load_from(text, {"model.safetensors": file}, EngineOptions(max_ctx=64, page_seed=6))
+    assert "MoE, %d experts" % experts in e.describe(), e.describe()
+    ids = f.tokens(42, 20)
+    want = f.model.logits(ids)
+    at = [0, 5, 11, 19]
+    graph = e.logits_at(ids, at, Route.DECODE)
+    for row, p in zip(graph, at):
+        assert_logits(f"moe {experts}/{top_k} position {p}", row, want[p])
+    e.set_decode_mode(DecodeMode.EAGER)
+    eager = e.logits_at(ids, at, Route.DECODE)
+    for a, b, p in zip(graph, eager, at):
+        assert (a.view(np.uint32) == b.view(np.uint32)).all(), f"graph and eager at {p}"
+    e.set_decode_mode(DecodeMode.GRAPH)
+    route = e.moe_routing(ids[:6]).reshape(6, f.cfg.layers, top_k)
+    assert (route == np.arange(top_k, dtype=np.uint32)).all(), route
+    dev = e.greedy(ids[:12], 8)
+    f.model.reset()
+    oracle, margins = f.model.greedy(ids[:12], 8)
+    agree = int(np.argmin(np.append(dev == oracle, False)))
+    if agree < 8:
+        full = f.model.logits(np.concatenate([ids[:12], oracle[:-1]]))
+        assert margins[agree] < 2 * LOGITS_ATOL_OF_MAX * float(np.abs(full[11 + agree]).max())
+    assert e.client_data_is_zero()
+
+
+def test_a_random_moe_routes_each_token_to_distinct_experts():
+    """Eight experts of their own, two per token, a random router: each layer's routing at each
+    position names two distinct experts below 8; the step is the same bits graph and eager and
+    over repeated requests; greedy decoding runs through the captured graph; a dense engine has
+    no routing to report."""
+    from x0ne_core import DecodeMode, Engine, EngineOptions, Route
+    f = Fixture(tiny(2, 4, 2, False), 43)
+    g = np.random.default_rng(44)
+    text, _ = moe_of_dense(f, 8, 2)
+    cfg = json.loads(text)
+    cfg["moe_intermediate_size"] = 64
+    out = {k: v for k, v in f.tensors.items() if ".mlp." not in k}
+    h = f.cfg.hidden
+
+    def bits(*shape):
+        vals = g.normal(0, 0.1, size=int(np.prod(shape))).astype(np.float32)
+        return shape, (vals.view(np.uint32) >> 16).astype(np.uint16)
+
+    for l in range(f.cfg.layers):
+        p = f"model.layers.{l}.mlp."
+        out[p + "gate.weight"] = bits(8, h)
+        for x in range(8):
+            out[f"{p}experts.{x}.gate_proj.weight"] = bits(64, h)
+            out[f"{p}experts.{x}.up_proj.weight"] = bits(64, h)
+            out[f"{p}experts.{x}.down_proj.weight"] = bits(h, 64)
+    e = Engine.load_from(json.dumps(cfg), {"model.safetensors": safetensors_bytes(out)},
+                         EngineOptions(max_ctx=64, page_seed=2))
+    ids = f.tokens(45, 16)
+    route = e.moe_routing(ids).reshape(16, f.cfg.layers, 2)
+    assert (route < 8).all() and (route[..., 0] != route[..., 1]).all()
+    assert len(set(route.reshape(-1).tolist())) > 2, "the router spreads the tokens"
+    a = e.logits_at(ids, [3, 15], Route.DECODE)
+    b = e.logits_at(ids, [3, 15], Route.DECODE)
+    e.set_decode_mode(DecodeMode.EAGER)
+    c = e.logits_at(ids, [3, 15], Route.DECODE)
+    e.set_decode_mode(DecodeMode.GRAPH)
+    for x, y, z in zip(a, b, c):
+        assert (x.view(np.uint32) == y.view(np.uint32)).all() and (x.view(np.uint32) == z.view(np.uint32)).all()
+        assert np.isfinite(x).all()
+    assert e.greedy(ids[:10], 6).size == 6 and e.client_data_is_zero()
+    dense = f.engine(64)
+    assert dense.moe_routing(ids).size == 0

@@ -44,11 +44,17 @@ constexpr size_t RING = 16;  // engine.rs:70
 constexpr uint64_t PREFILL_CHUNK = 2048;
 constexpr uint64_t MAX_BATCH = 64;  // the few-row GEMM's most rows
 constexpr uint32_t ARGMAX_SLICES = 64;  // blocks per logits row of the batched step's argmax
+constexpr uint64_t MOE_MAX_EXPERTS = 1024;  // kernels/src/lib.rs:147 (moe.hip)
+constexpr uint64_t MOE_MAX_TOP_K = 32;
 
 struct Cfg {
     uint64_t hidden = 0, inter = 0, layers = 0, q_heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, max_pos = 0;
     double eps = 0, theta = 0;
     bool tied = false;
+    // Qwen3-MoE (config.rs:218-335): every layer's feed-forward routes a token to top_k of
+    // `experts` SwiGLU experts of width moe_inter (intermediate_size is then unused).
+    bool moe = false;
+    uint64_t experts = 0, top_k = 0, moe_inter = 0;
     uint64_t q_dim() const { return q_heads * head_dim; }
     uint64_t kv_dim() const { return kv_heads * head_dim; }
     uint64_t qkv_rows() const { return q_dim() + 2 * kv_dim(); }
@@ -100,7 +106,10 @@ x0ne_status parse_config(const char* text, Cfg* c) {
     if (v.kind != Json::Object) return fail(X0NE_ERR_FORMAT, "config.json: not an object");
     const Json* mt = v.get("model_type");
     if (!mt) return fail(X0NE_ERR_FORMAT, "config.json: missing model_type");
-    if (mt->kind != Json::String || mt->text != "qwen3") return fail(X0NE_ERR_FORMAT, "config.json: model_type is not qwen3");
+    // read_any (config.rs:329-335): qwen3, or qwen3_moe with its sparse block.
+    if (mt->kind != Json::String || (mt->text != "qwen3" && mt->text != "qwen3_moe"))
+        return fail(X0NE_ERR_FORMAT, "config.json: model_type is not qwen3 or qwen3_moe");
+    c->moe = mt->text == "qwen3_moe";
     const Json* dt = v.get("dtype");
     if (!dt) dt = v.get("torch_dtype");
     if (!dt || dt->kind != Json::String || dt->text != "bfloat16")
@@ -130,12 +139,38 @@ x0ne_status parse_config(const char* text, Cfg* c) {
         if (rp) theta = rp->get("rope_theta");
     }
     if (!positive_f64(theta, "rope_theta", &c->theta, &err)) return fail(X0NE_ERR_FORMAT, err);
+    if (c->moe) {  // Qwen3MoeConfig::from_json (config.rs:237-279)
+        for (const char* key : {"shared_expert_intermediate_size", "n_shared_experts"}) {
+            const Json* f = v.get(key);
+            if (f && f->kind != Json::Null)
+                return fail(X0NE_ERR_FORMAT, std::string("config.json: ") + key + " is set, not implemented");
+        }
+        uint64_t step = 0;
+        if (!positive_u64(v, "decoder_sparse_step", &step, &err)) return fail(X0NE_ERR_FORMAT, err);
+        if (step != 1)
+            return fail(X0NE_ERR_FORMAT, "config.json: decoder_sparse_step is not 1, dense layers are not implemented");
+        const Json* mlp_only = v.get("mlp_only_layers");
+        if (mlp_only && mlp_only->kind != Json::Null && !(mlp_only->kind == Json::Array && mlp_only->items.empty()))
+            return fail(X0NE_ERR_FORMAT, "config.json: mlp_only_layers is not empty, dense layers are not implemented");
+        const Json* norm_topk = v.get("norm_topk_prob");
+        if (!norm_topk || norm_topk->kind != Json::Bool || !norm_topk->b)
+            return fail(X0NE_ERR_FORMAT,
+                        "config.json: norm_topk_prob is not true, only renormalised top-k is implemented");
+        if (!positive_u64(v, "num_experts", &c->experts, &err) ||
+            !positive_u64(v, "num_experts_per_tok", &c->top_k, &err) ||
+            !positive_u64(v, "moe_intermediate_size", &c->moe_inter, &err))
+            return fail(X0NE_ERR_FORMAT, err);
+        if (c->top_k > c->experts) return fail(X0NE_ERR_FORMAT, "config.json: num_experts_per_tok exceeds num_experts");
+        if (c->experts > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "config.json: num_experts does not fit a u32 expert id");
+    }
     if (c->q_heads % c->kv_heads != 0)
         return fail(X0NE_ERR_FORMAT, "config.json: attention heads are not a multiple of KV heads");
     if (c->head_dim % 2 != 0) return fail(X0NE_ERR_FORMAT, "config.json: head_dim is odd, RoPE needs pairs");
     if (c->vocab > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "config.json: vocab_size does not fit a u32 token id");
     // Every derived size must fit in 64 bits (config.rs check_sizes).
-    const long double big = (long double)c->layers * (long double)(c->qkv_rows() * c->hidden + 3 * c->inter * c->hidden) +
+    const long double ffn = c->moe ? (long double)c->experts * (3.0L * c->moe_inter * c->hidden + c->hidden)
+                                   : 3.0L * c->inter * c->hidden;
+    const long double big = (long double)c->layers * ((long double)(c->qkv_rows() * c->hidden) + ffn) +
                             (long double)c->vocab * c->hidden * 2;
     if (big > 1e18L) return fail(X0NE_ERR_FORMAT, "config.json: a derived size overflows");
     return X0NE_OK;
@@ -143,6 +178,17 @@ x0ne_status parse_config(const char* text, Cfg* c) {
 
 // Limits of the kernels (engine.rs:236-289, plus this build's GEMV and KV-page limits).
 x0ne_status check_config(const Cfg& c, uint64_t max_ctx) {
+    if (c.moe) {  // engine.rs:236-262
+        if (c.experts == 0 || c.experts > MOE_MAX_EXPERTS)
+            return fail(X0NE_ERR_FORMAT, "num_experts " + std::to_string(c.experts) + " outside 1..=" +
+                                             std::to_string(MOE_MAX_EXPERTS));
+        if (c.top_k == 0 || c.top_k > MOE_MAX_TOP_K)
+            return fail(X0NE_ERR_FORMAT, "num_experts_per_tok " + std::to_string(c.top_k) + " outside 1..=32");
+        if (c.moe_inter == 0 || c.moe_inter % 8 != 0)
+            return fail(X0NE_ERR_FORMAT, "moe_intermediate_size is not a positive multiple of 8");
+        if (c.experts * 2 * c.moe_inter > UINT32_MAX || c.top_k * c.hidden > UINT32_MAX)
+            return fail(X0NE_ERR_FORMAT, "a MoE dimension exceeds u32");
+    }
     if (c.head_dim != 128) return fail(X0NE_ERR_FORMAT, "head_dim " + std::to_string(c.head_dim) + ": kernels are built for 128");
     if (c.hidden % 8 != 0) return fail(X0NE_ERR_FORMAT, "hidden_size is not a multiple of 8");
     if (c.inter % 8 != 0) return fail(X0NE_ERR_FORMAT, "intermediate_size is not a multiple of 8");
@@ -185,6 +231,14 @@ std::vector<uint64_t> leaf_shape(const Cfg& c, int leaf) {
 std::string layer_name(uint64_t l, int leaf) {
     return "model.layers." + std::to_string(l) + "." + LEAF_NAMES[leaf] + ".weight";
 }
+
+// A Qwen3-MoE layer's feed-forward tensors (weights.rs:371-389): the router mlp.gate
+// [experts][hidden] and per expert e mlp.experts.e.{gate,up}_proj [moe_inter][hidden] and
+// down_proj [hidden][moe_inter].
+std::string expert_name(uint64_t l, uint64_t e, const char* leaf) {
+    return "model.layers." + std::to_string(l) + ".mlp.experts." + std::to_string(e) + "." + leaf + ".weight";
+}
+std::string router_name(uint64_t l) { return "model.layers." + std::to_string(l) + ".mlp.gate.weight"; }
 
 // ---- safetensors in memory (st.rs:21-277) ----
 
@@ -248,8 +302,20 @@ x0ne_status parse_safetensors(const std::string& file, const uint8_t* bytes, uin
 x0ne_status check_tensors(const Cfg& c, const std::map<std::string, TensorView>& t) {
     std::map<std::string, std::vector<uint64_t>> want;
     want["model.embed_tokens.weight"] = {c.vocab, c.hidden};
-    for (uint64_t l = 0; l < c.layers; ++l)
-        for (int leaf = 0; leaf < L_COUNT; ++leaf) want[layer_name(l, leaf)] = leaf_shape(c, leaf);
+    for (uint64_t l = 0; l < c.layers; ++l) {
+        for (int leaf = 0; leaf < L_COUNT; ++leaf) {
+            if (c.moe && (leaf == L_GATE || leaf == L_UP || leaf == L_DOWN)) continue;
+            want[layer_name(l, leaf)] = leaf_shape(c, leaf);
+        }
+        if (c.moe) {
+            want[router_name(l)] = {c.experts, c.hidden};
+            for (uint64_t e = 0; e < c.experts; ++e) {
+                want[expert_name(l, e, "gate_proj")] = {c.moe_inter, c.hidden};
+                want[expert_name(l, e, "up_proj")] = {c.moe_inter, c.hidden};
+                want[expert_name(l, e, "down_proj")] = {c.hidden, c.moe_inter};
+            }
+        }
+    }
     want["model.norm.weight"] = {c.hidden};
     if (!c.tied) want["lm_head.weight"] = {c.vocab, c.hidden};
     for (const auto& kv : t) {
@@ -289,6 +355,8 @@ uint64_t tensor_key(uint64_t seed, uint64_t index) {
 struct LayerW {
     x0ne_slice input_norm, qkv, q_norm, k_norm, o, post_norm, gate_up, down;
     x0ne_slice qkv_p{}, o_p{}, gate_up_p{}, down_p{};  // the batched step's copies in 16-row panels
+    x0ne_slice router{};  // MoE: [experts][hidden]; gate_up is then [experts][2 moe_inter][hidden],
+                          // down [experts][hidden][moe_inter]
 };
 
 struct x0ne_engine {
@@ -313,6 +381,10 @@ struct x0ne_engine {
     // The batched step's rows ([max_batch][...]): f32 residual, bf16 delta, normed x, qkv,
     // attention, SwiGLU activation, f32 logits; its split-K state and counters.
     x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{}, b_argmax{};
+    // The MoE feed-forward's rows: the normed x, the router's f32 logits, each layer's chosen
+    // expert ids and weights ([layers][top_k], read back by x0ne_engine_moe_routing), the chosen
+    // experts' [gate; up] rows, activations and f32 down rows.
+    x0ne_slice m_x{}, m_logits{}, m_ids{}, m_w{}, m_gu{}, m_act{}, m_y{};
     std::vector<uint32_t> page_of;
     x0ne_split_plan split{}, bsplit{};
     uint32_t grid_qkv = 0, grid_o = 0, grid_gu = 0, grid_down = 0, grid_head = 0;
@@ -387,8 +459,14 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("k_norm", c.head_dim * 2, W, &w.k_norm));
         X0NE_TRY(al("o", c.hidden * c.q_dim() * 2, W, &w.o));
         X0NE_TRY(al("post_norm", c.hidden * 2, W, &w.post_norm));
-        X0NE_TRY(al("gate_up", 2 * c.inter * c.hidden * 2, W, &w.gate_up));
-        X0NE_TRY(al("down", c.hidden * c.inter * 2, W, &w.down));
+        if (c.moe) {
+            X0NE_TRY(al("router", c.experts * c.hidden * 2, W, &w.router));
+            X0NE_TRY(al("experts_gate_up", c.experts * 2 * c.moe_inter * c.hidden * 2, W, &w.gate_up));
+            X0NE_TRY(al("experts_down", c.experts * c.hidden * c.moe_inter * 2, W, &w.down));
+        } else {
+            X0NE_TRY(al("gate_up", 2 * c.inter * c.hidden * 2, W, &w.gate_up));
+            X0NE_TRY(al("down", c.hidden * c.inter * 2, W, &w.down));
+        }
     }
     X0NE_TRY(al("final_norm", c.hidden * 2, W, &e->final_norm));
     e->has_lm_head = !c.tied;
@@ -429,6 +507,15 @@ x0ne_status plan(x0ne_engine* e) {
     X0NE_TRY(al("attention_split_state", x0ne_split_state_bytes((uint32_t)c.q_heads, e->split.splits), CD,
                 &e->attn_state));
     X0NE_TRY(al("attention_split_counter", c.kv_heads * 4, CD, &e->attn_counter));
+    if (c.moe) {
+        X0NE_TRY(al("moe_normed", c.hidden * 2, CD, &e->m_x));
+        X0NE_TRY(al("moe_router_logits", c.experts * 4, CD, &e->m_logits));
+        X0NE_TRY(al("moe_ids", c.layers * c.top_k * 4, CD, &e->m_ids));
+        X0NE_TRY(al("moe_weights", c.layers * c.top_k * 4, CD, &e->m_w));
+        X0NE_TRY(al("moe_gate_up", c.top_k * 2 * c.moe_inter * 2, CD, &e->m_gu));
+        X0NE_TRY(al("moe_act", c.top_k * c.moe_inter * 2, CD, &e->m_act));
+        X0NE_TRY(al("moe_y", c.top_k * c.hidden * 4, CD, &e->m_y));
+    }
     if (e->chunk > 1) {
         const uint64_t n = e->chunk;
         X0NE_TRY(al("prefill_residual", n * c.hidden * 4, CD, &e->p_res));
@@ -647,11 +734,79 @@ x0ne_status launch_head(x0ne_engine* e) {
 // The launches of one decode step at the device's pos on the device's tokens[0]: forward,
 // logits, argmax into tokens[0], pos += 1. No host copy and no synchronisation, so the
 // sequence can be captured (engine.rs:495-501, :718-839).
+x0ne_status launch_rows(x0ne_engine* e, const void* fn, dim3 grid, dim3 block, void** args, const char* what);
+
+// The sparse feed-forward of layer l (engine.rs:795-815): add + RMSNorm from residual buffer 1
+// into buffer 0 (the norm the dense gate/up GEMV fuses), the router GEMV (f32 logits), the
+// routing into layer l's ids and weights, the chosen experts' [gate; up] GEMVs, SwiGLU, their
+// down GEMVs in f32, and the weighted combination into delta.
+x0ne_status launch_moe(x0ne_engine* e, uint64_t l) {
+    const Cfg& c = e->c;
+    const LayerW& w = e->L[l];
+    const uint32_t h = (uint32_t)c.hidden, ne = (uint32_t)c.experts, k = (uint32_t)c.top_k, mi = (uint32_t)c.moe_inter;
+    {
+        const void* rin = residual_buf(e, 1);
+        void* rout = residual_buf(e, 0);
+        const void* dl = e->d(e->delta);
+        const void* nw = e->d(w.post_norm);
+        void* xo = e->d(e->m_x);
+        float eps = (float)c.eps;
+        void* args[] = {(void*)&rin, (void*)&rout, (void*)&dl, (void*)&nw, (void*)&xo, (void*)&h, (void*)&eps};
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_add_rmsnorm_to_bf16, dim3(1), dim3(256), args, "moe norm"));
+    }
+    X0NE_TRY(x0ne_gpu_gemv(e->gpu, (uint64_t)(uintptr_t)e->d(w.router), c.experts, c.hidden,
+                           (uint64_t)(uintptr_t)e->d(e->m_x), 1, (uint64_t)(uintptr_t)e->d(e->m_logits), 1));
+    void* ids = e->d(e->m_ids) + l * c.top_k * 4;
+    void* wts = e->d(e->m_w) + l * c.top_k * 4;
+    {
+        const void* lg = e->d(e->m_logits);
+        void* args[] = {(void*)&lg, (void*)&ne, (void*)&k, (void*)&ids, (void*)&wts};
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_route_f32, dim3(1), dim3(128), args, "moe route"));
+    }
+    {
+        const void* wg = e->d(w.gate_up);
+        const void* x = e->d(e->m_x);
+        void* y = e->d(e->m_gu);
+        uint32_t rows = 2 * mi, cols = h, grp = k, stride = h;
+        void* args[] = {(void*)&wg, (void*)&ids, (void*)&x, (void*)&y, (void*)&rows, (void*)&cols, (void*)&ne,
+                        (void*)&grp, (void*)&stride};
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_gemv_bf16, dim3((rows + 3) / 4, k), dim3(256), args,
+                             "moe gate_up"));
+    }
+    {
+        const void* gu = e->d(e->m_gu);
+        void* act = e->d(e->m_act);
+        void* args[] = {(void*)&gu, (void*)&act, (void*)&mi};
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_swiglu_bf16, dim3((mi + 255) / 256, k), dim3(256), args,
+                             "moe swiglu"));
+    }
+    {
+        const void* wd = e->d(w.down);
+        const void* x = e->d(e->m_act);
+        void* y = e->d(e->m_y);
+        uint32_t rows = h, cols = mi, grp = 1, stride = mi;
+        void* args[] = {(void*)&wd, (void*)&ids, (void*)&x, (void*)&y, (void*)&rows, (void*)&cols, (void*)&ne,
+                        (void*)&grp, (void*)&stride};
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_gemv_f32, dim3((rows + 3) / 4, k), dim3(256), args,
+                             "moe down"));
+    }
+    const void* y = e->d(e->m_y);
+    const void* wc = wts;
+    void* out = e->d(e->delta);
+    void* args[] = {(void*)&y, (void*)&wc, (void*)&out, (void*)&h, (void*)&k};
+    return launch_rows(e, (const void*)&x0ne_moe_combine_bf16, dim3((h + 255) / 256, 1), dim3(256), args,
+                       "moe combine");
+}
+
 x0ne_status step_launches(x0ne_engine* e) {
     for (uint64_t l = 0; l < e->c.layers; ++l) {
         X0NE_TRY(launch_qkv(e, l));
         X0NE_TRY(launch_attention(e, l));
         X0NE_TRY(launch_o(e, l));
+        if (e->c.moe) {
+            X0NE_TRY(launch_moe(e, l));
+            continue;
+        }
         X0NE_TRY(launch_gate_up(e, l));
         X0NE_TRY(launch_down(e, l));
     }
@@ -945,8 +1100,10 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     e->page_seed = opts->page_seed;
     e->f64_sums = opts->f64_sums ? 1 : 0;
     // The exact mode's sums are the decode GEMV's (f64): its prompts go one step per token.
-    e->chunk = e->f64_sums ? 1
-                           : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK, opts->max_ctx);
+    // A MoE engine prefills through the decode route too (engine.rs:322-328).
+    e->chunk = e->f64_sums || c.moe
+                   ? 1
+                   : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK, opts->max_ctx);
     if (e->chunk == 0) e->chunk = 1;
     if (e->f64_sums) {
         const uint64_t grp = c.q_heads / c.kv_heads;
@@ -965,6 +1122,10 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     if (e->max_batch > 1 && e->f64_sums) {
         delete e;
         return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding with f64 sums");
+    }
+    if (c.moe && (e->max_batch > 1 || e->f64_sums)) {
+        delete e;
+        return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
     }
     e->seq_pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
     e->pages = e->max_batch * e->seq_pages;
@@ -1152,6 +1313,16 @@ extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_f
         if (at != s.len) return fail(X0NE_ERR_FORMAT, "wrote " + std::to_string(at) + " bytes into a " + std::to_string(s.len) + "-byte slice");
         return X0NE_OK;
     };
+    auto put_all = [&](x0ne_slice s, const std::vector<std::string>& names_) -> x0ne_status {
+        uint64_t at = 0;
+        for (const auto& n : names_) {
+            const TensorView& t = tensors.at(n);
+            X0NE_TRY(x0ne_arena_write(e->arena, s, at, t.data, t.len));
+            at += t.len;
+        }
+        if (at != s.len) return fail(X0NE_ERR_FORMAT, "wrote " + std::to_string(at) + " bytes into a " + std::to_string(s.len) + "-byte slice");
+        return X0NE_OK;
+    };
     x0ne_status st = put(e->embed, {"model.embed_tokens.weight"});
     for (uint64_t l = 0; l < c.layers && st == X0NE_OK; ++l) {
         const LayerW& w = e->L[l];
@@ -1161,6 +1332,18 @@ extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_f
         if ((st = put(w.k_norm, {layer_name(l, L_KN)})) != X0NE_OK) break;
         if ((st = put(w.o, {layer_name(l, L_O)})) != X0NE_OK) break;
         if ((st = put(w.post_norm, {layer_name(l, L_POST_NORM)})) != X0NE_OK) break;
+        if (c.moe) {  // weights.rs:371-389: per expert its [gate; up] rows, then the down rows
+            std::vector<std::string> gu, dn;
+            for (uint64_t x = 0; x < c.experts; ++x) {
+                gu.push_back(expert_name(l, x, "gate_proj"));
+                gu.push_back(expert_name(l, x, "up_proj"));
+                dn.push_back(expert_name(l, x, "down_proj"));
+            }
+            if ((st = put_all(w.gate_up, gu)) != X0NE_OK) break;
+            if ((st = put_all(w.down, dn)) != X0NE_OK) break;
+            st = put(w.router, {router_name(l)});
+            continue;
+        }
         if ((st = put(w.gate_up, {layer_name(l, L_GATE), layer_name(l, L_UP)})) != X0NE_OK) break;
         st = put(w.down, {layer_name(l, L_DOWN)});
     }
@@ -1310,6 +1493,7 @@ extern "C" x0ne_status x0ne_engine_load_synthetic(const char* config_json, uint6
     X0NE_TRY(parse_config(config_json, &c));
     X0NE_TRY(check_config(c, opts->max_ctx));
     if (!(std_dev > 0) || !std::isfinite(std_dev)) return fail(X0NE_ERR_FORMAT, "std is not a positive number");
+    if (c.moe) return fail(X0NE_ERR_NOT_IMPLEMENTED, "synthetic weights of a MoE model (load its checkpoint)");
     x0ne_engine* e = nullptr;
     X0NE_TRY(build_begin(c, opts, &e));
     hipStream_t s = e->gpu->stream;
@@ -2048,6 +2232,29 @@ extern "C" x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size
     return st != X0NE_OK ? st : sc;
 }
 
+// Engine::moe_routing (engine.rs:612-640): the experts every layer chose at each position of
+// ids, fed one token per step through the decode route, [position][layer][top_k] into out
+// (cap entries); *written the count (0 for a dense engine). Client bytes are scrubbed after.
+extern "C" x0ne_status x0ne_engine_moe_routing(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t* out,
+                                               size_t cap, size_t* written) {
+    if (!e || !ids || !written) return fail(X0NE_ERR_FORMAT, "null argument");
+    *written = 0;
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
+    if (e->poisoned) X0NE_TRY(scrub(e));
+    X0NE_TRY(check_ids(e, ids, n));
+    if (!e->c.moe) return X0NE_OK;
+    const size_t per = e->c.layers * e->c.top_k;
+    if (cap < n * per || !out) return fail(X0NE_ERR_FORMAT, std::to_string(n * per) + " routing entries, room for " + std::to_string(cap));
+    x0ne_status st = put_prompt(e, ids, n);
+    for (size_t p = 0; p < n && st == X0NE_OK; ++p) {
+        st = feed(e, (uint32_t)p);
+        if (st == X0NE_OK) st = x0ne_arena_read(e->arena, e->m_ids, 0, out + p * per, per * 4);
+    }
+    if (st == X0NE_OK) *written = n * per;
+    x0ne_status sc = scrub(e);
+    return st != X0NE_OK ? st : sc;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Introspection
 // ---------------------------------------------------------------------------------------------
@@ -2066,18 +2273,23 @@ extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, siz
     if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
     char gpu[512];
     x0ne_gpu_describe(e->gpu, gpu, sizeof gpu);
+    const std::string moe_text =
+        e->c.moe ? "MoE, " + std::to_string(e->c.experts) + " experts of width " + std::to_string(e->c.moe_inter) + ", " +
+                       std::to_string(e->c.top_k) + " per token (prefill through the decode route)"
+                 : std::string("dense");
     char s[1024];
     std::snprintf(s, sizeof s,
                   "%s, arena %llu bytes, decode graph %zu nodes, decode attention split-K P %u (grid %u x %u, %u q "
                   "heads per block, %u blocks per CU, merge %s), KV pages of %d positions (%llu pages, %s order), "
                   "GEMV grids qkv %u o %u gate_up %u down %u head %u (%s sums), prefill passes of %llu rows, "
-                  "batch %llu (weights %s), feed-forward dense",
+                  "batch %llu (weights %s), feed-forward %s",
                   gpu, (unsigned long long)e->arena->len, e->graph ? e->graph->nodes : (size_t)0, e->split.splits,
                   e->split.grid_x, e->split.splits, e->split.group, e->split.per_cu,
                   e->split.grouped ? "LastBlock" : "Kernel", X0NE_PAGE_C, (unsigned long long)e->pages,
                   e->page_seed ? "shuffled" : "identity", e->grid_qkv, e->grid_o, e->grid_gu, e->grid_down,
                   e->grid_head, e->f64_sums ? "f64" : "f32", (unsigned long long)e->chunk,
-                  (unsigned long long)e->max_batch, e->wpanel ? "row-major and in 16-row panels" : "row-major");
+                  (unsigned long long)e->max_batch, e->wpanel ? "row-major and in 16-row panels" : "row-major",
+                  moe_text.c_str());
     if (buf && len) {
         std::strncpy(buf, s, len - 1);
         buf[len - 1] = 0;

@@ -74,6 +74,8 @@ __global__ void x0ne_argmax_pick_advance(const uint32_t* partial, uint32_t slice
 __global__ void x0ne_embed_rmsnorm_panel_bf16(const bf16_t* table, const uint32_t* tokens, float* residual,
                                               const bf16_t* w, bf16_t* out, uint32_t hidden, uint32_t vocab,
                                               float eps);
+__global__ void x0ne_add_rmsnorm_to_bf16(const float* res_in, float* res_out, const bf16_t* x, const bf16_t* w,
+                                         bf16_t* out, uint32_t hidden, float eps);
 __global__ void x0ne_add_rmsnorm_panel_bf16(float* residual, const bf16_t* x, const bf16_t* w, bf16_t* out,
                                             uint32_t hidden, float eps);
 __global__ void x0ne_advance_u32(uint32_t* pos);

@@ -103,6 +103,22 @@ extern "C" __global__ void __launch_bounds__(256)
                 hidden, eps);
 }
 
+// x0ne_add_rmsnorm_bf16 with the residual read from res_in and the sum written to res_out (the
+// decode step's two residual buffers, which the MoE feed-forward keeps: the GEMV prologues read
+// one and write the other). The same arithmetic as x0ne_add_rmsnorm_bf16. grid (rows), block 256;
+// res_in and res_out must not overlap.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_add_rmsnorm_to_bf16(const float* __restrict__ res_in, float* __restrict__ res_out,
+                             const bf16_t* __restrict__ x, const bf16_t* __restrict__ w, bf16_t* __restrict__ out,
+                             uint32_t hidden, float eps) {
+    const size_t base = (size_t)blockIdx.x * hidden;
+    const float* ri = res_in + base;
+    const bf16_t* xr = x + base;
+    bf16_t* o = out + base;
+    rmsnorm_row(res_out + base, [&](uint32_t i) { return ri[i] + bf2f(xr[i]); }, w,
+                [&](uint32_t i) -> bf16_t& { return o[i]; }, hidden, eps);
+}
+
 // x0ne_add_rmsnorm_bf16 with out in panels (hidden a multiple of 8): the batched step's norms,
 // whose rows feed the few-row GEMM. The same bits at the panel positions. grid (rows), block 256.
 extern "C" __global__ void __launch_bounds__(256)

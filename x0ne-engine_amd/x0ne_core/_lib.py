@@ -148,6 +148,7 @@ SIGNATURES = {
     "x0ne_engine_set_decode_mode": ([P, U32], ST),
     "x0ne_engine_decode_mode": ([P], U32),
     "x0ne_engine_logits_at": ([P, C.POINTER(U32), SZ, C.POINTER(SZ), SZ, U32, C.POINTER(F32)], ST),
+    "x0ne_engine_moe_routing": ([P, C.POINTER(U32), SZ, C.POINTER(U32), SZ, C.POINTER(SZ)], ST),
     "x0ne_engine_run": ([P, C.POINTER(U32), SZ, U32, C.POINTER(SZ), SZ, C.POINTER(PosStatsC), C.POINTER(F32)], ST),
     "x0ne_engine_describe": ([P, C.c_char_p, SZ], ST),
     "x0ne_engine_graph_nodes": ([P], SZ),

@@ -208,6 +208,18 @@ class Engine:
             out[i] = (stats[i].argmax, stats[i].logsumexp, stats[i].next_logprob)
         return out, [rows[i] for i in range(kp.size)]
 
+    def moe_routing(self, ids) -> np.ndarray:
+        """Engine::moe_routing (engine.rs:612-640): [position][layer][top_k] expert ids, flattened
+        (empty for a dense engine)."""
+        a, p = _ids(ids)
+        c = self.config
+        per = int(c.get("num_hidden_layers", 0)) * int(c.get("num_experts_per_tok", 0))
+        out = np.zeros(max(1, a.size * per), np.uint32)
+        n = C.c_size_t(0)
+        check(lib().x0ne_engine_moe_routing(self.h, p, a.size, out.ctypes.data_as(C.POINTER(C.c_uint32)), out.size,
+                                            C.byref(n)), "moe_routing")
+        return out[:n.value].copy()
+
     def stats(self, ids, route: Route = Route.DECODE):
         """Engine::stats (engine.rs:1003-1006)."""
         return self.run(ids, route)[0]
