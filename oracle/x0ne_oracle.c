@@ -1,5 +1,6 @@
 /*
- * CPU oracle of x0ne Core's Qwen3 dense bf16 decode path. TEST INFRASTRUCTURE, NOT PRODUCT:
+ * CPU oracle of x0ne Core's Qwen3 bf16 decode path (the dense forward, and the Qwen3-MoE block's
+ * routing, expert GEMVs and combination). TEST INFRASTRUCTURE, NOT PRODUCT:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
  *
  * Restates x0ne-core/oracle/src/{bf16,lib,model}.rs operation for operation: f64 inside, the
