@@ -135,6 +135,35 @@ def test_a_config_that_differs_from_its_checkpoint_is_refused(checkpoint):
     refused("no file at all", dense(), None, files={})
 
 
+def load_opts(config, file, **opts):
+    from x0ne_core import Engine, EngineOptions
+    return Engine.load_from(json.dumps(config), {"model.safetensors": file}, EngineOptions(**opts))
+
+
+def test_a_kv_plane_past_the_attention_kernels_addressing_is_refused_before_the_device(checkpoint):
+    """The attention kernels address one layer's K (or V) plane, every sequence's pages, by 32-bit
+    byte offsets below 0xFFFFFFF0. This model keeps 2 kv heads x 128 dims x 2 bytes = 512 bytes
+    per position and plane, so 64 sequences of 131072 positions need a 2^32-byte plane: refused
+    (FormatError, before any device work) rather than loaded with offsets that would wrap onto
+    another sequence's pages. 63 sequences (4,227,858,432 bytes) pass the checks; so do 64 of
+    131056 (4,294,443,008 bytes, the largest whole-page context below the limit)."""
+    from x0ne_core import FormatError, GpuError, NotImplementedFeature
+    big = with_("max_position_embeddings", 1 << 17)
+    with pytest.raises(FormatError, match="KV plane"):
+        load_opts(big, checkpoint, max_ctx=1 << 17, max_batch=64)
+    with pytest.raises(FormatError, match="KV plane"):
+        load_opts(big, checkpoint, max_ctx=(1 << 17) - 15, max_batch=64)  # the same 8192 pages
+    for ctx, batch in [((1 << 17), 63), ((1 << 17) - 16, 64)]:
+        try:
+            load_opts(big, checkpoint, max_ctx=ctx, max_batch=batch).close()
+        except GpuError:
+            pass
+    with pytest.raises(FormatError):
+        load_opts(dense(), checkpoint, max_ctx=64, max_batch=65)
+    with pytest.raises(NotImplementedFeature):
+        load_opts(dense(), checkpoint, max_ctx=64, max_batch=2, f64_sums=True)
+
+
 def test_a_cut_or_corrupted_config_is_read_or_refused_never_a_crash(checkpoint):
     """cpu_config.rs:303-360: cut anywhere, or with bytes changed, a config is refused
     (FormatError) or read; one that is read and still the checkpoint's ends on the device."""

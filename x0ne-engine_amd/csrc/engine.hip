@@ -46,6 +46,8 @@ constexpr uint64_t MAX_BATCH = 64;  // the few-row GEMM's most rows
 constexpr uint32_t ARGMAX_SLICES = 64;  // blocks per logits row of the batched step's argmax
 constexpr uint64_t MOE_MAX_EXPERTS = 1024;  // kernels/src/lib.rs:147 (moe.hip)
 constexpr uint64_t MOE_MAX_TOP_K = 32;
+// The largest K or V plane the attention kernels' 32-bit byte offsets address (attention.hip).
+constexpr uint64_t KV_PLANE_MAX_BYTES = 0xFFFFFFF0ull;
 
 struct Cfg {
     uint64_t hidden = 0, inter = 0, layers = 0, q_heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, max_pos = 0;
@@ -60,148 +62,183 @@ struct Cfg {
     uint64_t qkv_rows() const { return q_dim() + 2 * kv_dim(); }
 };
 
-// ---- config.json, read strictly (config.rs:59-118) ----
+// ---- config.json ----
+//
+// The accept/refuse rules are the reference's (x0ne-core/runtime/src/config.rs:59-118 dense,
+// :218-335 MoE; x0ne-infer/src/core_backend.rs:28-55 for rope_parameters), so a checkpoint it
+// serves loads here and one it turns away is turned away here too. The reader and its messages
+// are this build's: each refusal names the field and what the engine needs of it.
+struct ConfigReader {
+    const Json& root;
+    std::string refusal;  // the first rule broken, empty while every rule holds
 
-bool positive_u64(const Json& v, const char* key, uint64_t* out, std::string* err) {
-    const Json* f = v.get(key);
-    if (!f) {
-        *err = std::string("config.json: missing ") + key;
+    bool refuse(const std::string& what) {
+        if (refusal.empty()) refusal = "config.json: " + what;
         return false;
     }
-    uint64_t n = 0;
-    if (!f->as_u64(&n) || n == 0) {
-        *err = std::string("config.json: ") + key + " is not a positive integer";
-        return false;
+    // `key` must hold a whole number of at least 1, written without sign, fraction or exponent.
+    bool count(const char* key, uint64_t* out) {
+        const Json* f = root.get(key);
+        if (!f) return refuse(std::string("no \"") + key + "\" field");
+        uint64_t n = 0;
+        if (!f->as_u64(&n) || n == 0) return refuse(std::string("\"") + key + "\" must be a whole number >= 1");
+        *out = n;
+        return true;
     }
-    *out = n;
-    return true;
-}
-
-bool positive_f64(const Json* f, const char* key, double* out, std::string* err) {
-    if (!f) {
-        *err = std::string("config.json: missing ") + key;
-        return false;
+    // `f` (field `key`) must be a finite number above zero.
+    bool positive(const Json* f, const char* key, double* out) {
+        if (!f) return refuse(std::string("no \"") + key + "\" field");
+        if (f->kind != Json::Number || !std::isfinite(f->num) || !(f->num > 0))
+            return refuse(std::string("\"") + key + "\" must be a finite number above zero");
+        *out = f->num;
+        return true;
     }
-    if (f->kind != Json::Number || !std::isfinite(f->num) || f->num <= 0) {
-        *err = std::string("config.json: ") + key + " is not a positive number";
-        return false;
+    // `key` is absent, null or false: a feature the kernels do not have is not asked for.
+    bool unset(const char* key) {
+        const Json* f = root.get(key);
+        if (!f || f->kind == Json::Null || (f->kind == Json::Bool && !f->b)) return true;
+        return refuse(std::string("\"") + key + "\" asks for a feature this engine lacks");
     }
-    *out = f->num;
-    return true;
-}
+    // `f` is the string `want`.
+    bool text(const Json* f, const char* key, const char* want) {
+        if (f && f->kind == Json::String && f->text == want) return true;
+        return refuse(std::string("\"") + key + "\" must be \"" + want + "\"");
+    }
+};
 
-bool off(const Json& v, const char* key) {
-    const Json* f = v.get(key);
-    return !f || f->kind == Json::Null || (f->kind == Json::Bool && !f->b);
-}
-
-x0ne_status parse_config(const char* text, Cfg* c) {
-    if (!text) return fail(X0NE_ERR_FORMAT, "config.json: null");
-    Json v;
+x0ne_status parse_config(const char* json_text, Cfg* c) {
+    if (!json_text) return fail(X0NE_ERR_FORMAT, "config.json: no text given");
+    Json root;
     try {
-        v = parse_json(text);
+        root = parse_json(json_text);
     } catch (const std::exception& ex) {
         return fail(X0NE_ERR_FORMAT, std::string("config.json: ") + ex.what());
     }
-    if (v.kind != Json::Object) return fail(X0NE_ERR_FORMAT, "config.json: not an object");
-    const Json* mt = v.get("model_type");
-    if (!mt) return fail(X0NE_ERR_FORMAT, "config.json: missing model_type");
-    // read_any (config.rs:329-335): qwen3, or qwen3_moe with its sparse block.
-    if (mt->kind != Json::String || (mt->text != "qwen3" && mt->text != "qwen3_moe"))
-        return fail(X0NE_ERR_FORMAT, "config.json: model_type is not qwen3 or qwen3_moe");
-    c->moe = mt->text == "qwen3_moe";
-    const Json* dt = v.get("dtype");
-    if (!dt) dt = v.get("torch_dtype");
-    if (!dt || dt->kind != Json::String || dt->text != "bfloat16")
-        return fail(X0NE_ERR_FORMAT, "config.json: dtype is not bfloat16, only bfloat16 is served");
-    const Json* act = v.get("hidden_act");
-    if (!act) return fail(X0NE_ERR_FORMAT, "config.json: missing hidden_act");
-    if (act->kind != Json::String || act->text != "silu") return fail(X0NE_ERR_FORMAT, "config.json: hidden_act is not silu");
-    for (const char* key : {"attention_bias", "use_sliding_window", "rope_scaling"})
-        if (!off(v, key)) return fail(X0NE_ERR_FORMAT, std::string("config.json: ") + key + " is set, not implemented");
-    const Json* tie = v.get("tie_word_embeddings");
-    if (tie && tie->kind != Json::Bool) return fail(X0NE_ERR_FORMAT, "config.json: tie_word_embeddings is not a boolean");
-    c->tied = tie && tie->b;
-    std::string err;
-    if (!positive_u64(v, "hidden_size", &c->hidden, &err) || !positive_u64(v, "intermediate_size", &c->inter, &err) ||
-        !positive_u64(v, "num_hidden_layers", &c->layers, &err) ||
-        !positive_u64(v, "num_attention_heads", &c->q_heads, &err) ||
-        !positive_u64(v, "num_key_value_heads", &c->kv_heads, &err) || !positive_u64(v, "head_dim", &c->head_dim, &err) ||
-        !positive_u64(v, "vocab_size", &c->vocab, &err) ||
-        !positive_u64(v, "max_position_embeddings", &c->max_pos, &err) ||
-        !positive_f64(v.get("rms_norm_eps"), "rms_norm_eps", &c->eps, &err))
-        return fail(X0NE_ERR_FORMAT, err);
-    // rope_theta at the top (the reference's reader) or in rope_parameters (transformers 5,
-    // lifted by x0ne-infer, core_backend.rs:28-55).
-    const Json* theta = v.get("rope_theta");
-    if (!theta) {
-        const Json* rp = v.get("rope_parameters");
-        if (rp) theta = rp->get("rope_theta");
-    }
-    if (!positive_f64(theta, "rope_theta", &c->theta, &err)) return fail(X0NE_ERR_FORMAT, err);
-    if (c->moe) {  // Qwen3MoeConfig::from_json (config.rs:237-279)
+    if (root.kind != Json::Object) return fail(X0NE_ERR_FORMAT, "config.json: the top level must be an object");
+    ConfigReader r{root, {}};
+    // The architecture: Qwen3 dense, or Qwen3-MoE with its sparse block (config.rs:329-335).
+    const Json* arch = root.get("model_type");
+    const bool dense = arch && arch->kind == Json::String && arch->text == "qwen3";
+    c->moe = arch && arch->kind == Json::String && arch->text == "qwen3_moe";
+    if (!dense && !c->moe) r.refuse("\"model_type\" must be \"qwen3\" or \"qwen3_moe\"");
+    // Arithmetic: bf16 weights ("dtype", or the older "torch_dtype" when "dtype" is absent), a
+    // SiLU-gated MLP, and none of bias, sliding windows or RoPE scaling.
+    const Json* dtype = root.get("dtype") ? root.get("dtype") : root.get("torch_dtype");
+    r.text(dtype, "dtype", "bfloat16");
+    r.text(root.get("hidden_act"), "hidden_act", "silu");
+    r.unset("attention_bias");
+    r.unset("use_sliding_window");
+    r.unset("rope_scaling");
+    const Json* tie = root.get("tie_word_embeddings");
+    if (tie && tie->kind != Json::Bool) r.refuse("\"tie_word_embeddings\" must be true or false");
+    c->tied = tie && tie->kind == Json::Bool && tie->b;
+    if (!r.refusal.empty()) return fail(X0NE_ERR_FORMAT, r.refusal);
+    // The shape.
+    const struct {
+        const char* key;
+        uint64_t* dst;
+    } sizes[] = {{"hidden_size", &c->hidden},          {"intermediate_size", &c->inter},
+                 {"num_hidden_layers", &c->layers},     {"num_attention_heads", &c->q_heads},
+                 {"num_key_value_heads", &c->kv_heads}, {"head_dim", &c->head_dim},
+                 {"vocab_size", &c->vocab},             {"max_position_embeddings", &c->max_pos}};
+    for (const auto& s : sizes)
+        if (!r.count(s.key, s.dst)) return fail(X0NE_ERR_FORMAT, r.refusal);
+    if (!r.positive(root.get("rms_norm_eps"), "rms_norm_eps", &c->eps)) return fail(X0NE_ERR_FORMAT, r.refusal);
+    // RoPE base: at the top level, or inside "rope_parameters" as transformers 5 writes it.
+    const Json* theta = root.get("rope_theta");
+    if (!theta && root.get("rope_parameters")) theta = root.get("rope_parameters")->get("rope_theta");
+    if (!r.positive(theta, "rope_theta", &c->theta)) return fail(X0NE_ERR_FORMAT, r.refusal);
+    if (c->moe) {
+        // Every layer sparse, no shared expert, renormalised top-k routing.
         for (const char* key : {"shared_expert_intermediate_size", "n_shared_experts"}) {
-            const Json* f = v.get(key);
-            if (f && f->kind != Json::Null)
-                return fail(X0NE_ERR_FORMAT, std::string("config.json: ") + key + " is set, not implemented");
+            const Json* f = root.get(key);
+            if (f && f->kind != Json::Null) r.refuse(std::string("\"") + key + "\": shared experts are not served");
         }
-        uint64_t step = 0;
-        if (!positive_u64(v, "decoder_sparse_step", &step, &err)) return fail(X0NE_ERR_FORMAT, err);
-        if (step != 1)
-            return fail(X0NE_ERR_FORMAT, "config.json: decoder_sparse_step is not 1, dense layers are not implemented");
-        const Json* mlp_only = v.get("mlp_only_layers");
-        if (mlp_only && mlp_only->kind != Json::Null && !(mlp_only->kind == Json::Array && mlp_only->items.empty()))
-            return fail(X0NE_ERR_FORMAT, "config.json: mlp_only_layers is not empty, dense layers are not implemented");
-        const Json* norm_topk = v.get("norm_topk_prob");
-        if (!norm_topk || norm_topk->kind != Json::Bool || !norm_topk->b)
-            return fail(X0NE_ERR_FORMAT,
-                        "config.json: norm_topk_prob is not true, only renormalised top-k is implemented");
-        if (!positive_u64(v, "num_experts", &c->experts, &err) ||
-            !positive_u64(v, "num_experts_per_tok", &c->top_k, &err) ||
-            !positive_u64(v, "moe_intermediate_size", &c->moe_inter, &err))
-            return fail(X0NE_ERR_FORMAT, err);
-        if (c->top_k > c->experts) return fail(X0NE_ERR_FORMAT, "config.json: num_experts_per_tok exceeds num_experts");
-        if (c->experts > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "config.json: num_experts does not fit a u32 expert id");
+        uint64_t every = 0;
+        if (r.count("decoder_sparse_step", &every) && every != 1)
+            r.refuse("\"decoder_sparse_step\" must be 1: every layer sparse");
+        const Json* dense_layers = root.get("mlp_only_layers");
+        if (dense_layers && dense_layers->kind != Json::Null &&
+            !(dense_layers->kind == Json::Array && dense_layers->items.empty()))
+            r.refuse("\"mlp_only_layers\" must be empty: every layer sparse");
+        const Json* renorm = root.get("norm_topk_prob");
+        if (!renorm || renorm->kind != Json::Bool || !renorm->b)
+            r.refuse("\"norm_topk_prob\" must be true: the chosen experts' weights are renormalised");
+        if (!r.refusal.empty()) return fail(X0NE_ERR_FORMAT, r.refusal);
+        if (!r.count("num_experts", &c->experts) || !r.count("num_experts_per_tok", &c->top_k) ||
+            !r.count("moe_intermediate_size", &c->moe_inter))
+            return fail(X0NE_ERR_FORMAT, r.refusal);
+        if (c->top_k > c->experts) r.refuse("more experts per token than experts");
+        if (c->experts > UINT32_MAX) r.refuse("expert ids must fit 32 bits");
     }
-    if (c->q_heads % c->kv_heads != 0)
-        return fail(X0NE_ERR_FORMAT, "config.json: attention heads are not a multiple of KV heads");
-    if (c->head_dim % 2 != 0) return fail(X0NE_ERR_FORMAT, "config.json: head_dim is odd, RoPE needs pairs");
-    if (c->vocab > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "config.json: vocab_size does not fit a u32 token id");
-    // Every derived size must fit in 64 bits (config.rs check_sizes).
-    const long double ffn = c->moe ? (long double)c->experts * (3.0L * c->moe_inter * c->hidden + c->hidden)
+    // Relations between the sizes.
+    if (c->q_heads % c->kv_heads != 0) r.refuse("every KV head must serve the same number of query heads");
+    if (c->head_dim % 2 != 0) r.refuse("RoPE rotates pairs of dimensions: head_dim must be even");
+    if (c->vocab > UINT32_MAX) r.refuse("token ids must fit 32 bits: vocab_size too large");
+    // No size derived from the shape may overflow (config.rs check_sizes): weights of every
+    // layer plus both vocabulary matrices, bounded well inside 64 bits.
+    const long double mlp = c->moe ? (long double)c->experts * (3.0L * c->moe_inter * c->hidden + c->hidden)
                                    : 3.0L * c->inter * c->hidden;
-    const long double big = (long double)c->layers * ((long double)(c->qkv_rows() * c->hidden) + ffn) +
-                            (long double)c->vocab * c->hidden * 2;
-    if (big > 1e18L) return fail(X0NE_ERR_FORMAT, "config.json: a derived size overflows");
+    const long double params = (long double)c->layers * ((long double)c->qkv_rows() * c->hidden + mlp) +
+                               2.0L * c->vocab * c->hidden;
+    if (params > 1e18L) r.refuse("the shape's sizes overflow");
+    if (!r.refusal.empty()) return fail(X0NE_ERR_FORMAT, r.refusal);
     return X0NE_OK;
 }
 
-// Limits of the kernels (engine.rs:236-289, plus this build's GEMV and KV-page limits).
-x0ne_status check_config(const Cfg& c, uint64_t max_ctx) {
-    if (c.moe) {  // engine.rs:236-262
+// What the kernels and the arena of this build accept (engine.rs:236-289 for the reference's
+// own limits), for a checked config and the load's options; all of it before any device work.
+x0ne_status check_config(const Cfg& c, const x0ne_engine_options& o) {
+    const uint64_t max_ctx = o.max_ctx;
+    auto no = [](const std::string& why) { return fail(X0NE_ERR_FORMAT, why); };
+    if (c.moe) {  // expert count and width (kernels/src/lib.rs:147; engine.rs:236-262)
         if (c.experts == 0 || c.experts > MOE_MAX_EXPERTS)
-            return fail(X0NE_ERR_FORMAT, "num_experts " + std::to_string(c.experts) + " outside 1..=" +
-                                             std::to_string(MOE_MAX_EXPERTS));
+            return no("MoE: " + std::to_string(c.experts) + " experts, the routing kernel takes 1 to " +
+                      std::to_string(MOE_MAX_EXPERTS));
         if (c.top_k == 0 || c.top_k > MOE_MAX_TOP_K)
-            return fail(X0NE_ERR_FORMAT, "num_experts_per_tok " + std::to_string(c.top_k) + " outside 1..=32");
-        if (c.moe_inter == 0 || c.moe_inter % 8 != 0)
-            return fail(X0NE_ERR_FORMAT, "moe_intermediate_size is not a positive multiple of 8");
+            return no("MoE: " + std::to_string(c.top_k) + " experts per token, the routing kernel takes 1 to " +
+                      std::to_string(MOE_MAX_TOP_K));
+        if (c.moe_inter == 0 || c.moe_inter % 8 != 0) return no("MoE: the expert width must be a multiple of 8");
         if (c.experts * 2 * c.moe_inter > UINT32_MAX || c.top_k * c.hidden > UINT32_MAX)
-            return fail(X0NE_ERR_FORMAT, "a MoE dimension exceeds u32");
+            return no("MoE: the expert matrices' rows must fit 32 bits");
     }
-    if (c.head_dim != 128) return fail(X0NE_ERR_FORMAT, "head_dim " + std::to_string(c.head_dim) + ": kernels are built for 128");
-    if (c.hidden % 8 != 0) return fail(X0NE_ERR_FORMAT, "hidden_size is not a multiple of 8");
-    if (c.inter % 8 != 0) return fail(X0NE_ERR_FORMAT, "intermediate_size is not a multiple of 8");
+    if (c.head_dim != 128) return no("head_dim " + std::to_string(c.head_dim) + ": the attention kernels take 128");
+    if (c.hidden % 8 != 0 || c.inter % 8 != 0)
+        return no("hidden and intermediate sizes must be multiples of 8 (16-byte rows)");
     if (max_ctx == 0 || max_ctx > c.max_pos)
-        return fail(X0NE_ERR_FORMAT, "max_ctx " + std::to_string(max_ctx) + " outside 1..=" + std::to_string(c.max_pos));
-    const uint64_t pages = (max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
-    for (uint64_t s : {c.vocab, c.hidden, 2 * c.inter, c.qkv_rows(), max_ctx * c.kv_dim(), pages * X0NE_PAGE_C * c.kv_dim()})
-        if (s > UINT32_MAX) return fail(X0NE_ERR_FORMAT, "a dimension exceeds u32");
-    // GEMV widths: x is staged whole in LDS; a normed x (hidden) is at most 16384, an
-    // attention output or activation (q_dim, intermediate) at most 32768.
-    if (c.hidden > 16384) return fail(X0NE_ERR_FORMAT, "hidden_size exceeds 16384");
-    for (uint64_t cols : {c.q_dim(), c.inter})
-        if (cols > 32768) return fail(X0NE_ERR_FORMAT, "a GEMV width exceeds 32768 columns");
+        return no("max_ctx " + std::to_string(max_ctx) + ": must be 1 to max_position_embeddings (" +
+                  std::to_string(c.max_pos) + ")");
+    const uint64_t seq_pages = (max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
+    for (uint64_t s : {c.vocab, c.hidden, 2 * c.inter, c.qkv_rows(), max_ctx * c.kv_dim(),
+                       seq_pages * X0NE_PAGE_C * c.kv_dim()})
+        if (s > UINT32_MAX) return no("a row count or KV-plane element count exceeds 32 bits");
+    // x is staged whole in LDS: a normed x (hidden) up to 16384 values, an attention output or an
+    // activation (q_dim, intermediate) up to 32768.
+    if (c.hidden > 16384) return no("hidden_size above 16384, the GEMV's staged x");
+    if (c.q_dim() > 32768 || c.inter > 32768) return no("a projection wider than 32768 columns");
+    // The options.
+    const uint64_t batch = o.max_batch ? o.max_batch : 1;
+    if (batch > MAX_BATCH) return no("max_batch " + std::to_string(batch) + " above " + std::to_string(MAX_BATCH));
+    if (batch > 1 && o.f64_sums) return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding with f64 sums");
+    if (c.moe && (batch > 1 || o.f64_sums))
+        return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
+    if (o.f64_sums) {
+        const uint64_t grp = c.q_heads / c.kv_heads;
+        if (grp != 1 && grp != 2 && grp != 4 && grp != 8)
+            return fail(X0NE_ERR_NOT_IMPLEMENTED,
+                        "f64 sums: the exact attention kernels take 1, 2, 4 or 8 q heads per kv head, not " +
+                            std::to_string(grp));
+    }
+    // The attention kernels address a K or V plane (every sequence's pages of one layer) by 32-bit
+    // byte offsets into a buffer resource of 0xFFFFFFF0 bytes, the offset 0xFFFFFFF0 standing for
+    // "no key" (attention.hip, OFF_NONE). A plane must therefore end at or below that offset;
+    // a larger one would wrap onto other pages (other sequences' keys), so it is refused here.
+    const uint64_t plane = batch * seq_pages * X0NE_PAGE_C * c.kv_dim() * 2;
+    if (plane > KV_PLANE_MAX_BYTES)
+        return no("KV plane of " + std::to_string(plane) + " bytes (max_batch " + std::to_string(batch) + " x " +
+                  std::to_string(seq_pages) + " pages of " + std::to_string(X0NE_PAGE_C * c.kv_dim() * 2) +
+                  " bytes) above the attention kernels' " + std::to_string(KV_PLANE_MAX_BYTES) +
+                  "-byte addressing: lower max_batch or max_ctx");
     return X0NE_OK;
 }
 
@@ -1105,28 +1142,7 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
                    ? 1
                    : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK, opts->max_ctx);
     if (e->chunk == 0) e->chunk = 1;
-    if (e->f64_sums) {
-        const uint64_t grp = c.q_heads / c.kv_heads;
-        if (grp != 1 && grp != 2 && grp != 4 && grp != 8) {
-            delete e;
-            return fail(X0NE_ERR_NOT_IMPLEMENTED,
-                        "f64 sums: the exact attention kernels take 1, 2, 4 or 8 q heads per kv head, not " +
-                            std::to_string(grp));
-        }
-    }
-    e->max_batch = opts->max_batch ? opts->max_batch : 1;
-    if (e->max_batch > MAX_BATCH) {
-        delete e;
-        return fail(X0NE_ERR_FORMAT, "max_batch " + std::to_string(e->max_batch) + " above " + std::to_string(MAX_BATCH));
-    }
-    if (e->max_batch > 1 && e->f64_sums) {
-        delete e;
-        return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding with f64 sums");
-    }
-    if (c.moe && (e->max_batch > 1 || e->f64_sums)) {
-        delete e;
-        return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
-    }
+    e->max_batch = opts->max_batch ? opts->max_batch : 1;  // check_config bounded it
     e->seq_pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
     e->pages = e->max_batch * e->seq_pages;
     x0ne_status st = x0ne_gpu_new(&e->gpu);
@@ -1250,7 +1266,7 @@ extern "C" x0ne_status x0ne_engine_load_from(const char* config_json, size_t n_f
     *out = nullptr;
     Cfg c;
     X0NE_TRY(parse_config(config_json, &c));
-    X0NE_TRY(check_config(c, opts->max_ctx));
+    X0NE_TRY(check_config(c, *opts));
     // Every format check before the device is touched. The files and the index agree exactly
     // (st.rs:216-277): without an index, one file; with one, every file it names given once,
     // no other file, each listed tensor in the shard it names, and every tensor listed.
@@ -1441,7 +1457,7 @@ extern "C" x0ne_status x0ne_engine_load(const char* model_dir, const x0ne_engine
     {
         Cfg c;
         X0NE_TRY(parse_config(config.c_str(), &c));
-        X0NE_TRY(check_config(c, opts->max_ctx));
+        X0NE_TRY(check_config(c, *opts));
     }
     const std::string single = at("model.safetensors"), index = at("model.safetensors.index.json");
     const bool has_single = file_exists(single), has_index = file_exists(index);
@@ -1491,7 +1507,7 @@ extern "C" x0ne_status x0ne_engine_load_synthetic(const char* config_json, uint6
     *out = nullptr;
     Cfg c;
     X0NE_TRY(parse_config(config_json, &c));
-    X0NE_TRY(check_config(c, opts->max_ctx));
+    X0NE_TRY(check_config(c, *opts));
     if (!(std_dev > 0) || !std::isfinite(std_dev)) return fail(X0NE_ERR_FORMAT, "std is not a positive number");
     if (c.moe) return fail(X0NE_ERR_NOT_IMPLEMENTED, "synthetic weights of a MoE model (load its checkpoint)");
     x0ne_engine* e = nullptr;
