@@ -460,13 +460,17 @@ def test_batched_attention_is_each_sequence_alone_bit_for_bit(kernels, qh, kvh):
 def test_exact_attention_is_the_f64_oracle_bit_for_bit(kernels, qh, kvh):
     """The exact mode's fused attention (f64 scores, softmax and sums) gives the bits of the f64
     oracle's attention rounded f64 -> f32 -> bf16, on the q and K/V row its own QK-norm/RoPE
-    produced (which are the QK-norm/RoPE kernel's bits)."""
+    produced (which are the QK-norm/RoPE kernel's bits): at the engine's split plan and at split
+    factors 1, 4 and 16 (f64 slice states merged by the last block in a fixed order), over pages
+    in a shuffled order, up to 8192 keys."""
     from x0ne_core.ops import CacheAt
     h = H(qh, kvh)
     rng = O.Rng(490 + qh)
     theta, eps = 1e6, 1e-6
     total = differ = 0
-    for ctx in [1, 2, 17, 64, 65, 256, 257, 1000, 4097]:
+    cases = [(ctx, None) for ctx in [1, 2, 17, 64, 65, 256, 257, 1000, 4097]]
+    cases += [(ctx, p) for ctx in [300, 2049, 8192] for p in (1, 4, 16)]
+    for ctx, splits in cases:
         qkv = rng.bf16s(h.q_dim + 2 * h.kv_dim, 3.0)
         qn, kn = rng.bf16s(128, 1.5), rng.bf16s(128, 1.5)
         k = rng.bf16s((ctx - 1) * h.kv_dim, 1.0)
@@ -478,7 +482,7 @@ def test_exact_attention_is_the_f64_oracle_bit_for_bit(kernels, qh, kvh):
                                              CacheAt(1, ctx, 0, ctx - 1))
         out, k_row, v_row = kernels.attention_rope_decode(bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), eps, theta,
                                                           bf16_bits(k), bf16_bits(v), ctx, h, page_of=page_of,
-                                                          exact=True)
+                                                          exact=True, splits=splits)
         assert (k_row == rope.k_row).all() and (v_row == rope.v_row).all(), f"ctx {ctx}: the K/V row"
         kb = np.concatenate([bf16_bits(k), rope.k_row])
         vb = np.concatenate([bf16_bits(v), rope.v_row])

@@ -719,45 +719,391 @@ __device__ __forceinline__ void stash_wave(AttnShared<G, T>& sh, const T m[G], c
     }
 }
 
-// The exact mode's block (kv head kh, the whole context, P = 1): QK-norm + RoPE of the G q heads
-// and the K/V write of position pos, then scalar f64 scores, softmax and sums, scaled by
-// 1/sqrt(128) in f64 as the f64 oracle does, and the output.
+// ---- the exact mode (f64 scores, softmax and sums) ----
+//
+// The exact mode follows the f64 oracle's arithmetic (oracle/src/lib.rs:149-176): scores are
+// exact bf16 x bf16 products summed in f64 and scaled by the f64 1/sqrt(128), the softmax and
+// the weighted V sums are f64, and the result is rounded f64 -> f32 -> bf16. Only the order of
+// the f64 additions differs from the oracle's, which moves a result by about 1e-16 relative:
+// far below the bf16 rounding step the outputs are compared at.
+//
+// The work unit is one 16-key page of one kv head (4 KiB of K rows and 4 KiB of dim-major V).
+// Slices are the split-K slices of the fp32 kernels (split_of: runs of 64-key tiles, P of them);
+// inside a slice the 4 wavefronts take its pages in turn (wavefront w: pages w, w + 4, ...), so a
+// short context spreads over every wavefront of the block. Lanes of a page: for the scores lane
+// (k = l % 16, c = l / 16) holds key k's dims 32c .. 32c + 31 and sums them against the G q heads
+// (f64 FMAs), the four quarters then meet by shuffles; for the weighted sums lane l owns dims l
+// and l + 64 and reads the page's 16 weights per head from LDS. The next page's K and V are in
+// flight while a page is summed, and slice 0 requests its first page-table entry together with
+// pos, so the dependent chain of a short context is pos/page -> K,V -> sums.
+
+// The page split of a slice: pages p_begin, p_begin + 4, ... of the slice's run, below npages.
+struct ExactShared {
+    // q heads, bf16-rounded, as f64; the page weights and rescale factors per wavefront; the
+    // new K/V row; the block merge's states; the last block's slice factors.
+    double qd[8][X0NE_HEAD_DIM];
+    double pw[WAVES][8][X0NE_PAGE];
+    double alpha[WAVES][8];
+    alignas(16) bf16_t knew[X0NE_HEAD_DIM], vnew[X0NE_HEAD_DIM];
+    double wm[WAVES][8], wl[WAVES][8];
+    double wo[WAVES][8][X0NE_HEAD_DIM];
+    double wf[WAVES][8], mh[8], lh[8];
+    double f[WAVES][MERGE_MAX];
+    uint32_t last;
+};
+
+__device__ __forceinline__ void dstate_put(double* p, double v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double dstate_get(const double* p) {
+    return __hip_atomic_load(const_cast<double*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum over the 4 lane quarters (lane bits 4 and 5) of a G-vector of per-quarter partial dot
+// products. While more than one value is left a step keeps half of them (bit set: the upper
+// half); afterwards plain butterflies. Lane (k, c) ends with the whole score of head
+// quarter_head<G>(c, e) in v[e], e < max(G / 4, 1).
+template <int N, int K>
+__device__ __forceinline__ void quarter_reduce(double* v, uint32_t lane) {
+    if constexpr (K < 4) {
+        return;
+    } else if constexpr (N > 1) {
+        constexpr int H = N / 2;
+        const bool bit = (lane >> K) & 1u;
+#pragma unroll
+        for (int j = 0; j < H; ++j) {
+            const double send = bit ? v[j] : v[j + H];
+            const double keep = bit ? v[j + H] : v[j];
+            v[j] = keep + __shfl_xor(send, 1 << K, 64);
+        }
+        quarter_reduce<H, K - 1>(v, lane);
+    } else {
+        v[0] += __shfl_xor(v[0], 1 << K, 64);
+        quarter_reduce<1, K - 1>(v, lane);
+    }
+}
+// Head of value e in lane quarter c after quarter_reduce<G, 5>: the halving steps take lane bit
+// 5 then bit 4 as the high bits of the kept index.
 template <int G>
-__device__ __forceinline__ void attn_group_block_exact(const AttnArgs& a, AttnShared<G, double>& sh) {
-    const uint32_t kh = blockIdx.x;
-    if (a.splits != 1 || blockIdx.y != 0 || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ uint32_t quarter_head(uint32_t c, int e) {
+    if constexpr (G >= 4) return (c * (G / 4)) + (uint32_t)e;
+    else if constexpr (G == 2) return c >> 1;
+    else return 0;
+}
+
+template <int G>
+__device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) {
+    constexpr int HPL = G >= 4 ? G / 4 : 1;  // heads whose scores a lane holds
+    const uint32_t kh = blockIdx.x, y = blockIdx.y, P = a.splits;
+    if (P == 0 || P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;  // uniform
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t k = lane & 15, c = lane >> 4;
+    const uint32_t h0 = kh * G, q_dim = a.q_heads * X0NE_HEAD_DIM, kv_dim = a.kv_heads * X0NE_HEAD_DIM;
+    const uint32_t seq_pages = (a.max_ctx + X0NE_PAGE - 1) / X0NE_PAGE;
+
+    // Before pos: the q rows this wavefront ropes (heads wave, wave + 4, ...), in the last
+    // wavefront kv head kh's K and V rows, and in slice 0 the first page's table entry (slice 0's
+    // wavefront w starts at page w whatever the context; clamped inside the table).
+    constexpr int QPW = (G + WAVES - 1) / WAVES;
+    RopeIn qin[QPW], kin{};
+    bf16_t vrow[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+        const uint32_t g = wave + WAVES * j;
+        qin[j] = g < (uint32_t)G ? rope_in(a.qkv + (h0 + g) * X0NE_HEAD_DIM, a.q_norm) : RopeIn{};
+    }
+    const float invf = a.inv_freq[lane];
+    if (wave == WAVES - 1) {
+        kin = rope_in(a.qkv + q_dim + kh * X0NE_HEAD_DIM, a.k_norm);
+        const bf16_t* vs = a.qkv + q_dim + kv_dim + kh * X0NE_HEAD_DIM;
+        vrow[0] = vs[lane];
+        vrow[1] = vs[lane + 64];
+    }
+    const uint32_t first_entry = y == 0 ? a.pages[min(wave, seq_pages - 1)] : 0u;
+
     const uint32_t pos = a.pos[0];
     const uint32_t ctx = min(pos + 1u, a.max_ctx);
-    const uint32_t h0 = kh * G, q_dim = a.q_heads * X0NE_HEAD_DIM;
-    for (uint32_t g = wave; g < (uint32_t)G; g += WAVES) {
-        float ra, rb;
-        rope_pair(a.qkv + (h0 + g) * X0NE_HEAD_DIM, a.q_norm, a.inv_freq, pos, a.eps, &ra, &rb);
-        sh.qs[g][lane] = bf_round(ra);
-        sh.qs[g][lane + 64] = bf_round(rb);
+    const Split sp = split_of(ctx, P);
+    if (y >= sp.active) return;  // block-uniform: a slice past the context
+    const uint32_t npages = (ctx + X0NE_PAGE - 1) / X0NE_PAGE;
+    const uint32_t run_begin = y * sp.per * (X0NE_SPLIT_TILE / X0NE_PAGE);
+    const uint32_t run_end = min((y + 1) * sp.per * (X0NE_SPLIT_TILE / X0NE_PAGE), npages);
+    const uint32_t new_page = pos < a.max_ctx ? pos / X0NE_PAGE : ~0u;
+    const bool owner = new_page >= run_begin && new_page < run_end;
+
+    // Page-table entry and plane byte offsets of page p of this kv head; the K lane chunk is key
+    // k's dims 32c .. + 31, the V lane chunk dims lane and lane + 64 of the page's 16 keys.
+    const auto kr = plane_rsrc(a.k_cache, OFF_NONE), vr = plane_rsrc(a.v_cache, OFF_NONE);
+    const uint32_t page_b = a.kv_heads * X0NE_PAGE * X0NE_HEAD_DIM * 2, head_b = kh * X0NE_PAGE * X0NE_HEAD_DIM * 2;
+    auto entry = [&](uint32_t p) -> uint32_t { return p < run_end ? a.pages[p] : 0u; };
+    auto load_page = [&](uint32_t p, uint32_t pg, uint4 (&kk)[4], uint4 (&vv)[4]) {
+        const bool live = p < run_end;
+        const uint32_t kb = pg * page_b + head_b + k * X0NE_HEAD_DIM * 2 + 64 * c;
+        const uint32_t vb = pg * page_b + head_b + lane * X0NE_PAGE * 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kk[j] = bload16(kr, live ? kb + 16 * j : OFF_NONE);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            vv[j] = bload16(vr, live ? vb + 16 * j : OFF_NONE);
+            vv[2 + j] = bload16(vr, live ? vb + 64 * X0NE_PAGE * 2 + 16 * j : OFF_NONE);
+        }
+    };
+    uint32_t p = run_begin + wave;
+    uint4 kc[4], vc[4], kn[4], vn[4];
+    uint32_t pg = y == 0 ? (p < run_end ? first_entry : 0u) : entry(p);
+    load_page(p, pg, kc, vc);
+    uint32_t pg_next = entry(p + WAVES);
+
+    // QK-norm + RoPE (f64, the table's cosine and sine) while the first page is in flight; the
+    // owner's last wavefront writes position pos's K row and V column and keeps them in LDS.
+    double rc, rs;
+    if (pos < a.max_ctx) {
+        const double2 cs = *reinterpret_cast<const double2*>(a.rope_cs + 2 * ((size_t)pos * (X0NE_HEAD_DIM / 2) + lane));
+        rc = cs.x;
+        rs = cs.y;
+    } else {
+        const double angle = (double)((float)pos * invf);
+        rc = cos(angle);
+        rs = sin(angle);
     }
-    if (pos < a.max_ctx && wave == WAVES - 1) {
-        const uint32_t kv_dim = a.kv_heads * X0NE_HEAD_DIM;
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+        const uint32_t g = wave + WAVES * j;
+        if (g < (uint32_t)G) {
+            float ra, rb;
+            rope_rotate_cs(qin[j], rc, rs, a.eps, &ra, &rb);
+            sh.qd[g][lane] = (double)bf_round(ra);
+            sh.qd[g][lane + 64] = (double)bf_round(rb);
+        }
+    }
+    if (owner && wave == WAVES - 1) {
         float ra, rb;
-        rope_pair(a.qkv + q_dim + kh * X0NE_HEAD_DIM, a.k_norm, a.inv_freq, pos, a.eps, &ra, &rb);
+        rope_rotate_cs(kin, rc, rs, a.eps, &ra, &rb);
+        const bf16_t k0 = f2bf(ra), k1 = f2bf(rb);
         const uint32_t at = kv_row(a.pages, pos, kh, a.kv_heads);
-        a.k_cache[at + lane] = f2bf(ra);
-        a.k_cache[at + lane + 64] = f2bf(rb);
-        const bf16_t* vs = a.qkv + q_dim + kv_dim + kh * X0NE_HEAD_DIM;
+        a.k_cache[at + lane] = k0;
+        a.k_cache[at + lane + 64] = k1;
         const uint32_t vat = v_slot(a.pages, pos, kh, a.kv_heads);
-        a.v_cache[vat + lane * X0NE_PAGE] = vs[lane];
-        a.v_cache[vat + (lane + 64) * X0NE_PAGE] = vs[lane + 64];
+        a.v_cache[vat + lane * X0NE_PAGE] = vrow[0];
+        a.v_cache[vat + (lane + 64) * X0NE_PAGE] = vrow[1];
+        sh.knew[lane] = k0;
+        sh.knew[lane + 64] = k1;
+        sh.vnew[lane] = vrow[0];
+        sh.vnew[lane + 64] = vrow[1];
     }
-    __syncthreads();  // q in LDS; the new K/V row in memory for the wavefront that reads it
+    lds_barrier();  // q and the new row in LDS; the page loads stay in flight
+
     const double scale = 1.0 / sqrt((double)X0NE_HEAD_DIM);
-    double m[G], l[G], o[G][2];
-    attend_wave<G, double>(&sh.qs[0][0], a.k_cache, a.v_cache, a.pages, kh, a.kv_heads, ctx, wave, BLOCK_TILES,
-                           ~0u, scale, sh.xch[wave], m, l, o);
-    stash_wave<G, double>(sh, m, l, o);
+    double m[HPL], lsum[HPL], o[G][2];
+#pragma unroll
+    for (int e = 0; e < HPL; ++e) {
+        m[e] = -INFINITY;
+        lsum[e] = 0.0;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = 0.0;
+    double* pw = &sh.pw[wave][0][0];
+    double* alpha_l = &sh.alpha[wave][0];
+
+    for (; p < run_end; p += WAVES) {
+        if (p + WAVES < run_end) load_page(p + WAVES, pg_next, kn, vn);
+        const uint32_t pg_after = entry(p + 2 * WAVES);
+        const uint32_t base = p * X0NE_PAGE;
+        if (p == new_page) {  // wavefront-uniform: the new row from LDS, not from its write
+            if (k == pos % X0NE_PAGE) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kc[j] = *reinterpret_cast<const uint4*>(sh.knew + 32 * c + 8 * j);
+            }
+            const uint32_t e = pos % X0NE_PAGE, word = (e % 8) / 2, shift = 16 * (e & 1u);
+            const uint32_t keep = shift ? 0x0000FFFFu : 0xFFFF0000u;
+#pragma unroll
+            for (int dh = 0; dh < 2; ++dh) {
+                const uint32_t val = (uint32_t)sh.vnew[lane + 64 * dh] << shift;
+                uint4& w = vc[2 * dh + e / 8];
+                uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (j == (int)word) u[j] = (u[j] & keep) | val;
+                w = make_uint4(u[0], u[1], u[2], u[3]);
+            }
+        }
+        // Scores: key k's quarter c against every head, then the quarters summed.
+        double sc[G];
+        {
+            double kd[32];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t u[4] = {kc[j].x, kc[j].y, kc[j].z, kc[j].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kd[8 * j + 2 * i] = (double)bf_lo(u[i]);
+                    kd[8 * j + 2 * i + 1] = (double)bf_hi(u[i]);
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const double* q = &sh.qd[g][32 * c];
+                double s = 0.0;
+#pragma unroll
+                for (int d = 0; d < 32; d += 2) {
+                    const double2 qq = *reinterpret_cast<const double2*>(q + d);
+                    s = fma(qq.x, kd[d], s);
+                    s = fma(qq.y, kd[d + 1], s);
+                }
+                sc[g] = s;
+            }
+        }
+        quarter_reduce<G, 5>(sc, lane);
+        // Online softmax of the lane's heads over the page's 16 keys (lane bits 0..3).
+        const bool in = base + k < ctx;
+#pragma unroll
+        for (int e = 0; e < HPL; ++e) {
+            const double s = in ? sc[e] * scale : -INFINITY;
+            double mx = s;
+#pragma unroll
+            for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
+            const double mn = fmax(m[e], mx);  // key `base` is below ctx: mn is finite
+            const double al = exp(m[e] - mn);
+            const double pr = exp(s - mn);
+            lsum[e] = lsum[e] * al + pr;
+            m[e] = mn;
+            const uint32_t g = quarter_head<G>(c, e);
+            if (G >= 4 || (c & (4 / G - 1)) == 0) {
+                pw[g * X0NE_PAGE + k] = pr;
+                if (k == 0) alpha_l[g] = al;
+            }
+        }
+        wave_lds_sync();
+        // Weighted V sums: dims lane and lane + 64, keys past ctx taken as 0.
+        double v0[X0NE_PAGE], v1[X0NE_PAGE];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t u0[4] = {vc[j].x, vc[j].y, vc[j].z, vc[j].w};
+            const uint32_t u1[4] = {vc[2 + j].x, vc[2 + j].y, vc[2 + j].z, vc[2 + j].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t key = 8 * j + i;
+                const bool ok = base + key < ctx;
+                v0[key] = ok ? (double)((i & 1) ? bf_hi(u0[i / 2]) : bf_lo(u0[i / 2])) : 0.0;
+                v1[key] = ok ? (double)((i & 1) ? bf_hi(u1[i / 2]) : bf_lo(u1[i / 2])) : 0.0;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const double al = alpha_l[g];
+            double a0 = o[g][0] * al, a1 = o[g][1] * al;
+#pragma unroll
+            for (int key = 0; key < X0NE_PAGE; key += 2) {
+                const double2 pp = *reinterpret_cast<const double2*>(pw + g * X0NE_PAGE + key);
+                a0 = fma(pp.x, v0[key], a0);
+                a1 = fma(pp.x, v1[key], a1);
+                a0 = fma(pp.y, v0[key + 1], a0);
+                a1 = fma(pp.y, v1[key + 1], a1);
+            }
+            o[g][0] = a0;
+            o[g][1] = a1;
+        }
+        wave_lds_sync();  // the next page rewrites pw and alpha
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kc[j] = kn[j];
+            vc[j] = vn[j];
+        }
+        pg_next = pg_after;
+    }
+    // This wavefront's state: each head's m and l (the lane sums over keys 0..15), its o.
+#pragma unroll
+    for (int e = 0; e < HPL; ++e) {
+        double l = lsum[e];
+#pragma unroll
+        for (int o2 = 1; o2 < 16; o2 <<= 1) l += __shfl_xor(l, o2, 64);
+        const uint32_t g = quarter_head<G>(c, e);
+        if (k == 0 && (G >= 4 || (c & (4 / G - 1)) == 0)) {
+            sh.wm[wave][g] = m[e];
+            sh.wl[wave][g] = l;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        sh.wo[wave][g][lane] = o[g][0];
+        sh.wo[wave][g][lane + 64] = o[g][1];
+    }
     lds_barrier();
-    block_merge<G, double>(sh, [&](uint32_t g, uint32_t d, double, double lv, double ov) {
-        a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf((float)(ov / lv));
-    });
+    // The block's 4 wavefronts merged per head (in wave order, a wavefront without a page skipped).
+    if (t < (uint32_t)G) {
+        double mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) mx = fmax(mx, sh.wm[w][t]);
+        double l = 0.0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const bool seen = sh.wm[w][t] != -INFINITY;
+            const double fw = seen ? exp(sh.wm[w][t] - mx) : 0.0;
+            sh.wf[w][t] = fw;
+            if (seen) l += sh.wl[w][t] * fw;
+        }
+        sh.mh[t] = mx;
+        sh.lh[t] = l;
+    }
+    lds_barrier();
+    const bool whole = sp.active == 1;
+    double* st_base = reinterpret_cast<double*>(a.state);
+    for (uint32_t i = t; i < (uint32_t)G * X0NE_HEAD_DIM; i += BLOCK) {
+        const uint32_t g = i / X0NE_HEAD_DIM, d = i % X0NE_HEAD_DIM;
+        double ov = 0.0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w)
+            if (sh.wm[w][g] != -INFINITY) ov += sh.wo[w][g][d] * sh.wf[w][g];
+        if (whole) {
+            a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf((float)(ov / sh.lh[g]));
+        } else {
+            double* st = st_base + ((size_t)(h0 + g) * P + y) * X0NE_SPLIT_STATE;
+            dstate_put(st + 4 + d, ov);
+            if (d == 0) {
+                dstate_put(st, sh.mh[g]);
+                dstate_put(st + 1, sh.lh[g]);
+            }
+        }
+    }
+    if (whole) return;
+    // The slices' states acknowledged, then the count; the block that completes it merges each
+    // head's slices 0 .. active - 1 in that order (M = max m, f = exp(m - M), l = sum l f,
+    // o = sum o f; one rounding of o / l), and sets the count back to 0 for the next step.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0)
+        sh.last = __hip_atomic_fetch_add(a.counter + kh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  sp.active - 1;
+    __syncthreads();
+    if (!sh.last) return;  // block-uniform
+    const uint32_t active = sp.active;
+    for (uint32_t g = wave; g < (uint32_t)G; g += WAVES) {
+        const double* s = st_base + (size_t)(h0 + g) * P * X0NE_SPLIT_STATE;
+        double* f = sh.f[wave];
+        double mx = -INFINITY;
+        for (uint32_t yy = lane; yy < active; yy += 64) mx = fmax(mx, dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE));
+#pragma unroll
+        for (int o2 = 1; o2 < 64; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
+        double lp = 0.0;
+        for (uint32_t yy = lane; yy < active; yy += 64) {
+            const double fy = exp(dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE) - mx);
+            f[yy] = fy;
+            lp += dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE + 1) * fy;
+        }
+        const double l = wave_sum_d(lp);
+        wave_lds_sync();
+        double o0 = 0.0, o1 = 0.0;
+        for (uint32_t yy = 0; yy < active; ++yy) {
+            const double* so = s + (size_t)yy * X0NE_SPLIT_STATE + 4;
+            o0 = fma(dstate_get(so + lane), f[yy], o0);
+            o1 = fma(dstate_get(so + lane + 64), f[yy], o1);
+        }
+        a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + lane] = f2bf((float)(o0 / l));
+        a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + lane + 64] = f2bf((float)(o1 / l));
+        wave_lds_sync();
+    }
+    __syncthreads();
+    if (t == 0) __hip_atomic_store(a.counter + kh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next step
 }
 
 // Block (kv head kh, slice y) of the grouped kernel on the matrix cores: q heads kh G .. kh G +
@@ -1041,10 +1387,10 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
 // counters, and its output is row b of out, a [B][q_heads 128] matrix in panels (device.h): the
 // X operand of the batched O projection.
 //
-// x0ne_attention_rope_decode_exact_g*_bf16 is the fused variant with f64 scores, softmax and
-// sums and the f64 scale 1/sqrt(128), one block per kv head over the whole context (grid
-// (kv_heads, 1), block 256): the exact mode, whose outputs follow the f64 oracle's rounding
-// (oracle/src/lib.rs:112-176) rather than the f32 kernels'.
+// x0ne_attention_rope_decode_exact_g*_bf16 is the fused variant of the exact mode: the same
+// arguments, f64 scores, softmax and sums with the f64 scale 1/sqrt(128) (`scale` is unused),
+// grid (kv_heads, P); its split state is f64 (m, l, -, -, o[128] at state + (h P + y) 132
+// doubles: twice x0ne_split_state_bytes), merged in f64 by the last block of each kv head.
 #define X0NE_SPLIT_GROUP(G)                                                                                        \
     extern "C" __global__ void __launch_bounds__(256) x0ne_attention_decode_split_g##G##_bf16(                    \
         const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
@@ -1129,26 +1475,30 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
     }                                                                                                              \
     extern "C" __global__ void __launch_bounds__(256) x0ne_attention_rope_decode_exact_g##G##_bf16(               \
         const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm, const bf16_t* __restrict__ k_norm,    \
-        const float* __restrict__ inv_freq, bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,          \
-        const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,           \
-        uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float eps) {                                       \
-        __shared__ AttnShared<G, double> sh;                                                                       \
+        const float* __restrict__ inv_freq, const double* __restrict__ rope_cs, bf16_t* __restrict__ k_cache,    \
+        bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages, float* __restrict__ state,             \
+        uint32_t* __restrict__ counter, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,              \
+        uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale, float eps) {         \
+        __shared__ ExactShared sh;                                                                                 \
         AttnArgs a = {};                                                                                           \
         a.qkv = qkv;                                                                                               \
         a.q_norm = q_norm;                                                                                         \
         a.k_norm = k_norm;                                                                                         \
         a.inv_freq = inv_freq;                                                                                     \
+        a.rope_cs = rope_cs;                                                                                       \
         a.k_cache = k_cache;                                                                                       \
         a.v_cache = v_cache;                                                                                       \
         a.pages = pages;                                                                                           \
+        a.state = state;                                                                                           \
+        a.counter = counter;                                                                                       \
         a.out = out;                                                                                               \
         a.pos = pos;                                                                                               \
         a.q_heads = q_heads;                                                                                       \
         a.kv_heads = kv_heads;                                                                                     \
         a.max_ctx = max_ctx;                                                                                       \
-        a.splits = 1;                                                                                              \
+        a.splits = splits;                                                                                         \
         a.eps = eps;                                                                                               \
-        attn_group_block_exact<G>(a, sh);                                                                          \
+        exact_block<G>(a, sh);                                                                                     \
     }
 X0NE_SPLIT_GROUP(1)
 X0NE_SPLIT_GROUP(2)

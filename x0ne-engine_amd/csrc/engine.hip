@@ -541,7 +541,9 @@ x0ne_status plan(x0ne_engine* e) {
     X0NE_TRY(al("logits", c.vocab * 4, CD, &e->logits));
     X0NE_TRY(al("head_partial", (uint64_t)e->grid_head * 3 * 4, CD, &e->head_partial));
     X0NE_TRY(al("head_counter", 4, CD, &e->head_counter));
-    X0NE_TRY(al("attention_split_state", x0ne_split_state_bytes((uint32_t)c.q_heads, e->split.splits), CD,
+    // The exact mode's split state is f64: twice the bytes.
+    X0NE_TRY(al("attention_split_state",
+                x0ne_split_state_bytes((uint32_t)c.q_heads, e->split.splits) * (e->f64_sums ? 2 : 1), CD,
                 &e->attn_state));
     X0NE_TRY(al("attention_split_counter", c.kv_heads * 4, CD, &e->attn_counter));
     if (c.moe) {
@@ -665,20 +667,14 @@ x0ne_status launch_rope(x0ne_engine* e, uint64_t l) {
 x0ne_status launch_attention(x0ne_engine* e, uint64_t l) {
     const Cfg& c = e->c;
     const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));  // ops.rs:217-219
-    if (e->f64_sums) {  // the exact mode (group size checked at load)
-        const LayerW& w = e->L[l];
-        return attention_rope_exact(e->gpu, e->d(e->qkv), e->d(w.q_norm), e->d(w.k_norm), e->d(e->inv_freq),
-                                    e->plane(l, 0), e->plane(l, 1), e->d(e->page_table), e->d(e->attn), e->d(e->pos),
-                                    (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, (float)c.eps);
-    }
-    if (e->split.grouped) {
+    if (e->split.grouped) {  // the exact mode has grouped plans only (checked at load)
         const LayerW& w = e->L[l];
         return attention_rope_split(e->gpu, e->split, e->d(e->qkv), e->d(w.q_norm), e->d(w.k_norm),
                                     e->d(e->inv_freq), e->d(e->rope_cs), e->plane(l, 0), e->plane(l, 1),
                                     e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn),
                                     e->d(e->pos),
                                     (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, scale,
-                                    (float)c.eps);
+                                    (float)c.eps, e->f64_sums != 0);
     }
     X0NE_TRY(launch_rope(e, l));
     return attention_split(e->gpu, e->split, 0, e->d(e->q), e->plane(l, 0), e->plane(l, 1),

@@ -90,15 +90,11 @@ x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_b
                             uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
 // The decode step's attention in one launch for a grouped plan: QK-norm + RoPE of q, the K/V
 // row of position pos written into its page, split-K attention and the last-block merge. rope_cs:
-// the RoPE table of positions below max_ctx (x0ne_rope_table_f64 of inv_freq).
+// the RoPE table of positions below max_ctx (x0ne_rope_table_f64 of inv_freq). exact: the exact
+// mode's kernel (f64 scores, softmax and sums; its state is f64, twice x0ne_split_state_bytes).
 x0ne_status attention_rope_split(x0ne_gpu* g, const x0ne_split_plan& plan, const void* qkv, const void* q_norm,
                                  const void* k_norm, const void* inv_freq, const void* rope_cs, void* k, void* v,
                                  const void* pages,
                                  void* state, void* counter, void* out, const void* pos, uint32_t q_heads,
-                                 uint32_t kv_heads, uint32_t max_ctx, float scale, float eps);
-// The exact mode's decode attention: the fused work of attention_rope_split with f64 sums, one
-// block per kv head over the whole context, for group sizes 1, 2, 4 and 8.
-x0ne_status attention_rope_exact(x0ne_gpu* g, const void* qkv, const void* q_norm, const void* k_norm,
-                                 const void* inv_freq, void* k, void* v, const void* pages, void* out, const void* pos,
-                                 uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float eps);
+                                 uint32_t kv_heads, uint32_t max_ctx, float scale, float eps, bool exact = false);
 }  // namespace x0ne

@@ -43,9 +43,10 @@ __global__ void x0ne_attention_decode_split_bf16(const bf16_t* q, const bf16_t* 
         uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads,                \
         uint32_t max_ctx, uint32_t splits, float scale, float eps, uint32_t seq_pages);                          \
     __global__ void x0ne_attention_rope_decode_exact_g##G##_bf16(                                               \
-        const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq, bf16_t* k_cache,  \
-        bf16_t* v_cache, const uint32_t* pages, bf16_t* out, const uint32_t* pos, uint32_t q_heads,              \
-        uint32_t kv_heads, uint32_t max_ctx, float eps);
+        const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const float* inv_freq,                    \
+        const double* rope_cs, bf16_t* k_cache, bf16_t* v_cache, const uint32_t* pages, float* state,           \
+        uint32_t* counter, bf16_t* out, const uint32_t* pos, uint32_t q_heads, uint32_t kv_heads,                \
+        uint32_t max_ctx, uint32_t splits, float scale, float eps);
 X0NE_DECLARE_SPLIT_GROUP(1)
 X0NE_DECLARE_SPLIT_GROUP(2)
 X0NE_DECLARE_SPLIT_GROUP(4)

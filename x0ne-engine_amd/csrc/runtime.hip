@@ -482,32 +482,20 @@ x0ne_status attention_rope_split(x0ne_gpu* g, const x0ne_split_plan& plan, const
                                  const void* k_norm, const void* inv_freq, const void* rope_cs, void* k, void* v,
                                  const void* pages,
                                  void* state, void* counter, void* out, const void* pos, uint32_t qh, uint32_t kvh,
-                                 uint32_t max_ctx, float scale, float eps) {
+                                 uint32_t max_ctx, float scale, float eps, bool exact) {
     const uint32_t p = plan.splits;
     if (p == 0 || p > MAX_SPLITS) return fail(X0NE_ERR_GPU, "split-K: P " + std::to_string(p) + " outside 1..=256");
     if (!plan.grouped || kvh == 0 || qh % kvh != 0 || plan.group != qh / kvh)
         return fail(X0NE_ERR_GPU, "fused attention needs a grouped plan of this geometry");
-    const void* kern = rope_group_kernel(plan.group);
+    const void* kern = exact ? exact_group_kernel(plan.group) : rope_group_kernel(plan.group);
     if (!kern) return fail(X0NE_ERR_GPU, "fused attention: no kernel for this group size");
     void* args[] = {(void*)&qkv,     (void*)&q_norm, (void*)&k_norm, (void*)&inv_freq, (void*)&rope_cs,
                     (void*)&k,       (void*)&v,      (void*)&pages,  (void*)&state,    (void*)&counter,
                     (void*)&out,     (void*)&pos,    (void*)&qh,     (void*)&kvh,      (void*)&max_ctx,
                     (void*)&p,       (void*)&scale,  (void*)&eps};
     g->counts.launches++;
-    X0NE_HIP(x0ne_launch(kern, dim3(kvh, p), dim3(256), args, 0, g->stream), "fused decode attention");
-    return X0NE_OK;
-}
-
-x0ne_status attention_rope_exact(x0ne_gpu* g, const void* qkv, const void* q_norm, const void* k_norm,
-                                 const void* inv_freq, void* k, void* v, const void* pages, void* out, const void* pos,
-                                 uint32_t qh, uint32_t kvh, uint32_t max_ctx, float eps) {
-    if (kvh == 0 || qh % kvh != 0) return fail(X0NE_ERR_GPU, "exact attention: heads");
-    const void* kern = exact_group_kernel(qh / kvh);
-    if (!kern) return fail(X0NE_ERR_GPU, "exact attention: no kernel for group " + std::to_string(qh / kvh));
-    void* args[] = {(void*)&qkv, (void*)&q_norm, (void*)&k_norm, (void*)&inv_freq, (void*)&k, (void*)&v,
-                    (void*)&pages, (void*)&out, (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
-    g->counts.launches++;
-    X0NE_HIP(x0ne_launch(kern, dim3(kvh, 1), dim3(256), args, 0, g->stream), "exact decode attention");
+    X0NE_HIP(x0ne_launch(kern, dim3(kvh, p), dim3(256), args, 0, g->stream),
+             exact ? "exact decode attention" : "fused decode attention");
     return X0NE_OK;
 }
 

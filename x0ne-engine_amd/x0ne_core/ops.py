@@ -394,7 +394,8 @@ class Kernels:
         page, then split-K attention over keys 0..ctx-1 (k, v hold rows 0..ctx-2). last_block
         False runs the merge kernel after it. Returns (out, k_row, v_row) with the K/V row read
         back from the cache (the composition of ops.rs:138-208 and ops.rs:491-573). exact: the
-        exact mode's kernel (f64 scores, softmax and sums; one block per kv head, no split)."""
+        exact mode's kernel (f64 scores, softmax and sums, split-K with f64 states merged by the
+        last block; it needs last_block)."""
         h.check()
         qd, kvd = h.q_dim, h.kv_dim
         if ctx == 0 or qkv.size != qd + 2 * kvd or k.size < (ctx - 1) * kvd or v.size < (ctx - 1) * kvd:
@@ -409,7 +410,7 @@ class Kernels:
         vf = np.concatenate([np.asarray(v, np.uint16)[:(ctx - 1) * kvd], nan_row])
         hd = h.head_dim
         a, s = self._kv_arena(np.asarray(qkv, np.uint16), kf, vf, ctx, h, page_of, pool,
-                              [("out", qd * 2), ("state", split_state_bytes(h.q_heads, plan.splits)),
+                              [("out", qd * 2), ("state", split_state_bytes(h.q_heads, plan.splits) * (2 if exact else 1)),
                                ("counter", h.kv_heads * 4), ("q_norm", hd * 2), ("k_norm", hd * 2),
                                ("inv_freq", hd // 2 * 4), ("rope_cs", ctx * (hd // 2) * 16)])
         a.write(s["pos"], 0, np.array([ctx - 1], np.uint32))
@@ -418,22 +419,18 @@ class Kernels:
         a.write(s["inv_freq"], 0, inv_freq(hd, theta))
         self._rope_table(a.ptr(s["inv_freq"]), a.ptr(s["rope_cs"]), ctx, hd)
         counter = a.ptr(s["counter"]) if last_block else 0
-        if exact:
-            self.gpu.launch(f"x0ne_attention_rope_decode_exact_g{plan.group}_bf16", (h.kv_heads, 1), 256,
-                            [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["q_norm"])), Arg.ptr(a.ptr(s["k_norm"])),
-                             Arg.ptr(a.ptr(s["inv_freq"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
-                             Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])),
-                             Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.f32(eps)])
-            last_block = True
-        else:
-            self.gpu.launch(f"x0ne_attention_rope_decode_g{plan.group}_bf16", (h.kv_heads, plan.splits), 256,
-                            [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["q_norm"])), Arg.ptr(a.ptr(s["k_norm"])),
-                             Arg.ptr(a.ptr(s["inv_freq"])), Arg.ptr(a.ptr(s["rope_cs"])), Arg.ptr(a.ptr(s["k"])),
-                             Arg.ptr(a.ptr(s["v"])),
-                             Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["state"])), Arg.ptr(counter),
-                             Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(h.q_heads),
-                             Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.u32(plan.splits),
-                             Arg.f32(attn_scale(hd)), Arg.f32(eps)])
+        name = "exact" if exact else ""
+        self.gpu.launch(f"x0ne_attention_rope_decode_{name + '_' if name else ''}g{plan.group}_bf16",
+                        (h.kv_heads, plan.splits), 256,
+                        [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["q_norm"])), Arg.ptr(a.ptr(s["k_norm"])),
+                         Arg.ptr(a.ptr(s["inv_freq"])), Arg.ptr(a.ptr(s["rope_cs"])), Arg.ptr(a.ptr(s["k"])),
+                         Arg.ptr(a.ptr(s["v"])),
+                         Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["state"])), Arg.ptr(counter),
+                         Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(h.q_heads),
+                         Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.u32(plan.splits),
+                         Arg.f32(attn_scale(hd)), Arg.f32(eps)])
+        if exact and not last_block:
+            raise FormatError("attention_rope_decode: the exact kernel merges in its last block")
         if not last_block:
             self.gpu.launch("x0ne_attention_merge_bf16", h.q_heads, 64,
                             [Arg.ptr(a.ptr(s["state"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])),
