@@ -108,6 +108,35 @@ x0ne_status x0ne_gpu_launch_3d(x0ne_gpu* g, const char* name, uint32_t gx, uint3
 x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n, uint64_t y,
                           int out_f32);
 
+/* One launch of a fused decode GEMV instance on caller buffers: the kernels the decode step runs
+   for its projections, each with its prologue and epilogue, driven alone for kernel-level
+   parity tests. No counterpart in the reference, whose projections are cuBLAS calls beside
+   separate norm, SwiGLU and argmax kernels (gpu.rs:1098-1149; rmsnorm.cu, swiglu.cu, argmax.cu).
+   Device addresses; 0 for what the instance does not read or write.
+   prologue X0NE_GEMV_PRO_X: x given (bf16 [cols]). X0NE_GEMV_PRO_NORM: x = bf16(rmsnorm(res_in +
+   delta) * norm_w) (res_in f32, delta and norm_w bf16, [cols]), and res_out (may be 0) receives
+   res_in + delta. X0NE_GEMV_PRO_EMBED_NORM: the same on row tokens[0] of embed ([vocab][cols];
+   an id past vocab gives a zero row) over a zero residual.
+   epilogue X0NE_GEMV_EPI_BF16 / _F32: y[rows]. X0NE_GEMV_EPI_SWIGLU: W is [gate; up] (rows = 2
+   inter) and y[inter] = bf16(silu(bf16 gate) * bf16 up). X0NE_GEMV_EPI_ARGMAX: f32 logits in y,
+   the first largest index into token_out (0xFFFFFFFF when the row holds a NaN), pos[0] += 1 when
+   advance != 0; partial holds 3 words per block, counter one zeroed word that is left at zero.
+   Instances: (X, BF16), (X, F32), (NORM, BF16), (NORM, F32), (NORM, SWIGLU), (NORM, ARGMAX),
+   (EMBED_NORM, BF16); cols a multiple of 8, at most 32768 (X) or 16384 (the norm prologues).
+   f64_sums: each exact product added in f64 (the exact mode). X0NE_ERR_FORMAT for another
+   instance or shape, a missing or misaligned (16-byte) buffer. */
+enum { X0NE_GEMV_PRO_X = 0, X0NE_GEMV_PRO_NORM = 1, X0NE_GEMV_PRO_EMBED_NORM = 2 };
+enum { X0NE_GEMV_EPI_BF16 = 0, X0NE_GEMV_EPI_F32 = 1, X0NE_GEMV_EPI_SWIGLU = 2, X0NE_GEMV_EPI_ARGMAX = 3 };
+typedef struct {
+    uint64_t w, x, res_in, res_out, delta, norm_w, embed, tokens, y, partial, counter, token_out, pos;
+    uint32_t rows, cols, vocab, advance;
+    float eps;
+    uint32_t prologue, epilogue, f64_sums;
+} x0ne_gemv_fused;
+/* The blocks of that launch (the engine's grid for the shape), 0 for a refused instance. */
+uint32_t x0ne_gpu_gemv_fused_blocks(const x0ne_gpu* g, const x0ne_gemv_fused* d);
+x0ne_status x0ne_gpu_gemv_fused(x0ne_gpu* g, const x0ne_gemv_fused* d);
+
 /* Split-K plan (gpu.rs:958-985, SplitPlan): P for a geometry, and whether a grouped kernel
    serves it (group sizes 1, 2, 4, 8). */
 typedef struct {

@@ -327,6 +327,89 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
 
 }  // namespace x0ne
 
+// ---- one fused GEMV instance on caller buffers (the kernel-level test surface) ----
+namespace {
+bool fused_desc(const x0ne_gemv_fused& d, X0neGemv* a, std::string* why) {
+    auto aligned = [](uint64_t p) { return p % 16 == 0; };
+    if (d.prologue > X0NE_GEMV_PRO_EMBED_NORM || d.epilogue > X0NE_GEMV_EPI_ARGMAX) {
+        *why = "unknown prologue or epilogue";
+        return false;
+    }
+    if (!d.w || !d.y || !aligned(d.w)) {
+        *why = "W and y are required, W 16-byte aligned";
+        return false;
+    }
+    if (d.prologue == X0NE_GEMV_PRO_X && (!d.x || !aligned(d.x))) {
+        *why = "x (16-byte aligned) is required";
+        return false;
+    }
+    if (d.prologue == X0NE_GEMV_PRO_NORM &&
+        (!d.res_in || !d.delta || !d.norm_w || !aligned(d.res_in) || !aligned(d.delta) || !aligned(d.norm_w) ||
+         !aligned(d.res_out))) {
+        *why = "res_in, delta and norm_w (and res_out when given) are required, 16-byte aligned";
+        return false;
+    }
+    if (d.prologue == X0NE_GEMV_PRO_EMBED_NORM &&
+        (!d.embed || !d.tokens || !d.norm_w || !d.vocab || !aligned(d.embed) || !aligned(d.norm_w) ||
+         !aligned(d.res_out))) {
+        *why = "embed, tokens, vocab and norm_w (and res_out when given) are required, 16-byte aligned";
+        return false;
+    }
+    if (d.epilogue == X0NE_GEMV_EPI_ARGMAX && (!d.partial || !d.counter || !d.token_out || (d.advance && !d.pos))) {
+        *why = "partial, counter, token_out (and pos when advancing) are required";
+        return false;
+    }
+    *a = X0neGemv{};
+    a->w = (const uint16_t*)d.w;
+    a->x = (const uint16_t*)d.x;
+    a->res_in = (const float*)d.res_in;
+    a->res_out = (float*)d.res_out;
+    a->delta = (const uint16_t*)d.delta;
+    a->norm_w = (const uint16_t*)d.norm_w;
+    a->embed = (const uint16_t*)d.embed;
+    a->tokens = (const uint32_t*)d.tokens;
+    a->y = (void*)d.y;
+    a->partial = (float*)d.partial;
+    a->counter = (uint32_t*)d.counter;
+    a->token_out = (uint32_t*)d.token_out;
+    a->pos = (uint32_t*)d.pos;
+    a->rows = d.rows;
+    a->cols = d.cols;
+    a->vocab = d.vocab;
+    a->advance = d.advance ? 1u : 0u;
+    a->eps = d.eps;
+    a->prologue = (int)d.prologue;
+    a->epilogue = (int)d.epilogue;
+    a->f64acc = d.f64_sums ? 1 : 0;
+    return true;
+}
+}  // namespace
+
+extern "C" uint32_t x0ne_gpu_gemv_fused_blocks(const x0ne_gpu* g, const x0ne_gemv_fused* d) {
+    if (!g || !d) return 0;
+    X0neGemv a;
+    std::string why;
+    if (!fused_desc(*d, &a, &why)) return 0;
+    return x0ne_gemv_grid(a, g->cus, 0);
+}
+
+extern "C" x0ne_status x0ne_gpu_gemv_fused(x0ne_gpu* g, const x0ne_gemv_fused* d) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    if (!d) return fail(X0NE_ERR_FORMAT, "fused gemv: no descriptor");
+    X0neGemv a;
+    std::string why;
+    if (!fused_desc(*d, &a, &why)) return fail(X0NE_ERR_FORMAT, "fused gemv: " + why);
+    a.grid = x0ne_gemv_grid(a, g->cus, 0);
+    if (a.grid == 0)
+        return fail(X0NE_ERR_FORMAT, "fused gemv: instance (" + std::to_string(d->prologue) + ", " +
+                                         std::to_string(d->epilogue) + ") at " + std::to_string(d->rows) + "x" +
+                                         std::to_string(d->cols) + " is not served");
+    g->counts.launches++;
+    g->counts.gemms++;
+    X0NE_HIP(x0ne_launch_gemv(a, g->stream), "fused gemv");
+    return X0NE_OK;
+}
+
 extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n,
                                      uint64_t y, int out_f32) {
     if (!g) return fail(X0NE_ERR_GPU, "no device");

@@ -71,6 +71,14 @@ class PosStatsC(C.Structure):
     _fields_ = [("argmax", C.c_uint32), ("logsumexp", C.c_float), ("next_logprob", C.c_float)]
 
 
+class GemvFusedC(C.Structure):
+    """x0ne_gemv_fused: one fused decode GEMV instance on caller buffers."""
+    _fields_ = [(n, C.c_uint64) for n in ("w", "x", "res_in", "res_out", "delta", "norm_w", "embed", "tokens",
+                                          "y", "partial", "counter", "token_out", "pos")] + \
+               [(n, C.c_uint32) for n in ("rows", "cols", "vocab", "advance")] + [("eps", C.c_float)] + \
+               [(n, C.c_uint32) for n in ("prologue", "epilogue", "f64_sums")]
+
+
 class EngineOptionsC(C.Structure):
     _fields_ = [("max_ctx", C.c_uint64), ("page_seed", C.c_uint64), ("f64_sums", C.c_uint32),
                 ("prefill_chunk", C.c_uint32), ("max_batch", C.c_uint32), ("reserved", C.c_uint32)]
@@ -99,6 +107,8 @@ SIGNATURES = {
     "x0ne_gpu_launch": ([P, C.c_char_p, U32, U32, U32, C.POINTER(ArgC), SZ], ST),
     "x0ne_gpu_launch_3d": ([P, C.c_char_p, U32, U32, U32, U32, C.POINTER(ArgC), SZ], ST),
     "x0ne_gpu_gemv": ([P, U64, U64, U64, U64, U64, U64, I32], ST),
+    "x0ne_gpu_gemv_fused_blocks": ([P, C.POINTER(GemvFusedC)], U32),
+    "x0ne_gpu_gemv_fused": ([P, C.POINTER(GemvFusedC)], ST),
     "x0ne_gpu_split_plan": ([P, U32, U32, C.POINTER(SplitPlanC)], ST),
     "x0ne_gpu_attention_split": ([P, C.POINTER(SplitPlanC), I32, U64, U64, U64, U64, U64, U64, U64, U64,
                                   U32, U32, U32, F32], ST),

@@ -5,7 +5,7 @@ import ctypes as C
 from dataclasses import dataclass
 from enum import IntEnum
 
-from ._lib import ArgC, Counts, SplitPlanC, check, lib
+from ._lib import ArgC, Counts, GemvFusedC, SplitPlanC, check, lib
 
 
 class Param(IntEnum):
@@ -169,6 +169,15 @@ class Gpu:
     def gemv(self, w: int, rows: int, cols: int, x: int, n: int, y: int, out_f32: bool):
         """Gpu::gemm (gpu.rs:1098-1149): Y[n][rows] = X[n][cols] W^T on device addresses."""
         check(lib().x0ne_gpu_gemv(self.h, w, rows, cols, x, n, y, int(out_f32)), "gemv")
+
+    def gemv_fused(self, **fields) -> None:
+        """One fused decode GEMV instance (x0ne_gpu_gemv_fused) on device addresses."""
+        d = GemvFusedC(**fields)
+        check(lib().x0ne_gpu_gemv_fused(self.h, C.byref(d)), "gemv_fused")
+
+    def gemv_fused_blocks(self, **fields) -> int:
+        d = GemvFusedC(**fields)
+        return int(lib().x0ne_gpu_gemv_fused_blocks(self.h, C.byref(d)))
 
     def split_plan(self, q_heads: int, kv_heads: int) -> SplitPlan:
         p = SplitPlanC()

@@ -275,6 +275,76 @@ class Kernels:
         self.gpu.sync()
         return a.read_array(ys, 0, n * rows, np.float32 if out_f32 else np.uint16).reshape(n, rows)
 
+    # -- the fused decode GEMV instances (gemv.hip) --
+    PRO_X, PRO_NORM, PRO_EMBED_NORM = 0, 1, 2
+    EPI_BF16, EPI_F32, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3
+
+    def gemv_fused(self, w, rows: int, cols: int, prologue: int, epilogue: int, f64_sums: bool = False, x=None,
+                   residual=None, delta=None, norm_w=None, embed=None, token: int = 0, vocab: int = 0,
+                   eps: float = 1e-6, advance: bool = False, pos: int = 0) -> dict:
+        """One launch of a decode GEMV with its fused prologue and epilogue (x0ne_gpu_gemv_fused),
+        the instances the decode step runs: PRO_X takes x (bf16 bits); PRO_NORM takes the f32
+        residual, delta and norm_w (bf16) and also returns the new residual; PRO_EMBED_NORM takes
+        the embedding table ([vocab][cols] bf16), the token and norm_w. EPI_BF16 / EPI_F32 return
+        y; EPI_SWIGLU returns the inter = rows / 2 activations; EPI_ARGMAX the f32 logits, the
+        token, the position after (pos, advanced when asked) and the counter after (0)."""
+        w = np.ascontiguousarray(w, np.uint16)
+        if w.size != rows * cols:
+            raise FormatError(f"gemv_fused: W {w.size} for {rows}x{cols}")
+        out_rows = rows // 2 if epilogue == self.EPI_SWIGLU else rows
+        ob = 4 if epilogue in (self.EPI_F32, self.EPI_ARGMAX) else 2
+        a = self._arena()
+        s = {"w": a.alloc("w", w.size * 2, Class.WEIGHTS), "y": a.alloc("y", out_rows * ob, Class.CLIENT_DATA)}
+        if prologue == self.PRO_X:
+            s["x"] = a.alloc("x", cols * 2, Class.CLIENT_DATA)
+        if prologue in (self.PRO_NORM, self.PRO_EMBED_NORM):
+            s["norm_w"] = a.alloc("norm_w", cols * 2, Class.WEIGHTS)
+            s["res_out"] = a.alloc("res_out", cols * 4, Class.CLIENT_DATA)
+        if prologue == self.PRO_NORM:
+            s["res_in"] = a.alloc("res_in", cols * 4, Class.CLIENT_DATA)
+            s["delta"] = a.alloc("delta", cols * 2, Class.CLIENT_DATA)
+        if prologue == self.PRO_EMBED_NORM:
+            s["embed"] = a.alloc("embed", vocab * cols * 2, Class.WEIGHTS)
+            s["tokens"] = a.alloc("tokens", 4, Class.CLIENT_DATA)
+        fields = dict(rows=rows, cols=cols, prologue=prologue, epilogue=epilogue, f64_sums=int(f64_sums),
+                      vocab=vocab, eps=eps, advance=int(advance))
+        blocks = 0
+        if epilogue == self.EPI_ARGMAX:
+            blocks = self.gpu.gemv_fused_blocks(w=16, y=16, x=16, res_in=16, delta=16, norm_w=16, embed=16,
+                                                tokens=16, partial=16, counter=16, token_out=16, pos=16, **fields)
+            if blocks == 0:
+                raise FormatError("gemv_fused: instance refused")
+            s["partial"] = a.alloc("partial", blocks * 12, Class.CLIENT_DATA)
+            s["counter"] = a.alloc("counter", 4, Class.CLIENT_DATA)
+            s["token_out"] = a.alloc("token_out", 4, Class.CLIENT_DATA)
+            s["pos"] = a.alloc("pos", 4, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.scrub_client_data()
+        a.write(s["w"], 0, w)
+        if "x" in s:
+            a.write(s["x"], 0, np.ascontiguousarray(x, np.uint16))
+        if "norm_w" in s:
+            a.write(s["norm_w"], 0, np.ascontiguousarray(norm_w, np.uint16))
+        if "res_in" in s:
+            a.write(s["res_in"], 0, np.ascontiguousarray(residual, np.float32))
+            a.write(s["delta"], 0, np.ascontiguousarray(delta, np.uint16))
+        if "embed" in s:
+            a.write(s["embed"], 0, np.ascontiguousarray(embed, np.uint16))
+            a.write(s["tokens"], 0, np.array([token], np.uint32))
+        if "pos" in s:
+            a.write(s["pos"], 0, np.array([pos], np.uint32))
+        self.gpu.gemv_fused(**{k: a.ptr(v) for k, v in s.items()}, **fields)
+        self.gpu.sync()
+        out = {"y": a.read_array(s["y"], 0, out_rows, np.float32 if ob == 4 else np.uint16)}
+        if "res_out" in s:
+            out["residual"] = a.read_array(s["res_out"], 0, cols, np.float32)
+        if epilogue == self.EPI_ARGMAX:
+            out["token"] = int(a.read_array(s["token_out"], 0, 1, np.uint32)[0])
+            out["pos"] = int(a.read_array(s["pos"], 0, 1, np.uint32)[0])
+            out["counter"] = int(a.read_array(s["counter"], 0, 1, np.uint32)[0])
+            out["blocks"] = blocks
+        return out
+
     def gemv_f32_out(self, w, rows, cols, x) -> np.ndarray:
         return self._gemv(w, rows, cols, x, True)
 
