@@ -317,16 +317,34 @@ typedef enum { X0NE_DECODE_EAGER = 0, X0NE_DECODE_GRAPH = 1 } x0ne_decode_mode;
 x0ne_status x0ne_engine_set_decode_mode(x0ne_engine* e, uint32_t mode);
 uint32_t x0ne_engine_decode_mode(const x0ne_engine* e);
 
+/* DecodeAttention (ops.rs:55-62) and SplitMerge (ops.rs:64-70). Engine::set_decode_attention
+   (engine.rs:531-539): split-K (the default; one fused launch per layer on a grouped plan) or the
+   per-head kernel (the reference's E2 witness, after the QK-norm/RoPE kernel). Engine::
+   set_split_merge (engine.rs:547-560): the split-K states merged by the merge kernel or by the
+   last block of each kv head (X0NE_ERR_GPU without a grouped kernel). Either re-captures the
+   decode graph, which zeroes the client buffers: call them between requests (X0NE_ERR_FORMAT
+   while a session is open); if the capture fails no graph is left and the engine runs eager.
+   This build's default merge is the last block on a grouped plan (the reference's is the merge
+   kernel, engine.rs:35). The exact mode has only its f64 split-K kernel with the last-block merge
+   (X0NE_ERR_NOT_IMPLEMENTED for the others). */
+typedef enum { X0NE_ATTENTION_SPLIT_K = 0, X0NE_ATTENTION_PER_HEAD = 1 } x0ne_decode_attention;
+typedef enum { X0NE_MERGE_KERNEL = 0, X0NE_MERGE_LAST_BLOCK = 1 } x0ne_split_merge;
+x0ne_status x0ne_engine_set_decode_attention(x0ne_engine* e, uint32_t attention);
+uint32_t x0ne_engine_decode_attention(const x0ne_engine* e);
+x0ne_status x0ne_engine_set_split_merge(x0ne_engine* e, uint32_t merge);
+uint32_t x0ne_engine_split_merge(const x0ne_engine* e);
+
 /* Engine::logits_at (engine.rs:1012-1020): teacher-forced f32 logits at `positions` of ids,
-   rows[k * vocab ..] for positions[k]. */
+   rows[k * vocab ..] for positions[k]: x0ne_engine_run's kept rows (and its refusals). */
 x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids, size_t n, const size_t* positions,
                                   size_t n_positions, uint32_t route, float* rows);
 
 /* PosStats (engine.rs:60-64) and Engine::run (engine.rs:928-1006): the teacher-forced pass of
-   x0ne_engine_logits_at with, for each of the n positions, stats[p] (the device's argmax of the
-   row, 0xFFFFFFFF when it holds a NaN; the row's logsumexp, metrics.rs:4-7; the log-probability
-   of ids[p + 1], NaN at the last position), and the f32 rows at keep[k] in rows[k * vocab ..]
-   (the bits x0ne_engine_logits_at gives). Engine::stats is this with n_keep 0. */
+   ids with, for each of the n positions, stats[p] (the device's argmax of the row; the row's
+   logsumexp, metrics.rs:4-7; the log-probability of ids[p + 1], NaN at the last position), and
+   the f32 rows at keep[k] in rows[k * vocab ..]. A row without a finite maximum (a NaN in it)
+   refuses the whole pass with X0NE_ERR_GPU, as the reference's argmax read does
+   (engine.rs:855-864). Engine::stats is this with n_keep 0, Engine::logits_at its kept rows. */
 typedef struct {
     uint32_t argmax;
     float logsumexp;

@@ -613,3 +613,60 @@ def test_a_random_moe_routes_each_token_to_distinct_experts():
     assert e.greedy(ids[:10], 6).size == 6 and e.client_data_is_zero()
     dense = f.engine(64)
     assert dense.moe_routing(ids).size == 0
+
+
+@pytest.mark.parametrize("which", [0, 1])
+def test_the_decode_attention_kernels_agree_inside_the_engine(which):
+    """gpu_engine.rs:722-769: the per-head kernel and split-K agree within the model tolerance
+    against the oracle and each other at positions around the 64- and 256-key tile edges; the
+    merge kernel and the last-block merge give the same bits; switching back gives the first
+    bits again. A switch re-captures the graph and leaves the client bytes zeroed; it is refused
+    while a session is open, and the last-block merge is refused without a grouped kernel."""
+    from x0ne_core import DecodeAttention, FormatError, GpuError, SplitMerge
+    f = [Fixture(tiny(2, 4, 2, False), 14), Fixture(wide(), 15)][which]
+    e = f.engine(700)
+    ids = f.tokens(25, 520)
+    keep = [0, 63, 64, 127, 128, 129, 255, 256, 300, 519]
+    want = f.model.logits(ids)
+    assert e.decode_attention() == DecodeAttention.SPLIT_K
+    assert e.split_merge() == SplitMerge.LAST_BLOCK
+    split = e.logits_at(ids, keep)
+    e.set_decode_attention(DecodeAttention.PER_HEAD)
+    assert e.client_data_is_zero() and "per head" in e.describe()
+    per_head = e.logits_at(ids, keep)
+    e.set_decode_attention(DecodeAttention.SPLIT_K)
+    for a, b, p in zip(split, per_head, keep):
+        assert_logits(f"split-K at {p}", a, want[p])
+        assert_logits(f"per-head at {p}", b, want[p])
+        assert_logits(f"split-K against per-head at {p}", a, b)
+    e.set_split_merge(SplitMerge.KERNEL)
+    assert "merge Kernel" in e.describe()
+    kernel_merge = e.logits_at(ids, keep)
+    for a, b, p in zip(split, kernel_merge, keep):
+        assert (a.view(np.uint32) == b.view(np.uint32)).all(), f"the two merges differ at {p}"
+    e.set_split_merge(SplitMerge.LAST_BLOCK)
+    again = e.logits_at(ids, keep)
+    for a, b, p in zip(split, again, keep):
+        assert (a.view(np.uint32) == b.view(np.uint32)).all(), f"split-K again at {p}"
+    print(f"MEASURE P = {e.splits()}, {e.describe()}")
+    s = e.session(ids[:5])
+    with pytest.raises(FormatError):
+        e.set_decode_attention(DecodeAttention.PER_HEAD)
+    s.finish()
+    ex = Engine_exact(f)
+    from x0ne_core import NotImplementedFeature
+    with pytest.raises(NotImplementedFeature):
+        ex.set_decode_attention(DecodeAttention.PER_HEAD)
+    with pytest.raises(NotImplementedFeature):
+        ex.set_split_merge(SplitMerge.KERNEL)
+    ungrouped = Fixture(tiny(1, 3, 1, False), 16)
+    u = ungrouped.engine(64)
+    with pytest.raises(GpuError):
+        u.set_split_merge(SplitMerge.LAST_BLOCK)
+    assert u.split_merge() == SplitMerge.KERNEL
+
+
+def Engine_exact(f):
+    from x0ne_core import Engine, EngineOptions
+    return Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
+                            EngineOptions(max_ctx=64, page_seed=3, f64_sums=True))

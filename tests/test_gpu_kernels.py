@@ -412,6 +412,7 @@ def test_fused_rope_attention_is_the_two_kernel_path_bit_for_bit(kernels, qh, kv
                     bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), eps, theta, bf16_bits(k), bf16_bits(v), ctx, h,
                     last_block=last_block, splits=splits, page_of=page_of)
                 assert (k_row == rope.k_row).all() and (v_row == rope.v_row).all(), f"{what}: the K/V row"
+                assert kernels.kv_rest_untouched, f"{what}: a K/V byte other than the new row changed"
                 two = kernels.attention_decode_split(rope.q, kb, vb, ctx, h, last_block=last_block, splits=splits,
                                                      page_of=page_of)
                 assert (out == two).all(), f"{what} P {splits} last_block {last_block}: not the two-kernel bits"
@@ -440,6 +441,7 @@ def test_batched_attention_is_each_sequence_alone_bit_for_bit(kernels, qh, kvh):
         out, k_rows, v_rows = kernels.attention_rope_decode_batch(
             np.concatenate([bf16_bits(q) for q in qkv]), bf16_bits(qn), bf16_bits(kn), eps, theta,
             [bf16_bits(k) for k in ks], [bf16_bits(v) for v in vs], ctxs, h, splits, max_ctx, page_seed=5 + splits)
+        assert kernels.kv_rest_untouched, f"batched {qh}/{kvh} P {splits}: a K/V byte other than the new rows changed"
         for b, ctx in enumerate(ctxs):
             what = f"batched {qh}/{kvh} P {splits} sequence {b} ctx {ctx}"
             one, k_row, v_row = kernels.attention_rope_decode(
@@ -484,6 +486,7 @@ def test_exact_attention_is_the_f64_oracle_bit_for_bit(kernels, qh, kvh):
                                                           bf16_bits(k), bf16_bits(v), ctx, h, page_of=page_of,
                                                           exact=True, splits=splits)
         assert (k_row == rope.k_row).all() and (v_row == rope.v_row).all(), f"ctx {ctx}: the K/V row"
+        assert kernels.kv_rest_untouched, f"exact ctx {ctx}: a K/V byte other than the new row changed"
         kb = np.concatenate([bf16_bits(k), rope.k_row])
         vb = np.concatenate([bf16_bits(v), rope.v_row])
         want = bf16_bits(O.attention_decode(bf16_vals(rope.q), bf16_vals(kb), bf16_vals(vb), ctx, qh, kvh))

@@ -429,6 +429,11 @@ struct x0ne_engine {
     x0ne_graph* bgraph = nullptr;  // the batched step for bgraph_batch sequences
     uint64_t bgraph_batch = 0;
     uint32_t mode = X0NE_DECODE_GRAPH;
+    // The decode step's attention (Engine::decode_attention / split_merge, engine.rs:526-560):
+    // split-K (the fused kernel for a grouped plan) or per head; the split-K states merged by the
+    // last block of each kv head (grouped plans) or by the merge kernel.
+    uint32_t attention = X0NE_ATTENTION_SPLIT_K;
+    uint32_t merge = X0NE_MERGE_KERNEL;
     // host side (pinned)
     uint32_t* ring = nullptr;
     uint32_t* bring = nullptr;  // RING slots of max_batch token words
@@ -662,24 +667,45 @@ x0ne_status launch_rope(x0ne_engine* e, uint64_t l) {
     return X0NE_OK;
 }
 
-// A grouped plan: one fused launch (QK-norm + RoPE + K/V write + split-K + last-block merge).
-// Otherwise the QK-norm/RoPE kernel, then split-K and the merge kernel.
+// The decode attention of layer l. Split-K on a grouped plan is one fused launch (QK-norm +
+// RoPE + K/V write + split-K), merged by its last block or followed by the merge kernel; the
+// exact mode's fused kernel always merges in its last block. Otherwise the QK-norm/RoPE kernel,
+// then split-K and the merge kernel, or the per-head kernel (engine.rs:744-764).
 x0ne_status launch_attention(x0ne_engine* e, uint64_t l) {
     const Cfg& c = e->c;
     const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));  // ops.rs:217-219
-    if (e->split.grouped) {  // the exact mode has grouped plans only (checked at load)
+    const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads, max_ctx = (uint32_t)e->max_ctx;
+    if (e->attention == X0NE_ATTENTION_SPLIT_K && e->split.grouped) {  // the exact mode is grouped (load check)
         const LayerW& w = e->L[l];
-        return attention_rope_split(e->gpu, e->split, e->d(e->qkv), e->d(w.q_norm), e->d(w.k_norm),
-                                    e->d(e->inv_freq), e->d(e->rope_cs), e->plane(l, 0), e->plane(l, 1),
-                                    e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn),
-                                    e->d(e->pos),
-                                    (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, scale,
-                                    (float)c.eps, e->f64_sums != 0);
+        const bool last = e->f64_sums || e->merge == X0NE_MERGE_LAST_BLOCK;
+        X0NE_TRY(attention_rope_split(e->gpu, e->split, e->d(e->qkv), e->d(w.q_norm), e->d(w.k_norm),
+                                      e->d(e->inv_freq), e->d(e->rope_cs), e->plane(l, 0), e->plane(l, 1),
+                                      e->d(e->page_table), e->d(e->attn_state),
+                                      last ? e->d(e->attn_counter) : nullptr, e->d(e->attn), e->d(e->pos), qh, kvh,
+                                      max_ctx, scale, (float)c.eps, e->f64_sums != 0));
+        return last ? X0NE_OK : attention_merge(e->gpu, e->split, e->d(e->attn_state), e->d(e->attn), e->d(e->pos),
+                                                qh, max_ctx);
     }
     X0NE_TRY(launch_rope(e, l));
-    return attention_split(e->gpu, e->split, 0, e->d(e->q), e->plane(l, 0), e->plane(l, 1),
-                           e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter), e->d(e->attn),
-                           e->d(e->pos), (uint32_t)c.q_heads, (uint32_t)c.kv_heads, (uint32_t)e->max_ctx, scale);
+    if (e->attention == X0NE_ATTENTION_PER_HEAD) {
+        const void* q = e->d(e->q);
+        const void* kc = e->plane(l, 0);
+        const void* vc = e->plane(l, 1);
+        const void* pt = e->d(e->page_table);
+        void* out = e->d(e->attn);
+        const void* pos = e->d(e->pos);
+        uint32_t mc = max_ctx;
+        float sc = scale;
+        void* args[] = {(void*)&q,   (void*)&kc, (void*)&vc,  (void*)&pt, (void*)&out,
+                        (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&mc, (void*)&sc};
+        e->gpu->counts.launches++;
+        X0NE_HIP(x0ne_launch((const void*)&x0ne_attention_decode_bf16, dim3(qh), dim3(256), args, 0, e->gpu->stream),
+                 "per-head decode attention");
+        return X0NE_OK;
+    }
+    return attention_split(e->gpu, e->split, e->merge == X0NE_MERGE_LAST_BLOCK ? 1 : 0, e->d(e->q), e->plane(l, 0),
+                           e->plane(l, 1), e->d(e->page_table), e->d(e->attn_state), e->d(e->attn_counter),
+                           e->d(e->attn), e->d(e->pos), qh, kvh, max_ctx, scale);
 }
 
 x0ne_status launch_o(x0ne_engine* e, uint64_t l) {
@@ -1151,6 +1177,9 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
         return s;
     };
     if ((st = split_plan(e->gpu, (uint32_t)c.q_heads, (uint32_t)c.kv_heads, &e->split)) != X0NE_OK) return bail(st);
+    // A grouped plan merges in its last block by default (one launch per layer); the reference's
+    // default is the merge kernel (engine.rs:35), which set_split_merge selects.
+    e->merge = e->split.grouped ? X0NE_MERGE_LAST_BLOCK : X0NE_MERGE_KERNEL;
     if (e->max_batch > 1) {
         if (!e->split.grouped)
             return bail(fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding needs 1, 2, 4 or 8 q heads per kv head"));
@@ -2138,45 +2167,13 @@ extern "C" x0ne_status x0ne_engine_greedy_with_last_logits(x0ne_engine* e, const
     return st != X0NE_OK ? st : sc;
 }
 
+// Engine::logits_at (engine.rs:1012-1020) is Engine::run's kept rows: the same pass, the same
+// refusal of a row without a finite maximum.
 extern "C" x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids, size_t n, const size_t* positions,
                                              size_t n_positions, uint32_t route, float* rows) {
-    if (!e || (!rows && n_positions)) return fail(X0NE_ERR_FORMAT, "null argument");
-    if (route != X0NE_ROUTE_PREFILL && route != X0NE_ROUTE_DECODE) return fail(X0NE_ERR_FORMAT, "unknown route");
-    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
-    if (e->poisoned) X0NE_TRY(scrub(e));
-    X0NE_TRY(check_ids(e, ids, n));
-    for (size_t k = 0; k < n_positions; ++k)
-        if (positions[k] >= n)
-            return fail(X0NE_ERR_FORMAT, "position " + std::to_string(positions[k]) + " outside " + std::to_string(n) + " tokens");
-    // The decode route feeds one position per step (graph or eager); the prefill route runs
-    // passes of up to `chunk` rows and the LM head on each kept row (engine.rs:946-1016).
-    x0ne_status st = put_prompt(e, ids, n);
-    auto take = [&](size_t p) -> x0ne_status {
-        for (size_t k = 0; k < n_positions; ++k)
-            if (positions[k] == p) X0NE_TRY(x0ne_arena_read(e->arena, e->logits, 0, rows + k * e->c.vocab, e->c.vocab * 4));
-        return X0NE_OK;
-    };
-    if (route == X0NE_ROUTE_PREFILL && e->chunk > 1) {
-        for (size_t start = 0; start < n && st == X0NE_OK;) {
-            const size_t len = std::min<size_t>(e->chunk, n - start);
-            st = prefill_pass(e, start, len);
-            for (size_t p = start; p < start + len && st == X0NE_OK; ++p) {
-                bool kept = false;
-                for (size_t k = 0; k < n_positions; ++k) kept |= positions[k] == p;
-                if (!kept) continue;
-                st = prefill_head(e, p - start, p, false);
-                if (st == X0NE_OK) st = take(p);
-            }
-            start += len;
-        }
-    } else {
-        for (size_t p = 0; p < n && st == X0NE_OK; ++p) {
-            st = feed(e, (uint32_t)p);
-            if (st == X0NE_OK) st = take(p);
-        }
-    }
-    x0ne_status sc = scrub(e);
-    return st != X0NE_OK ? st : sc;
+    if (!e || !ids || (!rows && n_positions) || (!positions && n_positions)) return fail(X0NE_ERR_FORMAT, "null argument");
+    std::vector<x0ne_pos_stats> stats(n ? n : 1);
+    return x0ne_engine_run(e, ids, n, route, positions, n_positions, stats.data(), rows);
 }
 
 namespace {
@@ -2215,6 +2212,9 @@ extern "C" x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size
         uint32_t am = 0;
         X0NE_TRY(x0ne_arena_read(e->arena, e->logits, 0, row.data(), vocab * 4));
         X0NE_TRY(x0ne_arena_read(e->arena, e->tokens, 0, &am, 4));
+        // A row without a finite maximum refuses the pass, as the host's read of the argmax does
+        // (engine.rs:855-864).
+        if (am >= vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
         const double lse = logsumexp_row(row.data(), vocab);
         stats[p].argmax = am;
         stats[p].logsumexp = (float)lse;
@@ -2281,6 +2281,47 @@ extern "C" x0ne_status x0ne_engine_set_decode_mode(x0ne_engine* e, uint32_t mode
 
 extern "C" uint32_t x0ne_engine_decode_mode(const x0ne_engine* e) { return e ? e->mode : 0; }
 
+namespace {
+// A new decode attention or merge: the graph is captured again (which zeroes the client
+// buffers); a failed capture leaves no graph and eager mode (engine.rs:531-560).
+x0ne_status recapture(x0ne_engine* e) {
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open: change the decode attention between requests");
+    x0ne_status st = capture(e);
+    if (st != X0NE_OK) {
+        if (e->graph) x0ne_graph_free(e->graph);
+        e->graph = nullptr;
+        e->mode = X0NE_DECODE_EAGER;
+    }
+    return st;
+}
+}  // namespace
+
+extern "C" x0ne_status x0ne_engine_set_decode_attention(x0ne_engine* e, uint32_t a) {
+    if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
+    if (a != X0NE_ATTENTION_SPLIT_K && a != X0NE_ATTENTION_PER_HEAD) return fail(X0NE_ERR_FORMAT, "unknown decode attention");
+    if (e->f64_sums && a != X0NE_ATTENTION_SPLIT_K)
+        return fail(X0NE_ERR_NOT_IMPLEMENTED, "the exact mode has one decode attention kernel (f64 split-K)");
+    if (a == e->attention && e->graph) return X0NE_OK;
+    e->attention = a;
+    return recapture(e);
+}
+
+extern "C" uint32_t x0ne_engine_decode_attention(const x0ne_engine* e) { return e ? e->attention : 0; }
+
+extern "C" x0ne_status x0ne_engine_set_split_merge(x0ne_engine* e, uint32_t m) {
+    if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
+    if (m != X0NE_MERGE_KERNEL && m != X0NE_MERGE_LAST_BLOCK) return fail(X0NE_ERR_FORMAT, "unknown split merge");
+    if (m == X0NE_MERGE_LAST_BLOCK && !e->split.grouped)
+        return fail(X0NE_ERR_GPU, "the last-block merge needs a grouped split-K kernel");
+    if (e->f64_sums && m != X0NE_MERGE_LAST_BLOCK)
+        return fail(X0NE_ERR_NOT_IMPLEMENTED, "the exact mode merges its f64 states in the last block");
+    if (m == e->merge && e->graph) return X0NE_OK;
+    e->merge = m;
+    return recapture(e);
+}
+
+extern "C" uint32_t x0ne_engine_split_merge(const x0ne_engine* e) { return e ? e->merge : 0; }
+
 extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, size_t len) {
     if (!e) return fail(X0NE_ERR_FORMAT, "null engine");
     char gpu[512];
@@ -2291,13 +2332,14 @@ extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, siz
                  : std::string("dense");
     char s[1024];
     std::snprintf(s, sizeof s,
-                  "%s, arena %llu bytes, decode graph %zu nodes, decode attention split-K P %u (grid %u x %u, %u q "
+                  "%s, arena %llu bytes, decode graph %zu nodes, decode attention %s P %u (grid %u x %u, %u q "
                   "heads per block, %u blocks per CU, merge %s), KV pages of %d positions (%llu pages, %s order), "
                   "GEMV grids qkv %u o %u gate_up %u down %u head %u (%s sums), prefill passes of %llu rows, "
                   "batch %llu (weights %s), feed-forward %s",
-                  gpu, (unsigned long long)e->arena->len, e->graph ? e->graph->nodes : (size_t)0, e->split.splits,
+                  gpu, (unsigned long long)e->arena->len, e->graph ? e->graph->nodes : (size_t)0,
+                  e->attention == X0NE_ATTENTION_PER_HEAD ? "per head (E2), split-K" : "split-K", e->split.splits,
                   e->split.grid_x, e->split.splits, e->split.group, e->split.per_cu,
-                  e->split.grouped ? "LastBlock" : "Kernel", X0NE_PAGE_C, (unsigned long long)e->pages,
+                  (e->f64_sums || e->merge == X0NE_MERGE_LAST_BLOCK) ? "LastBlock" : "Kernel", X0NE_PAGE_C, (unsigned long long)e->pages,
                   e->page_seed ? "shuffled" : "identity", e->grid_qkv, e->grid_o, e->grid_gu, e->grid_down,
                   e->grid_head, e->f64_sums ? "f64" : "f32", (unsigned long long)e->chunk,
                   (unsigned long long)e->max_batch, e->wpanel ? "row-major and in 16-row panels" : "row-major",

@@ -88,6 +88,9 @@ x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x
 x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_block, const void* q, const void* k,
                             const void* v, const void* pages, void* state, void* counter, void* out, const void* pos,
                             uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
+// The merge kernel over P = plan.splits slices of f32 states (x0ne_attention_merge_bf16).
+x0ne_status attention_merge(x0ne_gpu* g, const x0ne_split_plan& plan, const void* state, void* out, const void* pos,
+                            uint32_t q_heads, uint32_t max_ctx);
 // The decode step's attention in one launch for a grouped plan: QK-norm + RoPE of q, the K/V
 // row of position pos written into its page, split-K attention and the last-block merge. rope_cs:
 // the RoPE table of positions below max_ctx (x0ne_rope_table_f64 of inv_freq). exact: the exact

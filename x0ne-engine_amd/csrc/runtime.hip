@@ -554,6 +554,13 @@ x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_b
                              g->stream),
                  "split-K attention");
     }
+    return attention_merge(g, plan, state, out, pos, qh, max_ctx);
+}
+
+x0ne_status attention_merge(x0ne_gpu* g, const x0ne_split_plan& plan, const void* state, void* out, const void* pos,
+                            uint32_t qh, uint32_t max_ctx) {
+    uint32_t p = plan.splits;
+    if (p == 0 || p > MAX_SPLITS) return fail(X0NE_ERR_GPU, "split-K: P " + std::to_string(p) + " outside 1..=256");
     g->counts.launches++;
     void* margs[] = {(void*)&state, (void*)&out, (void*)&pos, (void*)&max_ctx, (void*)&p};
     X0NE_HIP(x0ne_launch((const void*)&x0ne_attention_merge_bf16, dim3(qh), dim3(64), margs, 0, g->stream),

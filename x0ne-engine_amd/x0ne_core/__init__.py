@@ -7,13 +7,13 @@ CPU fallback."""
 from ._lib import (ArenaError, Error, FormatError, GpuError, IoError, NotImplementedFeature, Slice, last_error,
                    lib)
 from .arena import ALIGN, Arena, Class
-from .engine import (GREEDY_AHEAD, GREEDY_AHEAD_MAX, DecodeMode, Engine, EngineOptions, Greedy, Route,
-                     Session)
+from .engine import (GREEDY_AHEAD, GREEDY_AHEAD_MAX, DecodeAttention, DecodeMode, Engine, EngineOptions, Greedy,
+                     Route, Session, SplitMerge)
 from .gpu import Arg, Gpu, Graph, Param, SplitPlan, check_args, kernel_names, kernel_set, params_of, split_state_bytes
 
 __all__ = [
-    "ALIGN", "Arena", "ArenaError", "Arg", "Class", "DecodeMode", "Engine", "EngineOptions", "Error",
+    "ALIGN", "Arena", "ArenaError", "Arg", "Class", "DecodeAttention", "DecodeMode", "Engine", "EngineOptions", "Error",
     "FormatError", "GREEDY_AHEAD", "GREEDY_AHEAD_MAX", "Gpu", "GpuError", "Graph", "Greedy", "IoError",
-    "NotImplementedFeature", "Param", "Route", "Session", "Slice", "SplitPlan", "check_args", "kernel_names",
+    "NotImplementedFeature", "Param", "Route", "Session", "Slice", "SplitMerge", "SplitPlan", "check_args", "kernel_names",
     "kernel_set", "last_error", "lib", "params_of", "split_state_bytes",
 ]

@@ -157,6 +157,10 @@ SIGNATURES = {
     "x0ne_engine_decode_batch_timed": ([P, C.POINTER(U32), SZ, SZ, SZ, SZ, C.POINTER(U32), C.POINTER(F64)], ST),
     "x0ne_engine_set_decode_mode": ([P, U32], ST),
     "x0ne_engine_decode_mode": ([P], U32),
+    "x0ne_engine_set_decode_attention": ([P, U32], ST),
+    "x0ne_engine_decode_attention": ([P], U32),
+    "x0ne_engine_set_split_merge": ([P, U32], ST),
+    "x0ne_engine_split_merge": ([P], U32),
     "x0ne_engine_logits_at": ([P, C.POINTER(U32), SZ, C.POINTER(SZ), SZ, U32, C.POINTER(F32)], ST),
     "x0ne_engine_moe_routing": ([P, C.POINTER(U32), SZ, C.POINTER(U32), SZ, C.POINTER(SZ)], ST),
     "x0ne_engine_run": ([P, C.POINTER(U32), SZ, U32, C.POINTER(SZ), SZ, C.POINTER(PosStatsC), C.POINTER(F32)], ST),

@@ -30,6 +30,18 @@ class DecodeMode(IntEnum):
     GRAPH = 1
 
 
+class DecodeAttention(IntEnum):
+    """ops.rs:55-62"""
+    SPLIT_K = 0
+    PER_HEAD = 1
+
+
+class SplitMerge(IntEnum):
+    """ops.rs:64-70"""
+    KERNEL = 0
+    LAST_BLOCK = 1
+
+
 @dataclass
 class EngineOptions:
     """EngineOptions (engine.rs:38-40) plus the KV page order (0: identity, else a seeded
@@ -240,6 +252,22 @@ class Engine:
     def decode_mode(self) -> DecodeMode:
         return DecodeMode(lib().x0ne_engine_decode_mode(self.h))
 
+    def set_decode_attention(self, a: DecodeAttention):
+        """Engine::set_decode_attention (engine.rs:531-539): re-captures the decode graph, which
+        zeroes the client buffers; call it between requests."""
+        check(lib().x0ne_engine_set_decode_attention(self.h, int(a)), "set_decode_attention")
+
+    def decode_attention(self) -> DecodeAttention:
+        return DecodeAttention(lib().x0ne_engine_decode_attention(self.h))
+
+    def set_split_merge(self, m: SplitMerge):
+        """Engine::set_split_merge (engine.rs:547-560): LAST_BLOCK needs a grouped split-K kernel
+        (GpuError otherwise); re-captures the decode graph."""
+        check(lib().x0ne_engine_set_split_merge(self.h, int(m)), "set_split_merge")
+
+    def split_merge(self) -> SplitMerge:
+        return SplitMerge(lib().x0ne_engine_split_merge(self.h))
+
     def graph_nodes(self) -> int:
         return lib().x0ne_engine_graph_nodes(self.h)
 
@@ -303,6 +331,15 @@ class Session:
     def __del__(self):
         self._drop()
 
+    # A `with` block is the scope a Rust Session lives in: leaving it by an exception drops the
+    # session (zeroing the client bytes), as unwinding a panic drops it (engine.rs:1346-1353).
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self._drop()
+        return False
+
     def logits(self) -> np.ndarray:
         """f32 logits of the last position (a copy; empty after a failed step)."""
         ptr = C.POINTER(C.c_float)()
@@ -350,6 +387,13 @@ class Greedy:
 
     def __del__(self):
         self._drop()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self._drop()
+        return False
 
     def next_token(self) -> int:
         out = C.c_uint32()

@@ -411,6 +411,7 @@ class Kernels:
         a.write(sl["k"], 0, kp)
         a.write(sl["v"], 0, vp)
         a.write(sl["pt"], 0, np.array(page_of, np.uint32))
+        self._uploaded = (kp, vp)
         return a, sl
 
     def _check_attention(self, q, k, v, ctx, h: Heads, rows=1):
@@ -512,14 +513,20 @@ class Kernels:
         pages = n_pages(ctx)
         page_of = list(range(pages)) if page_of is None else list(page_of)
         pg, slot = page_of[(ctx - 1) // PAGE], (ctx - 1) % PAGE
-        k_rows, v_rows = [], []
-        v_all = None
-        for kh in range(h.kv_heads):
-            at = ((pg * h.kv_heads + kh) * PAGE + slot) * HEAD_DIM
-            k_rows.append(a.read_array(s["k"], at * 2, HEAD_DIM, np.uint16))
-            if v_all is None:
-                v_all = a.read_array(s["v"], 0, s["v"].len // 2, np.uint16)
-            v_rows.append(v_all[[v_offset(pg, h.kv_heads, kh, slot, d) for d in range(HEAD_DIM)]])
+        # The planes as the kernel left them: the K row and V column of position ctx - 1 in page
+        # pg, and every other element as uploaded (ops.rs:322-373, the sentinel check).
+        k_all = a.read_array(s["k"], 0, s["k"].len // 2, np.uint16)
+        v_all = a.read_array(s["v"], 0, s["v"].len // 2, np.uint16)
+        k_up, v_up = self._uploaded
+        pool = k_all.size // (h.kv_heads * PAGE * HEAD_DIM)
+        k4 = k_all.reshape(pool, h.kv_heads, PAGE, HEAD_DIM)
+        v4 = v_all.reshape(pool, h.kv_heads, HEAD_DIM, PAGE)
+        k_rows = [k4[pg, kh, slot, :].copy() for kh in range(h.kv_heads)]
+        v_rows = [v4[pg, kh, :, slot].copy() for kh in range(h.kv_heads)]
+        k_rest, v_rest = k4.copy(), v4.copy()
+        k_rest[pg, :, slot, :] = k_up.reshape(k4.shape)[pg, :, slot, :]
+        v_rest[pg, :, :, slot] = v_up.reshape(v4.shape)[pg, :, :, slot]
+        self.kv_rest_untouched = bool((k_rest.ravel() == k_up.ravel()).all() and (v_rest.ravel() == v_up.ravel()).all())
         return a.read_array(s["out"], 0, qd, np.uint16), np.concatenate(k_rows), np.concatenate(v_rows)
 
     def attention_rope_decode_batch(self, qkv, q_norm, k_norm, eps: float, theta: float, ks, vs, ctxs, h: Heads,
@@ -589,10 +596,15 @@ class Kernels:
         k_all = a.read_array(sl["k"], 0, kp.size, np.uint16).reshape(kp.shape)
         v_all = a.read_array(sl["v"], 0, vp.size, np.uint16).reshape(vp.shape)
         k_rows, v_rows = [], []
+        k_rest, v_rest = k_all.copy(), v_all.copy()
         for b, c in enumerate(ctxs):
             pg, slot = order[b * sp + (c - 1) // PAGE], (c - 1) % PAGE
             k_rows.append(k_all[pg, :, slot, :].reshape(-1).copy())
             v_rows.append(v_all[pg, :, :, slot].reshape(-1).copy())
+            k_rest[pg, :, slot, :] = kp[pg, :, slot, :]
+            v_rest[pg, :, :, slot] = vp[pg, :, :, slot]
+        # Every sequence's K row and V column at its own position, nothing else (ops.rs:322-373).
+        self.kv_rest_untouched = bool((k_rest == kp).all() and (v_rest == vp).all())
         return out, k_rows, v_rows
 
     FEW_KERNELS = {(1, 1): 8, (1, 2): 8, (1, 4): 8, (1, 8): 8, (2, 1): 8, (2, 2): 8, (4, 1): 8}
