@@ -150,6 +150,17 @@ x0ne_status x0ne_gpu_attention_split(x0ne_gpu* g, const x0ne_split_plan* plan, i
                                      uint64_t k, uint64_t v, uint64_t page_table, uint64_t state, uint64_t counter,
                                      uint64_t out, uint64_t pos, uint32_t q_heads, uint32_t kv_heads,
                                      uint32_t max_ctx, float scale);
+/* x0ne_gpu_attention_split without a workspace argument and without allocating: no counterpart
+   in the reference. For callers that cannot allocate device memory (code under HIP graph
+   capture, tight serving loops, harnesses that forbid hipMalloc). The split-K states and the
+   last-block counters live in a static device array of this library (4 MiB of states and 256
+   counter words per GPU, held until the process ends); the counters are zeroed by a fill kernel
+   at the start of each call. X0NE_ERR_FORMAT when x0ne_split_state_bytes(q_heads, P) exceeds
+   4 MiB or kv_heads exceeds 256. Every call on a GPU shares that GPU's array and it keeps the
+   last call's contents: calls that overlap on one GPU (other streams, other threads) race. */
+x0ne_status x0ne_gpu_attention_split_scratch(x0ne_gpu* g, const x0ne_split_plan* plan, int last_block, uint64_t q,
+                                             uint64_t k, uint64_t v, uint64_t page_table, uint64_t out, uint64_t pos,
+                                             uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
 /* split_state_bytes (ops.rs:125-127) */
 uint64_t x0ne_split_state_bytes(uint32_t q_heads, uint32_t splits);
 /* BASELINE.json config 2, the isolated decode attention of ops.rs:585-681: the grouped split-K

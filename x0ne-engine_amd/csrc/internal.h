@@ -46,6 +46,9 @@ struct x0ne_gpu {
     uint64_t total_mem = 0;
     x0ne::Counts counts;
     bool capturing = false;
+    // This device's copy of the library's static scratch array (runtime.hip, `scratch`), as
+    // hipGetSymbolAddress gave it at x0ne_gpu_new with the device current.
+    void* scratch = nullptr;
 };
 
 struct x0ne_graph {

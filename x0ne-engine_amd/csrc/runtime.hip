@@ -53,6 +53,14 @@ extern "C" size_t x0ne_kernel_set(char* buf, size_t len) {
 // The device (gpu.rs:750-928)
 // ---------------------------------------------------------------------------------------------
 
+// Split-K workspace for callers that cannot allocate (x0ne_gpu_attention_split_scratch): the
+// f32 slice states, then one counter word per kv head. Each GPU holds its own copy for the life
+// of the process; every call on a GPU shares it, so calls that overlap on one GPU race.
+constexpr uint64_t SCRATCH_STATE_BYTES = 4ull << 20;
+constexpr uint64_t SCRATCH_COUNTERS = 256;
+constexpr uint64_t SCRATCH_BYTES = SCRATCH_STATE_BYTES + SCRATCH_COUNTERS * 4;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
 extern "C" x0ne_status x0ne_gpu_new(x0ne_gpu** out) {
     if (!out) return fail(X0NE_ERR_FORMAT, "x0ne_gpu_new: null out");
     *out = nullptr;
@@ -68,6 +76,13 @@ extern "C" x0ne_status x0ne_gpu_new(x0ne_gpu** out) {
         return fail(X0NE_ERR_GPU, "device 0 is " + arch + ": the kernels are built for gfx950 only");
     x0ne_gpu* g = new x0ne_gpu();
     g->device = 0;
+    // The device address of this device's scratch array (device 0 is current): host code uses
+    // this pointer, never the array's name, which on the host is only a stand-in.
+    e = hipGetSymbolAddress(&g->scratch, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !g->scratch) {
+        delete g;
+        return gpu_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    }
     g->name = p.name;
     g->arch = arch;
     g->cus = (uint32_t)p.multiProcessorCount;
@@ -595,6 +610,34 @@ extern "C" x0ne_status x0ne_gpu_split_plan(const x0ne_gpu* g, uint32_t q_heads, 
                                            x0ne_split_plan* out) {
     if (!g || !out) return fail(X0NE_ERR_GPU, "no device");
     return split_plan(g, q_heads, kv_heads, out);
+}
+
+// x0ne_gpu_attention_split with its workspace in the library's scratch array: the states at its
+// start, the counters after SCRATCH_STATE_BYTES. The counters are zeroed by a fill kernel first
+// (a kernel, not a memset, so the call may be captured into a graph); nothing is allocated.
+extern "C" x0ne_status x0ne_gpu_attention_split_scratch(x0ne_gpu* g, const x0ne_split_plan* plan, int last_block,
+                                                        uint64_t q, uint64_t k, uint64_t v, uint64_t page_table,
+                                                        uint64_t out, uint64_t pos, uint32_t q_heads,
+                                                        uint32_t kv_heads, uint32_t max_ctx, float scale) {
+    if (!g || !plan) return fail(X0NE_ERR_GPU, "no device");
+    if (!g->scratch) return fail(X0NE_ERR_GPU, "no scratch array on this device");
+    const uint64_t state_bytes = x0ne_split_state_bytes(q_heads, plan->splits);
+    if (state_bytes > SCRATCH_STATE_BYTES || kv_heads > SCRATCH_COUNTERS)
+        return fail(X0NE_ERR_FORMAT, "split-K scratch: " + std::to_string(q_heads) + " q heads x P " +
+                                         std::to_string(plan->splits) + " need " + std::to_string(state_bytes) +
+                                         " bytes of states and " + std::to_string(kv_heads) +
+                                         " counters; the static scratch holds " +
+                                         std::to_string(SCRATCH_STATE_BYTES) + " bytes and " +
+                                         std::to_string(SCRATCH_COUNTERS) + " counters");
+    uint8_t* base = static_cast<uint8_t*>(g->scratch);
+    void* counter = base + SCRATCH_STATE_BYTES;
+    if (last_block) {
+        g->counts.launches++;
+        X0NE_HIP(x0ne_launch_fill_u16(static_cast<uint16_t*>(counter), 2ull * kv_heads, 0, g->stream),
+                 "zero the scratch counters");
+    }
+    return attention_split(g, *plan, last_block, (const void*)q, (const void*)k, (const void*)v, (const void*)page_table,
+                           base, counter, (void*)out, (const void*)pos, q_heads, kv_heads, max_ctx, scale);
 }
 
 extern "C" x0ne_status x0ne_gpu_attention_split(x0ne_gpu* g, const x0ne_split_plan* plan, int last_block, uint64_t q,

@@ -112,6 +112,8 @@ SIGNATURES = {
     "x0ne_gpu_split_plan": ([P, U32, U32, C.POINTER(SplitPlanC)], ST),
     "x0ne_gpu_attention_split": ([P, C.POINTER(SplitPlanC), I32, U64, U64, U64, U64, U64, U64, U64, U64,
                                   U32, U32, U32, F32], ST),
+    "x0ne_gpu_attention_split_scratch": ([P, C.POINTER(SplitPlanC), I32, U64, U64, U64, U64, U64, U64,
+                                          U32, U32, U32, F32], ST),
     "x0ne_split_state_bytes": ([U32, U32], U64),
     "x0ne_gpu_time_attention": ([P, U32, U32, U32, U32, U32, U64, C.POINTER(F64), C.POINTER(U32)], ST),
     "x0ne_gpu_capture_begin": ([P], ST),

@@ -190,6 +190,14 @@ class Gpu:
         check(lib().x0ne_gpu_attention_split(self.h, C.byref(pc), int(last_block), q, k, v, pages, state, counter,
                                               out, pos, q_heads, kv_heads, max_ctx, scale), "split-K attention")
 
+    def attention_split_scratch(self, plan: SplitPlan, last_block: bool, q, k, v, pages, out, pos, q_heads, kv_heads,
+                                max_ctx, scale):
+        """attention_split with the states and counters in the library's static scratch array
+        (x0ne_gpu_attention_split_scratch: no workspace argument, no allocation)."""
+        pc = plan.c()
+        check(lib().x0ne_gpu_attention_split_scratch(self.h, C.byref(pc), int(last_block), q, k, v, pages, out, pos,
+                                                      q_heads, kv_heads, max_ctx, scale), "split-K attention (scratch)")
+
     def time_attention(self, q_heads: int, kv_heads: int, ctx: int, splits: int, iters: int, seed: int = 0):
         """the isolated split-K decode attention over more than 512 MiB of
         rotating K/V planes; (mean kernel µs per launch, planes rotated)."""

@@ -458,6 +458,24 @@ class Kernels:
             raise GpuError(f"split-K counters not reset: {counts.tolist()}")
         return a.read_array(s["out"], 0, h.q_dim, np.uint16)
 
+    def attention_decode_split_scratch(self, q, k, v, ctx: int, h: Heads, last_block=None, splits=None,
+                                       page_of=None, pool=None) -> np.ndarray:
+        """attention_decode_split through x0ne_gpu_attention_split_scratch: the states and
+        counters in the library's static scratch array, nothing allocated for them."""
+        self._check_attention(q, k, v, ctx, h)
+        plan = self.split_plan(h)
+        if splits is not None:
+            plan.splits = int(splits)
+        if last_block is None:
+            last_block = plan.grouped
+        a, s = self._kv_arena(q, k, v, ctx, h, page_of, pool, [("out", h.q_dim * 2)])
+        a.write(s["pos"], 0, np.array([ctx - 1], np.uint32))
+        self.gpu.attention_split_scratch(plan, last_block, a.ptr(s["q"]), a.ptr(s["k"]), a.ptr(s["v"]),
+                                         a.ptr(s["pt"]), a.ptr(s["out"]), a.ptr(s["pos"]), h.q_heads, h.kv_heads,
+                                         ctx, attn_scale(h.head_dim))
+        self.gpu.sync()
+        return a.read_array(s["out"], 0, h.q_dim, np.uint16)
+
     def attention_rope_decode(self, qkv, q_norm, k_norm, eps: float, theta: float, k, v, ctx: int, h: Heads,
                               last_block=True, splits=None, page_of=None, pool=None, exact=False):
         """The engine's fused decode attention (one launch per layer): QK-norm + RoPE of the q
