@@ -188,8 +188,9 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
     B = args.batch
     prompts = np.stack([splitmix_ids(args.prompt, cfg["vocab_size"], SEED + b) for b in range(B)])
     n_tokens = args.warmup + args.steps + 1
+    max_ctx = args.prompt + max(n_tokens, 64) + 16  # room for the oracle fixture's 64 steps too
     t = time.perf_counter()
-    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=args.prompt + n_tokens + 16, page_seed=1,
+    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=max_ctx, page_seed=1,
                                                             max_batch=B))
     if args.eager:
         e.set_decode_mode(DecodeMode.EAGER)
@@ -239,6 +240,32 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
           f"others {others}", file=sys.stderr, flush=True)
     if args.calibrate_copy:
         copy_calibration(args.calibrate_copy << 20)
+
+    # Parity of the timed path: its greedy tokens against the CPU oracle's committed fixture for
+    # this workload (64 steps), and the other accumulation mode timed and checked the same way.
+    fixture = oracle_fixture(args.model, prompt)
+    parity = {"oracle_fixture": fixture["path"] if fixture else None,
+              "timed_path": mode_parity(e, prompt, fixture, args.f64_sums)}
+    if not args.no_other_mode:
+        e.close()
+        other = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=max_ctx, page_seed=1,
+                                                                    f64_sums=not args.f64_sums))
+        if args.eager:
+            other.set_decode_mode(DecodeMode.EAGER)
+        o_runs = []
+        for _ in range(max(1, min(args.runs, 2))):
+            o_toks, o_secs = other.decode_timed(prompt, args.warmup, args.steps)
+            o_runs.append(o_secs)
+        o_secs = min(o_runs)
+        o = mode_parity(other, prompt, fixture, not args.f64_sums)
+        o.update({"value": round(args.steps / o_secs, 3), "unit": "tok/s", "ms_per_step": round(1e3 * o_secs / args.steps, 4),
+                  "decode_hbm_frac": round(step_bytes * args.steps / o_secs / 1e9 / 8000.0, 4),
+                  "same_tokens_as_timed_path": int(next((i for i in range(min(o_toks.size, tokens.size))
+                                                         if o_toks[i] != tokens[i]), min(o_toks.size, tokens.size)))})
+        parity["other_mode"] = o
+        other.close()
+        print(f"[bench] other mode {o}", file=sys.stderr, flush=True)
+    print(f"[bench] parity {parity['timed_path']}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
@@ -280,6 +307,42 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
     }
 
 
+FIXTURES = {"8b": "oracle_greedy_8b.json", "0.6b": "oracle_greedy_0_6b.json"}
+
+
+def oracle_fixture(model: str, prompt: np.ndarray):
+    """The CPU oracle's greedy tokens for this workload (tests/golden/make_oracle_greedy.py), when
+    one is committed for this shape and prompt."""
+    name = FIXTURES.get(model)
+    if name is None:
+        return None
+    path = os.path.join(ROOT, "tests", "golden", name)
+    try:
+        with open(path) as fh:
+            fx = json.load(fh)
+    except OSError:
+        return None
+    if fx["prompt"] != prompt.tolist() or fx["seed"] != SEED or fx["std"] != STD:
+        return None
+    return {"path": os.path.relpath(path, ROOT), "tokens": np.array(fx["tokens"], np.uint32),
+            "margins": fx["margins"]}
+
+
+def mode_parity(e, prompt, fixture, f64: bool) -> dict:
+    """The engine's greedy tokens against the oracle fixture's: how many of the first steps agree,
+    and the oracle's top-2 margin where they first differ."""
+    out = {"mode": "f64 sums (exact mode)" if f64 else "f32 sums"}
+    if fixture is None:
+        out["tokens_equal_to_oracle"] = None
+        return out
+    n = fixture["tokens"].size
+    got = e.greedy(prompt, n)
+    agree = next((i for i in range(n) if got[i] != fixture["tokens"][i]), n)
+    out.update({"tokens_equal_to_oracle": agree, "of": n,
+                "oracle_margin_at_first_difference": None if agree == n else round(fixture["margins"][agree], 6)})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -291,7 +354,10 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch each step's kernels one by one instead of replaying the captured graph "
                          "(for kernel-trace profilers; the same kernels and results)")
-    ap.add_argument("--f64-sums", action="store_true", help="f64 accumulation in the GEMVs")
+    ap.add_argument("--f64-sums", action="store_true",
+                    help="time the exact mode (f64 sums in the projections and attention) instead of the f32 path")
+    ap.add_argument("--no-other-mode", action="store_true",
+                    help="skip timing the other accumulation mode (f64 sums when the f32 path is timed, and back)")
     ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt tokens (config 4: 8192)")
     ap.add_argument("--model", choices=sorted(MODELS), default="8b", help="the Qwen3 shape (default 8b)")
     ap.add_argument("--batch", type=int, default=1,
@@ -319,8 +385,9 @@ def main():
         return
     prompt = splitmix_ids(args.prompt, cfg["vocab_size"], SEED)
     n_tokens = args.warmup + args.steps + 1
+    max_ctx = args.prompt + max(n_tokens, 64) + 16  # room for the oracle fixture's 64 steps too
     t = time.perf_counter()
-    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=args.prompt + n_tokens + 16, page_seed=1,
+    e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=max_ctx, page_seed=1,
                                                             f64_sums=args.f64_sums))
     if args.eager:
         e.set_decode_mode(DecodeMode.EAGER)
@@ -377,6 +444,32 @@ def main():
     if args.calibrate_copy:
         copy_calibration(args.calibrate_copy << 20)
 
+    # Parity of the timed path: its greedy tokens against the CPU oracle's committed fixture for
+    # this workload (64 steps), and the other accumulation mode timed and checked the same way.
+    fixture = oracle_fixture(args.model, prompt)
+    parity = {"oracle_fixture": fixture["path"] if fixture else None,
+              "timed_path": mode_parity(e, prompt, fixture, args.f64_sums)}
+    if not args.no_other_mode:
+        e.close()
+        other = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=max_ctx, page_seed=1,
+                                                                    f64_sums=not args.f64_sums))
+        if args.eager:
+            other.set_decode_mode(DecodeMode.EAGER)
+        o_runs = []
+        for _ in range(max(1, min(args.runs, 2))):
+            o_toks, o_secs = other.decode_timed(prompt, args.warmup, args.steps)
+            o_runs.append(o_secs)
+        o_secs = min(o_runs)
+        o = mode_parity(other, prompt, fixture, not args.f64_sums)
+        o.update({"value": round(args.steps / o_secs, 3), "unit": "tok/s", "ms_per_step": round(1e3 * o_secs / args.steps, 4),
+                  "decode_hbm_frac": round(step_bytes * args.steps / o_secs / 1e9 / 8000.0, 4),
+                  "same_tokens_as_timed_path": int(next((i for i in range(min(o_toks.size, tokens.size))
+                                                         if o_toks[i] != tokens[i]), min(o_toks.size, tokens.size)))})
+        parity["other_mode"] = o
+        other.close()
+        print(f"[bench] other mode {o}", file=sys.stderr, flush=True)
+    print(f"[bench] parity {parity['timed_path']}", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
@@ -418,6 +511,7 @@ def main():
                      "other_kernels": others},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "parity": parity,
         "tokens_head": tokens[:8].tolist(),
     }
     print(json.dumps(line))
