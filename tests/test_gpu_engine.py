@@ -571,11 +571,74 @@ def test_a_moe_of_identical_experts_is_the_dense_model(experts, top_k):
     assert e.client_data_is_zero()
 
 
+class HostMoe:
+    """The MoE decode step composed on the host from the oracle's kernels (oracle/src/lib.rs): the
+    dense step of model.rs:196-262 with each layer's MLP replaced as engine.rs:795-815 does it:
+    router GEMV (f32 logits) -> moe_route -> expert [gate; up] GEMVs (bf16) -> SwiGLU (bf16) ->
+    expert down GEMVs (f32) -> the weighted combination (bf16)."""
+
+    def __init__(self, cfg, experts, top_k, mi, tensors):
+        self.c, self.E, self.K, self.mi = cfg, experts, top_k, mi
+        self.W = {k: O.bf16_values(b).astype(np.float32) for k, (_, b) in tensors.items()}
+        self.inv = O.inv_freq_f32(cfg.head_dim, cfg.theta)
+
+    def layer(self, l, leaf):
+        return self.W[f"model.layers.{l}.{leaf}.weight"]
+
+    def run(self, ids):
+        c, hd = self.c, self.c.head_dim
+        qd, kvd, h = c.q_heads * hd, c.kv_heads * hd, c.hidden
+        K = [[] for _ in range(c.layers)]
+        V = [[] for _ in range(c.layers)]
+        rows, routes, router_logits = [], [], []
+        for pos, tok in enumerate(ids):
+            residual = np.zeros(h, np.float32)
+            delta = O.embedding(self.W["model.embed_tokens.weight"], h, int(tok))
+            route_p, logit_p = [], []
+            for l in range(c.layers):
+                residual, x = O.add_rmsnorm(residual, delta, self.layer(l, "input_layernorm"), c.eps)
+                x = O.bf16_round(x)
+                wqkv = np.concatenate([self.layer(l, "self_attn.q_proj"), self.layer(l, "self_attn.k_proj"),
+                                       self.layer(l, "self_attn.v_proj")])
+                qkv = O.bf16_round(O.gemv(wqkv, qd + 2 * kvd, h, x))
+                q, k, v = O.qk_norm_rope(qkv, self.layer(l, "self_attn.q_norm"), self.layer(l, "self_attn.k_norm"),
+                                         self.inv, c.q_heads, c.kv_heads, hd, pos, c.eps)
+                K[l].append(O.bf16_round(k))
+                V[l].append(v)
+                attn = O.bf16_round(O.attention_decode(O.bf16_round(q), np.concatenate(K[l]), np.concatenate(V[l]),
+                                                       pos + 1, c.q_heads, c.kv_heads))
+                delta = O.bf16_round(O.gemv(self.layer(l, "self_attn.o_proj"), h, qd, attn))
+                residual, x = O.add_rmsnorm(residual, delta, self.layer(l, "post_attention_layernorm"), c.eps)
+                x = O.bf16_round(x)
+                lg = O.gemv(self.W[f"model.layers.{l}.mlp.gate.weight"], self.E, h, x)
+                eids, wts = O.moe_route(lg, self.E, self.K)
+                gu_all = np.concatenate([np.concatenate([self.W[f"model.layers.{l}.mlp.experts.{e}.gate_proj.weight"],
+                                                         self.W[f"model.layers.{l}.mlp.experts.{e}.up_proj.weight"]])
+                                         for e in range(self.E)])
+                gu = O.bf16_round(O.moe_gemv(gu_all, self.E, 2 * self.mi, h, eids, x, self.K))
+                act = O.bf16_round(np.concatenate([O.swiglu(gu[s * 2 * self.mi:(s + 1) * 2 * self.mi])
+                                                   for s in range(self.K)]))
+                d_all = np.concatenate([self.W[f"model.layers.{l}.mlp.experts.{e}.down_proj.weight"]
+                                        for e in range(self.E)])
+                y = O.moe_gemv(d_all, self.E, h, self.mi, eids, act, 1)
+                delta = O.bf16_round(O.moe_combine(y, wts, h, self.K))
+                route_p.append(eids)
+                logit_p.append(lg)
+            residual, x = O.add_rmsnorm(residual, delta, self.W["model.norm.weight"], c.eps)
+            head = self.W["model.embed_tokens.weight"] if c.tied else self.W["lm_head.weight"]
+            rows.append(O.gemv(head, c.vocab, h, O.bf16_round(x)))
+            routes.append(np.stack(route_p))
+            router_logits.append(np.stack(logit_p))
+        return rows, np.stack(routes), router_logits
+
+
 def test_a_random_moe_routes_each_token_to_distinct_experts():
-    """Eight experts of their own, two per token, a random router: each layer's routing at each
-    position names two distinct experts below 8; the step is the same bits graph and eager and
-    over repeated requests; greedy decoding runs through the captured graph; a dense engine has
-    no routing to report."""
+    """Eight experts of their own, two per token, a random router, against the MoE step composed
+    from the oracle's kernels (HostMoe): the engine's routing at every layer and position is the
+    host's (a differing pick only where the host's two router logits are within the GEMV
+    tolerance of each other, the comparison ending there), its logits within the model tolerance
+    at every position; the step is the same bits graph and eager and over repeated requests;
+    greedy decoding runs through the captured graph; a dense engine has no routing to report."""
     from x0ne_core import DecodeMode, Engine, EngineOptions, Route
     f = Fixture(tiny(2, 4, 2, False), 43)
     g = np.random.default_rng(44)
@@ -602,6 +665,21 @@ def test_a_random_moe_routes_each_token_to_distinct_experts():
     route = e.moe_routing(ids).reshape(16, f.cfg.layers, 2)
     assert (route < 8).all() and (route[..., 0] != route[..., 1]).all()
     assert len(set(route.reshape(-1).tolist())) > 2, "the router spreads the tokens"
+    want_rows, want_route, router_logits = HostMoe(f.cfg, 8, 2, 64, out).run(ids)
+    upto = len(ids)
+    for p in range(len(ids)):
+        for l in range(f.cfg.layers):
+            if (route[p, l] != want_route[p, l]).any():
+                lg = router_logits[p][l]
+                picked = sorted(set(route[p, l].tolist()) ^ set(want_route[p, l].tolist()))
+                gap = abs(float(lg[picked[0]]) - float(lg[picked[-1]]))
+                assert gap <= 1e-3 * float(np.abs(lg).max()), f"position {p} layer {l}: routing differs at gap {gap}"
+                upto = min(upto, p)
+    rows = e.logits_at(ids, list(range(upto)), Route.DECODE)
+    for p in range(upto):
+        assert_logits(f"random moe position {p}", rows[p], want_rows[p])
+    print(f"MEASURE random MoE: routing equal to the host's at {upto} of {len(ids)} positions, logits compared there")
+    assert upto >= 8
     a = e.logits_at(ids, [3, 15], Route.DECODE)
     b = e.logits_at(ids, [3, 15], Route.DECODE)
     e.set_decode_mode(DecodeMode.EAGER)

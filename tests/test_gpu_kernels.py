@@ -458,6 +458,45 @@ def test_batched_attention_is_each_sequence_alone_bit_for_bit(kernels, qh, kvh):
             assert_close(what, bf16_vals(out[b]), want, ATTENTION_ATOL_OF_VMAX * max_abs(vb), 0.0)
 
 
+@pytest.mark.parametrize("ctx", [8192, 32768])
+def test_config2_decode_attention_at_long_contexts(kernels, ctx):
+    """BASELINE.json config 2 at its long contexts: 32 q / 8 kv heads, head_dim 128, bf16 Q, K and V
+    drawn N(0, 1) from a seed, the keys in 16-position pages in a shuffled order, split-K at P 1,
+    4, 16 and the engine's plan: within max|V|/128 of the oracle (gpu_kernels.rs:437-599), the
+    merge kernel and the last-block merge the same bits, a repeated launch the same bits; and
+    the fused kernel (QK-norm, RoPE and the K/V write in front) on the same cache."""
+    from x0ne_core.ops import CacheAt
+    h = H(32, 8)
+    g = np.random.default_rng(ctx)
+    normal = lambda n: bf16_bits(g.standard_normal(n).astype(np.float32))
+    q, k, v = normal(h.q_dim), normal(ctx * h.kv_dim), normal(ctx * h.kv_dim)
+    pages = ctx // 16
+    page_of = [int(p) for p in g.permutation(pages)]
+    want = O.attention_decode(bf16_vals(q), bf16_vals(k), bf16_vals(v), ctx, 32, 8)
+    atol = ATTENTION_ATOL_OF_VMAX * max_abs(bf16_vals(v))
+    for splits in (1, 4, 16, None):
+        outs = []
+        for last_block in (True, False, True):
+            out = kernels.attention_decode_split(q, k, v, ctx, h, last_block=last_block, splits=splits,
+                                                 page_of=page_of)
+            outs.append(out)
+        what = f"config 2 ctx {ctx} P {splits}"
+        assert_close(what, bf16_vals(outs[0]), want, atol, 0.0)
+        assert (outs[0] == outs[1]).all(), f"{what}: the two merges differ"
+        assert (outs[0] == outs[2]).all(), f"{what}: a repeat differs"
+    qkv = np.concatenate([q, normal(2 * h.kv_dim)])
+    qn, kn = bf16_bits(np.ones(128, np.float32)), bf16_bits(np.ones(128, np.float32))
+    out, k_row, v_row = kernels.attention_rope_decode(qkv, qn, kn, 1e-6, 1e6, k[:(ctx - 1) * h.kv_dim],
+                                                      v[:(ctx - 1) * h.kv_dim], ctx, h, page_of=page_of)
+    assert kernels.kv_rest_untouched, f"fused ctx {ctx}: a K/V byte other than the new row changed"
+    rope = kernels.qk_norm_rope_kv_write(qkv, qn, kn, h, 1e6, 1e-6, CacheAt(1, ctx, 0, ctx - 1))
+    kb = np.concatenate([k[:(ctx - 1) * h.kv_dim], rope.k_row])
+    vb = np.concatenate([v[:(ctx - 1) * h.kv_dim], rope.v_row])
+    want = O.attention_decode(bf16_vals(rope.q), bf16_vals(kb), bf16_vals(vb), ctx, 32, 8)
+    assert_close(f"config 2 fused ctx {ctx}", bf16_vals(out), want, ATTENTION_ATOL_OF_VMAX * max_abs(bf16_vals(vb)),
+                 0.0)
+
+
 @pytest.mark.parametrize("qh,kvh", [(1, 1), (2, 1), (16, 8), (32, 8), (64, 8)])
 def test_exact_attention_is_the_f64_oracle_bit_for_bit(kernels, qh, kvh):
     """The exact mode's fused attention (f64 scores, softmax and sums) gives the bits of the f64
@@ -684,6 +723,63 @@ def test_moe_kernels_are_the_reference(kernels, seed):
     wts = np.asarray(rng.f32s(rows * top_k, 1.0), np.float32)
     got = bf16_vals(kernels.moe_combine(y, wts, hidden, top_k))
     assert_close(f"moe combine {what}", got, O.moe_combine(y, wts, hidden, top_k), 1e-4, BF16_RTOL)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_the_fused_moe_projections_are_the_composed_oracle(kernels, seed):
+    """The kernels the MoE step runs: [gate; up] with SwiGLU behind against the oracle's expert
+    GEMV then swiglu (oracle/src/lib.rs:284-312, :205-214), and down with the weighted
+    combination behind against the oracle's f32 expert GEMV then combination (:314-329); the
+    projections within the GEMV tolerance, each activation within the SwiGLU of its gate and up
+    intervals, the combination within one bf16 rounding past them; a slot without an expert gives
+    NaN."""
+    rng = O.Rng(850 + seed)
+    experts = rng.pick([2, 8, 64])
+    top_k = rng.range(1, min(experts, 8))
+    inter = 8 * rng.range(1, 40)
+    hidden = 8 * rng.range(1, 64)
+    wgu = np.asarray(rng.bf16s(experts * 2 * inter * hidden, 0.2), np.float32)
+    wd = np.asarray(rng.bf16s(experts * hidden * inter, 0.2), np.float32)
+    x = np.asarray(rng.bf16s(hidden, 2.0), np.float32)
+    ids = np.array([rng.below(experts) for _ in range(top_k)], np.uint32)
+    if seed == 3:
+        ids[-1] = O.MOE_NO_EXPERT
+    wts = np.asarray(rng.f32s(top_k, 1.0), np.float32)
+    what = f"seed {seed}: {experts} experts, top {top_k}, inter {inter}, hidden {hidden}"
+    gu = O.moe_gemv(wgu, experts, 2 * inter, hidden, ids, x, top_k).reshape(top_k, 2 * inter)
+    act = bf16_vals(kernels.moe_gate_up_swiglu(bf16_bits(wgu), experts, inter, hidden, ids, bf16_bits(x)))
+    act = act.reshape(top_k, inter)
+    want_act = O.bf16_round(np.stack([O.swiglu(O.bf16_round(gu[s])) for s in range(top_k)]))
+    for s in range(top_k):
+        if ids[s] == O.MOE_NO_EXPERT:
+            assert np.isnan(act[s]).all(), f"{what}: slot {s} without an expert"
+            continue
+        e = int(ids[s])
+        mag = O.gemv_magnitude(wgu[e * 2 * inter * hidden:(e + 1) * 2 * inter * hidden], 2 * inter, hidden, x)
+        tol = F32_RTOL * mag + 1e-30
+        for i in range(inter):
+            g, u = float(gu[s, i]), float(gu[s, inter + i])
+            cands = [O.swiglu(np.array([gg, uu], np.float32))[0]
+                     for gg in O.bf16_round(np.array([g - tol[i], g + tol[i]], np.float32))
+                     for uu in O.bf16_round(np.array([u - tol[inter + i], u + tol[inter + i]], np.float32))]
+            lo, hi = O.bf16_round(np.float32(min(cands)))[0], O.bf16_round(np.float32(max(cands)))[0]
+            assert lo - abs(lo) * 2 ** -7 <= act[s, i] <= hi + abs(hi) * 2 ** -7, f"{what}: act [{s}][{i}]"
+    exact = float((bf16_bits(act) == bf16_bits(want_act)).mean())
+    ok = ids != O.MOE_NO_EXPERT
+    y = O.moe_gemv(wd, experts, hidden, inter, ids, want_act, 1).reshape(top_k, hidden)
+    out = bf16_vals(kernels.moe_down_combine(bf16_bits(wd), experts, hidden, inter, ids, wts,
+                                             bf16_bits(want_act.ravel())))
+    want = O.moe_combine(y, wts, hidden, top_k)
+    if not ok.all():
+        assert np.isnan(out).all(), f"{what}: a slot without an expert makes the row NaN"
+    else:
+        mags = np.stack([O.gemv_magnitude(wd[int(e) * hidden * inter:(int(e) + 1) * hidden * inter], hidden, inter,
+                                          want_act[s]) for s, e in enumerate(ids)])
+        atol = F32_RTOL * (np.abs(wts)[:, None] * mags).sum(0) + 1e-6
+        r = np.abs(out.astype(np.float64) - want) / (atol + BF16_RTOL * np.abs(want))
+        print(f"MEASURE moe down + combination {what}: worst ratio {r.max():.4f}")
+        assert (r <= 1.0).all(), f"{what}: output {int(np.argmax(r))}"
+    print(f"MEASURE fused moe {what}: {exact:.4f} of the activations bit-equal to the oracle's")
 
 
 def test_moe_routing_refuses_what_the_kernel_does_not_take(kernels):

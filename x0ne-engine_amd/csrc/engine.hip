@@ -420,8 +420,8 @@ struct x0ne_engine {
     x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{}, b_argmax{};
     // The MoE feed-forward's rows: the normed x, the router's f32 logits, each layer's chosen
     // expert ids and weights ([layers][top_k], read back by x0ne_engine_moe_routing), the chosen
-    // experts' [gate; up] rows, activations and f32 down rows.
-    x0ne_slice m_x{}, m_logits{}, m_ids{}, m_w{}, m_gu{}, m_act{}, m_y{};
+    // experts' SwiGLU activations.
+    x0ne_slice m_x{}, m_logits{}, m_ids{}, m_w{}, m_act{};
     std::vector<uint32_t> page_of;
     x0ne_split_plan split{}, bsplit{};
     uint32_t grid_qkv = 0, grid_o = 0, grid_gu = 0, grid_down = 0, grid_head = 0;
@@ -556,9 +556,7 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("moe_router_logits", c.experts * 4, CD, &e->m_logits));
         X0NE_TRY(al("moe_ids", c.layers * c.top_k * 4, CD, &e->m_ids));
         X0NE_TRY(al("moe_weights", c.layers * c.top_k * 4, CD, &e->m_w));
-        X0NE_TRY(al("moe_gate_up", c.top_k * 2 * c.moe_inter * 2, CD, &e->m_gu));
         X0NE_TRY(al("moe_act", c.top_k * c.moe_inter * 2, CD, &e->m_act));
-        X0NE_TRY(al("moe_y", c.top_k * c.hidden * 4, CD, &e->m_y));
     }
     if (e->chunk > 1) {
         const uint64_t n = e->chunk;
@@ -797,8 +795,8 @@ x0ne_status launch_rows(x0ne_engine* e, const void* fn, dim3 grid, dim3 block, v
 
 // The sparse feed-forward of layer l (engine.rs:795-815): add + RMSNorm from residual buffer 1
 // into buffer 0 (the norm the dense gate/up GEMV fuses), the router GEMV (f32 logits), the
-// routing into layer l's ids and weights, the chosen experts' [gate; up] GEMVs, SwiGLU, their
-// down GEMVs in f32, and the weighted combination into delta.
+// routing into layer l's ids and weights, the chosen experts' [gate; up] projections with SwiGLU
+// behind, and their down projections with the weighted combination behind, into delta.
 x0ne_status launch_moe(x0ne_engine* e, uint64_t l) {
     const Cfg& c = e->c;
     const LayerW& w = e->L[l];
@@ -820,41 +818,24 @@ x0ne_status launch_moe(x0ne_engine* e, uint64_t l) {
     {
         const void* lg = e->d(e->m_logits);
         void* args[] = {(void*)&lg, (void*)&ne, (void*)&k, (void*)&ids, (void*)&wts};
-        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_route_f32, dim3(1), dim3(128), args, "moe route"));
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_route_f32, dim3(1), dim3(64), args, "moe route"));
     }
     {
         const void* wg = e->d(w.gate_up);
         const void* x = e->d(e->m_x);
-        void* y = e->d(e->m_gu);
-        uint32_t rows = 2 * mi, cols = h, grp = k, stride = h;
-        void* args[] = {(void*)&wg, (void*)&ids, (void*)&x, (void*)&y, (void*)&rows, (void*)&cols, (void*)&ne,
-                        (void*)&grp, (void*)&stride};
-        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_gemv_bf16, dim3((rows + 3) / 4, k), dim3(256), args,
-                             "moe gate_up"));
-    }
-    {
-        const void* gu = e->d(e->m_gu);
         void* act = e->d(e->m_act);
-        void* args[] = {(void*)&gu, (void*)&act, (void*)&mi};
-        X0NE_TRY(launch_rows(e, (const void*)&x0ne_swiglu_bf16, dim3((mi + 255) / 256, k), dim3(256), args,
-                             "moe swiglu"));
+        void* args[] = {(void*)&wg, (void*)&ids, (void*)&x, (void*)&act, (void*)&mi, (void*)&h, (void*)&ne};
+        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_gate_up_swiglu_bf16, dim3((mi + 7) / 8, k), dim3(256), args,
+                             "moe gate_up + swiglu"));
     }
-    {
-        const void* wd = e->d(w.down);
-        const void* x = e->d(e->m_act);
-        void* y = e->d(e->m_y);
-        uint32_t rows = h, cols = mi, grp = 1, stride = mi;
-        void* args[] = {(void*)&wd, (void*)&ids, (void*)&x, (void*)&y, (void*)&rows, (void*)&cols, (void*)&ne,
-                        (void*)&grp, (void*)&stride};
-        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_gemv_f32, dim3((rows + 3) / 4, k), dim3(256), args,
-                             "moe down"));
-    }
-    const void* y = e->d(e->m_y);
+    const void* wd = e->d(w.down);
     const void* wc = wts;
+    const void* act = e->d(e->m_act);
     void* out = e->d(e->delta);
-    void* args[] = {(void*)&y, (void*)&wc, (void*)&out, (void*)&h, (void*)&k};
-    return launch_rows(e, (const void*)&x0ne_moe_combine_bf16, dim3((h + 255) / 256, 1), dim3(256), args,
-                       "moe combine");
+    void* args[] = {(void*)&wd, (void*)&ids, (void*)&wc, (void*)&act, (void*)&out, (void*)&h, (void*)&mi, (void*)&ne,
+                    (void*)&k};
+    return launch_rows(e, (const void*)&x0ne_moe_down_combine_bf16, dim3((h + 7) / 8), dim3(256), args,
+                       "moe down + combination");
 }
 
 x0ne_status step_launches(x0ne_engine* e) {
@@ -2167,15 +2148,6 @@ extern "C" x0ne_status x0ne_engine_greedy_with_last_logits(x0ne_engine* e, const
     return st != X0NE_OK ? st : sc;
 }
 
-// Engine::logits_at (engine.rs:1012-1020) is Engine::run's kept rows: the same pass, the same
-// refusal of a row without a finite maximum.
-extern "C" x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids, size_t n, const size_t* positions,
-                                             size_t n_positions, uint32_t route, float* rows) {
-    if (!e || !ids || (!rows && n_positions) || (!positions && n_positions)) return fail(X0NE_ERR_FORMAT, "null argument");
-    std::vector<x0ne_pos_stats> stats(n ? n : 1);
-    return x0ne_engine_run(e, ids, n, route, positions, n_positions, stats.data(), rows);
-}
-
 namespace {
 
 // metrics::logsumexp (metrics.rs:4-7): the f32 maximum (NaN values skipped, as f32::max does),
@@ -2190,15 +2162,15 @@ double logsumexp_row(const float* x, size_t n) {
 
 }  // namespace
 
-// Engine::run (engine.rs:928-1006): a teacher-forced pass over ids by `route`; for every
-// position its PosStats (engine.rs:60-64: the device's argmax of the row, the row's logsumexp,
-// the log-probability of the next id, NaN at the last position) and the full f32 rows at
-// `keep`. The rows come from the launches x0ne_engine_logits_at makes for each position (per
-// row the LM head with the final norm, or the decode step), so both give the same bits; the
-// client bytes are scrubbed after, on success and on failure.
-extern "C" x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t route,
-                                       const size_t* keep, size_t n_keep, x0ne_pos_stats* stats, float* rows) {
-    if (!e || !ids || !stats || (!rows && n_keep) || (!keep && n_keep)) return fail(X0NE_ERR_FORMAT, "null argument");
+namespace {
+// The teacher-forced pass of Engine::run (engine.rs:928-1006) over ids by `route`: every
+// position's row computed (per row the LM head with the final norm on the prefill route, or the
+// decode step) and its device argmax read, a row without a finite maximum refusing the pass
+// (engine.rs:855-864); with `stats`, each position's PosStats (the argmax, the row's logsumexp,
+// the log-probability of the next id, NaN at the last position); the full f32 rows at `keep`.
+// Client bytes are scrubbed after, on success and on failure.
+x0ne_status teacher_forced(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t route, const size_t* keep,
+                           size_t n_keep, x0ne_pos_stats* stats, float* rows) {
     if (route != X0NE_ROUTE_PREFILL && route != X0NE_ROUTE_DECODE) return fail(X0NE_ERR_FORMAT, "unknown route");
     if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open on this engine");
     if (e->poisoned) X0NE_TRY(scrub(e));
@@ -2210,15 +2182,18 @@ extern "C" x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size
     std::vector<float> row(vocab);
     auto collect = [&](size_t p) -> x0ne_status {
         uint32_t am = 0;
-        X0NE_TRY(x0ne_arena_read(e->arena, e->logits, 0, row.data(), vocab * 4));
         X0NE_TRY(x0ne_arena_read(e->arena, e->tokens, 0, &am, 4));
-        // A row without a finite maximum refuses the pass, as the host's read of the argmax does
-        // (engine.rs:855-864).
         if (am >= vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
-        const double lse = logsumexp_row(row.data(), vocab);
-        stats[p].argmax = am;
-        stats[p].logsumexp = (float)lse;
-        stats[p].next_logprob = p + 1 < n ? (float)((double)row[ids[p + 1]] - lse) : NAN;
+        bool kept = false;
+        for (size_t k = 0; k < n_keep; ++k) kept |= keep[k] == p;
+        if (!stats && !kept) return X0NE_OK;  // the row is not asked for
+        X0NE_TRY(x0ne_arena_read(e->arena, e->logits, 0, row.data(), vocab * 4));
+        if (stats) {
+            const double lse = logsumexp_row(row.data(), vocab);
+            stats[p].argmax = am;
+            stats[p].logsumexp = (float)lse;
+            stats[p].next_logprob = p + 1 < n ? (float)((double)row[ids[p + 1]] - lse) : NAN;
+        }
         for (size_t k = 0; k < n_keep; ++k)
             if (keep[k] == p) std::memcpy(rows + k * vocab, row.data(), vocab * 4);
         return X0NE_OK;
@@ -2242,6 +2217,21 @@ extern "C" x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size
     }
     x0ne_status sc = scrub(e);
     return st != X0NE_OK ? st : sc;
+}
+}  // namespace
+
+extern "C" x0ne_status x0ne_engine_run(x0ne_engine* e, const uint32_t* ids, size_t n, uint32_t route,
+                                       const size_t* keep, size_t n_keep, x0ne_pos_stats* stats, float* rows) {
+    if (!e || !ids || !stats || (!rows && n_keep) || (!keep && n_keep)) return fail(X0NE_ERR_FORMAT, "null argument");
+    return teacher_forced(e, ids, n, route, keep, n_keep, stats, rows);
+}
+
+// Engine::logits_at (engine.rs:1012-1020) is Engine::run's kept rows: the same pass, the same
+// refusal of a row without a finite maximum.
+extern "C" x0ne_status x0ne_engine_logits_at(x0ne_engine* e, const uint32_t* ids, size_t n, const size_t* positions,
+                                             size_t n_positions, uint32_t route, float* rows) {
+    if (!e || !ids || (!rows && n_positions) || (!positions && n_positions)) return fail(X0NE_ERR_FORMAT, "null argument");
+    return teacher_forced(e, ids, n, route, positions, n_positions, nullptr, rows);
 }
 
 // Engine::moe_routing (engine.rs:612-640): the experts every layer chose at each position of

@@ -753,7 +753,7 @@ class Kernels:
         ws = a.alloc("weights", rows * top_k * 4, Class.CLIENT_DATA)
         self._freeze(a)
         a.write(ls, 0, lg)
-        self.gpu.launch("x0ne_moe_route_f32", rows, 128,
+        self.gpu.launch("x0ne_moe_route_f32", rows, 64,
                         [Arg.ptr(a.ptr(ls)), Arg.u32(experts), Arg.u32(top_k), Arg.ptr(a.ptr(ids)),
                          Arg.ptr(a.ptr(ws))])
         self.gpu.sync()
@@ -780,7 +780,7 @@ class Kernels:
         a.write(ws, 0, w)
         a.write(is_, 0, ids)
         a.write(xs, 0, x)
-        self.gpu.launch("x0ne_moe_gemv_f32" if f32_out else "x0ne_moe_gemv_bf16", ((rows + 3) // 4, slots), 256,
+        self.gpu.launch("x0ne_moe_gemv_f32" if f32_out else "x0ne_moe_gemv_bf16", ((rows + 7) // 8, slots), 256,
                         [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(is_)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)),
                          Arg.u32(rows), Arg.u32(cols), Arg.u32(experts), Arg.u32(x_group), Arg.u32(cols)])
         self.gpu.sync()
@@ -808,6 +808,56 @@ class Kernels:
                         [Arg.ptr(a.ptr(ys)), Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(out)), Arg.u32(hidden), Arg.u32(top_k)])
         self.gpu.sync()
         return a.read_array(out, 0, rows * hidden, np.uint16)
+
+    def moe_gate_up_swiglu(self, w, experts: int, inter: int, cols: int, ids, x) -> np.ndarray:
+        """x0ne_moe_gate_up_swiglu_bf16: act[s] = bf16(silu(bf16 g) bf16 u) for the gate and up
+        rows of expert ids[s] (W [experts][2 inter][cols] bf16 bits) against x; [slots][inter]
+        bf16 bits."""
+        w = np.ascontiguousarray(w, np.uint16).ravel()
+        x = np.ascontiguousarray(x, np.uint16).ravel()
+        ids = np.ascontiguousarray(ids, np.uint32).ravel()
+        if experts == 0 or inter == 0 or cols % 8 or w.size != experts * 2 * inter * cols or x.size != cols or \
+                ids.size == 0 or ids.size > 32:
+            raise FormatError("moe_gate_up_swiglu: shapes")
+        a = self._arena()
+        ws, is_ = a.alloc("w", w.size * 2, Class.WEIGHTS), a.alloc("ids", ids.size * 4, Class.CLIENT_DATA)
+        xs, act = a.alloc("x", x.size * 2, Class.CLIENT_DATA), a.alloc("act", ids.size * inter * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ws, 0, w)
+        a.write(is_, 0, ids)
+        a.write(xs, 0, x)
+        self.gpu.launch("x0ne_moe_gate_up_swiglu_bf16", ((inter + 7) // 8, ids.size), 256,
+                        [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(is_)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(act)),
+                         Arg.u32(inter), Arg.u32(cols), Arg.u32(experts)])
+        self.gpu.sync()
+        return a.read_array(act, 0, ids.size * inter, np.uint16)
+
+    def moe_down_combine(self, w, experts: int, hidden: int, inter: int, ids, weights, act) -> np.ndarray:
+        """x0ne_moe_down_combine_bf16: out = bf16(sum_s weights[s] W[ids[s]] act[s]) (the down rows
+        in f32, the combination in slot order); W [experts][hidden][inter] bf16 bits, act
+        [slots][inter] bf16 bits; hidden bf16 bits."""
+        w = np.ascontiguousarray(w, np.uint16).ravel()
+        act = np.ascontiguousarray(act, np.uint16).ravel()
+        ids = np.ascontiguousarray(ids, np.uint32).ravel()
+        wt = np.ascontiguousarray(weights, np.float32).ravel()
+        k = ids.size
+        if experts == 0 or hidden == 0 or inter % 8 or w.size != experts * hidden * inter or act.size != k * inter or \
+                wt.size != k or k == 0 or k > 32:
+            raise FormatError("moe_down_combine: shapes")
+        a = self._arena()
+        ws, is_ = a.alloc("w", w.size * 2, Class.WEIGHTS), a.alloc("ids", k * 4, Class.CLIENT_DATA)
+        wts, xs = a.alloc("weights", k * 4, Class.CLIENT_DATA), a.alloc("act", act.size * 2, Class.CLIENT_DATA)
+        out = a.alloc("out", hidden * 2, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.write(ws, 0, w)
+        a.write(is_, 0, ids)
+        a.write(wts, 0, wt)
+        a.write(xs, 0, act)
+        self.gpu.launch("x0ne_moe_down_combine_bf16", (hidden + 7) // 8, 256,
+                        [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(is_)), Arg.ptr(a.ptr(wts)), Arg.ptr(a.ptr(xs)),
+                         Arg.ptr(a.ptr(out)), Arg.u32(hidden), Arg.u32(inter), Arg.u32(experts), Arg.u32(k)])
+        self.gpu.sync()
+        return a.read_array(out, 0, hidden, np.uint16)
 
     # -- advance, argmax (ops.rs:925-976) --
     def advance(self, value: int) -> int:
