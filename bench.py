@@ -369,6 +369,13 @@ def main():
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel of known size, "
                          "for scaling hardware byte counters)")
     args = ap.parse_args()
+    # Under rocprofv3 the steps run as eager launches (the same kernels in the same order): a
+    # kernel trace over graph replays ended once in a crash inside hipGraphLaunch whose cause was
+    # not found, so profiles are taken over eager launches only.
+    if not args.eager and (any(k.startswith("ROCPROF") for k in os.environ)
+                           or "rocprofiler" in os.environ.get("LD_PRELOAD", "")):
+        args.eager = True
+        print("[bench] under a profiler: eager launches instead of graph replays", file=sys.stderr, flush=True)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); every box here has one, "
               "and no figure at several GPUs is produced. Run with --gpus 1.", file=sys.stderr)

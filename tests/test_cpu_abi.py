@@ -53,6 +53,36 @@ def test_the_python_mirror_binds_every_function_with_the_headers_arity():
         assert len(SIGNATURES[name][0]) == n, f"{name}: {len(SIGNATURES[name][0])} arguments bound, header has {n}"
 
 
+RUST_SYS = os.path.join(ROOT, "x0ne-engine_amd", "rust", "x0ne-core-runtime-mi355x", "src", "sys.rs")
+
+
+def test_the_rust_crates_bindings_are_the_headers():
+    """The Rust crate (x0ne-engine_amd/rust/x0ne-core-runtime-mi355x, x0ne-core/runtime's drop-in)
+    cannot be compiled here (no cargo); its raw bindings are held to the header instead: every
+    extern function it declares is declared in include/x0ne_core.h with the same number of
+    parameters and exported by the library, and its options, statistics and counts structs have
+    the header's fields in order."""
+    from x0ne_core._lib import lib
+    decls = header_functions()
+    text = open(RUST_SYS).read()
+    block = text[text.index('extern "C" {'):]
+    fns = re.findall(r"pub fn (x0ne_[a-z0-9_]+)\s*\(([^)]*)\)", block, re.S)
+    assert len(fns) >= 35
+    L = lib()
+    for name, args in fns:
+        n = 0 if not args.strip() else args.strip().rstrip(",").count(",") + 1
+        assert name in decls, f"{name}: not in the header"
+        assert decls[name] == n, f"{name}: {n} parameters in Rust, {decls[name]} in the header"
+        assert hasattr(L, name), f"{name}: not exported"
+    header = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for rust, c in [("x0ne_engine_options", "x0ne_engine_options"), ("x0ne_pos_stats", "x0ne_pos_stats"),
+                    ("x0ne_counts", "x0ne_counts")]:
+        rf = re.findall(r"pub (\w+): \w+", re.search(r"pub struct %s \{(.*?)\}" % rust, text, re.S).group(1))
+        body = re.search(r"typedef struct \{([^}]*)\}\s*%s;" % c, header, re.S).group(1)
+        cf = [w for line in body.split(";") for w in re.findall(r"(\w+)\s*(?:,|$)", line.strip()) if w]
+        assert rf == cf, f"{rust}: Rust fields {rf}, header fields {cf}"
+
+
 def kernel_declarations():
     """Parameter kinds of each kernel in kernels.h, with the declaration macros expanded."""
     text = open(KERNELS_H).read()

@@ -445,9 +445,11 @@ struct x0ne_engine {
     bool session_open = false;
 
     ~x0ne_engine() {
+        // Drain the stream first: a graph's executable must not be destroyed while a replay of it
+        // is still queued (a caller that frees the engine with steps in flight).
+        if (gpu && gpu->stream) (void)hipStreamSynchronize(gpu->stream);
         if (graph) x0ne_graph_free(graph);
         if (bgraph) x0ne_graph_free(bgraph);
-        if (gpu && gpu->stream) (void)hipStreamSynchronize(gpu->stream);
         for (auto& ev : ring_ev)
             if (ev) (void)hipEventDestroy(ev);
         if (logits_ev) (void)hipEventDestroy(logits_ev);
