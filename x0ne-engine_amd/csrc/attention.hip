@@ -535,12 +535,13 @@ __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewR
 
 // The shared memory of one block: q of its heads, each wavefront's exchange area, each
 // wavefront's state for the block merge, each wavefront's slice weights for a global merge.
-template <int G, class T = float>
+// VEC = false: the matrix-core kernels' (no vector-path q or exchange area).
+template <int G, class T = float, bool VEC = true>
 struct AttnShared {
-    float qs[G][X0NE_HEAD_DIM];                      // the vector-unit paths' q
+    float qs[VEC ? G : 1][X0NE_HEAD_DIM];            // the vector-unit paths' q
     alignas(16) bf16_t qh[G][X0NE_HEAD_DIM];         // the matrix-core path's q (bf16)
     alignas(16) bf16_t knew[X0NE_HEAD_DIM], vnew[X0NE_HEAD_DIM];  // the fused variant's new K/V row
-    T xch[WAVES][2 * G * 64];
+    T xch[VEC ? WAVES : 1][VEC ? 2 * G * 64 : 1];
     T wm[WAVES][G], wl[WAVES][G];
     T wo[WAVES][G][X0NE_HEAD_DIM];
     T wf[WAVES][G], mh[G], lh[G];  // the block merge's factors, maximum and sum per head
@@ -610,8 +611,8 @@ __device__ __forceinline__ void merge_head(const float* __restrict__ s, Store&& 
 // per head g and dim d: threads 0..G-1 first take each head's maximum, factors and sum into LDS;
 // then thread t takes the (g, d) pairs t, t + 256, ... and calls f(g, d, m, l, o). Every thread
 // of the block calls it (it holds a barrier), after the wavefronts' states are in LDS.
-template <int G, class T, class F>
-__device__ __forceinline__ void block_merge(AttnShared<G, T>& sh, F f) {
+template <int G, class T, bool V, class F>
+__device__ __forceinline__ void block_merge(AttnShared<G, T, V>& sh, F f) {
     const uint32_t t = threadIdx.x;
     if (t < (uint32_t)G) {
         T mx = -INFINITY;
@@ -702,8 +703,8 @@ __device__ __forceinline__ size_t out_index(const AttnArgs& a, uint32_t h, uint3
 }
 
 // A wavefront's state into the block's LDS for the block merge.
-template <int G, class T>
-__device__ __forceinline__ void stash_wave(AttnShared<G, T>& sh, const T m[G], const T l[G], const T o[G][2]) {
+template <int G, class T, bool V>
+__device__ __forceinline__ void stash_wave(AttnShared<G, T, V>& sh, const T m[G], const T l[G], const T o[G][2]) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) {
 #pragma unroll
@@ -1113,7 +1114,7 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
 // variant the block owning pos's tile writes that position's K and V rows to their page and
 // keeps them in LDS for its wavefront that attends them, so no wavefront waits for that write.
 template <int G, bool FUSED>
-__device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G>& sh) {
+__device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G, float, false>& sh) {
     const uint32_t kh = blockIdx.x, y = blockIdx.y, P = a.splits;
     // Block-uniform exits for a launch that does not fit the geometry, before any load.
     if (P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;
@@ -1397,7 +1398,7 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         const uint32_t* __restrict__ pages, float* __restrict__ state, uint32_t* __restrict__ counter,           \
         bf16_t* __restrict__ out, const uint32_t* __restrict__ pos, uint32_t q_heads, uint32_t kv_heads,         \
         uint32_t max_ctx, uint32_t splits, float scale) {                                                         \
-        __shared__ AttnShared<G> sh;                                                                               \
+        __shared__ AttnShared<G, float, false> sh;                                                                 \
         AttnArgs a = {};                                                                                           \
         a.q = q;                                                                                                   \
         a.k_cache = const_cast<bf16_t*>(k_cache);                                                                  \
@@ -1420,7 +1421,7 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages, float* __restrict__ state,             \
         uint32_t* __restrict__ counter, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,              \
         uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale, float eps) {         \
-        __shared__ AttnShared<G> sh;                                                                               \
+        __shared__ AttnShared<G, float, false> sh;                                                                 \
         AttnArgs a = {};                                                                                           \
         a.qkv = qkv;                                                                                               \
         a.q_norm = q_norm;                                                                                         \
@@ -1449,7 +1450,7 @@ __device__ __forceinline__ void attn_head_block(const bf16_t* __restrict__ q_row
         uint32_t* __restrict__ counter, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos,              \
         uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, uint32_t splits, float scale, float eps,          \
         uint32_t seq_pages) {                                                                                      \
-        __shared__ AttnShared<G> sh;                                                                               \
+        __shared__ AttnShared<G, float, false> sh;                                                                 \
         const size_t b = blockIdx.z;                                                                               \
         AttnArgs a = {};                                                                                           \
         a.qkv = qkv + b * (q_heads + 2 * kv_heads) * X0NE_HEAD_DIM;                                                \

@@ -184,86 +184,6 @@ __device__ __forceinline__ void x_stage(const GemvArgs& a, const XIn<PRO, XC>& i
     lds_barrier();
 }
 
-template <class A>
-__device__ __forceinline__ A dot8(const uint4 w, const float* x, A acc);
-
-template <>
-__device__ __forceinline__ float dot8<float>(const uint4 w, const float* x, float acc) {
-    acc = fmaf(bf_lo(w.x), x[0], acc);
-    acc = fmaf(bf_hi(w.x), x[1], acc);
-    acc = fmaf(bf_lo(w.y), x[2], acc);
-    acc = fmaf(bf_hi(w.y), x[3], acc);
-    acc = fmaf(bf_lo(w.z), x[4], acc);
-    acc = fmaf(bf_hi(w.z), x[5], acc);
-    acc = fmaf(bf_lo(w.w), x[6], acc);
-    acc = fmaf(bf_hi(w.w), x[7], acc);
-    return acc;
-}
-
-// Each product of two bf16 is exact in f32; it is added in f64.
-template <>
-__device__ __forceinline__ double dot8<double>(const uint4 w, const float* x, double acc) {
-    acc += (double)(bf_lo(w.x) * x[0]);
-    acc += (double)(bf_hi(w.x) * x[1]);
-    acc += (double)(bf_lo(w.y) * x[2]);
-    acc += (double)(bf_hi(w.y) * x[3]);
-    acc += (double)(bf_lo(w.z) * x[4]);
-    acc += (double)(bf_hi(w.z) * x[5]);
-    acc += (double)(bf_lo(w.w) * x[6]);
-    acc += (double)(bf_hi(w.w) * x[7]);
-    return acc;
-}
-
-// Sum of R values over the 64 lanes. At the first log2(R) steps (lane bits 5, 4, ...) each lane
-// keeps half of its values (bit set: the upper half) and adds its partner's copy of them; the
-// remaining steps are plain butterflies. Lane l ends with the sum of value reduced_row<R>(l).
-template <int N, int K, class A>
-struct RowReduce {
-    static __device__ __forceinline__ void run(A* v, uint32_t lane) {
-        constexpr int H = N >> 1;
-        const bool bit = (lane >> K) & 1u;
-#pragma unroll
-        for (int j = 0; j < H; ++j) {
-            const A send = bit ? v[j] : v[j + H];
-            const A keep = bit ? v[j + H] : v[j];
-            v[j] = keep + __shfl_xor(send, 1 << K, 64);
-        }
-        RowReduce<H, K - 1, A>::run(v, lane);
-    }
-};
-template <int K, class A>
-struct RowReduce<1, K, A> {
-    static __device__ __forceinline__ void run(A* v, uint32_t lane) {
-        v[0] += __shfl_xor(v[0], 1 << K, 64);
-        RowReduce<1, K - 1, A>::run(v, lane);
-    }
-};
-template <class A>
-struct RowReduce<1, -1, A> {
-    static __device__ __forceinline__ void run(A*, uint32_t) {}
-};
-
-template <int R, class A>
-__device__ __forceinline__ A wave_reduce_rows(A* v) {
-    RowReduce<R, 5, A>::run(v, threadIdx.x & 63);
-    return v[0];
-}
-
-template <int R>
-__device__ __forceinline__ uint32_t reduced_row(uint32_t lane) {
-    uint32_t idx = 0;
-    int n = R;
-#pragma unroll
-    for (int k = 5; k >= 0; --k) {
-        if (n > 1) {
-            const int h = n >> 1;
-            if ((lane >> k) & 1u) idx += h;
-            n = h;
-        }
-    }
-    return idx;
-}
-
 // A wavefront's work is a sequence of tiles: row group g (R rows; for EPI_SWIGLU R / 2 gate rows
 // i.. and the up rows inter + i..) times batch b (chunks 64 BATCH b + lane + 64 j, j < BATCH, of
 // each row). Tiles are double-buffered in registers: while one is summed the next is in flight,
