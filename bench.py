@@ -73,6 +73,12 @@ def splitmix_ids(n: int, vocab: int, seed: int) -> np.ndarray:
     return np.array(out, np.uint32)
 
 
+def cpu_threads() -> int:
+    """The host threads of the CPU leg: the GPU box's CPU share per GPU (its OMP_NUM_THREADS, 16
+    on the box), else every core this host has."""
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+
+
 def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, prompt_len: int = 4,
                  name: str = "Qwen3-8B") -> dict:
     """The CPU oracle on the same shape and weights (drawn by the oracle's generator, the same
@@ -99,16 +105,19 @@ def cpu_baseline(cfg: dict, prompt: np.ndarray, threads: int, steps: int = 8, pr
         times.append(time.perf_counter() - t0)
     value = steps / times[-1]
     O.set_threads(1)
+    single_steps = 2
     t0 = time.perf_counter()
-    logits = m.step(O.argmax(logits))
-    single = 1 / (time.perf_counter() - t0)
+    for _ in range(single_steps):
+        logits = m.step(O.argmax(logits))
+    single = single_steps / (time.perf_counter() - t0)
     O.set_threads(threads)
     return {"value": round(value, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "single_thread_value": round(single, 4),
             "sample": f"{name} shape, the same N(0,{STD}) bf16 weights (seed {SEED}, drawn by the oracle's "
                       f"generator in {init_s:.1f} s, not timed), {prompt_len}-token prompt, {steps} greedy decode "
-                      f"steps timed on {threads} threads (rows split, f64 sums in the reference's order); "
-                      f"single_thread_value: 1 step on 1 thread"}
+                      f"steps timed on {threads} threads (rows split, f64 sums in the reference's order; the "
+                      f"GPU box's CPU share per GPU); single_thread_value: {single_steps} more steps on 1 thread, "
+                      f"as the reference's oracle runs"}
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qwen3-8b-decode_hbm-bytes.md")
@@ -268,7 +277,7 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
     print(f"[bench] parity {parity['timed_path']}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         try:
             cpu = cpu_baseline(cfg, prompts[0], threads, name=model_name)
             cpu["sample"] += "; the oracle decodes one sequence at a time (its tok/s is per sequence)"
@@ -479,9 +488,15 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         try:
             cpu = cpu_baseline(cfg, prompt, threads, name=model_name)
+            if args.model != "0.6b":
+                # BASELINE.json config 1 (Qwen3-0.6B, tied, a 20-token prompt, 64 greedy steps) in
+                # full: the shape the reference's CPU oracle is quoted on.
+                c1 = cpu_baseline(QWEN3_0_6B, prompt[:20], threads, steps=64, prompt_len=min(20, prompt.size),
+                                  name="Qwen3-0.6B")
+                cpu["config1"] = {k: c1[k] for k in ("value", "unit", "cores", "single_thread_value", "sample")}
         except Exception as ex:  # a baseline that cannot run is reported as missing, not as the GPU's failure
             cpu = {"value": None, "error": str(ex)}
         print(f"[bench] cpu baseline {cpu}", file=sys.stderr, flush=True)

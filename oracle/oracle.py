@@ -14,7 +14,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# X0NE_ORACLE_LIB: another build of the same restatement (the Makefile's sanitizer build).
+LIB_PATH = os.environ.get("X0NE_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 _lib = None
 

@@ -48,9 +48,18 @@ def fingerprint() -> str:
     return h.hexdigest()[:16]
 
 
-def _compile(src: str, kernel_set: str) -> str:
-    obj = os.path.join(OUT_DIR, src.replace(".hip", ".o"))
-    cmd = [HIPCC] + FLAGS + [f'-DX0NE_KERNEL_SET="{kernel_set}"', "-c", os.path.join(CSRC, src), "-o", obj]
+# --asan: the host code (loaders, parsers, arena, runtime) under AddressSanitizer; the device
+# code is unchanged. Output x0ne_core/libx0ne_core_asan.so, loaded with the sanitizer runtime
+# preloaded and X0NE_CORE_LIB naming it.
+ASAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer", "-g"]
+ASAN_LIB = os.path.join(HERE, "x0ne_core", "libx0ne_core_asan.so")
+
+
+def _compile(src: str, kernel_set: str, asan: bool = False) -> str:
+    out_dir = OUT_DIR + ("_asan" if asan else "")
+    obj = os.path.join(out_dir, src.replace(".hip", ".o"))
+    cmd = [HIPCC] + FLAGS + (ASAN_FLAGS if asan else []) + [f'-DX0NE_KERNEL_SET="{kernel_set}"', "-c",
+                                                            os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
@@ -62,20 +71,21 @@ def _compile(src: str, kernel_set: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None) -> str:
-    os.makedirs(OUT_DIR, exist_ok=True)
+def build(jobs: int | None = None, asan: bool = False) -> str:
+    os.makedirs(OUT_DIR + ("_asan" if asan else ""), exist_ok=True)
     kernel_set = fingerprint()
     jobs = jobs or min(8, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, kernel_set), sources()))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
+        objs = list(ex.map(lambda s: _compile(s, kernel_set, asan), sources()))
+    lib = ASAN_LIB if asan else LIB
+    tmp = lib + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC"] + (ASAN_FLAGS if asan else []) + ["-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build())
+    print(build(asan="--asan" in sys.argv[1:]))

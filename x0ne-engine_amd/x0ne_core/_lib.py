@@ -6,7 +6,9 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libx0ne_core.so")
+# X0NE_CORE_LIB: another build of this library (build.py --asan: the host code under
+# AddressSanitizer, for the CPU suite).
+LIB_PATH = os.environ.get("X0NE_CORE_LIB") or os.path.join(HERE, "libx0ne_core.so")
 
 OK, ERR_IO, ERR_FORMAT, ERR_ARENA, ERR_NOT_IMPLEMENTED, ERR_GPU = range(6)
 
