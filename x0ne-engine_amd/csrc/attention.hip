@@ -563,44 +563,63 @@ __device__ __forceinline__ float state_get(const float* p) {
 
 // Merge of one q head's slices 0..active-1 (FlashInfer's: M = max m_y, f_y = exp(m_y - M),
 // l = sum l_y f_y, o = sum o_y f_y; one rounding, of o / l), the sums in a fixed order so the
-// result depends on the states only. One wavefront; lane y reads slice y's (m, l) (and y + 64,
-// ...), lane d owns dims d and d + 64 of o, whose loads are issued 8 slices at a time. f: this
-// wavefront's LDS for `active` floats. Every active slice saw a key, so each m is finite. The
-// caller has made other workgroups' states visible (their release, its acquire): plain loads.
+// result depends on the states only. One wavefront; lane y holds slice y's (m, l) (and y + 64,
+// ...), lane d owns dims d and d + 64 of o. Every load of a chunk of MERGE_CHUNK slices (their
+// (m, l) and o values) is issued before any is used, so a merge of up to MERGE_CHUNK slices costs
+// one round trip to memory. f: this wavefront's LDS for `active` floats. Every active slice saw a
+// key, so each m is finite. The caller has made other workgroups' states visible (their release,
+// its acquire): the loads are coherent.
+constexpr uint32_t MERGE_CHUNK = 32;
 template <class Store>
 __device__ __forceinline__ void merge_head(const float* __restrict__ s, Store&& store, uint32_t active, float* f) {
     const uint32_t lane = threadIdx.x & 63;
+    constexpr int MLK = MERGE_MAX / 64;
+    float mv[MLK], lv[MLK];
+#pragma unroll
+    for (int k = 0; k < MLK; ++k) {
+        const uint32_t y = lane + 64 * k;
+        if (64 * k < active) {  // wave-uniform
+            mv[k] = y < active ? state_get(s + (size_t)y * X0NE_SPLIT_STATE) : -INFINITY;
+            lv[k] = y < active ? state_get(s + (size_t)y * X0NE_SPLIT_STATE + 1) : 0.f;
+        }
+    }
+    float a[MERGE_CHUNK], b[MERGE_CHUNK];
+    auto request = [&](uint32_t y0) {
+#pragma unroll
+        for (uint32_t k = 0; k < MERGE_CHUNK; ++k)
+            if (y0 + k < active) {  // wave-uniform
+                const float* st = s + (size_t)(y0 + k) * X0NE_SPLIT_STATE + 4;
+                a[k] = state_get(st + lane);
+                b[k] = state_get(st + lane + 64);
+            }
+    };
+    request(0);
     float mx = -INFINITY;
-    for (uint32_t y = lane; y < active; y += 64) mx = fmaxf(mx, state_get(s + (size_t)y * X0NE_SPLIT_STATE));
+#pragma unroll
+    for (int k = 0; k < MLK; ++k)
+        if (64 * k < active) mx = fmaxf(mx, mv[k]);
     mx = wave_max(mx);
     float lp = 0.f;
-    for (uint32_t y = lane; y < active; y += 64) {
-        const float fy = expf(state_get(s + (size_t)y * X0NE_SPLIT_STATE) - mx);
-        f[y] = fy;
-        lp += state_get(s + (size_t)y * X0NE_SPLIT_STATE + 1) * fy;
+#pragma unroll
+    for (int k = 0; k < MLK; ++k) {
+        const uint32_t y = lane + 64 * k;
+        if (64 * k < active && y < active) {
+            const float fy = expf(mv[k] - mx);
+            f[y] = fy;
+            lp += lv[k] * fy;
+        }
     }
     const float l = wave_sum(lp);
     wave_lds_sync();
     float o0 = 0.f, o1 = 0.f;
-    uint32_t y = 0;
-    for (; y + 8 <= active; y += 8) {
-        float a[8], b[8];
+    for (uint32_t y0 = 0; y0 < active; y0 += MERGE_CHUNK) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float* st = s + (size_t)(y + k) * X0NE_SPLIT_STATE + 4;
-            a[k] = state_get(st + lane);
-            b[k] = state_get(st + lane + 64);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            o0 = fmaf(a[k], f[y + k], o0);
-            o1 = fmaf(b[k], f[y + k], o1);
-        }
-    }
-    for (; y < active; ++y) {
-        const float* st = s + (size_t)y * X0NE_SPLIT_STATE + 4;
-        o0 = fmaf(state_get(st + lane), f[y], o0);
-        o1 = fmaf(state_get(st + lane + 64), f[y], o1);
+        for (uint32_t k = 0; k < MERGE_CHUNK; ++k)
+            if (y0 + k < active) {
+                o0 = fmaf(a[k], f[y0 + k], o0);
+                o1 = fmaf(b[k], f[y0 + k], o1);
+            }
+        if (y0 + MERGE_CHUNK < active) request(y0 + MERGE_CHUNK);
     }
     store(lane, f2bf(o0 / l));
     store(lane + 64, f2bf(o1 / l));
