@@ -126,6 +126,9 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qwen3-8b-decode_hbm-bytes.md")
 BATCH8_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qwen3-8b-decode-batch8_hbm-bytes.md")
 
 
+ATTENTION_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode-attention-8k-32k_hbm-bytes.md")
+
+
 def measured_traffic(kernel: str, profile: str = TRAFFIC_PROFILE):
     """HBM bytes per launch of `kernel` from a committed rocprofv3 byte-counter summary
     (FETCH_SIZE and WRITE_SIZE runs, scaled by a copy of known size), or None."""
@@ -167,15 +170,20 @@ def attention_line(args) -> dict:
     g = Gpu()
     qh, kvh = 32, 8
     rows = []
-    for ctx in (1024, 8192, 32768):
-        for P in (1, 4, 16, 32):
-            us, planes = g.time_attention(qh, kvh, ctx, P, args.attention_iters, SEED)
-            nbytes = 2 * ctx * kvh * 128 * 2 + qh * 128 * 2 * 2 + (qh * P * 132 * 4 if P > 1 else 0)
-            rows.append({"ctx": ctx, "splits": P, "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
-                         "frac": round(nbytes / us / 1e3 / 8000.0, 4), "bytes": nbytes, "planes": planes})
-            print(f"[bench] attention ctx {ctx} P {P}: {us:.2f} us, {nbytes / us / 1e3:.1f} GB/s ({planes} planes)",
-                  file=sys.stderr, flush=True)
-    best = max((r for r in rows if r["ctx"] == 32768), key=lambda r: r["gbs"])
+    cases = [(c, p) for c in (1024, 8192, 32768) for p in (1, 4, 16, 32)]
+    if args.attention_case:  # one (ctx, P), e.g. for a counter run whose dispatches are all that case
+        c, p = (int(v) for v in args.attention_case.split(":"))
+        cases = [(c, p)]
+    if args.calibrate_copy:
+        copy_calibration(args.calibrate_copy << 20)
+    for ctx, P in cases:
+        us, planes = g.time_attention(qh, kvh, ctx, P, args.attention_iters, SEED)
+        nbytes = 2 * ctx * kvh * 128 * 2 + qh * 128 * 2 * 2 + (qh * P * 132 * 4 if P > 1 else 0)
+        rows.append({"ctx": ctx, "splits": P, "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / 8000.0, 4), "bytes": nbytes, "planes": planes})
+        print(f"[bench] attention ctx {ctx} P {P}: {us:.2f} us, {nbytes / us / 1e3:.1f} GB/s ({planes} planes)",
+              file=sys.stderr, flush=True)
+    best = max((r for r in rows if r["ctx"] == max(c for c, _ in cases)), key=lambda r: r["gbs"])
     return {
         "metric": "Qwen3-8B decode attention GB/s (BASELINE.json config 2) vs 8 TB/s peak",
         "value": best["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.attention_iters, "warmup": 0,
@@ -185,7 +193,9 @@ def attention_line(args) -> dict:
                                "value at ctx 32768 with the fastest P", "ctx": best["ctx"], "splits": best["splits"],
                    "table": rows},
         "roofline": {"kernel": "x0ne_attention_decode_split_g4_bf16", "bound": "hbm", "achieved": best["gbs"],
-                     "peak": 8000.0, "unit": "GB/s", "frac": best["frac"], "traffic": None,
+                     "peak": 8000.0, "unit": "GB/s", "frac": best["frac"],
+                     "traffic": measured_traffic(f"attention_{best['ctx']}_{best['splits']}", ATTENTION_TRAFFIC_PROFILE),
+                     "traffic_source": os.path.relpath(ATTENTION_TRAFFIC_PROFILE, ROOT),
                      "bytes_per_launch": best["bytes"], "avg_us": best["us"],
                      "timing": "hipExtLaunchKernel start/stop events per launch"},
     }
@@ -374,6 +384,8 @@ def main():
     ap.add_argument("--attention", action="store_true",
                     help="BASELINE.json config 2 instead: the isolated decode attention at ctx 1k/8k/32k, P 1/4/16")
     ap.add_argument("--attention-iters", type=int, default=64)
+    ap.add_argument("--attention-case", default="", metavar="CTX:P",
+                    help="--attention at one context and split count only")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel of known size, "
                          "for scaling hardware byte counters)")
