@@ -1648,8 +1648,11 @@ extern "C" void x0ne_session_drop(x0ne_session* s) {
 
 namespace {
 
-// Launches steps until `ahead` tokens are in flight or every token asked is launched; step j
-// writes its token into ring word j % RING (engine.rs:1322-1343).
+// Keeps the device busy ahead of the caller: queues decode steps (graph replay, then the copy
+// of the step's token into ring word j % RING) while fewer than `ahead` of them sit beyond the
+// last token the caller has taken and the request still wants tokens. A queued step's word
+// cannot be overwritten before it is read: at most `ahead` (< RING) steps are ever outstanding.
+// The semantics of the reference's Greedy ring (engine.rs:1322-1343).
 x0ne_status greedy_fill(x0ne_greedy* g) {
     x0ne_engine* e = g->s->e;
     const size_t taken_m1 = g->taken ? g->taken - 1 : 0;
