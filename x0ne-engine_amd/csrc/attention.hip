@@ -29,6 +29,7 @@
 //    block that owns position pos, the K/V write of that position's row (rope.cu:7-47), so a
 //    decode step's attention is one launch.
 #include "device.h"
+#include "kernels.h"
 
 namespace {
 
@@ -1294,47 +1295,251 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
     if (t == 0) __hip_atomic_store(a.counter + kh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next step
 }
 
-// Causal prefill on the matrix cores, for G q heads per kv head: rows r of q ([rows][q_heads][128]
-// bf16) at positions pos0 + r, over the cache (which already holds their keys). Wavefront w of
-// block (kh, y) takes the R = 16 / G rows 4 R y + R w .. and the G q heads of kv head kh: the 16
-// columns of its products (column c: row c / G, head c % G), each over keys 0 .. min(pos0 + row,
-// max_ctx - 1), in one pass over the tiles up to its last row's; its output goes straight to
-// out ([rows][q_heads][128]). The wavefronts of a block do not wait for each other.
-template <int G>
-__device__ __forceinline__ void prefill_wave(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
-                                             const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
-                                             bf16_t* __restrict__ out, uint32_t p0, uint32_t rows, uint32_t q_heads,
-                                             uint32_t kv_heads, uint32_t max_ctx, float scale) {
-    constexpr uint32_t R = 16 / G;
-    const uint32_t kh = blockIdx.x, lane = threadIdx.x & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t r0 = (4 * blockIdx.y + wave) * R;  // the wavefront's first row
-    if (kh >= kv_heads || q_heads != G * kv_heads || r0 >= rows || max_ctx == 0) return;  // wavefront-uniform
+// ---- causal prefill on the matrix cores ----
+//
+// Block (kv head kh, row block) serves the G q heads of kv head kh for RB = 128 / G rows of q
+// ([rows][q_heads][128] bf16, at positions pos0 + row): its 128 columns (column c: row
+// r0 + c / G, head kh G + c % G) go 32 to a wavefront, as two groups of 16 (the 16 columns of a
+// product). The keys pass in tiles of 64 (4 pages) staged in LDS once per block and read by all
+// 4 wavefronts: K rows padded to 136 bf16, V dim-major [128][64 + 8], so the operand reads of a
+// product spread over the LDS banks; each K or V piece a wavefront reads serves both groups.
+// Per tile and column group: S^T = K Q^T (16 products; the S^T blocks X0, Y0, X1, Y1 of the
+// decode wavefront, which leave each lane the 8 keys of its P row for a 32-key step), a
+// per-column causal mask (keys up to the column's own position; skipped for a tile inside every
+// limit of the wavefront), the online softmax in units of log2 (the rescale of O skipped when no
+// maximum of the group moved), and O += P V with P as bf16 hi + lo (32 products). The next
+// tile's loads are in flight while a tile is multiplied (two LDS buffers). Each column's output
+// goes straight to out ([rows][q_heads][128]). Blocks whose rows reach more keys are dispatched
+// first. Keys at or past the block's context are read as zeros (V) or masked (K); no page past
+// the context is read. Two blocks share a CU (2 x 70 KiB of LDS, at most 256 registers per
+// lane), so one block's products overlap the other's softmax and loads.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    return v;
+}
+constexpr int PF_CG = 2;              // column groups of 16 per wavefront
+static_assert(4 * 16 * PF_CG == X0NE_PREFILL_COLS, "columns per prefill block");
+constexpr uint32_t PF_KS = 136;       // bf16 per K row in LDS (128 dims + 8)
+constexpr uint32_t PF_VS = 72;        // bf16 per V dim row in LDS (64 keys + 8)
+
+struct PrefillShared {
+    alignas(16) bf16_t k[2][X0NE_SPLIT_TILE * PF_KS];
+    alignas(16) bf16_t v[2][X0NE_HEAD_DIM * PF_VS];
+};
+
+template <int G, int CG>
+__device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
+                                              const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
+                                              bf16_t* __restrict__ out, uint32_t p0, uint32_t rows, uint32_t q_heads,
+                                              uint32_t kv_heads, uint32_t max_ctx, float scale, PrefillShared& sh) {
+    constexpr uint32_t COLS = 4 * 16 * CG;  // columns per block: CG groups of 16 per wavefront
+    constexpr uint32_t RB = COLS / G;
+    const uint32_t kh = blockIdx.x, rb = gridDim.y - 1 - blockIdx.y;  // the rows with the most keys first
+    const uint32_t r0 = rb * RB;
+    if (kh >= kv_heads || q_heads != (uint32_t)G * kv_heads || r0 >= rows || max_ctx == 0) return;  // block-uniform
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t n = lane & 15, q4 = lane >> 4;
-    const uint32_t r = r0 + n / G, h = kh * G + n % G;
-    const bool col = r < rows;
-    const uint32_t ctx_col = col ? min(p0 + r + 1, max_ctx) : 1u;
-    const uint32_t ctx = min(p0 + min(r0 + R, rows), max_ctx);  // through the wavefront's last row
-    const bf16_t* qr = q + ((size_t)(col ? r : 0) * q_heads + h) * X0NE_HEAD_DIM + 8 * q4;
-    auto prologue = [&](uint4 qb[4]) {
+    const uint32_t ctx = min(p0 + min(r0 + RB, rows), max_ctx);  // keys the block reads
+    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
+    const uint32_t npages = (ctx + X0NE_PAGE - 1) / X0NE_PAGE;
+    const float scale2 = scale * LOG2E;
+
+    // The lane's CG columns (one per group): their q pieces (the B operand of Q^T for each
+    // 32-dim step) and causal limits; a column past the rows attends key 0 only and is not written.
+    uint4 qb[CG][4];
+    uint32_t ctx_col[CG];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+        const uint32_t c = 16 * CG * wave + 16 * cg + n, r = r0 + c / G, h = kh * G + c % G;
+        const bool live = r < rows;
+        ctx_col[cg] = live ? min(p0 + r + 1, max_ctx) : 1u;
+        const bf16_t* qr = q + ((size_t)(live ? r : 0) * q_heads + h) * X0NE_HEAD_DIM + 8 * q4;
 #pragma unroll
         for (int st = 0; st < 4; ++st)
-            qb[st] = col ? *reinterpret_cast<const uint4*>(qr + 32 * st) : make_uint4(0, 0, 0, 0);
+            qb[cg][st] = live ? *reinterpret_cast<const uint4*>(qr + 32 * st) : make_uint4(0, 0, 0, 0);
+    }
+
+    // A tile's K and V pieces for this thread: K chunk i = t + 256 j is page i / 256, key
+    // (i / 16) % 16, 16-byte piece i % 16; V chunk i is page i / 256, dim (i / 2) % 128, keys
+    // 8 (i % 2) .. + 7 of the page.
+    // Their loads are issued by fetch() and waited for only by stash(), after a tile's products.
+    // The page-table entries of a tile are requested one tile before its K and V.
+    uint4 kr[4], vr[4];
+    const auto kres = plane_rsrc(k_cache, OFF_NONE), vres = plane_rsrc(v_cache, OFF_NONE);
+    uint32_t pe[4];  // entries of the next tile to fetch (chunk j of a thread is in page j)
+    auto entries = [&](uint32_t tile) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pe[j] = 4 * tile + j < npages ? pages[4 * tile + j] : 0u;
     };
-    const NewRow none = {~0u, 0, nullptr, nullptr};
-    float mw, lw;
-    f32x4 ow[8];
-    attend_wave_mfma(prologue, none, k_cache, v_cache, pages, kh, kv_heads, ctx, ctx_col, 0, 1, ~0u, scale, mw, lw, ow);
-    // ow[nb][i] = O[column 4 q4 + i][dim 16 nb + n]; lane c < 16 holds column c's sum.
+    auto fetch = [&](uint32_t tile) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t c = 4 * q4 + i;
-        const float l = __shfl(lw, (int)c, 64);
-        const uint32_t rc = r0 + c / G;
-        if (rc < rows) {
-            bf16_t* o = out + ((size_t)rc * q_heads + kh * G + c % G) * X0NE_HEAD_DIM;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = t + BLOCK * j, pi = i >> 8, lp = 4 * tile + pi;
+            const uint32_t pb = pe[j] * kv_heads + kh;
+            kr[j] = bload16(kres, lp < npages ? ((pb * X0NE_PAGE + ((i >> 4) & 15)) * X0NE_HEAD_DIM + 8 * (i & 15)) * 2
+                                              : OFF_NONE);
+            vr[j] = bload16(vres, lp < npages ? ((pb * X0NE_HEAD_DIM + ((i >> 1) & 127)) * X0NE_PAGE + 8 * (i & 1)) * 2
+                                              : OFF_NONE);
+        }
+    };
+    auto stash = [&](uint32_t tile, int buf) {
 #pragma unroll
-            for (int nb = 0; nb < 8; ++nb) o[16 * nb + n] = f2bf(ow[nb][i] / l);
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = t + BLOCK * j, pi = i >> 8;
+            // Keys at or past ctx hold anything: zeros (their weight is 0, and 0 times a value that is
+            // not a number would not be).
+            const uint32_t key0 = X0NE_SPLIT_TILE * tile + X0NE_PAGE * pi + 8 * (i & 1);
+            const uint32_t valid = key0 >= ctx ? 0u : min(ctx - key0, 8u);
+            uint32_t w[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] &= (2 * e + 1 < (int)valid ? 0xFFFF0000u : 0u) | (2 * e < (int)valid ? 0xFFFFu : 0u);
+            *reinterpret_cast<uint4*>(&sh.k[buf][(16 * pi + ((i >> 4) & 15)) * PF_KS + 8 * (i & 15)]) = kr[j];
+            *reinterpret_cast<uint4*>(&sh.v[buf][((i >> 1) & 127) * PF_VS + 16 * pi + 8 * (i & 1)]) =
+                make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    };
+
+    float m_run[CG], lsum[CG];
+    f32x4 o[CG][8];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+        m_run[cg] = -INFINITY;
+        lsum[cg] = 0.f;
+    }
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) o[cg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    entries(0);
+    fetch(0);
+    entries(1);
+    stash(0, 0);
+    __syncthreads();
+    for (uint32_t tile = 0; tile < ntiles; ++tile) {
+        const int buf = tile & 1;
+        if (tile + 1 < ntiles) {  // block-uniform; in flight during the products
+            fetch(tile + 1);
+            entries(tile + 2);
+        }
+        const bf16_t* K = sh.k[buf];
+        const bf16_t* V = sh.v[buf];
+        const uint32_t base = X0NE_SPLIT_TILE * tile;
+        // S^T blocks (kp, h) for every column group: one K piece serves all of them.
+        f32x4 s[CG][2][2];
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t key = 32 * kp + 8 * (n >> 2) + 4 * h + (n & 3);
+                f32x4 acc[CG];
+#pragma unroll
+                for (int cg = 0; cg < CG; ++cg) acc[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const uint4 kk = *reinterpret_cast<const uint4*>(K + key * PF_KS + 32 * st + 8 * q4);
+#pragma unroll
+                    for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma16x16x32(kk, qb[cg][st], acc[cg]);
+                }
+#pragma unroll
+                for (int cg = 0; cg < CG; ++cg) s[cg][kp][h] = acc[cg];
+            }
+        // Tiles wholly below every column's limit need no mask (wavefront-uniform).
+        uint32_t lim = ctx_col[0];
+#pragma unroll
+        for (int cg = 1; cg < CG; ++cg) lim = min(lim, ctx_col[cg]);
+        const bool full = base + X0NE_SPLIT_TILE <= __builtin_amdgcn_readfirstlane(wave_min_u32(lim));
+        // Mask and online softmax per column group; P as bf16 hi + lo.
+        uint4 phi[CG][2], plo[CG][2];
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) {
+            float sc[2][2][4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t key = 32 * kp + 8 * q4 + 4 * h + i;
+                        sc[kp][h][i] = full || base + key < ctx_col[cg] ? s[cg][kp][h][i] * scale2 : -INFINITY;
+                        mx = fmaxf(mx, sc[kp][h][i]);
+                    }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m_run[cg], mx);  // key 0 is in every column's first tile: finite
+            const float alpha = __builtin_amdgcn_exp2f(m_run[cg] - mn);
+            m_run[cg] = mn;
+            float psum = 0.f;
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        sc[kp][h][i] = __builtin_amdgcn_exp2f(sc[kp][h][i] - mn);
+                        psum += sc[kp][h][i];
+                    }
+            lsum[cg] = lsum[cg] * alpha + psum;
+            if (__any(alpha != 1.f)) {  // multiplying by 1 changes nothing: skipped when no max moved
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float ai = __shfl(alpha, 4 * q4 + i, 64);
+#pragma unroll
+                    for (int nb = 0; nb < 8; ++nb) o[cg][nb][i] *= ai;
+                }
+            }
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                float pv[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pv[i] = sc[kp][0][i];
+                    pv[4 + i] = sc[kp][1][i];
+                }
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hw[j] = pack_bf16(pv[2 * j], pv[2 * j + 1]);
+                    lw[j] = pack_bf16(pv[2 * j] - bf_lo(hw[j]), pv[2 * j + 1] - bf_hi(hw[j]));  // exact
+                }
+                phi[cg][kp] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                plo[cg][kp] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            }
+        }
+        // O += P V: the V piece (keys 32 kp + 8 q4 .., dim 16 nb + n) serves every group.
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) {
+                const uint4 vb = *reinterpret_cast<const uint4*>(V + (16 * nb + n) * PF_VS + 32 * kp + 8 * q4);
+#pragma unroll
+                for (int cg = 0; cg < CG; ++cg) {
+                    o[cg][nb] = mfma16x16x32(phi[cg][kp], vb, o[cg][nb]);
+                    o[cg][nb] = mfma16x16x32(plo[cg][kp], vb, o[cg][nb]);
+                }
+            }
+        if (tile + 1 < ntiles) stash(tile + 1, buf ^ 1);  // the other buffer was last read before the barrier
+        __syncthreads();
+    }
+    // o[cg][nb][i] = O[column 16 cg + 4 q4 + i of the wavefront][dim 16 nb + n]; lane c < 16 of
+    // the group holds column c's sum once the 4 lanes of a column are added.
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+        float l = lsum[cg] + __shfl_xor(lsum[cg], 16, 64);
+        l += __shfl_xor(l, 32, 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t cl = 4 * q4 + i, c = 16 * CG * wave + 16 * cg + cl;
+            const float lc = __shfl(l, (int)cl, 64);
+            const uint32_t rc = r0 + c / G;
+            if (rc < rows) {
+                bf16_t* op = out + ((size_t)rc * q_heads + kh * G + c % G) * X0NE_HEAD_DIM;
+#pragma unroll
+                for (int nb = 0; nb < 8; ++nb) op[16 * nb + n] = f2bf(o[cg][nb][i] / lc);
+            }
         }
     }
 }
@@ -1343,13 +1548,16 @@ __device__ __forceinline__ void prefill_wave(const bf16_t* __restrict__ q, const
 
 // x0ne_attention_prefill_g{G}_bf16: the causal prefill of x0ne_attention_prefill_bf16 (same
 // arguments and semantics) on the matrix cores for G q heads per kv head; grid (kv_heads,
-// ceil(rows / (64 / G))), block 256.
+// ceil(rows / (128 / G))), block 256, two wavefronts per SIMD.
 #define X0NE_PREFILL_GROUP(G)                                                                                      \
-    extern "C" __global__ void __launch_bounds__(256) x0ne_attention_prefill_g##G##_bf16(                          \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))                  \
+        x0ne_attention_prefill_g##G##_bf16(                                                                       \
         const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
         const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos0,          \
         uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale) {                       \
-        prefill_wave<G>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx, scale);       \
+        __shared__ PrefillShared sh;                                                                               \
+        prefill_block<G, PF_CG>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx, scale, \
+                                sh);                                                                               \
     }
 X0NE_PREFILL_GROUP(1)
 X0NE_PREFILL_GROUP(2)

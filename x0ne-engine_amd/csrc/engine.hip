@@ -963,7 +963,7 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
             void* args[] = {(void*)&q,    (void*)&kc, (void*)&vc,  (void*)&pt,      (void*)&out, (void*)&pos,
                             (void*)&rows, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&scale};
             if (grouped) {
-                const uint32_t per = 64 / group;  // rows per block
+                const uint32_t per = X0NE_PREFILL_COLS / group;  // rows per block
                 X0NE_TRY(launch_rows(e, grouped, dim3(kvh, (rows + per - 1) / per), dim3(256), args, "prefill attention"));
             } else {
                 X0NE_TRY(launch_rows(e, (const void*)&x0ne_attention_prefill_bf16, dim3(qh, rows), dim3(256), args,

@@ -20,6 +20,7 @@ from .gpu import Arg, Gpu, SplitPlan, split_state_bytes
 HEAD_DIM = 128
 PAGE = 16
 SPLIT_STATE = HEAD_DIM + 4
+PREFILL_COLS = 128  # columns (row, q head) per block of x0ne_attention_prefill_g*_bf16
 NAN_BF16 = 0x7FC0
 
 
@@ -699,7 +700,7 @@ class Kernels:
         g = h.q_heads // h.kv_heads
         if grouped and g not in (1, 2, 4, 8):
             raise FormatError(f"attention_prefill_at: no grouped kernel for group {g}")
-        name, grid = ((f"x0ne_attention_prefill_g{g}_bf16", (h.kv_heads, (m + 64 // g - 1) // (64 // g))) if grouped
+        name, grid = ((f"x0ne_attention_prefill_g{g}_bf16", (h.kv_heads, (m + PREFILL_COLS // g - 1) // (PREFILL_COLS // g))) if grouped
                       else ("x0ne_attention_prefill_bf16", (h.q_heads, m)))
         self.gpu.launch(name, grid, 256,
                         [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
