@@ -104,7 +104,8 @@ x0ne_status x0ne_gpu_launch_3d(x0ne_gpu* g, const char* name, uint32_t gx, uint3
    X[n][cols] W^T, W [rows][cols] row-major bf16, X bf16, f32 accumulation; out_f32 = 0 gives
    bf16 Y, 1 f32 Y. Device addresses. One row of X: the bandwidth-bound GEMV; 2 to 64 rows (cols
    a multiple of 8, W and X each below 4 GiB): one few-row matrix-core launch that reads each W
-   row once (x0ne_gemm_few_*); more rows: one tiled matrix-core GEMM launch (x0ne_gemm_bf16). */
+   row once (x0ne_gemm_few_*); more rows: hipBLASLt (bf16 in, f32 accumulation, one fixed
+   algorithm per shape, no workspace), as the reference hands it to cuBLAS. */
 x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n, uint64_t y,
                           int out_f32);
 

@@ -221,9 +221,12 @@ def test_gemv_is_the_oracle_on_random_shapes(kernels, seed):
 
 @pytest.mark.parametrize("seed", range(16))
 def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
-    """Gpu::gemm over many rows (the matrix-core GEMM from 4 rows on): every row of Y is the
-    oracle's GEMV of that row of X within the GEMV tolerance (gpu_kernels.rs:331-393), at tile
-    edges of both sides and K tails; the bf16 output is the f32 output rounded."""
+    """Gpu::gemm over many rows (the few-row matrix-core kernel up to 64 rows, hipBLASLt past
+    them): every row of Y is the oracle's GEMV of that row of X within the GEMV tolerance
+    (gpu_kernels.rs:331-393), at tile edges of both sides and K tails. Up to 64 rows the bf16
+    output is the f32 output rounded (one accumulation, two stores); past them the library may
+    pick different kernels for the two output types, and, as the reference does for its GEMV
+    (gpu_kernels.rs:372-377), the test only reports whether they agree."""
     rng = O.Rng(700 + seed)
     n = rng.pick([2, 3, 4, 5, 16, 17, 31, 33, 64, 65, 128, 129, 257])
     rows = rng.pick([1, 15, 128, 129, 384, 1000])
@@ -240,7 +243,13 @@ def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
         mag = O.gemv_magnitude(w, rows, cols, xr)
         assert_gemv(f"{what} row {r} f32", f[r], want, mag, False)
         assert_gemv(f"{what} row {r} bf16", bf16_vals(b[r]), want, mag, True)
-    assert (b == bf16_bits(f).reshape(b.shape)).all(), what
+    same = bool((b == bf16_bits(f).reshape(b.shape)).all())
+    if n <= 64:
+        assert same, what
+    else:
+        print(f"MEASURE {what}: bf16 out is the rounded f32 out: {same}")
+    # Each shape runs the same kernels on every call: the same bits.
+    assert (kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True).view(np.uint32) == f.view(np.uint32)).all(), what
 
 
 @pytest.mark.parametrize("seed", range(24))

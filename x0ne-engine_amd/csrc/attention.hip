@@ -439,8 +439,7 @@ __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewR
                     sc[kp][h][i] = base + key < ctx_col ? sacc[kp][h][i] * scale2 : -INFINITY;
                     mx = fmaxf(mx, sc[kp][h][i]);
                 }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = rows_max(mx);
         const float mn = fmaxf(m_run, mx);  // key `base` is below ctx: mn is finite
         const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
         m_run = mn;
@@ -528,8 +527,7 @@ __device__ __forceinline__ void attend_wave_mfma(Prologue&& prologue, const NewR
         for (int i = 0; i < 4; ++i) pg[i] = pg_next[i];
         tile_pages(t + 2 * tstep, pg_next);
     }
-    float l = lsum + __shfl_xor(lsum, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = rows_sum(lsum);
     m_out = m_run * LN2;  // back to natural units for the merges
     l_out = l;
 }
@@ -1501,8 +1499,7 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[cg][kp][h][i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = rows_max(mx);
             // Key 0 is in every column's first tile, so m_run is finite from there on.
             const float mn = fmaxf(m_run[cg], mx * scale2);
             const float alpha = __builtin_amdgcn_exp2f(m_run[cg] - mn);
@@ -1565,8 +1562,7 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
     // the group holds column c's sum once the 4 lanes of a column are added.
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) {
-        float l = lsum[cg] + __shfl_xor(lsum[cg], 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        const float l = rows_sum(lsum[cg]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t cl = 4 * q4 + i, c = 16 * CG * wave + 16 * cg + cl;

@@ -37,6 +37,10 @@ struct Counts {
         if (s_ != X0NE_OK) return s_;           \
     } while (0)
 
+namespace x0ne {
+struct LibGemm;  // the library GEMM's handle and per-shape plans (runtime.hip)
+}
+
 struct x0ne_gpu {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -49,6 +53,8 @@ struct x0ne_gpu {
     // This device's copy of the library's static scratch array (runtime.hip, `scratch`), as
     // hipGetSymbolAddress gave it at x0ne_gpu_new with the device current.
     void* scratch = nullptr;
+    // hipBLASLt for the many-row projections, opened at the first one.
+    x0ne::LibGemm* lib_gemm = nullptr;
 };
 
 struct x0ne_graph {

@@ -84,8 +84,6 @@ __global__ void x0ne_add_rmsnorm_panel_bf16(float* residual, const bf16_t* x, co
                                             uint32_t hidden, float eps);
 __global__ void x0ne_advance_u32(uint32_t* pos);
 __global__ void x0ne_feed_u32(const uint32_t* ids, uint32_t i, uint32_t* tokens, uint32_t* pos);
-__global__ void x0ne_gemm_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, uint32_t n,
-                               uint32_t out_f32);
 #define X0NE_DECLARE_FEW(V)                                                                                      \
     __global__ void x0ne_gemm_few_##V##_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, \
                                              uint32_t n, uint32_t out_f32);

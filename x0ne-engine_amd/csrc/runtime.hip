@@ -1,8 +1,12 @@
 // The device, the kernel-launch API, graph capture and the arena: the reference's
 // x0ne-core/runtime/src/{gpu,arena,error}.rs, on the HIP runtime for gfx950.
+#include <hipblaslt/hipblaslt.h>
+
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
+#include <tuple>
 
 #include "internal.h"
 
@@ -99,10 +103,15 @@ extern "C" x0ne_status x0ne_gpu_new(x0ne_gpu** out) {
     return X0NE_OK;
 }
 
+namespace x0ne {
+void lib_gemm_close(x0ne_gpu* g);
+}
+
 extern "C" void x0ne_gpu_free(x0ne_gpu* g) {
     if (!g) return;
     if (g->stream) {
         (void)hipStreamSynchronize(g->stream);
+        x0ne::lib_gemm_close(g);
         (void)hipStreamDestroy(g->stream);
     }
     delete g;
@@ -273,6 +282,103 @@ static constexpr uint64_t GEMM_MAX_BYTES = 0xFFFFFFF0ull;
 
 namespace x0ne {
 
+// ---- many rows: hipBLASLt ----
+// The reference hands Gpu::gemm to cuBLAS (gpu.rs:1098-1149); from SKINNY_MAX_ROWS + 1 rows on
+// this library hands it to hipBLASLt. Row-major Y[n][rows] = X[n][cols] W^T is, column-major,
+// D (rows x n) = op(A) B with A = W as a cols x rows matrix (op T) and B = X as cols x n (op N):
+// bf16 A and B, f32 accumulation, D bf16 or f32. Each shape's plan (descriptors and the
+// heuristic's first algorithm among those that need no workspace) is made once and kept, so a
+// shape always runs the same kernels: results are the same from call to call.
+struct LibGemm {
+    hipblasLtHandle_t handle = nullptr;
+    struct Plan {
+        hipblasLtMatmulDesc_t desc = nullptr;
+        hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+        hipblasLtMatmulAlgo_t algo;
+    };
+    std::map<std::tuple<uint64_t, uint64_t, uint64_t, bool>, Plan> plans;
+};
+
+void lib_gemm_close(x0ne_gpu* g) {
+    if (!g->lib_gemm) return;
+    for (auto& kv : g->lib_gemm->plans) {
+        auto& p = kv.second;
+        if (p.a) (void)hipblasLtMatrixLayoutDestroy(p.a);
+        if (p.b) (void)hipblasLtMatrixLayoutDestroy(p.b);
+        if (p.d) (void)hipblasLtMatrixLayoutDestroy(p.d);
+        if (p.desc) (void)hipblasLtMatmulDescDestroy(p.desc);
+    }
+    if (g->lib_gemm->handle) (void)hipblasLtDestroy(g->lib_gemm->handle);
+    delete g->lib_gemm;
+    g->lib_gemm = nullptr;
+}
+
+static x0ne_status lt_fail(hipblasStatus_t st, const std::string& what) {
+    return fail(X0NE_ERR_GPU, "hipBLASLt " + what + ": status " + std::to_string((int)st));
+}
+
+x0ne_status lib_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
+                     bool out_f32) {
+    if (g->capturing) return fail(X0NE_ERR_GPU, "gemm: the many-row projection is not captured into a graph");
+    hipblasStatus_t st;
+    if (!g->lib_gemm) {
+        auto* lg = new LibGemm();
+        st = hipblasLtCreate(&lg->handle);
+        if (st != HIPBLAS_STATUS_SUCCESS) {
+            delete lg;
+            return lt_fail(st, "create");
+        }
+        g->lib_gemm = lg;
+    }
+    auto key = std::make_tuple(rows, cols, n, out_f32);
+    auto it = g->lib_gemm->plans.find(key);
+    if (it == g->lib_gemm->plans.end()) {
+        LibGemm::Plan p;
+        auto done = [&](hipblasStatus_t s, const char* what) -> x0ne_status {
+            if (p.a) (void)hipblasLtMatrixLayoutDestroy(p.a);
+            if (p.b) (void)hipblasLtMatrixLayoutDestroy(p.b);
+            if (p.d) (void)hipblasLtMatrixLayoutDestroy(p.d);
+            if (p.desc) (void)hipblasLtMatmulDescDestroy(p.desc);
+            return lt_fail(s, what);
+        };
+        if ((st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) != HIPBLAS_STATUS_SUCCESS)
+            return done(st, "descriptor");
+        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+        if ((st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) !=
+                HIPBLAS_STATUS_SUCCESS ||
+            (st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb))) !=
+                HIPBLAS_STATUS_SUCCESS)
+            return done(st, "transposes");
+        if ((st = hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, cols, rows, cols)) != HIPBLAS_STATUS_SUCCESS ||
+            (st = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, cols, n, cols)) != HIPBLAS_STATUS_SUCCESS ||
+            (st = hipblasLtMatrixLayoutCreate(&p.d, out_f32 ? HIP_R_32F : HIP_R_16BF, rows, n, rows)) !=
+                HIPBLAS_STATUS_SUCCESS)
+            return done(st, "layouts");
+        hipblasLtMatmulPreference_t pref = nullptr;
+        if ((st = hipblasLtMatmulPreferenceCreate(&pref)) != HIPBLAS_STATUS_SUCCESS) return done(st, "preference");
+        const uint64_t no_workspace = 0;
+        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_workspace,
+                                                   sizeof(no_workspace));
+        hipblasLtMatmulHeuristicResult_t res = {};
+        int got = 0;
+        if (st == HIPBLAS_STATUS_SUCCESS)
+            st = hipblasLtMatmulAlgoGetHeuristic(g->lib_gemm->handle, p.desc, p.a, p.b, p.d, p.d, pref, 1, &res, &got);
+        (void)hipblasLtMatmulPreferenceDestroy(pref);
+        if (st != HIPBLAS_STATUS_SUCCESS) return done(st, "heuristic");
+        if (got < 1) return done(HIPBLAS_STATUS_NOT_SUPPORTED, "heuristic (no algorithm)");
+        p.algo = res.algo;
+        it = g->lib_gemm->plans.emplace(key, p).first;
+    }
+    const auto& p = it->second;
+    const float alpha = 1.f, beta = 0.f;
+    g->counts.gemms++;
+    g->counts.launches++;
+    st = hipblasLtMatmul(g->lib_gemm->handle, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.algo, nullptr,
+                         0, g->stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return lt_fail(st, "matmul");
+    return X0NE_OK;
+}
+
 x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
                    uint32_t mode, uint32_t panels) {
     const uint64_t wrows = mode == 2 ? 2 * rows : rows;
@@ -435,20 +541,10 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
     if (n >= 2 && n <= SKINNY_MAX_ROWS && cols % 8 == 0 && rows * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 &&
         x % 16 == 0)
         return x0ne::skinny(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 ? 1 : 0, 0);
-    // Many rows: one matrix-core GEMM launch, the weights read once.
+    // Many rows: hipBLASLt.
     if (n > SKINNY_MAX_ROWS && cols % 8 == 0 && n <= UINT32_MAX && rows * cols * 2 <= GEMM_MAX_BYTES &&
-        n * cols * 2 <= GEMM_MAX_BYTES) {
-        g->counts.gemms++;
-        g->counts.launches++;
-        const bf16_t* wp = (const bf16_t*)w;
-        const bf16_t* xp = (const bf16_t*)x;
-        void* yp = (void*)y;
-        uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, f32 = out_f32 ? 1u : 0u;
-        void* args[] = {(void*)&wp, (void*)&xp, (void*)&yp, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&f32};
-        const uint32_t tiles = (uint32_t)(((rows + 127) / 128) * ((n + 127) / 128));
-        X0NE_HIP(x0ne_launch((const void*)&x0ne_gemm_bf16, dim3(tiles), dim3(256), args, 0, g->stream), "gemm");
-        return X0NE_OK;
-    }
+        n * cols * 2 <= GEMM_MAX_BYTES)
+        return x0ne::lib_gemm(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 != 0);
     for (uint64_t r = 0; r < n; ++r) {
         const uint16_t* wp = (const uint16_t*)w;
         const uint16_t* xp = (const uint16_t*)(x + r * cols * 2);

@@ -261,7 +261,8 @@ class Kernels:
 
     def gemm(self, w, rows, cols, x, n, out_f32) -> np.ndarray:
         """Gpu::gemm over n rows of X (gpu.rs:1098-1149): Y[n][rows] = X[n][cols] W^T, the
-        matrix-core GEMM from 4 rows on; returns Y (f32, or bf16 bits)."""
+        few-row matrix-core kernel from 2 to 64 rows, hipBLASLt past them; returns Y (f32, or
+        bf16 bits)."""
         if rows == 0 or cols == 0 or n == 0 or w.size != rows * cols or x.size != n * cols:
             raise FormatError(f"gemm: W {w.size} for {rows}x{cols}, X {x.size} for {n} rows")
         ob = 4 if out_f32 else 2
