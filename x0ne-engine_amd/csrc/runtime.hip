@@ -1,5 +1,6 @@
 // The device, the kernel-launch API, graph capture and the arena: the reference's
 // x0ne-core/runtime/src/{gpu,arena,error}.rs, on the HIP runtime for gfx950.
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdio>
@@ -286,9 +287,13 @@ namespace x0ne {
 // The reference hands Gpu::gemm to cuBLAS (gpu.rs:1098-1149); from SKINNY_MAX_ROWS + 1 rows on
 // this library hands it to hipBLASLt. Row-major Y[n][rows] = X[n][cols] W^T is, column-major,
 // D (rows x n) = op(A) B with A = W as a cols x rows matrix (op T) and B = X as cols x n (op N):
-// bf16 A and B, f32 accumulation, D bf16 or f32. Each shape's plan (descriptors and the
-// heuristic's first algorithm among those that need no workspace) is made once and kept, so a
-// shape always runs the same kernels: results are the same from call to call.
+// bf16 A and B, f32 accumulation, D bf16 or f32. Each shape's plan (descriptors and one
+// algorithm) is made once and kept, so a shape always runs the same kernels: results are the
+// same from call to call. The algorithm: among the heuristic's first 16 that need no workspace,
+// the first whose macro tiles (MTaxb in its kernel name: a rows of D by b columns) number at
+// least the device's CUs, else the heuristic's first. (Measured on MI355X at 2048 rows: the
+// heuristic's first pick for a 4096-wide projection is a 256 x 256 tile, 128 tiles for 256
+// CUs, 74.5 us; its second, 256 x 128, takes 57.8 us.)
 struct LibGemm {
     hipblasLtHandle_t handle = nullptr;
     struct Plan {
@@ -359,14 +364,26 @@ x0ne_status lib_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, c
         const uint64_t no_workspace = 0;
         st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_workspace,
                                                    sizeof(no_workspace));
-        hipblasLtMatmulHeuristicResult_t res = {};
+        hipblasLtMatmulHeuristicResult_t res[16] = {};
         int got = 0;
         if (st == HIPBLAS_STATUS_SUCCESS)
-            st = hipblasLtMatmulAlgoGetHeuristic(g->lib_gemm->handle, p.desc, p.a, p.b, p.d, p.d, pref, 1, &res, &got);
+            st = hipblasLtMatmulAlgoGetHeuristic(g->lib_gemm->handle, p.desc, p.a, p.b, p.d, p.d, pref, 16, res, &got);
         (void)hipblasLtMatmulPreferenceDestroy(pref);
         if (st != HIPBLAS_STATUS_SUCCESS) return done(st, "heuristic");
         if (got < 1) return done(HIPBLAS_STATUS_NOT_SUPPORTED, "heuristic (no algorithm)");
-        p.algo = res.algo;
+        int pick = 0;
+        for (int i = 0; i < got; ++i) {
+            const std::string name = hipblaslt_ext::getKernelNameFromAlgo(g->lib_gemm->handle, res[i].algo);
+            const size_t at = name.find("_MT");
+            unsigned ma = 0, mb = 0;
+            if (at == std::string::npos || std::sscanf(name.c_str() + at, "_MT%ux%u", &ma, &mb) != 2 || !ma || !mb)
+                continue;
+            if (((rows + ma - 1) / ma) * ((n + mb - 1) / mb) >= g->cus) {
+                pick = i;
+                break;
+            }
+        }
+        p.algo = res[pick].algo;
         it = g->lib_gemm->plans.emplace(key, p).first;
     }
     const auto& p = it->second;
