@@ -260,30 +260,18 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
     if args.calibrate_copy:
         copy_calibration(args.calibrate_copy << 20)
 
-    # Parity of the timed path: its greedy tokens against the CPU oracle's committed fixture for
-    # this workload (64 steps), and the other accumulation mode timed and checked the same way.
-    fixture = oracle_fixture(args.model, prompt)
-    parity = {"oracle_fixture": fixture["path"] if fixture else None,
-              "timed_path": mode_parity(e, prompt, fixture, args.f64_sums)}
-    if not args.no_other_mode:
-        e.close()
-        other = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=max_ctx, page_seed=1,
-                                                                    f64_sums=not args.f64_sums))
-        if args.eager:
-            other.set_decode_mode(DecodeMode.EAGER)
-        o_runs = []
-        for _ in range(max(1, min(args.runs, 2))):
-            o_toks, o_secs = other.decode_timed(prompt, args.warmup, args.steps)
-            o_runs.append(o_secs)
-        o_secs = min(o_runs)
-        o = mode_parity(other, prompt, fixture, not args.f64_sums)
-        o.update({"value": round(args.steps / o_secs, 3), "unit": "tok/s", "ms_per_step": round(1e3 * o_secs / args.steps, 4),
-                  "decode_hbm_frac": round(step_bytes * args.steps / o_secs / 1e9 / 8000.0, 4),
-                  "same_tokens_as_timed_path": int(next((i for i in range(min(o_toks.size, tokens.size))
-                                                         if o_toks[i] != tokens[i]), min(o_toks.size, tokens.size)))})
-        parity["other_mode"] = o
-        other.close()
-        print(f"[bench] other mode {o}", file=sys.stderr, flush=True)
+    # Parity of the timed path: sequence 0's batched greedy tokens against the CPU oracle's
+    # committed fixture for its prompt, where one exists. The exact mode has no batched step, so
+    # no other mode is timed here.
+    fixture = oracle_fixture(args.model, prompts[0])
+    timed = {"mode": "f64 sums (exact mode)" if args.f64_sums else "f32 sums", "tokens_equal_to_oracle": None}
+    if fixture is not None:
+        n = min(fixture["tokens"].size, tokens.shape[1])
+        agree = next((i for i in range(n) if tokens[0][i] != fixture["tokens"][i]), n)
+        timed.update({"tokens_equal_to_oracle": agree, "of": n, "source": "batched tokens of sequence 0",
+                      "oracle_margin_at_first_difference": None if agree == n else round(fixture["margins"][agree], 6)})
+    parity = {"oracle_fixture": fixture["path"] if fixture else None, "timed_path": timed,
+              "other_mode": None}
     print(f"[bench] parity {parity['timed_path']}", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
