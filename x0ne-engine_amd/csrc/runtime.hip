@@ -558,9 +558,9 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
     if (n >= 2 && n <= SKINNY_MAX_ROWS && cols % 8 == 0 && rows * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 &&
         x % 16 == 0)
         return x0ne::skinny(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 ? 1 : 0, 0);
-    // Many rows: hipBLASLt.
+    // Many rows: hipBLASLt (16-byte aligned operands; otherwise the row-by-row GEMV below).
     if (n > SKINNY_MAX_ROWS && cols % 8 == 0 && n <= UINT32_MAX && rows * cols * 2 <= GEMM_MAX_BYTES &&
-        n * cols * 2 <= GEMM_MAX_BYTES)
+        n * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 && x % 16 == 0 && y % 16 == 0)
         return x0ne::lib_gemm(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 != 0);
     for (uint64_t r = 0; r < n; ++r) {
         const uint16_t* wp = (const uint16_t*)w;
