@@ -471,7 +471,8 @@ def test_batched_attention_is_each_sequence_alone_bit_for_bit(kernels, qh, kvh):
 def test_config2_decode_attention_at_long_contexts(kernels, ctx):
     """BASELINE.json config 2 at its long contexts: 32 q / 8 kv heads, head_dim 128, bf16 Q, K and V
     drawn N(0, 1) from a seed, the keys in 16-position pages in a shuffled order, split-K at P 1,
-    4, 16 and the engine's plan: within max|V|/128 of the oracle (gpu_kernels.rs:437-599), the
+    4, 16, the engine's plan, 64 and 128 (more slices than one merge chunk of 32): within
+    max|V|/128 of the oracle (gpu_kernels.rs:437-599), the
     merge kernel and the last-block merge the same bits, a repeated launch the same bits; and
     the fused kernel (QK-norm, RoPE and the K/V write in front) on the same cache."""
     from x0ne_core.ops import CacheAt
@@ -483,7 +484,7 @@ def test_config2_decode_attention_at_long_contexts(kernels, ctx):
     page_of = [int(p) for p in g.permutation(pages)]
     want = O.attention_decode(bf16_vals(q), bf16_vals(k), bf16_vals(v), ctx, 32, 8)
     atol = ATTENTION_ATOL_OF_VMAX * max_abs(bf16_vals(v))
-    for splits in (1, 4, 16, None):
+    for splits in (1, 4, 16, None, 64, 128):
         outs = []
         for last_block in (True, False, True):
             out = kernels.attention_decode_split(q, k, v, ctx, h, last_block=last_block, splits=splits,
