@@ -159,6 +159,12 @@ def test_qk_norm_rope_is_the_oracle_and_writes_one_paged_slot(kernels, seed):
     assert (out.v_row == bf16_bits(v)).all(), f"{what}: v is copied"
     for name, got, want in [("q", out.q, q), ("k", out.k_row, k)]:
         assert_close(f"{what} {name}", bf16_vals(got), want, ROPE_ATOL_OF_XMAX * max_abs(want) + BF16_ATOL, BF16_RTOL)
+    # The prefill pass's kernel, cos and sin from the RoPE table: the same bits and the same slot.
+    rows = kernels.qk_norm_rope_kv_write(bf16_bits(qkv), bf16_bits(qn), bf16_bits(kn), h, theta, 1e-6, at,
+                                         page_of=page_of, pool=pool, table=True)
+    assert rows.rest_untouched, f"{what} (table): a cache byte outside the slot was written"
+    for name, got, want in [("q", rows.q, out.q), ("k", rows.k_row, out.k_row), ("v", rows.v_row, out.v_row)]:
+        assert (got == want).all(), f"{what} (table): {name} differs from the direct kernel's"
 
 
 def test_rope_far_into_a_long_context(kernels):
@@ -174,6 +180,9 @@ def test_rope_far_into_a_long_context(kernels):
         q, _, _ = O.qk_norm_rope(qkv, ones, ones, inv_freq(128, 1e6), 2, 1, 128, pos, 1e-6)
         assert_close(f"rope at {pos}", bf16_vals(out.q), q, ROPE_ATOL_OF_XMAX * max_abs(q), BF16_RTOL)
         assert out.rest_untouched
+        rows = kernels.qk_norm_rope_kv_write(bf16_bits(qkv), bf16_bits(ones), bf16_bits(ones), h, 1e6, 1e-6,
+                                             CacheAt(1, pos + 1, 0, pos), table=True)
+        assert (rows.q == out.q).all() and (rows.k_row == out.k_row).all(), f"table rope at {pos}"
 
 
 def test_rope_table_is_the_cosine_and_sine_of_the_f32_angle(kernels):
@@ -631,7 +640,9 @@ def test_swiglu_is_the_oracle(kernels, seed):
 def test_swiglu_special_values(kernels):
     s = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 200.0, -200.0, bf16_vals(1)[0], bf16_vals(0x7F7F)[0],
                   bf16_vals(0xFF7F)[0]], np.float32)
-    for gate, up in [(s, np.full(s.size, 2.0, np.float32)), (np.ones(s.size, np.float32), s)]:
+    s16 = np.concatenate([s, s[:6]])  # 16 values: the 16-byte path (inter a multiple of 8)
+    for gate, up in [(s, np.full(s.size, 2.0, np.float32)), (np.ones(s.size, np.float32), s),
+                     (s16, np.full(16, 2.0, np.float32)), (np.ones(16, np.float32), s16)]:
         gu = np.concatenate([gate, up])
         got = bf16_vals(kernels.swiglu(bf16_bits(gu)))
         want = O.bf16_round(O.swiglu(gu))

@@ -942,16 +942,16 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
             const void* qkv = e->d(e->p_qkv);
             const void* qn = e->d(w.q_norm);
             const void* kn = e->d(w.k_norm);
-            const void* inv = e->d(e->inv_freq);
+            const void* cs = e->d(e->rope_cs);
             void* q = e->d(e->p_q);
             void* kc = e->plane(l, 0);
             void* vc = e->plane(l, 1);
             const void* pt = e->pages_of(b);
             const void* pos = e->pos_of(b);
-            void* args[] = {(void*)&qkv, (void*)&qn, (void*)&kn, (void*)&inv, (void*)&q,       (void*)&kc, (void*)&vc,
+            void* args[] = {(void*)&qkv, (void*)&qn, (void*)&kn, (void*)&cs, (void*)&q,       (void*)&kc, (void*)&vc,
                             (void*)&pt,  (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
-            X0NE_TRY(launch_rows(e, (const void*)&x0ne_qk_norm_rope_kv_write_bf16, dim3(qh + kvh, rows), dim3(64), args,
-                                 "qk_norm_rope_kv_write"));
+            X0NE_TRY(launch_rows(e, (const void*)&x0ne_qk_norm_rope_kv_write_rows_bf16, dim3((qh + kvh + 3) / 4, rows),
+                                 dim3(256), args, "qk_norm_rope_kv_write"));
         }
         {
             const void* q = e->d(e->p_q);
@@ -977,7 +977,7 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
             const void* gu = e->d(e->p_gu);
             void* act = e->d(e->p_act);
             void* args[] = {(void*)&gu, (void*)&act, (void*)&inter};
-            X0NE_TRY(launch_rows(e, (const void*)&x0ne_swiglu_bf16, dim3((inter + 255) / 256, rows), dim3(256), args,
+            X0NE_TRY(launch_rows(e, (const void*)&x0ne_swiglu_bf16, dim3((inter + 2047) / 2048, rows), dim3(256), args,
                                  "swiglu"));
         }
         X0NE_TRY(gemm(e, w.down, c.hidden, c.inter, e->p_act, n, e->p_delta));

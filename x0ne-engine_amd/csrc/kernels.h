@@ -20,6 +20,10 @@ __global__ void x0ne_qk_norm_rope_kv_write_bf16(const bf16_t* qkv, const bf16_t*
                                                 const float* inv_freq, bf16_t* q_out, bf16_t* k_cache,
                                                 bf16_t* v_cache, const uint32_t* pages, const uint32_t* pos0,
                                                 uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float eps);
+__global__ void x0ne_qk_norm_rope_kv_write_rows_bf16(const bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm,
+                                                     const double* cs, bf16_t* q_out, bf16_t* k_cache,
+                                                     bf16_t* v_cache, const uint32_t* pages, const uint32_t* pos0,
+                                                     uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float eps);
 __global__ void x0ne_attention_decode_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache,
                                            const uint32_t* pages, bf16_t* out, const uint32_t* pos, uint32_t q_heads,
                                            uint32_t kv_heads, uint32_t max_ctx, float scale);

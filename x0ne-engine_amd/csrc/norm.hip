@@ -203,6 +203,53 @@ extern "C" __global__ void __launch_bounds__(64)
     v_cache[vat + (i + HALF) * X0NE_PAGE] = vs[i + HALF];
 }
 
+// x0ne_qk_norm_rope_kv_write_bf16 for the rows of a prefill pass: the same arithmetic and
+// writes, with each position's cos and sin read from the RoPE table cs (x0ne_rope_table_f64 below,
+// positions < max_ctx) instead of computed, and four heads of one row per 256-thread block (one
+// per wavefront). The table holds the f64 values the direct kernel computes, so the two give
+// the same bits. grid (ceil((q_heads + kv_heads) / 4), rows), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_qk_norm_rope_kv_write_rows_bf16(const bf16_t* __restrict__ qkv, const bf16_t* __restrict__ q_norm,
+                                         const bf16_t* __restrict__ k_norm, const double* __restrict__ cs,
+                                         bf16_t* __restrict__ q_out, bf16_t* __restrict__ k_cache,
+                                         bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
+                                         const uint32_t* __restrict__ pos0, uint32_t q_heads, uint32_t kv_heads,
+                                         uint32_t max_ctx, float eps) {
+    constexpr uint32_t HD = X0NE_HEAD_DIM, HALF = HD / 2;
+    const uint32_t head = blockIdx.x * 4 + (threadIdx.x >> 6), row = blockIdx.y, i = threadIdx.x & 63;
+    if (head >= q_heads + kv_heads) return;  // wavefront-uniform
+    const uint32_t q_dim = q_heads * HD, kv_dim = kv_heads * HD, qkv_dim = q_dim + 2 * kv_dim;
+    const uint32_t pos = pos0[0] + row;
+    if (pos >= max_ctx) return;  // no table entry, and no cache slot; a pass never reaches it
+    const bool is_q = head < q_heads;
+    const uint32_t kh = is_q ? 0 : head - q_heads;
+    const bf16_t* src = qkv + (size_t)row * qkv_dim + (is_q ? head * HD : q_dim + kh * HD);
+    const bf16_t* nw = is_q ? q_norm : k_norm;
+
+    const double2 t = reinterpret_cast<const double2*>(cs)[(size_t)pos * HALF + i];  // (cos, sin)
+    const float a = bf2f(src[i]), b = bf2f(src[i + HALF]);
+    const double ss = wave_sum_d((double)a * (double)a + (double)b * (double)b);
+    const double scale = 1.0 / sqrt(ss / (double)HD + (double)eps);
+    const double na = (double)a * scale * (double)bf2f(nw[i]);
+    const double nb = (double)b * scale * (double)bf2f(nw[i + HALF]);
+    const float ra = (float)(na * t.x - nb * t.y);
+    const float rb = (float)(nb * t.x + na * t.y);
+
+    if (is_q) {
+        bf16_t* d = q_out + (size_t)row * q_dim + head * HD;
+        d[i] = f2bf(ra);
+        d[i + HALF] = f2bf(rb);
+        return;
+    }
+    const uint32_t at = kv_row(pages, pos, kh, kv_heads);
+    k_cache[at + i] = f2bf(ra);
+    k_cache[at + i + HALF] = f2bf(rb);
+    const bf16_t* vs = qkv + (size_t)row * qkv_dim + q_dim + kv_dim + kh * HD;
+    const uint32_t vat = v_slot(pages, pos, kh, kv_heads);
+    v_cache[vat + i * X0NE_PAGE] = vs[i];
+    v_cache[vat + (i + HALF) * X0NE_PAGE] = vs[i + HALF];
+}
+
 // The RoPE table of the fused decode attention: cs[2 (p 64 + i)] = cos and cs[2 (p 64 + i) + 1] =
 // sin of the f64 angle (double)((float)p * inv_freq[i]), positions p < positions: the values the
 // rotation above computes, so a kernel that reads them rotates to the same bits. grid
@@ -218,14 +265,32 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 // SwiGLU on the packed [gate; up] row: out[i] = g / (1 + e^-g) * u, in f64 (swiglu.cu:5-11;
-// oracle/src/lib.rs:205-214). grid (ceil(inter / 256), rows), block 256.
+// oracle/src/lib.rs:205-214). Thread t of block x takes values 8 (256 x + t) .. + 7 of row y:
+// 16-byte loads of gate and up and one 16-byte store where inter is a multiple of 8 (single
+// values otherwise). grid (ceil(inter / 2048), rows), block 256.
+__device__ __forceinline__ bf16_t swiglu1(bf16_t g16, bf16_t u16) {
+    const double g = (double)bf2f(g16), u = (double)bf2f(u16);
+    return f2bf((float)(g / (1.0 + exp(-g)) * u));
+}
 extern "C" __global__ void __launch_bounds__(256)
     x0ne_swiglu_bf16(const bf16_t* __restrict__ gate_up, bf16_t* __restrict__ out, uint32_t inter) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
-    if (i >= inter) return;
+    const uint32_t i0 = 8 * (blockIdx.x * blockDim.x + threadIdx.x), r = blockIdx.y;
+    if (i0 >= inter) return;
     const bf16_t* row = gate_up + (size_t)r * 2 * inter;
-    const double g = (double)bf2f(row[i]), u = (double)bf2f(row[inter + i]);
-    out[(size_t)r * inter + i] = f2bf((float)(g / (1.0 + exp(-g)) * u));
+    bf16_t* o = out + (size_t)r * inter;
+    if (inter % 8 == 0) {
+        const uint4 g = *reinterpret_cast<const uint4*>(row + i0);
+        const uint4 u = *reinterpret_cast<const uint4*>(row + inter + i0);
+        const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            ow[j] = (uint32_t)swiglu1((bf16_t)(gw[j] & 0xFFFFu), (bf16_t)(uw[j] & 0xFFFFu)) |
+                    ((uint32_t)swiglu1((bf16_t)(gw[j] >> 16), (bf16_t)(uw[j] >> 16)) << 16);
+        *reinterpret_cast<uint4*>(o + i0) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        return;
+    }
+    for (uint32_t i = i0; i < min(i0 + 8, inter); ++i) o[i] = swiglu1(row[i], row[inter + i]);
 }
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {

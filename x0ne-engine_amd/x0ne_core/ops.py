@@ -188,7 +188,9 @@ class Kernels:
 
     # -- qk_norm_rope_kv_write (ops.rs:302-384), paged --
     def qk_norm_rope_kv_write(self, qkv, q_norm, k_norm, heads: Heads, theta: float, eps: float, at: CacheAt,
-                              page_of=None, pool=None) -> QkvOut:
+                              page_of=None, pool=None, table: bool = False) -> QkvOut:
+        """table: the prefill pass's kernel (x0ne_qk_norm_rope_kv_write_rows_bf16), reading cos and
+        sin from the RoPE table (filled here for max_ctx positions) instead of computing them."""
         heads.check()
         hd, qd, kvd = heads.head_dim, heads.q_dim, heads.kv_dim
         if qkv.size != qd + 2 * kvd or q_norm.size != hd or k_norm.size != hd:
@@ -210,18 +212,23 @@ class Kernels:
         q = a.alloc("q", qd * 2, Class.CLIENT_DATA)
         cache = a.alloc("cache", cache_bytes, Class.CLIENT_DATA)
         pos = a.alloc("pos", 4, Class.CLIENT_DATA)
+        cs = a.alloc("rope_cs", at.max_ctx * (hd // 2) * 16, Class.CLIENT_DATA) if table else None
         self._freeze(a)
         a.write(x, 0, qkv.astype(np.uint16))
         a.write(qn, 0, q_norm.astype(np.uint16))
         a.write(kn, 0, k_norm.astype(np.uint16))
         a.write(inv, 0, inv_freq(hd, theta))
+        if table:
+            self._rope_table(a.ptr(inv), a.ptr(cs), at.max_ctx, hd)
         a.write(pt, 0, np.array(page_of, np.uint32))
         a.write(cache, 0, np.full(cache_bytes, SENTINEL, np.uint8))
         a.write(pos, 0, np.array([at.pos], np.uint32))
         k_off = at.layer * 2 * plane
         v_off = k_off + plane
-        self.gpu.launch("x0ne_qk_norm_rope_kv_write_bf16", heads.q_heads + heads.kv_heads, 64,
-                        [Arg.ptr(a.ptr(x)), Arg.ptr(a.ptr(qn)), Arg.ptr(a.ptr(kn)), Arg.ptr(a.ptr(inv)),
+        name, grid, block = (("x0ne_qk_norm_rope_kv_write_rows_bf16", (heads.q_heads + heads.kv_heads + 3) // 4, 256)
+                             if table else ("x0ne_qk_norm_rope_kv_write_bf16", heads.q_heads + heads.kv_heads, 64))
+        self.gpu.launch(name, grid, block,
+                        [Arg.ptr(a.ptr(x)), Arg.ptr(a.ptr(qn)), Arg.ptr(a.ptr(kn)), Arg.ptr(a.ptr(cs if table else inv)),
                          Arg.ptr(a.ptr(q)), Arg.ptr(a.addr(cache, k_off)), Arg.ptr(a.addr(cache, v_off)),
                          Arg.ptr(a.ptr(pt)), Arg.ptr(a.ptr(pos)), Arg.u32(heads.q_heads), Arg.u32(heads.kv_heads),
                          Arg.u32(at.max_ctx), Arg.f32(eps)])
@@ -727,7 +734,7 @@ class Kernels:
         out = a.alloc("out", rows * inter * 2, Class.CLIENT_DATA)
         self._freeze(a)
         a.write(gu, 0, gate_up.astype(np.uint16))
-        self.gpu.launch("x0ne_swiglu_bf16", ((inter + 255) // 256, rows), 256,
+        self.gpu.launch("x0ne_swiglu_bf16", ((inter + 2047) // 2048, rows), 256,
                         [Arg.ptr(a.ptr(gu)), Arg.ptr(a.ptr(out)), Arg.u32(inter)])
         self.gpu.sync()
         return a.read_array(out, 0, rows * inter, np.uint16)
