@@ -46,52 +46,65 @@ extern "C" __global__ void __launch_bounds__(128)
 
 // residual[r] += x[r] (f32, one addition per value); out[r] = bf16(residual / rms * w), the rms
 // and the product in f64 (rmsnorm.cu:5-21; oracle/src/lib.rs:50-67). grid (rows), block 256.
-// Thread t owns values t, t + 256, ..; up to NORM_HELD of them are loaded into registers at once
-// (every load in flight together, one memory round trip per row), the rest of a wider row in a
-// loop. Each thread sums its squares in that order, then the block (block_sum_d).
-constexpr uint32_t NORM_HELD = 32;  // values per thread kept in registers: hidden <= 8192 at 256
+// Thread t owns the 8-value chunks t, t + 256, .. of its row (values 8 chunk .. 8 chunk + 7); the
+// first NORM_CHUNKS of them are loaded into registers at once (every load in flight together,
+// one memory round trip per row), the rest of a wider row in a loop. Each thread sums its squares
+// chunk by chunk in that order, then the block (block_sum_d): every norm kernel of this file sums
+// in this order, so they give the same bits for the same row.
+constexpr uint32_t NORM_CHUNKS = 4;  // 8-value chunks per thread kept in registers: hidden <= 8192 at 256
 
 template <class Src, class Dst>
 __device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& src, const bf16_t* __restrict__ w,
                                             Dst&& out, uint32_t hidden, float eps) {
     __shared__ double sh[16];
     const uint32_t t = threadIdx.x, step = blockDim.x;
-    float r[NORM_HELD], wv[NORM_HELD];
+    float r[NORM_CHUNKS][8], wv[NORM_CHUNKS][8];
     double ss = 0.0;
     // Loads of a clamped index, selected after: no branch between them, so all (the row's values
     // and the norm weights) are in flight at once.
 #pragma unroll
-    for (uint32_t c = 0; c < NORM_HELD; ++c) {
-        const uint32_t i = t + c * step;
-        const uint32_t j = i < hidden ? i : 0u;
-        const float v = src(j);
-        wv[c] = bf2f(w[j]);
-        r[c] = i < hidden ? v : 0.0f;
-    }
+    for (uint32_t c = 0; c < NORM_CHUNKS; ++c)
 #pragma unroll
-    for (uint32_t c = 0; c < NORM_HELD; ++c) {
-        const uint32_t i = t + c * step;
-        if (i < hidden) {
-            residual[i] = r[c];
-            ss += (double)r[c] * (double)r[c];
+        for (uint32_t e = 0; e < 8; ++e) {
+            const uint32_t i = 8 * (t + c * step) + e;
+            const uint32_t j = i < hidden ? i : 0u;
+            const float v = src(j);
+            wv[c][e] = bf2f(w[j]);
+            r[c][e] = i < hidden ? v : 0.0f;
         }
-    }
-    for (uint32_t i = t + NORM_HELD * step; i < hidden; i += step) {  // rows wider than held
-        const float v = src(i);
-        residual[i] = v;
-        ss += (double)v * (double)v;
-    }
+#pragma unroll
+    for (uint32_t c = 0; c < NORM_CHUNKS; ++c)
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) {
+            const uint32_t i = 8 * (t + c * step) + e;
+            if (i < hidden) {
+                residual[i] = r[c][e];
+                ss += (double)r[c][e] * (double)r[c][e];
+            }
+        }
+    for (uint32_t k = t + NORM_CHUNKS * step; 8 * k < hidden; k += step)  // rows wider than held
+        for (uint32_t i = 8 * k; i < min(8 * k + 8, hidden); ++i) {
+            const float v = src(i);
+            residual[i] = v;
+            ss += (double)v * (double)v;
+        }
     const double total = block_sum_d(ss, sh);
     const double scale = 1.0 / sqrt(total / (double)hidden + (double)eps);
 #pragma unroll
-    for (uint32_t c = 0; c < NORM_HELD; ++c) {
-        const uint32_t i = t + c * step;
-        if (i < hidden) out(i) = f2bf((float)((double)r[c] * scale * (double)wv[c]));
-    }
-    for (uint32_t i = t + NORM_HELD * step; i < hidden; i += step)
-        out(i) = f2bf((float)((double)residual[i] * scale * (double)bf2f(w[i])));
+    for (uint32_t c = 0; c < NORM_CHUNKS; ++c)
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) {
+            const uint32_t i = 8 * (t + c * step) + e;
+            if (i < hidden) out(i) = f2bf((float)((double)r[c][e] * scale * (double)wv[c][e]));
+        }
+    for (uint32_t k = t + NORM_CHUNKS * step; 8 * k < hidden; k += step)
+        for (uint32_t i = 8 * k; i < min(8 * k + 8, hidden); ++i)
+            out(i) = f2bf((float)((double)residual[i] * scale * (double)bf2f(w[i])));
 }
 
+// The prefill pass's rows: rmsnorm_row's chunks and order, moved with 16-byte loads and stores
+// (residual as two float4, x, w and out as 8 bf16) where hidden is a multiple of 8 and at most
+// 8192; other widths take rmsnorm_row itself. grid (rows), block 256.
 extern "C" __global__ void __launch_bounds__(256)
     x0ne_add_rmsnorm_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
                           bf16_t* __restrict__ out, uint32_t hidden, float eps) {
@@ -99,8 +112,54 @@ extern "C" __global__ void __launch_bounds__(256)
     float* res = residual + base;
     const bf16_t* xr = x + base;
     bf16_t* o = out + base;
-    rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w, [&](uint32_t i) -> bf16_t& { return o[i]; },
-                hidden, eps);
+    if (hidden % 8 != 0 || hidden > 8 * 256 * NORM_CHUNKS || blockDim.x != 256) {  // grid-uniform
+        rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w,
+                    [&](uint32_t i) -> bf16_t& { return o[i]; }, hidden, eps);
+        return;
+    }
+    __shared__ double sh[16];
+    const uint32_t t = threadIdx.x, chunks = hidden / 8;
+    float r[NORM_CHUNKS][8];
+    uint4 wv[NORM_CHUNKS];
+#pragma unroll
+    for (uint32_t c = 0; c < NORM_CHUNKS; ++c) {
+        const uint32_t k = t + 256 * c;
+        const uint32_t j = k < chunks ? k : 0u;  // loads of a clamped chunk, selected after
+        const float4 r0 = reinterpret_cast<const float4*>(res)[2 * j], r1 = reinterpret_cast<const float4*>(res)[2 * j + 1];
+        const uint4 xv = reinterpret_cast<const uint4*>(xr)[j];
+        wv[c] = reinterpret_cast<const uint4*>(w)[j];
+        const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[c][e] = rv[e] + (e & 1 ? bf_hi(xw[e / 2]) : bf_lo(xw[e / 2]));
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (uint32_t c = 0; c < NORM_CHUNKS; ++c) {
+        const uint32_t k = t + 256 * c;
+        if (k < chunks) {
+            reinterpret_cast<float4*>(res)[2 * k] = make_float4(r[c][0], r[c][1], r[c][2], r[c][3]);
+            reinterpret_cast<float4*>(res)[2 * k + 1] = make_float4(r[c][4], r[c][5], r[c][6], r[c][7]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += (double)r[c][e] * (double)r[c][e];
+        }
+    }
+    const double total = block_sum_d(ss, sh);
+    const double scale = 1.0 / sqrt(total / (double)hidden + (double)eps);
+#pragma unroll
+    for (uint32_t c = 0; c < NORM_CHUNKS; ++c) {
+        const uint32_t k = t + 256 * c;
+        if (k >= chunks) continue;
+        const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bf16_t lo = f2bf((float)((double)r[c][2 * e] * scale * (double)bf_lo(ww[e])));
+            const bf16_t hi = f2bf((float)((double)r[c][2 * e + 1] * scale * (double)bf_hi(ww[e])));
+            ow[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        reinterpret_cast<uint4*>(o)[k] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
 }
 
 // x0ne_add_rmsnorm_bf16 with the residual read from res_in and the sum written to res_out (the
