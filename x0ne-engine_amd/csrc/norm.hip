@@ -104,7 +104,7 @@ __device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& 
 
 // The prefill pass's rows: rmsnorm_row's chunks and order, moved with 16-byte loads and stores
 // (residual as two float4, x, w and out as 8 bf16) where hidden is a multiple of 8 and at most
-// 8192; other widths take rmsnorm_row itself. grid (rows), block 256.
+// 8192 and every pointer is 16-byte aligned; otherwise rmsnorm_row itself. grid (rows), block 256.
 extern "C" __global__ void __launch_bounds__(256)
     x0ne_add_rmsnorm_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
                           bf16_t* __restrict__ out, uint32_t hidden, float eps) {
@@ -112,7 +112,8 @@ extern "C" __global__ void __launch_bounds__(256)
     float* res = residual + base;
     const bf16_t* xr = x + base;
     bf16_t* o = out + base;
-    if (hidden % 8 != 0 || hidden > 8 * 256 * NORM_CHUNKS || blockDim.x != 256) {  // grid-uniform
+    const bool aligned = (((uintptr_t)residual | (uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0;
+    if (hidden % 8 != 0 || hidden > 8 * 256 * NORM_CHUNKS || blockDim.x != 256 || !aligned) {  // grid-uniform
         rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w,
                     [&](uint32_t i) -> bf16_t& { return o[i]; }, hidden, eps);
         return;
@@ -325,8 +326,8 @@ extern "C" __global__ void __launch_bounds__(256)
 
 // SwiGLU on the packed [gate; up] row: out[i] = g / (1 + e^-g) * u, in f64 (swiglu.cu:5-11;
 // oracle/src/lib.rs:205-214). Thread t of block x takes values 8 (256 x + t) .. + 7 of row y:
-// 16-byte loads of gate and up and one 16-byte store where inter is a multiple of 8 (single
-// values otherwise). grid (ceil(inter / 2048), rows), block 256.
+// 16-byte loads of gate and up and one 16-byte store where inter is a multiple of 8 and both
+// pointers are 16-byte aligned (single values otherwise). grid (ceil(inter / 2048), rows), block 256.
 __device__ __forceinline__ bf16_t swiglu1(bf16_t g16, bf16_t u16) {
     const double g = (double)bf2f(g16), u = (double)bf2f(u16);
     return f2bf((float)(g / (1.0 + exp(-g)) * u));
@@ -337,7 +338,7 @@ extern "C" __global__ void __launch_bounds__(256)
     if (i0 >= inter) return;
     const bf16_t* row = gate_up + (size_t)r * 2 * inter;
     bf16_t* o = out + (size_t)r * inter;
-    if (inter % 8 == 0) {
+    if (inter % 8 == 0 && (((uintptr_t)gate_up | (uintptr_t)out) & 15) == 0) {  // grid-uniform
         const uint4 g = *reinterpret_cast<const uint4*>(row + i0);
         const uint4 u = *reinterpret_cast<const uint4*>(row + inter + i0);
         const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
