@@ -102,22 +102,13 @@ __device__ __forceinline__ void rmsnorm_row(float* __restrict__ residual, Src&& 
             out(i) = f2bf((float)((double)residual[i] * scale * (double)bf2f(w[i])));
 }
 
-// The prefill pass's rows: rmsnorm_row's chunks and order, moved with 16-byte loads and stores
-// (residual as two float4, x, w and out as 8 bf16) where hidden is a multiple of 8 and at most
-// 8192 and every pointer is 16-byte aligned; otherwise rmsnorm_row itself. grid (rows), block 256.
-extern "C" __global__ void __launch_bounds__(256)
-    x0ne_add_rmsnorm_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
-                          bf16_t* __restrict__ out, uint32_t hidden, float eps) {
-    const size_t base = (size_t)blockIdx.x * hidden;
-    float* res = residual + base;
-    const bf16_t* xr = x + base;
-    bf16_t* o = out + base;
-    const bool aligned = (((uintptr_t)residual | (uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0;
-    if (hidden % 8 != 0 || hidden > 8 * 256 * NORM_CHUNKS || blockDim.x != 256 || !aligned) {  // grid-uniform
-        rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w,
-                    [&](uint32_t i) -> bf16_t& { return o[i]; }, hidden, eps);
-        return;
-    }
+// rmsnorm_row's chunks, order and arithmetic with 16-byte memory operations: load(j, v) gives the
+// 8 f32 values of chunk j (residual + x), the residual is written as two float4 at res + 8 k and
+// out chunk k as 8 bf16 by store(k, value). For hidden a multiple of 8 and at most 8192, a
+// 256-thread block and 16-byte aligned rows (the callers check and fall back to rmsnorm_row).
+template <class Load, class Store>
+__device__ __forceinline__ void rmsnorm_row_vec(float* __restrict__ res, Load&& load, const bf16_t* __restrict__ w,
+                                                Store&& store, uint32_t hidden, float eps) {
     __shared__ double sh[16];
     const uint32_t t = threadIdx.x, chunks = hidden / 8;
     float r[NORM_CHUNKS][8];
@@ -126,13 +117,8 @@ extern "C" __global__ void __launch_bounds__(256)
     for (uint32_t c = 0; c < NORM_CHUNKS; ++c) {
         const uint32_t k = t + 256 * c;
         const uint32_t j = k < chunks ? k : 0u;  // loads of a clamped chunk, selected after
-        const float4 r0 = reinterpret_cast<const float4*>(res)[2 * j], r1 = reinterpret_cast<const float4*>(res)[2 * j + 1];
-        const uint4 xv = reinterpret_cast<const uint4*>(xr)[j];
+        load(j, r[c]);
         wv[c] = reinterpret_cast<const uint4*>(w)[j];
-        const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) r[c][e] = rv[e] + (e & 1 ? bf_hi(xw[e / 2]) : bf_lo(xw[e / 2]));
     }
     double ss = 0.0;
 #pragma unroll
@@ -159,8 +145,40 @@ extern "C" __global__ void __launch_bounds__(256)
             const bf16_t hi = f2bf((float)((double)r[c][2 * e + 1] * scale * (double)bf_hi(ww[e])));
             ow[e] = (uint32_t)lo | ((uint32_t)hi << 16);
         }
-        reinterpret_cast<uint4*>(o)[k] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        store(k, make_uint4(ow[0], ow[1], ow[2], ow[3]));
     }
+}
+
+__device__ __forceinline__ bool vec_norm_ok(uint32_t hidden, uintptr_t ptrs) {
+    return hidden % 8 == 0 && hidden <= 8 * 256 * NORM_CHUNKS && blockDim.x == 256 && (ptrs & 15) == 0;
+}
+
+// The 8 values of chunk j of a row: an f32 residual plus a bf16 x.
+__device__ __forceinline__ void add_chunk(const float* __restrict__ res, const bf16_t* __restrict__ x, uint32_t j,
+                                          float (&v)[8]) {
+    const float4 r0 = reinterpret_cast<const float4*>(res)[2 * j], r1 = reinterpret_cast<const float4*>(res)[2 * j + 1];
+    const uint4 xv = reinterpret_cast<const uint4*>(x)[j];
+    const float rv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = rv[e] + (e & 1 ? bf_hi(xw[e / 2]) : bf_lo(xw[e / 2]));
+}
+
+// The prefill pass's rows. grid (rows), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_add_rmsnorm_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+                          bf16_t* __restrict__ out, uint32_t hidden, float eps) {
+    const size_t base = (size_t)blockIdx.x * hidden;
+    float* res = residual + base;
+    const bf16_t* xr = x + base;
+    bf16_t* o = out + base;
+    if (!vec_norm_ok(hidden, (uintptr_t)residual | (uintptr_t)x | (uintptr_t)w | (uintptr_t)out)) {  // grid-uniform
+        rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w,
+                    [&](uint32_t i) -> bf16_t& { return o[i]; }, hidden, eps);
+        return;
+    }
+    rmsnorm_row_vec(res, [&](uint32_t j, float (&v)[8]) { add_chunk(res, xr, j, v); }, w,
+                    [&](uint32_t k, uint4 v) { reinterpret_cast<uint4*>(o)[k] = v; }, hidden, eps);
 }
 
 // x0ne_add_rmsnorm_bf16 with the residual read from res_in and the sum written to res_out (the
@@ -175,12 +193,18 @@ extern "C" __global__ void __launch_bounds__(256)
     const float* ri = res_in + base;
     const bf16_t* xr = x + base;
     bf16_t* o = out + base;
-    rmsnorm_row(res_out + base, [&](uint32_t i) { return ri[i] + bf2f(xr[i]); }, w,
-                [&](uint32_t i) -> bf16_t& { return o[i]; }, hidden, eps);
+    if (!vec_norm_ok(hidden, (uintptr_t)res_in | (uintptr_t)res_out | (uintptr_t)x | (uintptr_t)w | (uintptr_t)out)) {
+        rmsnorm_row(res_out + base, [&](uint32_t i) { return ri[i] + bf2f(xr[i]); }, w,
+                    [&](uint32_t i) -> bf16_t& { return o[i]; }, hidden, eps);
+        return;
+    }
+    rmsnorm_row_vec(res_out + base, [&](uint32_t j, float (&v)[8]) { add_chunk(ri, xr, j, v); }, w,
+                    [&](uint32_t k, uint4 v) { reinterpret_cast<uint4*>(o)[k] = v; }, hidden, eps);
 }
 
 // x0ne_add_rmsnorm_bf16 with out in panels (hidden a multiple of 8): the batched step's norms,
-// whose rows feed the few-row GEMM. The same bits at the panel positions. grid (rows), block 256.
+// whose rows feed the few-row GEMM. The same bits at the panel positions (a chunk of 8 values is
+// 8 consecutive panel elements). grid (rows), block 256.
 extern "C" __global__ void __launch_bounds__(256)
     x0ne_add_rmsnorm_panel_bf16(float* __restrict__ residual, const bf16_t* __restrict__ x,
                                 const bf16_t* __restrict__ w, bf16_t* __restrict__ out, uint32_t hidden, float eps) {
@@ -189,8 +213,14 @@ extern "C" __global__ void __launch_bounds__(256)
     float* res = residual + base;
     const bf16_t* xr = x + base;
     if (hidden % 8 != 0) return;
-    rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w,
-                [&](uint32_t i) -> bf16_t& { return out[panel_index(row, i, hidden)]; }, hidden, eps);
+    if (!vec_norm_ok(hidden, (uintptr_t)residual | (uintptr_t)x | (uintptr_t)w | (uintptr_t)out)) {
+        rmsnorm_row(res, [&](uint32_t i) { return res[i] + bf2f(xr[i]); }, w,
+                    [&](uint32_t i) -> bf16_t& { return out[panel_index(row, i, hidden)]; }, hidden, eps);
+        return;
+    }
+    rmsnorm_row_vec(res, [&](uint32_t j, float (&v)[8]) { add_chunk(res, xr, j, v); }, w,
+                    [&](uint32_t k, uint4 v) { *reinterpret_cast<uint4*>(out + panel_index(row, 8 * k, hidden)) = v; },
+                    hidden, eps);
 }
 
 // The first norm of a batched step: residual[r] = 0 + table[tokens[r]] (f32; an id >= vocab gives
@@ -207,10 +237,20 @@ extern "C" __global__ void __launch_bounds__(256)
     const uint32_t tok = tokens[blockIdx.x];
     const bf16_t* src = table + (size_t)(tok < vocab ? tok : 0) * hidden;
     const bool in = tok < vocab;
-    rmsnorm_row(residual + base, [&](uint32_t i) {
-        const float v = bf2f(src[i]);  // row 0 for an id past the table, then not used
-        return 0.0f + (in ? v : 0.0f);
-    }, w, [&](uint32_t i) -> bf16_t& { return out[panel_index(row, i, hidden)]; }, hidden, eps);
+    if (!vec_norm_ok(hidden, (uintptr_t)table | (uintptr_t)residual | (uintptr_t)w | (uintptr_t)out)) {
+        rmsnorm_row(residual + base, [&](uint32_t i) {
+            const float v = bf2f(src[i]);  // row 0 for an id past the table, then not used
+            return 0.0f + (in ? v : 0.0f);
+        }, w, [&](uint32_t i) -> bf16_t& { return out[panel_index(row, i, hidden)]; }, hidden, eps);
+        return;
+    }
+    rmsnorm_row_vec(residual + base, [&](uint32_t j, float (&v)[8]) {
+        const uint4 sv = reinterpret_cast<const uint4*>(src)[j];
+        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f + (in ? (e & 1 ? bf_hi(sw[e / 2]) : bf_lo(sw[e / 2])) : 0.0f);
+    }, w, [&](uint32_t k, uint4 v) { *reinterpret_cast<uint4*>(out + panel_index(row, 8 * k, hidden)) = v; },
+                    hidden, eps);
 }
 
 // Per-head RMSNorm of q and k, rotate-half RoPE, and the K/V write into the paged cache
