@@ -112,7 +112,7 @@ __device__ __forceinline__ double block_sum_d(double v, double* sh) {
 // ---- GEMV row sums (the decode GEMV and the O projection fused behind the decode attention) ----
 
 template <class A>
-__device__ __forceinline__ A dot8(const uint4 w, const float* x, A acc);
+__device__ __forceinline__ A dot8(const uint4 w, const A* x, A acc);
 
 template <>
 __device__ __forceinline__ float dot8<float>(const uint4 w, const float* x, float acc) {
@@ -127,17 +127,18 @@ __device__ __forceinline__ float dot8<float>(const uint4 w, const float* x, floa
     return acc;
 }
 
-// Each product of two bf16 is exact in f32; it is added in f64.
+// x already in f64. The product of two bf16 values is exact in f64, so each FMA is the exact
+// product added to the sum with one rounding, as the f64 oracle sums (w as f64 times x, added).
 template <>
-__device__ __forceinline__ double dot8<double>(const uint4 w, const float* x, double acc) {
-    acc += (double)(bf_lo(w.x) * x[0]);
-    acc += (double)(bf_hi(w.x) * x[1]);
-    acc += (double)(bf_lo(w.y) * x[2]);
-    acc += (double)(bf_hi(w.y) * x[3]);
-    acc += (double)(bf_lo(w.z) * x[4]);
-    acc += (double)(bf_hi(w.z) * x[5]);
-    acc += (double)(bf_lo(w.w) * x[6]);
-    acc += (double)(bf_hi(w.w) * x[7]);
+__device__ __forceinline__ double dot8<double>(const uint4 w, const double* x, double acc) {
+    acc = fma((double)bf_lo(w.x), x[0], acc);
+    acc = fma((double)bf_hi(w.x), x[1], acc);
+    acc = fma((double)bf_lo(w.y), x[2], acc);
+    acc = fma((double)bf_hi(w.y), x[3], acc);
+    acc = fma((double)bf_lo(w.z), x[4], acc);
+    acc = fma((double)bf_hi(w.z), x[5], acc);
+    acc = fma((double)bf_lo(w.w), x[6], acc);
+    acc = fma((double)bf_hi(w.w), x[7], acc);
     return acc;
 }
 

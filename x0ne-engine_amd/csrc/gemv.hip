@@ -298,9 +298,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
             const uint4 u = xl[ok ? c : 0];
             // A chunk past the row: its weights are zeros, and so is x (0 times a value that is
             // not finite would not be 0).
-            const float x[8] = {ok ? bf_lo(u.x) : 0.f, ok ? bf_hi(u.x) : 0.f, ok ? bf_lo(u.y) : 0.f,
-                                ok ? bf_hi(u.y) : 0.f, ok ? bf_lo(u.z) : 0.f, ok ? bf_hi(u.z) : 0.f,
-                                ok ? bf_lo(u.w) : 0.f, ok ? bf_hi(u.w) : 0.f};
+            // x in the accumulation type, converted once for the R rows.
+            const Acc x[8] = {(Acc)(ok ? bf_lo(u.x) : 0.f), (Acc)(ok ? bf_hi(u.x) : 0.f), (Acc)(ok ? bf_lo(u.y) : 0.f),
+                              (Acc)(ok ? bf_hi(u.y) : 0.f), (Acc)(ok ? bf_lo(u.z) : 0.f), (Acc)(ok ? bf_hi(u.z) : 0.f),
+                              (Acc)(ok ? bf_lo(u.w) : 0.f), (Acc)(ok ? bf_hi(u.w) : 0.f)};
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = dot8<Acc>(w[r][j], x, acc[r]);
         }
