@@ -491,17 +491,23 @@ namespace {
 // normed projections, 4 x 4 tiles at the kernel's occupancy for gate/up (both rows of a SwiGLU
 // pair in one wavefront), and whole-row 4 x 8 tiles at one block per CU for the LM head. More
 // resident wavefronts than that (more rows streamed at once) lowered the achieved bandwidth.
-template <int E>
+// Rows of at most 1024 columns (Qwen3-0.6B's hidden size: 128 chunks, two per lane) take tiles
+// of two chunks per lane and as many more rows, so a tile is the same size and every load reads
+// weights (a 4- or 8-chunk tile of a 2 KiB row would leave half or three quarters of its loads
+// past the row). Each lane sums the same chunks in the same order and the lane sums meet in the
+// same butterfly, so the sums are the same bits.
+constexpr uint32_t NARROW_COLS = 1024;
+template <int E, bool NARROW = false>
 struct Tile {
-    static constexpr int R = 2, BATCH = 4, BLOCKS_PER_CU = 1;
+    static constexpr int R = NARROW ? 4 : 2, BATCH = NARROW ? 2 : 4, BLOCKS_PER_CU = 1;
 };
-template <>
-struct Tile<EPI_SWIGLU> {
-    static constexpr int R = 4, BATCH = 4, BLOCKS_PER_CU = 0;  // 0: the occupancy
+template <bool NARROW>
+struct Tile<EPI_SWIGLU, NARROW> {
+    static constexpr int R = NARROW ? 8 : 4, BATCH = NARROW ? 2 : 4, BLOCKS_PER_CU = 0;  // 0: the occupancy
 };
-template <>
-struct Tile<EPI_ARGMAX> {
-    static constexpr int R = 4, BATCH = 8, BLOCKS_PER_CU = 1;
+template <bool NARROW>
+struct Tile<EPI_ARGMAX, NARROW> {
+    static constexpr int R = NARROW ? 16 : 4, BATCH = NARROW ? 2 : 8, BLOCKS_PER_CU = 1;
 };
 constexpr int TILE_MAP = 0;  // strided row groups, launch order
 
@@ -512,15 +518,17 @@ int x_chunks(uint32_t cols) {
     return per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
 }
 
-template <int P, int E, int XC>
+template <int P, int E, int XC, bool NARROW = false>
 const void* instance(int f64acc) {
-    constexpr int R = Tile<E>::R, B = Tile<E>::BATCH;
+    constexpr int R = Tile<E, NARROW>::R, B = Tile<E, NARROW>::BATCH;
     return f64acc ? (const void*)&gemv_kernel<R, B, P, E, double, XC, TILE_MAP>
                   : (const void*)&gemv_kernel<R, B, P, E, float, XC, TILE_MAP>;
 }
 
+// A narrow row (at most 1024 columns) always takes 2 x chunks per thread.
 template <int P, int E>
-const void* instance_x(int f64acc, int xc) {
+const void* instance_x(int f64acc, int xc, bool narrow) {
+    if (narrow) return xc == 2 ? instance<P, E, 2, true>(f64acc) : nullptr;
     if (xc == 2) return instance<P, E, 2>(f64acc);
     if (xc == 4) return instance<P, E, 4>(f64acc);
     if (xc == 8) return instance<P, E, 8>(f64acc);
@@ -532,8 +540,9 @@ const void* instance_x(int f64acc, int xc) {
 
 const void* pick(int pro, int epi, int f64acc, uint32_t cols) {
     const int xc = x_chunks(cols);
+    const bool narrow = cols <= NARROW_COLS;
 #define X0NE_CASE(P, E) \
-    if (pro == P && epi == E) return instance_x<P, E>(f64acc, xc);
+    if (pro == P && epi == E) return instance_x<P, E>(f64acc, xc, narrow);
     X0NE_CASE(PRO_X, EPI_BF16)
     X0NE_CASE(PRO_X, EPI_F32)
     X0NE_CASE(PRO_NORM, EPI_BF16)
@@ -545,18 +554,25 @@ const void* pick(int pro, int epi, int f64acc, uint32_t cols) {
     return nullptr;
 }
 
-// Rows per row group and the default blocks-per-CU cap of an epilogue's tile.
-void tile_of(int epi, uint32_t* rows, uint32_t* blocks_per_cu) {
+// Rows per row group and the default blocks-per-CU cap of an epilogue's tile at this width.
+template <bool NARROW>
+void tile_of_w(int epi, uint32_t* rows, uint32_t* blocks_per_cu) {
     if (epi == EPI_SWIGLU) {
-        *rows = Tile<EPI_SWIGLU>::R;
-        *blocks_per_cu = Tile<EPI_SWIGLU>::BLOCKS_PER_CU;
+        *rows = Tile<EPI_SWIGLU, NARROW>::R;
+        *blocks_per_cu = Tile<EPI_SWIGLU, NARROW>::BLOCKS_PER_CU;
     } else if (epi == EPI_ARGMAX) {
-        *rows = Tile<EPI_ARGMAX>::R;
-        *blocks_per_cu = Tile<EPI_ARGMAX>::BLOCKS_PER_CU;
+        *rows = Tile<EPI_ARGMAX, NARROW>::R;
+        *blocks_per_cu = Tile<EPI_ARGMAX, NARROW>::BLOCKS_PER_CU;
     } else {
-        *rows = Tile<EPI_BF16>::R;
-        *blocks_per_cu = Tile<EPI_BF16>::BLOCKS_PER_CU;
+        *rows = Tile<EPI_BF16, NARROW>::R;
+        *blocks_per_cu = Tile<EPI_BF16, NARROW>::BLOCKS_PER_CU;
     }
+}
+void tile_of(int epi, uint32_t cols, uint32_t* rows, uint32_t* blocks_per_cu) {
+    if (cols <= NARROW_COLS)
+        tile_of_w<true>(epi, rows, blocks_per_cu);
+    else
+        tile_of_w<false>(epi, rows, blocks_per_cu);
 }
 
 bool shape_ok(const X0neGemv& g) {
@@ -579,7 +595,7 @@ uint32_t x0ne_gemv_grid(const X0neGemv& g, uint32_t cus, uint32_t max_blocks_per
         per_cu <= 0)
         per_cu = 1;
     uint32_t rows = 0, cap = 0;
-    tile_of(g.epilogue, &rows, &cap);
+    tile_of(g.epilogue, g.cols, &rows, &cap);
     if (max_blocks_per_cu != 0) cap = max_blocks_per_cu;
     if (cap != 0 && (uint32_t)per_cu > cap) per_cu = (int)cap;
     const uint64_t groups = g.epilogue == EPI_SWIGLU ? ((uint64_t)g.rows / 2 + rows / 2 - 1) / (rows / 2)
