@@ -9,7 +9,8 @@ index, a NaN row gives 0xFFFFFFFF; advance). The f32-sum instances are held to t
 the f64-sum instances (the exact mode) add each exact product in f64 as the oracle does, so
 their outputs are the oracle's bits. Widths: the hidden sizes of Qwen3-0.6B/8B/32B for the norm
 prologues (1024, 4096, 5120), and also their attention and MLP widths (12288, 25600) where x is
-given."""
+given; and two rows narrower than the 0.6B's, which take the same narrow tiles (two chunks per
+lane): 8 (one chunk in all) and 520 (65 chunks, the 65th in lane 0's second slot)."""
 import numpy as np
 import pytest
 
@@ -17,8 +18,8 @@ from common import BF16_RTOL, F32_RTOL, O, bf16_bits, bf16_vals, bf16s_with_edge
 
 pytestmark = pytest.mark.gpu
 
-NORM_WIDTHS = [1024, 4096, 5120]
-X_WIDTHS = [1024, 4096, 5120, 12288, 25600]
+NORM_WIDTHS = [8, 520, 1024, 4096, 5120]
+X_WIDTHS = [8, 520, 1024, 4096, 5120, 12288, 25600]
 NO_TOKEN = 0xFFFFFFFF
 
 
