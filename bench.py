@@ -7,7 +7,10 @@ head_dim 128, intermediate 12288, vocab 151936, untied), random-init bf16 weight
 on the device from seed 0 (norm weights 1.0), a 20-token prompt of uniform random ids
 (splitmix64 seed 0), then greedy decode steps at batch 1, each step one replay of the captured
 HIP graph. A step is one decode step (one token); W untimed steps, then exactly K steps timed
-between two stream synchronisations. value = K / seconds.
+between two stream synchronisations. value = K / seconds. The timed path is the engine's default,
+the exact mode (f64 sums in the projections and attention, the oracle's rounding points, so the
+greedy tokens are the oracle's); --f32-sums times the fp32-accumulating path instead, and the
+other of the two is timed after it on the same workload (parity.other_mode).
 
 Also printed, in the same JSON line:
 - roofline: the dominant kernel (the gate/up GEMV with its fused RMSNorm and SwiGLU, 201 MB of
@@ -17,9 +20,10 @@ Also printed, in the same JSON line:
   positions) x steps / s, against 8 TB/s.
 - cpu_baseline: the CPU oracle (oracle/, a C restatement of the reference's Rust oracle, f64
   inside) on this host's cores, on a bounded sample of the same workload.
-- prefill: the prompt's time to the first token (greedy_timed's first host time: the prompt in
-  passes of up to 2048 rows through matrix-core GEMMs and the causal prefill attention, then the
-  LM head on the last row), as tok/s and TFLOP/s against the 2.5 PFLOP/s dense bf16 peak.
+- prefill: the prompt's time to the first token (greedy_timed's first host time; the f32 path
+  runs the prompt in passes of up to 2048 rows through matrix-core GEMMs and the causal prefill
+  attention, the exact mode one exact step per token; then the LM head on the last row), as
+  tok/s and TFLOP/s against the 2.5 PFLOP/s dense bf16 peak.
 
 --prompt 8192 --steps 512 is BASELINE.json config 4 (8B, 8192-token prompt, 512 decode steps);
 --model 32b --prompt 512 is config 5's batch-1 case; --model 0.6b --steps 64 config 1's.
@@ -265,7 +269,7 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
     # committed fixture for its prompt, where one exists. The exact mode has no batched step, so
     # no other mode is timed here.
     fixture = oracle_fixture(args.model, prompts[0])
-    timed = {"mode": "f64 sums (exact mode)" if args.f64_sums else "f32 sums", "tokens_equal_to_oracle": None}
+    timed = {"mode": "f64 sums (exact mode)" if e.exact() else "f32 sums", "tokens_equal_to_oracle": None}
     if fixture is not None:
         n = min(fixture["tokens"].size, tokens.shape[1])
         agree = next((i for i in range(n) if tokens[0][i] != fixture["tokens"][i]), n)
@@ -362,10 +366,12 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch each step's kernels one by one instead of replaying the captured graph "
                          "(for kernel-trace profilers; the same kernels and results)")
-    ap.add_argument("--f64-sums", action="store_true",
-                    help="time the exact mode (f64 sums in the projections and attention) instead of the f32 path")
+    ap.add_argument("--f32-sums", action="store_true",
+                    help="time the fp32-accumulating path instead of the engine's default, the exact mode "
+                         "(f64 sums in the projections and attention)")
     ap.add_argument("--no-other-mode", action="store_true",
-                    help="skip timing the other accumulation mode (f64 sums when the f32 path is timed, and back)")
+                    help="skip timing the other accumulation mode (the f32 path when the exact mode is timed, "
+                         "and back)")
     ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt tokens (config 4: 8192)")
     ap.add_argument("--model", choices=sorted(MODELS), default="8b", help="the Qwen3 shape (default 8b)")
     ap.add_argument("--batch", type=int, default=1,
@@ -404,8 +410,11 @@ def main():
     n_tokens = args.warmup + args.steps + 1
     max_ctx = args.prompt + max(n_tokens, 64) + 16  # room for the oracle fixture's 64 steps too
     t = time.perf_counter()
+    # The default options (EngineOptions { max_ctx }): the exact mode on this dense batch-1
+    # engine; --f32-sums asks for the f32 path.
     e = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=max_ctx, page_seed=1,
-                                                            f64_sums=args.f64_sums))
+                                                            f64_sums=False if args.f32_sums else None))
+    exact = e.exact()
     if args.eager:
         e.set_decode_mode(DecodeMode.EAGER)
     load_s = time.perf_counter() - t
@@ -465,11 +474,11 @@ def main():
     # this workload (64 steps), and the other accumulation mode timed and checked the same way.
     fixture = oracle_fixture(args.model, prompt)
     parity = {"oracle_fixture": fixture["path"] if fixture else None,
-              "timed_path": mode_parity(e, prompt, fixture, args.f64_sums)}
+              "timed_path": mode_parity(e, prompt, fixture, exact)}
     if not args.no_other_mode:
         e.close()
         other = Engine.load_synthetic(cfg, SEED, STD, EngineOptions(max_ctx=max_ctx, page_seed=1,
-                                                                    f64_sums=not args.f64_sums))
+                                                                    f64_sums=not exact))
         if args.eager:
             other.set_decode_mode(DecodeMode.EAGER)
         o_runs = []
@@ -477,11 +486,13 @@ def main():
             o_toks, o_secs = other.decode_timed(prompt, args.warmup, args.steps)
             o_runs.append(o_secs)
         o_secs = min(o_runs)
-        o = mode_parity(other, prompt, fixture, not args.f64_sums)
+        o = mode_parity(other, prompt, fixture, not exact)
+        compared = min(o_toks.size, tokens.size)
+        first_diff = next((i for i in range(compared) if o_toks[i] != tokens[i]), None)
         o.update({"value": round(args.steps / o_secs, 3), "unit": "tok/s", "ms_per_step": round(1e3 * o_secs / args.steps, 4),
                   "decode_hbm_frac": round(step_bytes * args.steps / o_secs / 1e9 / 8000.0, 4),
-                  "same_tokens_as_timed_path": int(next((i for i in range(min(o_toks.size, tokens.size))
-                                                         if o_toks[i] != tokens[i]), min(o_toks.size, tokens.size)))})
+                  "first_difference_from_timed_path": first_diff,
+                  "tokens_compared_with_timed_path": int(compared)})
         parity["other_mode"] = o
         other.close()
         print(f"[bench] other mode {o}", file=sys.stderr, flush=True)
@@ -517,7 +528,7 @@ def main():
         "data": "synthetic: random-init N(0,0.02) bf16 weights (seed 0), uniform random token ids (seed 0)",
         "config": {"workload": f"{model_name}-shape batch-1 greedy decode, {args.prompt}-token prompt, "
                                + ("eager launches" if args.eager else "hipGraph per step")
-                               + (", f64 GEMV sums" if args.f64_sums else ""),
+                               + (", exact mode (f64 sums)" if exact else ", f32 sums"),
                    "layers": cfg["num_hidden_layers"], "hidden": cfg["hidden_size"],
                    "heads": f"{cfg['num_attention_heads']}q/{cfg['num_key_value_heads']}kv", "head_dim": 128,
                    "intermediate": cfg["intermediate_size"], "vocab": cfg["vocab_size"],

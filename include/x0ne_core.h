@@ -173,7 +173,8 @@ x0ne_status x0ne_gpu_time_attention(x0ne_gpu* g, uint32_t q_heads, uint32_t kv_h
                                     uint32_t iters, uint64_t seed, double* us, uint32_t* planes_out);
 
 /* Graph capture (gpu.rs:1170-1238): every launch between begin and end is recorded, then
-   replayed by x0ne_gpu_launch_graph. */
+   replayed by x0ne_gpu_launch_graph on the Gpu that captured it (another Gpu is refused with
+   X0NE_ERR_GPU, gpu.rs:1225-1230). */
 typedef struct x0ne_graph x0ne_graph;
 x0ne_status x0ne_gpu_capture_begin(x0ne_gpu* g);
 x0ne_status x0ne_gpu_capture_end(x0ne_gpu* g, x0ne_graph** out);
@@ -227,11 +228,17 @@ typedef struct x0ne_greedy x0ne_greedy;
 /* EngineOptions (engine.rs:38-40), plus this build's choices:
    - page_seed: 0 keeps logical KV page i at physical page i, another seed shuffles the pages
      with a seeded permutation;
-   - f64_sums: 1 selects the exact mode: the projections add their exact bf16 products in f64,
-     and decode attention computes scores, softmax and sums in f64 with the f64 scale
-     1/sqrt(128) (one block per kv head, no split), so every rounding point of the step is the
-     f64 oracle's; 1, 2, 4 or 8 q heads per kv head (X0NE_ERR_NOT_IMPLEMENTED otherwise).
-     0, the default, is the fp32-accumulating decode path.
+   - sums: the accumulation of the projections and of decode attention.
+     X0NE_SUMS_F64 is the exact mode: the projections add their exact bf16 products in f64, and
+     decode attention computes scores, softmax and sums in f64 with the f64 scale 1/sqrt(128)
+     (split-K with f64 states merged in f64), so every rounding point of the step is the f64
+     oracle's (oracle/src/lib.rs:123-187) and the greedy tokens are the oracle's; a prompt is fed
+     one exact step per token. It serves a dense model decoding one sequence with 1, 2, 4 or 8 q
+     heads per kv head (X0NE_ERR_NOT_IMPLEMENTED otherwise).
+     X0NE_SUMS_F32 is the fp32-accumulating path (the reference engine's arithmetic: f32 sums,
+     matrix-core prefill passes).
+     X0NE_SUMS_DEFAULT (0, what EngineOptions { max_ctx } gives) is the exact mode wherever the
+     engine can serve it, else the f32 path (MoE models, max_batch > 1).
    - prefill_chunk: prompt rows per prefill pass (engine.rs:67, PREFILL_CHUNK); 0 takes
      min(2048, max_ctx). A pass runs every layer over its rows with matrix-core GEMMs and the
      causal prefill attention; the exact mode feeds a prompt one decode step per token.
@@ -239,11 +246,14 @@ typedef struct x0ne_greedy x0ne_greedy;
      single-sequence engine). Each sequence has its own max_ctx positions of KV pages (the page
      table holds max_batch runs of ceil(max_ctx / 16) pages) and its own position; the batched
      step's projections read every weight once for all sequences. 1 to 64; the f32 path only
-     (X0NE_ERR_NOT_IMPLEMENTED with f64_sums or a group size without a grouped kernel). */
+     (X0NE_ERR_NOT_IMPLEMENTED with X0NE_SUMS_F64 or a group size without a grouped kernel). */
+#define X0NE_SUMS_DEFAULT 0u
+#define X0NE_SUMS_F64 1u
+#define X0NE_SUMS_F32 2u
 typedef struct {
     uint64_t max_ctx;
     uint64_t page_seed;
-    uint32_t f64_sums;
+    uint32_t sums;
     uint32_t prefill_chunk;
     uint32_t max_batch;
     uint32_t reserved; /* 0 */
@@ -381,6 +391,9 @@ x0ne_status x0ne_engine_counts(const x0ne_engine* e, x0ne_counts* out);
 x0ne_status x0ne_engine_client_data_is_zero(const x0ne_engine* e, int* out);
 int x0ne_engine_host_buffers_are_zero(const x0ne_engine* e);
 uint64_t x0ne_engine_max_ctx(const x0ne_engine* e);
+/* The accumulation the engine runs with, X0NE_SUMS_F64 or X0NE_SUMS_F32 (the default resolved;
+   this build's, no counterpart in the reference, whose engine has the f32 path only). */
+uint32_t x0ne_engine_sums(const x0ne_engine* e);
 /* The engine's arena, for tests that read a buffer back (KV pages, residual). Not owned. */
 const x0ne_arena* x0ne_engine_arena(const x0ne_engine* e);
 /* Physical page of logical page i (this build's paged KV arena). */

@@ -351,9 +351,12 @@ void xo_embedding(const float* table, size_t vocab, size_t hidden, uint32_t toke
     memcpy(out, table + (size_t)token * hidden, hidden * sizeof(float));
 }
 
-/* lib.rs:64-67: 1 / sqrt(sum(x^2) / n + eps), the sum a sequential f64 fold. */
+/* lib.rs:64-67: 1 / sqrt(sum(x^2) / n + eps), the sum a sequential f64 fold. Every sum the
+   reference forms with Iterator::sum::<f64>() starts from -0.0, the neutral element of f64's Sum
+   in the Rust the reference pins (rust-toolchain.toml: 1.98.1), so a sum of nothing or of
+   negative zeros only is -0.0 here too; a sum it folds from an explicit 0f64 starts at +0.0. */
 double xo_rms_scale(const float* x, size_t n, float eps) {
-    double ss = 0.0;
+    double ss = -0.0;
     for (size_t i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
     return 1.0 / sqrt(ss / (double)n + (double)eps);
 }
@@ -430,7 +433,7 @@ static void gemv_rows(void* p, size_t b, size_t e) {
     size_t cols = j->cols, r = b;
     const double* x = j->x;
     for (; r + 4 <= e; r += 4) {
-        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+        double s0 = -0.0, s1 = -0.0, s2 = -0.0, s3 = -0.0; /* lib.rs:130, .sum::<f64>() */
         if (j->bf16) {
             const uint16_t* w0 = (const uint16_t*)j->w + r * cols;
             const uint16_t* w1 = w0 + cols;
@@ -460,7 +463,7 @@ static void gemv_rows(void* p, size_t b, size_t e) {
         j->y[r + 3] = (float)s3;
     }
     for (; r < e; ++r) {
-        double s = 0.0;
+        double s = -0.0;
         for (size_t c = 0; c < cols; ++c) s += wval(j, r * cols + c) * x[c];
         j->y[r] = (float)s;
     }
@@ -486,7 +489,7 @@ void xo_gemv_bf16w(const uint16_t* w, size_t rows, size_t cols, const float* x, 
 /* lib.rs:136-146 */
 void xo_gemv_magnitude(const float* w, size_t rows, size_t cols, const float* x, double* y) {
     for (size_t r = 0; r < rows; ++r) {
-        double s = 0.0;
+        double s = -0.0;
         for (size_t c = 0; c < cols; ++c) s += fabs((double)w[r * cols + c] * (double)x[c]);
         y[r] = s;
     }
@@ -500,14 +503,14 @@ static void attend(const float* q, const float* k, const float* v, size_t keys, 
     double m = -INFINITY;
     for (size_t j = 0; j < keys; ++j) {
         const float* kr = k + j * kvd + kh * hd;
-        double d = 0.0;
+        double d = -0.0; /* lib.rs:160, .sum::<f64>() */
         for (size_t i = 0; i < hd; ++i) d += (double)q[i] * (double)kr[i];
         scores[j] = d * scale;
         /* f64::max: a NaN operand gives the other one */
         if (scores[j] > m || m != m) m = (scores[j] != scores[j]) ? m : scores[j];
     }
-    double l = 0.0;
-    for (size_t i = 0; i < hd; ++i) acc[i] = 0.0;
+    double l = -0.0;                              /* lib.rs:166, .sum() */
+    for (size_t i = 0; i < hd; ++i) acc[i] = 0.0; /* lib.rs:167, vec![0f64; hd] */
     for (size_t j = 0; j < keys; ++j) {
         double p = exp(scores[j] - m);
         scores[j] = p;
@@ -569,7 +572,7 @@ void xo_moe_route(const float* logits, size_t rows, size_t experts, size_t top_k
             ri[s] = (uint32_t)best;
         }
         const double m = (double)row[ri[0]];
-        double e[64], sum = 0.0;
+        double e[64], sum = -0.0;
         for (size_t s = 0; s < top_k; ++s) {
             e[s] = exp((double)row[ri[s]] - m);
             sum += e[s];
@@ -597,7 +600,7 @@ void xo_moe_gemv(const float* w, size_t experts, size_t rows, size_t cols, const
 void xo_moe_combine(const float* y, const float* weights, size_t rows, size_t hidden, size_t top_k, float* out) {
     for (size_t r = 0; r < rows; ++r)
         for (size_t i = 0; i < hidden; ++i) {
-            double acc = 0.0;
+            double acc = -0.0;
             for (size_t s = 0; s < top_k; ++s) acc += (double)weights[r * top_k + s] * (double)y[(r * top_k + s) * hidden + i];
             out[r * hidden + i] = (float)acc;
         }
@@ -621,7 +624,7 @@ double xo_logsumexp(const float* x, size_t n) {
         if (v > m || m != m) m = (v != v) ? m : v;
     }
     if (!isfinite(m)) return m;
-    double s = 0.0;
+    double s = -0.0;
     for (size_t i = 0; i < n; ++i) s += exp((double)x[i] - m);
     return m + log(s);
 }
@@ -629,7 +632,7 @@ double xo_logsumexp(const float* x, size_t n) {
 /* lib.rs:242-252 */
 double xo_kl(const float* p, const float* q, size_t n) {
     double lp = xo_logsumexp(p, n), lq = xo_logsumexp(q, n);
-    double s = 0.0;
+    double s = -0.0;
     for (size_t i = 0; i < n; ++i) {
         double a = (double)p[i] - lp, b = (double)q[i] - lq;
         s += exp(a) * (a - b);

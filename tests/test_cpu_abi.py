@@ -75,12 +75,88 @@ def test_the_rust_crates_bindings_are_the_headers():
         assert decls[name] == n, f"{name}: {n} parameters in Rust, {decls[name]} in the header"
         assert hasattr(L, name), f"{name}: not exported"
     header = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
-    for rust, c in [("x0ne_engine_options", "x0ne_engine_options"), ("x0ne_pos_stats", "x0ne_pos_stats"),
-                    ("x0ne_counts", "x0ne_counts")]:
-        rf = re.findall(r"pub (\w+): \w+", re.search(r"pub struct %s \{(.*?)\}" % rust, text, re.S).group(1))
-        body = re.search(r"typedef struct \{([^}]*)\}\s*%s;" % c, header, re.S).group(1)
-        cf = [w for line in body.split(";") for w in re.findall(r"(\w+)\s*(?:,|$)", line.strip()) if w]
-        assert rf == cf, f"{rust}: Rust fields {rf}, header fields {cf}"
+    c_to_rust = {"uint64_t": "u64", "uint32_t": "u32", "float": "f32", "double": "f64"}
+    for name in ["x0ne_engine_options", "x0ne_pos_stats", "x0ne_counts", "x0ne_arg", "x0ne_split_plan",
+                 "x0ne_gemv_fused", "x0ne_slice"]:
+        # repr(C) with the header's fields, in order and of the same types: the same layout.
+        m = re.search(r"#\[repr\(C\)\]\s*(?:#\[derive\([^)]*\)\]\s*)?pub struct %s \{(.*?)\}" % name, text, re.S)
+        assert m, f"{name}: no repr(C) struct in sys.rs"
+        rf = re.findall(r"pub (\w+): (\w+)", m.group(1))
+        body = re.search(r"typedef struct \{([^}]*)\}\s*%s;" % name, header, re.S).group(1)
+        cf = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            ctype, names = decl.split(None, 1)
+            cf += [(n.strip(), c_to_rust[ctype]) for n in names.split(",")]
+        assert rf == cf, f"{name}: Rust fields {rf}, header fields {cf}"
+    for const, value in re.findall(r"#define (X0NE_\w+) (\d+)u?\b", header):
+        if re.search(r"pub const %s\b" % const, text):
+            assert re.search(r"pub const %s: \w+ = %s;" % (const, value), text), const
+
+
+RUST_SRC = os.path.join(ROOT, "x0ne-engine_amd", "rust", "x0ne-core-runtime-mi355x", "src")
+
+
+def test_the_rust_crate_has_the_references_kernel_launch_and_arena_api():
+    """gpu.rs and arena.rs of the drop-in crate carry the public items of x0ne-core/runtime's
+    (gpu.rs:262-314, 317-333, 958-985, 988-1008, 1031-1238, 1343-1364, 1383-1387; arena.rs:37-303)
+    with the reference's signatures, and every sys:: function they, engine.rs and lib.rs call is
+    one sys.rs declares (held to the header by the test above). The crate is not compiled here
+    (no cargo); this is the check that holds its surface to the reference's."""
+    sys_text = open(os.path.join(RUST_SRC, "sys.rs")).read()
+    declared = set(re.findall(r"pub fn (x0ne_[a-z0-9_]+)", sys_text))
+    squash = lambda t: re.sub(r"\s+", " ", t)
+    gpu = squash(open(os.path.join(RUST_SRC, "gpu.rs")).read())
+    arena = squash(open(os.path.join(RUST_SRC, "arena.rs")).read())
+    lib = open(os.path.join(RUST_SRC, "lib.rs")).read()
+    for m in ["pub mod gpu;", "pub mod arena;", "pub mod engine;", "pub mod st;"]:
+        assert m in lib, m
+    for sig in ["pub enum Arg { Ptr(u64), U32(u32), F32(f32), }",
+                "pub fn param(&self) -> Param",
+                "pub fn check_args(name: &str, params: &[Param], args: &[Arg]) -> Result<()>",
+                "pub struct SplitPlan", "pub kernel: Kernel", "pub grid_x: u32", "pub group: u32",
+                "pub grouped: bool", "pub per_sm: u32", "pub splits: u32",
+                "pub fn new() -> Result<Gpu>",
+                "pub fn split_plan(&self, q_heads: usize, kv_heads: usize) -> Result<SplitPlan>",
+                "pub fn allocate(&self, len: u64) -> Result<DeviceBacking>",
+                "pub unsafe fn launch(&self, k: Kernel, grid: (u32, u32), block: u32, args: &[Arg]) -> Result<()>",
+                "pub unsafe fn gemm(&self, w: u64, rows: usize, cols: usize, x: u64, n: usize, y: u64, out: Out) -> Result<()>",
+                "pub fn capture(&self, f: impl FnOnce() -> Result<()>) -> Result<Graph>",
+                "pub unsafe fn launch_graph(&self, g: &Graph) -> Result<()>",
+                "pub fn sync(&self) -> Result<()>", "pub fn counts(&self) -> Counts",
+                "pub fn mem_info(&self) -> Result<(u64, u64)>", "pub fn nodes(&self) -> usize",
+                "pub enum Out { Bf16, F32, }", "pub kernel_launches: u64",
+                "macro_rules! launch { ($gpu:expr, $k:expr, $grid:expr, $block:expr; $($arg:expr),* $(,)?)"]:
+        assert sig in gpu, f"gpu.rs: {sig}"
+    for sig in ["pub const ALIGN: u64", "pub enum Class { Weights, ClientData, }",
+                "pub fn offset(&self) -> u64", "pub fn len(&self) -> u64",
+                "pub struct Region { pub label: String, pub class: Class, pub offset: u64, pub len: u64, }",
+                "pub fn new() -> Self",
+                "pub fn alloc(&mut self, label: &str, len: u64, class: Class) -> Result<Slice>",
+                "pub fn planned_bytes(&self) -> u64",
+                "pub fn freeze<B: Backing>(self, allocate: impl FnOnce(u64) -> Result<B>) -> Result<Arena<Frozen<B>>>",
+                "pub fn write(&mut self, s: Slice, at: u64, data: &[u8]) -> Result<()>",
+                "pub fn read(&self, s: Slice, at: u64, out: &mut [u8]) -> Result<()>",
+                "pub fn scrub_client_data(&mut self) -> Result<u64>",
+                "pub fn addr(&self, s: Slice, at: u64) -> Result<u64>",
+                "pub fn ptr(&self, s: Slice) -> Result<u64>",
+                "pub fn span(&self, s: Slice, at: u64, len: u64) -> Result<u64>",
+                "pub fn allocate(len: u64) -> Result<Self>"]:
+        assert sig in arena, f"arena.rs: {sig}"
+    assert "ALIGN: u64 = sys::X0NE_ARENA_ALIGN" in arena
+    assert re.search(r"pub const X0NE_ARENA_ALIGN: u64 = 256;", sys_text)
+    for f in ["gpu.rs", "arena.rs", "engine.rs", "lib.rs", "error.rs", "st.rs"]:
+        used = set(re.findall(r"sys::(x0ne_[a-z0-9_]+)\s*\(", open(os.path.join(RUST_SRC, f)).read()))
+        assert used <= declared, f"{f} calls {sorted(used - declared)}, not declared in sys.rs"
+    # Every unsafe block carries its reason, as the reference's code does.
+    for f in ["gpu.rs", "arena.rs"]:
+        lines = open(os.path.join(RUST_SRC, f)).read().splitlines()
+        for i, line in enumerate(lines):
+            if re.search(r"unsafe \{", line) and "unsafe impl" not in line:
+                window = "\n".join(lines[max(0, i - 4):i + 1])
+                assert "SAFETY" in window, f"{f}:{i + 1}: an unsafe block without a SAFETY comment"
 
 
 def kernel_declarations():

@@ -64,3 +64,25 @@ def test_panel_layout_round_trips_and_places_each_element():
         for t, k in [(0, 0), (n - 1, cols - 1), (n // 2, cols // 3)]:
             assert p[(((t // 16) * (cols // 8) + k // 8) * 16 + t % 16) * 8 + k % 8] == m[t, k]
         assert (from_panels(p, n, cols) == m).all()
+
+
+def test_the_exact_attention_without_a_last_block_merge_is_refused_before_any_device_work():
+    """The exact decode attention has no f64 merge kernel behind it, so the helper refuses
+    last_block=False before it plans, allocates or launches anything: the stub device below
+    raises on any use."""
+    import pytest
+    from x0ne_core import FormatError
+    from x0ne_core.ops import Heads, Kernels
+
+    class NoDevice:
+        def __getattr__(self, name):
+            raise AssertionError(f"device touched: {name}")
+
+    h = Heads(4, 2, 128)
+    ctx = 5
+    qkv = np.zeros(h.q_dim + 2 * h.kv_dim, np.uint16)
+    kv = np.zeros((ctx - 1) * h.kv_dim, np.uint16)
+    norm = np.zeros(128, np.uint16)
+    with pytest.raises(FormatError, match="last block"):
+        Kernels(NoDevice()).attention_rope_decode(qkv, norm, norm, 1e-6, 1e6, kv, kv, ctx, h, last_block=False,
+                                                  exact=True)

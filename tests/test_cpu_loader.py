@@ -499,3 +499,42 @@ def test_read_any_tells_dense_from_moe_and_refuses_the_rest(checkpoint, moe_file
         refused(f"{key} = {value}", with_(key, value, big), moe_file)
     for bad in ["", "[]"]:
         refused(f"config {bad!r}", bad, moe_file)
+
+
+def test_the_accumulation_option_is_checked_before_the_device(checkpoint):
+    """x0ne_engine_options.sums: 0 (the default: the exact mode where the engine has its kernels,
+    else f32), 1 (f64, refused with X0NE_ERR_NOT_IMPLEMENTED where there are none: batched
+    engines), 2 (f32); any other value is a format error. All of it before any device work, so
+    without a GPU an accepted load ends in GpuError."""
+    import ctypes as C
+    from x0ne_core import FormatError, GpuError, NotImplementedFeature
+    from x0ne_core import _lib
+    from x0ne_core.engine import SUMS_DEFAULT, SUMS_F32, SUMS_F64
+    lib = _lib.lib()
+    cfg = json.dumps(dense()).encode()
+    names = (C.c_char_p * 1)(b"model.safetensors")
+    buf = C.create_string_buffer(checkpoint, len(checkpoint))
+    data = (C.c_void_p * 1)(C.addressof(buf))
+    lens = (C.c_uint64 * 1)(len(checkpoint))
+
+    def status(sums, max_batch=0):
+        opts = _lib.EngineOptionsC(64, 0, sums, 0, max_batch, 0)
+        out = C.c_void_p()
+        st = lib.x0ne_engine_load_from(cfg, 1, names, data, lens, None, C.byref(opts), C.byref(out))
+        if out.value:
+            lib.x0ne_engine_free(out)
+        return st
+    assert status(3) == _lib.ERR_FORMAT
+    assert status(0xFFFFFFFF) == _lib.ERR_FORMAT
+    assert status(SUMS_F64, max_batch=2) == _lib.ERR_NOT_IMPLEMENTED
+    for sums, batch in [(SUMS_DEFAULT, 0), (SUMS_DEFAULT, 2), (SUMS_F64, 1), (SUMS_F32, 2)]:
+        assert status(sums, batch) in (_lib.OK, _lib.ERR_GPU), (sums, batch)
+    with pytest.raises(FormatError):
+        load_opts(dense(), checkpoint, max_ctx=64, max_batch=65, f64_sums=None)
+    with pytest.raises(NotImplementedFeature):
+        load_opts(dense(), checkpoint, max_ctx=64, max_batch=2, f64_sums=True)
+    for f64 in (None, False):
+        try:
+            load_opts(dense(), checkpoint, max_ctx=64, max_batch=2, f64_sums=f64).close()
+        except GpuError:
+            pass

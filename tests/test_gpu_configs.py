@@ -94,7 +94,7 @@ def test_config4_prefill_passes_are_the_decode_route_at_full_size():
     decode route's (8192 decode steps), within the model tolerance."""
     from x0ne_core import Engine, EngineOptions, Route
     prompt = O.synthetic_ids(8192, QWEN3_8B["vocab_size"], 0)
-    e = Engine.load_synthetic(QWEN3_8B, 0, 0.02, EngineOptions(max_ctx=8192 + 16, page_seed=1))
+    e = Engine.load_synthetic(QWEN3_8B, 0, 0.02, EngineOptions(max_ctx=8192 + 16, page_seed=1, f64_sums=False))
     assert "prefill passes of 2048 rows" in e.describe()
     keep = [2047, 2048, 4095, 4096, 6144, 8191]
     pre = e.logits_at(prompt, keep, Route.PREFILL)

@@ -26,10 +26,12 @@ class Fixture:
         for name, (_, bits) in self.tensors.items():
             self.model.set(name, bits)
 
-    def engine(self, max_ctx, page_seed=7):
+    def engine(self, max_ctx, page_seed=7, f64_sums=False):
+        """The f32 path unless asked (these tests hold its kernels to the oracle's tolerances);
+        f64_sums None gives the engine's default."""
         from x0ne_core import Engine, EngineOptions
         return Engine.load_from(self.cfg.to_json(), {"model.safetensors": self.file},
-                                EngineOptions(max_ctx=max_ctx, page_seed=page_seed))
+                                EngineOptions(max_ctx=max_ctx, page_seed=page_seed, f64_sums=f64_sums))
 
     def tokens(self, seed, n):
         return O.Rng(seed).tokens(n, self.cfg.vocab)
@@ -91,7 +93,7 @@ def test_prefill_passes_across_chunk_boundaries_give_the_oracle_logits(chunk):
     from x0ne_core import Engine, EngineOptions, Route
     f = Fixture(wide(), 6)
     e = Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
-                         EngineOptions(max_ctx=96, page_seed=5, prefill_chunk=min(chunk, 96)))
+                         EngineOptions(max_ctx=96, page_seed=5, prefill_chunk=min(chunk, 96), f64_sums=False))
     c = min(chunk, 96)
     assert f"prefill passes of {c} rows" in e.describe(), e.describe()
     ids = f.tokens(14, 50)
@@ -359,6 +361,10 @@ def check_against_fixture(fx, f64, min_agree, max_ctx_extra=16):
     n = want.size
     e = Engine.load_synthetic(fx["config"], fx["seed"], fx["std"],
                               EngineOptions(max_ctx=prompt.size + n + max_ctx_extra, page_seed=1, f64_sums=f64))
+    if f64 is None:  # the default options: a dense engine of one sequence runs the exact mode
+        assert e.exact(), e.describe()
+        f64 = True
+    assert e.exact() == f64
     got = e.greedy(prompt, n)
     agree = next((i for i in range(n) if got[i] != want[i]), n)
     mode = "f64" if f64 else "f32"
@@ -400,9 +406,10 @@ def test_qwen3_8b_greedy_is_the_oracle_fixture():
     the model tolerance (0.05 of each row's own scale) at all 64 positions, an argmax that differs
     does so only where the oracle's margin is within twice that tolerance, and its own greedy
     run agrees for at least 32 steps (37 on this build; 55 of the 64 oracle margins are below
-    twice the tolerance, the first mismatch is at a 9.6e-4 margin)."""
+    twice the tolerance, the first mismatch is at a 9.6e-4 margin). The engine's default options
+    (EngineOptions { max_ctx }, what the bench times) are the exact mode: all 64."""
     fx = oracle_fixture("8b")
-    assert check_against_fixture(fx, True, 64) == 64
+    assert check_against_fixture(fx, None, 64) == 64
     check_against_fixture(fx, False, 32)
 
 
@@ -411,7 +418,7 @@ def test_qwen3_0_6b_greedy_is_the_oracle_fixture():
     embeddings) with the same synthetic weights and prompt: the exact mode gives the oracle's 64
     greedy tokens, the fp32 path its logits within the model tolerance (oracle_greedy_0_6b.json)."""
     fx = oracle_fixture("0_6b")
-    assert check_against_fixture(fx, True, 64) == 64
+    assert check_against_fixture(fx, None, 64) == 64
     check_against_fixture(fx, False, 1)
 
 
@@ -421,7 +428,7 @@ def test_a_model_directory_loads_as_its_files_in_memory(tmp_path):
     from x0ne_core import Engine, EngineOptions, Route
     f = Fixture(wide(), 9)
     ids = f.tokens(21, 12)
-    opts = EngineOptions(max_ctx=64, page_seed=3)
+    opts = EngineOptions(max_ctx=64, page_seed=3, f64_sums=False)
     e = f.engine(64, page_seed=3)
     want_tokens = e.greedy(ids, 8)
     want_logits = e.logits_at(ids, [11], Route.PREFILL)[0]
@@ -730,7 +737,21 @@ def test_the_decode_attention_kernels_agree_inside_the_engine(which):
     s = e.session(ids[:5])
     with pytest.raises(FormatError):
         e.set_decode_attention(DecodeAttention.PER_HEAD)
+    with pytest.raises(FormatError):
+        e.set_split_merge(SplitMerge.KERNEL)
+    # A refused change leaves every piece of state as it was: the getters, the description and
+    # the graph (the session still decodes with the split-K kernel's bits).
+    assert e.decode_attention() == DecodeAttention.SPLIT_K
+    assert e.split_merge() == SplitMerge.LAST_BLOCK
+    assert "merge LastBlock" in e.describe()
     s.finish()
+    # Between requests the same change is taken and captured again.
+    e.set_decode_attention(DecodeAttention.PER_HEAD)
+    assert e.decode_attention() == DecodeAttention.PER_HEAD
+    again_per_head = e.logits_at(ids, keep)
+    for a, b, p in zip(per_head, again_per_head, keep):
+        assert (a.view(np.uint32) == b.view(np.uint32)).all(), f"per-head after a refused change at {p}"
+    e.set_decode_attention(DecodeAttention.SPLIT_K)
     ex = Engine_exact(f)
     from x0ne_core import NotImplementedFeature
     with pytest.raises(NotImplementedFeature):

@@ -274,3 +274,26 @@ def test_refused_instances_and_buffers(K):
     with pytest.raises(FormatError):
         g.gemv_fused(w=16, y=16, res_in=16, delta=16, norm_w=16, rows=8, cols=64, prologue=1, epilogue=3)
     assert g.gemv_fused_blocks(w=16, y=16, x=16, rows=8, cols=64, prologue=0, epilogue=2) == 0
+
+
+@pytest.mark.parametrize("cols", [8, 520, 4096])
+def test_a_row_of_negative_zero_products_sums_to_negative_zero(K, cols):
+    """The reference's f64 sums start from -0.0 (Rust's Iterator::sum, lib.rs:123-133): a row
+    whose products are all -0.0 gives -0.0 (bf16 0x8000), a row with one +0.0 product gives +0.0,
+    as the oracle does, in both accumulations and across the chunks past a narrow row (8 and 520
+    columns pad to the tile)."""
+    x = np.full(cols, -1.0, np.float32)
+    x[1::2] = 2.0
+    w = np.zeros((6, cols), np.float32)
+    w[0, 1::2] = -0.0           # (+0)(-1) = -0 and (-0)(2) = -0: all -0
+    w[1, 1::2] = -0.0
+    w[1, 1] = 0.0               # one (+0)(2) = +0: +0
+    w[3, 0::2] = -0.0           # (-0)(-1) = +0 everywhere: +0
+    w[4, 1::2] = -0.0           # as row 0
+    w[5, :] = 0.0
+    w[5, 0] = 1.0               # a nonzero row: -1
+    want = O.gemv(w.ravel(), 6, cols, x)
+    for f64 in (False, True):
+        out = K.gemv_fused(bf16_bits(w.ravel()), 6, cols, K.PRO_X, K.EPI_BF16, f64, x=bf16_bits(x))
+        assert out["y"].tolist() == bf16_bits(want).tolist(), f"{'f64' if f64 else 'f32'} sums, {cols} columns"
+    assert bf16_bits(want)[:5].tolist() == [0x8000, 0x0000, 0x0000, 0x0000, 0x8000]

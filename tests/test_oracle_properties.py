@@ -324,3 +324,25 @@ def test_routing_ties_keep_the_smaller_index_and_signed_zeros_are_equal():
     ids, w = O.moe_route(np.array([0.0, -0.0, 1.0, 1.0, -0.0], np.float32), 5, 4)
     assert ids.tolist() == [2, 3, 0, 1]
     assert w[0] == w[1] and w[2] == w[3] and w[0] > w[2]
+
+
+def test_the_oracles_sums_start_from_negative_zero_as_rusts_sum_does():
+    """Iterator::sum::<f64>() folds from -0.0 in the Rust the reference pins (1.98.1): a GEMV row
+    whose products are all negative zeros sums to -0.0, one with a positive zero among them to
+    +0.0 (lib.rs:123-133); the same for the expert combination (lib.rs:314-329). The attention's
+    output starts from an explicit 0f64 (lib.rs:167): a V column of negative zeros gives +0.0."""
+    neg = np.float32(-0.0).view(np.uint32)
+    pos = np.float32(0.0).view(np.uint32)
+    w = np.array([0.0, -0.0, 0.0, 0.0, 0.0, 0.0], np.float32)
+    y = O.gemv(w, 3, 2, np.array([-1.0, 1.0], np.float32))
+    # rows: (+0 * -1, -0 * 1) = (-0, -0); (+0 * -1, +0 * 1) = (-0, +0); the same again
+    assert y.view(np.uint32).tolist() == [neg, pos, pos]
+    y4 = O.gemv(np.zeros(4 * 3, np.float32), 4, 3, np.array([-1.0, -2.0, -3.0], np.float32))
+    assert (y4.view(np.uint32) == neg).all(), "every row of a 4-row block"
+    c = O.moe_combine(np.array([-0.0, -0.0], np.float32), np.array([1.0, 0.5], np.float32), 1, 2)
+    assert c.view(np.uint32).tolist() == [neg]
+    q = np.ones(128, np.float32)
+    k = np.ones(2 * 128, np.float32)
+    v = np.full(2 * 128, -0.0, np.float32)
+    out = O.attention_decode(q, k, v, 2, 1, 1)
+    assert (np.asarray(out, np.float32).view(np.uint32) == pos).all()

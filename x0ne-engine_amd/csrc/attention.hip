@@ -1085,6 +1085,9 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         }
     }
     if (whole) return;
+    // Without counters (a null pointer) the states are left for the caller and no block merges:
+    // grid-uniform, so no block counts at address 0.
+    if (a.counter == nullptr) return;
     // The slices' states acknowledged, then the count; the block that completes it merges each
     // head's slices 0 .. active - 1 in that order (M = max m, f = exp(m - M), l = sum l f,
     // o = sum o f; one rounding of o / l), and sets the count back to 0 for the next step.

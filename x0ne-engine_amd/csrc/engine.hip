@@ -33,12 +33,12 @@
 
 #include "internal.h"
 #include "json.h"
+#include "ring.h"
 
 using namespace x0ne;
 
 namespace {
 
-constexpr size_t RING = 16;  // engine.rs:70
 // Prompt rows per prefill pass by default (engine.rs:67 has 512; the matrix-core GEMM's tiles are
 // 128 rows, and 2048 rows keep it compute-bound).
 constexpr uint64_t PREFILL_CHUNK = 2048;
@@ -186,6 +186,17 @@ x0ne_status parse_config(const char* json_text, Cfg* c) {
     return X0NE_OK;
 }
 
+// The accumulation an engine runs with: f64 when asked, or by default wherever this build has the
+// exact kernels (a dense model decoding one sequence, 1, 2, 4 or 8 q heads per kv head); f32
+// when asked, and by default for MoE and batched engines (check_config has refused an f64
+// request those cannot serve).
+bool exact_sums(const Cfg& c, const x0ne_engine_options& o) {
+    if (o.sums == X0NE_SUMS_F64) return true;
+    if (o.sums == X0NE_SUMS_F32) return false;
+    const uint64_t grp = c.kv_heads ? c.q_heads / c.kv_heads : 0;
+    return !c.moe && (o.max_batch == 0 || o.max_batch == 1) && (grp == 1 || grp == 2 || grp == 4 || grp == 8);
+}
+
 // What the kernels and the arena of this build accept (engine.rs:236-289 for the reference's
 // own limits), for a checked config and the load's options; all of it before any device work.
 x0ne_status check_config(const Cfg& c, const x0ne_engine_options& o) {
@@ -219,16 +230,17 @@ x0ne_status check_config(const Cfg& c, const x0ne_engine_options& o) {
     // The options.
     const uint64_t batch = o.max_batch ? o.max_batch : 1;
     if (batch > MAX_BATCH) return no("max_batch " + std::to_string(batch) + " above " + std::to_string(MAX_BATCH));
-    if (batch > 1 && o.f64_sums) return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding with f64 sums");
-    if (c.moe && (batch > 1 || o.f64_sums))
-        return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
-    if (o.f64_sums) {
+    if (o.sums > X0NE_SUMS_F32) return no("sums " + std::to_string(o.sums) + ": 0 (default), 1 (f64) or 2 (f32)");
+    if (o.sums == X0NE_SUMS_F64) {
+        if (batch > 1) return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding with f64 sums");
+        if (c.moe) return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
         const uint64_t grp = c.q_heads / c.kv_heads;
         if (grp != 1 && grp != 2 && grp != 4 && grp != 8)
             return fail(X0NE_ERR_NOT_IMPLEMENTED,
                         "f64 sums: the exact attention kernels take 1, 2, 4 or 8 q heads per kv head, not " +
                             std::to_string(grp));
     }
+    if (c.moe && batch > 1) return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
     // The attention kernels address a K or V plane (every sequence's pages of one layer) by 32-bit
     // byte offsets into a buffer resource of 0xFFFFFFF0 bytes, the offset 0xFFFFFFF0 standing for
     // "no key" (attention.hip, OFF_NONE). A plane must therefore end at or below that offset;
@@ -1050,15 +1062,15 @@ x0ne_status pull_logits(x0ne_engine* e) {
 // tokens[0] into ring word j % RING, then its event.
 x0ne_status ring_fetch(x0ne_engine* e, size_t j) {
     e->gpu->counts.dtoh++;
-    X0NE_HIP(hipMemcpyAsync(&e->ring[j % RING], e->d(e->tokens), 4, hipMemcpyDeviceToHost, e->gpu->stream),
+    X0NE_HIP(hipMemcpyAsync(&e->ring[ring_word(j)], e->d(e->tokens), 4, hipMemcpyDeviceToHost, e->gpu->stream),
              "ring copy");
-    X0NE_HIP(hipEventRecord(e->ring_ev[j % RING], e->gpu->stream), "ring event");
+    X0NE_HIP(hipEventRecord(e->ring_ev[ring_word(j)], e->gpu->stream), "ring event");
     return X0NE_OK;
 }
 
 x0ne_status ring_take(x0ne_engine* e, size_t j, uint32_t* out) {
-    X0NE_HIP(hipEventSynchronize(e->ring_ev[j % RING]), "ring wait");
-    *out = e->ring[j % RING];
+    X0NE_HIP(hipEventSynchronize(e->ring_ev[ring_word(j)]), "ring wait");
+    *out = e->ring[ring_word(j)];
     return X0NE_OK;
 }
 
@@ -1140,7 +1152,7 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     e->c = c;
     e->max_ctx = opts->max_ctx;
     e->page_seed = opts->page_seed;
-    e->f64_sums = opts->f64_sums ? 1 : 0;
+    e->f64_sums = exact_sums(c, *opts) ? 1 : 0;
     // The exact mode's sums are the decode GEMV's (f64): its prompts go one step per token.
     // A MoE engine prefills through the decode route too (engine.rs:322-328).
     e->chunk = e->f64_sums || c.moe
@@ -1655,8 +1667,7 @@ namespace {
 // The semantics of the reference's Greedy ring (engine.rs:1322-1343).
 x0ne_status greedy_fill(x0ne_greedy* g) {
     x0ne_engine* e = g->s->e;
-    const size_t taken_m1 = g->taken ? g->taken - 1 : 0;
-    while (g->launched + 1 < g->max_tokens && g->launched - taken_m1 < g->ahead) {
+    while (greedy_may_launch(g->launched, g->taken, g->max_tokens, g->ahead)) {
         const size_t j = g->launched + 1;
         x0ne_status st = run_step(e);
         if (st == X0NE_OK) st = ring_fetch(e, j);
@@ -1777,7 +1788,7 @@ x0ne_status greedy_inner(x0ne_engine* e, const uint32_t* prompt, size_t np, size
     for (size_t i = 1; i < n; ++i) {
         X0NE_TRY(run_step(e));
         X0NE_TRY(ring_fetch(e, i));
-        if (i + 1 - next >= RING - 1) {
+        if (timed_must_collect(i, next)) {
             X0NE_TRY(collect(next));
             next += 1;
         }
@@ -1953,18 +1964,18 @@ x0ne_status batch_capture(x0ne_engine* e, uint32_t B) {
 // The B token words into ring slot j % RING, then its event.
 x0ne_status batch_ring_fetch(x0ne_engine* e, size_t j, uint32_t B) {
     e->gpu->counts.dtoh++;
-    X0NE_HIP(hipMemcpyAsync(e->bring + (j % RING) * e->max_batch, e->token_of(0), B * 4, hipMemcpyDeviceToHost,
+    X0NE_HIP(hipMemcpyAsync(e->bring + ring_word(j) * e->max_batch, e->token_of(0), B * 4, hipMemcpyDeviceToHost,
                             e->gpu->stream),
              "batch ring copy");
-    X0NE_HIP(hipEventRecord(e->ring_ev[j % RING], e->gpu->stream), "ring event");
+    X0NE_HIP(hipEventRecord(e->ring_ev[ring_word(j)], e->gpu->stream), "ring event");
     return X0NE_OK;
 }
 
 // Step j's tokens out of the ring into column j of the [B][n] token rows.
 x0ne_status batch_ring_take(x0ne_engine* e, size_t j, uint32_t B, size_t n, uint32_t* out) {
-    X0NE_HIP(hipEventSynchronize(e->ring_ev[j % RING]), "ring wait");
+    X0NE_HIP(hipEventSynchronize(e->ring_ev[ring_word(j)]), "ring wait");
     for (uint32_t b = 0; b < B; ++b) {
-        const uint32_t t = e->bring[(j % RING) * e->max_batch + b];
+        const uint32_t t = e->bring[ring_word(j) * e->max_batch + b];
         if (t >= e->c.vocab) return fail(X0NE_ERR_GPU, "argmax: a logits row has no finite maximum");
         out[b * n + j] = t;
     }
@@ -2025,7 +2036,7 @@ x0ne_status batch_steps(x0ne_engine* e, uint32_t B, size_t first, size_t last, s
     for (size_t i = first; i <= last; ++i) {
         X0NE_TRY(batch_run_step(e, B));
         X0NE_TRY(batch_ring_fetch(e, i, B));
-        if (i + 1 - next >= RING - 1) {
+        if (timed_must_collect(i, next)) {
             X0NE_TRY(batch_ring_take(e, next, B, n, tokens));
             arrived(next++);
         }
@@ -2279,8 +2290,9 @@ extern "C" uint32_t x0ne_engine_decode_mode(const x0ne_engine* e) { return e ? e
 namespace {
 // A new decode attention or merge: the graph is captured again (which zeroes the client
 // buffers); a failed capture leaves no graph and eager mode (engine.rs:531-560).
+// The caller has already refused an open session (before changing any state), so the graph, the
+// getters and the eager path always use the same kernel.
 x0ne_status recapture(x0ne_engine* e) {
-    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open: change the decode attention between requests");
     x0ne_status st = capture(e);
     if (st != X0NE_OK) {
         if (e->graph) x0ne_graph_free(e->graph);
@@ -2296,6 +2308,8 @@ extern "C" x0ne_status x0ne_engine_set_decode_attention(x0ne_engine* e, uint32_t
     if (a != X0NE_ATTENTION_SPLIT_K && a != X0NE_ATTENTION_PER_HEAD) return fail(X0NE_ERR_FORMAT, "unknown decode attention");
     if (e->f64_sums && a != X0NE_ATTENTION_SPLIT_K)
         return fail(X0NE_ERR_NOT_IMPLEMENTED, "the exact mode has one decode attention kernel (f64 split-K)");
+    // A session borrows the engine (engine.rs:389-406): refused before anything changes.
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open: change the decode attention between requests");
     if (a == e->attention && e->graph) return X0NE_OK;
     e->attention = a;
     return recapture(e);
@@ -2310,6 +2324,7 @@ extern "C" x0ne_status x0ne_engine_set_split_merge(x0ne_engine* e, uint32_t m) {
         return fail(X0NE_ERR_GPU, "the last-block merge needs a grouped split-K kernel");
     if (e->f64_sums && m != X0NE_MERGE_LAST_BLOCK)
         return fail(X0NE_ERR_NOT_IMPLEMENTED, "the exact mode merges its f64 states in the last block");
+    if (e->session_open) return fail(X0NE_ERR_FORMAT, "a session is open: change the split merge between requests");
     if (m == e->merge && e->graph) return X0NE_OK;
     e->merge = m;
     return recapture(e);
@@ -2349,6 +2364,9 @@ extern "C" x0ne_status x0ne_engine_describe(const x0ne_engine* e, char* buf, siz
 extern "C" size_t x0ne_engine_graph_nodes(const x0ne_engine* e) { return e && e->graph ? e->graph->nodes : 0; }
 extern "C" uint32_t x0ne_engine_splits(const x0ne_engine* e) { return e ? e->split.splits : 0; }
 extern "C" uint64_t x0ne_engine_max_ctx(const x0ne_engine* e) { return e ? e->max_ctx : 0; }
+extern "C" uint32_t x0ne_engine_sums(const x0ne_engine* e) {
+    return e ? (e->f64_sums ? X0NE_SUMS_F64 : X0NE_SUMS_F32) : 0;
+}
 extern "C" const x0ne_arena* x0ne_engine_arena(const x0ne_engine* e) { return e ? e->arena : nullptr; }
 
 extern "C" x0ne_status x0ne_engine_counts(const x0ne_engine* e, x0ne_counts* out) {

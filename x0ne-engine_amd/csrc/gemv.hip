@@ -286,9 +286,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
     float bv = -INFINITY;
     uint32_t bi = NO_TOKEN;
     bool nan = false;
+    // Sums start from -0.0, the neutral element of the reference's f64 sums (Rust's
+    // Iterator::sum, oracle/src/lib.rs:123-133): a row whose products are all negative zeros
+    // sums to -0.0, any other as from +0.0.
     Acc acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = (Acc)0;
+    for (int r = 0; r < R; ++r) acc[r] = (Acc)-0.0f;
 
     auto consume = [&](const uint4 (&w)[R][BATCH], TilePos p) {
 #pragma unroll
@@ -296,12 +299,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
             const uint32_t c = chunk(p.b, j);
             const bool ok = c < C;
             const uint4 u = xl[ok ? c : 0];
-            // A chunk past the row: its weights are zeros, and so is x (0 times a value that is
-            // not finite would not be 0).
+            // A chunk past the row: its weights are zeros, and x is -0.0 (0 times a value that
+            // is not finite would not be 0), so each product is -0.0 and leaves a sum as it is.
             // x in the accumulation type, converted once for the R rows.
-            const Acc x[8] = {(Acc)(ok ? bf_lo(u.x) : 0.f), (Acc)(ok ? bf_hi(u.x) : 0.f), (Acc)(ok ? bf_lo(u.y) : 0.f),
-                              (Acc)(ok ? bf_hi(u.y) : 0.f), (Acc)(ok ? bf_lo(u.z) : 0.f), (Acc)(ok ? bf_hi(u.z) : 0.f),
-                              (Acc)(ok ? bf_lo(u.w) : 0.f), (Acc)(ok ? bf_hi(u.w) : 0.f)};
+            const Acc x[8] = {(Acc)(ok ? bf_lo(u.x) : -0.f), (Acc)(ok ? bf_hi(u.x) : -0.f), (Acc)(ok ? bf_lo(u.y) : -0.f),
+                              (Acc)(ok ? bf_hi(u.y) : -0.f), (Acc)(ok ? bf_lo(u.z) : -0.f), (Acc)(ok ? bf_hi(u.z) : -0.f),
+                              (Acc)(ok ? bf_lo(u.w) : -0.f), (Acc)(ok ? bf_hi(u.w) : -0.f)};
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = dot8<Acc>(w[r][j], x, acc[r]);
         }
@@ -309,7 +312,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint4* xl) {
         // The group's last batch: reduce and write.
         const Acc sum = wave_reduce_rows<R, Acc>(acc);
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = (Acc)0;
+        for (int r = 0; r < R; ++r) acc[r] = (Acc)-0.0f;
         const uint32_t k = reduced_row<R>(lane);
         const bool holder = (lane & (64 / R - 1)) == 0;  // one lane per row holds its sum
         if (EPI == EPI_SWIGLU) {

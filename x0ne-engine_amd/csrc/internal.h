@@ -61,6 +61,7 @@ struct x0ne_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     size_t nodes = 0;
+    const x0ne_gpu* owner = nullptr;  // the Gpu that captured it: launch_graph refuses any other
 };
 
 struct x0ne_arena {

@@ -873,6 +873,7 @@ extern "C" x0ne_status x0ne_gpu_capture_end(x0ne_gpu* g, x0ne_graph** out) {
     size_t nodes = 0;
     (void)hipGraphGetNodes(graph, nullptr, &nodes);
     gr->nodes = nodes;
+    gr->owner = g;
     hipError_t e = hipGraphInstantiate(&gr->exec, graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         (void)hipGraphDestroy(graph);
@@ -885,6 +886,8 @@ extern "C" x0ne_status x0ne_gpu_capture_end(x0ne_gpu* g, x0ne_graph** out) {
 
 extern "C" x0ne_status x0ne_gpu_launch_graph(x0ne_gpu* g, const x0ne_graph* graph) {
     if (!g || !graph) return fail(X0NE_ERR_GPU, "no device or graph");
+    // A graph's launches address its own Gpu's stream and memory (gpu.rs:1225-1230).
+    if (graph->owner != g) return fail(X0NE_ERR_GPU, "graph captured by another Gpu");
     g->counts.graph_launches++;
     X0NE_HIP(hipGraphLaunch(graph->exec, g->stream), "hipGraphLaunch");
     return X0NE_OK;

@@ -9,8 +9,9 @@ use crate::error::check;
 use crate::st::SliceSource;
 use crate::{sys, Error, Result};
 
-/// Prompt rows per prefill pass of this engine (the reference's is 512, engine.rs:67; 2048 rows
-/// keep the matrix-core GEMM's 128-row tiles busy on MI355X).
+/// Prompt rows per prefill pass of this engine's f32 path (the reference's is 512, engine.rs:67;
+/// a 2048-row pass gives the prefill GEMM enough output tiles to fill MI355X's 256 compute units).
+/// The exact mode, the default, feeds a prompt one exact step per token.
 pub const PREFILL_CHUNK: usize = 2048;
 /// Steps ahead of the host in a greedy session by default, and at most (engine.rs:67-79).
 pub const GREEDY_AHEAD: usize = 2;
@@ -53,7 +54,7 @@ pub struct PosStats {
     pub next_logprob: f32,
 }
 
-pub use sys::x0ne_counts as Counts;
+pub use crate::gpu::Counts;
 
 pub struct Engine {
     h: *mut sys::x0ne_engine,
@@ -231,9 +232,15 @@ impl Engine {
         unsafe { sys::x0ne_engine_max_ctx(self.h) as usize }
     }
     pub fn counts(&self) -> Counts {
-        let mut c = Counts::default();
+        let mut c = sys::x0ne_counts::default();
         let _ = unsafe { sys::x0ne_engine_counts(self.h, &mut c) };
-        c
+        c.into()
+    }
+    /// The engine runs the exact mode (f64 sums, the oracle's rounding points): what
+    /// EngineOptions { max_ctx } gives a dense model decoding one sequence. This build's; the
+    /// reference's engine has the f32 path only.
+    pub fn exact(&self) -> bool {
+        unsafe { sys::x0ne_engine_sums(self.h) == sys::X0NE_SUMS_F64 }
     }
     pub fn client_data_is_zero(&self) -> Result<bool> {
         let mut z: c_int = 0;

@@ -1,8 +1,11 @@
 //! x0ne Core's runtime API (x0ne-core/runtime, crate x0ne_core_runtime) on MI355X: the engine,
-//! its sessions and the safetensors source of the reference, over libx0ne_core.so's C ABI
-//! (include/x0ne_core.h), whose hand-written gfx950 kernels replace the CUDA cubins and cuBLAS.
+//! its sessions, the kernel-launch API (gpu), the KV arena (arena) and the safetensors source of
+//! the reference, over libx0ne_core.so's C ABI (include/x0ne_core.h), whose hand-written gfx950
+//! kernels replace the CUDA cubins and cuBLAS.
+pub mod arena;
 pub mod engine;
 mod error;
+pub mod gpu;
 pub mod st;
 pub mod sys;
 

@@ -82,7 +82,7 @@ class GemvFusedC(C.Structure):
 
 
 class EngineOptionsC(C.Structure):
-    _fields_ = [("max_ctx", C.c_uint64), ("page_seed", C.c_uint64), ("f64_sums", C.c_uint32),
+    _fields_ = [("max_ctx", C.c_uint64), ("page_seed", C.c_uint64), ("sums", C.c_uint32),
                 ("prefill_chunk", C.c_uint32), ("max_batch", C.c_uint32), ("reserved", C.c_uint32)]
 
 
@@ -175,6 +175,7 @@ SIGNATURES = {
     "x0ne_engine_client_data_is_zero": ([P, C.POINTER(I32)], ST),
     "x0ne_engine_host_buffers_are_zero": ([P], I32),
     "x0ne_engine_max_ctx": ([P], U64),
+    "x0ne_engine_sums": ([P], U32),
     "x0ne_engine_arena": ([P], P),
     "x0ne_engine_page": ([P, U64, C.POINTER(U32)], ST),
     "x0ne_engine_time_kernel": ([P, U32, U32, C.POINTER(F64), C.POINTER(F64), C.POINTER(U64)], ST),

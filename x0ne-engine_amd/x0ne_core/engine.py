@@ -42,21 +42,26 @@ class SplitMerge(IntEnum):
     LAST_BLOCK = 1
 
 
+# x0ne_engine_options.sums
+SUMS_DEFAULT, SUMS_F64, SUMS_F32 = 0, 1, 2
+
+
 @dataclass
 class EngineOptions:
     """EngineOptions (engine.rs:38-40) plus the KV page order (0: identity, else a seeded
-    shuffle), the projections' summation (f32 FMA, or each exact product added in f64), the
-    prompt rows per prefill pass (0: min(2048, max_ctx)) and the sequences the batched greedy
-    entry points serve (0 or 1: one)."""
+    shuffle), the accumulation (f64_sums True: the exact mode, each exact product added in f64;
+    False: the f32 path; None, the default: the exact mode wherever the engine can serve it,
+    else f32), the prompt rows per prefill pass (0: min(2048, max_ctx)) and the sequences the
+    batched greedy entry points serve (0 or 1: one)."""
     max_ctx: int
     page_seed: int = 0
-    f64_sums: bool = False
+    f64_sums: bool | None = None
     prefill_chunk: int = 0
     max_batch: int = 0
 
     def c(self):
-        return EngineOptionsC(self.max_ctx, self.page_seed, int(self.f64_sums), int(self.prefill_chunk),
-                              int(self.max_batch), 0)
+        sums = SUMS_DEFAULT if self.f64_sums is None else SUMS_F64 if self.f64_sums else SUMS_F32
+        return EngineOptionsC(self.max_ctx, self.page_seed, sums, int(self.prefill_chunk), int(self.max_batch), 0)
 
 
 def _ids(ids):
@@ -276,6 +281,10 @@ class Engine:
 
     def max_ctx(self) -> int:
         return lib().x0ne_engine_max_ctx(self.h)
+
+    def exact(self) -> bool:
+        """True when the engine runs the exact mode (f64 sums), the default resolved."""
+        return lib().x0ne_engine_sums(self.h) == SUMS_F64
 
     def counts(self) -> dict:
         c = Counts()

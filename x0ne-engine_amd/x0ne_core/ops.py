@@ -498,6 +498,9 @@ class Kernels:
         qd, kvd = h.q_dim, h.kv_dim
         if ctx == 0 or qkv.size != qd + 2 * kvd or k.size < (ctx - 1) * kvd or v.size < (ctx - 1) * kvd:
             raise FormatError("attention_rope_decode: lengths")
+        # The exact kernel has no f64 merge kernel behind it: refused before any device work.
+        if exact and not last_block:
+            raise FormatError("attention_rope_decode: the exact kernel merges in its last block")
         plan = self.split_plan(h)
         if not plan.grouped:
             raise FormatError(f"attention_rope_decode: no grouped kernel for group {h.q_heads // h.kv_heads}")
@@ -527,8 +530,6 @@ class Kernels:
                          Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(h.q_heads),
                          Arg.u32(h.kv_heads), Arg.u32(ctx), Arg.u32(plan.splits),
                          Arg.f32(attn_scale(hd)), Arg.f32(eps)])
-        if exact and not last_block:
-            raise FormatError("attention_rope_decode: the exact kernel merges in its last block")
         if not last_block:
             self.gpu.launch("x0ne_attention_merge_bf16", h.q_heads, 64,
                             [Arg.ptr(a.ptr(s["state"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])),
