@@ -104,10 +104,30 @@ x0ne_status x0ne_gpu_launch_3d(x0ne_gpu* g, const char* name, uint32_t gx, uint3
    X[n][cols] W^T, W [rows][cols] row-major bf16, X bf16, f32 accumulation; out_f32 = 0 gives
    bf16 Y, 1 f32 Y. Device addresses. One row of X: the bandwidth-bound GEMV; 2 to 64 rows (cols
    a multiple of 8, W and X each below 4 GiB): one few-row matrix-core launch that reads each W
-   row once (x0ne_gemm_few_*); more rows: hipBLASLt (bf16 in, f32 accumulation, one fixed
-   algorithm per shape, no workspace), as the reference hands it to cuBLAS. */
+   row once (x0ne_gemm_few_*); more rows (rows a multiple of 4, 16-byte aligned operands): this
+   library's tiled matrix-core GEMM (x0ne_gpu_gemm_tiled with the tile chosen for the shape);
+   other shapes: one GEMV per row of X. */
 x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n, uint64_t y,
                           int out_f32);
+/* The tiled matrix-core GEMM of x0ne_gpu_gemv past 64 rows with an explicit block tile (output
+   features x tokens; AUTO: the one x0ne_gpu_gemv picks) and operand layout, for kernel tests and
+   tuning; no counterpart in the reference, whose Gpu::gemm is one cuBLAS call
+   (gpu.rs:1098-1149). Y[n][rows] = X[n][cols] W^T, bf16 W and X, f32 accumulation in a fixed
+   order (the same bits from call to call), bf16 or f32 Y row-major. layout: X0NE_GEMM_W_PANELS
+   and/or X0NE_GEMM_X_PANELS for W and/or X in 16-row panels (element (r, k) at
+   ((r / 16 * cols / 8 + k / 8) * 16 + r % 16) * 8 + k % 8; X's last panel whole, the rows past n
+   any value), else row-major. rows a multiple of 4 (of 16 with W in panels), cols of 8, W and
+   X below 4 GiB, 16-byte aligned operands, else X0NE_ERR_FORMAT. It may be captured into a
+   graph. */
+enum {
+    X0NE_GEMM_TILE_AUTO = 0,
+    X0NE_GEMM_TILE_256x256 = 1,
+    X0NE_GEMM_TILE_256x128 = 2,
+    X0NE_GEMM_TILE_128x128 = 3
+};
+enum { X0NE_GEMM_W_PANELS = 1, X0NE_GEMM_X_PANELS = 2 };
+x0ne_status x0ne_gpu_gemm_tiled(x0ne_gpu* g, uint32_t tile, uint32_t layout, uint64_t w, uint64_t rows, uint64_t cols,
+                                uint64_t x, uint64_t n, uint64_t y, int out_f32);
 
 /* One launch of a fused decode GEMV instance on caller buffers: the kernels the decode step runs
    for its projections, each with its prologue and epilogue, driven alone for kernel-level

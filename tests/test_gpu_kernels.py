@@ -230,12 +230,13 @@ def test_gemv_is_the_oracle_on_random_shapes(kernels, seed):
 
 @pytest.mark.parametrize("seed", range(16))
 def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
-    """Gpu::gemm over many rows (the few-row matrix-core kernel up to 64 rows, hipBLASLt past
-    them): every row of Y is the oracle's GEMV of that row of X within the GEMV tolerance
-    (gpu_kernels.rs:331-393), at tile edges of both sides and K tails. Up to 64 rows the bf16
-    output is the f32 output rounded (one accumulation, two stores); past them the library may
-    pick different kernels for the two output types, and, as the reference does for its GEMV
-    (gpu_kernels.rs:372-377), the test only reports whether they agree."""
+    """Gpu::gemm over many rows (the few-row matrix-core kernel up to 64 rows, this library's
+    tiled matrix-core GEMM past them when W's rows are a multiple of 4, a GEMV per row of X
+    otherwise): every row of Y is the oracle's GEMV of that row of X within the GEMV tolerance
+    (gpu_kernels.rs:331-393), at tile edges of both sides and K tails. The bf16 output is the f32
+    output rounded where the same kernel serves both (one accumulation, two stores); the per-row
+    GEMV may differ between the two, and, as the reference does for its GEMV
+    (gpu_kernels.rs:372-377), the test only reports whether they agree there."""
     rng = O.Rng(700 + seed)
     n = rng.pick([2, 3, 4, 5, 16, 17, 31, 33, 64, 65, 128, 129, 257])
     rows = rng.pick([1, 15, 128, 129, 384, 1000])
@@ -253,12 +254,77 @@ def test_gemm_is_the_oracle_gemv_of_every_row(kernels, seed):
         assert_gemv(f"{what} row {r} f32", f[r], want, mag, False)
         assert_gemv(f"{what} row {r} bf16", bf16_vals(b[r]), want, mag, True)
     same = bool((b == bf16_bits(f).reshape(b.shape)).all())
-    if n <= 64:
+    if n <= 64 or rows % 4 == 0:
         assert same, what
     else:
         print(f"MEASURE {what}: bf16 out is the rounded f32 out: {same}")
     # Each shape runs the same kernels on every call: the same bits.
     assert (kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True).view(np.uint32) == f.view(np.uint32)).all(), what
+
+
+TILES = {"256x256": 1, "256x128": 2, "128x128": 3}
+W_PANELS, X_PANELS = 1, 2
+
+
+@pytest.mark.parametrize("tile", sorted(TILES))
+@pytest.mark.parametrize("seed", range(6))
+def test_the_tiled_gemm_is_the_oracle_gemv_at_every_tile(kernels, tile, seed):
+    """The prefill passes' GEMM (x0ne_gpu_gemm_tiled) at each of its block tiles, on shapes that
+    cut the tiles on every side: tokens from one to past a 256-row tile, W rows a multiple of 4
+    that end inside a tile, K tails inside a 32-column fragment (cols a multiple of 8 only) and
+    values at the bf16 edges. Every row of Y is the oracle's GEMV of that row of X within the
+    GEMV tolerance (gpu_kernels.rs:331-393), the bf16 output is the f32 output rounded (one
+    accumulation, two stores), a second call gives the same bits, and W and/or X handed over in
+    16-row panels (W rows then a multiple of 16) give the same bits as row-major: the loads fill
+    the same fragments, the products sum in the same order."""
+    rng = O.Rng(900 + 17 * seed + TILES[tile])
+    n = rng.pick([1, 2, 17, 65, 128, 129, 255, 256, 257, 300])
+    rows = rng.pick([4, 16, 60, 128, 132, 256, 260, 272, 516, 528])
+    cols = rng.pick([8, 24, 32, 40, 96, 1000])
+    scale = rng.pick([1e-2, 1.0, 50.0])
+    w = bf16s_with_edges(rng, rows * cols, scale)
+    x = bf16s_with_edges(rng, n * cols, scale)
+    t = TILES[tile]
+    f = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True, tile=t)
+    b = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, False, tile=t)
+    what = f"tiled gemm {tile} seed {seed}: {n} tokens x {rows} rows x {cols}"
+    for r in range(n):
+        xr = x[r * cols:(r + 1) * cols]
+        want = O.gemv(w, rows, cols, xr)
+        mag = O.gemv_magnitude(w, rows, cols, xr)
+        assert_gemv(f"{what} token {r} f32", f[r], want, mag, False)
+    assert (b == bf16_bits(f).reshape(b.shape)).all(), f"{what}: bf16 out is the rounded f32 out"
+    again = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True, tile=t)
+    assert (again.view(np.uint32) == f.view(np.uint32)).all(), f"{what}: the same bits twice"
+    for layout in [X_PANELS] + ([W_PANELS, W_PANELS | X_PANELS] if rows % 16 == 0 else []):
+        p = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True, tile=t, layout=layout)
+        assert (p.view(np.uint32) == f.view(np.uint32)).all(), f"{what}: layout {layout} is row-major's bits"
+        pb = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, False, tile=t, layout=layout)
+        assert (pb == b).all(), f"{what}: layout {layout} bf16"
+
+
+@pytest.mark.parametrize("name,rows,cols", [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096),
+                                            ("down", 4096, 12288)])
+def test_the_tiled_gemm_at_the_prefill_shapes(kernels, name, rows, cols):
+    """Qwen3-8B's four projections as a 2048-row prefill pass runs them, the tile the library
+    picks for each (x0ne_gpu_gemv past 64 rows), on 300 tokens (two token tiles of every
+    shape, the second cut): N(0, 0.02) weights, x of unit scale, against float64 products
+    (the oracle's GEMV arithmetic) within the GEMV tolerance; the engine's form (W and X in
+    panels, the same tile) gives the same bits."""
+    rng = np.random.default_rng(rows + cols)
+    n = 300
+    w = O.bf16_round(rng.normal(0, 0.02, rows * cols).astype(np.float32))
+    x = O.bf16_round(rng.normal(0, 1.0, n * cols).astype(np.float32))
+    f = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True)
+    W = w.reshape(rows, cols).astype(np.float64)
+    X = x.reshape(n, cols).astype(np.float64)
+    want = X @ W.T
+    mag = np.abs(X) @ np.abs(W).T
+    r = np.abs(f.astype(np.float64) - want) / (1e-5 * mag + 1e-30)
+    print(f"MEASURE tiled gemm {name} {n}x{rows}x{cols}: worst ratio {r.max():.4f}")
+    assert (r <= 1.0).all(), name
+    p = kernels.gemm(bf16_bits(w), rows, cols, bf16_bits(x), n, True, tile=0, layout=W_PANELS | X_PANELS)
+    assert (p.view(np.uint32) == f.view(np.uint32)).all(), f"{name}: panels"
 
 
 @pytest.mark.parametrize("seed", range(24))
@@ -601,6 +667,11 @@ def test_prefill_attention_is_the_oracle_whole_and_from_a_chunk_boundary(kernels
             got = kernels.attention_prefill_rows(bf16_bits(q), bf16_bits(k), bf16_bits(v), t, h, rows, grouped=grouped)
             for r, g, w in zip(rows, got, want):
                 assert_close(f"prefill {qh}/{kvh} t {t} row {r} grouped {grouped}", bf16_vals(g), w, atol, 0.0)
+        # The panel-output variant: the grouped kernel's bits at the panel positions.
+        every = list(range(t))
+        rowwise = kernels.attention_prefill_rows(bf16_bits(q), bf16_bits(k), bf16_bits(v), t, h, every, grouped=True)
+        panel = kernels.attention_prefill_rows(bf16_bits(q), bf16_bits(k), bf16_bits(v), t, h, every, panel=True)
+        assert (np.array(panel) == np.array(rowwise)).all(), f"prefill panel {qh}/{kvh} t {t}"
         for pos0 in sorted(set([0, 1, t // 2, t - 1])):
             if pos0 >= t:
                 continue
@@ -635,6 +706,12 @@ def test_swiglu_is_the_oracle(kernels, seed):
     got = bf16_vals(kernels.swiglu_rows(bf16_bits(many), rows))
     want = np.concatenate([O.swiglu(r) for r in many.reshape(rows, -1)])
     assert_close(f"swiglu rows seed {seed}", got, want, BF16_ATOL, BF16_RTOL)
+    # The panel-output variant (inter a multiple of 8): the same bits at the panel positions.
+    if inter % 8 == 0:
+        prow = rng.pick([1, 15, 17, 40])
+        gu2 = bf16s_with_edges(rng, prow * 2 * inter, scale)
+        rowwise = kernels.swiglu_rows(bf16_bits(gu2), prow)
+        assert (kernels.swiglu_rows(bf16_bits(gu2), prow, panel=True) == rowwise).all(), f"swiglu panel seed {seed}"
 
 
 def test_swiglu_special_values(kernels):

@@ -79,9 +79,7 @@ def build(jobs: int | None = None, asan: bool = False) -> str:
         objs = list(ex.map(lambda s: _compile(s, kernel_set, asan), sources()))
     lib = ASAN_LIB if asan else LIB
     tmp = lib + ".tmp"
-    # hipBLASLt takes the many-row projections (runtime.hip).
-    cmd = ([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC"] + (ASAN_FLAGS if asan else []) + ["-o", tmp] + objs +
-           ["-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib", "-lhipblaslt"])
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC"] + (ASAN_FLAGS if asan else []) + ["-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

@@ -1340,7 +1340,7 @@ struct PrefillShared {
     alignas(16) bf16_t v[2][X0NE_HEAD_DIM * PF_VS];
 };
 
-template <int G, int CG>
+template <int G, int CG, bool OUT_PANEL = false>
 __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
                                               const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
                                               bf16_t* __restrict__ out, uint32_t p0, uint32_t rows, uint32_t q_heads,
@@ -1576,9 +1576,16 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
             const float lc = __shfl(l, (int)cl, 64);
             const uint32_t rc = r0 + c / G;
             if (rc < rows) {
-                bf16_t* op = out + ((size_t)rc * q_heads + kh * G + c % G) * X0NE_HEAD_DIM;
+                const uint32_t k0 = (kh * G + c % G) * X0NE_HEAD_DIM;
+                bf16_t* op = out + (size_t)rc * q_heads * X0NE_HEAD_DIM + k0;
 #pragma unroll
-                for (int nb = 0; nb < 8; ++nb) op[16 * nb + n] = f2bf(o[cg][nb][i] / lc);
+                for (int nb = 0; nb < 8; ++nb) {
+                    const bf16_t v = f2bf(o[cg][nb][i] / lc);
+                    if (OUT_PANEL)
+                        out[panel_index(rc, k0 + 16 * nb + n, q_heads * X0NE_HEAD_DIM)] = v;
+                    else
+                        op[16 * nb + n] = v;
+                }
             }
         }
     }
@@ -1598,6 +1605,17 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
         __shared__ PrefillShared sh;                                                                               \
         prefill_block<G, PF_CG>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx, scale, \
                                 sh);                                                                               \
+    }                                                                                                              \
+    /* The same with out in 16-row panels (device.h) of q_heads 128 columns: the prefill pass's O      */          \
+    /* projection reads it so.                                                                          */          \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))                  \
+        x0ne_attention_prefill_panel_g##G##_bf16(                                                                 \
+        const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
+        const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos0,          \
+        uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale) {                       \
+        __shared__ PrefillShared sh;                                                                               \
+        prefill_block<G, PF_CG, true>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx,  \
+                                      scale, sh);                                                                  \
     }
 X0NE_PREFILL_GROUP(1)
 X0NE_PREFILL_GROUP(2)

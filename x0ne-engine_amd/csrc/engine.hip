@@ -403,7 +403,7 @@ uint64_t tensor_key(uint64_t seed, uint64_t index) {
 
 struct LayerW {
     x0ne_slice input_norm, qkv, q_norm, k_norm, o, post_norm, gate_up, down;
-    x0ne_slice qkv_p{}, o_p{}, gate_up_p{}, down_p{};  // the batched step's copies in 16-row panels
+    x0ne_slice qkv_p{}, o_p{}, gate_up_p{}, down_p{};  // copies in 16-row panels (wpanel)
     x0ne_slice router{};  // MoE: [experts][hidden]; gate_up is then [experts][2 moe_inter][hidden],
                           // down [experts][hidden][moe_inter]
 };
@@ -418,9 +418,11 @@ struct x0ne_engine {
     x0ne_arena* arena = nullptr;
     // weights
     x0ne_slice embed{}, final_norm{}, lm_head{};
-    x0ne_slice head_p{};  // the LM head (or tied embedding) in 16-row panels
+    x0ne_slice head_p{};  // the LM head (or tied embedding) in 16-row panels (hpanel)
     bool has_lm_head = false;
-    bool wpanel = false;  // the batched step reads the panel copies
+    bool wpanel = false;  // the projections' panel copies exist: the batched step reads them
+    bool ppanel = false;  // the prefill pass keeps W and X in panels (wpanel too)
+    bool hpanel = false;  // the batched LM head reads head_p
     std::vector<LayerW> L;
     // buffers
     x0ne_slice inv_freq{}, rope_cs{}, page_table{}, kv{}, prompt{}, tokens{}, pos{}, residual{}, delta{}, qkv{}, q{}, attn{},
@@ -527,11 +529,17 @@ x0ne_status plan(x0ne_engine* e) {
     X0NE_TRY(al("final_norm", c.hidden * 2, W, &e->final_norm));
     e->has_lm_head = !c.tied;
     if (e->has_lm_head) X0NE_TRY(al("lm_head", c.vocab * c.hidden * 2, W, &e->lm_head));
-    // A batched engine's second copy of the projections and the LM head in 16-row panels
-    // (gemm.hip, FEW_W_PANEL), filled from the row-major copy at load: the few-row GEMM then reads
-    // one contiguous KiB of W per step instead of 64 bytes of 16 rows.
-    e->wpanel = e->max_batch > 1 && c.qkv_rows() % 16 == 0 && c.hidden % 16 == 0 && c.inter % 16 == 0 &&
-                c.vocab % 16 == 0;
+    // A second copy of the projections in 16-row panels (device.h), filled from the row-major
+    // copy at load, for a batched engine (the few-row GEMM then reads one contiguous KiB of W per
+    // step instead of 64 bytes of 16 rows) and for a prefill pass of more than one row (the
+    // tiled GEMM's loads fetch whole 1 KiB fragments: 25 TB/s from the L2 against 9.5
+    // row-major on MI355X). The prefill pass's GEMM inputs (normed rows, attention, SwiGLU) are
+    // then written in panels too. A batched engine's LM head has a panel copy as well.
+    const bool dims16 = c.qkv_rows() % 16 == 0 && c.hidden % 16 == 0 && c.inter % 16 == 0;
+    const uint64_t group = c.q_heads / c.kv_heads;
+    e->ppanel = dims16 && e->chunk > 1 && !c.moe && (group == 1 || group == 2 || group == 4 || group == 8);
+    e->hpanel = dims16 && e->max_batch > 1 && c.vocab % 16 == 0;
+    e->wpanel = e->ppanel || (dims16 && e->max_batch > 1);
     if (e->wpanel) {
         for (uint64_t l = 0; l < c.layers; ++l) {
             LayerW& w = e->L[l];
@@ -540,8 +548,8 @@ x0ne_status plan(x0ne_engine* e) {
             X0NE_TRY(al("gate_up_panel", 2 * c.inter * c.hidden * 2, W, &w.gate_up_p));
             X0NE_TRY(al("down_panel", c.hidden * c.inter * 2, W, &w.down_p));
         }
-        X0NE_TRY(al("lm_head_panel", c.vocab * c.hidden * 2, W, &e->head_p));
     }
+    if (e->hpanel) X0NE_TRY(al("lm_head_panel", c.vocab * c.hidden * 2, W, &e->head_p));
     // Engine tables, not client data: the host's f32 inverse frequencies and the page order.
     X0NE_TRY(al("inv_freq", c.head_dim / 2 * 4, W, &e->inv_freq));
     X0NE_TRY(al("rope_cs", e->max_ctx * (c.head_dim / 2) * 16, W, &e->rope_cs));
@@ -573,15 +581,16 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("moe_act", c.top_k * c.moe_inter * 2, CD, &e->m_act));
     }
     if (e->chunk > 1) {
-        const uint64_t n = e->chunk;
+        // The GEMM inputs in panels hold whole tiles of 16 rows.
+        const uint64_t n = e->chunk, np = e->ppanel ? (n + 15) / 16 * 16 : n;
         X0NE_TRY(al("prefill_residual", n * c.hidden * 4, CD, &e->p_res));
         X0NE_TRY(al("prefill_delta", n * c.hidden * 2, CD, &e->p_delta));
-        X0NE_TRY(al("prefill_normed", n * c.hidden * 2, CD, &e->p_x));
+        X0NE_TRY(al("prefill_normed", np * c.hidden * 2, CD, &e->p_x));
         X0NE_TRY(al("prefill_qkv", n * c.qkv_rows() * 2, CD, &e->p_qkv));
         X0NE_TRY(al("prefill_q", n * c.q_dim() * 2, CD, &e->p_q));
-        X0NE_TRY(al("prefill_attn", n * c.q_dim() * 2, CD, &e->p_attn));
+        X0NE_TRY(al("prefill_attn", np * c.q_dim() * 2, CD, &e->p_attn));
         X0NE_TRY(al("prefill_gate_up", n * 2 * c.inter * 2, CD, &e->p_gu));
-        X0NE_TRY(al("prefill_act", n * c.inter * 2, CD, &e->p_act));
+        X0NE_TRY(al("prefill_act", np * c.inter * 2, CD, &e->p_act));
     }
     if (e->max_batch > 1) {
         const uint64_t b = e->max_batch, bp = (b + 15) / 16 * 16;  // panels hold whole tiles of 16 rows
@@ -903,10 +912,17 @@ x0ne_status launch_rows(x0ne_engine* e, const void* fn, dim3 grid, dim3 block, v
     return X0NE_OK;
 }
 
-// Y[n][rows] = X[n][cols] W^T on arena slices (Gpu::gemm, bf16 out).
-x0ne_status gemm(x0ne_engine* e, x0ne_slice w, uint64_t rows, uint64_t cols, x0ne_slice x, uint64_t n, x0ne_slice y) {
-    return x0ne_gpu_gemv(e->gpu, (uint64_t)(uintptr_t)e->d(w), rows, cols, (uint64_t)(uintptr_t)e->d(x), n,
-                         (uint64_t)(uintptr_t)e->d(y), 0);
+// Y[n][rows] = X[n][cols] W^T on arena slices (Gpu::gemm, bf16 out). A panel prefill pass
+// (ppanel) passes W's panel copy and X in panels: up to 64 rows the few-row GEMM, more the tiled
+// GEMM. Y is row-major either way.
+x0ne_status gemm(x0ne_engine* e, x0ne_slice w, x0ne_slice w_panels, uint64_t rows, uint64_t cols, x0ne_slice x,
+                 uint64_t n, x0ne_slice y) {
+    if (!e->ppanel)
+        return x0ne_gpu_gemv(e->gpu, (uint64_t)(uintptr_t)e->d(w), rows, cols, (uint64_t)(uintptr_t)e->d(x), n,
+                             (uint64_t)(uintptr_t)e->d(y), 0);
+    if (n <= 64) return skinny(e->gpu, e->d(w_panels), rows, cols, e->d(x), n, e->d(y), 0, PANEL_X | PANEL_W);
+    return tiled_gemm(e->gpu, 0, X0NE_GEMM_W_PANELS | X0NE_GEMM_X_PANELS, e->d(w_panels), rows, cols, e->d(x), n,
+                      e->d(y), false);
 }
 
 // Prompt rows pos0 .. pos0 + n - 1 through every layer (engine.rs:729-839 with n rows): the
@@ -914,7 +930,8 @@ x0ne_status gemm(x0ne_engine* e, x0ne_slice w, uint64_t rows, uint64_t cols, x0n
 // + RoPE with the K/V rows written at their positions, the causal attention (matrix-core kernel
 // for 1, 2, 4 or 8 q heads per kv head), the O GEMM, add + RMSNorm, the gate/up GEMM, SwiGLU,
 // the down GEMM. Leaves the rows' residual and last delta for the final norm. Sequence b: its
-// prompt row, position and KV pages.
+// prompt row, position and KV pages. With ppanel the GEMM inputs are written in panels (the same
+// values at panel_index) and the GEMMs read W's panel copies.
 x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b = 0) {
     const Cfg& c = e->c;
     if (e->chunk < 2 || n == 0 || n > e->chunk || pos0 + n > e->max_ctx || b >= e->max_batch)
@@ -938,18 +955,20 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
     auto norm = [&](x0ne_slice w) {
         const void* wp = e->d(w);
         void* args[] = {(void*)&res, (void*)&dl, (void*)&wp, (void*)&xn, (void*)&h, (void*)&eps};
-        return launch_rows(e, (const void*)&x0ne_add_rmsnorm_bf16, dim3(rows), dim3(256), args, "add_rmsnorm");
+        return launch_rows(e, e->ppanel ? (const void*)&x0ne_add_rmsnorm_panel_bf16 : (const void*)&x0ne_add_rmsnorm_bf16,
+                           dim3(rows), dim3(256), args, "add_rmsnorm");
     };
     const uint32_t group = qh / kvh;
-    const void* grouped = group == 1   ? (const void*)&x0ne_attention_prefill_g1_bf16
-                          : group == 2 ? (const void*)&x0ne_attention_prefill_g2_bf16
-                          : group == 4 ? (const void*)&x0ne_attention_prefill_g4_bf16
-                          : group == 8 ? (const void*)&x0ne_attention_prefill_g8_bf16
+    const bool pp = e->ppanel;
+    const void* grouped = group == 1   ? (pp ? (const void*)&x0ne_attention_prefill_panel_g1_bf16 : (const void*)&x0ne_attention_prefill_g1_bf16)
+                          : group == 2 ? (pp ? (const void*)&x0ne_attention_prefill_panel_g2_bf16 : (const void*)&x0ne_attention_prefill_g2_bf16)
+                          : group == 4 ? (pp ? (const void*)&x0ne_attention_prefill_panel_g4_bf16 : (const void*)&x0ne_attention_prefill_g4_bf16)
+                          : group == 8 ? (pp ? (const void*)&x0ne_attention_prefill_panel_g8_bf16 : (const void*)&x0ne_attention_prefill_g8_bf16)
                                        : nullptr;
     for (uint64_t l = 0; l < c.layers; ++l) {
         const LayerW& w = e->L[l];
         X0NE_TRY(norm(w.input_norm));
-        X0NE_TRY(gemm(e, w.qkv, c.qkv_rows(), c.hidden, e->p_x, n, e->p_qkv));
+        X0NE_TRY(gemm(e, w.qkv, w.qkv_p, c.qkv_rows(), c.hidden, e->p_x, n, e->p_qkv));
         {
             const void* qkv = e->d(e->p_qkv);
             const void* qn = e->d(w.q_norm);
@@ -982,17 +1001,17 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
                                      "prefill attention"));
             }
         }
-        X0NE_TRY(gemm(e, w.o, c.hidden, c.q_dim(), e->p_attn, n, e->p_delta));
+        X0NE_TRY(gemm(e, w.o, w.o_p, c.hidden, c.q_dim(), e->p_attn, n, e->p_delta));
         X0NE_TRY(norm(w.post_norm));
-        X0NE_TRY(gemm(e, w.gate_up, 2 * c.inter, c.hidden, e->p_x, n, e->p_gu));
+        X0NE_TRY(gemm(e, w.gate_up, w.gate_up_p, 2 * c.inter, c.hidden, e->p_x, n, e->p_gu));
         {
             const void* gu = e->d(e->p_gu);
             void* act = e->d(e->p_act);
             void* args[] = {(void*)&gu, (void*)&act, (void*)&inter};
-            X0NE_TRY(launch_rows(e, (const void*)&x0ne_swiglu_bf16, dim3((inter + 2047) / 2048, rows), dim3(256), args,
-                                 "swiglu"));
+            X0NE_TRY(launch_rows(e, pp ? (const void*)&x0ne_swiglu_panel_bf16 : (const void*)&x0ne_swiglu_bf16,
+                                 dim3((inter + 2047) / 2048, rows), dim3(256), args, "swiglu"));
         }
-        X0NE_TRY(gemm(e, w.down, c.hidden, c.inter, e->p_act, n, e->p_delta));
+        X0NE_TRY(gemm(e, w.down, w.down_p, c.hidden, c.inter, e->p_act, n, e->p_delta));
     }
     return X0NE_OK;
 }
@@ -1242,7 +1261,7 @@ x0ne_status fill_panels(x0ne_engine* e) {
         X0NE_TRY(panel(w.gate_up, w.gate_up_p, 2 * c.inter, c.hidden));
         X0NE_TRY(panel(w.down, w.down_p, c.hidden, c.inter));
     }
-    X0NE_TRY(panel(e->has_lm_head ? e->lm_head : e->embed, e->head_p, c.vocab, c.hidden));
+    if (e->hpanel) X0NE_TRY(panel(e->has_lm_head ? e->lm_head : e->embed, e->head_p, c.vocab, c.hidden));
     X0NE_HIP(hipStreamSynchronize(e->gpu->stream), "panel copies");
     return X0NE_OK;
 }
@@ -1900,9 +1919,9 @@ x0ne_status batch_down(x0ne_engine* e, uint32_t B, uint64_t l) {
 // The f32 LM head over the B normed rows, then each row's argmax into its token, position + 1.
 x0ne_status batch_head(x0ne_engine* e, uint32_t B) {
     const Cfg& c = e->c;
-    const x0ne_slice head = e->wpanel ? e->head_p : e->has_lm_head ? e->lm_head : e->embed;
+    const x0ne_slice head = e->hpanel ? e->head_p : e->has_lm_head ? e->lm_head : e->embed;
     X0NE_TRY(skinny(e->gpu, e->d(head), c.vocab, c.hidden, e->d(e->b_x), B, e->d(e->b_logits), 1,
-                    PANEL_X | wpanel_bit(e)));
+                    PANEL_X | (e->hpanel ? PANEL_W : 0u)));
     const void* lg = e->d(e->b_logits);
     uint32_t vocab = (uint32_t)c.vocab, slices = ARGMAX_SLICES;
     void* part = e->d(e->b_argmax);

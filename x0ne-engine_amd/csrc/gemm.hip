@@ -204,3 +204,297 @@ extern "C" __global__ void __launch_bounds__(256)
     const uint64_t r = j / (16 * c8) * 16 + j % 16, k8 = j / 16 % c8;
     reinterpret_cast<uint4*>(dst)[j] = reinterpret_cast<const uint4*>(src)[r * c8 + k8];
 }
+
+// ---- many rows: Y[n][rows] = X[n][cols] W^T, compute-bound, on the matrix cores ----
+// The prefill passes' projections (2048 rows of X at Qwen3 widths: 0.07-0.41 TFLOP a launch).
+// A block of NWF x NWT wavefronts computes a tile of BF = NWF WF output features (W rows) by
+// BT = NWT WT tokens (X rows); wavefront (wf, wt) holds WF x WT of it in f32 accumulators as
+// (WF / 16) x (WT / 16) products v_mfma_f32_16x16x32_bf16 with W as the A operand (16 features x
+// 32 k) and X as the B operand (16 tokens x 32 k), so each lane ends with 4 consecutive
+// features of one token and stores them as one 8-byte (bf16) or 16-byte (f32) write.
+//  - K passes in stages of 32 columns through a ring of STAGES buffers in LDS, filled by direct
+//    buffer-to-LDS loads (buffer_load_dwordx4 ... lds: no registers, no VALU) issued STAGES
+//    stages ahead. One barrier per stage.
+//  - The operands of stage s + 1 are read from LDS into a second register set while the
+//    products of stage s run, the reads interleaved with the products (one read, then
+//    products), so the matrix cores do not wait for LDS. Measured on MI355X (Qwen3-8B shapes,
+//    2048 rows): 0.4-0.47 of bf16 peak against 0.36-0.43 without the overlap.
+//  - LDS holds operand fragments in the order the products read them: a fragment is 16 rows x
+//    32 k (1 KiB), lane l's 16 bytes (row l % 16, k 8 (l / 16) .. + 7) at byte 16 l, so each
+//    ds_read_b128 reads 1 KiB contiguous in lane order (no bank conflicts).
+//  - Operands in 16-row panels (device.h: [rows / 16][cols / 8][16][8]) hold a fragment as
+//    1 KiB contiguous in exactly that order, so one load instruction fetches it whole. Row-major
+//    operands (Gpu::gemm's) give each load 16 rows x 64 bytes: measured on MI355X, a tile's
+//    loads stream from the L2 at 25 TB/s (all CUs) from panels against 9.5 TB/s row-major, so
+//    the engine's prefill passes keep W and X in panels.
+//  - A load past the matrix (a token past n, a feature past rows, k past cols) is a buffer load
+//    at an offset past the buffer: zeros, no memory touched.
+//  - Tiles in launch order go round the 8 XCDs (each with its own L2): the launch's blocks are
+//    renumbered so each XCD takes a contiguous run of tiles, and runs are ordered TILE_GROUP
+//    feature tiles wide, tokens fastest, so the blocks an XCD holds at once share their W and X
+//    pieces in its L2.
+// Each output is summed over k by one wavefront in a fixed order: bit-reproducible, and the
+// same bits whatever the operands' layout.
+namespace {
+
+constexpr int TILE_GROUP = 4;  // feature tiles side by side in one run of tiles
+constexpr uint32_t TILE_F32 = 1, TILE_W_PANEL = 2, TILE_X_PANEL = 4;
+
+template <int WF, int WT, int NWF, int NWT, int STAGES>
+struct TileCfg {
+    static constexpr int NW = NWF * NWT;
+    static constexpr int BF = NWF * WF, BT = NWT * WT;  // block tile: features x tokens
+    static constexpr int WFR = BF / 16, XFR = BT / 16;   // fragments per 32-column stage
+    static constexpr int FR = WFR + XFR;
+    static constexpr int LOADS = FR / NW;               // load instructions per wavefront per stage
+    static constexpr int BYTES = FR * 1024;             // one stage in LDS
+    static constexpr int RA = WF / 16, RB = WT / 16;    // fragments a wavefront reads per stage
+    static_assert(FR % NW == 0 && WF % 16 == 0 && WT % 16 == 0, "tile shape");
+    static_assert(STAGES >= 2 && STAGES * BYTES <= 160 * 1024, "LDS");
+};
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// A raw buffer descriptor (the 48-bit base, stride 0, `bytes` records, word 3 of
+// make_buffer_rsrc) as four scalar words, for the load below.
+__device__ __forceinline__ i32x4 rsrc_words(const void* base, uint64_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    const uint32_t n = bytes > OFF_NONE ? OFF_NONE : (uint32_t)bytes;
+    return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xFFFFu), (int)n, (int)RSRC_WORD3};
+}
+
+// One direct buffer-to-LDS load (buffer_load_dwordx4 ... lds): lane l's 16 bytes at byte offset
+// `off` of the buffer (zeros past it) land at LDS byte lds + 16 l. Written as an instruction of
+// its own so the compiler adds no wait of its own for it: the loop below counts these loads and
+// waits for them itself. M0 holds the LDS address; nothing else in these kernels uses M0.
+__device__ __forceinline__ void load_lds16(const i32x4& r, uint32_t lds, uint32_t off) {
+    // The descriptor and the LDS address are wavefront-uniform; read from lane 0 so they are
+    // scalar registers whatever the compiler concluded.
+    const i32x4 u = {__builtin_amdgcn_readfirstlane(r[0]), __builtin_amdgcn_readfirstlane(r[1]),
+                     __builtin_amdgcn_readfirstlane(r[2]), __builtin_amdgcn_readfirstlane(r[3])};
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off),
+                 "s"(__builtin_amdgcn_readfirstlane(lds)), "s"(u)
+                 : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+    return __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(p));
+}
+
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt at their maxima) through the compiler's builtin, so its
+// own wait bookkeeping knows the LDS reads are done.
+constexpr int WAIT_LGKM0 = 0xC07F;
+
+template <int WF, int WT, int NWF, int NWT, int STAGES>
+__device__ __forceinline__ void gemm_tiles(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
+                                           void* __restrict__ y, uint32_t rows, uint32_t cols, uint32_t n,
+                                           uint32_t flags, uint8_t* lds) {
+    using C = TileCfg<WF, WT, NWF, NWT, STAGES>;
+    const uint32_t tiles_f = (rows + C::BF - 1) / C::BF, tiles_t = (n + C::BT - 1) / C::BT;
+    const uint32_t tiles = tiles_f * tiles_t;
+    // Launch id -> tile: ids alternate over the 8 XCDs, so id b runs on XCD b % 8; the XCD's
+    // ids b % 8, b % 8 + 8, .. take the run of tiles (b % 8) (tiles / 8) + b / 8.
+    const uint32_t b = blockIdx.x;
+    const uint32_t seq = tiles % 8 == 0 ? (b & 7) * (tiles >> 3) + (b >> 3) : b;
+    const uint32_t group = seq / (TILE_GROUP * tiles_t), in_group = seq % (TILE_GROUP * tiles_t);
+    const uint32_t width = min((uint32_t)TILE_GROUP, tiles_f - group * TILE_GROUP);
+    const uint32_t f0 = (group * TILE_GROUP + in_group % width) * C::BF, t0 = in_group / width * C::BT;
+
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wf = wave % NWF, wt = wave / NWF;
+    const bool w_panel = flags & TILE_W_PANEL, x_panel = flags & TILE_X_PANEL;
+    // Panels hold whole groups of 16 rows.
+    const i32x4 wr = rsrc_words(w, (uint64_t)(w_panel ? (rows + 15) / 16 * 16 : rows) * cols * 2);
+    const i32x4 xr = rsrc_words(x, (uint64_t)(x_panel ? (n + 15) / 16 * 16 : n) * cols * 2);
+    const uint32_t stages = (cols + 31) / 32, c8 = cols / 8;
+
+    // This wavefront's loads of a stage: fragment f = wave + NW q (W fragments first), lane l
+    // fetching row 16 g + l % 16, columns 32 s + 8 (l / 16) .. + 7 of its operand: byte
+    // base[q] + step[q] s of the buffer while those columns exist and the row (panel: its group
+    // of 16) does.
+    uint32_t base[C::LOADS], step[C::LOADS];
+    bool row_in[C::LOADS];
+#pragma unroll
+    for (int q = 0; q < C::LOADS; ++q) {
+        const int f = (int)wave + C::NW * q;
+        const bool is_w = f < C::WFR;
+        const uint32_t g16 = ((is_w ? f0 : t0) >> 4) + (uint32_t)(is_w ? f : f - C::WFR);
+        const uint32_t row = 16 * g16 + (lane & 15);
+        const bool panel = is_w ? w_panel : x_panel;
+        row_in[q] = (panel ? 16 * g16 : row) < (is_w ? rows : n);
+        base[q] = panel ? g16 * c8 * 256 + lane * 16 : row * cols * 2 + (lane >> 4) * 16;
+        step[q] = panel ? 1024 : 64;
+    }
+    auto issue = [&](uint32_t s) {
+        uint8_t* dst = lds + (s % STAGES) * C::BYTES;
+#pragma unroll
+        for (int q = 0; q < C::LOADS; ++q) {
+            const int f = (int)wave + C::NW * q;
+            const bool in = row_in[q] && 4 * s + (lane >> 4) < c8;
+            load_lds16(f < C::WFR ? wr : xr, lds_addr(dst + f * 1024), in ? base[q] + step[q] * s : OFF_NONE);
+        }
+    };
+
+    f32x4 acc[C::RA][C::RB];
+#pragma unroll
+    for (int i = 0; i < C::RA; ++i)
+#pragma unroll
+        for (int j = 0; j < C::RB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 a0[C::RA], b0[C::RB], a1[C::RA], b1[C::RB];
+    auto read = [&](uint32_t s, uint4 (&a)[C::RA], uint4 (&bx)[C::RB]) {
+        const uint8_t* src = lds + (s % STAGES) * C::BYTES;
+#pragma unroll
+        for (int i = 0; i < C::RA; ++i)
+            a[i] = *reinterpret_cast<const uint4*>(src + (wf * C::RA + i) * 1024 + lane * 16);
+#pragma unroll
+        for (int j = 0; j < C::RB; ++j)
+            bx[j] = *reinterpret_cast<const uint4*>(src + (C::WFR + wt * C::RB + j) * 1024 + lane * 16);
+    };
+    // The products of one stage, with the reads issued just before them interleaved: one LDS
+    // read, then its share of the products.
+    auto compute = [&](const uint4 (&a)[C::RA], const uint4 (&bx)[C::RB]) {
+#pragma unroll
+        for (int i = 0; i < C::RA; ++i)
+#pragma unroll
+            for (int j = 0; j < C::RB; ++j) acc[i][j] = mfma(a[i], bx[j], acc[i][j]);
+        constexpr int R = C::RA + C::RB, M = C::RA * C::RB;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // one LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, M / R, 0);  // then products
+        }
+        if (M % R) __builtin_amdgcn_sched_group_barrier(0x008, M % R, 0);
+    };
+
+    // Prologue: stages 0 .. STAGES - 1 in flight, stage 0 complete (this wavefront's loads: at
+    // most the later stages' in flight; then the barrier: every wavefront's), its operands read.
+#pragma unroll
+    for (int p = 0; p < STAGES; ++p)
+        if ((uint32_t)p < stages) issue(p);
+    if (stages >= (uint32_t)STAGES) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::LOADS * (STAGES - 1)) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_barrier" ::: "memory");
+    read(0, a0, b0);
+    // Stage s: stage s + 1 complete in this wavefront (at most min(stages - s - 2, STAGES - 2)
+    // later stages' loads in flight) and its own reads of stage s done; the barrier: the same in
+    // every wavefront, so stage s's slot is no longer read and takes stage s + STAGES. Then the
+    // products of stage s run while stage s + 1's operands are read (at the last stage, stage s's
+    // again: a harmless read that keeps the reads unconditional). Stages go in pairs so each
+    // stage's register set is fixed at compile time.
+    for (uint32_t s2 = 0; s2 < stages; s2 += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t s = s2 + h;
+            if (s >= stages) break;
+            if (s + 1 < stages) {
+                if (stages - s - 2 >= (uint32_t)(STAGES - 2)) {
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::LOADS * (STAGES - 2)) : "memory");
+                } else {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+            asm volatile("s_barrier" ::: "memory");
+            if (s + STAGES < stages) issue(s + STAGES);
+            const uint32_t next = s + 1 < stages ? s + 1 : s;
+            if (h == 0) {
+                read(next, a1, b1);
+                compute(a0, b0);
+            } else {
+                read(next, a0, b0);
+                compute(a1, b1);
+            }
+        }
+    }
+
+    // acc[i][j][r]: feature f0 + WF wf + 16 i + 4 (lane / 16) + r, token t0 + WT wt + 16 j + lane % 16.
+    const bool out_f32 = flags & TILE_F32;
+#pragma unroll
+    for (int j = 0; j < C::RB; ++j) {
+        const uint32_t t = t0 + WT * wt + 16 * j + (lane & 15);
+        if (t >= n) continue;
+#pragma unroll
+        for (int i = 0; i < C::RA; ++i) {
+            const uint32_t f = f0 + WF * wf + 16 * i + 4 * (lane >> 4);
+            if (f >= rows) continue;
+            const f32x4 v = acc[i][j];
+            const size_t o = (size_t)t * rows + f;
+            if (out_f32) {
+                *reinterpret_cast<f32x4*>(static_cast<float*>(y) + o) = v;
+            } else {
+                const uint32_t lo = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+                const uint32_t hi = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+                *reinterpret_cast<uint2*>(static_cast<bf16_t*>(y) + o) = make_uint2(lo, hi);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+// Tiled GEMM kernels: grid ceil(rows / BF) ceil(n / BT), block 64 NWF NWT; rows a multiple of 4,
+// cols of 8 (and rows of 16 with W in panels), W and X below 4 GiB - 16 bytes, Y 8-byte (bf16)
+// or 16-byte (f32) aligned; flags TILE_F32 | TILE_W_PANEL | TILE_X_PANEL.
+#define X0NE_TILES(NAME, WF, WT, NWF, NWT, STAGES)                                                             \
+    extern "C" __global__ void __launch_bounds__(64 * NWF * NWT)                                                  \
+        NAME(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, uint32_t rows,     \
+             uint32_t cols, uint32_t n, uint32_t flags) {                                                         \
+        __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * TileCfg<WF, WT, NWF, NWT, STAGES>::BYTES]; \
+        if (rows % 4 != 0 || cols % 8 != 0 || n == 0 || ((flags & TILE_W_PANEL) && rows % 16 != 0)) return;     \
+        gemm_tiles<WF, WT, NWF, NWT, STAGES>(w, x, y, rows, cols, n, flags, lds);                                 \
+    }
+// Block tiles, all of four stages, from sweeps on MI355X over the Qwen3-8B prefill shapes at 2048
+// rows, operands in panels: 256 x 256 of 8 wavefronts (64 features x 128 tokens each; two per
+// SIMD), 256 x 128 of 8 (64 x 64 each), and 128 x 128 of 4 (64 x 64 each; two blocks per CU).
+X0NE_TILES(x0ne_gemm_tiles_256x256_bf16, 64, 128, 4, 2, 4)
+X0NE_TILES(x0ne_gemm_tiles_256x128_bf16, 64, 64, 4, 2, 4)
+X0NE_TILES(x0ne_gemm_tiles_128x128_bf16, 64, 64, 2, 2, 4)
+
+// ---- typed launchers of the tiled GEMM (called by the runtime) ----
+
+#include "launch.h"
+
+namespace {
+
+struct TileKind {
+    const void* fn;
+    uint32_t bf, bt;    // block tile: features x tokens
+    uint32_t threads;
+};
+
+TileKind tile_kind(int tile) {
+    switch (tile) {
+        case X0NE_TILE_256x256: return {(const void*)&x0ne_gemm_tiles_256x256_bf16, 256, 256, 512};
+        case X0NE_TILE_256x128: return {(const void*)&x0ne_gemm_tiles_256x128_bf16, 256, 128, 512};
+        case X0NE_TILE_128x128: return {(const void*)&x0ne_gemm_tiles_128x128_bf16, 128, 128, 256};
+        default: return {nullptr, 0, 0, 0};
+    }
+}
+
+}  // namespace
+
+// The tile for a shape, from the MI355X sweeps at 2048 rows of X (operands in panels): the
+// 256 x 256 tile while it gives at least 0.7 of a tile per CU (gate/up 24576 rows: 335-360 us;
+// QKV 6144 rows: 98-106 us against 125 for 256 x 128), else 256 x 128 while that does (O and down,
+// 4096 rows: 68 and 186 us against 99 and 278 for 256 x 256), else 128 x 128.
+int x0ne_gemm_tile_pick(uint32_t rows, uint32_t cols, uint32_t n, uint32_t cus) {
+    auto tiles = [&](uint32_t bf, uint32_t bt) { return (uint64_t)((rows + bf - 1) / bf) * ((n + bt - 1) / bt); };
+    if (10 * tiles(256, 256) >= 7ull * cus) return X0NE_TILE_256x256;
+    if (10 * tiles(256, 128) >= 7ull * cus) return X0NE_TILE_256x128;
+    return X0NE_TILE_128x128;
+}
+
+hipError_t x0ne_launch_gemm_tiles(int tile, const void* w, const void* x, void* y, uint32_t rows, uint32_t cols,
+                                  uint32_t n, uint32_t flags, hipStream_t s) {
+    const TileKind k = tile_kind(tile);
+    if (!k.fn || rows % 4 != 0 || cols % 8 != 0 || n == 0 || flags > 7 || ((flags & TILE_W_PANEL) && rows % 16 != 0))
+        return hipErrorInvalidValue;
+    const uint64_t blocks = (uint64_t)((rows + k.bf - 1) / k.bf) * ((n + k.bt - 1) / k.bt);
+    if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    void* args[] = {(void*)&w, (void*)&x, (void*)&y, (void*)&rows, (void*)&cols, (void*)&n, (void*)&flags};
+    return x0ne_launch(k.fn, dim3((uint32_t)blocks), dim3(k.threads), args, 0, s);
+}

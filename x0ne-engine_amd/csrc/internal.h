@@ -38,7 +38,6 @@ struct Counts {
     } while (0)
 
 namespace x0ne {
-struct LibGemm;  // the library GEMM's handle and per-shape plans (runtime.hip)
 }
 
 struct x0ne_gpu {
@@ -54,7 +53,6 @@ struct x0ne_gpu {
     // hipGetSymbolAddress gave it at x0ne_gpu_new with the device current.
     void* scratch = nullptr;
     // hipBLASLt for the many-row projections, opened at the first one.
-    x0ne::LibGemm* lib_gemm = nullptr;
 };
 
 struct x0ne_graph {
@@ -93,6 +91,10 @@ x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32
 constexpr uint32_t PANEL_X = 2, PANEL_Y = 4, PANEL_W = 8;
 x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
                    uint32_t mode, uint32_t panels);
+// The tiled matrix-core GEMM (gemm.hip) behind x0ne_gpu_gemm_tiled: tile 0 picks per shape;
+// layout X0NE_GEMM_W_PANELS | X0NE_GEMM_X_PANELS names the operands held in 16-row panels.
+x0ne_status tiled_gemm(x0ne_gpu* g, int tile, uint32_t layout, const void* w, uint64_t rows, uint64_t cols,
+                       const void* x, uint64_t n, void* y, bool out_f32);
 // Split plan for a geometry (gpu.rs:958-985), P capped at `cap`.
 x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out);
 x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_block, const void* q, const void* k,

@@ -69,13 +69,17 @@ __global__ void x0ne_rope_table_f64(const float* inv_freq, double* cs, uint32_t 
     __global__ void x0ne_attention_prefill_g##G##_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache, \
                                                       const uint32_t* pages, bf16_t* out, const uint32_t* pos0,  \
                                                       uint32_t rows, uint32_t q_heads, uint32_t kv_heads,        \
-                                                      uint32_t max_ctx, float scale);
+                                                      uint32_t max_ctx, float scale);                    \
+    __global__ void x0ne_attention_prefill_panel_g##G##_bf16(                                                    \
+        const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache, const uint32_t* pages, bf16_t* out,       \
+        const uint32_t* pos0, uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
 X0NE_DECLARE_PREFILL_GROUP(1)
 X0NE_DECLARE_PREFILL_GROUP(2)
 X0NE_DECLARE_PREFILL_GROUP(4)
 X0NE_DECLARE_PREFILL_GROUP(8)
 #undef X0NE_DECLARE_PREFILL_GROUP
 __global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
+__global__ void x0ne_swiglu_panel_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
 __global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
 __global__ void x0ne_argmax_slices_f32(const float* logits, uint32_t n, uint32_t slices, uint32_t* partial);
 __global__ void x0ne_argmax_pick_advance(const uint32_t* partial, uint32_t slices, uint32_t* tokens, uint32_t* pos);

@@ -393,6 +393,29 @@ extern "C" __global__ void __launch_bounds__(256)
     for (uint32_t i = i0; i < min(i0 + 8, inter); ++i) o[i] = swiglu1(row[i], row[inter + i]);
 }
 
+// x0ne_swiglu_bf16 with out in 16-row panels (device.h) of inter columns, for the prefill pass's
+// down projection: the same values (swiglu1 of each gate and up pair), stored at panel_index.
+// grid (ceil(inter / 2048), rows), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_swiglu_panel_bf16(const bf16_t* __restrict__ gate_up, bf16_t* __restrict__ out, uint32_t inter) {
+    const uint32_t i0 = 8 * (blockIdx.x * blockDim.x + threadIdx.x), r = blockIdx.y;
+    if (i0 >= inter) return;
+    const bf16_t* row = gate_up + (size_t)r * 2 * inter;
+    if (inter % 8 == 0 && ((uintptr_t)gate_up & 15) == 0 && ((uintptr_t)out & 15) == 0) {  // grid-uniform
+        const uint4 g = *reinterpret_cast<const uint4*>(row + i0);
+        const uint4 u = *reinterpret_cast<const uint4*>(row + inter + i0);
+        const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            ow[j] = (uint32_t)swiglu1((bf16_t)(gw[j] & 0xFFFFu), (bf16_t)(uw[j] & 0xFFFFu)) |
+                    ((uint32_t)swiglu1((bf16_t)(gw[j] >> 16), (bf16_t)(uw[j] >> 16)) << 16);
+        *reinterpret_cast<uint4*>(out + panel_index(r, i0, inter)) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        return;
+    }
+    for (uint32_t i = i0; i < min(i0 + 8, inter); ++i) out[panel_index(r, i, inter)] = swiglu1(row[i], row[inter + i]);
+}
+
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
     return v > bv || (v == bv && i < bi);
 }

@@ -1,7 +1,5 @@
 // The device, the kernel-launch API, graph capture and the arena: the reference's
 // x0ne-core/runtime/src/{gpu,arena,error}.rs, on the HIP runtime for gfx950.
-#include <hipblaslt/hipblaslt-ext.hpp>
-#include <hipblaslt/hipblaslt.h>
 
 #include <cstdio>
 #include <cstring>
@@ -105,14 +103,12 @@ extern "C" x0ne_status x0ne_gpu_new(x0ne_gpu** out) {
 }
 
 namespace x0ne {
-void lib_gemm_close(x0ne_gpu* g);
 }
 
 extern "C" void x0ne_gpu_free(x0ne_gpu* g) {
     if (!g) return;
     if (g->stream) {
         (void)hipStreamSynchronize(g->stream);
-        x0ne::lib_gemm_close(g);
         (void)hipStreamDestroy(g->stream);
     }
     delete g;
@@ -283,116 +279,28 @@ static constexpr uint64_t GEMM_MAX_BYTES = 0xFFFFFFF0ull;
 
 namespace x0ne {
 
-// ---- many rows: hipBLASLt ----
+// ---- many rows: the tiled matrix-core GEMM of gemm.hip ----
 // The reference hands Gpu::gemm to cuBLAS (gpu.rs:1098-1149); from SKINNY_MAX_ROWS + 1 rows on
-// this library hands it to hipBLASLt. Row-major Y[n][rows] = X[n][cols] W^T is, column-major,
-// D (rows x n) = op(A) B with A = W as a cols x rows matrix (op T) and B = X as cols x n (op N):
-// bf16 A and B, f32 accumulation, D bf16 or f32. Each shape's plan (descriptors and one
-// algorithm) is made once and kept, so a shape always runs the same kernels: results are the
-// same from call to call. The algorithm: among the heuristic's first 16 that need no workspace,
-// the first whose macro tiles (MTaxb in its kernel name: a rows of D by b columns) number at
-// least the device's CUs, else the heuristic's first. (Measured on MI355X at 2048 rows: the
-// heuristic's first pick for a 4096-wide projection is a 256 x 256 tile, 128 tiles for 256
-// CUs, 74.5 us; its second, 256 x 128, takes 57.8 us.)
-struct LibGemm {
-    hipblasLtHandle_t handle = nullptr;
-    struct Plan {
-        hipblasLtMatmulDesc_t desc = nullptr;
-        hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
-        hipblasLtMatmulAlgo_t algo;
-    };
-    std::map<std::tuple<uint64_t, uint64_t, uint64_t, bool>, Plan> plans;
-};
-
-void lib_gemm_close(x0ne_gpu* g) {
-    if (!g->lib_gemm) return;
-    for (auto& kv : g->lib_gemm->plans) {
-        auto& p = kv.second;
-        if (p.a) (void)hipblasLtMatrixLayoutDestroy(p.a);
-        if (p.b) (void)hipblasLtMatrixLayoutDestroy(p.b);
-        if (p.d) (void)hipblasLtMatrixLayoutDestroy(p.d);
-        if (p.desc) (void)hipblasLtMatmulDescDestroy(p.desc);
-    }
-    if (g->lib_gemm->handle) (void)hipblasLtDestroy(g->lib_gemm->handle);
-    delete g->lib_gemm;
-    g->lib_gemm = nullptr;
-}
-
-static x0ne_status lt_fail(hipblasStatus_t st, const std::string& what) {
-    return fail(X0NE_ERR_GPU, "hipBLASLt " + what + ": status " + std::to_string((int)st));
-}
-
-x0ne_status lib_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
-                     bool out_f32) {
-    if (g->capturing) return fail(X0NE_ERR_GPU, "gemm: the many-row projection is not captured into a graph");
-    hipblasStatus_t st;
-    if (!g->lib_gemm) {
-        auto* lg = new LibGemm();
-        st = hipblasLtCreate(&lg->handle);
-        if (st != HIPBLAS_STATUS_SUCCESS) {
-            delete lg;
-            return lt_fail(st, "create");
-        }
-        g->lib_gemm = lg;
-    }
-    auto key = std::make_tuple(rows, cols, n, out_f32);
-    auto it = g->lib_gemm->plans.find(key);
-    if (it == g->lib_gemm->plans.end()) {
-        LibGemm::Plan p;
-        auto done = [&](hipblasStatus_t s, const char* what) -> x0ne_status {
-            if (p.a) (void)hipblasLtMatrixLayoutDestroy(p.a);
-            if (p.b) (void)hipblasLtMatrixLayoutDestroy(p.b);
-            if (p.d) (void)hipblasLtMatrixLayoutDestroy(p.d);
-            if (p.desc) (void)hipblasLtMatmulDescDestroy(p.desc);
-            return lt_fail(s, what);
-        };
-        if ((st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) != HIPBLAS_STATUS_SUCCESS)
-            return done(st, "descriptor");
-        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-        if ((st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) !=
-                HIPBLAS_STATUS_SUCCESS ||
-            (st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb))) !=
-                HIPBLAS_STATUS_SUCCESS)
-            return done(st, "transposes");
-        if ((st = hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, cols, rows, cols)) != HIPBLAS_STATUS_SUCCESS ||
-            (st = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, cols, n, cols)) != HIPBLAS_STATUS_SUCCESS ||
-            (st = hipblasLtMatrixLayoutCreate(&p.d, out_f32 ? HIP_R_32F : HIP_R_16BF, rows, n, rows)) !=
-                HIPBLAS_STATUS_SUCCESS)
-            return done(st, "layouts");
-        hipblasLtMatmulPreference_t pref = nullptr;
-        if ((st = hipblasLtMatmulPreferenceCreate(&pref)) != HIPBLAS_STATUS_SUCCESS) return done(st, "preference");
-        const uint64_t no_workspace = 0;
-        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_workspace,
-                                                   sizeof(no_workspace));
-        hipblasLtMatmulHeuristicResult_t res[16] = {};
-        int got = 0;
-        if (st == HIPBLAS_STATUS_SUCCESS)
-            st = hipblasLtMatmulAlgoGetHeuristic(g->lib_gemm->handle, p.desc, p.a, p.b, p.d, p.d, pref, 16, res, &got);
-        (void)hipblasLtMatmulPreferenceDestroy(pref);
-        if (st != HIPBLAS_STATUS_SUCCESS) return done(st, "heuristic");
-        if (got < 1) return done(HIPBLAS_STATUS_NOT_SUPPORTED, "heuristic (no algorithm)");
-        int pick = 0;
-        for (int i = 0; i < got; ++i) {
-            const std::string name = hipblaslt_ext::getKernelNameFromAlgo(g->lib_gemm->handle, res[i].algo);
-            const size_t at = name.find("_MT");
-            unsigned ma = 0, mb = 0;
-            if (at == std::string::npos || std::sscanf(name.c_str() + at, "_MT%ux%u", &ma, &mb) != 2 || !ma || !mb)
-                continue;
-            if (((rows + ma - 1) / ma) * ((n + mb - 1) / mb) >= g->cus) {
-                pick = i;
-                break;
-            }
-        }
-        p.algo = res[pick].algo;
-        it = g->lib_gemm->plans.emplace(key, p).first;
-    }
-    const auto& p = it->second;
-    const float alpha = 1.f, beta = 0.f;
+// this library runs its own tiled GEMM (x0ne_launch_gemm_tiles), the tile chosen per shape by
+// x0ne_gemm_tile_pick unless `tile` names one. A shape always runs the same kernel, and each
+// output is summed in a fixed order: results are the same from call to call.
+x0ne_status tiled_gemm(x0ne_gpu* g, int tile, uint32_t layout, const void* w, uint64_t rows, uint64_t cols,
+                       const void* x, uint64_t n, void* y, bool out_f32) {
+    const bool wp = layout & X0NE_GEMM_W_PANELS, xp = layout & X0NE_GEMM_X_PANELS;
+    const uint64_t xrows = xp ? (n + 15) / 16 * 16 : n;
+    if (rows == 0 || cols == 0 || n == 0 || rows % 4 != 0 || cols % 8 != 0 || (wp && rows % 16 != 0) ||
+        layout > 3 || rows > UINT32_MAX || n > UINT32_MAX || rows * cols * 2 > GEMM_MAX_BYTES ||
+        xrows * cols * 2 > GEMM_MAX_BYTES || (uintptr_t)w % 16 != 0 || (uintptr_t)x % 16 != 0 ||
+        (uintptr_t)y % (out_f32 ? 16 : 8) != 0)
+        return fail(X0NE_ERR_FORMAT, "tiled gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
+                                         std::to_string(n) + " (rows a multiple of 4, of 16 with W in panels, "
+                                         "cols of 8, W and X below 4 GiB, 16-byte aligned operands)");
+    if (tile == 0) tile = x0ne_gemm_tile_pick((uint32_t)rows, (uint32_t)cols, (uint32_t)n, g->cus);
+    const uint32_t flags = (out_f32 ? X0NE_TILE_F32 : 0u) | (wp ? X0NE_TILE_W_PANEL : 0u) | (xp ? X0NE_TILE_X_PANEL : 0u);
     g->counts.gemms++;
     g->counts.launches++;
-    st = hipblasLtMatmul(g->lib_gemm->handle, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.algo, nullptr,
-                         0, g->stream);
-    if (st != HIPBLAS_STATUS_SUCCESS) return lt_fail(st, "matmul");
+    X0NE_HIP(x0ne_launch_gemm_tiles(tile, w, x, y, (uint32_t)rows, (uint32_t)cols, (uint32_t)n, flags, g->stream),
+             "tiled gemm");
     return X0NE_OK;
 }
 
@@ -548,6 +456,13 @@ extern "C" x0ne_status x0ne_gpu_gemv_fused(x0ne_gpu* g, const x0ne_gemv_fused* d
     return X0NE_OK;
 }
 
+extern "C" x0ne_status x0ne_gpu_gemm_tiled(x0ne_gpu* g, uint32_t tile, uint32_t layout, uint64_t w, uint64_t rows,
+                                           uint64_t cols, uint64_t x, uint64_t n, uint64_t y, int out_f32) {
+    if (!g) return fail(X0NE_ERR_GPU, "no device");
+    if (tile > X0NE_GEMM_TILE_128x128) return fail(X0NE_ERR_FORMAT, "tiled gemm: tile " + std::to_string(tile));
+    return x0ne::tiled_gemm(g, (int)tile, layout, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 != 0);
+}
+
 extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uint64_t cols, uint64_t x, uint64_t n,
                                      uint64_t y, int out_f32) {
     if (!g) return fail(X0NE_ERR_GPU, "no device");
@@ -558,10 +473,12 @@ extern "C" x0ne_status x0ne_gpu_gemv(x0ne_gpu* g, uint64_t w, uint64_t rows, uin
     if (n >= 2 && n <= SKINNY_MAX_ROWS && cols % 8 == 0 && rows * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 &&
         x % 16 == 0)
         return x0ne::skinny(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 ? 1 : 0, 0);
-    // Many rows: hipBLASLt (16-byte aligned operands; otherwise the row-by-row GEMV below).
-    if (n > SKINNY_MAX_ROWS && cols % 8 == 0 && n <= UINT32_MAX && rows * cols * 2 <= GEMM_MAX_BYTES &&
-        n * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 && x % 16 == 0 && y % 16 == 0)
-        return x0ne::lib_gemm(g, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 != 0);
+    // Many rows: the tiled matrix-core GEMM (rows a multiple of 4, aligned operands; otherwise the
+    // row-by-row GEMV below).
+    if (n > SKINNY_MAX_ROWS && cols % 8 == 0 && rows % 4 == 0 && n <= UINT32_MAX &&
+        rows * cols * 2 <= GEMM_MAX_BYTES && n * cols * 2 <= GEMM_MAX_BYTES && w % 16 == 0 && x % 16 == 0 &&
+        y % 16 == 0)
+        return x0ne::tiled_gemm(g, 0, 0, (const void*)w, rows, cols, (const void*)x, n, (void*)y, out_f32 != 0);
     for (uint64_t r = 0; r < n; ++r) {
         const uint16_t* wp = (const uint16_t*)w;
         const uint16_t* xp = (const uint16_t*)(x + r * cols * 2);

@@ -109,6 +109,7 @@ SIGNATURES = {
     "x0ne_gpu_launch": ([P, C.c_char_p, U32, U32, U32, C.POINTER(ArgC), SZ], ST),
     "x0ne_gpu_launch_3d": ([P, C.c_char_p, U32, U32, U32, U32, C.POINTER(ArgC), SZ], ST),
     "x0ne_gpu_gemv": ([P, U64, U64, U64, U64, U64, U64, I32], ST),
+    "x0ne_gpu_gemm_tiled": ([P, U32, U32, U64, U64, U64, U64, U64, U64, I32], ST),
     "x0ne_gpu_gemv_fused_blocks": ([P, C.POINTER(GemvFusedC)], U32),
     "x0ne_gpu_gemv_fused": ([P, C.POINTER(GemvFusedC)], ST),
     "x0ne_gpu_split_plan": ([P, U32, U32, C.POINTER(SplitPlanC)], ST),

@@ -170,6 +170,12 @@ class Gpu:
         """Gpu::gemm (gpu.rs:1098-1149): Y[n][rows] = X[n][cols] W^T on device addresses."""
         check(lib().x0ne_gpu_gemv(self.h, w, rows, cols, x, n, y, int(out_f32)), "gemv")
 
+    def gemm_tiled(self, tile: int, w: int, rows: int, cols: int, x: int, n: int, y: int, out_f32: bool,
+                   layout: int = 0):
+        """The tiled matrix-core GEMM with block tile `tile` (x0ne_gpu_gemm_tiled; 0 picks one),
+        layout bit 0 W in 16-row panels, bit 1 X in panels."""
+        check(lib().x0ne_gpu_gemm_tiled(self.h, tile, layout, w, rows, cols, x, n, y, int(out_f32)), "gemm_tiled")
+
     def gemv_fused(self, **fields) -> None:
         """One fused decode GEMV instance (x0ne_gpu_gemv_fused) on device addresses."""
         d = GemvFusedC(**fields)

@@ -266,21 +266,38 @@ class Kernels:
         self.gpu.sync()
         return a.read_array(ys, 0, rows, np.float32 if out_f32 else np.uint16)
 
-    def gemm(self, w, rows, cols, x, n, out_f32) -> np.ndarray:
+    # x0ne_gpu_gemm_tiled's block tiles (features x tokens) and operand layouts
+    TILE_AUTO, TILE_256x256, TILE_256x128, TILE_128x128 = 0, 1, 2, 3
+    W_PANELS, X_PANELS = 1, 2
+
+    def gemm(self, w, rows, cols, x, n, out_f32, tile=None, layout=0) -> np.ndarray:
         """Gpu::gemm over n rows of X (gpu.rs:1098-1149): Y[n][rows] = X[n][cols] W^T, the
-        few-row matrix-core kernel from 2 to 64 rows, hipBLASLt past them; returns Y (f32, or
-        bf16 bits)."""
+        few-row matrix-core kernel from 2 to 64 rows, the tiled matrix-core GEMM past them;
+        tile names a block tile of the tiled GEMM (x0ne_gpu_gemm_tiled) at any row count, and
+        layout asks it to read W and/or X in 16-row panels (uploaded as such from the row-major
+        arguments); returns Y (f32, or bf16 bits)."""
         if rows == 0 or cols == 0 or n == 0 or w.size != rows * cols or x.size != n * cols:
             raise FormatError(f"gemm: W {w.size} for {rows}x{cols}, X {x.size} for {n} rows")
+        if layout and tile is None:
+            raise FormatError("gemm: a panel layout needs the tiled GEMM (tile; 0 picks one)")
         ob = 4 if out_f32 else 2
+        wv = np.asarray(w).astype(np.uint16)
+        xv = np.asarray(x).astype(np.uint16)
+        if layout & self.W_PANELS:
+            wv = to_panels(wv.reshape(rows, cols))
+        if layout & self.X_PANELS:
+            xv = to_panels(xv.reshape(n, cols))
         a = self._arena()
-        ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
-        xs = a.alloc("x", x.size * 2, Class.CLIENT_DATA)
+        ws = a.alloc("w", wv.size * 2, Class.WEIGHTS)
+        xs = a.alloc("x", xv.size * 2, Class.CLIENT_DATA)
         ys = a.alloc("y", n * rows * ob, Class.CLIENT_DATA)
         self._freeze(a)
-        a.write(ws, 0, w.astype(np.uint16))
-        a.write(xs, 0, x.astype(np.uint16))
-        self.gpu.gemv(a.ptr(ws), rows, cols, a.ptr(xs), n, a.ptr(ys), out_f32)
+        a.write(ws, 0, wv)
+        a.write(xs, 0, xv)
+        if tile is None:
+            self.gpu.gemv(a.ptr(ws), rows, cols, a.ptr(xs), n, a.ptr(ys), out_f32)
+        else:
+            self.gpu.gemm_tiled(tile, a.ptr(ws), rows, cols, a.ptr(xs), n, a.ptr(ys), out_f32, layout)
         self.gpu.sync()
         return a.read_array(ys, 0, n * rows, np.float32 if out_f32 else np.uint16).reshape(n, rows)
 
@@ -695,50 +712,62 @@ class Kernels:
         return a.read_array(dst, 0, m.size, np.uint16)
 
     def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None,
-                             grouped=False):
+                             grouped=False, panel=False):
         """Causal attention for positions pos0..t of a t-position cache in one launch at pos0
         (ops.rs:724-775); q holds those t - pos0 rows; returns the rows asked for. grouped: the
-        matrix-core kernel for the geometry's group size (x0ne_attention_prefill_g*_bf16)."""
+        matrix-core kernel for the geometry's group size (x0ne_attention_prefill_g*_bf16);
+        panel: its variant writing out in 16-row panels (x0ne_attention_prefill_panel_g*_bf16),
+        read back row-major."""
         h.check()
         m = t - pos0
         if m <= 0 or q.size != m * h.q_dim or k.size != t * h.kv_dim or v.size != t * h.kv_dim or \
                 any(r >= m for r in rows):
             raise FormatError("attention_prefill_at: lengths")
-        a, s = self._kv_arena(q, k, v, t, h, page_of, pool, [("out", m * h.q_dim * 2)])
-        a.write(s["pos"], 0, np.array([pos0], np.uint32))
         g = h.q_heads // h.kv_heads
-        if grouped and g not in (1, 2, 4, 8):
+        if (grouped or panel) and g not in (1, 2, 4, 8):
             raise FormatError(f"attention_prefill_at: no grouped kernel for group {g}")
-        name, grid = ((f"x0ne_attention_prefill_g{g}_bf16", (h.kv_heads, (m + PREFILL_COLS // g - 1) // (PREFILL_COLS // g))) if grouped
-                      else ("x0ne_attention_prefill_bf16", (h.q_heads, m)))
+        mp = -(-m // 16) * 16 if panel else m
+        a, s = self._kv_arena(q, k, v, t, h, page_of, pool, [("out", mp * h.q_dim * 2)])
+        a.write(s["pos"], 0, np.array([pos0], np.uint32))
+        kind = "prefill_panel" if panel else "prefill"
+        name, grid = ((f"x0ne_attention_{kind}_g{g}_bf16", (h.kv_heads, (m + PREFILL_COLS // g - 1) // (PREFILL_COLS // g)))
+                      if grouped or panel else ("x0ne_attention_prefill_bf16", (h.q_heads, m)))
         self.gpu.launch(name, grid, 256,
                         [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
                          Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(m),
                          Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(t), Arg.f32(attn_scale(h.head_dim))])
         self.gpu.sync()
-        out = a.read_array(s["out"], 0, m * h.q_dim, np.uint16).reshape(m, h.q_dim)
+        out = a.read_array(s["out"], 0, mp * h.q_dim, np.uint16)
+        out = from_panels(out, m, h.q_dim) if panel else out.reshape(m, h.q_dim)
         return [out[r].copy() for r in rows]
 
-    def attention_prefill_rows(self, q, k, v, t: int, h: Heads, rows, page_of=None, pool=None, grouped=False):
+    def attention_prefill_rows(self, q, k, v, t: int, h: Heads, rows, page_of=None, pool=None, grouped=False,
+                               panel=False):
         """ops.rs:683-722: causal attention over t positions, the rows asked for."""
         if t == 0:
             raise FormatError("attention_prefill_rows: lengths")
-        return self.attention_prefill_at(q, k, v, t, 0, h, rows, page_of, pool, grouped)
+        return self.attention_prefill_at(q, k, v, t, 0, h, rows, page_of, pool, grouped, panel)
 
     # -- swiglu (ops.rs:777-795, :978-1001) --
-    def swiglu_rows(self, gate_up, rows: int) -> np.ndarray:
+    def swiglu_rows(self, gate_up, rows: int, panel: bool = False) -> np.ndarray:
+        """x0ne_swiglu_bf16 over rows of [gate; up]; panel: x0ne_swiglu_panel_bf16 (out in
+        16-row panels, read back row-major). Returns [rows][inter] flattened."""
         if rows == 0 or gate_up.size == 0 or gate_up.size % (2 * rows):
             raise FormatError("swiglu_rows: length is not rows x 2 x inter")
         inter = gate_up.size // rows // 2
+        if panel and inter % 8:
+            raise FormatError("swiglu_rows: panels need inter a multiple of 8")
+        rp = -(-rows // 16) * 16 if panel else rows
         a = self._arena()
         gu = a.alloc("gate_up", gate_up.size * 2, Class.CLIENT_DATA)
-        out = a.alloc("out", rows * inter * 2, Class.CLIENT_DATA)
+        out = a.alloc("out", rp * inter * 2, Class.CLIENT_DATA)
         self._freeze(a)
         a.write(gu, 0, gate_up.astype(np.uint16))
-        self.gpu.launch("x0ne_swiglu_bf16", ((inter + 2047) // 2048, rows), 256,
+        self.gpu.launch("x0ne_swiglu_panel_bf16" if panel else "x0ne_swiglu_bf16", ((inter + 2047) // 2048, rows), 256,
                         [Arg.ptr(a.ptr(gu)), Arg.ptr(a.ptr(out)), Arg.u32(inter)])
         self.gpu.sync()
-        return a.read_array(out, 0, rows * inter, np.uint16)
+        got = a.read_array(out, 0, rp * inter, np.uint16)
+        return from_panels(got, rows, inter).reshape(-1) if panel else got
 
     def swiglu(self, gate_up) -> np.ndarray:
         if gate_up.size == 0 or gate_up.size % 2:
