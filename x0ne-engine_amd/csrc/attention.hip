@@ -1308,9 +1308,9 @@ __device__ __forceinline__ void attn_group_block(const AttnArgs& a, AttnShared<G
 // decode wavefront, which leave each lane the 8 keys of its P row for a 32-key step), a
 // per-column causal mask (keys up to the column's own position; skipped for a tile inside every
 // limit of the wavefront), the online softmax in units of log2 (the rescale of O skipped when no
-// maximum of the group moved), and O += P V with P as bf16 hi + lo (32 products). The next
+// maximum of the group moved), and O += P V with P rounded to bf16 (16 products). The next
 // tile's loads are in flight while a tile is multiplied (two LDS buffers). Each column's output
-// goes straight to out ([rows][q_heads][128]). The heavier half of the row blocks is dispatched
+// goes straight to out ([rows][q_heads][128], or in 16-row panels). The heavier half of the row blocks is dispatched
 // first, heaviest first, then the lighter half, lightest first. Keys at or past the block's context are read as zeros (V) or masked (K); no page past
 // the context is read. Two blocks share a CU (2 x 64 KiB of LDS, at most 256 registers per
 // lane), so one block's products overlap the other's softmax and loads.
@@ -1495,8 +1495,10 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
             }
         }
         // Online softmax per column group in units of log2 (the scale folded into the exponent);
-        // P as bf16 hi + lo.
-        uint4 phi[CG][2], plo[CG][2];
+        // P rounded to bf16 for the P V product (relative error 2^-9 per weight, so at most
+        // max|V| / 512 in an output, against the reference's max|V| / 128; the row sums l are
+        // of the unrounded weights).
+        uint4 phi[CG][2];
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
             float mx = -INFINITY;
@@ -1539,14 +1541,10 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
                     pv[i] = sc[kp][0][i];
                     pv[4 + i] = sc[kp][1][i];
                 }
-                uint32_t hw[4], lw[4];
+                uint32_t hw[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    hw[j] = pack_bf16(pv[2 * j], pv[2 * j + 1]);
-                    lw[j] = pack_bf16(pv[2 * j] - bf_lo(hw[j]), pv[2 * j + 1] - bf_hi(hw[j]));  // exact
-                }
+                for (int j = 0; j < 4; ++j) hw[j] = pack_bf16(pv[2 * j], pv[2 * j + 1]);
                 phi[cg][kp] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-                plo[cg][kp] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
             }
         }
         // O += P V: the V piece (keys 32 kp + 8 q4 .., dim 16 nb + n) serves every group.
@@ -1557,10 +1555,7 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
                 const uint32_t d = 16 * nb + n;
                 const uint4 vb = *reinterpret_cast<const uint4*>(V + d * PF_VS + 8 * pf_v_chunk(d, 4 * kp + q4));
 #pragma unroll
-                for (int cg = 0; cg < CG; ++cg) {
-                    o[cg][nb] = mfma16x16x32(phi[cg][kp], vb, o[cg][nb]);
-                    o[cg][nb] = mfma16x16x32(plo[cg][kp], vb, o[cg][nb]);
-                }
+                for (int cg = 0; cg < CG; ++cg) o[cg][nb] = mfma16x16x32(phi[cg][kp], vb, o[cg][nb]);
             }
         if (tile + 1 < ntiles) stash(tile + 1, buf ^ 1);  // the other buffer was last read before the barrier
         __syncthreads();

@@ -212,11 +212,11 @@ extern "C" __global__ void __launch_bounds__(256)
 // (WF / 16) x (WT / 16) products v_mfma_f32_16x16x32_bf16 with W as the A operand (16 features x
 // 32 k) and X as the B operand (16 tokens x 32 k), so each lane ends with 4 consecutive
 // features of one token and stores them as one 8-byte (bf16) or 16-byte (f32) write.
-//  - K passes in stages of 32 columns through a ring of STAGES buffers in LDS, filled by direct
-//    buffer-to-LDS loads (buffer_load_dwordx4 ... lds: no registers, no VALU) issued STAGES
-//    stages ahead. One barrier per stage.
-//  - The operands of stage s + 1 are read from LDS into a second register set while the
-//    products of stage s run, the reads interleaved with the products (one read, then
+//  - K passes in stages of KS x 32 columns through a ring of STAGES buffers in LDS, filled by
+//    direct buffer-to-LDS loads (buffer_load_dwordx4 ... lds: no registers, no VALU) issued
+//    STAGES stages ahead. One barrier per stage.
+//  - The operands of each 32-column step are read from LDS into a second register set while the
+//    products of the step before run, the reads interleaved with the products (one read, then
 //    products), so the matrix cores do not wait for LDS. Measured on MI355X (Qwen3-8B shapes,
 //    2048 rows): 0.4-0.47 of bf16 peak against 0.36-0.43 without the overlap.
 //  - LDS holds operand fragments in the order the products read them: a fragment is 16 rows x
@@ -240,16 +240,16 @@ namespace {
 constexpr int TILE_GROUP = 4;  // feature tiles side by side in one run of tiles
 constexpr uint32_t TILE_F32 = 1, TILE_W_PANEL = 2, TILE_X_PANEL = 4;
 
-template <int WF, int WT, int NWF, int NWT, int STAGES>
+template <int WF, int WT, int NWF, int NWT, int STAGES, int KS>
 struct TileCfg {
     static constexpr int NW = NWF * NWT;
     static constexpr int BF = NWF * WF, BT = NWT * WT;  // block tile: features x tokens
-    static constexpr int WFR = BF / 16, XFR = BT / 16;   // fragments per 32-column stage
+    static constexpr int WFR = BF / 16, XFR = BT / 16;   // fragments per 32-column step
     static constexpr int FR = WFR + XFR;
-    static constexpr int LOADS = FR / NW;               // load instructions per wavefront per stage
-    static constexpr int BYTES = FR * 1024;             // one stage in LDS
-    static constexpr int RA = WF / 16, RB = WT / 16;    // fragments a wavefront reads per stage
-    static_assert(FR % NW == 0 && WF % 16 == 0 && WT % 16 == 0, "tile shape");
+    static constexpr int LOADS = KS * FR / NW;          // load instructions per wavefront per stage
+    static constexpr int BYTES = KS * FR * 1024;        // one stage (KS steps) in LDS
+    static constexpr int RA = WF / 16, RB = WT / 16;    // fragments a wavefront reads per step
+    static_assert((KS * FR) % NW == 0 && WF % 16 == 0 && WT % 16 == 0, "tile shape");
     static_assert(STAGES >= 2 && STAGES * BYTES <= 160 * 1024, "LDS");
 };
 
@@ -286,11 +286,11 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
 // own wait bookkeeping knows the LDS reads are done.
 constexpr int WAIT_LGKM0 = 0xC07F;
 
-template <int WF, int WT, int NWF, int NWT, int STAGES>
+template <int WF, int WT, int NWF, int NWT, int STAGES, int KS>
 __device__ __forceinline__ void gemm_tiles(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
                                            void* __restrict__ y, uint32_t rows, uint32_t cols, uint32_t n,
                                            uint32_t flags, uint8_t* lds) {
-    using C = TileCfg<WF, WT, NWF, NWT, STAGES>;
+    using C = TileCfg<WF, WT, NWF, NWT, STAGES, KS>;
     const uint32_t tiles_f = (rows + C::BF - 1) / C::BF, tiles_t = (n + C::BT - 1) / C::BT;
     const uint32_t tiles = tiles_f * tiles_t;
     // Launch id -> tile: ids alternate over the 8 XCDs, so id b runs on XCD b % 8; the XCD's
@@ -307,32 +307,34 @@ __device__ __forceinline__ void gemm_tiles(const bf16_t* __restrict__ w, const b
     // Panels hold whole groups of 16 rows.
     const i32x4 wr = rsrc_words(w, (uint64_t)(w_panel ? (rows + 15) / 16 * 16 : rows) * cols * 2);
     const i32x4 xr = rsrc_words(x, (uint64_t)(x_panel ? (n + 15) / 16 * 16 : n) * cols * 2);
-    const uint32_t stages = (cols + 31) / 32, c8 = cols / 8;
+    const uint32_t steps = (cols + 31) / 32, stages = (steps + KS - 1) / KS, c8 = cols / 8;
 
-    // This wavefront's loads of a stage: fragment f = wave + NW q (W fragments first), lane l
-    // fetching row 16 g + l % 16, columns 32 s + 8 (l / 16) .. + 7 of its operand: byte
-    // base[q] + step[q] s of the buffer while those columns exist and the row (panel: its group
-    // of 16) does.
-    uint32_t base[C::LOADS], step[C::LOADS];
+    // This wavefront's loads of a stage: fragment f = wave + NW q of the stage's KS x FR (step
+    // kk = f / FR, fragment f % FR, W fragments first), lane l fetching row 16 g + l % 16,
+    // columns 32 (KS s + kk) + 8 (l / 16) .. + 7 of its operand: byte base[q] + step[q] KS s of
+    // the buffer while those columns exist and the row (panel: its group of 16) does.
+    uint32_t base[C::LOADS], step[C::LOADS], chunk0[C::LOADS];
     bool row_in[C::LOADS];
 #pragma unroll
     for (int q = 0; q < C::LOADS; ++q) {
-        const int f = (int)wave + C::NW * q;
-        const bool is_w = f < C::WFR;
-        const uint32_t g16 = ((is_w ? f0 : t0) >> 4) + (uint32_t)(is_w ? f : f - C::WFR);
+        const int f = (int)wave + C::NW * q, kk = f / C::FR, fr = f % C::FR;
+        const bool is_w = fr < C::WFR;
+        const uint32_t g16 = ((is_w ? f0 : t0) >> 4) + (uint32_t)(is_w ? fr : fr - C::WFR);
         const uint32_t row = 16 * g16 + (lane & 15);
         const bool panel = is_w ? w_panel : x_panel;
         row_in[q] = (panel ? 16 * g16 : row) < (is_w ? rows : n);
-        base[q] = panel ? g16 * c8 * 256 + lane * 16 : row * cols * 2 + (lane >> 4) * 16;
         step[q] = panel ? 1024 : 64;
+        base[q] = (panel ? g16 * c8 * 256 + lane * 16 : row * cols * 2 + (lane >> 4) * 16) + step[q] * kk;
+        chunk0[q] = 4 * kk + (lane >> 4);
     }
     auto issue = [&](uint32_t s) {
         uint8_t* dst = lds + (s % STAGES) * C::BYTES;
 #pragma unroll
         for (int q = 0; q < C::LOADS; ++q) {
             const int f = (int)wave + C::NW * q;
-            const bool in = row_in[q] && 4 * s + (lane >> 4) < c8;
-            load_lds16(f < C::WFR ? wr : xr, lds_addr(dst + f * 1024), in ? base[q] + step[q] * s : OFF_NONE);
+            const bool is_w = f % C::FR < C::WFR;
+            const bool in = row_in[q] && 4 * KS * s + chunk0[q] < c8;
+            load_lds16(is_w ? wr : xr, lds_addr(dst + f * 1024), in ? base[q] + step[q] * KS * s : OFF_NONE);
         }
     };
 
@@ -342,8 +344,8 @@ __device__ __forceinline__ void gemm_tiles(const bf16_t* __restrict__ w, const b
 #pragma unroll
         for (int j = 0; j < C::RB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     uint4 a0[C::RA], b0[C::RB], a1[C::RA], b1[C::RB];
-    auto read = [&](uint32_t s, uint4 (&a)[C::RA], uint4 (&bx)[C::RB]) {
-        const uint8_t* src = lds + (s % STAGES) * C::BYTES;
+    auto read = [&](uint32_t s, int kk, uint4 (&a)[C::RA], uint4 (&bx)[C::RB]) {
+        const uint8_t* src = lds + (s % STAGES) * C::BYTES + kk * C::FR * 1024;
 #pragma unroll
         for (int i = 0; i < C::RA; ++i)
             a[i] = *reinterpret_cast<const uint4*>(src + (wf * C::RA + i) * 1024 + lane * 16);
@@ -368,7 +370,8 @@ __device__ __forceinline__ void gemm_tiles(const bf16_t* __restrict__ w, const b
     };
 
     // Prologue: stages 0 .. STAGES - 1 in flight, stage 0 complete (this wavefront's loads: at
-    // most the later stages' in flight; then the barrier: every wavefront's), its operands read.
+    // most the later stages' in flight; then the barrier: every wavefront's), its first step's
+    // operands read.
 #pragma unroll
     for (int p = 0; p < STAGES; ++p)
         if ((uint32_t)p < stages) issue(p);
@@ -378,35 +381,44 @@ __device__ __forceinline__ void gemm_tiles(const bf16_t* __restrict__ w, const b
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     asm volatile("s_barrier" ::: "memory");
-    read(0, a0, b0);
-    // Stage s: stage s + 1 complete in this wavefront (at most min(stages - s - 2, STAGES - 2)
-    // later stages' loads in flight) and its own reads of stage s done; the barrier: the same in
-    // every wavefront, so stage s's slot is no longer read and takes stage s + STAGES. Then the
-    // products of stage s run while stage s + 1's operands are read (at the last stage, stage s's
-    // again: a harmless read that keeps the reads unconditional). Stages go in pairs so each
-    // stage's register set is fixed at compile time.
+    read(0, 0, a0, b0);
+    // Step kk of stage s: its products run while the next step's operands are read. Before the
+    // last step of stage s: stage s + 1 complete in this wavefront (at most min(stages - s - 2,
+    // STAGES - 2) later stages' loads in flight) and its own reads of stage s done; the barrier:
+    // the same in every wavefront, so stage s's slot is no longer read and takes stage
+    // s + STAGES. The next step after the last one reads stage s's last step again (a harmless
+    // read that keeps the reads unconditional). Stages go in pairs so each step's register set
+    // is fixed at compile time.
     for (uint32_t s2 = 0; s2 < stages; s2 += 2) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t s = s2 + h;
             if (s >= stages) break;
-            if (s + 1 < stages) {
-                if (stages - s - 2 >= (uint32_t)(STAGES - 2)) {
-                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::LOADS * (STAGES - 2)) : "memory");
-                } else {
-                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                uint32_t ns = s;
+                int nk = kk + 1;
+                if (kk == KS - 1) {
+                    if (s + 1 < stages) {
+                        if (stages - s - 2 >= (uint32_t)(STAGES - 2)) {
+                            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::LOADS * (STAGES - 2)) : "memory");
+                        } else {
+                            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                        }
+                    }
+                    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+                    asm volatile("s_barrier" ::: "memory");
+                    if (s + STAGES < stages) issue(s + STAGES);
+                    ns = s + 1 < stages ? s + 1 : s;
+                    nk = s + 1 < stages ? 0 : kk;
                 }
-            }
-            __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
-            asm volatile("s_barrier" ::: "memory");
-            if (s + STAGES < stages) issue(s + STAGES);
-            const uint32_t next = s + 1 < stages ? s + 1 : s;
-            if (h == 0) {
-                read(next, a1, b1);
-                compute(a0, b0);
-            } else {
-                read(next, a0, b0);
-                compute(a1, b1);
+                if (((h * KS + kk) & 1) == 0) {
+                    read(ns, nk, a1, b1);
+                    compute(a0, b0);
+                } else {
+                    read(ns, nk, a0, b0);
+                    compute(a1, b1);
+                }
             }
         }
     }
@@ -439,20 +451,22 @@ __device__ __forceinline__ void gemm_tiles(const bf16_t* __restrict__ w, const b
 // Tiled GEMM kernels: grid ceil(rows / BF) ceil(n / BT), block 64 NWF NWT; rows a multiple of 4,
 // cols of 8 (and rows of 16 with W in panels), W and X below 4 GiB - 16 bytes, Y 8-byte (bf16)
 // or 16-byte (f32) aligned; flags TILE_F32 | TILE_W_PANEL | TILE_X_PANEL.
-#define X0NE_TILES(NAME, WF, WT, NWF, NWT, STAGES)                                                             \
-    extern "C" __global__ void __launch_bounds__(64 * NWF * NWT)                                                  \
-        NAME(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, uint32_t rows,     \
-             uint32_t cols, uint32_t n, uint32_t flags) {                                                         \
-        __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * TileCfg<WF, WT, NWF, NWT, STAGES>::BYTES]; \
-        if (rows % 4 != 0 || cols % 8 != 0 || n == 0 || ((flags & TILE_W_PANEL) && rows % 16 != 0)) return;     \
-        gemm_tiles<WF, WT, NWF, NWT, STAGES>(w, x, y, rows, cols, n, flags, lds);                                 \
+#define X0NE_TILES(NAME, WF, WT, NWF, NWT, STAGES, KS)                                                          \
+    extern "C" __global__ void __launch_bounds__(64 * NWF * NWT)                                                      \
+        NAME(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, uint32_t rows,         \
+             uint32_t cols, uint32_t n, uint32_t flags) {                                                             \
+        __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * TileCfg<WF, WT, NWF, NWT, STAGES, KS>::BYTES]; \
+        if (rows % 4 != 0 || cols % 8 != 0 || n == 0 || ((flags & TILE_W_PANEL) && rows % 16 != 0)) return;         \
+        gemm_tiles<WF, WT, NWF, NWT, STAGES, KS>(w, x, y, rows, cols, n, flags, lds);                                 \
     }
-// Block tiles, all of four stages, from sweeps on MI355X over the Qwen3-8B prefill shapes at 2048
-// rows, operands in panels: 256 x 256 of 8 wavefronts (64 features x 128 tokens each; two per
-// SIMD), 256 x 128 of 8 (64 x 64 each), and 128 x 128 of 4 (64 x 64 each; two blocks per CU).
-X0NE_TILES(x0ne_gemm_tiles_256x256_bf16, 64, 128, 4, 2, 4)
-X0NE_TILES(x0ne_gemm_tiles_256x128_bf16, 64, 64, 4, 2, 4)
-X0NE_TILES(x0ne_gemm_tiles_128x128_bf16, 64, 64, 2, 2, 4)
+// Block tiles from sweeps on MI355X over the Qwen3-8B prefill shapes at 2048 rows, operands in
+// panels, all in four stages of 32 columns (64-column stages, two of them for 256 x 256 and three
+// for 256 x 128, measured 3-10 % slower in the engine's prefill): 256 x 256 of 8 wavefronts
+// (64 features x 128 tokens each; two per SIMD), 256 x 128 of 8 (64 x 64 each), and 128 x 128 of
+// 4 (64 x 64 each; two blocks per CU).
+X0NE_TILES(x0ne_gemm_tiles_256x256_bf16, 64, 128, 4, 2, 4, 1)
+X0NE_TILES(x0ne_gemm_tiles_256x128_bf16, 64, 64, 4, 2, 4, 1)
+X0NE_TILES(x0ne_gemm_tiles_128x128_bf16, 64, 64, 2, 2, 4, 1)
 
 // ---- typed launchers of the tiled GEMM (called by the runtime) ----
 
