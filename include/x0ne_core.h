@@ -260,8 +260,9 @@ typedef struct x0ne_greedy x0ne_greedy;
      X0NE_SUMS_DEFAULT (0, what EngineOptions { max_ctx } gives) is the exact mode wherever the
      engine can serve it, else the f32 path (MoE models, max_batch > 1).
    - prefill_chunk: prompt rows per prefill pass (engine.rs:67, PREFILL_CHUNK); 0 takes
-     min(2048, max_ctx). A pass runs every layer over its rows with matrix-core GEMMs and the
-     causal prefill attention; the exact mode feeds a prompt one decode step per token.
+     min(2048, max_ctx x max_batch). A pass runs every layer over its rows with matrix-core
+     GEMMs and the causal prefill attention; the exact mode feeds a prompt one decode step per
+     token.
    - max_batch: independent sequences the batched greedy entry points serve (0 or 1: the
      single-sequence engine). Each sequence has its own max_ctx positions of KV pages (the page
      table holds max_batch runs of ceil(max_ctx / 16) pages) and its own position; the batched
@@ -339,9 +340,10 @@ x0ne_status x0ne_engine_decode_timed(x0ne_engine* e, const uint32_t* prompt, siz
 /* Batched greedy decoding of `batch` independent sequences (1 <= batch <= max_batch): no
    counterpart in the reference, whose engine serves one sequence at a time (engine.rs:389-406);
    it is Engine::greedy_timed applied to each of `batch` prompts at once. prompts holds
-   batch rows of n_prompt ids. Each prompt is prefilled into its own KV pages (passes of
-   prefill_chunk rows), then every decode step advances all sequences: one graph launch (or the
-   eager launches) and one copy of `batch` token words. tokens receives batch rows of n tokens;
+   batch rows of n_prompt ids. Each prompt is prefilled into its own KV pages: prompts of more
+   than 64 ids that fit a pass share passes (prefill_chunk / n_prompt of them side by side),
+   longer ones take passes of up to prefill_chunk rows each. Then every decode step advances
+   all sequences: one graph launch (or the eager launches) and one copy of `batch` token words. tokens receives batch rows of n tokens;
    times (may be NULL) the wall time of each step's tokens, seconds from the call; last_logits
    (may be NULL) batch rows of vocab_size floats, the logits of each sequence's last token.
    A sequence's tokens and logits do not depend on the other sequences of the batch: the same

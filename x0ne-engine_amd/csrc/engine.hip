@@ -429,6 +429,7 @@ struct x0ne_engine {
         act{}, logits{}, head_partial{}, head_counter{}, attn_state{}, attn_counter{};
     // A prefill pass's rows: f32 residual, bf16 delta, normed x, qkv, q, attention, [gate; up], act.
     x0ne_slice p_res{}, p_delta{}, p_x{}, p_qkv{}, p_q{}, p_attn{}, p_gu{}, p_act{};
+    x0ne_slice p_tok{};  // a batched engine's pass of several sequences: their ids side by side
     // The batched step's rows ([max_batch][...]): f32 residual, bf16 delta, normed x, qkv,
     // attention, SwiGLU activation, f32 logits; its split-K state and counters.
     x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{}, b_argmax{};
@@ -591,6 +592,7 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("prefill_attn", np * c.q_dim() * 2, CD, &e->p_attn));
         X0NE_TRY(al("prefill_gate_up", n * 2 * c.inter * 2, CD, &e->p_gu));
         X0NE_TRY(al("prefill_act", np * c.inter * 2, CD, &e->p_act));
+        if (e->max_batch > 1) X0NE_TRY(al("prefill_ids", n * 4, CD, &e->p_tok));
     }
     if (e->max_batch > 1) {
         const uint64_t b = e->max_batch, bp = (b + 15) / 16 * 16;  // panels hold whole tiles of 16 rows
@@ -932,17 +934,33 @@ x0ne_status gemm(x0ne_engine* e, x0ne_slice w, x0ne_slice w_panels, uint64_t row
 // the down GEMM. Leaves the rows' residual and last delta for the final norm. Sequence b: its
 // prompt row, position and KV pages. With ppanel the GEMM inputs are written in panels (the same
 // values at panel_index) and the GEMMs read W's panel copies.
-x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b = 0) {
+// seqs > 1 (a batched engine's prompts of one length): sequences b .. b + seqs - 1 in one pass,
+// n rows each at the same positions, side by side (rows s n .. s n + n - 1 are sequence b + s):
+// the GEMMs, norms and SwiGLU take all seqs n rows at once, QK-norm + RoPE and the attention run
+// per sequence on its rows, pages and position. With panels n is a multiple of 16, so each
+// sequence's rows start a panel.
+x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b = 0, uint64_t seqs = 1) {
     const Cfg& c = e->c;
-    if (e->chunk < 2 || n == 0 || n > e->chunk || pos0 + n > e->max_ctx || b >= e->max_batch)
-        return fail(X0NE_ERR_FORMAT, "prefill: " + std::to_string(n) + " rows at " + std::to_string(pos0));
-    X0NE_TRY(set_position(e, pos0, b));
+    if (e->chunk < 2 || n == 0 || seqs == 0 || n * seqs > e->chunk || pos0 + n > e->max_ctx || b + seqs > e->max_batch ||
+        (seqs > 1 && e->ppanel && n % 16 != 0))
+        return fail(X0NE_ERR_FORMAT, "prefill: " + std::to_string(seqs) + " x " + std::to_string(n) + " rows at " +
+                                         std::to_string(pos0));
+    for (uint64_t s = 0; s < seqs; ++s) X0NE_TRY(set_position(e, pos0, b + s));
+    const uint32_t sn = (uint32_t)n;  // rows of one sequence
+    n *= seqs;
     const uint32_t rows = (uint32_t)n, h = (uint32_t)c.hidden, vocab = (uint32_t)c.vocab, inter = (uint32_t)c.inter;
     const uint32_t qh = (uint32_t)c.q_heads, kvh = (uint32_t)c.kv_heads, max_ctx = (uint32_t)e->max_ctx;
     const float eps = (float)c.eps, scale = (float)(1.0 / std::sqrt((double)c.head_dim));
     {
         const void* table = e->d(e->embed);
         const void* toks = e->prompt_of(b) + pos0;
+        if (seqs > 1) {  // the sequences' ids of this pass side by side
+            e->gpu->counts.launches++;
+            X0NE_HIP(hipMemcpy2DAsync(e->d(e->p_tok), (size_t)sn * 4, toks, e->max_ctx * 4, (size_t)sn * 4, seqs,
+                                      hipMemcpyDeviceToDevice, e->gpu->stream),
+                     "pass ids");
+            toks = e->d(e->p_tok);
+        }
         void* out = e->d(e->p_delta);
         void* args[] = {(void*)&table, (void*)&toks, (void*)&out, (void*)&h, (void*)&vocab};
         X0NE_TRY(launch_rows(e, (const void*)&x0ne_embedding_bf16, dim3(rows), dim3(128), args, "embedding"));
@@ -969,35 +987,35 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
         const LayerW& w = e->L[l];
         X0NE_TRY(norm(w.input_norm));
         X0NE_TRY(gemm(e, w.qkv, w.qkv_p, c.qkv_rows(), c.hidden, e->p_x, n, e->p_qkv));
-        {
-            const void* qkv = e->d(e->p_qkv);
+        for (uint64_t sq = 0; sq < seqs; ++sq) {
+            const void* qkv = e->d(e->p_qkv) + sq * sn * c.qkv_rows() * 2;
             const void* qn = e->d(w.q_norm);
             const void* kn = e->d(w.k_norm);
             const void* cs = e->d(e->rope_cs);
-            void* q = e->d(e->p_q);
+            void* q = e->d(e->p_q) + sq * sn * c.q_dim() * 2;
             void* kc = e->plane(l, 0);
             void* vc = e->plane(l, 1);
-            const void* pt = e->pages_of(b);
-            const void* pos = e->pos_of(b);
+            const void* pt = e->pages_of(b + sq);
+            const void* pos = e->pos_of(b + sq);
             void* args[] = {(void*)&qkv, (void*)&qn, (void*)&kn, (void*)&cs, (void*)&q,       (void*)&kc, (void*)&vc,
                             (void*)&pt,  (void*)&pos, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&eps};
-            X0NE_TRY(launch_rows(e, (const void*)&x0ne_qk_norm_rope_kv_write_rows_bf16, dim3((qh + kvh + 3) / 4, rows),
+            X0NE_TRY(launch_rows(e, (const void*)&x0ne_qk_norm_rope_kv_write_rows_bf16, dim3((qh + kvh + 3) / 4, sn),
                                  dim3(256), args, "qk_norm_rope_kv_write"));
         }
-        {
-            const void* q = e->d(e->p_q);
+        for (uint64_t sq = 0; sq < seqs; ++sq) {
+            const void* q = e->d(e->p_q) + sq * sn * c.q_dim() * 2;
             const void* kc = e->plane(l, 0);
             const void* vc = e->plane(l, 1);
-            const void* pt = e->pages_of(b);
-            void* out = e->d(e->p_attn);
-            const void* pos = e->pos_of(b);
-            void* args[] = {(void*)&q,    (void*)&kc, (void*)&vc,  (void*)&pt,      (void*)&out, (void*)&pos,
-                            (void*)&rows, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&scale};
+            const void* pt = e->pages_of(b + sq);
+            void* out = e->d(e->p_attn) + sq * sn * c.q_dim() * 2;  // a whole number of panels
+            const void* pos = e->pos_of(b + sq);
+            void* args[] = {(void*)&q,  (void*)&kc, (void*)&vc,  (void*)&pt,      (void*)&out, (void*)&pos,
+                            (void*)&sn, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&scale};
             if (grouped) {
                 const uint32_t per = X0NE_PREFILL_COLS / group;  // rows per block
-                X0NE_TRY(launch_rows(e, grouped, dim3(kvh, (rows + per - 1) / per), dim3(256), args, "prefill attention"));
+                X0NE_TRY(launch_rows(e, grouped, dim3(kvh, (sn + per - 1) / per), dim3(256), args, "prefill attention"));
             } else {
-                X0NE_TRY(launch_rows(e, (const void*)&x0ne_attention_prefill_bf16, dim3(qh, rows), dim3(256), args,
+                X0NE_TRY(launch_rows(e, (const void*)&x0ne_attention_prefill_bf16, dim3(qh, sn), dim3(256), args,
                                      "prefill attention"));
             }
         }
@@ -1174,11 +1192,13 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     e->f64_sums = exact_sums(c, *opts) ? 1 : 0;
     // The exact mode's sums are the decode GEMV's (f64): its prompts go one step per token.
     // A MoE engine prefills through the decode route too (engine.rs:322-328).
-    e->chunk = e->f64_sums || c.moe
-                   ? 1
-                   : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK, opts->max_ctx);
-    if (e->chunk == 0) e->chunk = 1;
+    // A pass holds up to max_ctx rows of one sequence, or of several for a batched engine (its
+    // prompts of one length share a pass).
     e->max_batch = opts->max_batch ? opts->max_batch : 1;  // check_config bounded it
+    e->chunk = e->f64_sums || c.moe ? 1
+                                    : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK,
+                                                         opts->max_ctx * e->max_batch);
+    if (e->chunk == 0) e->chunk = 1;
     e->seq_pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
     e->pages = e->max_batch * e->seq_pages;
     x0ne_status st = x0ne_gpu_new(&e->gpu);
@@ -2022,13 +2042,35 @@ x0ne_status batch_prefill(x0ne_engine* e, const uint32_t* prompts, size_t np, ui
     if (e->mode == X0NE_DECODE_GRAPH) X0NE_TRY(batch_capture(e, B));
     for (uint32_t b = 0; b < B; ++b)
         X0NE_TRY(x0ne_arena_write(e->arena, e->prompt, (uint64_t)b * e->max_ctx * 4, prompts + (size_t)b * np, np * 4));
-    for (uint32_t b = 0; b < B; ++b) {
-        X0NE_TRY(prefill_passes(e, np, b));
-        // Its logits row where the batched step leaves the others' (the last token's logits of a
-        // one-token request).
+    // Prompts that fit a pass several at a time go together (chunk / np of them; with panels np
+    // a multiple of 16), the others one sequence at a time in passes of up to chunk rows. Only
+    // prompts of more than 64 rows: a sequence alone then runs the same tiled GEMM as the shared
+    // pass (64 rows or fewer take the few-row kernel), so each sequence's bits do not depend on
+    // the batch.
+    const uint64_t per_pass =
+        np > 64 && np <= e->chunk && (!e->ppanel || np % 16 == 0) ? e->chunk / np : 1;
+    // Its logits row where the batched step leaves the others' (the last token's logits of a
+    // one-token request).
+    auto keep_logits = [&](uint32_t b) -> x0ne_status {
         X0NE_HIP(hipMemcpyAsync(e->d(e->b_logits) + (uint64_t)b * e->c.vocab * 4, e->d(e->logits), e->c.vocab * 4,
                                 hipMemcpyDeviceToDevice, e->gpu->stream),
                  "first logits");
+        return X0NE_OK;
+    };
+    for (uint32_t b = 0; b < B;) {
+        if (per_pass > 1) {
+            const uint32_t seqs = (uint32_t)std::min<uint64_t>(per_pass, B - b);
+            X0NE_TRY(prefill_pass(e, 0, np, b, seqs));
+            for (uint32_t s = 0; s < seqs; ++s) {
+                X0NE_TRY(prefill_head(e, (uint64_t)s * np + np - 1, np - 1, true, b + s));
+                X0NE_TRY(keep_logits(b + s));
+            }
+            b += seqs;
+        } else {
+            X0NE_TRY(prefill_passes(e, np, b));
+            X0NE_TRY(keep_logits(b));
+            ++b;
+        }
     }
     std::vector<uint32_t> first(B);
     X0NE_TRY(x0ne_arena_read(e->arena, e->tokens, 0, first.data(), B * 4));
