@@ -771,6 +771,8 @@ struct ExactShared {
     uint32_t last;
 };
 
+constexpr uint32_t EXACT_CHUNK = 16;  // slices whose f64 o values the exact merge loads at once
+
 __device__ __forceinline__ void dstate_put(double* p, double v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1114,11 +1116,28 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         }
         const double l = wave_sum_d(lp);
         wave_lds_sync();
+        // The slices' o values in chunks of EXACT_CHUNK, every load of a chunk issued before any
+        // is used (one round trip to memory per chunk, not per slice), summed in slice order.
         double o0 = 0.0, o1 = 0.0;
-        for (uint32_t yy = 0; yy < active; ++yy) {
-            const double* so = s + (size_t)yy * X0NE_SPLIT_STATE + 4;
-            o0 = fma(dstate_get(so + lane), f[yy], o0);
-            o1 = fma(dstate_get(so + lane + 64), f[yy], o1);
+        double av[EXACT_CHUNK], bv[EXACT_CHUNK];
+        auto request = [&](uint32_t y0) {
+#pragma unroll
+            for (uint32_t k = 0; k < EXACT_CHUNK; ++k)
+                if (y0 + k < active) {  // wave-uniform
+                    const double* so = s + (size_t)(y0 + k) * X0NE_SPLIT_STATE + 4;
+                    av[k] = dstate_get(so + lane);
+                    bv[k] = dstate_get(so + lane + 64);
+                }
+        };
+        request(0);
+        for (uint32_t y0 = 0; y0 < active; y0 += EXACT_CHUNK) {
+#pragma unroll
+            for (uint32_t k = 0; k < EXACT_CHUNK; ++k)
+                if (y0 + k < active) {
+                    o0 = fma(av[k], f[y0 + k], o0);
+                    o1 = fma(bv[k], f[y0 + k], o1);
+                }
+            if (y0 + EXACT_CHUNK < active) request(y0 + EXACT_CHUNK);
         }
         a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + lane] = f2bf((float)(o0 / l));
         a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + lane + 64] = f2bf((float)(o1 / l));

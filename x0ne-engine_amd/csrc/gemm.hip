@@ -2,7 +2,7 @@
 // matrix cores: Y[n][rows] = X[n][cols] W^T with W [rows][cols] and X [n][cols] bf16 row-major,
 // f32 accumulation, Y bf16 or f32 (the reference's Gpu::gemm, gpu.rs:1098-1149). At one row the
 // decode GEMV (gemv.hip) is the right kernel; past 64 rows the work is a compute-bound GEMM,
-// which the runtime hands to hipBLASLt as the reference hands it to cuBLAS (runtime.hip).
+// the tiled kernels further down.
 #include "device.h"
 
 namespace {

@@ -52,7 +52,6 @@ struct x0ne_gpu {
     // This device's copy of the library's static scratch array (runtime.hip, `scratch`), as
     // hipGetSymbolAddress gave it at x0ne_gpu_new with the device current.
     void* scratch = nullptr;
-    // hipBLASLt for the many-row projections, opened at the first one.
 };
 
 struct x0ne_graph {
