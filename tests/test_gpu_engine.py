@@ -171,18 +171,21 @@ def test_greedy_on_the_device_is_greedy_on_the_host(which):
         print(f"MEASURE greedy prompt {prompt_len}: compared {compared} of {n} tokens with the oracle")
 
 
-@pytest.mark.parametrize("which", [0, 1])
-def test_batched_greedy_is_each_sequence_alone_and_the_oracle(which):
+@pytest.mark.parametrize("which,np_,chunk", [(0, 21, 16), (1, 21, 16), (0, 80, 0), (1, 80, 0)])
+def test_batched_greedy_is_each_sequence_alone_and_the_oracle(which, np_, chunk):
     """B independent prompts decoded together (the batched step: few-row GEMMs, one attention
     launch over every sequence's own pages): each sequence's tokens and last logits are the bits
     it gets alone or in another batch order, graph and eager alike; they are the oracle's greedy
     tokens until the oracle's top-2 margin is within the tolerance, and its logits within the
-    model tolerance; and the client bytes are zeroed after."""
+    model tolerance; and the client bytes are zeroed after. Prompts of 21 ids go in passes of 16
+    rows, one sequence at a time; prompts of 80 ids (more than 64, a multiple of 16) share one
+    prefill pass of 320 rows (the default pass size, min(2048, max_ctx x max_batch)), and alone
+    take a pass of 80: the same bits either way."""
     from x0ne_core import DecodeMode, Engine, EngineOptions
     f = [Fixture(tiny(2, 4, 2, False), 21), Fixture(wide(), 22)][which]
     e = Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
-                         EngineOptions(max_ctx=96, page_seed=9, prefill_chunk=16, max_batch=4))
-    B, np_, n = 4, 21, 30
+                         EngineOptions(max_ctx=128, page_seed=9, prefill_chunk=chunk, max_batch=4))
+    B, n = 4, 30
     prompts = np.stack([f.tokens(300 + b, np_) for b in range(B)])
     toks, times, logits = e.greedy_batch(prompts, n, logits=True)
     assert toks.shape == (B, n) and (np.diff(times) >= 0).all()

@@ -1339,7 +1339,8 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     return v;
 }
 constexpr int PF_CG = 2;              // column groups of 16 per wavefront
-static_assert(4 * 16 * PF_CG == X0NE_PREFILL_COLS, "columns per prefill block");
+constexpr int PF_NW = X0NE_PREFILL_THREADS / 64;  // wavefronts per block
+static_assert(PF_NW * 16 * PF_CG == X0NE_PREFILL_COLS, "columns per prefill block");
 // LDS tiles without padding: K [64 keys][128 dims], V [128 dims][64 keys], their 16-byte chunks
 // placed by an XOR of the row (pf_k_chunk, pf_v_chunk) so that neither the products' reads nor
 // the stores of a tile meet in a bank. Measured on gfx950 (bank-conflict counters over single
@@ -1359,20 +1360,23 @@ struct PrefillShared {
     alignas(16) bf16_t v[2][X0NE_HEAD_DIM * PF_VS];
 };
 
-template <int G, int CG, bool OUT_PANEL = false>
+template <int G, int CG, bool OUT_PANEL = false, int NW = 4>
 __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
                                               const bf16_t* __restrict__ v_cache, const uint32_t* __restrict__ pages,
                                               bf16_t* __restrict__ out, uint32_t p0, uint32_t rows, uint32_t q_heads,
                                               uint32_t kv_heads, uint32_t max_ctx, float scale, PrefillShared& sh) {
-    constexpr uint32_t COLS = 4 * 16 * CG;  // columns per block: CG groups of 16 per wavefront
+    constexpr uint32_t COLS = NW * 16 * CG;  // columns per block: CG groups of 16 per wavefront
     constexpr uint32_t RB = COLS / G;
+    constexpr uint32_t NT = 64 * NW, J = 1024 / NT;  // threads; K (and V) chunks of a tile per thread
+    static_assert(1024 % NT == 0, "a tile's 1024 chunks over the block's threads");
     // Dispatch order: the first half of the row blocks heaviest first, then the second half
     // lightest first, so the two blocks that share a CU (block i and block i + half the grid)
     // hold a heavy and a light row block (four 2048-row passes: 245.5 against 251.4 µs mean).
     const uint32_t ny = gridDim.y, half = (ny + 1) / 2, y = blockIdx.y;
     const uint32_t kh = blockIdx.x, rb = y < half ? ny - 1 - y : y - half;
     const uint32_t r0 = rb * RB;
-    if (kh >= kv_heads || q_heads != (uint32_t)G * kv_heads || r0 >= rows || max_ctx == 0) return;  // block-uniform
+    if (kh >= kv_heads || q_heads != (uint32_t)G * kv_heads || r0 >= rows || max_ctx == 0 || blockDim.x != NT)
+        return;  // block-uniform
     const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t n = lane & 15, q4 = lane >> 4;
     const uint32_t ctx = min(p0 + min(r0 + RB, rows), max_ctx);  // keys the block reads
@@ -1395,7 +1399,7 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
             qb[cg][st] = live ? *reinterpret_cast<const uint4*>(qr + 32 * st) : make_uint4(0, 0, 0, 0);
     }
 
-    // A tile's K and V pieces for this thread: K chunk i = t + 256 j is page i / 256, key
+    // A tile's K and V pieces for this thread: K chunk i = t + NT j is page i / 256, key
     // (i / 16) % 16, 16-byte piece i % 16; V chunk i is page i / 256, dim v_dim(i), keys
     // 8 (i % 2) .. + 7 of the page. A wavefront's V loads cover 32 dims of a page (1 KiB
     // contiguous), and 8 neighbouring lanes hold dims 4 apart, so their LDS chunks differ.
@@ -1403,17 +1407,20 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
     // The page-table entries of a tile are requested one tile before its K and V.
     auto v_dim = [](uint32_t i) { return 32 * ((i >> 6) & 3) + 16 * ((i >> 5) & 1) + 4 * ((i >> 1) & 3) + ((i >> 3) & 3); };
     auto v_half = [](uint32_t i) { return i & 1; };
-    uint4 kr[4], vr[4];
+    uint4 kr[J], vr[J];
     const auto kres = plane_rsrc(k_cache, OFF_NONE), vres = plane_rsrc(v_cache, OFF_NONE);
-    uint32_t pe[4];  // entries of the next tile to fetch (chunk j of a thread is in page j)
+    uint32_t pe[J];  // entries of the next tile to fetch (chunk j of a thread is in page (t + NT j) / 256)
     auto entries = [&](uint32_t tile) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pe[j] = 4 * tile + j < npages ? pages[4 * tile + j] : 0u;
+        for (int j = 0; j < (int)J; ++j) {
+            const uint32_t pi = (t + NT * j) >> 8;
+            pe[j] = 4 * tile + pi < npages ? pages[4 * tile + pi] : 0u;
+        }
     };
     auto fetch = [&](uint32_t tile) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t i = t + BLOCK * j, pi = i >> 8, lp = 4 * tile + pi;
+        for (int j = 0; j < (int)J; ++j) {
+            const uint32_t i = t + NT * j, pi = i >> 8, lp = 4 * tile + pi;
             const uint32_t pb = pe[j] * kv_heads + kh;
             kr[j] = bload16(kres, lp < npages ? ((pb * X0NE_PAGE + ((i >> 4) & 15)) * X0NE_HEAD_DIM + 8 * (i & 15)) * 2
                                               : OFF_NONE);
@@ -1427,8 +1434,8 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
         const bool edge = X0NE_SPLIT_TILE * (tile + 1) > ctx;  // block-uniform
         if (edge) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t i = t + BLOCK * j, pi = i >> 8;
+            for (int j = 0; j < (int)J; ++j) {
+                const uint32_t i = t + NT * j, pi = i >> 8;
                 const uint32_t key0 = X0NE_SPLIT_TILE * tile + X0NE_PAGE * pi + 8 * v_half(i);
                 const uint32_t valid = key0 >= ctx ? 0u : min(ctx - key0, 8u);
                 uint32_t w[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
@@ -1439,8 +1446,8 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
             }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t i = t + BLOCK * j, pi = i >> 8, r = 16 * pi + ((i >> 4) & 15), d = v_dim(i);
+        for (int j = 0; j < (int)J; ++j) {
+            const uint32_t i = t + NT * j, pi = i >> 8, r = 16 * pi + ((i >> 4) & 15), d = v_dim(i);
             *reinterpret_cast<uint4*>(&sh.k[buf][r * PF_KS + 8 * pf_k_chunk(r, i & 15)]) = kr[j];
             *reinterpret_cast<uint4*>(&sh.v[buf][d * PF_VS + 8 * pf_v_chunk(d, 2 * pi + v_half(i))]) = vr[j];
         }
@@ -1611,25 +1618,25 @@ __device__ __forceinline__ void prefill_block(const bf16_t* __restrict__ q, cons
 // arguments and semantics) on the matrix cores for G q heads per kv head; grid (kv_heads,
 // ceil(rows / (128 / G))), block 256, two wavefronts per SIMD.
 #define X0NE_PREFILL_GROUP(G)                                                                                      \
-    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))                  \
+    extern "C" __global__ void __launch_bounds__(X0NE_PREFILL_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) \
         x0ne_attention_prefill_g##G##_bf16(                                                                       \
         const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
         const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos0,          \
         uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale) {                       \
         __shared__ PrefillShared sh;                                                                               \
-        prefill_block<G, PF_CG>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx, scale, \
-                                sh);                                                                               \
+        prefill_block<G, PF_CG, false, PF_NW>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads,     \
+                                              max_ctx, scale, sh);                                                 \
     }                                                                                                              \
     /* The same with out in 16-row panels (device.h) of q_heads 128 columns: the prefill pass's O      */          \
     /* projection reads it so.                                                                          */          \
-    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))                  \
+    extern "C" __global__ void __launch_bounds__(X0NE_PREFILL_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) \
         x0ne_attention_prefill_panel_g##G##_bf16(                                                                 \
         const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
         const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos0,          \
         uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale) {                       \
         __shared__ PrefillShared sh;                                                                               \
-        prefill_block<G, PF_CG, true>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx,  \
-                                      scale, sh);                                                                  \
+        prefill_block<G, PF_CG, true, PF_NW>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads,      \
+                                             max_ctx, scale, sh);                                                  \
     }
 X0NE_PREFILL_GROUP(1)
 X0NE_PREFILL_GROUP(2)

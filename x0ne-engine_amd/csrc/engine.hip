@@ -1013,7 +1013,8 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
                             (void*)&sn, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&scale};
             if (grouped) {
                 const uint32_t per = X0NE_PREFILL_COLS / group;  // rows per block
-                X0NE_TRY(launch_rows(e, grouped, dim3(kvh, (sn + per - 1) / per), dim3(256), args, "prefill attention"));
+                X0NE_TRY(launch_rows(e, grouped, dim3(kvh, (sn + per - 1) / per), dim3(X0NE_PREFILL_THREADS), args,
+                                     "prefill attention"));
             } else {
                 X0NE_TRY(launch_rows(e, (const void*)&x0ne_attention_prefill_bf16, dim3(qh, sn), dim3(256), args,
                                      "prefill attention"));

@@ -62,9 +62,11 @@ __global__ void x0ne_attention_prefill_bf16(const bf16_t* q, const bf16_t* k_cac
                                             const uint32_t* pages, bf16_t* out, const uint32_t* pos0, uint32_t rows,
                                             uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
 __global__ void x0ne_rope_table_f64(const float* inv_freq, double* cs, uint32_t positions);
-// Columns (row, q head) per block of x0ne_attention_prefill_g{G}_bf16: its grid is (kv_heads,
-// ceil(rows / (X0NE_PREFILL_COLS / G))).
+// Columns (row, q head) per block of x0ne_attention_prefill_g{G}_bf16 and its threads: its grid
+// is (kv_heads, ceil(rows / (X0NE_PREFILL_COLS / G))), its block X0NE_PREFILL_THREADS (a block
+// of another size does nothing).
 #define X0NE_PREFILL_COLS 128
+#define X0NE_PREFILL_THREADS 256
 #define X0NE_DECLARE_PREFILL_GROUP(G)                                                                            \
     __global__ void x0ne_attention_prefill_g##G##_bf16(const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache, \
                                                       const uint32_t* pages, bf16_t* out, const uint32_t* pos0,  \

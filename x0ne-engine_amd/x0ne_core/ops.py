@@ -21,6 +21,7 @@ HEAD_DIM = 128
 PAGE = 16
 SPLIT_STATE = HEAD_DIM + 4
 PREFILL_COLS = 128  # columns (row, q head) per block of x0ne_attention_prefill_g*_bf16
+PREFILL_THREADS = 256  # its block
 NAN_BF16 = 0x7FC0
 
 
@@ -732,7 +733,7 @@ class Kernels:
         kind = "prefill_panel" if panel else "prefill"
         name, grid = ((f"x0ne_attention_{kind}_g{g}_bf16", (h.kv_heads, (m + PREFILL_COLS // g - 1) // (PREFILL_COLS // g)))
                       if grouped or panel else ("x0ne_attention_prefill_bf16", (h.q_heads, m)))
-        self.gpu.launch(name, grid, 256,
+        self.gpu.launch(name, grid, PREFILL_THREADS if grouped or panel else 256,
                         [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
                          Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(m),
                          Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(t), Arg.f32(attn_scale(h.head_dim))])
