@@ -24,10 +24,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)n, RSRC_WORD3);
 }
 
-// The default cache policy throughout: a non-temporal hint on the few-row GEMM's weight stream
-// (which speeds the decode GEMV's, gemv.hip) made its launches 5-15 % slower on MI355X.
+// CPOL: the cache policy (0 the default; CPOL_NT non-temporal, for a stream read once).
+constexpr int CPOL_NT = 2;
+template <int CPOL = 0>
 __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL);
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
 
@@ -38,14 +39,19 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // kernel streams W at the HBM rate and the few-row matrix-core products cost nothing beside it:
 //  - Block b takes the RG row groups of 16 W rows 16 RG b .. 16 RG b + 16 RG - 1 over all of K;
 //    its V wavefronts (V = blockDim / 64, chosen by the host with RG so the launch holds enough
-//    loads in flight) take V contiguous runs of K, in whole steps of 32 columns.
+//    loads in flight) take its steps of 32 columns in turn (wavefront w: steps w, w + V, ..), so
+//    at any time a block reads one contiguous run of each of its panels.
+//  - W is read with a non-temporal hint (each byte read once), X with the default policy (every
+//    block reads it, from the L2). Measured on MI355X on the batched Qwen3-8B and -32B shapes
+//    (W and X in panels): 3-19 % faster than each wavefront reading its own quarter of K with the
+//    default policy.
 //  - A step is TT x RG 16 x 16 x 32 products (TT tiles of 16 tokens, RG row groups) whose A
 //    operand is X (row = token, zero past n) and B operand W (column = W row): lane l loads
 //    16 bytes, columns k0 + 8 (l / 16) .. + 7, of W row 16 (RG b + g) + l % 16 and of X row
 //    16 tt + l % 16; the 4 lane groups cover 64 contiguous bytes of each row. One X piece
 //    serves the RG row groups, so X (read from the L2 by every block) costs TT / RG of W's loads.
 //  - U steps are in flight per wavefront: the slot a product has consumed is refilled at once
-//    with the step U ahead, so U - 1 steps stay in flight while one multiplies. A piece past K
+//    with the wavefront's step U ahead, so U - 1 steps stay in flight while one multiplies. A piece past K
 //    (or a token past n, a W row past rows) is a raw buffer load at an offset past the buffer,
 //    which returns zeros without touching memory.
 //  - The wavefronts' partial tiles are summed in LDS in wavefront order (deterministic).
@@ -61,7 +67,7 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // costs the W stream up to a fifth of its rate at 16 rows (measured on MI355X). W is laid out the
 // same way for the same reason: row-major, each step reads 64 bytes of 16 rows cols apart, and
 // the W stream of the Qwen3 decode shapes runs at 3.1-5.1 TB/s; in panels each step reads one
-// contiguous KiB and a wavefront's steps run through its panel in order, 3.7-5.9 TB/s (MI355X).
+// contiguous KiB and a block's steps run through its panel in order, 3.7-5.9 TB/s (MI355X).
 namespace {
 
 constexpr uint32_t FEW_F32 = 1, FEW_X_PANEL = 2, FEW_Y_PANEL = 4, FEW_W_PANEL = 8;
@@ -83,8 +89,7 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
     // Panels hold whole tiles of 16 rows.
     const auto xr = rsrc(x, (uint64_t)(x_panel ? (n + 15) / 16 * 16 : n) * cols * 2);
     const auto wr = rsrc(w, (uint64_t)KINDS * rows * cols * 2);
-    const uint32_t steps = (cols + 31) / 32, per = (steps + V - 1) / V;
-    const uint32_t s_begin = min(wave * per, steps), s_end = min(s_begin + per, steps);
+    const uint32_t steps = (cols + 31) / 32;
     f32x4 acc[KINDS][RG][TT];
 #pragma unroll
     for (int kd = 0; kd < KINDS; ++kd)
@@ -95,12 +100,12 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
     uint4 xa[U][TT], wb[U][KINDS][RG];
     auto request = [&](int u, uint32_t s) {
         const uint32_t k = 32 * s + 8 * q4;
-        const bool in = s < s_end && k < cols;  // a K tail: pieces past the row read zeros
+        const bool in = s < steps && k < cols;  // a K tail: pieces past the row read zeros
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
             const uint32_t t = 16 * tt + r;
             const uint32_t off = x_panel ? (uint32_t)panel_index(t, k, cols) * 2 : (t * cols + k) * 2;
-            xa[u][tt] = bload(xr, in && t < n ? off : OFF_NONE);
+            xa[u][tt] = bload<>(xr, in && t < n ? off : OFF_NONE);
         }
 #pragma unroll
         for (int kd = 0; kd < KINDS; ++kd)
@@ -108,14 +113,14 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
             for (int g = 0; g < RG; ++g) {
                 const uint32_t row = 16 * (RG * b + g) + r;
                 const uint32_t wrow = kd * rows + row;
-                wb[u][kd][g] = bload(wr, !(in && row < rows) ? OFF_NONE
+                wb[u][kd][g] = bload<CPOL_NT>(wr, !(in && row < rows) ? OFF_NONE
                                          : w_panel ? (uint32_t)panel_index(wrow, k, cols) * 2
                                                    : (wrow * cols + k) * 2);
             }
     };
 #pragma unroll
-    for (int u = 0; u < U; ++u) request(u, s_begin + u);
-    for (uint32_t s0 = s_begin; s0 < s_end; s0 += U) {
+    for (int u = 0; u < U; ++u) request(u, wave + V * u);
+    for (uint32_t s0 = wave; s0 < steps; s0 += U * V) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
@@ -124,7 +129,7 @@ __device__ __forceinline__ void few_rows(const bf16_t* __restrict__ w, const bf1
                 for (int g = 0; g < RG; ++g)
 #pragma unroll
                     for (int tt = 0; tt < TT; ++tt) acc[kd][g][tt] = mfma(xa[u][tt], wb[u][kd][g], acc[kd][g][tt]);
-            request(u, s0 + U + u);
+            request(u, s0 + V * (U + u));
         }
     }
     // part[(((kd V + wave) RG + g) TT + tt) 64 + lane]

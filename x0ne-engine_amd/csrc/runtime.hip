@@ -318,7 +318,8 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
     // KiB of a launch fastest alone, so a launch of up to two blocks per CU takes RG so that at
     // most one block lands on each CU (a CU with two finishes last); large launches (the LM
     // head) take RG 2 at up to 8 rows of X and 8 beyond, where each X piece costs as much as a
-    // W piece; SwiGLU launches, two W pieces per X piece already, keep RG 1. With W in panels
+    // W piece; SwiGLU launches, two W pieces per X piece already, keep RG 1 over 8 wavefronts
+    // (Qwen3-8B at 8 rows 31.6 against 32.4 us over 4, -32B at 16 rows 82.4 against 83.3). With W in panels
     // (PANEL_W) the one-block-per-CU rule extends to RG 4, and a large launch takes RG 2 over 8
     // wavefronts at every n up to 16.
     const bool glu = mode == 2, wpan = panels & PANEL_W;
@@ -328,7 +329,7 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
     if (n <= 16) {
         if (glu) {
             fn = (const void*)&x0ne_gemm_few_t1_r1_swiglu_bf16;
-            waves = blocks_of(1) >= 4 * g->cus ? 8 : 4;
+            waves = 8;
         } else if (wpan) {
             if (blocks_of(1) <= g->cus)
                 rg = 1;
