@@ -396,6 +396,38 @@ def test_few_row_gemm_reads_w_in_panels_bit_for_bit(kernels, seed):
         kernels.gemm_few(w[:(rows + 8) * 8], rows + 8, 8, x[:n * 8], n, 0, w_panel=True)
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_balanced_few_row_gemm_is_the_oracle_and_the_same_bits_every_time(kernels, seed):
+    """The balanced few-row kernel (one block per equal run of the groups' steps; groups cut
+    between two runs finished by the last block to count): every row of Y is the oracle's GEMV
+    within the GEMV tolerance, bf16 Y is f32 Y rounded, a row alone gets the bits it gets in the
+    batch, repeated launches give the same bits and leave every count at zero. Runs shorter and
+    longer than a group, cut groups, K tails, 4 and 8 wavefronts."""
+    rng = O.Rng(1900 + seed)
+    n = rng.pick([1, 5, 8, 16])
+    rows = 16 * rng.pick([3, 17, 40, 300])
+    cols = rng.pick([264, 1024, 2056, 8192])
+    block = rng.pick([256, 512])
+    groups, steps = rows // 16, -(-cols // 32)
+    T = rng.pick([max(block // 64, steps // 2 + 3), steps + 5, 2 * steps - 1, -(-groups * steps // 7)])
+    T = max(block // 64, min(T, 4 * steps + 1))
+    scale = rng.pick([1e-2, 1.0])
+    w = bf16s_with_edges(rng, rows * cols, scale)
+    x = bf16s_with_edges(rng, n * cols, scale)
+    what = f"balanced few-row seed {seed} {n}x{rows}x{cols} block {block} run {T}"
+    f, zero = kernels.gemm_few_bal(bf16_bits(w), rows, cols, bf16_bits(x), n, 1, block, T, calls=2)
+    assert zero, f"{what}: counts left at zero"
+    for r in range(n):
+        xr = x[r * cols:(r + 1) * cols]
+        assert_gemv(f"{what} row {r} f32", f[r], O.gemv(w, rows, cols, xr), O.gemv_magnitude(w, rows, cols, xr), False)
+    b, _ = kernels.gemm_few_bal(bf16_bits(w), rows, cols, bf16_bits(x), n, 0, block, T)
+    assert (b == bf16_bits(f).reshape(b.shape)).all(), f"{what}: bf16 is the f32 rounded"
+    f2, _ = kernels.gemm_few_bal(bf16_bits(w), rows, cols, bf16_bits(x), n, 1, block, T)
+    assert (f2.view(np.uint32) == f.view(np.uint32)).all(), f"{what}: the same bits again"
+    f1, _ = kernels.gemm_few_bal(bf16_bits(w), rows, cols, bf16_bits(x[:cols]), 1, 1, block, T)
+    assert (f1[0].view(np.uint32) == f[0].view(np.uint32)).all(), f"{what}: row 0 alone"
+
+
 @pytest.mark.parametrize("rows,cols", [(16, 8), (48, 40), (32, 1000), (1024, 4096), (17, 8), (16, 12)])
 def test_panel_copy_is_the_panel_layout(kernels, rows, cols):
     """x0ne_panel_bf16 (the load-time copy of a batched engine's weights) writes the host's panel

@@ -433,6 +433,8 @@ struct x0ne_engine {
     // The batched step's rows ([max_batch][...]): f32 residual, bf16 delta, normed x, qkv,
     // attention, SwiGLU activation, f32 logits; its split-K state and counters.
     x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{}, b_argmax{};
+    // The balanced few-row GEMM's parts and counts (runtime.hip, skinny).
+    x0ne_slice b_few_ws{}, b_few_cnt{};
     // The MoE feed-forward's rows: the normed x, the router's f32 logits, each layer's chosen
     // expert ids and weights ([layers][top_k], read back by x0ne_engine_moe_routing), the chosen
     // experts' SwiGLU activations.
@@ -607,6 +609,9 @@ x0ne_status plan(x0ne_engine* e) {
                     &e->b_state));
         X0NE_TRY(al("batch_split_counter", b * c.kv_heads * 4, CD, &e->b_counter));
         X0NE_TRY(al("batch_argmax", b * ARGMAX_SLICES * 3 * 4, CD, &e->b_argmax));
+        const uint64_t groups = std::max<uint64_t>(c.hidden, c.qkv_rows()) / 16;
+        X0NE_TRY(al("batch_gemm_parts", groups * 2 * 256 * 4, CD, &e->b_few_ws));
+        X0NE_TRY(al("batch_gemm_counts", groups * 4, CD, &e->b_few_cnt));
     }
     return X0NE_OK;
 }
@@ -1877,11 +1882,21 @@ x0ne_status batch_embed_norm(x0ne_engine* e, uint32_t B) {
 
 uint32_t wpanel_bit(const x0ne_engine* e) { return e->wpanel ? PANEL_W : 0u; }
 
+// The workspace of the batched projections' balanced kernel.
+FewWork few_work(x0ne_engine* e) {
+    FewWork w;
+    w.ws = reinterpret_cast<float*>(e->d(e->b_few_ws));
+    w.cnt = reinterpret_cast<uint32_t*>(e->d(e->b_few_cnt));
+    w.groups = e->b_few_cnt.len / 4;
+    return w;
+}
+
 x0ne_status batch_qkv(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
     const LayerW& w = e->L[l];
+    const FewWork fw = few_work(e);
     return skinny(e->gpu, e->d(e->wpanel ? w.qkv_p : w.qkv), c.qkv_rows(), c.hidden, e->d(e->b_x), B, e->d(e->b_qkv),
-                  0, PANEL_X | wpanel_bit(e));
+                  0, PANEL_X | wpanel_bit(e), &fw);
 }
 
 x0ne_status batch_attention(x0ne_engine* e, uint32_t B, uint64_t l) {
@@ -1919,8 +1934,9 @@ x0ne_status batch_attention(x0ne_engine* e, uint32_t B, uint64_t l) {
 x0ne_status batch_o(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
     const LayerW& w = e->L[l];
+    const FewWork fw = few_work(e);
     return skinny(e->gpu, e->d(e->wpanel ? w.o_p : w.o), c.hidden, c.q_dim(), e->d(e->b_attn), B, e->d(e->b_delta), 0,
-                  PANEL_X | wpanel_bit(e));
+                  PANEL_X | wpanel_bit(e), &fw);
 }
 
 x0ne_status batch_gate_up(x0ne_engine* e, uint32_t B, uint64_t l) {
@@ -1933,8 +1949,9 @@ x0ne_status batch_gate_up(x0ne_engine* e, uint32_t B, uint64_t l) {
 x0ne_status batch_down(x0ne_engine* e, uint32_t B, uint64_t l) {
     const Cfg& c = e->c;
     const LayerW& w = e->L[l];
+    const FewWork fw = few_work(e);
     return skinny(e->gpu, e->d(e->wpanel ? w.down_p : w.down), c.hidden, c.inter, e->d(e->b_act), B, e->d(e->b_delta),
-                  0, PANEL_X | wpanel_bit(e));
+                  0, PANEL_X | wpanel_bit(e), &fw);
 }
 
 // The f32 LM head over the B normed rows, then each row's argmax into its token, position + 1.

@@ -197,6 +197,156 @@ X0NE_FEW(x0ne_gemm_few_t4_r1_bf16, 4, 1, 4, false, 8)
 X0NE_FEW(x0ne_gemm_few_t4_r1_swiglu_bf16, 4, 1, 4, true, 8)
 #endif
 
+// ---- a few rows balanced over the CUs: one block per CU, an equal run of the steps ----
+// Where the 16-row groups are between one and two per CU (the Qwen3-32B O and down projections:
+// 320 groups on 256 CUs), whole groups per block leave CUs idle (RG 2: 160 blocks) or doubled
+// (RG 1). Here the steps of all groups, group-major (G groups x S steps of 32 columns), are cut
+// into runs of T steps, one run per block and one block per CU, and the block's V wavefronts
+// take its run's steps in turn (wavefront w: steps Lb + w, Lb + w + V, ..), so every block
+// streams the same bytes as one contiguous run through the panels (a run crosses a group's end
+// where one panel ends and the next begins).
+//  - A wavefront sums its steps in order, one accumulator at a time: where its next step is in
+//    the next group, the sums go to LDS (slot g - g0), so its loads never wait on a store.
+//  - The block sums each group's wavefront partials in wavefront order. A group inside its run is
+//    written at once. A group cut between runs (at most two blocks meet in a group here) is
+//    finished by the last of its blocks to count: each stores its sums in slot (g, block - first
+//    block of g) through agent-scope stores (coherent across the XCDs' L2s), waits for their
+//    acknowledgment and counts in cnt[g]; the one that completes the count adds the slots in
+//    slot order, writes Y and sets the count back to 0 for the next launch.
+// Every sum's order is fixed by (rows, cols, T, V): the same bits whatever n, the timing or
+// which block finishes a group. Measured on MI355X (32B down, 16 rows, 262 MB): 48.1 against
+// 53.0 us for RG 2 (160 blocks); shapes whose groups are not cut this way (the 8B projections,
+// SwiGLU, 640 or 1600 groups) measured no faster than whole groups per block.
+namespace {
+
+__device__ __forceinline__ void bal_put(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float bal_get(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int U, int MAXG, int MAXV>
+__device__ __forceinline__ void few_bal(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
+                                        void* __restrict__ y, uint32_t rows, uint32_t cols, uint32_t n,
+                                        uint32_t flags, uint32_t T, float* __restrict__ ws,
+                                        uint32_t* __restrict__ cnt, f32x4* stash) {
+    const bool out_f32 = flags & FEW_F32, y_panel = flags & FEW_Y_PANEL;
+    const uint32_t S = (cols + 31) / 32, G = rows / 16, V = blockDim.x >> 6;
+    const uint64_t total = (uint64_t)G * S;
+    // Grid-uniform exits for a launch that does not fit: a run touches at most MAXG groups and
+    // gives every wavefront a step; X and W in panels.
+    if (n == 0 || n > 16 || cols % 8 != 0 || rows % 16 != 0 || T < V || (uint64_t)T > (uint64_t)(MAXG - 2) * S + 1 ||
+        total >= (1ull << 31) || V > MAXV || S < V || flags > 15 || !(flags & FEW_W_PANEL) || !(flags & FEW_X_PANEL) ||
+        (out_f32 && y_panel) || (y_panel && rows % 8 != 0) || ws == nullptr || cnt == nullptr)
+        return;
+    const uint32_t b = blockIdx.x;
+    if ((uint64_t)b * T >= total) return;  // block-uniform
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t r = lane & 15, q4 = lane >> 4;
+    const uint32_t Lb = b * T, Le = (uint32_t)min<uint64_t>((uint64_t)Lb + T, total), g0 = Lb / S;
+    const uint32_t cmax = (S + T - 1) / T + 1;  // blocks that can meet in one group
+    const auto xr = rsrc(x, (uint64_t)16 * cols * 2);
+    const auto wr = rsrc(w, (uint64_t)rows * cols * 2);
+    f32x4* mine = stash + (size_t)wave * MAXG * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < MAXG; ++j) mine[j * 64] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 xa[U], wb[U];
+    // Requests run through the wavefront's steps: (rg, rs) is request rq's group and step.
+    const uint32_t L0 = Lb + wave;
+    uint32_t rq = L0, rg = L0 / S, rs = L0 - rg * S;
+    auto request = [&](int u) {
+        const uint32_t k = 32 * rs + 8 * q4;
+        const bool in = rq < Le && k < cols;  // a K tail: pieces past the row read zeros
+        xa[u] = bload<>(xr, in && r < n ? (uint32_t)panel_index(r, k, cols) * 2 : OFF_NONE);
+        wb[u] = bload<CPOL_NT>(wr, in ? (uint32_t)panel_index(16 * rg + r, k, cols) * 2 : OFF_NONE);
+        rq += V;
+        rs += V;
+        if (rs >= S) {
+            rs -= S;
+            ++rg;
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < U; ++u) request(u);
+    uint32_t cq = L0, cg = L0 / S, cs = L0 - cg * S;  // the consumed step, its group and place
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t q0 = L0; q0 < Le; q0 += U * V) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (cq < Le) {  // wavefront-uniform
+                acc = mfma(xa[u], wb[u], acc);
+                cq += V;
+                cs += V;
+                if (cs >= S) {  // this wavefront's part of group cg ends: its sums to LDS
+                    mine[(cg - g0) * 64] = acc;
+                    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+                    cs -= S;
+                    ++cg;
+                }
+            }
+            request(u);
+        }
+    }
+    if (cs != 0) mine[(cg - g0) * 64] = acc;  // the run ends inside group cg
+    lds_barrier();
+    // sg[i]: token 4 (lane / 16) + i, W row 16 g + lane % 16.
+    auto emit = [&](uint32_t g, const f32x4& sg) {
+        const uint32_t wrow = 16 * g + r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t t = 4 * q4 + i;
+            if (t >= n) continue;
+            const size_t o = y_panel ? panel_index(t, wrow, rows) : (size_t)t * rows + wrow;
+            if (out_f32)
+                static_cast<float*>(y)[o] = sg[i];
+            else
+                static_cast<bf16_t*>(y)[o] = f2bf(sg[i]);
+        }
+    };
+    auto slot = [&](uint32_t g, uint32_t c) { return ws + ((size_t)g * cmax + c) * 256 + lane * 4; };
+    const uint32_t ng = (Le - 1) / S - g0 + 1;
+    // Wavefront w finishes the block's groups w, w + V, ..
+    for (uint32_t j = wave; j < ng; j += V) {
+        const uint32_t g = g0 + j;
+        f32x4 sg = stash[j * 64 + lane];
+        for (uint32_t v = 1; v < V; ++v) sg += stash[(v * MAXG + j) * 64 + lane];
+        const uint32_t fb = (uint32_t)((uint64_t)g * S / T), lb = (uint32_t)(((uint64_t)g * S + S - 1) / T);
+        if (fb == lb) {
+            emit(g, sg);
+            continue;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bal_put(slot(g, b - fb) + e, sg[e]);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slot acknowledged, then the count
+        uint32_t old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(old) != lb - fb) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sg[e] = bal_get(slot(g, 0) + e);
+        for (uint32_t c = 1; c <= lb - fb; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sg[e] += bal_get(slot(g, c) + e);
+        emit(g, sg);
+        if (lane == 0) __hip_atomic_store(cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+}  // namespace
+
+// x0ne_gemm_few_bal_bf16: grid ceil(G S / T) for G = rows / 16 groups and S = ceil(cols / 32)
+// steps, block 64 V threads (V <= 8, V <= T <= 4 S + 1); n in 1 .. 16; rows a multiple of 16,
+// cols of 8; X and W in panels (flags FEW_X_PANEL | FEW_W_PANEL, FEW_F32 or FEW_Y_PANEL as
+// above; no SwiGLU); ws: G (ceil(S / T) + 1) 256 floats, cnt: G words, zero before the first
+// launch and left zero by every launch. Launches sharing ws and cnt must not overlap.
+extern "C" __global__ void __launch_bounds__(512)
+    x0ne_gemm_few_bal_bf16(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y,
+                           uint32_t rows, uint32_t cols, uint32_t n, uint32_t flags, uint32_t T, float* __restrict__ ws,
+                           uint32_t* __restrict__ cnt) {
+    __shared__ f32x4 stash[8 * 6 * 64];
+    few_bal<8, 6, 8>(w, x, y, rows, cols, n, flags, T, ws, cnt, stash);
+}
+
 // x0ne_panel_bf16: a row-major [rows][cols] bf16 matrix copied into 16-row panels (element (r, k)
 // at panel_index(r, k, cols)), one 16-byte chunk per thread in destination order, so the writes
 // are contiguous; grid ceil(rows cols / 8 / 256), block 256. rows a multiple of 16 and cols of 8,

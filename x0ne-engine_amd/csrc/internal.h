@@ -88,8 +88,15 @@ x0ne_status launch_checked(x0ne_gpu* g, const X0neKernel& k, uint32_t gx, uint32
 // (mode 0 bf16 Y, 1 f32 Y, 2 SwiGLU over a packed [gate; up] W of 2 rows rows); panels: 2 X in
 // panels, 4 Y in panels (bf16 Y), 8 W in panels (rows a multiple of 16), the layout of device.h.
 constexpr uint32_t PANEL_X = 2, PANEL_Y = 4, PANEL_W = 8;
+// With `work` (a workspace for up to work->groups 16-row groups), a shape whose groups are
+// between one and two per CU takes the balanced kernel (x0ne_gemm_few_bal_bf16) instead.
+struct FewWork {
+    float* ws = nullptr;      // 2 x 256 floats per group
+    uint32_t* cnt = nullptr;  // one word per group: zero, left zero by every launch
+    uint64_t groups = 0;
+};
 x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
-                   uint32_t mode, uint32_t panels);
+                   uint32_t mode, uint32_t panels, const FewWork* work = nullptr);
 // The tiled matrix-core GEMM (gemm.hip) behind x0ne_gpu_gemm_tiled: tile 0 picks per shape;
 // layout X0NE_GEMM_W_PANELS | X0NE_GEMM_X_PANELS names the operands held in 16-row panels.
 x0ne_status tiled_gemm(x0ne_gpu* g, int tile, uint32_t layout, const void* w, uint64_t rows, uint64_t cols,

@@ -109,6 +109,8 @@ X0NE_DECLARE_FEW(t2_r1_swiglu)
 X0NE_DECLARE_FEW(t4_r1)
 X0NE_DECLARE_FEW(t4_r1_swiglu)
 #undef X0NE_DECLARE_FEW
+__global__ void x0ne_gemm_few_bal_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols,
+                                       uint32_t n, uint32_t flags, uint32_t T, float* ws, uint32_t* cnt);
 __global__ void x0ne_moe_route_f32(const float* logits, uint32_t experts, uint32_t top_k, uint32_t* ids,
                                    float* weights);
 __global__ void x0ne_moe_gemv_bf16(const bf16_t* w, const uint32_t* ids, const bf16_t* x, bf16_t* y, uint32_t rows,

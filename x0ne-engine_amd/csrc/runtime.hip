@@ -305,7 +305,7 @@ x0ne_status tiled_gemm(x0ne_gpu* g, int tile, uint32_t layout, const void* w, ui
 }
 
 x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
-                   uint32_t mode, uint32_t panels) {
+                   uint32_t mode, uint32_t panels, const FewWork* work) {
     const uint64_t wrows = mode == 2 ? 2 * rows : rows;
     if (n == 0 || n > SKINNY_MAX_ROWS || rows == 0 || cols == 0 || cols % 8 != 0 || mode > 2 || (panels & ~14u) ||
         ((panels & 4) && (mode == 1 || rows % 8 != 0)) || ((panels & 8) && rows % 16 != 0) ||
@@ -313,6 +313,27 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
         (uintptr_t)x % 16 != 0)
         return fail(X0NE_ERR_FORMAT, "few-row gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
                                          std::to_string(n) + ", mode " + std::to_string(mode));
+    // Between one and two 16-row groups per CU, each of at least 512 steps, with X and W in
+    // panels: one block per CU over an equal run of the steps (gemm.hip, few_bal; 4 wavefronts,
+    // swept on MI355X; the 32B O projection's 256-step groups measured no faster). Runs are
+    // longer than a group (T >= S), so at most two blocks meet in one.
+    const uint64_t groups = rows / 16, steps = (cols + 31) / 32;
+    if (work && work->ws && work->cnt && n <= 16 && mode != 2 && (panels & PANEL_X) && (panels & PANEL_W) &&
+        rows % 16 == 0 && groups > g->cus && groups < 2ull * g->cus && steps >= 512 && groups <= work->groups) {
+        const uint64_t T = (groups * steps + g->cus - 1) / g->cus;
+        uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, t32 = (uint32_t)T;
+        uint32_t flags = (mode == 1 ? 1u : 0u) | panels;
+        float* wsp = work->ws;
+        uint32_t* cntp = work->cnt;
+        void* args[] = {(void*)&w,     (void*)&x,  (void*)&y,   (void*)&r32,  (void*)&c32,
+                        (void*)&n32,   (void*)&flags, (void*)&t32, (void*)&wsp, (void*)&cntp};
+        g->counts.gemms++;
+        g->counts.launches++;
+        X0NE_HIP(x0ne_launch((const void*)&x0ne_gemm_few_bal_bf16, dim3((uint32_t)((groups * steps + T - 1) / T)),
+                             dim3(256), args, 0, g->stream),
+                 "balanced few-row gemm");
+        return X0NE_OK;
+    }
     // Row groups per block (each X piece serves RG W pieces) and wavefronts per block, from sweeps
     // on MI355X over the decode shapes (X in panels, 8 and 16 rows): a CU streams a few hundred
     // KiB of a launch fastest alone, so a launch of up to two blocks per CU takes RG so that at

@@ -694,6 +694,40 @@ class Kernels:
         y = a.read_array(ys, 0, yrows * rows, np.float32 if mode == 1 else np.uint16)
         return from_panels(y, n, rows) if y_panel else y.reshape(n, rows)
 
+    def gemm_few_bal(self, w, rows: int, cols: int, x, n: int, mode: int, block: int = 256, T: int = 0,
+                     calls: int = 1):
+        """x0ne_gemm_few_bal_bf16, the balanced few-row kernel (one block per run of T of the
+        groups' steps, X and W handed over in panels): mode 0 bf16 Y, 1 f32 Y. T 0 takes the
+        runs the runtime takes (ceil(groups steps / CUs)). `calls` launches in a row (the last
+        one's Y). Returns (Y [n][rows], every count left zero)."""
+        groups, steps = rows // 16, -(-cols // 32)
+        if T == 0:
+            T = -(-groups * steps // self.gpu.compute_units())
+        if w.size != rows * cols or x.size != n * cols or not 1 <= n <= 16 or cols % 8 or rows % 16 or mode not in (0, 1) \
+                or not block // 64 <= T <= 4 * steps + 1 or block // 64 > 8:
+            raise FormatError("gemm_few_bal: lengths or run")
+        cmax = -(-steps // T) + 1
+        ob = 4 if mode == 1 else 2
+        a = self._arena()
+        ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
+        xin = to_panels(np.asarray(x, np.uint16).reshape(n, cols))
+        xs = a.alloc("x", xin.size * 2, Class.CLIENT_DATA)
+        ys = a.alloc("y", n * rows * ob, Class.CLIENT_DATA)
+        parts = a.alloc("parts", groups * cmax * 256 * 4, Class.CLIENT_DATA)
+        counts = a.alloc("counts", groups * 4, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.scrub_client_data()
+        a.write(ws, 0, to_panels(np.asarray(w, np.uint16).reshape(rows, cols)))
+        a.write(xs, 0, xin)
+        for _ in range(calls):
+            self.gpu.launch("x0ne_gemm_few_bal_bf16", -(-groups * steps // T), block,
+                            [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(cols),
+                             Arg.u32(n), Arg.u32((1 if mode == 1 else 0) | 2 | 8), Arg.u32(T), Arg.ptr(a.ptr(parts)),
+                             Arg.ptr(a.ptr(counts))])
+        self.gpu.sync()
+        y = a.read_array(ys, 0, n * rows, np.float32 if mode == 1 else np.uint16).reshape(n, rows)
+        return y, bool((a.read_array(counts, 0, groups, np.uint32) == 0).all())
+
     def panel(self, m, rows: int, cols: int) -> np.ndarray:
         """x0ne_panel_bf16: the [rows][cols] bf16 matrix m copied into 16-row panels on the device
         (flat, rows x cols values; left as the destination held it, 0xFFFF here, when rows is not a
