@@ -260,6 +260,7 @@ def batch_line(args, model_name: str, cfg: dict) -> dict:
     for k in ("qkv", "attention", "o", "down", "head"):
         kus, wus, _ = e.time_kernel(k, args.kernel_iters, batch=B)
         others[k] = {"kernel_us": round(kus, 2), "wall_us": round(wus, 2)}
+    others["attention"]["keys_per_sequence"] = e.max_ctx()  # timed at position max_ctx - 1
     print(f"[bench] batched gate_up {avg_us:.2f} us ({achieved:.0f} GB/s), {wall_us:.2f} us per launch with gaps; "
           f"others {others}", file=sys.stderr, flush=True)
     if args.calibrate_copy:
@@ -464,6 +465,7 @@ def main():
     for k in ("qkv", "attention", "o", "down", "head"):
         kus, wus, _ = e.time_kernel(k, args.kernel_iters)
         others[k] = {"kernel_us": round(kus, 2), "wall_us": round(wus, 2)}
+    others["attention"]["keys"] = e.max_ctx()  # timed at position max_ctx - 1
     print(f"[bench] gate_up {avg_us:.2f} us ({achieved:.0f} GB/s), {wall_us:.2f} us per launch with gaps; "
           f"others {others}", file=sys.stderr, flush=True)
 

@@ -427,8 +427,9 @@ x0ne_status x0ne_engine_page(const x0ne_engine* e, uint64_t i, uint32_t* out);
    warm-up round. kernel_us: the average duration of one launch's kernels, from the start and
    stop events hipExtLaunchKernel records at the kernel's own begin and end (the figure a kernel
    trace reports); wall_us: the average time per launch between events around the whole run,
-   gaps between launches included (either pointer may be NULL). Client bytes are zeroed
-   afterwards. */
+   gaps between launches included (either pointer may be NULL). The attention runs with every
+   sequence at position max_ctx - 1, the longest context the engine holds. Client bytes are
+   zeroed afterwards. */
 typedef enum {
     X0NE_KERNEL_QKV = 0,
     X0NE_KERNEL_ATTENTION = 1,

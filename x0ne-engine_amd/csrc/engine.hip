@@ -2482,6 +2482,14 @@ x0ne_status time_kernel(x0ne_engine* e, uint32_t which, uint32_t batch, uint32_t
             default: return launch_head(e);
         }
     };
+    // The attention is timed at the longest context the engine holds: every sequence at
+    // position max_ctx - 1 (the client state, zeroed between calls, would leave it at 1 key).
+    if (which == X0NE_KERNEL_ATTENTION) {
+        const std::vector<uint32_t> at(batch > 0 ? batch : 1, (uint32_t)(e->max_ctx - 1));
+        X0NE_HIP(hipMemcpyAsync(e->d(e->pos), at.data(), at.size() * 4, hipMemcpyHostToDevice, e->gpu->stream),
+                 "timing position");
+        X0NE_HIP(hipStreamSynchronize(e->gpu->stream), "timing position");
+    }
     // Layer 0's QKV kernel also reads the embedding; the others are timed.
     const uint64_t per = which == X0NE_KERNEL_HEAD ? 1
                          : which == X0NE_KERNEL_QKV ? (e->c.layers > 1 ? e->c.layers - 1 : 1)

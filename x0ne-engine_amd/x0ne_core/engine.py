@@ -309,7 +309,8 @@ class Engine:
         """One decode-step kernel alone, `iters` rounds over every layer, launched back to back on
         the engine's stream: (average kernel duration in microseconds from the start/stop events
         hipExtLaunchKernel records, average wall time per launch with the gaps, launches).
-        batch > 0: the batched step's kernel at that many sequences."""
+        batch > 0: the batched step's kernel at that many sequences. The attention runs with
+        every sequence at position max_ctx - 1."""
         kern, wall, n = C.c_double(), C.c_double(), C.c_uint64()
         if batch:
             check(lib().x0ne_engine_time_batch_kernel(self.h, self.KERNELS[which], batch, iters, C.byref(kern),
