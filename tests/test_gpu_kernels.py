@@ -428,6 +428,46 @@ def test_balanced_few_row_gemm_is_the_oracle_and_the_same_bits_every_time(kernel
     assert (f1[0].view(np.uint32) == f[0].view(np.uint32)).all(), f"{what}: row 0 alone"
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_the_f64_gemm_is_the_exact_sum_of_the_products(kernels, seed):
+    """The exact mode's projection (x0ne_gemm_f64_t*_bf16): each output is the f64 sum of its
+    exact bf16 products, rounded to f32 (and the bf16 output that f32 rounded). Against the
+    exactly rounded sum (math.fsum): equal in f32 but where the f64 sums' own rounding (at most
+    cols x 2^-53 of the sum of the magnitudes) reaches an f32 rounding boundary. Every tile width,
+    K cut into slices (more slices than steps too), K tails, rows and tokens past a tile's edge,
+    zeros and denormals among the values."""
+    import math
+    rng = O.Rng(2000 + seed)
+    n = rng.pick([1, 5, 16, 17, 33, 70])
+    rows = rng.pick([1, 16, 63, 200])
+    cols = rng.pick([8, 40, 264, 1032])
+    tt = rng.pick([1, 2, 4])
+    ks = rng.pick([1, 1, 3, 16])
+    scale = rng.pick([1e-2, 1.0])
+    w = bf16s_with_edges(rng, rows * cols, scale)
+    x = bf16s_with_edges(rng, n * cols, scale)
+    what = f"f64 gemm seed {seed} {n}x{rows}x{cols} tiles {tt} K slices {ks}"
+    f = kernels.gemm_f64(bf16_bits(w), rows, cols, bf16_bits(x), n, True, tt, ks)
+    b = kernels.gemm_f64(bf16_bits(w), rows, cols, bf16_bits(x), n, False, tt, ks)
+    assert (b == bf16_bits(f).reshape(b.shape)).all(), f"{what}: bf16 is the f32 rounded"
+    W = w.astype(np.float64).reshape(rows, cols)
+    X = x.astype(np.float64).reshape(n, cols)
+    equal = 0
+    for t in range(n):
+        for r in range(rows):
+            p = X[t] * W[r]
+            exact = math.fsum(p)
+            got = float(f[t, r])
+            want = float(np.float32(exact))
+            if got == want or (got != got and want != want):
+                equal += 1
+                continue
+            bound = cols * 2.0 ** -53 * float(np.abs(p).sum())
+            assert abs(got - exact) <= abs(want - exact) + bound + np.spacing(np.float32(abs(exact))), \
+                f"{what}: token {t} row {r}: {got!r} against {want!r}"
+    assert equal >= 0.999 * n * rows, f"{what}: {equal} of {n * rows} equal"
+
+
 @pytest.mark.parametrize("rows,cols", [(16, 8), (48, 40), (32, 1000), (1024, 4096), (17, 8), (16, 12)])
 def test_panel_copy_is_the_panel_layout(kernels, rows, cols):
     """x0ne_panel_bf16 (the load-time copy of a batched engine's weights) writes the host's panel
@@ -650,6 +690,37 @@ def test_exact_attention_is_the_f64_oracle_bit_for_bit(kernels, qh, kvh):
         differ += int((out != want).sum())
     print(f"MEASURE exact attention {qh}/{kvh}: {differ} of {total} outputs differ from the f64 oracle's bits")
     assert differ == 0
+
+
+@pytest.mark.parametrize("qh,kvh", [(1, 1), (2, 1), (16, 8), (32, 8), (64, 8)])
+def test_exact_prefill_attention_is_the_f64_oracle_bit_for_bit(kernels, qh, kvh):
+    """The exact mode's causal prefill (x0ne_attention_prefill_exact_g*_bf16: f64 scores,
+    softmax and sums for every row of a pass) gives the bits of the f64 oracle's attention
+    rounded f64 -> f32 -> bf16 for each row, whole and from a chunk boundary, over pages in a
+    shuffled order, across block boundaries of rows and tiles of keys."""
+    h = H(qh, kvh)
+    rng = O.Rng(520 + qh)
+    total = differ = 0
+    for t, pos0 in [(1, 0), (2, 0), (17, 0), (64, 0), (65, 0), (130, 0), (130, 1), (130, 64), (513, 0),
+                    (513, 448), (1025, 1000), (4097, 3990)]:
+        q = rng.bf16s((t - pos0) * h.q_dim, 3.0)
+        k = rng.bf16s(t * h.kv_dim, 3.0)
+        v = bf16s_with_edges(rng, t * h.kv_dim, 4.0)
+        v[~np.isfinite(v)] = 0.0
+        m = t - pos0
+        rows = list(range(m)) if m <= 130 else sorted(set([0, 1, m - 1, m // 2] + [rng.below(m) for _ in range(6)]))
+        pages = (t + 15) // 16
+        page_of = [int(p) for p in np.random.default_rng(t).permutation(pages + 2)[:pages]]
+        got = kernels.attention_prefill_at(bf16_bits(q), bf16_bits(k), bf16_bits(v), t, pos0, h, rows,
+                                           page_of=page_of, exact=True)
+        want = O.attention_rows(q, k, v, pos0, qh, kvh, 128, rows)
+        for r, g, w in zip(rows, got, want):
+            wb = bf16_bits(w)
+            total += wb.size
+            bad = int((g != wb).sum())
+            differ += bad
+            assert bad == 0, f"exact prefill {qh}/{kvh} t {t} pos0 {pos0} row {r}: {bad} outputs differ"
+    print(f"MEASURE exact prefill attention {qh}/{kvh}: {differ} of {total} outputs differ from the f64 oracle's bits")
 
 
 def test_decode_attention_on_one_key_a_dominant_key_and_equal_keys(kernels):

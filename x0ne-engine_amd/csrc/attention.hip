@@ -1643,6 +1643,216 @@ X0NE_PREFILL_GROUP(2)
 X0NE_PREFILL_GROUP(4)
 X0NE_PREFILL_GROUP(8)
 
+// ---- causal prefill in the exact mode (f64 scores, softmax and sums) ----
+//
+// The exact mode's prefill passes: the arithmetic of the exact decode kernel (exact_block: exact
+// bf16 x bf16 products summed in f64, the f64 scale 1/sqrt(128), an f64 softmax with the maximum
+// subtracted, f64 weighted V sums, the result rounded f64 -> f32 -> bf16) for every row of the
+// pass, on the vector units (MI355X runs f64 on the vector units at its f64 matrix rate). Block
+// (kv head kh, row block) serves 64 columns (column c: row r0 + c / G, head kh G + c % G), 8
+// to each of its 8 wavefronts; the keys pass in tiles of 64 staged in LDS once per block (K swizzled by key,
+// V dim-major swizzled by dim, so no two lanes of a read meet in a bank group), the next tile's
+// loads in flight while one is summed, and the 64 columns' q (as f64) stay in LDS:
+//  - scores: lane l takes key l of the tile and, 8 dims at a time, adds its exact products
+//    with each of the wavefront's 8 q columns (read by every lane at once) in dim order;
+//  - the online softmax per column over the tile's 64 keys (maxima and sums by butterflies);
+//  - weighted sums: lane l owns dims l and l + 64 of the 8 columns and adds weight x value
+//    over the tile's keys in key order (weights through LDS, V 8 keys at a time).
+// Keys at or past a column's own position + 1 score -inf; V of keys at or past the block's
+// context is zeroed in LDS (its weight is 0, and 0 times a value that is not a number would
+// not be). Each output depends on its column's own inputs and the fixed order above.
+namespace {
+
+constexpr uint32_t PX_COLS = X0NE_PREFILL_EXACT_COLS;       // columns per block
+constexpr uint32_t PX_BLOCK = X0NE_PREFILL_EXACT_THREADS;
+constexpr uint32_t PX_WAVES = PX_BLOCK / 64;                // wavefronts per block
+constexpr uint32_t PX_WC = PX_COLS / PX_WAVES;              // columns per wavefront
+
+struct PrefillExactShared {
+    double qd[PX_COLS][X0NE_HEAD_DIM];
+    alignas(16) bf16_t k[X0NE_SPLIT_TILE * X0NE_HEAD_DIM];  // [key][16 chunks of 8 dims], chunk c at c ^ (key % 16)
+    alignas(16) bf16_t v[X0NE_HEAD_DIM * X0NE_SPLIT_TILE];  // [dim][8 chunks of 8 keys], chunk c at c ^ (dim % 8)
+    double p[PX_WAVES][PX_WC][X0NE_SPLIT_TILE];
+};
+
+template <int G>
+__device__ __forceinline__ void prefill_exact_block(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache,
+                                                    const bf16_t* __restrict__ v_cache,
+                                                    const uint32_t* __restrict__ pages, bf16_t* __restrict__ out,
+                                                    uint32_t p0, uint32_t rows, uint32_t q_heads, uint32_t kv_heads,
+                                                    uint32_t max_ctx, PrefillExactShared& sh) {
+    constexpr uint32_t RB = PX_COLS / G;
+    const uint32_t kh = blockIdx.x, r0 = blockIdx.y * RB;
+    if (kh >= kv_heads || q_heads != (uint32_t)G * kv_heads || r0 >= rows || max_ctx == 0 || blockDim.x != PX_BLOCK)
+        return;  // block-uniform
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t ctx = min(p0 + min(r0 + RB, rows), max_ctx);  // keys the block reads
+    const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
+    const uint32_t npages = (ctx + X0NE_PAGE - 1) / X0NE_PAGE;
+    // q of the block's columns as f64 (a column past the rows: zeros).
+    for (uint32_t i = t; i < PX_COLS * X0NE_HEAD_DIM; i += PX_BLOCK) {
+        const uint32_t c = i / X0NE_HEAD_DIM, d = i % X0NE_HEAD_DIM, r = r0 + c / G;
+        sh.qd[c][d] = r < rows ? (double)bf2f(q[((size_t)r * q_heads + kh * G + c % G) * X0NE_HEAD_DIM + d]) : 0.0;
+    }
+    // The wavefront's columns: their limits (keys below p0 + row + 1; a column past the rows
+    // attends key 0 only and is not written).
+    uint32_t lim[PX_WC];
+#pragma unroll
+    for (int j = 0; j < (int)PX_WC; ++j) {
+        const uint32_t r = r0 + (PX_WC * wave + j) / G;
+        lim[j] = r < rows ? min(p0 + r + 1, max_ctx) : 1u;
+    }
+    // A tile's K chunk i (i = t + 512 j): key i / 16, dims 8 (i % 16) ..; V chunk i: dim i / 8,
+    // keys 8 (i % 8) .. of the tile.
+    constexpr int J = X0NE_SPLIT_TILE * X0NE_HEAD_DIM / 8 / PX_BLOCK;
+    const auto kres = plane_rsrc(k_cache, OFF_NONE), vres = plane_rsrc(v_cache, OFF_NONE);
+    uint4 kr[J], vr[J];
+    auto fetch = [&](uint32_t tile) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t i = t + PX_BLOCK * j;
+            const uint32_t key = X0NE_SPLIT_TILE * tile + i / 16, kp = key / X0NE_PAGE;
+            const uint32_t pb = (kp < npages ? pages[kp] : 0u) * kv_heads + kh;
+            kr[j] = bload16(kres, kp < npages ? ((pb * X0NE_PAGE + key % X0NE_PAGE) * X0NE_HEAD_DIM + 8 * (i % 16)) * 2
+                                              : OFF_NONE);
+            const uint32_t d = i / 8, vkey = X0NE_SPLIT_TILE * tile + 8 * (i % 8), vp = vkey / X0NE_PAGE;
+            const uint32_t vb = (vp < npages ? pages[vp] : 0u) * kv_heads + kh;
+            vr[j] = bload16(vres, vp < npages ? ((vb * X0NE_HEAD_DIM + d) * X0NE_PAGE + vkey % X0NE_PAGE) * 2 : OFF_NONE);
+        }
+    };
+    auto stash = [&](uint32_t tile) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t i = t + PX_BLOCK * j, key = i / 16, kc = i % 16;
+            *reinterpret_cast<uint4*>(&sh.k[key * X0NE_HEAD_DIM + 8 * (kc ^ (key % 16))]) = kr[j];
+            const uint32_t d = i / 8, vc = i % 8, key0 = X0NE_SPLIT_TILE * tile + 8 * vc;
+            const uint32_t valid = key0 >= ctx ? 0u : min(ctx - key0, 8u);
+            uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w4[e] &= (2 * e + 1 < (int)valid ? 0xFFFF0000u : 0u) | (2 * e < (int)valid ? 0xFFFFu : 0u);
+            *reinterpret_cast<uint4*>(&sh.v[d * X0NE_SPLIT_TILE + 8 * (vc ^ (d % 8))]) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+    };
+    const double scale = 1.0 / sqrt((double)X0NE_HEAD_DIM);
+    double m[PX_WC], l[PX_WC], o[PX_WC][2];
+#pragma unroll
+    for (int j = 0; j < (int)PX_WC; ++j) {
+        m[j] = -INFINITY;
+        l[j] = 0.0;
+        o[j][0] = o[j][1] = 0.0;
+    }
+    fetch(0);
+    for (uint32_t tile = 0; tile < ntiles; ++tile) {
+        __syncthreads();  // the tile before is summed (and, first time round, q is in LDS)
+        stash(tile);
+        if (tile + 1 < ntiles) fetch(tile + 1);  // block-uniform; in flight while this tile is summed
+        __syncthreads();
+        // Scores of key `lane` against the wavefront's 8 columns, 8 dims at a time.
+        const uint32_t key = X0NE_SPLIT_TILE * tile + lane;
+        double sc[PX_WC];
+#pragma unroll
+        for (int j = 0; j < (int)PX_WC; ++j) sc[j] = 0.0;
+        for (uint32_t kc = 0; kc < X0NE_HEAD_DIM / 8; ++kc) {
+            const uint4 kv = *reinterpret_cast<const uint4*>(&sh.k[lane * X0NE_HEAD_DIM + 8 * (kc ^ (lane % 16))]);
+            const uint32_t u[4] = {kv.x, kv.y, kv.z, kv.w};
+            double kd[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kd[2 * e] = (double)bf_lo(u[e]);
+                kd[2 * e + 1] = (double)bf_hi(u[e]);
+            }
+#pragma unroll
+            for (int j = 0; j < (int)PX_WC; ++j) {
+                const double* qc = &sh.qd[PX_WC * wave + j][8 * kc];
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const double2 qq = *reinterpret_cast<const double2*>(qc + e);
+                    sc[j] = fma(qq.x, kd[e], sc[j]);
+                    sc[j] = fma(qq.y, kd[e + 1], sc[j]);
+                }
+            }
+        }
+        // The online softmax per column; the weights to LDS for the weighted sums.
+        double al[PX_WC];
+#pragma unroll
+        for (int j = 0; j < (int)PX_WC; ++j) {
+            const double s = key < lim[j] ? sc[j] * scale : -INFINITY;
+            double mx = s;
+#pragma unroll
+            for (int o2 = 1; o2 < 64; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
+            const double mn = fmax(m[j], mx);  // key 0 is in every column's first tile: mn is finite
+            al[j] = exp(m[j] - mn);
+            const double pr = exp(s - mn);
+            double ps = pr;
+#pragma unroll
+            for (int o2 = 1; o2 < 64; o2 <<= 1) ps += __shfl_xor(ps, o2, 64);
+            l[j] = l[j] * al[j] + ps;
+            m[j] = mn;
+            sh.p[wave][j][lane] = pr;
+        }
+        wave_lds_sync();
+        // Weighted V sums: dims lane and lane + 64, the keys in order, 8 at a time.
+#pragma unroll
+        for (int j = 0; j < (int)PX_WC; ++j) {
+            o[j][0] *= al[j];
+            o[j][1] *= al[j];
+        }
+        for (int vc = 0; vc < 8; ++vc) {
+            const uint4 a = *reinterpret_cast<const uint4*>(&sh.v[lane * X0NE_SPLIT_TILE + 8 * (vc ^ (lane % 8))]);
+            const uint4 b = *reinterpret_cast<const uint4*>(&sh.v[(lane + 64) * X0NE_SPLIT_TILE + 8 * (vc ^ (lane % 8))]);
+            const uint32_t ua[4] = {a.x, a.y, a.z, a.w}, ub[4] = {b.x, b.y, b.z, b.w};
+            double v0[8], v1[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v0[2 * e] = (double)bf_lo(ua[e]);
+                v0[2 * e + 1] = (double)bf_hi(ua[e]);
+                v1[2 * e] = (double)bf_lo(ub[e]);
+                v1[2 * e + 1] = (double)bf_hi(ub[e]);
+            }
+#pragma unroll
+            for (int j = 0; j < (int)PX_WC; ++j) {
+                const double* pj = &sh.p[wave][j][8 * vc];
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const double2 pp = *reinterpret_cast<const double2*>(pj + e);
+                    o[j][0] = fma(pp.x, v0[e], o[j][0]);
+                    o[j][1] = fma(pp.x, v1[e], o[j][1]);
+                    o[j][0] = fma(pp.y, v0[e + 1], o[j][0]);
+                    o[j][1] = fma(pp.y, v1[e + 1], o[j][1]);
+                }
+            }
+        }
+        wave_lds_sync();  // the next tile rewrites the weights
+    }
+#pragma unroll
+    for (int j = 0; j < (int)PX_WC; ++j) {
+        const uint32_t c = PX_WC * wave + j, r = r0 + c / G;
+        if (r >= rows) continue;
+        bf16_t* op = out + ((size_t)r * q_heads + kh * G + c % G) * X0NE_HEAD_DIM;
+        op[lane] = f2bf((float)(o[j][0] / l[j]));
+        op[lane + 64] = f2bf((float)(o[j][1] / l[j]));
+    }
+}
+
+}  // namespace
+
+// x0ne_attention_prefill_exact_g{G}_bf16: the causal prefill of x0ne_attention_prefill_bf16
+// (same arguments; `scale` unused: the f64 1/sqrt(128)) in the exact mode's arithmetic, for G q
+// heads per kv head; grid (kv_heads, ceil(rows / (64 / G))), block 512.
+#define X0NE_PREFILL_EXACT(G)                                                                                      \
+    extern "C" __global__ void __launch_bounds__(PX_BLOCK) x0ne_attention_prefill_exact_g##G##_bf16(              \
+        const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \
+        const uint32_t* __restrict__ pages, bf16_t* __restrict__ out, const uint32_t* __restrict__ pos0,          \
+        uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale) {                       \
+        __shared__ PrefillExactShared sh;                                                                          \
+        prefill_exact_block<G>(q, k_cache, v_cache, pages, out, pos0[0], rows, q_heads, kv_heads, max_ctx, sh);     \
+    }
+X0NE_PREFILL_EXACT(1)
+X0NE_PREFILL_EXACT(2)
+X0NE_PREFILL_EXACT(4)
+X0NE_PREFILL_EXACT(8)
+
 namespace {
 
 // One q head per block (group sizes without a grouped kernel, the per-head witness, prefill):

@@ -347,6 +347,148 @@ extern "C" __global__ void __launch_bounds__(512)
     few_bal<8, 6, 8>(w, x, y, rows, cols, n, flags, T, ws, cnt, stash);
 }
 
+// ---- exact sums: Y[n][rows] = X[n][cols] W^T, every product summed in f64 ----
+// The exact mode's prefill passes (the f64 sums of the exact GEMV, gemv.hip, over many rows):
+// W [rows][cols] and X [n][cols] bf16 row-major, the products exact on the f64 matrix cores
+// (v_mfma_f64_16x16x4_f64, W the A operand: 16 features x 4 k; X the B operand: 4 k x 16
+// tokens), f64 accumulators, and Y = bf16(f32(sum)) or f32(sum): the exact GEMV's rounding.
+//  - A wavefront owns 16 TF features x 16 TT tokens over all of K and works alone (no LDS, no
+//    barrier): at 64 cycles per product on MI355X the matrix cores, not the loads, bound it, so
+//    its operands come straight from memory (the L2), one step of 32 columns ahead.
+//  - In a step lane l loads 16 bytes, columns k0 + 8 (l / 16) .. + 7, of W row 16 f + l % 16
+//    and of X row 16 t + l % 16; product e (0..7) of the step feeds element e of both, so lane
+//    group l / 16 supplies column k0 + 8 (l / 16) + e and each product sums 4 columns.
+//  - Each output is summed in a fixed order (steps, then products within a step, then the
+//    product's own 4 columns): the same bits from call to call, within f64 rounding of the
+//    oracle's sequential sum.
+//  - A wavefront's steps run one after the other (8 x 16 products of 64 cycles per step at
+//    64 x 64 outputs), so a launch of few tiles (a short prompt) is latency-bound: with ks > 1
+//    the steps are cut into ks equal runs, wavefront (tile, slice) writes its f64 partial sums
+//    to ws[slice][token][feature], and x0ne_gemm_f64_reduce adds the slices in slice order.
+// Wavefronts are numbered tokens fastest, then slices, so neighbouring wavefronts share W rows.
+namespace {
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <int TF, int TT>
+__device__ __forceinline__ void gemm_f64(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
+                                         void* __restrict__ y, uint32_t rows, uint32_t cols, uint32_t n,
+                                         uint32_t out_f32, uint32_t ks, double* __restrict__ ws) {
+    const uint32_t lane = threadIdx.x & 63, V = blockDim.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tiles_t = (n + 16 * TT - 1) / (16 * TT), tiles_f = (rows + 16 * TF - 1) / (16 * TF);
+    const uint32_t id = blockIdx.x * V + wave;
+    if (cols % 8 != 0 || out_f32 > 1 || ks == 0 || (ks > 1 && ws == nullptr) ||
+        (uint64_t)id >= (uint64_t)tiles_f * tiles_t * ks)
+        return;  // wavefront-uniform; no barrier
+    const uint32_t tile = id / (tiles_t * ks) * tiles_t + id % tiles_t, slice = id / tiles_t % ks;
+    const uint32_t ft = tile / tiles_t, tt = tile % tiles_t, r = lane & 15, q = lane >> 4;
+    const auto wr = rsrc(w, (uint64_t)rows * cols * 2);
+    const auto xr = rsrc(x, (uint64_t)n * cols * 2);
+    f64x4 acc[TF][TT];
+#pragma unroll
+    for (int f = 0; f < TF; ++f)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[f][t] = f64x4{0.0, 0.0, 0.0, 0.0};
+    uint4 a[2][TF], b[2][TT];
+    const uint32_t all = (cols + 31) / 32, s_lo = all * slice / ks, steps = all * (slice + 1) / ks;
+    auto load = [&](int buf, uint32_t s) {
+        const uint32_t k = 32 * s + 8 * q;
+        const bool in = s < steps && k < cols;  // a K tail: pieces past the row read zeros
+#pragma unroll
+        for (int f = 0; f < TF; ++f) {
+            const uint32_t row = 16 * (TF * ft + f) + r;
+            a[buf][f] = bload<>(wr, in && row < rows ? (row * cols + k) * 2 : OFF_NONE);
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const uint32_t tok = 16 * (TT * tt + t) + r;
+            b[buf][t] = bload<>(xr, in && tok < n ? (tok * cols + k) * 2 : OFF_NONE);
+        }
+    };
+    auto elem = [](const uint4& v, int e) -> double {
+        const uint32_t u = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+        return (double)((e & 1) ? bf_hi(u) : bf_lo(u));
+    };
+    auto step = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            double av[TF], bv[TT];
+#pragma unroll
+            for (int f = 0; f < TF; ++f) av[f] = elem(a[buf][f], e);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) bv[t] = elem(b[buf][t], e);
+#pragma unroll
+            for (int f = 0; f < TF; ++f)
+#pragma unroll
+                for (int t = 0; t < TT; ++t) acc[f][t] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[f], bv[t], acc[f][t], 0, 0, 0);
+        }
+    };
+    // Steps in pairs, so each register set is named statically.
+    load(0, s_lo);
+    for (uint32_t s = s_lo; s < steps; s += 2) {
+        load(1, s + 1);
+        step(0);
+        if (s + 1 >= steps) break;  // wavefront-uniform
+        load(0, s + 2);
+        step(1);
+    }
+    // acc[f][t][i]: feature 16 (TF ft + f) + l / 16 + 4 i, token 16 (TT tt + t) + l % 16 (the
+    // f64 product's result rows interleave over the lane groups).
+#pragma unroll
+    for (int f = 0; f < TF; ++f)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const uint32_t tok = 16 * (TT * tt + t) + r;
+            if (tok >= n) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t feat = 16 * (TF * ft + f) + q + 4 * i;
+                if (feat >= rows) continue;
+                if (ks > 1) {
+                    ws[((size_t)slice * n + tok) * rows + feat] = acc[f][t][i];
+                    continue;
+                }
+                const float v = (float)acc[f][t][i];
+                if (out_f32)
+                    static_cast<float*>(y)[(size_t)tok * rows + feat] = v;
+                else
+                    static_cast<bf16_t*>(y)[(size_t)tok * rows + feat] = f2bf(v);
+            }
+        }
+}
+
+}  // namespace
+
+// x0ne_gemm_f64_t{TT}_bf16: grid ceil(ceil(rows / 64) ceil(n / (16 TT)) ks / V), block 64 V
+// threads (any V); cols a multiple of 8; W and X below 4 GiB - 16 bytes; out_f32 0 (bf16 Y) or
+// 1 (f32 Y); ks 1 (Y written) or more (the partial sums into ws: [ks][n][rows] f64, then
+// x0ne_gemm_f64_reduce).
+#define X0NE_GEMM_F64(NAME, TT)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(256)                                                              \
+        NAME(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, uint32_t rows,      \
+             uint32_t cols, uint32_t n, uint32_t out_f32, uint32_t ks, double* __restrict__ ws) {                 \
+        gemm_f64<4, TT>(w, x, y, rows, cols, n, out_f32, ks, ws);                                                  \
+    }
+X0NE_GEMM_F64(x0ne_gemm_f64_t1_bf16, 1)
+X0NE_GEMM_F64(x0ne_gemm_f64_t2_bf16, 2)
+X0NE_GEMM_F64(x0ne_gemm_f64_t4_bf16, 4)
+
+// x0ne_gemm_f64_reduce: y[t][f] = the f32 (out_f32 1) or bf16 of the f32 of sum over slices 0 ..
+// ks - 1, in that order, of ws[slice][t][f] (f64); grid ceil(n rows / 256), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_gemm_f64_reduce(const double* __restrict__ ws, void* __restrict__ y, uint32_t rows, uint32_t n, uint32_t ks,
+                         uint32_t out_f32) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x, total = (uint64_t)rows * n;
+    if (i >= total || ks == 0 || out_f32 > 1) return;
+    double sum = ws[i];
+    for (uint32_t s = 1; s < ks; ++s) sum += ws[(uint64_t)s * total + i];
+    if (out_f32)
+        static_cast<float*>(y)[i] = (float)sum;
+    else
+        static_cast<bf16_t*>(y)[i] = f2bf((float)sum);
+}
+
 // x0ne_panel_bf16: a row-major [rows][cols] bf16 matrix copied into 16-row panels (element (r, k)
 // at panel_index(r, k, cols)), one 16-byte chunk per thread in destination order, so the writes
 // are contiguous; grid ceil(rows cols / 8 / 256), block 256. rows a multiple of 16 and cols of 8,

@@ -80,6 +80,20 @@ X0NE_DECLARE_PREFILL_GROUP(2)
 X0NE_DECLARE_PREFILL_GROUP(4)
 X0NE_DECLARE_PREFILL_GROUP(8)
 #undef X0NE_DECLARE_PREFILL_GROUP
+// x0ne_attention_prefill_exact_g{G}_bf16: the exact mode's causal prefill; grid (kv_heads,
+// ceil(rows / (X0NE_PREFILL_EXACT_COLS / G))), block X0NE_PREFILL_EXACT_THREADS (a block of
+// another size does nothing).
+#define X0NE_PREFILL_EXACT_COLS 64
+#define X0NE_PREFILL_EXACT_THREADS 512
+#define X0NE_DECLARE_PREFILL_EXACT(G)                                                                            \
+    __global__ void x0ne_attention_prefill_exact_g##G##_bf16(                                                    \
+        const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache, const uint32_t* pages, bf16_t* out,       \
+        const uint32_t* pos0, uint32_t rows, uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);
+X0NE_DECLARE_PREFILL_EXACT(1)
+X0NE_DECLARE_PREFILL_EXACT(2)
+X0NE_DECLARE_PREFILL_EXACT(4)
+X0NE_DECLARE_PREFILL_EXACT(8)
+#undef X0NE_DECLARE_PREFILL_EXACT
 __global__ void x0ne_swiglu_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
 __global__ void x0ne_swiglu_panel_bf16(const bf16_t* gate_up, bf16_t* out, uint32_t inter);
 __global__ void x0ne_argmax_f32(const float* logits, uint32_t n, uint32_t* out);
@@ -109,6 +123,15 @@ X0NE_DECLARE_FEW(t2_r1_swiglu)
 X0NE_DECLARE_FEW(t4_r1)
 X0NE_DECLARE_FEW(t4_r1_swiglu)
 #undef X0NE_DECLARE_FEW
+#define X0NE_DECLARE_GEMM_F64(V)                                                                                 \
+    __global__ void x0ne_gemm_f64_##V##_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols, \
+                                             uint32_t n, uint32_t out_f32, uint32_t ks, double* ws);
+X0NE_DECLARE_GEMM_F64(t1)
+X0NE_DECLARE_GEMM_F64(t2)
+X0NE_DECLARE_GEMM_F64(t4)
+#undef X0NE_DECLARE_GEMM_F64
+__global__ void x0ne_gemm_f64_reduce(const double* ws, void* y, uint32_t rows, uint32_t n, uint32_t ks,
+                                     uint32_t out_f32);
 __global__ void x0ne_gemm_few_bal_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols,
                                        uint32_t n, uint32_t flags, uint32_t T, float* ws, uint32_t* cnt);
 __global__ void x0ne_moe_route_f32(const float* logits, uint32_t experts, uint32_t top_k, uint32_t* ids,

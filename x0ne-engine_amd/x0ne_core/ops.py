@@ -22,6 +22,8 @@ PAGE = 16
 SPLIT_STATE = HEAD_DIM + 4
 PREFILL_COLS = 128  # columns (row, q head) per block of x0ne_attention_prefill_g*_bf16
 PREFILL_THREADS = 256  # its block
+PREFILL_EXACT_COLS = 64  # columns per block of x0ne_attention_prefill_exact_g*_bf16
+PREFILL_EXACT_THREADS = 512  # its block
 NAN_BF16 = 0x7FC0
 
 
@@ -728,6 +730,38 @@ class Kernels:
         y = a.read_array(ys, 0, n * rows, np.float32 if mode == 1 else np.uint16).reshape(n, rows)
         return y, bool((a.read_array(counts, 0, groups, np.uint32) == 0).all())
 
+    def gemm_f64(self, w, rows: int, cols: int, x, n: int, out_f32: bool, tt: int = 0, ks: int = 1) -> np.ndarray:
+        """x0ne_gemm_f64_t{TT}_bf16, the exact mode's projection: Y [n][rows] = X [n][cols] W^T,
+        every bf16 product summed in f64 on the matrix cores, Y f32 or bf16 (bits) of the f32
+        of the sum. tt 0 takes the kernel the engine takes for n (1, 2 or 4 tiles of 16 tokens
+        per wavefront); ks > 1 cuts K into ks slices whose f64 partial sums
+        x0ne_gemm_f64_reduce adds."""
+        if tt == 0:
+            tt = 1 if n <= 16 else 2 if n <= 32 else 4
+        if w.size != rows * cols or x.size != n * cols or cols % 8 or tt not in (1, 2, 4) or n == 0 or rows == 0 \
+                or ks < 1:
+            raise FormatError("gemm_f64: lengths")
+        ob = 4 if out_f32 else 2
+        a = self._arena()
+        ws = a.alloc("w", w.size * 2, Class.WEIGHTS)
+        xs = a.alloc("x", x.size * 2, Class.CLIENT_DATA)
+        ys = a.alloc("y", n * rows * ob, Class.CLIENT_DATA)
+        parts = a.alloc("parts", max(ks, 2) * n * rows * 8, Class.CLIENT_DATA)
+        self._freeze(a)
+        a.scrub_client_data()
+        a.write(ws, 0, np.asarray(w, np.uint16))
+        a.write(xs, 0, np.asarray(x, np.uint16))
+        tiles = -(-rows // 64) * -(-n // (16 * tt))
+        self.gpu.launch(f"x0ne_gemm_f64_t{tt}_bf16", -(-tiles * ks // 4), 256,
+                        [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(cols),
+                         Arg.u32(n), Arg.u32(1 if out_f32 else 0), Arg.u32(ks), Arg.ptr(a.ptr(parts))])
+        if ks > 1:
+            self.gpu.launch("x0ne_gemm_f64_reduce", -(-n * rows // 256), 256,
+                            [Arg.ptr(a.ptr(parts)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(n), Arg.u32(ks),
+                             Arg.u32(1 if out_f32 else 0)])
+        self.gpu.sync()
+        return a.read_array(ys, 0, n * rows, np.float32 if out_f32 else np.uint16).reshape(n, rows)
+
     def panel(self, m, rows: int, cols: int) -> np.ndarray:
         """x0ne_panel_bf16: the [rows][cols] bf16 matrix m copied into 16-row panels on the device
         (flat, rows x cols values; left as the destination held it, 0xFFFF here, when rows is not a
@@ -747,27 +781,34 @@ class Kernels:
         return a.read_array(dst, 0, m.size, np.uint16)
 
     def attention_prefill_at(self, q, k, v, t: int, pos0: int, h: Heads, rows, page_of=None, pool=None,
-                             grouped=False, panel=False):
+                             grouped=False, panel=False, exact=False):
         """Causal attention for positions pos0..t of a t-position cache in one launch at pos0
         (ops.rs:724-775); q holds those t - pos0 rows; returns the rows asked for. grouped: the
         matrix-core kernel for the geometry's group size (x0ne_attention_prefill_g*_bf16);
         panel: its variant writing out in 16-row panels (x0ne_attention_prefill_panel_g*_bf16),
-        read back row-major."""
+        read back row-major; exact: the exact mode's f64 kernel (x0ne_attention_prefill_exact_g*_bf16)."""
         h.check()
         m = t - pos0
         if m <= 0 or q.size != m * h.q_dim or k.size != t * h.kv_dim or v.size != t * h.kv_dim or \
                 any(r >= m for r in rows):
             raise FormatError("attention_prefill_at: lengths")
         g = h.q_heads // h.kv_heads
-        if (grouped or panel) and g not in (1, 2, 4, 8):
+        if (grouped or panel or exact) and g not in (1, 2, 4, 8):
             raise FormatError(f"attention_prefill_at: no grouped kernel for group {g}")
         mp = -(-m // 16) * 16 if panel else m
         a, s = self._kv_arena(q, k, v, t, h, page_of, pool, [("out", mp * h.q_dim * 2)])
         a.write(s["pos"], 0, np.array([pos0], np.uint32))
         kind = "prefill_panel" if panel else "prefill"
-        name, grid = ((f"x0ne_attention_{kind}_g{g}_bf16", (h.kv_heads, (m + PREFILL_COLS // g - 1) // (PREFILL_COLS // g)))
-                      if grouped or panel else ("x0ne_attention_prefill_bf16", (h.q_heads, m)))
-        self.gpu.launch(name, grid, PREFILL_THREADS if grouped or panel else 256,
+        if exact:
+            name, grid, block = (f"x0ne_attention_prefill_exact_g{g}_bf16",
+                                 (h.kv_heads, (m + PREFILL_EXACT_COLS // g - 1) // (PREFILL_EXACT_COLS // g)),
+                                 PREFILL_EXACT_THREADS)
+        elif grouped or panel:
+            name, grid, block = (f"x0ne_attention_{kind}_g{g}_bf16",
+                                 (h.kv_heads, (m + PREFILL_COLS // g - 1) // (PREFILL_COLS // g)), PREFILL_THREADS)
+        else:
+            name, grid, block = "x0ne_attention_prefill_bf16", (h.q_heads, m), 256
+        self.gpu.launch(name, grid, block,
                         [Arg.ptr(a.ptr(s["q"])), Arg.ptr(a.ptr(s["k"])), Arg.ptr(a.ptr(s["v"])),
                          Arg.ptr(a.ptr(s["pt"])), Arg.ptr(a.ptr(s["out"])), Arg.ptr(a.ptr(s["pos"])), Arg.u32(m),
                          Arg.u32(h.q_heads), Arg.u32(h.kv_heads), Arg.u32(t), Arg.f32(attn_scale(h.head_dim))])
@@ -777,11 +818,11 @@ class Kernels:
         return [out[r].copy() for r in rows]
 
     def attention_prefill_rows(self, q, k, v, t: int, h: Heads, rows, page_of=None, pool=None, grouped=False,
-                               panel=False):
+                               panel=False, exact=False):
         """ops.rs:683-722: causal attention over t positions, the rows asked for."""
         if t == 0:
             raise FormatError("attention_prefill_rows: lengths")
-        return self.attention_prefill_at(q, k, v, t, 0, h, rows, page_of, pool, grouped, panel)
+        return self.attention_prefill_at(q, k, v, t, 0, h, rows, page_of, pool, grouped, panel, exact)
 
     # -- swiglu (ops.rs:777-795, :978-1001) --
     def swiglu_rows(self, gate_up, rows: int, panel: bool = False) -> np.ndarray:
