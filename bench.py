@@ -20,10 +20,11 @@ Also printed, in the same JSON line:
   positions) x steps / s, against 8 TB/s.
 - cpu_baseline: the CPU oracle (oracle/, a C restatement of the reference's Rust oracle, f64
   inside) on this host's cores, on a bounded sample of the same workload.
-- prefill: the prompt's time to the first token (greedy_timed's first host time; the f32 path
-  runs the prompt in passes of up to 2048 rows through matrix-core GEMMs and the causal prefill
-  attention, the exact mode one exact step per token; then the LM head on the last row), as
-  tok/s and TFLOP/s against the 2.5 PFLOP/s dense bf16 peak.
+- prefill: the prompt's time to the first token (greedy_timed's first host time: the prompt in
+  passes of up to 2048 rows, the f32 path through bf16 matrix-core GEMMs and the causal prefill
+  attention, the exact mode through the f64-sum GEMM on the f64 matrix cores and the f64 causal
+  attention; then the LM head on the last row), as tok/s and TFLOP/s against the dense peak of
+  the arithmetic it runs in (bf16 2.5 PFLOP/s; the exact mode's f64 78.6 TFLOP/s).
 
 --prompt 8192 --steps 512 is BASELINE.json config 4 (8B, 8192-token prompt, 512 decode steps);
 --model 32b --prompt 512 is config 5's batch-1 case; --model 0.6b --steps 64 config 1's.
@@ -442,9 +443,10 @@ def main():
     P = args.prompt
     pre_flops = 2 * P * L * (h * (qd + 2 * kvd) + qd * h + 3 * h * inter) + 2 * V * h \
         + 4 * cfg["num_attention_heads"] * 128 * L * (P * (P + 1) // 2)
+    pre_peak = 78.6 if exact else 2500.0  # f64 or dense bf16 TFLOP/s of MI355X
     prefill = {"tokens": P, "seconds": round(pre_s, 6), "tok_s": round(P / pre_s, 1),
-               "tflops": round(pre_flops / pre_s / 1e12, 2), "peak_tflops": 2500.0,
-               "frac": round(pre_flops / pre_s / 1e12 / 2500.0, 4), "flops": pre_flops,
+               "tflops": round(pre_flops / pre_s / 1e12, 2), "peak_tflops": pre_peak,
+               "frac": round(pre_flops / pre_s / 1e12 / pre_peak, 4), "flops": pre_flops,
                "timing": "greedy_timed: host time from the call to the first token on the host"}
     print(f"[bench] prefill {P} tokens: {pre_s * 1e3:.2f} ms, {prefill['tok_s']} tok/s, {prefill['tflops']} TFLOP/s",
           file=sys.stderr, flush=True)

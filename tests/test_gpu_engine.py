@@ -87,6 +87,35 @@ def test_every_route_gives_the_oracle_logits_at_every_position(name, make):
 
 
 @pytest.mark.parametrize("chunk", [1 << 30, 16, 7])
+@pytest.mark.parametrize("name,make", FIXTURES, ids=[f[0] for f in FIXTURES])
+def test_the_exact_mode_prefill_passes_give_the_decode_steps_bits(name, make, chunk):
+    """The exact mode's prefill passes (the f64-sum GEMM on the f64 matrix cores, the f64 causal
+    attention) round where its decode step rounds and sum every product in f64, so a prompt's
+    logits through passes of `chunk` rows are the decode route's bit for bit at every position,
+    and both are the oracle's within the model tolerance; the greedy tokens agree."""
+    from x0ne_core import Engine, EngineOptions, Route
+    f = make()
+    e = Engine.load_from(f.cfg.to_json(), {"model.safetensors": f.file},
+                         EngineOptions(max_ctx=96, page_seed=5, prefill_chunk=min(chunk, 96), f64_sums=True))
+    assert e.exact() and f"prefill passes of {min(chunk, 96)} rows" in e.describe(), e.describe()
+    ids = f.tokens(15, 50)
+    want = f.model.logits(ids)
+    every = list(range(len(ids)))
+    passes = e.logits_at(ids, every, Route.PREFILL)
+    steps = e.logits_at(ids, every, Route.DECODE)
+    for p in every:
+        assert_logits(f"{name} exact chunk {chunk} pos {p}", passes[p], want[p])
+        assert (passes[p].view(np.uint32) == steps[p].view(np.uint32)).all(), \
+            f"{name} exact chunk {chunk} pos {p}: the passes' logits differ from the decode steps'"
+    g = e.greedy(ids[:45], 6)
+    assert g.size == 6 and e.client_data_is_zero()
+    want_g = [int(np.argmax(r)) for r in e.logits_at(np.concatenate([ids[:45], g[:-1]]), list(range(44, 50)),
+                                                       Route.DECODE)]
+    assert g.tolist() == want_g, f"{name} exact chunk {chunk}: greedy {g.tolist()} against {want_g}"
+    e.close()
+
+
+@pytest.mark.parametrize("chunk", [1 << 30, 16, 7])
 def test_prefill_passes_across_chunk_boundaries_give_the_oracle_logits(chunk):
     """A prompt cut in passes of `chunk` rows (gpu_engine.rs:229-302): the logits at and around
     every boundary are the oracle's, and the first pass's rows equal those of that pass alone."""
@@ -390,6 +419,10 @@ def check_against_fixture(fx, f64, min_agree, max_ctx_extra=16):
             assert margins[i] < 2 * tol, f"{mode}: step {i} argmax differs at margin {margins[i]:.3e}"
         if f64:
             assert err <= 1e-5 * scales[i], f"f64 sums: step {i}: top logits {err:.3e} from the oracle's"
+    if f64:  # the exact mode's prefill passes: the decode steps' bits
+        passes = e.logits_at(ids, at, Route.PREFILL)
+        for i, (row, row_p) in enumerate(zip(rows, passes)):
+            assert (row.view(np.uint32) == row_p.view(np.uint32)).all(), f"f64 sums: step {i}: passes against steps"
     print(f"MEASURE {fx['what']}, {mode} sums: {agree} of {n} greedy tokens equal to the oracle's "
           f"(first mismatch margin {margins[agree] if agree < n else None}); teacher-forced: top-16 logits within "
           f"{worst:.3f} and log-sum-exp within {worst_lse:.3f} of the 0.05 x row-scale tolerance, argmax differs at "

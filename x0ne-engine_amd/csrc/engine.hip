@@ -15,8 +15,10 @@
 // j + 1 % 2), so no block of a GEMV reads a residual another block has already advanced.
 //
 // A prompt is prefilled in passes of up to `chunk` rows through the MFMA GEMMs and the causal
-// matrix-core attention (prefill_pass); with chunk 1 (the exact mode) it is fed through the
-// decode step one position at a time (a feed kernel puts ids[i] and i where the step reads them).
+// matrix-core attention (prefill_pass); the exact mode's passes sum in f64 on the f64 matrix
+// cores and vector units with the decode step's roundings. With chunk 1 (a MoE engine) it is
+// fed through the decode step one position at a time (a feed kernel puts ids[i] and i where the
+// step reads them).
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -42,6 +44,9 @@ namespace {
 // Prompt rows per prefill pass by default (engine.rs:67 has 512; the matrix-core GEMM's tiles are
 // 128 rows, and 2048 rows keep it compute-bound).
 constexpr uint64_t PREFILL_CHUNK = 2048;
+// The exact mode's prefill GEMM: f64 parts of up to this many bytes (a short pass cuts K into
+// slices to fill the chip).
+constexpr uint64_t EXACT_PARTS_BYTES = 32ull << 20;
 constexpr uint64_t MAX_BATCH = 64;  // the few-row GEMM's most rows
 constexpr uint32_t ARGMAX_SLICES = 64;  // blocks per logits row of the batched step's argmax
 constexpr uint64_t MOE_MAX_EXPERTS = 1024;  // kernels/src/lib.rs:147 (moe.hip)
@@ -430,6 +435,7 @@ struct x0ne_engine {
     // A prefill pass's rows: f32 residual, bf16 delta, normed x, qkv, q, attention, [gate; up], act.
     x0ne_slice p_res{}, p_delta{}, p_x{}, p_qkv{}, p_q{}, p_attn{}, p_gu{}, p_act{};
     x0ne_slice p_tok{};  // a batched engine's pass of several sequences: their ids side by side
+    x0ne_slice p_parts{};  // the exact mode's prefill GEMM: f64 partial sums of K slices
     // The batched step's rows ([max_batch][...]): f32 residual, bf16 delta, normed x, qkv,
     // attention, SwiGLU activation, f32 logits; its split-K state and counters.
     x0ne_slice b_res{}, b_delta{}, b_x{}, b_qkv{}, b_attn{}, b_act{}, b_logits{}, b_state{}, b_counter{}, b_argmax{};
@@ -540,7 +546,7 @@ x0ne_status plan(x0ne_engine* e) {
     // then written in panels too. A batched engine's LM head has a panel copy as well.
     const bool dims16 = c.qkv_rows() % 16 == 0 && c.hidden % 16 == 0 && c.inter % 16 == 0;
     const uint64_t group = c.q_heads / c.kv_heads;
-    e->ppanel = dims16 && e->chunk > 1 && !c.moe && (group == 1 || group == 2 || group == 4 || group == 8);
+    e->ppanel = dims16 && e->chunk > 1 && !c.moe && !e->f64_sums && (group == 1 || group == 2 || group == 4 || group == 8);
     e->hpanel = dims16 && e->max_batch > 1 && c.vocab % 16 == 0;
     e->wpanel = e->ppanel || (dims16 && e->max_batch > 1);
     if (e->wpanel) {
@@ -595,6 +601,7 @@ x0ne_status plan(x0ne_engine* e) {
         X0NE_TRY(al("prefill_gate_up", n * 2 * c.inter * 2, CD, &e->p_gu));
         X0NE_TRY(al("prefill_act", np * c.inter * 2, CD, &e->p_act));
         if (e->max_batch > 1) X0NE_TRY(al("prefill_ids", n * 4, CD, &e->p_tok));
+        if (e->f64_sums) X0NE_TRY(al("prefill_f64_parts", EXACT_PARTS_BYTES, CD, &e->p_parts));
     }
     if (e->max_batch > 1) {
         const uint64_t b = e->max_batch, bp = (b + 15) / 16 * 16;  // panels hold whole tiles of 16 rows
@@ -921,9 +928,12 @@ x0ne_status launch_rows(x0ne_engine* e, const void* fn, dim3 grid, dim3 block, v
 
 // Y[n][rows] = X[n][cols] W^T on arena slices (Gpu::gemm, bf16 out). A panel prefill pass
 // (ppanel) passes W's panel copy and X in panels: up to 64 rows the few-row GEMM, more the tiled
-// GEMM. Y is row-major either way.
+// GEMM. The exact mode's: the f64-sum GEMM (its K slices' parts in p_parts). Y is row-major.
 x0ne_status gemm(x0ne_engine* e, x0ne_slice w, x0ne_slice w_panels, uint64_t rows, uint64_t cols, x0ne_slice x,
                  uint64_t n, x0ne_slice y) {
+    if (e->f64_sums)
+        return exact_gemm(e->gpu, e->d(w), rows, cols, e->d(x), n, e->d(y), false, (double*)e->d(e->p_parts),
+                          EXACT_PARTS_BYTES);
     if (!e->ppanel)
         return x0ne_gpu_gemv(e->gpu, (uint64_t)(uintptr_t)e->d(w), rows, cols, (uint64_t)(uintptr_t)e->d(x), n,
                              (uint64_t)(uintptr_t)e->d(y), 0);
@@ -988,6 +998,13 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
                           : group == 4 ? (pp ? (const void*)&x0ne_attention_prefill_panel_g4_bf16 : (const void*)&x0ne_attention_prefill_g4_bf16)
                           : group == 8 ? (pp ? (const void*)&x0ne_attention_prefill_panel_g8_bf16 : (const void*)&x0ne_attention_prefill_g8_bf16)
                                        : nullptr;
+    // The exact mode (1, 2, 4 or 8 q heads per kv head, check_config): f64 scores and sums.
+    const void* exact = group == 1   ? (const void*)&x0ne_attention_prefill_exact_g1_bf16
+                        : group == 2 ? (const void*)&x0ne_attention_prefill_exact_g2_bf16
+                        : group == 4 ? (const void*)&x0ne_attention_prefill_exact_g4_bf16
+                        : group == 8 ? (const void*)&x0ne_attention_prefill_exact_g8_bf16
+                                     : nullptr;
+    if (e->f64_sums && !exact) return fail(X0NE_ERR_FORMAT, "exact prefill: a group of " + std::to_string(group));
     for (uint64_t l = 0; l < c.layers; ++l) {
         const LayerW& w = e->L[l];
         X0NE_TRY(norm(w.input_norm));
@@ -1016,7 +1033,11 @@ x0ne_status prefill_pass(x0ne_engine* e, uint64_t pos0, uint64_t n, uint64_t b =
             const void* pos = e->pos_of(b + sq);
             void* args[] = {(void*)&q,  (void*)&kc, (void*)&vc,  (void*)&pt,      (void*)&out, (void*)&pos,
                             (void*)&sn, (void*)&qh, (void*)&kvh, (void*)&max_ctx, (void*)&scale};
-            if (grouped) {
+            if (e->f64_sums) {
+                const uint32_t per = X0NE_PREFILL_EXACT_COLS / group;  // rows per block
+                X0NE_TRY(launch_rows(e, exact, dim3(kvh, (sn + per - 1) / per), dim3(X0NE_PREFILL_EXACT_THREADS), args,
+                                     "exact prefill attention"));
+            } else if (grouped) {
                 const uint32_t per = X0NE_PREFILL_COLS / group;  // rows per block
                 X0NE_TRY(launch_rows(e, grouped, dim3(kvh, (sn + per - 1) / per), dim3(X0NE_PREFILL_THREADS), args,
                                      "prefill attention"));
@@ -1128,7 +1149,7 @@ x0ne_status read_token(x0ne_engine* e, uint32_t* out) {
 
 // A prompt into the cache: passes of up to `chunk` rows, then the last row's logits and argmax
 // (engine.rs:408-425); tokens[0] holds the first generated token and pos the prompt's length.
-// With chunk 1 (the exact mode) one decode step per token.
+// With chunk 1 (a MoE engine) one decode step per token.
 // The passes of sequence b's prompt (n ids, already in its prompt row) and its first token.
 x0ne_status prefill_passes(x0ne_engine* e, size_t n, uint64_t b) {
     size_t start = 0;
@@ -1196,14 +1217,13 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
     e->max_ctx = opts->max_ctx;
     e->page_seed = opts->page_seed;
     e->f64_sums = exact_sums(c, *opts) ? 1 : 0;
-    // The exact mode's sums are the decode GEMV's (f64): its prompts go one step per token.
-    // A MoE engine prefills through the decode route too (engine.rs:322-328).
+    // A MoE engine prefills through the decode route (engine.rs:322-328).
     // A pass holds up to max_ctx rows of one sequence, or of several for a batched engine (its
     // prompts of one length share a pass).
     e->max_batch = opts->max_batch ? opts->max_batch : 1;  // check_config bounded it
-    e->chunk = e->f64_sums || c.moe ? 1
-                                    : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK,
-                                                         opts->max_ctx * e->max_batch);
+    e->chunk = c.moe ? 1
+                     : std::min<uint64_t>(opts->prefill_chunk ? opts->prefill_chunk : PREFILL_CHUNK,
+                                          opts->max_ctx * e->max_batch);
     if (e->chunk == 0) e->chunk = 1;
     e->seq_pages = (e->max_ctx + X0NE_PAGE_C - 1) / X0NE_PAGE_C;
     e->pages = e->max_batch * e->seq_pages;

@@ -101,6 +101,14 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
 // layout X0NE_GEMM_W_PANELS | X0NE_GEMM_X_PANELS names the operands held in 16-row panels.
 x0ne_status tiled_gemm(x0ne_gpu* g, int tile, uint32_t layout, const void* w, uint64_t rows, uint64_t cols,
                        const void* x, uint64_t n, void* y, bool out_f32);
+// Y[n][rows] = X[n][cols] W^T with every product summed in f64 (the exact mode's prefill
+// passes; x0ne_gemm_f64_t*_bf16), Y = bf16(f32(sum)) or f32(sum); W and X row-major. ks K slices
+// (0: picked per shape, up to what ws_bytes of ws holds) summed in slice order by
+// x0ne_gemm_f64_reduce. Launches sharing ws must not overlap.
+constexpr uint32_t EXACT_GEMM_MAX_SLICES = 16;
+constexpr uint32_t EXACT_GEMM_WAVES_PER_CU = 8;
+x0ne_status exact_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
+                       bool out_f32, double* ws, uint64_t ws_bytes, uint32_t ks = 0);
 // Split plan for a geometry (gpu.rs:958-985), P capped at `cap`.
 x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out);
 x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_block, const void* q, const void* k,

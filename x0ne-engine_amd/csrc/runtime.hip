@@ -1,6 +1,7 @@
 // The device, the kernel-launch API, graph capture and the arena: the reference's
 // x0ne-core/runtime/src/{gpu,arena,error}.rs, on the HIP runtime for gfx950.
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -390,6 +391,51 @@ x0ne_status skinny(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, con
     g->counts.gemms++;
     g->counts.launches++;
     X0NE_HIP(x0ne_launch(fn, dim3(blocks_of(rg)), dim3(64 * waves), args, 0, g->stream), "few-row gemm");
+    return X0NE_OK;
+}
+
+x0ne_status exact_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
+                       bool out_f32, double* ws, uint64_t ws_bytes, uint32_t ks) {
+    if (rows == 0 || cols == 0 || n == 0 || cols % 8 != 0 || rows > UINT32_MAX || n > UINT32_MAX ||
+        rows * cols * 2 > GEMM_MAX_BYTES || n * cols * 2 > GEMM_MAX_BYTES || (uintptr_t)w % 16 != 0 ||
+        (uintptr_t)x % 16 != 0 || ks > EXACT_GEMM_MAX_SLICES || (ks > 1 && ws_bytes / 8 / ks / n < rows) ||
+        (ks > 1 && ws == nullptr))
+        return fail(X0NE_ERR_FORMAT, "exact gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
+                                         std::to_string(n) + ", " + std::to_string(ks) + " slices");
+    // Tokens per wavefront: 16 TT, the smallest TT of 1, 2, 4 that covers n (up to 64).
+    const uint32_t tt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
+    const uint64_t tiles = (rows + 63) / 64 * ((n + 16 * tt - 1) / (16 * tt)), steps = (cols + 31) / 32;
+    if (ks == 0) {
+        // A wavefront's steps run back to back on its SIMD's f64 matrix core, so a launch wants
+        // EXACT_GEMM_WAVES_PER_CU wavefronts per CU: fewer tiles than that cut K into slices of
+        // at least 8 steps, as many as the workspace holds.
+        ks = 1;
+        const uint64_t want = (uint64_t)EXACT_GEMM_WAVES_PER_CU * g->cus;
+        if (tiles < want && ws) {
+            uint64_t k = std::min<uint64_t>({(want + tiles - 1) / tiles, EXACT_GEMM_MAX_SLICES, steps / 8,
+                                             ws_bytes / (n * rows * 8)});
+            ks = (uint32_t)std::max<uint64_t>(k, 1);
+        }
+    }
+    const void* fn = tt == 1 ? (const void*)&x0ne_gemm_f64_t1_bf16
+                     : tt == 2 ? (const void*)&x0ne_gemm_f64_t2_bf16
+                               : (const void*)&x0ne_gemm_f64_t4_bf16;
+    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, of = out_f32 ? 1u : 0u, k32 = ks;
+    double* wsp = ks > 1 ? ws : nullptr;
+    void* yp = y;
+    void* args[] = {(void*)&w, (void*)&x, (void*)&yp, (void*)&r32, (void*)&c32, (void*)&n32, (void*)&of, (void*)&k32,
+                    (void*)&wsp};
+    g->counts.gemms++;
+    g->counts.launches++;
+    X0NE_HIP(x0ne_launch(fn, dim3((uint32_t)((tiles * ks + 3) / 4)), dim3(256), args, 0, g->stream), "exact gemm");
+    if (ks > 1) {
+        const double* wsc = wsp;
+        void* rargs[] = {(void*)&wsc, (void*)&yp, (void*)&r32, (void*)&n32, (void*)&k32, (void*)&of};
+        g->counts.launches++;
+        X0NE_HIP(x0ne_launch((const void*)&x0ne_gemm_f64_reduce, dim3((uint32_t)((rows * n + 255) / 256)), dim3(256),
+                             rargs, 0, g->stream),
+                 "exact gemm slices");
+    }
     return X0NE_OK;
 }
 
