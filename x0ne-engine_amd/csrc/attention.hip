@@ -295,6 +295,11 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
     return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
+// One word through the vector memory path: a page-table entry fetched ahead this way is waited
+// for by the in-order vector count, not by the LDS count every LDS read in between waits on.
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
 
 // One wavefront on the matrix cores (v_mfma_f32_16x16x32_bf16; lane l: row or column l % 16,
 // k = 8 (l / 16) .. + 7 of a 32-wide step; result rows 4 (l / 16) .. + 3, column l % 16). The
@@ -681,6 +686,21 @@ __device__ __forceinline__ void rope_rotate_cs(const RopeIn& r, double c, double
     *rb = (float)(nb * c + na * s);
 }
 
+// rope_rotate_cs in two steps: the RMS norm, which does not depend on the position, then the
+// rotation; the same operations in the same order, so the same bits.
+struct RopeNormed {
+    double na, nb;
+};
+__device__ __forceinline__ RopeNormed rope_norm(const RopeIn& r, float eps) {
+    const double ss = wave_sum_d((double)r.a * (double)r.a + (double)r.b * (double)r.b);
+    const double scale = 1.0 / sqrt(ss / (double)X0NE_HEAD_DIM + (double)eps);
+    return {(double)r.a * scale * (double)r.wa, (double)r.b * scale * (double)r.wb};
+}
+__device__ __forceinline__ void rope_turn(const RopeNormed& n, double c, double s, float* ra, float* rb) {
+    *ra = (float)(n.na * c - n.nb * s);
+    *rb = (float)(n.nb * c + n.na * s);
+}
+
 // The angle of lane i is the f32 product pos * inv_freq[i] (invf), its sine and cosine in f64.
 __device__ __forceinline__ void rope_rotate(const RopeIn& r, float invf, uint32_t pos, float eps, float* ra,
                                             float* rb) {
@@ -749,17 +769,28 @@ __device__ __forceinline__ void stash_wave(AttnShared<G, T, V>& sh, const T m[G]
 // The work unit is one 16-key page of one kv head (4 KiB of K rows and 4 KiB of dim-major V).
 // Slices are the split-K slices of the fp32 kernels (split_of: runs of 64-key tiles, P of them);
 // inside a slice the 4 wavefronts take its pages in turn (wavefront w: pages w, w + 4, ...), so a
-// short context spreads over every wavefront of the block. Lanes of a page: for the scores lane
-// (k = l % 16, c = l / 16) holds key k's dims 32c .. 32c + 31 and sums them against the G q heads
-// (f64 FMAs), the four quarters then meet by shuffles; for the weighted sums lane l owns dims l
-// and l + 64 and reads the page's 16 weights per head from LDS. The next page's K and V are in
-// flight while a page is summed, and slice 0 requests its first page-table entry together with
-// pos, so the dependent chain of a short context is pos/page -> K,V -> sums.
+// short context spreads over every wavefront of the block. The products and their sums run on
+// the f64 matrix cores: v_mfma_f64_4x4x4f64 computes 4 blocks b of D[4][4] += A[4][4] B[4][4],
+// lane l = 16 k + 4 b + x holding A_b[x][k], B_b[k][x] and D_b[l / 16][x] (measured on gfx950).
+//  - scores S^T: block b's rows are keys 4 b .. 4 b + 3 of the page, its columns 4 q heads, its
+//    k 4 dims: lane l supplies K[key 4 b + x][dim 32 k + t] at product t (64 contiguous bytes of
+//    its key) and q[head x][dim 32 k + t] (32 f64 values held in registers from the prologue);
+//    32 products over the 128 dims, in 4 interleaved chains of 8 (t % 4) added at the end, leave
+//    lane l with the score of key 4 b + l / 16 for head x;
+//  - the online softmax per head over the lanes of its column (xor 4, 8, 16, 32);
+//  - O += P V: rows are the 4 heads, k 4 keys, block b's columns dims 16 i + 4 b .. + 3 for
+//    product i (0..7): lane l supplies P[head x][key 4 k + s] at step s (through LDS) and
+//    V[key 4 k + s][dim 16 i + 4 b + x] (8 contiguous bytes of each of its 8 dims), and ends
+//    with O[head l / 16][dim 16 i + 4 b + x] in 8 accumulators.
+// A group of 8 q heads runs both sets of 4 columns; of 1 or 2 the columns repeat the heads.
+// The next page's K and V are in flight while a page is summed, its page-table entry one page
+// further ahead (a vector load, so the LDS waits in between do not wait for it); slice 0 requests
+// its first entry together with pos and the RoPE factors before the first page, so the
+// dependent chain of a short context is pos/page -> K,V -> sums.
 
-// The page split of a slice: pages p_begin, p_begin + 4, ... of the slice's run, below npages.
 struct ExactShared {
-    // q heads, bf16-rounded, as f64; the page weights and rescale factors per wavefront; the
-    // new K/V row; the block merge's states; the last block's slice factors.
+    // q heads, bf16-rounded, as f64; the page weights (per wavefront, head, key) and rescale
+    // factors; the new K/V row; the block merge's states; the last block's slice factors.
     double qd[8][X0NE_HEAD_DIM];
     double pw[WAVES][8][X0NE_PAGE];
     double alpha[WAVES][8];
@@ -771,7 +802,7 @@ struct ExactShared {
     uint32_t last;
 };
 
-constexpr uint32_t EXACT_CHUNK = 16;  // slices whose f64 o values the exact merge loads at once
+constexpr uint32_t EXACT_CHUNK = 40;  // slices whose f64 o values the exact merge loads at once
 
 __device__ __forceinline__ void dstate_put(double* p, double v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -780,51 +811,31 @@ __device__ __forceinline__ double dstate_get(const double* p) {
     return __hip_atomic_load(const_cast<double*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Sum over the 4 lane quarters (lane bits 4 and 5) of a G-vector of per-quarter partial dot
-// products. While more than one value is left a step keeps half of them (bit set: the upper
-// half); afterwards plain butterflies. Lane (k, c) ends with the whole score of head
-// quarter_head<G>(c, e) in v[e], e < max(G / 4, 1).
-template <int N, int K>
-__device__ __forceinline__ void quarter_reduce(double* v, uint32_t lane) {
-    if constexpr (K < 4) {
-        return;
-    } else if constexpr (N > 1) {
-        constexpr int H = N / 2;
-        const bool bit = (lane >> K) & 1u;
-#pragma unroll
-        for (int j = 0; j < H; ++j) {
-            const double send = bit ? v[j] : v[j + H];
-            const double keep = bit ? v[j + H] : v[j];
-            v[j] = keep + __shfl_xor(send, 1 << K, 64);
-        }
-        quarter_reduce<H, K - 1>(v, lane);
-    } else {
-        v[0] += __shfl_xor(v[0], 1 << K, 64);
-        quarter_reduce<1, K - 1>(v, lane);
-    }
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
 }
-// Head of value e in lane quarter c after quarter_reduce<G, 5>: the halving steps take lane bit
-// 5 then bit 4 as the high bits of the kept index.
-template <int G>
-__device__ __forceinline__ uint32_t quarter_head(uint32_t c, int e) {
-    if constexpr (G >= 4) return (c * (G / 4)) + (uint32_t)e;
-    else if constexpr (G == 2) return c >> 1;
-    else return 0;
+
+// bf16 element e (0..7) of 8 packed in a uint4, as f64.
+__device__ __forceinline__ double bf_of(const uint4& v, int e) {
+    const uint32_t u = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+    return (double)((e & 1) ? bf_hi(u) : bf_lo(u));
 }
 
 template <int G>
 __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) {
-    constexpr int HPL = G >= 4 ? G / 4 : 1;  // heads whose scores a lane holds
+    constexpr int HS = G > 4 ? G / 4 : 1;  // sets of 4 head columns
     const uint32_t kh = blockIdx.x, y = blockIdx.y, P = a.splits;
     if (P == 0 || P > MERGE_MAX || kh >= a.kv_heads || a.q_heads != (uint32_t)G * a.kv_heads) return;  // uniform
     const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t k = lane & 15, c = lane >> 4;
+    const uint32_t kq = lane >> 4, bq = (lane >> 2) & 3, x = lane & 3;
     const uint32_t h0 = kh * G, q_dim = a.q_heads * X0NE_HEAD_DIM, kv_dim = a.kv_heads * X0NE_HEAD_DIM;
     const uint32_t seq_pages = (a.max_ctx + X0NE_PAGE - 1) / X0NE_PAGE;
 
     // Before pos: the q rows this wavefront ropes (heads wave, wave + 4, ...), in the last
-    // wavefront kv head kh's K and V rows, and in slice 0 the first page's table entry (slice 0's
-    // wavefront w starts at page w whatever the context; clamped inside the table).
+    // wavefront kv head kh's K and V rows, their RMS norms (which do not depend on pos), and in
+    // slice 0 the first page's table entry (slice 0's wavefront w starts at page w whatever the
+    // context; clamped inside the table).
     constexpr int QPW = (G + WAVES - 1) / WAVES;
     RopeIn qin[QPW], kin{};
     bf16_t vrow[2] = {0, 0};
@@ -841,42 +852,17 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         vrow[1] = vs[lane + 64];
     }
     const uint32_t first_entry = y == 0 ? a.pages[min(wave, seq_pages - 1)] : 0u;
+    RopeNormed qnm[QPW], knm{};
+#pragma unroll
+    for (int j = 0; j < QPW; ++j)
+        if (wave + WAVES * j < (uint32_t)G) qnm[j] = rope_norm(qin[j], a.eps);
+    if (wave == WAVES - 1) knm = rope_norm(kin, a.eps);
 
     const uint32_t pos = a.pos[0];
     const uint32_t ctx = min(pos + 1u, a.max_ctx);
     const Split sp = split_of(ctx, P);
     if (y >= sp.active) return;  // block-uniform: a slice past the context
-    const uint32_t npages = (ctx + X0NE_PAGE - 1) / X0NE_PAGE;
-    const uint32_t run_begin = y * sp.per * (X0NE_SPLIT_TILE / X0NE_PAGE);
-    const uint32_t run_end = min((y + 1) * sp.per * (X0NE_SPLIT_TILE / X0NE_PAGE), npages);
-    const uint32_t new_page = pos < a.max_ctx ? pos / X0NE_PAGE : ~0u;
-    const bool owner = new_page >= run_begin && new_page < run_end;
-
-    // Page-table entry and plane byte offsets of page p of this kv head; the K lane chunk is key
-    // k's dims 32c .. + 31, the V lane chunk dims lane and lane + 64 of the page's 16 keys.
-    const auto kr = plane_rsrc(a.k_cache, OFF_NONE), vr = plane_rsrc(a.v_cache, OFF_NONE);
-    const uint32_t page_b = a.kv_heads * X0NE_PAGE * X0NE_HEAD_DIM * 2, head_b = kh * X0NE_PAGE * X0NE_HEAD_DIM * 2;
-    auto entry = [&](uint32_t p) -> uint32_t { return p < run_end ? a.pages[p] : 0u; };
-    auto load_page = [&](uint32_t p, uint32_t pg, uint4 (&kk)[4], uint4 (&vv)[4]) {
-        const bool live = p < run_end;
-        const uint32_t kb = pg * page_b + head_b + k * X0NE_HEAD_DIM * 2 + 64 * c;
-        const uint32_t vb = pg * page_b + head_b + lane * X0NE_PAGE * 2;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kk[j] = bload16(kr, live ? kb + 16 * j : OFF_NONE);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            vv[j] = bload16(vr, live ? vb + 16 * j : OFF_NONE);
-            vv[2 + j] = bload16(vr, live ? vb + 64 * X0NE_PAGE * 2 + 16 * j : OFF_NONE);
-        }
-    };
-    uint32_t p = run_begin + wave;
-    uint4 kc[4], vc[4], kn[4], vn[4];
-    uint32_t pg = y == 0 ? (p < run_end ? first_entry : 0u) : entry(p);
-    load_page(p, pg, kc, vc);
-    uint32_t pg_next = entry(p + WAVES);
-
-    // QK-norm + RoPE (f64, the table's cosine and sine) while the first page is in flight; the
-    // owner's last wavefront writes position pos's K row and V column and keeps them in LDS.
+    // The RoPE factors at pos (the table's below max_ctx, else computed alike) before any page.
     double rc, rs;
     if (pos < a.max_ctx) {
         const double2 cs = *reinterpret_cast<const double2*>(a.rope_cs + 2 * ((size_t)pos * (X0NE_HEAD_DIM / 2) + lane));
@@ -887,19 +873,51 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         rc = cos(angle);
         rs = sin(angle);
     }
+    const uint32_t npages = (ctx + X0NE_PAGE - 1) / X0NE_PAGE;
+    const uint32_t run_begin = y * sp.per * (X0NE_SPLIT_TILE / X0NE_PAGE);
+    const uint32_t run_end = min((y + 1) * sp.per * (X0NE_SPLIT_TILE / X0NE_PAGE), npages);
+    const uint32_t new_page = pos < a.max_ctx ? pos / X0NE_PAGE : ~0u;
+    const bool owner = new_page >= run_begin && new_page < run_end;
+
+    // Page-table entry and plane byte offsets of page p of this kv head: K key 4 bq + x's dims
+    // 32 kq .. + 31 (four 16-byte pieces); V keys 4 kq .. + 3 of dims 16 i + 4 bq + x (8 bytes
+    // each, i = 0..7).
+    const auto kr = plane_rsrc(a.k_cache, OFF_NONE), vr = plane_rsrc(a.v_cache, OFF_NONE);
+    const auto pr_ = plane_rsrc(a.pages, run_end * 4);  // entries past the run read 0
+    const uint32_t page_b = a.kv_heads * X0NE_PAGE * X0NE_HEAD_DIM * 2, head_b = kh * X0NE_PAGE * X0NE_HEAD_DIM * 2;
+    // (kept in a vector register: only the load offsets use it, so nothing waits for it early)
+    auto entry = [&](uint32_t p) -> uint32_t { return bload4(pr_, p < run_end ? 4 * p : OFF_NONE); };
+    auto load_page = [&](uint32_t p, uint32_t pg, uint4 (&kk)[4], uint2 (&vv)[8]) {
+        const bool live = p < run_end;
+        const uint32_t kb = pg * page_b + head_b + (4 * bq + x) * X0NE_HEAD_DIM * 2 + 64 * kq;
+        const uint32_t vb = pg * page_b + head_b + ((4 * bq + x) * X0NE_PAGE + 4 * kq) * 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kk[j] = bload16(kr, live ? kb + 16 * j : OFF_NONE);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vv[i] = bload8(vr, live ? vb + 16 * i * X0NE_PAGE * 2 : OFF_NONE);
+    };
+    uint32_t p = run_begin + wave;
+    uint4 kc[4], kn[4];
+    uint2 vc[8], vn[8];
+    uint32_t pg = y == 0 ? (p < run_end ? first_entry : 0u) : entry(p);
+    load_page(p, pg, kc, vc);
+    uint32_t pg_next = entry(p + WAVES);
+
+    // RoPE while the first page is in flight; the owner's last wavefront writes position pos's K
+    // row and V column and keeps them in LDS.
 #pragma unroll
     for (int j = 0; j < QPW; ++j) {
         const uint32_t g = wave + WAVES * j;
         if (g < (uint32_t)G) {
             float ra, rb;
-            rope_rotate_cs(qin[j], rc, rs, a.eps, &ra, &rb);
+            rope_turn(qnm[j], rc, rs, &ra, &rb);
             sh.qd[g][lane] = (double)bf_round(ra);
             sh.qd[g][lane + 64] = (double)bf_round(rb);
         }
     }
     if (owner && wave == WAVES - 1) {
         float ra, rb;
-        rope_rotate_cs(kin, rc, rs, a.eps, &ra, &rb);
+        rope_turn(knm, rc, rs, &ra, &rb);
         const bf16_t k0 = f2bf(ra), k1 = f2bf(rb);
         const uint32_t at = kv_row(a.pages, pos, kh, a.kv_heads);
         a.k_cache[at + lane] = k0;
@@ -913,141 +931,145 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         sh.vnew[lane + 64] = vrow[1];
     }
     lds_barrier();  // q and the new row in LDS; the page loads stay in flight
+    // This lane's q operand: head column x of each set (a group of 1 or 2 repeats its heads),
+    // dims 32 kq .. + 31.
+    double qv[HS][32];
+#pragma unroll
+    for (int hs = 0; hs < HS; ++hs) {
+        const uint32_t h = G >= 4 ? 4 * hs + x : x % (uint32_t)G;
+#pragma unroll
+        for (int d = 0; d < 32; d += 2) {
+            const double2 v = *reinterpret_cast<const double2*>(&sh.qd[h][32 * kq + d]);
+            qv[hs][d] = v.x;
+            qv[hs][d + 1] = v.y;
+        }
+    }
 
     const double scale = 1.0 / sqrt((double)X0NE_HEAD_DIM);
-    double m[HPL], lsum[HPL], o[G][2];
+    double m[HS], lsum[HS];
+    double o[HS][8];
 #pragma unroll
-    for (int e = 0; e < HPL; ++e) {
-        m[e] = -INFINITY;
-        lsum[e] = 0.0;
+    for (int hs = 0; hs < HS; ++hs) {
+        m[hs] = -INFINITY;
+        lsum[hs] = 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[hs][i] = 0.0;
     }
-#pragma unroll
-    for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = 0.0;
-    double* pw = &sh.pw[wave][0][0];
-    double* alpha_l = &sh.alpha[wave][0];
 
     for (; p < run_end; p += WAVES) {
+        const uint32_t pg_after = entry(p + 2 * WAVES);  // requested before the page it follows
         if (p + WAVES < run_end) load_page(p + WAVES, pg_next, kn, vn);
-        const uint32_t pg_after = entry(p + 2 * WAVES);
         const uint32_t base = p * X0NE_PAGE;
         if (p == new_page) {  // wavefront-uniform: the new row from LDS, not from its write
-            if (k == pos % X0NE_PAGE) {
+            const uint32_t e = pos % X0NE_PAGE;
+            if (4 * bq + x == e) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) kc[j] = *reinterpret_cast<const uint4*>(sh.knew + 32 * c + 8 * j);
+                for (int j = 0; j < 4; ++j) kc[j] = *reinterpret_cast<const uint4*>(sh.knew + 32 * kq + 8 * j);
             }
-            const uint32_t e = pos % X0NE_PAGE, word = (e % 8) / 2, shift = 16 * (e & 1u);
-            const uint32_t keep = shift ? 0x0000FFFFu : 0xFFFF0000u;
+            if (e / 4 == kq) {
+                const uint32_t sel = e % 4, shift = 16 * (sel & 1u), keep = shift ? 0x0000FFFFu : 0xFFFF0000u;
 #pragma unroll
-            for (int dh = 0; dh < 2; ++dh) {
-                const uint32_t val = (uint32_t)sh.vnew[lane + 64 * dh] << shift;
-                uint4& w = vc[2 * dh + e / 8];
-                uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (j == (int)word) u[j] = (u[j] & keep) | val;
-                w = make_uint4(u[0], u[1], u[2], u[3]);
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t val = (uint32_t)sh.vnew[16 * i + 4 * bq + x] << shift;
+                    if (sel < 2)
+                        vc[i].x = (vc[i].x & keep) | val;
+                    else
+                        vc[i].y = (vc[i].y & keep) | val;
+                }
             }
         }
-        // Scores: key k's quarter c against every head, then the quarters summed.
-        double sc[G];
+        // Scores: key 4 bq + l / 16 of the page for head column x of each set.
+        double sc[HS];
         {
-            double kd[32];
+            double acc[HS][4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t u[4] = {kc[j].x, kc[j].y, kc[j].z, kc[j].w};
+            for (int hs = 0; hs < HS; ++hs)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    kd[8 * j + 2 * i] = (double)bf_lo(u[i]);
-                    kd[8 * j + 2 * i + 1] = (double)bf_hi(u[i]);
-                }
+                for (int c4 = 0; c4 < 4; ++c4) acc[hs][c4] = 0.0;
+#pragma unroll
+            for (int d = 0; d < 32; ++d) {
+                const double kd = bf_of(kc[d / 8], d % 8);
+#pragma unroll
+                for (int hs = 0; hs < HS; ++hs)
+                    acc[hs][d % 4] = __builtin_amdgcn_mfma_f64_4x4x4f64(kd, qv[hs][d], acc[hs][d % 4], 0, 0, 0);
             }
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const double* q = &sh.qd[g][32 * c];
-                double s = 0.0;
-#pragma unroll
-                for (int d = 0; d < 32; d += 2) {
-                    const double2 qq = *reinterpret_cast<const double2*>(q + d);
-                    s = fma(qq.x, kd[d], s);
-                    s = fma(qq.y, kd[d + 1], s);
-                }
-                sc[g] = s;
-            }
+            for (int hs = 0; hs < HS; ++hs) sc[hs] = (acc[hs][0] + acc[hs][1]) + (acc[hs][2] + acc[hs][3]);
         }
-        quarter_reduce<G, 5>(sc, lane);
-        // Online softmax of the lane's heads over the page's 16 keys (lane bits 0..3).
-        const bool in = base + k < ctx;
+        // Online softmax per head column over the page's 16 keys (the lanes of column x).
+        const bool in = base + 4 * bq + kq < ctx;
+        double pr[HS];
 #pragma unroll
-        for (int e = 0; e < HPL; ++e) {
-            const double s = in ? sc[e] * scale : -INFINITY;
+        for (int hs = 0; hs < HS; ++hs) {
+            const double s = in ? sc[hs] * scale : -INFINITY;
             double mx = s;
 #pragma unroll
-            for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
-            const double mn = fmax(m[e], mx);  // key `base` is below ctx: mn is finite
-            const double al = exp(m[e] - mn);
-            const double pr = exp(s - mn);
-            lsum[e] = lsum[e] * al + pr;
-            m[e] = mn;
-            const uint32_t g = quarter_head<G>(c, e);
-            if (G >= 4 || (c & (4 / G - 1)) == 0) {
-                pw[g * X0NE_PAGE + k] = pr;
-                if (k == 0) alpha_l[g] = al;
-            }
+            for (int o2 = 4; o2 < 64; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
+            const double mn = fmax(m[hs], mx);  // key `base` is below ctx: mn is finite
+            const double al = exp(m[hs] - mn);
+            pr[hs] = exp(s - mn);
+            lsum[hs] = lsum[hs] * al + pr[hs];
+            m[hs] = mn;
+            sh.pw[wave][4 * hs + x][4 * bq + kq] = pr[hs];
+            if (lane < 4) sh.alpha[wave][4 * hs + x] = al;
         }
         wave_lds_sync();
-        // Weighted V sums: dims lane and lane + 64, keys past ctx taken as 0.
-        double v0[X0NE_PAGE], v1[X0NE_PAGE];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t u0[4] = {vc[j].x, vc[j].y, vc[j].z, vc[j].w};
-            const uint32_t u1[4] = {vc[2 + j].x, vc[2 + j].y, vc[2 + j].z, vc[2 + j].w};
+        // V of keys past ctx taken as 0 (their weight is 0, and 0 times a value that is not a
+        // number would not be); then O rescaled and O += P V.
+        if (base + X0NE_PAGE > ctx) {
+            const uint32_t k0 = base + 4 * kq;
+            const uint32_t valid = k0 >= ctx ? 0u : min(ctx - k0, 4u);
+            const uint32_t mlo = (valid > 1 ? 0xFFFF0000u : 0u) | (valid > 0 ? 0xFFFFu : 0u);
+            const uint32_t mhi = (valid > 3 ? 0xFFFF0000u : 0u) | (valid > 2 ? 0xFFFFu : 0u);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t key = 8 * j + i;
-                const bool ok = base + key < ctx;
-                v0[key] = ok ? (double)((i & 1) ? bf_hi(u0[i / 2]) : bf_lo(u0[i / 2])) : 0.0;
-                v1[key] = ok ? (double)((i & 1) ? bf_hi(u1[i / 2]) : bf_lo(u1[i / 2])) : 0.0;
+                vc[i].x &= mlo;
+                vc[i].y &= mhi;
             }
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const double al = alpha_l[g];
-            double a0 = o[g][0] * al, a1 = o[g][1] * al;
+        for (int hs = 0; hs < HS; ++hs) {
+            const double al = sh.alpha[wave][4 * hs + kq];
 #pragma unroll
-            for (int key = 0; key < X0NE_PAGE; key += 2) {
-                const double2 pp = *reinterpret_cast<const double2*>(pw + g * X0NE_PAGE + key);
-                a0 = fma(pp.x, v0[key], a0);
-                a1 = fma(pp.x, v1[key], a1);
-                a0 = fma(pp.y, v0[key + 1], a0);
-                a1 = fma(pp.y, v1[key + 1], a1);
+            for (int i = 0; i < 8; ++i) o[hs][i] *= al;
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            double pv[HS];
+#pragma unroll
+            for (int hs = 0; hs < HS; ++hs) pv[hs] = sh.pw[wave][4 * hs + x][4 * kq + s4];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t w = s4 < 2 ? vc[i].x : vc[i].y;
+                const double vd = (double)((s4 & 1) ? bf_hi(w) : bf_lo(w));
+#pragma unroll
+                for (int hs = 0; hs < HS; ++hs) o[hs][i] = __builtin_amdgcn_mfma_f64_4x4x4f64(pv[hs], vd, o[hs][i], 0, 0, 0);
             }
-            o[g][0] = a0;
-            o[g][1] = a1;
         }
         wave_lds_sync();  // the next page rewrites pw and alpha
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            kc[j] = kn[j];
-            vc[j] = vn[j];
-        }
+        for (int j = 0; j < 4; ++j) kc[j] = kn[j];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vc[i] = vn[i];
         pg_next = pg_after;
     }
-    // This wavefront's state: each head's m and l (the lane sums over keys 0..15), its o.
+    // This wavefront's state: each head's m and l (the lane sums over the column's 16 lanes),
+    // its o (lane l: head 4 hs + l / 16, dims 16 i + 4 bq + x).
 #pragma unroll
-    for (int e = 0; e < HPL; ++e) {
-        double l = lsum[e];
+    for (int hs = 0; hs < HS; ++hs) {
+        double l = lsum[hs];
 #pragma unroll
-        for (int o2 = 1; o2 < 16; o2 <<= 1) l += __shfl_xor(l, o2, 64);
-        const uint32_t g = quarter_head<G>(c, e);
-        if (k == 0 && (G >= 4 || (c & (4 / G - 1)) == 0)) {
-            sh.wm[wave][g] = m[e];
+        for (int o2 = 4; o2 < 64; o2 <<= 1) l += __shfl_xor(l, o2, 64);
+        const uint32_t g = 4 * hs + x;
+        if (lane < 4 && g < (uint32_t)G) {
+            sh.wm[wave][g] = m[hs];
             sh.wl[wave][g] = l;
         }
-    }
+        const uint32_t go = 4 * hs + kq;
+        if (go < (uint32_t)G) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        sh.wo[wave][g][lane] = o[g][0];
-        sh.wo[wave][g][lane + 64] = o[g][1];
+            for (int i = 0; i < 8; ++i) sh.wo[wave][go][16 * i + 4 * bq + x] = o[hs][i];
+        }
     }
     lds_barrier();
     // The block's 4 wavefronts merged per head (in wave order, a wavefront without a page skipped).
@@ -1104,21 +1126,10 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
     for (uint32_t g = wave; g < (uint32_t)G; g += WAVES) {
         const double* s = st_base + (size_t)(h0 + g) * P * X0NE_SPLIT_STATE;
         double* f = sh.f[wave];
-        double mx = -INFINITY;
-        for (uint32_t yy = lane; yy < active; yy += 64) mx = fmax(mx, dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE));
-#pragma unroll
-        for (int o2 = 1; o2 < 64; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
-        double lp = 0.0;
-        for (uint32_t yy = lane; yy < active; yy += 64) {
-            const double fy = exp(dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE) - mx);
-            f[yy] = fy;
-            lp += dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE + 1) * fy;
-        }
-        const double l = wave_sum_d(lp);
-        wave_lds_sync();
-        // The slices' o values in chunks of EXACT_CHUNK, every load of a chunk issued before any
-        // is used (one round trip to memory per chunk, not per slice), summed in slice order.
-        double o0 = 0.0, o1 = 0.0;
+        // The slices' m and l (lane l: slices l, l + 64, ...) and the first EXACT_CHUNK slices'
+        // o values are requested together, before any is used: one round trip to memory for up
+        // to EXACT_CHUNK slices. Later chunks of o follow one round trip each, summed in slice
+        // order.
         double av[EXACT_CHUNK], bv[EXACT_CHUNK];
         auto request = [&](uint32_t y0) {
 #pragma unroll
@@ -1129,7 +1140,37 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
                     bv[k] = dstate_get(so + lane + 64);
                 }
         };
+        constexpr int ML = MERGE_MAX / 64;
+        double mv[ML], lv[ML];
+#pragma unroll
+        for (int j = 0; j < ML; ++j) {
+            const uint32_t yy = lane + 64 * j;
+            mv[j] = -INFINITY;
+            lv[j] = 0.0;
+            if (64 * j < active && yy < active) {
+                mv[j] = dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE);
+                lv[j] = dstate_get(s + (size_t)yy * X0NE_SPLIT_STATE + 1);
+            }
+        }
         request(0);
+        double mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < ML; ++j) mx = fmax(mx, mv[j]);
+#pragma unroll
+        for (int o2 = 1; o2 < 64; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
+        double lp = 0.0;
+#pragma unroll
+        for (int j = 0; j < ML; ++j) {
+            const uint32_t yy = lane + 64 * j;
+            if (64 * j < active && yy < active) {
+                const double fy = exp(mv[j] - mx);
+                f[yy] = fy;
+                lp += lv[j] * fy;
+            }
+        }
+        const double l = wave_sum_d(lp);
+        wave_lds_sync();
+        double o0 = 0.0, o1 = 0.0;
         for (uint32_t y0 = 0; y0 < active; y0 += EXACT_CHUNK) {
 #pragma unroll
             for (uint32_t k = 0; k < EXACT_CHUNK; ++k)

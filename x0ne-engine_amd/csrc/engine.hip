@@ -1236,7 +1236,12 @@ x0ne_status build_begin(const Cfg& c, const x0ne_engine_options* opts, x0ne_engi
         delete e;
         return s;
     };
-    if ((st = split_plan(e->gpu, (uint32_t)c.q_heads, (uint32_t)c.kv_heads, &e->split)) != X0NE_OK) return bail(st);
+    if ((st = split_plan(e->gpu, (uint32_t)c.q_heads, (uint32_t)c.kv_heads, &e->split, e->f64_sums != 0)) != X0NE_OK)
+        return bail(st);
+    if (e->f64_sums) {
+        static const char* env = std::getenv("X0NE_EXACT_SPLITS");  // a tuning knob
+        if (env && std::atoi(env) > 0) e->split.splits = (uint32_t)std::min(std::atoi(env), 256);
+    }
     // A grouped plan merges in its last block by default (one launch per layer); the reference's
     // default is the merge kernel (engine.rs:35), which set_split_merge selects.
     e->merge = e->split.grouped ? X0NE_MERGE_LAST_BLOCK : X0NE_MERGE_KERNEL;

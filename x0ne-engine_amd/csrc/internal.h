@@ -110,7 +110,9 @@ constexpr uint32_t EXACT_GEMM_WAVES_PER_CU = 8;
 x0ne_status exact_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols, const void* x, uint64_t n, void* y,
                        bool out_f32, double* ws, uint64_t ws_bytes, uint32_t ks = 0);
 // Split plan for a geometry (gpu.rs:958-985), P capped at `cap`.
-x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out);
+// exact: the plan of the exact mode's f64 kernel (its occupancy sets P).
+x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out,
+                       bool exact = false);
 x0ne_status attention_split(x0ne_gpu* g, const x0ne_split_plan& plan, int last_block, const void* q, const void* k,
                             const void* v, const void* pages, void* state, void* counter, void* out, const void* pos,
                             uint32_t q_heads, uint32_t kv_heads, uint32_t max_ctx, float scale);

@@ -617,11 +617,12 @@ static constexpr uint32_t DEFAULT_SPLIT_CAP = 128;
 
 namespace x0ne {
 
-x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out) {
+x0ne_status split_plan(const x0ne_gpu* g, uint32_t q_heads, uint32_t kv_heads, x0ne_split_plan* out, bool exact) {
     if (kv_heads == 0 || q_heads % kv_heads != 0)
         return fail(X0NE_ERR_GPU, std::to_string(q_heads) + " q heads for " + std::to_string(kv_heads) + " kv heads");
     const uint32_t group = q_heads / kv_heads;
-    const void* k = group_kernel(group);
+    const void* k = exact ? exact_group_kernel(group) : group_kernel(group);
+    if (exact && !k) return fail(X0NE_ERR_GPU, "the exact attention takes 1, 2, 4 or 8 q heads per kv head");
     x0ne_split_plan p = {};
     p.grouped = k != nullptr;
     p.group = p.grouped ? group : 1;
