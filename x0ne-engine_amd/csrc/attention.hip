@@ -791,13 +791,15 @@ __device__ __forceinline__ void stash_wave(AttnShared<G, T, V>& sh, const T m[G]
 struct ExactShared {
     // q heads, bf16-rounded, as f64; the page weights (per wavefront, head, key) and rescale
     // factors; the new K/V row; the block merge's states; the last block's slice factors.
-    double qd[8][X0NE_HEAD_DIM];
+    // qd[head][d / 32][d % 32]: each quarter row padded to 34, so the 16 quarters a read of the
+    // q operand meets (4 heads x 4 quarters) fall in distinct LDS banks.
+    double qd[8][4][34];
     double pw[WAVES][8][X0NE_PAGE];
     double alpha[WAVES][8];
     alignas(16) bf16_t knew[X0NE_HEAD_DIM], vnew[X0NE_HEAD_DIM];
     double wm[WAVES][8], wl[WAVES][8];
     double wo[WAVES][8][X0NE_HEAD_DIM];
-    double wf[WAVES][8], mh[8], lh[8];
+    double wf[WAVES][8], mh[8];
     double f[WAVES][MERGE_MAX];
     uint32_t last;
 };
@@ -911,8 +913,8 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         if (g < (uint32_t)G) {
             float ra, rb;
             rope_turn(qnm[j], rc, rs, &ra, &rb);
-            sh.qd[g][lane] = (double)bf_round(ra);
-            sh.qd[g][lane + 64] = (double)bf_round(rb);
+            sh.qd[g][lane / 32][lane % 32] = (double)bf_round(ra);
+            sh.qd[g][lane / 32 + 2][lane % 32] = (double)bf_round(rb);
         }
     }
     if (owner && wave == WAVES - 1) {
@@ -939,7 +941,7 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         const uint32_t h = G >= 4 ? 4 * hs + x : x % (uint32_t)G;
 #pragma unroll
         for (int d = 0; d < 32; d += 2) {
-            const double2 v = *reinterpret_cast<const double2*>(&sh.qd[h][32 * kq + d]);
+            const double2 v = *reinterpret_cast<const double2*>(&sh.qd[h][kq][d]);
             qv[hs][d] = v.x;
             qv[hs][d + 1] = v.y;
         }
@@ -1072,39 +1074,40 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
         }
     }
     lds_barrier();
-    // The block's 4 wavefronts merged per head (in wave order, a wavefront without a page skipped).
-    if (t < (uint32_t)G) {
+    // The block's 4 wavefronts merged per head, in wave order: thread 4 g + w forms wavefront
+    // w's factor for head g (the block's exps side by side), then every thread adds its outputs'
+    // terms. Wavefront 0 always has a page, so each maximum is finite, and a wavefront without
+    // one (m -inf, l and o 0) adds +0.
+    if (t < 4 * (uint32_t)G) {
+        const uint32_t g = t / 4, w = t % 4;
         double mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) mx = fmax(mx, sh.wm[w][t]);
-        double l = 0.0;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            const bool seen = sh.wm[w][t] != -INFINITY;
-            const double fw = seen ? exp(sh.wm[w][t] - mx) : 0.0;
-            sh.wf[w][t] = fw;
-            if (seen) l += sh.wl[w][t] * fw;
-        }
-        sh.mh[t] = mx;
-        sh.lh[t] = l;
+        for (int v = 0; v < WAVES; ++v) mx = fmax(mx, sh.wm[v][g]);
+        sh.wf[w][g] = exp(sh.wm[w][g] - mx);
+        if (w == 0) sh.mh[g] = mx;
     }
     lds_barrier();
     const bool whole = sp.active == 1;
     double* st_base = reinterpret_cast<double*>(a.state);
+#pragma unroll
     for (uint32_t i = t; i < (uint32_t)G * X0NE_HEAD_DIM; i += BLOCK) {
         const uint32_t g = i / X0NE_HEAD_DIM, d = i % X0NE_HEAD_DIM;
-        double ov = 0.0;
+        const double mx = sh.mh[g];
+        double l = 0.0, ov = 0.0;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w)
-            if (sh.wm[w][g] != -INFINITY) ov += sh.wo[w][g][d] * sh.wf[w][g];
+        for (int w = 0; w < WAVES; ++w) {
+            const double fw = sh.wf[w][g];
+            l += sh.wl[w][g] * fw;
+            ov += sh.wo[w][g][d] * fw;
+        }
         if (whole) {
-            a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf((float)(ov / sh.lh[g]));
+            a.out[(size_t)(h0 + g) * X0NE_HEAD_DIM + d] = f2bf((float)(ov / l));
         } else {
             double* st = st_base + ((size_t)(h0 + g) * P + y) * X0NE_SPLIT_STATE;
             dstate_put(st + 4 + d, ov);
             if (d == 0) {
-                dstate_put(st, sh.mh[g]);
-                dstate_put(st + 1, sh.lh[g]);
+                dstate_put(st, mx);
+                dstate_put(st + 1, l);
             }
         }
     }
@@ -1153,11 +1156,14 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
             }
         }
         request(0);
+        // Maximum and sum over the lanes that hold slices: butterflies over the smallest power
+        // of two of lanes covering them (lane 0's group), then lane 0's sum for every lane.
+        uint32_t span = 1;
+        while (span < active && span < 64) span <<= 1;
         double mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < ML; ++j) mx = fmax(mx, mv[j]);
-#pragma unroll
-        for (int o2 = 1; o2 < 64; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
+        for (uint32_t o2 = 1; o2 < span; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, (int)o2, 64));
         double lp = 0.0;
 #pragma unroll
         for (int j = 0; j < ML; ++j) {
@@ -1168,7 +1174,8 @@ __device__ __forceinline__ void exact_block(const AttnArgs& a, ExactShared& sh) 
                 lp += lv[j] * fy;
             }
         }
-        const double l = wave_sum_d(lp);
+        for (uint32_t o2 = 1; o2 < span; o2 <<= 1) lp += __shfl_xor(lp, (int)o2, 64);
+        const double l = __shfl(lp, 0, 64);
         wave_lds_sync();
         double o0 = 0.0, o1 = 0.0;
         for (uint32_t y0 = 0; y0 < active; y0 += EXACT_CHUNK) {
