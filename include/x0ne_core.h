@@ -252,8 +252,9 @@ typedef struct x0ne_greedy x0ne_greedy;
      X0NE_SUMS_F64 is the exact mode: the projections add their exact bf16 products in f64, and
      decode attention computes scores, softmax and sums in f64 with the f64 scale 1/sqrt(128)
      (split-K with f64 states merged in f64), so every rounding point of the step is the f64
-     oracle's (oracle/src/lib.rs:123-187) and the greedy tokens are the oracle's; a prompt is fed
-     one exact step per token. It serves a dense model decoding one sequence with 1, 2, 4 or 8 q
+     oracle's (oracle/src/lib.rs:123-187) and the greedy tokens are the oracle's; its prefill
+     passes sum in f64 too (the same bits as feeding the prompt one decode step per token). It
+     serves a dense model decoding one sequence with 1, 2, 4 or 8 q
      heads per kv head (X0NE_ERR_NOT_IMPLEMENTED otherwise).
      X0NE_SUMS_F32 is the fp32-accumulating path (the reference engine's arithmetic: f32 sums,
      matrix-core prefill passes).
@@ -261,8 +262,8 @@ typedef struct x0ne_greedy x0ne_greedy;
      engine can serve it, else the f32 path (MoE models, max_batch > 1).
    - prefill_chunk: prompt rows per prefill pass (engine.rs:67, PREFILL_CHUNK); 0 takes
      min(2048, max_ctx x max_batch). A pass runs every layer over its rows with matrix-core
-     GEMMs and the causal prefill attention; the exact mode feeds a prompt one decode step per
-     token.
+     GEMMs and the causal prefill attention (the exact mode's in f64; a MoE engine feeds a
+     prompt one decode step per token).
    - max_batch: independent sequences the batched greedy entry points serve (0 or 1: the
      single-sequence engine). Each sequence has its own max_ctx positions of KV pages (the page
      table holds max_batch runs of ceil(max_ctx / 16) pages) and its own position; the batched
