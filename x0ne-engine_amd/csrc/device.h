@@ -170,6 +170,32 @@ template <class A>
 struct RowReduce<1, -1, A> {
     static __device__ __forceinline__ void run(A*, uint32_t) {}
 };
+// f64 values moved between lanes of a row of 16 by DPP (a VALU operand modifier, no LDS round
+// trip), the two 32-bit halves alike: CTRL 0x124 / 0x128 rotate the row by 4 / 8 lanes, 0x4E
+// and 0xB1 swap lanes by xor 2 and xor 1 within each group of 4.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// The last four steps of an f64 sum (lane bits 3..0) within each row of 16: the rotations by 4
+// and 8 leave every lane the sum of its 4 lanes of equal index mod 4, the two swaps add the 4
+// such sums; each lane ends with the whole row's sum (in an association of its own). The f32
+// sums keep their xor butterflies (measured no faster with this, and their bits are the tests'
+// recorded ones).
+template <>
+struct RowReduce<1, 3, double> {
+    static __device__ __forceinline__ void run(double* v, uint32_t) {
+        double x = v[0];
+        x += dpp_d<0x124>(x);
+        x += dpp_d<0x128>(x);
+        x += dpp_d<0x4E>(x);
+        x += dpp_d<0xB1>(x);
+        v[0] = x;
+    }
+};
 
 template <int R, class A>
 __device__ __forceinline__ A wave_reduce_rows(A* v) {
