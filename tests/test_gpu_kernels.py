@@ -428,27 +428,30 @@ def test_balanced_few_row_gemm_is_the_oracle_and_the_same_bits_every_time(kernel
     assert (f1[0].view(np.uint32) == f[0].view(np.uint32)).all(), f"{what}: row 0 alone"
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(16))
 def test_the_f64_gemm_is_the_exact_sum_of_the_products(kernels, seed):
-    """The exact mode's projection (x0ne_gemm_f64_t*_bf16): each output is the f64 sum of its
-    exact bf16 products, rounded to f32 (and the bf16 output that f32 rounded). Against the
-    exactly rounded sum (math.fsum): equal in f32 but where the f64 sums' own rounding (at most
-    cols x 2^-53 of the sum of the magnitudes) reaches an f32 rounding boundary. Every tile width,
-    K cut into slices (more slices than steps too), K tails, rows and tokens past a tile's edge,
-    zeros and denormals among the values."""
+    """The exact mode's projection (x0ne_gemm_f64_t*_bf16, and x0ne_gemm_f64_q*_bf16 for up to
+    32 rows of X): each output is the f64 sum of its exact bf16 products, rounded to f32 (and the
+    bf16 output that f32 rounded). Against the exactly rounded sum (math.fsum): equal in f32 but
+    where the f64 sums' own rounding (at most cols x 2^-53 of the sum of the magnitudes) reaches
+    an f32 rounding boundary. Every tile width and quad count, K cut into slices (more slices than
+    steps too), K tails, rows and tokens past a tile's edge, zeros and denormals among the values."""
     import math
     rng = O.Rng(2000 + seed)
-    n = rng.pick([1, 5, 16, 17, 33, 70])
+    n = rng.pick([1, 5, 16, 17, 20, 33, 70] if seed < 8 else [1, 3, 4, 5, 8, 13, 20, 31, 32])
     rows = rng.pick([1, 16, 63, 200])
     cols = rng.pick([8, 40, 264, 1032])
-    tt = rng.pick([1, 2, 4])
     ks = rng.pick([1, 1, 3, 16])
+    if seed < 8:
+        tt, tq = rng.pick([1, 2, 4]), 0
+    else:
+        tt, tq = 0, rng.pick([q for q in range(1, 9) if 4 * q >= n])
     scale = rng.pick([1e-2, 1.0])
     w = bf16s_with_edges(rng, rows * cols, scale)
     x = bf16s_with_edges(rng, n * cols, scale)
-    what = f"f64 gemm seed {seed} {n}x{rows}x{cols} tiles {tt} K slices {ks}"
-    f = kernels.gemm_f64(bf16_bits(w), rows, cols, bf16_bits(x), n, True, tt, ks)
-    b = kernels.gemm_f64(bf16_bits(w), rows, cols, bf16_bits(x), n, False, tt, ks)
+    what = f"f64 gemm seed {seed} {n}x{rows}x{cols} tiles {tt} quads {tq} K slices {ks}"
+    f = kernels.gemm_f64(bf16_bits(w), rows, cols, bf16_bits(x), n, True, tt, ks, tq)
+    b = kernels.gemm_f64(bf16_bits(w), rows, cols, bf16_bits(x), n, False, tt, ks, tq)
     assert (b == bf16_bits(f).reshape(b.shape)).all(), f"{what}: bf16 is the f32 rounded"
     W = w.astype(np.float64).reshape(rows, cols)
     X = x.astype(np.float64).reshape(n, cols)

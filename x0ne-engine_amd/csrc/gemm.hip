@@ -474,6 +474,115 @@ X0NE_GEMM_F64(x0ne_gemm_f64_t1_bf16, 1)
 X0NE_GEMM_F64(x0ne_gemm_f64_t2_bf16, 2)
 X0NE_GEMM_F64(x0ne_gemm_f64_t4_bf16, 4)
 
+// ---- exact sums for a few rows: 4-token quads ----
+// The same product for n <= 32 rows of X on v_mfma_f64_4x4x4f64, which computes 4 blocks b of
+// D[4][4] += A[4][4] B[4][4] with lane l = 16 k + 4 b + x holding A_b[x][k], B_b[k][x] and
+// D_b[l / 16][x] (about 18 cycles per product against 64 for the 16x16x4 product, the same f64
+// rate): A is W as in gemm_f64 (lane l loads row 16 f + l % 16, columns k0 + 8 (l / 16) ..), B
+// the quad's 4 tokens (lane l loads token 4 t + l % 4, the same columns), so a wavefront covers
+// 16 TF features x 4 TQ tokens without padding 20 rows to 32. D of lane l: feature
+// 16 f + 4 ((l % 16) / 4) + l / 16, token 4 t + l % 4.
+namespace {
+
+template <int TF, int TQ>
+__device__ __forceinline__ void gemm_f64_quads(const bf16_t* __restrict__ w, const bf16_t* __restrict__ x,
+                                               void* __restrict__ y, uint32_t rows, uint32_t cols, uint32_t n,
+                                               uint32_t out_f32, uint32_t ks, double* __restrict__ ws) {
+    const uint32_t lane = threadIdx.x & 63, V = blockDim.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tiles_f = (rows + 16 * TF - 1) / (16 * TF);
+    const uint32_t id = blockIdx.x * V + wave;
+    if (cols % 8 != 0 || out_f32 > 1 || ks == 0 || (ks > 1 && ws == nullptr) || n > 4u * TQ ||
+        (uint64_t)id >= (uint64_t)tiles_f * ks)
+        return;  // wavefront-uniform; no barrier
+    const uint32_t ft = id / ks, slice = id % ks;
+    const uint32_t r = lane & 15, q = lane >> 4, xq = lane & 3;
+    const auto wr = rsrc(w, (uint64_t)rows * cols * 2);
+    const auto xr = rsrc(x, (uint64_t)n * cols * 2);
+    double acc[TF][TQ];
+#pragma unroll
+    for (int f = 0; f < TF; ++f)
+#pragma unroll
+        for (int t = 0; t < TQ; ++t) acc[f][t] = 0.0;
+    uint4 a[2][TF], b[2][TQ];
+    const uint32_t all = (cols + 31) / 32, s_lo = all * slice / ks, steps = all * (slice + 1) / ks;
+    auto load = [&](int buf, uint32_t s) {
+        const uint32_t k = 32 * s + 8 * q;
+        const bool in = s < steps && k < cols;
+#pragma unroll
+        for (int f = 0; f < TF; ++f) {
+            const uint32_t row = 16 * (TF * ft + f) + r;
+            a[buf][f] = bload<>(wr, in && row < rows ? (row * cols + k) * 2 : OFF_NONE);
+        }
+#pragma unroll
+        for (int t = 0; t < TQ; ++t) {
+            const uint32_t tok = 4 * t + xq;
+            b[buf][t] = bload<>(xr, in && tok < n ? (tok * cols + k) * 2 : OFF_NONE);
+        }
+    };
+    auto elem = [](const uint4& v, int e) -> double {
+        const uint32_t u = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+        return (double)((e & 1) ? bf_hi(u) : bf_lo(u));
+    };
+    auto step = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            double av[TF], bv[TQ];
+#pragma unroll
+            for (int f = 0; f < TF; ++f) av[f] = elem(a[buf][f], e);
+#pragma unroll
+            for (int t = 0; t < TQ; ++t) bv[t] = elem(b[buf][t], e);
+#pragma unroll
+            for (int f = 0; f < TF; ++f)
+#pragma unroll
+                for (int t = 0; t < TQ; ++t) acc[f][t] = __builtin_amdgcn_mfma_f64_4x4x4f64(av[f], bv[t], acc[f][t], 0, 0, 0);
+        }
+    };
+    load(0, s_lo);
+    for (uint32_t s = s_lo; s < steps; s += 2) {
+        load(1, s + 1);
+        step(0);
+        if (s + 1 >= steps) break;  // wavefront-uniform
+        load(0, s + 2);
+        step(1);
+    }
+#pragma unroll
+    for (int f = 0; f < TF; ++f)
+#pragma unroll
+        for (int t = 0; t < TQ; ++t) {
+            const uint32_t tok = 4 * t + xq, feat = 16 * (TF * ft + f) + 4 * (r / 4) + q;
+            if (tok >= n || feat >= rows) continue;
+            if (ks > 1) {
+                ws[((size_t)slice * n + tok) * rows + feat] = acc[f][t];
+                continue;
+            }
+            const float v = (float)acc[f][t];
+            if (out_f32)
+                static_cast<float*>(y)[(size_t)tok * rows + feat] = v;
+            else
+                static_cast<bf16_t*>(y)[(size_t)tok * rows + feat] = f2bf(v);
+        }
+}
+
+}  // namespace
+
+// x0ne_gemm_f64_q{TQ}_bf16: x0ne_gemm_f64_t*_bf16's arguments for 1 <= n <= 4 TQ rows; grid
+// ceil(ceil(rows / 64) ks / V), block 64 V threads (any V).
+#define X0NE_GEMM_F64_Q(TQ)                                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) x0ne_gemm_f64_q##TQ##_bf16(                                 \
+        const bf16_t* __restrict__ w, const bf16_t* __restrict__ x, void* __restrict__ y, uint32_t rows,          \
+        uint32_t cols, uint32_t n, uint32_t out_f32, uint32_t ks, double* __restrict__ ws) {                      \
+        gemm_f64_quads<4, TQ>(w, x, y, rows, cols, n, out_f32, ks, ws);                                            \
+    }
+X0NE_GEMM_F64_Q(1)
+X0NE_GEMM_F64_Q(2)
+X0NE_GEMM_F64_Q(3)
+X0NE_GEMM_F64_Q(4)
+X0NE_GEMM_F64_Q(5)
+X0NE_GEMM_F64_Q(6)
+X0NE_GEMM_F64_Q(7)
+X0NE_GEMM_F64_Q(8)
+
 // x0ne_gemm_f64_reduce: y[t][f] = the f32 (out_f32 1) or bf16 of the f32 of sum over slices 0 ..
 // ks - 1, in that order, of ws[slice][t][f] (f64); grid ceil(n rows / 256), block 256.
 extern "C" __global__ void __launch_bounds__(256)

@@ -129,6 +129,14 @@ X0NE_DECLARE_FEW(t4_r1_swiglu)
 X0NE_DECLARE_GEMM_F64(t1)
 X0NE_DECLARE_GEMM_F64(t2)
 X0NE_DECLARE_GEMM_F64(t4)
+X0NE_DECLARE_GEMM_F64(q1)
+X0NE_DECLARE_GEMM_F64(q2)
+X0NE_DECLARE_GEMM_F64(q3)
+X0NE_DECLARE_GEMM_F64(q4)
+X0NE_DECLARE_GEMM_F64(q5)
+X0NE_DECLARE_GEMM_F64(q6)
+X0NE_DECLARE_GEMM_F64(q7)
+X0NE_DECLARE_GEMM_F64(q8)
 #undef X0NE_DECLARE_GEMM_F64
 __global__ void x0ne_gemm_f64_reduce(const double* ws, void* y, uint32_t rows, uint32_t n, uint32_t ks,
                                      uint32_t out_f32);

@@ -402,9 +402,10 @@ x0ne_status exact_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols,
         (ks > 1 && ws == nullptr))
         return fail(X0NE_ERR_FORMAT, "exact gemm: " + std::to_string(rows) + "x" + std::to_string(cols) + ", n " +
                                          std::to_string(n) + ", " + std::to_string(ks) + " slices");
-    // Tokens per wavefront: 16 TT, the smallest TT of 1, 2, 4 that covers n (up to 64).
-    const uint32_t tt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
-    const uint64_t tiles = (rows + 63) / 64 * ((n + 16 * tt - 1) / (16 * tt)), steps = (cols + 31) / 32;
+    // Tokens per wavefront: up to 32 rows of X in quads of 4 (x0ne_gemm_f64_q*, no padding to 16),
+    // beyond that 64 (x0ne_gemm_f64_t4); 64 features per wavefront either way.
+    const uint32_t tq = n <= 32 ? (uint32_t)(n + 3) / 4 : 0, tt = 4;
+    const uint64_t tiles = (rows + 63) / 64 * (tq ? 1 : (n + 16 * tt - 1) / (16 * tt)), steps = (cols + 31) / 32;
     if (ks == 0) {
         // A wavefront's steps run back to back on its SIMD's f64 matrix core, so a launch wants
         // EXACT_GEMM_WAVES_PER_CU wavefronts per CU: fewer tiles than that cut K into slices of
@@ -417,9 +418,11 @@ x0ne_status exact_gemm(x0ne_gpu* g, const void* w, uint64_t rows, uint64_t cols,
             ks = (uint32_t)std::max<uint64_t>(k, 1);
         }
     }
-    const void* fn = tt == 1 ? (const void*)&x0ne_gemm_f64_t1_bf16
-                     : tt == 2 ? (const void*)&x0ne_gemm_f64_t2_bf16
-                               : (const void*)&x0ne_gemm_f64_t4_bf16;
+    static const void* const quads[8] = {(const void*)&x0ne_gemm_f64_q1_bf16, (const void*)&x0ne_gemm_f64_q2_bf16,
+                                         (const void*)&x0ne_gemm_f64_q3_bf16, (const void*)&x0ne_gemm_f64_q4_bf16,
+                                         (const void*)&x0ne_gemm_f64_q5_bf16, (const void*)&x0ne_gemm_f64_q6_bf16,
+                                         (const void*)&x0ne_gemm_f64_q7_bf16, (const void*)&x0ne_gemm_f64_q8_bf16};
+    const void* fn = tq ? quads[tq - 1] : (const void*)&x0ne_gemm_f64_t4_bf16;
     uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, n32 = (uint32_t)n, of = out_f32 ? 1u : 0u, k32 = ks;
     double* wsp = ks > 1 ? ws : nullptr;
     void* yp = y;

@@ -730,16 +730,21 @@ class Kernels:
         y = a.read_array(ys, 0, n * rows, np.float32 if mode == 1 else np.uint16).reshape(n, rows)
         return y, bool((a.read_array(counts, 0, groups, np.uint32) == 0).all())
 
-    def gemm_f64(self, w, rows: int, cols: int, x, n: int, out_f32: bool, tt: int = 0, ks: int = 1) -> np.ndarray:
+    def gemm_f64(self, w, rows: int, cols: int, x, n: int, out_f32: bool, tt: int = 0, ks: int = 1,
+                 tq: int = 0) -> np.ndarray:
         """x0ne_gemm_f64_t{TT}_bf16, the exact mode's projection: Y [n][rows] = X [n][cols] W^T,
         every bf16 product summed in f64 on the matrix cores, Y f32 or bf16 (bits) of the f32
-        of the sum. tt 0 takes the kernel the engine takes for n (1, 2 or 4 tiles of 16 tokens
-        per wavefront); ks > 1 cuts K into ks slices whose f64 partial sums
+        of the sum. tt 1, 2 or 4: tiles of 16 tokens per wavefront; tq 1..8: the 4-token-quad
+        kernel x0ne_gemm_f64_q{TQ}_bf16 (n <= 4 tq); both 0: the kernel the engine takes for n
+        (quads up to 32 rows). ks > 1 cuts K into ks slices whose f64 partial sums
         x0ne_gemm_f64_reduce adds."""
-        if tt == 0:
-            tt = 1 if n <= 16 else 2 if n <= 32 else 4
-        if w.size != rows * cols or x.size != n * cols or cols % 8 or tt not in (1, 2, 4) or n == 0 or rows == 0 \
-                or ks < 1:
+        if tt == 0 and tq == 0:
+            if n <= 32:
+                tq = -(-n // 4)
+            else:
+                tt = 4
+        if w.size != rows * cols or x.size != n * cols or cols % 8 or n == 0 or rows == 0 or ks < 1 or \
+                (tq == 0 and tt not in (1, 2, 4)) or (tq and (tt or not 1 <= tq <= 8 or n > 4 * tq)):
             raise FormatError("gemm_f64: lengths")
         ob = 4 if out_f32 else 2
         a = self._arena()
@@ -751,8 +756,8 @@ class Kernels:
         a.scrub_client_data()
         a.write(ws, 0, np.asarray(w, np.uint16))
         a.write(xs, 0, np.asarray(x, np.uint16))
-        tiles = -(-rows // 64) * -(-n // (16 * tt))
-        self.gpu.launch(f"x0ne_gemm_f64_t{tt}_bf16", -(-tiles * ks // 4), 256,
+        tiles = -(-rows // 64) * (1 if tq else -(-n // (16 * tt)))
+        self.gpu.launch(f"x0ne_gemm_f64_q{tq}_bf16" if tq else f"x0ne_gemm_f64_t{tt}_bf16", -(-tiles * ks // 4), 256,
                         [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(ys)), Arg.u32(rows), Arg.u32(cols),
                          Arg.u32(n), Arg.u32(1 if out_f32 else 0), Arg.u32(ks), Arg.ptr(a.ptr(parts))])
         if ks > 1:
