@@ -1693,34 +1693,36 @@ X0NE_PREFILL_GROUP(8)
 
 // ---- causal prefill in the exact mode (f64 scores, softmax and sums) ----
 //
-// The exact mode's prefill passes: the arithmetic of the exact decode kernel (exact_block: exact
-// bf16 x bf16 products summed in f64, the f64 scale 1/sqrt(128), an f64 softmax with the maximum
+// The exact mode's prefill passes: the arithmetic of the exact decode kernel (exact bf16 x bf16
+// products summed in f64, the f64 scale 1/sqrt(128), an f64 online softmax with the maximum
 // subtracted, f64 weighted V sums, the result rounded f64 -> f32 -> bf16) for every row of the
-// pass, on the vector units (MI355X runs f64 on the vector units at its f64 matrix rate). Block
-// (kv head kh, row block) serves 64 columns (column c: row r0 + c / G, head kh G + c % G), 8
-// to each of its 8 wavefronts; the keys pass in tiles of 64 staged in LDS once per block (K swizzled by key,
-// V dim-major swizzled by dim, so no two lanes of a read meet in a bank group), the next tile's
-// loads in flight while one is summed, and the 64 columns' q (as f64) stay in LDS:
-//  - scores: lane l takes key l of the tile and, 8 dims at a time, adds its exact products
-//    with each of the wavefront's 8 q columns (read by every lane at once) in dim order;
-//  - the online softmax per column over the tile's 64 keys (maxima and sums by butterflies);
-//  - weighted sums: lane l owns dims l and l + 64 of the 8 columns and adds weight x value
-//    over the tile's keys in key order (weights through LDS, V 8 keys at a time).
+// pass, on the f64 matrix cores: v_mfma_f64_16x16x4f64, lane l supplying A[l % 16][l / 16] and
+// B[l / 16][l % 16] and holding D[l / 16 + 4 i][l % 16], i = 0..3. Block (kv head kh, row
+// block) serves 64 columns (column c: row r0 + c / G, head kh G + c % G), 16 to each of its 4
+// wavefronts; the keys pass in tiles of 64 staged in LDS once per block (K swizzled by key, V
+// dim-major swizzled by dim), the next tile's loads in flight while one is summed:
+//  - scores S^T per 16-key block kb: A = K, product row r holding key 16 kb + 4 (r % 4) + r / 4,
+//    so that lane l's results are the 4 consecutive keys 16 kb + 4 (l / 16) + i; k = dims
+//    32 (l / 16) + j at product j; B = the wavefront's 16 q columns, lane l holding column
+//    l % 16's dims 32 (l / 16) .. + 31 as f64 in registers for the whole pass;
+//  - the online softmax per column: lane l holds 16 of its column's 64 keys, the other 48 sit in
+//    lanes l ^ 16, l ^ 32, l ^ 48;
+//  - O^T += V^T P^T: A = V^T (row = dim 16 db + l % 16, k = the key of step (kb, i),
+//    16 kb + 4 (l / 16) + i: 4 consecutive keys of one dim, one 8-byte LDS read), B = P^T, whose
+//    value at lane l is the lane's own weight of that key (no exchange); D = O^T, lane l holding
+//    dims 16 db + l / 16 + 4 i of column l % 16 in 8 accumulators.
 // Keys at or past a column's own position + 1 score -inf; V of keys at or past the block's
 // context is zeroed in LDS (its weight is 0, and 0 times a value that is not a number would
 // not be). Each output depends on its column's own inputs and the fixed order above.
 namespace {
 
+typedef double px_f64x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t PX_COLS = X0NE_PREFILL_EXACT_COLS;       // columns per block
 constexpr uint32_t PX_BLOCK = X0NE_PREFILL_EXACT_THREADS;
-constexpr uint32_t PX_WAVES = PX_BLOCK / 64;                // wavefronts per block
-constexpr uint32_t PX_WC = PX_COLS / PX_WAVES;              // columns per wavefront
 
 struct PrefillExactShared {
-    double qd[PX_COLS][X0NE_HEAD_DIM];
     alignas(16) bf16_t k[X0NE_SPLIT_TILE * X0NE_HEAD_DIM];  // [key][16 chunks of 8 dims], chunk c at c ^ (key % 16)
     alignas(16) bf16_t v[X0NE_HEAD_DIM * X0NE_SPLIT_TILE];  // [dim][8 chunks of 8 keys], chunk c at c ^ (dim % 8)
-    double p[PX_WAVES][PX_WC][X0NE_SPLIT_TILE];
 };
 
 template <int G>
@@ -1734,23 +1736,27 @@ __device__ __forceinline__ void prefill_exact_block(const bf16_t* __restrict__ q
     if (kh >= kv_heads || q_heads != (uint32_t)G * kv_heads || r0 >= rows || max_ctx == 0 || blockDim.x != PX_BLOCK)
         return;  // block-uniform
     const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t n16 = lane & 15, q4 = lane >> 4;
     const uint32_t ctx = min(p0 + min(r0 + RB, rows), max_ctx);  // keys the block reads
     const uint32_t ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
     const uint32_t npages = (ctx + X0NE_PAGE - 1) / X0NE_PAGE;
-    // q of the block's columns as f64 (a column past the rows: zeros).
-    for (uint32_t i = t; i < PX_COLS * X0NE_HEAD_DIM; i += PX_BLOCK) {
-        const uint32_t c = i / X0NE_HEAD_DIM, d = i % X0NE_HEAD_DIM, r = r0 + c / G;
-        sh.qd[c][d] = r < rows ? (double)bf2f(q[((size_t)r * q_heads + kh * G + c % G) * X0NE_HEAD_DIM + d]) : 0.0;
-    }
-    // The wavefront's columns: their limits (keys below p0 + row + 1; a column past the rows
-    // attends key 0 only and is not written).
-    uint32_t lim[PX_WC];
+    // This lane's column 16 wave + l % 16: its row and key limit (keys below p0 + row + 1; a
+    // column past the rows attends key 0 only and is not written), and its q dims 32 q4 .. + 31.
+    const uint32_t col = 16 * wave + n16, r = r0 + col / G;
+    const bool live = r < rows;
+    const uint32_t lim = live ? min(p0 + r + 1, max_ctx) : 1u;
+    double qv[32];
+    {
+        const uint4* qp = reinterpret_cast<const uint4*>(
+            q + ((size_t)(live ? r : r0) * q_heads + kh * G + col % G) * X0NE_HEAD_DIM + 32 * q4);
 #pragma unroll
-    for (int j = 0; j < (int)PX_WC; ++j) {
-        const uint32_t r = r0 + (PX_WC * wave + j) / G;
-        lim[j] = r < rows ? min(p0 + r + 1, max_ctx) : 1u;
+        for (int j = 0; j < 4; ++j) {
+            const uint4 u = live ? qp[j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[8 * j + e] = bf_of(u, e);
+        }
     }
-    // A tile's K chunk i (i = t + 512 j): key i / 16, dims 8 (i % 16) ..; V chunk i: dim i / 8,
+    // A tile's K chunk i (i = t + 256 j): key i / 16, dims 8 (i % 16) ..; V chunk i: dim i / 8,
     // keys 8 (i % 8) .. of the tile.
     constexpr int J = X0NE_SPLIT_TILE * X0NE_HEAD_DIM / 8 / PX_BLOCK;
     const auto kres = plane_rsrc(k_cache, OFF_NONE), vres = plane_rsrc(v_cache, OFF_NONE);
@@ -1783,111 +1789,89 @@ __device__ __forceinline__ void prefill_exact_block(const bf16_t* __restrict__ q
         }
     };
     const double scale = 1.0 / sqrt((double)X0NE_HEAD_DIM);
-    double m[PX_WC], l[PX_WC], o[PX_WC][2];
+    double m = -INFINITY, lsum = 0.0;
+    px_f64x4 o[8];
 #pragma unroll
-    for (int j = 0; j < (int)PX_WC; ++j) {
-        m[j] = -INFINITY;
-        l[j] = 0.0;
-        o[j][0] = o[j][1] = 0.0;
-    }
+    for (int db = 0; db < 8; ++db) o[db] = px_f64x4{0.0, 0.0, 0.0, 0.0};
     fetch(0);
     for (uint32_t tile = 0; tile < ntiles; ++tile) {
-        __syncthreads();  // the tile before is summed (and, first time round, q is in LDS)
+        __syncthreads();  // the tile before is summed
         stash(tile);
         if (tile + 1 < ntiles) fetch(tile + 1);  // block-uniform; in flight while this tile is summed
         __syncthreads();
-        // Scores of key `lane` against the wavefront's 8 columns, 8 dims at a time.
-        const uint32_t key = X0NE_SPLIT_TILE * tile + lane;
-        double sc[PX_WC];
+        // Scores of keys 16 kb + 4 q4 + i against the lane's column.
+        double sc[16];
+        {
+            const uint32_t kt = 4 * (n16 % 4) + n16 / 4;  // the key of product row l % 16 in a block of 16
 #pragma unroll
-        for (int j = 0; j < (int)PX_WC; ++j) sc[j] = 0.0;
-        for (uint32_t kc = 0; kc < X0NE_HEAD_DIM / 8; ++kc) {
-            const uint4 kv = *reinterpret_cast<const uint4*>(&sh.k[lane * X0NE_HEAD_DIM + 8 * (kc ^ (lane % 16))]);
-            const uint32_t u[4] = {kv.x, kv.y, kv.z, kv.w};
-            double kd[8];
+            for (int kb = 0; kb < 4; ++kb) {
+                const uint32_t key = 16 * kb + kt;
+                uint4 kv[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kd[2 * e] = (double)bf_lo(u[e]);
-                kd[2 * e + 1] = (double)bf_hi(u[e]);
+                for (int c4 = 0; c4 < 4; ++c4)
+                    kv[c4] = *reinterpret_cast<const uint4*>(&sh.k[key * X0NE_HEAD_DIM + 8 * ((4 * q4 + c4) ^ (key % 16))]);
+                px_f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                for (int j = 0; j < 32; ++j)
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(bf_of(kv[j / 8], j % 8), qv[j], acc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sc[4 * kb + i] = acc[i];
             }
+        }
+        // The online softmax of the lane's column over the tile's 64 keys.
+        double mx = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < (int)PX_WC; ++j) {
-                const double* qc = &sh.qd[PX_WC * wave + j][8 * kc];
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t key = X0NE_SPLIT_TILE * tile + 16 * (e / 4) + 4 * q4 + e % 4;
+            sc[e] = key < lim ? sc[e] * scale : -INFINITY;
+            mx = fmax(mx, sc[e]);
+        }
+        mx = fmax(mx, __shfl_xor(mx, 16, 64));
+        mx = fmax(mx, __shfl_xor(mx, 32, 64));
+        const double mn = fmax(m, mx);  // key 0 is in every column's first tile: mn is finite
+        const double al = exp(m - mn);
+        double ps = 0.0;
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const double2 qq = *reinterpret_cast<const double2*>(qc + e);
-                    sc[j] = fma(qq.x, kd[e], sc[j]);
-                    sc[j] = fma(qq.y, kd[e + 1], sc[j]);
+        for (int e = 0; e < 16; ++e) {
+            sc[e] = exp(sc[e] - mn);
+            ps += sc[e];
+        }
+        lsum = lsum * al + ps;
+        m = mn;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[db] *= al;
+        // O^T += V^T P^T over the tile's keys, 4 per product.
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const uint32_t d = 16 * db + n16;
+                const uint2 vv = *reinterpret_cast<const uint2*>(
+                    &sh.v[d * X0NE_SPLIT_TILE + 8 * ((2 * kb + q4 / 2) ^ (d % 8)) + 4 * (q4 % 2)]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t w = i < 2 ? vv.x : vv.y;
+                    const double vd = (double)((i & 1) ? bf_hi(w) : bf_lo(w));
+                    o[db] = __builtin_amdgcn_mfma_f64_16x16x4f64(vd, sc[4 * kb + i], o[db], 0, 0, 0);
                 }
             }
-        }
-        // The online softmax per column; the weights to LDS for the weighted sums.
-        double al[PX_WC];
-#pragma unroll
-        for (int j = 0; j < (int)PX_WC; ++j) {
-            const double s = key < lim[j] ? sc[j] * scale : -INFINITY;
-            double mx = s;
-#pragma unroll
-            for (int o2 = 1; o2 < 64; o2 <<= 1) mx = fmax(mx, __shfl_xor(mx, o2, 64));
-            const double mn = fmax(m[j], mx);  // key 0 is in every column's first tile: mn is finite
-            al[j] = exp(m[j] - mn);
-            const double pr = exp(s - mn);
-            double ps = pr;
-#pragma unroll
-            for (int o2 = 1; o2 < 64; o2 <<= 1) ps += __shfl_xor(ps, o2, 64);
-            l[j] = l[j] * al[j] + ps;
-            m[j] = mn;
-            sh.p[wave][j][lane] = pr;
-        }
-        wave_lds_sync();
-        // Weighted V sums: dims lane and lane + 64, the keys in order, 8 at a time.
-#pragma unroll
-        for (int j = 0; j < (int)PX_WC; ++j) {
-            o[j][0] *= al[j];
-            o[j][1] *= al[j];
-        }
-        for (int vc = 0; vc < 8; ++vc) {
-            const uint4 a = *reinterpret_cast<const uint4*>(&sh.v[lane * X0NE_SPLIT_TILE + 8 * (vc ^ (lane % 8))]);
-            const uint4 b = *reinterpret_cast<const uint4*>(&sh.v[(lane + 64) * X0NE_SPLIT_TILE + 8 * (vc ^ (lane % 8))]);
-            const uint32_t ua[4] = {a.x, a.y, a.z, a.w}, ub[4] = {b.x, b.y, b.z, b.w};
-            double v0[8], v1[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v0[2 * e] = (double)bf_lo(ua[e]);
-                v0[2 * e + 1] = (double)bf_hi(ua[e]);
-                v1[2 * e] = (double)bf_lo(ub[e]);
-                v1[2 * e + 1] = (double)bf_hi(ub[e]);
-            }
-#pragma unroll
-            for (int j = 0; j < (int)PX_WC; ++j) {
-                const double* pj = &sh.p[wave][j][8 * vc];
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const double2 pp = *reinterpret_cast<const double2*>(pj + e);
-                    o[j][0] = fma(pp.x, v0[e], o[j][0]);
-                    o[j][1] = fma(pp.x, v1[e], o[j][1]);
-                    o[j][0] = fma(pp.y, v0[e + 1], o[j][0]);
-                    o[j][1] = fma(pp.y, v1[e + 1], o[j][1]);
-                }
-            }
-        }
-        wave_lds_sync();  // the next tile rewrites the weights
     }
+    // The column's weight sum over its 4 lanes (the same association in each).
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (!live) return;
+    bf16_t* op = out + ((size_t)r * q_heads + kh * G + col % G) * X0NE_HEAD_DIM;
 #pragma unroll
-    for (int j = 0; j < (int)PX_WC; ++j) {
-        const uint32_t c = PX_WC * wave + j, r = r0 + c / G;
-        if (r >= rows) continue;
-        bf16_t* op = out + ((size_t)r * q_heads + kh * G + c % G) * X0NE_HEAD_DIM;
-        op[lane] = f2bf((float)(o[j][0] / l[j]));
-        op[lane + 64] = f2bf((float)(o[j][1] / l[j]));
-    }
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) op[16 * db + q4 + 4 * i] = f2bf((float)(o[db][i] / lsum));
 }
 
 }  // namespace
 
 // x0ne_attention_prefill_exact_g{G}_bf16: the causal prefill of x0ne_attention_prefill_bf16
 // (same arguments; `scale` unused: the f64 1/sqrt(128)) in the exact mode's arithmetic, for G q
-// heads per kv head; grid (kv_heads, ceil(rows / (64 / G))), block 512.
+// heads per kv head; grid (kv_heads, ceil(rows / (64 / G))), block 256.
 #define X0NE_PREFILL_EXACT(G)                                                                                      \
     extern "C" __global__ void __launch_bounds__(PX_BLOCK) x0ne_attention_prefill_exact_g##G##_bf16(              \
         const bf16_t* __restrict__ q, const bf16_t* __restrict__ k_cache, const bf16_t* __restrict__ v_cache,    \

@@ -84,7 +84,7 @@ X0NE_DECLARE_PREFILL_GROUP(8)
 // ceil(rows / (X0NE_PREFILL_EXACT_COLS / G))), block X0NE_PREFILL_EXACT_THREADS (a block of
 // another size does nothing).
 #define X0NE_PREFILL_EXACT_COLS 64
-#define X0NE_PREFILL_EXACT_THREADS 512
+#define X0NE_PREFILL_EXACT_THREADS 256
 #define X0NE_DECLARE_PREFILL_EXACT(G)                                                                            \
     __global__ void x0ne_attention_prefill_exact_g##G##_bf16(                                                    \
         const bf16_t* q, const bf16_t* k_cache, const bf16_t* v_cache, const uint32_t* pages, bf16_t* out,       \

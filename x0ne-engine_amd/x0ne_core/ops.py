@@ -23,7 +23,7 @@ SPLIT_STATE = HEAD_DIM + 4
 PREFILL_COLS = 128  # columns (row, q head) per block of x0ne_attention_prefill_g*_bf16
 PREFILL_THREADS = 256  # its block
 PREFILL_EXACT_COLS = 64  # columns per block of x0ne_attention_prefill_exact_g*_bf16
-PREFILL_EXACT_THREADS = 512  # its block
+PREFILL_EXACT_THREADS = 256  # its block
 NAN_BF16 = 0x7FC0
 
 
