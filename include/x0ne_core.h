@@ -254,12 +254,12 @@ typedef struct x0ne_greedy x0ne_greedy;
      (split-K with f64 states merged in f64), so every rounding point of the step is the f64
      oracle's (oracle/src/lib.rs:123-187) and the greedy tokens are the oracle's; its prefill
      passes sum in f64 too (the same bits as feeding the prompt one decode step per token). It
-     serves a dense model decoding one sequence with 1, 2, 4 or 8 q
+     serves a dense or MoE model decoding one sequence with 1, 2, 4 or 8 q
      heads per kv head (X0NE_ERR_NOT_IMPLEMENTED otherwise).
      X0NE_SUMS_F32 is the fp32-accumulating path (the reference engine's arithmetic: f32 sums,
      matrix-core prefill passes).
      X0NE_SUMS_DEFAULT (0, what EngineOptions { max_ctx } gives) is the exact mode wherever the
-     engine can serve it, else the f32 path (MoE models, max_batch > 1).
+     engine can serve it, else the f32 path (max_batch > 1).
    - prefill_chunk: prompt rows per prefill pass (engine.rs:67, PREFILL_CHUNK); 0 takes
      min(2048, max_ctx x max_batch). A pass runs every layer over its rows with matrix-core
      GEMMs and the causal prefill attention (the exact mode's in f64; a MoE engine feeds a

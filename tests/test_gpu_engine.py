@@ -588,7 +588,8 @@ def test_a_moe_of_identical_experts_is_the_dense_model(experts, top_k):
     f32 down rows, weighted combination) whose experts all equal the dense MLP: top-1 weighs its
     expert exactly 1, and two experts with equal router logits route to [0, 1] at 0.5 each, so
     the combination is exact; the logits are the dense oracle's within the model tolerance
-    (gpu_engine.rs:29-32) at every position, graph and eager give the same bits, the routing
+    (gpu_engine.rs:29-32) at every position, and its very bits in the exact mode (a MoE engine's
+    default, f64 sums as the oracle's), graph and eager give the same bits, the routing
     diagnostic reads [0 .. top_k) at every layer and position, and the client bytes are zeroed."""
     from x0ne_core import DecodeMode, Engine, EngineOptions, Route
     f = Fixture(wide(), 41)
@@ -599,8 +600,10 @@ def test_a_moe_of_identical_experts_is_the_dense_model(experts, top_k):
     want = f.model.logits(ids)
     at = [0, 5, 11, 19]
     graph = e.logits_at(ids, at, Route.DECODE)
+    assert e.exact(), e.describe()
     for row, p in zip(graph, at):
         assert_logits(f"moe {experts}/{top_k} position {p}", row, want[p])
+        assert (row.view(np.uint32) == want[p].view(np.uint32)).all(), f"moe position {p}: the oracle's bits"
     e.set_decode_mode(DecodeMode.EAGER)
     eager = e.logits_at(ids, at, Route.DECODE)
     for a, b, p in zip(graph, eager, at):
@@ -725,8 +728,12 @@ def test_a_random_moe_routes_each_token_to_distinct_experts():
     rows = e.logits_at(ids, list(range(upto)), Route.DECODE)
     for p in range(upto):
         assert_logits(f"random moe position {p}", rows[p], want_rows[p])
-    print(f"MEASURE random MoE: routing equal to the host's at {upto} of {len(ids)} positions, logits compared there")
+    same = sum(int((rows[p].view(np.uint32) == want_rows[p].view(np.uint32)).all()) for p in range(upto))
+    print(f"MEASURE random MoE: routing equal to the host's at {upto} of {len(ids)} positions, logits compared "
+          f"there, {same} of them bit-equal")
     assert upto >= 8
+    # A MoE engine sums in f64 by default, as the oracle's kernels do: the same routing and bits.
+    assert e.exact() and upto == len(ids) and same == upto
     a = e.logits_at(ids, [3, 15], Route.DECODE)
     b = e.logits_at(ids, [3, 15], Route.DECODE)
     e.set_decode_mode(DecodeMode.EAGER)

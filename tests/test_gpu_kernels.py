@@ -986,6 +986,50 @@ def test_the_fused_moe_projections_are_the_composed_oracle(kernels, seed):
     print(f"MEASURE fused moe {what}: {exact:.4f} of the activations bit-equal to the oracle's")
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_the_exact_moe_projections_are_the_oracle_bit_for_bit(kernels, seed):
+    """The exact mode's MoE kernels against the oracle's composition, bit for bit: [gate; up]
+    with SwiGLU behind, each sum in f64 rounded to f32, is the oracle's expert GEMV then
+    bf16 and swiglu (oracle/src/lib.rs:284-312, :205-214); down with the f64 combination behind
+    is the oracle's f32 expert GEMV then combination (:314-329) rounded to bf16. Rows of up to
+    1592 columns, so the lanes' two-chunk loop runs; a slot without an expert gives NaN."""
+    g = np.random.default_rng(870 + seed)
+    experts = int(g.choice([2, 8]))
+    top_k = int(g.integers(1, experts + 1))
+    inter, hidden = 8 * int(g.integers(1, 100)), 8 * int(g.integers(1, 200))
+    if seed == 0:
+        inter, hidden = 8, 8
+    bf = lambda n, sd: O.bf16_round(g.normal(0, sd, n).astype(np.float32))
+    wgu, wd = bf(experts * 2 * inter * hidden, 0.2), bf(experts * hidden * inter, 0.2)
+    x = bf(hidden, 2.0)
+    if seed == 1:
+        x[:] = 0.0
+        x[::3] = -0.0
+    ids = g.integers(0, experts, top_k).astype(np.uint32)
+    if seed == 3:
+        ids[-1] = O.MOE_NO_EXPERT
+    wts = g.uniform(0.0, 1.0, top_k).astype(np.float32)
+    what = f"seed {seed}: {experts} experts, top {top_k}, inter {inter}, hidden {hidden}"
+    gu = O.moe_gemv(wgu, experts, 2 * inter, hidden, ids, x, top_k).reshape(top_k, 2 * inter)
+    act = kernels.moe_gate_up_swiglu(bf16_bits(wgu), experts, inter, hidden, ids, bf16_bits(x), exact=True)
+    act = act.reshape(top_k, inter)
+    want_act = np.stack([O.bf16_round(O.swiglu(O.bf16_round(gu[s]))) for s in range(top_k)])
+    for s in range(top_k):
+        if ids[s] == O.MOE_NO_EXPERT:
+            assert np.isnan(bf16_vals(act[s])).all(), f"{what}: slot {s} without an expert"
+            continue
+        assert (act[s] == bf16_bits(want_act[s])).all(), f"{what}: slot {s} activations"
+    act_in = np.where(np.isnan(want_act), np.float32(0.5), want_act).astype(np.float32)
+    y = O.moe_gemv(wd, experts, hidden, inter, ids, act_in, 1).reshape(top_k, hidden)
+    out = kernels.moe_down_combine(bf16_bits(wd), experts, hidden, inter, ids, wts, bf16_bits(act_in.ravel()),
+                                   exact=True)
+    if (ids == O.MOE_NO_EXPERT).any():
+        assert np.isnan(bf16_vals(out)).all(), f"{what}: a slot without an expert makes the row NaN"
+    else:
+        want = bf16_bits(O.bf16_round(O.moe_combine(y, wts, hidden, top_k)))
+        assert (out == want).all(), f"{what}: output {int(np.argmax(out != want))}"
+
+
 def test_moe_routing_refuses_what_the_kernel_does_not_take(kernels):
     """gpu_kernels.rs:915-930."""
     from x0ne_core import FormatError

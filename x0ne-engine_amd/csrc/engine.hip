@@ -192,14 +192,14 @@ x0ne_status parse_config(const char* json_text, Cfg* c) {
 }
 
 // The accumulation an engine runs with: f64 when asked, or by default wherever this build has the
-// exact kernels (a dense model decoding one sequence, 1, 2, 4 or 8 q heads per kv head); f32
-// when asked, and by default for MoE and batched engines (check_config has refused an f64
-// request those cannot serve).
+// exact kernels (a dense or MoE model decoding one sequence, 1, 2, 4 or 8 q heads per kv head);
+// f32 when asked, and by default for batched engines (check_config has refused an f64 request
+// those cannot serve).
 bool exact_sums(const Cfg& c, const x0ne_engine_options& o) {
     if (o.sums == X0NE_SUMS_F64) return true;
     if (o.sums == X0NE_SUMS_F32) return false;
     const uint64_t grp = c.kv_heads ? c.q_heads / c.kv_heads : 0;
-    return !c.moe && (o.max_batch == 0 || o.max_batch == 1) && (grp == 1 || grp == 2 || grp == 4 || grp == 8);
+    return (o.max_batch == 0 || o.max_batch == 1) && (grp == 1 || grp == 2 || grp == 4 || grp == 8);
 }
 
 // What the kernels and the arena of this build accept (engine.rs:236-289 for the reference's
@@ -238,14 +238,13 @@ x0ne_status check_config(const Cfg& c, const x0ne_engine_options& o) {
     if (o.sums > X0NE_SUMS_F32) return no("sums " + std::to_string(o.sums) + ": 0 (default), 1 (f64) or 2 (f32)");
     if (o.sums == X0NE_SUMS_F64) {
         if (batch > 1) return fail(X0NE_ERR_NOT_IMPLEMENTED, "batched decoding with f64 sums");
-        if (c.moe) return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
         const uint64_t grp = c.q_heads / c.kv_heads;
         if (grp != 1 && grp != 2 && grp != 4 && grp != 8)
             return fail(X0NE_ERR_NOT_IMPLEMENTED,
                         "f64 sums: the exact attention kernels take 1, 2, 4 or 8 q heads per kv head, not " +
                             std::to_string(grp));
     }
-    if (c.moe && batch > 1) return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence with f32 sums");
+    if (c.moe && batch > 1) return fail(X0NE_ERR_NOT_IMPLEMENTED, "a MoE engine decodes one sequence");
     // The attention kernels address a K or V plane (every sequence's pages of one layer) by 32-bit
     // byte offsets into a buffer resource of 0xFFFFFFF0 bytes, the offset 0xFFFFFFF0 standing for
     // "no key" (attention.hip, OFF_NONE). A plane must therefore end at or below that offset;
@@ -848,8 +847,21 @@ x0ne_status launch_moe(x0ne_engine* e, uint64_t l) {
         void* args[] = {(void*)&rin, (void*)&rout, (void*)&dl, (void*)&nw, (void*)&xo, (void*)&h, (void*)&eps};
         X0NE_TRY(launch_rows(e, (const void*)&x0ne_add_rmsnorm_to_bf16, dim3(1), dim3(256), args, "moe norm"));
     }
-    X0NE_TRY(x0ne_gpu_gemv(e->gpu, (uint64_t)(uintptr_t)e->d(w.router), c.experts, c.hidden,
-                           (uint64_t)(uintptr_t)e->d(e->m_x), 1, (uint64_t)(uintptr_t)e->d(e->m_logits), 1));
+    {  // router logits in f32, summed as the engine sums
+        X0neGemv r = {};
+        r.w = (const uint16_t*)e->d(w.router);
+        r.x = (const uint16_t*)e->d(e->m_x);
+        r.y = e->d(e->m_logits);
+        r.rows = ne;
+        r.cols = h;
+        r.prologue = 0;
+        r.epilogue = 1;
+        r.grid = x0ne_gemv_grid(r, e->gpu->cus, 0);
+        r.f64acc = e->f64_sums;
+        e->gpu->counts.gemms++;
+        e->gpu->counts.launches++;
+        X0NE_HIP(x0ne_launch_gemv(r, e->gpu->stream), "router gemv");
+    }
     void* ids = e->d(e->m_ids) + l * c.top_k * 4;
     void* wts = e->d(e->m_w) + l * c.top_k * 4;
     {
@@ -862,8 +874,10 @@ x0ne_status launch_moe(x0ne_engine* e, uint64_t l) {
         const void* x = e->d(e->m_x);
         void* act = e->d(e->m_act);
         void* args[] = {(void*)&wg, (void*)&ids, (void*)&x, (void*)&act, (void*)&mi, (void*)&h, (void*)&ne};
-        X0NE_TRY(launch_rows(e, (const void*)&x0ne_moe_gate_up_swiglu_bf16, dim3((mi + 7) / 8, k), dim3(256), args,
-                             "moe gate_up + swiglu"));
+        X0NE_TRY(launch_rows(e,
+                             e->f64_sums ? (const void*)&x0ne_moe_gate_up_swiglu_exact_bf16
+                                         : (const void*)&x0ne_moe_gate_up_swiglu_bf16,
+                             dim3((mi + 7) / 8, k), dim3(256), args, "moe gate_up + swiglu"));
     }
     const void* wd = e->d(w.down);
     const void* wc = wts;
@@ -871,8 +885,10 @@ x0ne_status launch_moe(x0ne_engine* e, uint64_t l) {
     void* out = e->d(e->delta);
     void* args[] = {(void*)&wd, (void*)&ids, (void*)&wc, (void*)&act, (void*)&out, (void*)&h, (void*)&mi, (void*)&ne,
                     (void*)&k};
-    return launch_rows(e, (const void*)&x0ne_moe_down_combine_bf16, dim3((h + 7) / 8), dim3(256), args,
-                       "moe down + combination");
+    return launch_rows(e,
+                       e->f64_sums ? (const void*)&x0ne_moe_down_combine_exact_bf16
+                                   : (const void*)&x0ne_moe_down_combine_bf16,
+                       dim3((h + 7) / 8), dim3(256), args, "moe down + combination");
 }
 
 x0ne_status step_launches(x0ne_engine* e) {

@@ -155,6 +155,11 @@ __global__ void x0ne_moe_gate_up_swiglu_bf16(const bf16_t* w, const uint32_t* id
 __global__ void x0ne_moe_down_combine_bf16(const bf16_t* w, const uint32_t* ids, const float* wts, const bf16_t* act,
                                            bf16_t* out, uint32_t hidden, uint32_t inter, uint32_t experts,
                                            uint32_t top_k);
+__global__ void x0ne_moe_gate_up_swiglu_exact_bf16(const bf16_t* w, const uint32_t* ids, const bf16_t* x, bf16_t* act,
+                                                   uint32_t inter, uint32_t cols, uint32_t experts);
+__global__ void x0ne_moe_down_combine_exact_bf16(const bf16_t* w, const uint32_t* ids, const float* wts,
+                                                 const bf16_t* act, bf16_t* out, uint32_t hidden, uint32_t inter,
+                                                 uint32_t experts, uint32_t top_k);
 __global__ void x0ne_panel_bf16(const bf16_t* src, bf16_t* dst, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_bf16(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);
 __global__ void x0ne_gemv_f32(const bf16_t* w, const bf16_t* x, void* y, uint32_t rows, uint32_t cols);

@@ -39,8 +39,8 @@ __device__ __forceinline__ bool earlier(float v, uint32_t i, float bv, uint32_t 
 // Sum over the 64 lanes of R values, transposing: at each of the first log2(R) steps a lane
 // keeps half of its values (lane bit set: the upper half) and adds its partner's copy of them,
 // then plain butterflies. Lane l ends with the whole sum of value `row_of_lane<R>(l)`.
-template <int R>
-__device__ __forceinline__ float rows_sum(float (&v)[R], uint32_t lane) {
+template <int R, class Acc>
+__device__ __forceinline__ Acc rows_sum(Acc (&v)[R], uint32_t lane) {
     int n = R;
 #pragma unroll
     for (int k = 5; k >= 0; --k) {
@@ -50,8 +50,8 @@ __device__ __forceinline__ float rows_sum(float (&v)[R], uint32_t lane) {
 #pragma unroll
             for (int j = 0; j < R / 2; ++j)
                 if (j < h) {
-                    const float give = up ? v[j] : v[j + h];
-                    const float keep = up ? v[j + h] : v[j];
+                    const Acc give = up ? v[j] : v[j + h];
+                    const Acc keep = up ? v[j + h] : v[j];
                     v[j] = keep + __shfl_xor(give, 1 << k, 64);
                 }
             n = h;
@@ -75,22 +75,20 @@ __device__ __forceinline__ uint32_t row_of_lane(uint32_t lane) {
 }
 
 // Dot products of R rows (16-byte chunk pointers, each `chunks` long) with x over the lanes'
-// chunks, two chunks of each row in flight; lane l ends with row row_of_lane<R>(l)'s sum.
-template <int R>
-__device__ __forceinline__ float rows_dot(const uint4* const (&w)[R], const uint4* __restrict__ x, uint32_t chunks,
-                                          uint32_t lane) {
-    float acc[R];
+// chunks, two chunks of each row in flight; lane l ends with row row_of_lane<R>(l)'s sum. Acc =
+// float: f32 FMA from 0 (each bf16 product exact in f32); double: each exact product added in
+// f64 from -0.0, as the oracle's GEMV sums (oracle/src/lib.rs:123-133).
+template <int R, class Acc = float>
+__device__ __forceinline__ Acc rows_dot(const uint4* const (&w)[R], const uint4* __restrict__ x, uint32_t chunks,
+                                        uint32_t lane) {
+    constexpr Acc zero = sizeof(Acc) == 8 ? (Acc)-0.0 : (Acc)0.0;
+    Acc acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-    auto madd = [](float a, uint4 p, uint4 q) {
-        a = fmaf(bf_lo(p.x), bf_lo(q.x), a);
-        a = fmaf(bf_hi(p.x), bf_hi(q.x), a);
-        a = fmaf(bf_lo(p.y), bf_lo(q.y), a);
-        a = fmaf(bf_hi(p.y), bf_hi(q.y), a);
-        a = fmaf(bf_lo(p.z), bf_lo(q.z), a);
-        a = fmaf(bf_hi(p.z), bf_hi(q.z), a);
-        a = fmaf(bf_lo(p.w), bf_lo(q.w), a);
-        return fmaf(bf_hi(p.w), bf_hi(q.w), a);
+    for (int r = 0; r < R; ++r) acc[r] = zero;
+    auto madd = [](Acc a, uint4 p, uint4 q) {
+        const Acc xs[8] = {(Acc)bf_lo(q.x), (Acc)bf_hi(q.x), (Acc)bf_lo(q.y), (Acc)bf_hi(q.y),
+                           (Acc)bf_lo(q.z), (Acc)bf_hi(q.z), (Acc)bf_lo(q.w), (Acc)bf_hi(q.w)};
+        return dot8<Acc>(p, xs, a);
     };
     uint32_t c = lane;
     for (; c + 64 < chunks; c += 128) {
@@ -109,7 +107,7 @@ __device__ __forceinline__ float rows_dot(const uint4* const (&w)[R], const uint
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = madd(acc[r], w[r][c], xa);
     }
-    return rows_sum<R>(acc, lane);
+    return rows_sum<R, Acc>(acc, lane);
 }
 
 }  // namespace
@@ -258,14 +256,14 @@ extern "C" __global__ void __launch_bounds__(256)
         weigh_slots(weights + (size_t)r * top_k, y + (size_t)r * top_k * hidden + i, hidden, top_k);
 }
 
-// x0ne_moe_gate_up_swiglu_bf16: grid (ceil(inter / 2 / 4) = ceil(inter / 8), slots), block 256.
-// W [experts][2 inter][cols] holds each expert's gate rows then up rows; act[s][i] =
-// bf16(silu(bf16 g) bf16 u) for g, u = rows i and inter + i of expert ids[s] against x (shared
-// by the slots); a wavefront takes 2 activations (4 rows). An id >= experts gives NaN.
-extern "C" __global__ void __launch_bounds__(256)
-    x0ne_moe_gate_up_swiglu_bf16(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
-                                 const bf16_t* __restrict__ x, bf16_t* __restrict__ act, uint32_t inter, uint32_t cols,
-                                 uint32_t experts) {
+namespace {
+
+// [gate; up] of expert ids[slot] with SwiGLU behind: a wavefront takes 2 activations (4 rows).
+// Each projection's sum is rounded to f32 (the oracle's GEMV output), then to bf16.
+template <class Acc>
+__device__ __forceinline__ void gate_up_swiglu(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
+                                               const bf16_t* __restrict__ x, bf16_t* __restrict__ act, uint32_t inter,
+                                               uint32_t cols, uint32_t experts) {
     constexpr int R = 4;  // gate i0, gate i0 + 1, up i0, up i0 + 1
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t i0 = (blockIdx.x * 4 + wave) * 2, slot = blockIdx.y;
@@ -281,7 +279,7 @@ extern "C" __global__ void __launch_bounds__(256)
             wr[j] = reinterpret_cast<const uint4*>(w + (base + i) * cols);
             wr[2 + j] = reinterpret_cast<const uint4*>(w + (base + inter + i) * cols);
         }
-        sum = rows_dot<R>(wr, reinterpret_cast<const uint4*>(x), cols / 8, lane);
+        sum = (float)rows_dot<R, Acc>(wr, reinterpret_cast<const uint4*>(x), cols / 8, lane);
     }
     // Lanes holding up sums (k = 2, 3) sit 32 above the gate sums of the same activation.
     const float up = __shfl_xor(sum, 32, 64);
@@ -292,14 +290,16 @@ extern "C" __global__ void __launch_bounds__(256)
     }
 }
 
-// x0ne_moe_down_combine_bf16: grid (ceil(hidden / 8)), block 256. out[i] = bf16(sum_s wts[s]
-// y_s[i]), y_s[i] = row i of expert ids[s]'s down matrix W [experts][hidden][inter] against
-// act[s] (f32), the slots added in order: x0ne_moe_gemv_f32 then x0ne_moe_combine_bf16 in one
-// launch. A wavefront takes 2 output rows over every slot (top_k <= 32).
-extern "C" __global__ void __launch_bounds__(256)
-    x0ne_moe_down_combine_bf16(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
-                               const float* __restrict__ wts, const bf16_t* __restrict__ act, bf16_t* __restrict__ out,
-                               uint32_t hidden, uint32_t inter, uint32_t experts, uint32_t top_k) {
+// Down rows of every slot's expert with the weighted combination behind: a wavefront takes 2
+// output rows over every slot (top_k <= 32), each slot's row sum rounded to f32 (the oracle's
+// f32 expert GEMV) and staged in LDS, then weighed in slot order: Acc = float, f32 FMA from 0;
+// double, each product of two f32 values (exact in f64) added in f64 from -0.0 as the oracle's
+// combination (oracle/src/lib.rs:314-329), one rounding to f32 and one to bf16.
+template <class Acc>
+__device__ __forceinline__ void down_combine(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
+                                             const float* __restrict__ wts, const bf16_t* __restrict__ act,
+                                             bf16_t* __restrict__ out, uint32_t hidden, uint32_t inter,
+                                             uint32_t experts, uint32_t top_k) {
     constexpr int R = 2;
     __shared__ float ys[4][MAX_TOP_K][R];
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -312,10 +312,58 @@ extern "C" __global__ void __launch_bounds__(256)
         if (e < experts) {
             const uint4* wr[R];
             expert_rows<R>(w, e, hidden, inter, r0, wr);
-            sum = rows_dot<R>(wr, reinterpret_cast<const uint4*>(act + (size_t)s * inter), inter / 8, lane);
+            sum = (float)rows_dot<R, Acc>(wr, reinterpret_cast<const uint4*>(act + (size_t)s * inter), inter / 8, lane);
         }
         if ((lane & 31) == 0) ys[wave][s][k] = sum;
     }
     wave_lds_wait();
-    if (lane < (uint32_t)R && r0 + lane < hidden) out[r0 + lane] = weigh_slots(wts, &ys[wave][0][lane], R, top_k);
+    if (lane < (uint32_t)R && r0 + lane < hidden) {
+        if (sizeof(Acc) == 8) {
+            double acc = -0.0;
+            for (uint32_t s = 0; s < top_k; ++s) acc += (double)wts[s] * (double)ys[wave][s][lane];
+            out[r0 + lane] = f2bf((float)acc);
+        } else {
+            out[r0 + lane] = weigh_slots(wts, &ys[wave][0][lane], R, top_k);
+        }
+    }
+}
+
+}  // namespace
+
+// x0ne_moe_gate_up_swiglu_bf16 / _exact_bf16: grid (ceil(inter / 2 / 4) = ceil(inter / 8),
+// slots), block 256. W [experts][2 inter][cols] holds each expert's gate rows then up rows;
+// act[s][i] = bf16(silu(bf16 g) bf16 u) for g, u = rows i and inter + i of expert ids[s] against
+// x (shared by the slots), summed in f32 (_bf16) or f64 (_exact_bf16). An id >= experts gives NaN.
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_moe_gate_up_swiglu_bf16(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
+                                 const bf16_t* __restrict__ x, bf16_t* __restrict__ act, uint32_t inter, uint32_t cols,
+                                 uint32_t experts) {
+    gate_up_swiglu<float>(w, ids, x, act, inter, cols, experts);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_moe_gate_up_swiglu_exact_bf16(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
+                                       const bf16_t* __restrict__ x, bf16_t* __restrict__ act, uint32_t inter,
+                                       uint32_t cols, uint32_t experts) {
+    gate_up_swiglu<double>(w, ids, x, act, inter, cols, experts);
+}
+
+// x0ne_moe_down_combine_bf16 / _exact_bf16: grid (ceil(hidden / 8)), block 256. out[i] =
+// bf16(sum_s wts[s] y_s[i]), y_s[i] = row i of expert ids[s]'s down matrix W
+// [experts][hidden][inter] against act[s] (f32), the slots added in order: x0ne_moe_gemv_f32
+// then x0ne_moe_combine_bf16 in one launch (_bf16), or the same with f64 sums and an f64
+// combination (_exact_bf16).
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_moe_down_combine_bf16(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
+                               const float* __restrict__ wts, const bf16_t* __restrict__ act, bf16_t* __restrict__ out,
+                               uint32_t hidden, uint32_t inter, uint32_t experts, uint32_t top_k) {
+    down_combine<float>(w, ids, wts, act, out, hidden, inter, experts, top_k);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    x0ne_moe_down_combine_exact_bf16(const bf16_t* __restrict__ w, const uint32_t* __restrict__ ids,
+                                     const float* __restrict__ wts, const bf16_t* __restrict__ act,
+                                     bf16_t* __restrict__ out, uint32_t hidden, uint32_t inter, uint32_t experts,
+                                     uint32_t top_k) {
+    down_combine<double>(w, ids, wts, act, out, hidden, inter, experts, top_k);
 }

@@ -929,10 +929,10 @@ class Kernels:
         self.gpu.sync()
         return a.read_array(out, 0, rows * hidden, np.uint16)
 
-    def moe_gate_up_swiglu(self, w, experts: int, inter: int, cols: int, ids, x) -> np.ndarray:
-        """x0ne_moe_gate_up_swiglu_bf16: act[s] = bf16(silu(bf16 g) bf16 u) for the gate and up
-        rows of expert ids[s] (W [experts][2 inter][cols] bf16 bits) against x; [slots][inter]
-        bf16 bits."""
+    def moe_gate_up_swiglu(self, w, experts: int, inter: int, cols: int, ids, x, exact: bool = False) -> np.ndarray:
+        """x0ne_moe_gate_up_swiglu_bf16 (exact: _exact_bf16, the sums in f64): act[s] =
+        bf16(silu(bf16 g) bf16 u) for the gate and up rows of expert ids[s] (W [experts][2
+        inter][cols] bf16 bits) against x; [slots][inter] bf16 bits."""
         w = np.ascontiguousarray(w, np.uint16).ravel()
         x = np.ascontiguousarray(x, np.uint16).ravel()
         ids = np.ascontiguousarray(ids, np.uint32).ravel()
@@ -946,16 +946,19 @@ class Kernels:
         a.write(ws, 0, w)
         a.write(is_, 0, ids)
         a.write(xs, 0, x)
-        self.gpu.launch("x0ne_moe_gate_up_swiglu_bf16", ((inter + 7) // 8, ids.size), 256,
+        self.gpu.launch("x0ne_moe_gate_up_swiglu_exact_bf16" if exact else "x0ne_moe_gate_up_swiglu_bf16",
+                        ((inter + 7) // 8, ids.size), 256,
                         [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(is_)), Arg.ptr(a.ptr(xs)), Arg.ptr(a.ptr(act)),
                          Arg.u32(inter), Arg.u32(cols), Arg.u32(experts)])
         self.gpu.sync()
         return a.read_array(act, 0, ids.size * inter, np.uint16)
 
-    def moe_down_combine(self, w, experts: int, hidden: int, inter: int, ids, weights, act) -> np.ndarray:
-        """x0ne_moe_down_combine_bf16: out = bf16(sum_s weights[s] W[ids[s]] act[s]) (the down rows
-        in f32, the combination in slot order); W [experts][hidden][inter] bf16 bits, act
-        [slots][inter] bf16 bits; hidden bf16 bits."""
+    def moe_down_combine(self, w, experts: int, hidden: int, inter: int, ids, weights, act,
+                         exact: bool = False) -> np.ndarray:
+        """x0ne_moe_down_combine_bf16 (exact: _exact_bf16, the sums and the combination in f64):
+        out = bf16(sum_s weights[s] W[ids[s]] act[s]) (the down rows rounded to f32, the
+        combination in slot order); W [experts][hidden][inter] bf16 bits, act [slots][inter] bf16
+        bits; hidden bf16 bits."""
         w = np.ascontiguousarray(w, np.uint16).ravel()
         act = np.ascontiguousarray(act, np.uint16).ravel()
         ids = np.ascontiguousarray(ids, np.uint32).ravel()
@@ -973,7 +976,8 @@ class Kernels:
         a.write(is_, 0, ids)
         a.write(wts, 0, wt)
         a.write(xs, 0, act)
-        self.gpu.launch("x0ne_moe_down_combine_bf16", (hidden + 7) // 8, 256,
+        self.gpu.launch("x0ne_moe_down_combine_exact_bf16" if exact else "x0ne_moe_down_combine_bf16",
+                        (hidden + 7) // 8, 256,
                         [Arg.ptr(a.ptr(ws)), Arg.ptr(a.ptr(is_)), Arg.ptr(a.ptr(wts)), Arg.ptr(a.ptr(xs)),
                          Arg.ptr(a.ptr(out)), Arg.u32(hidden), Arg.u32(inter), Arg.u32(experts), Arg.u32(k)])
         self.gpu.sync()
