@@ -809,12 +809,18 @@ constexpr uint32_t EXACT_CHUNK = 40;  // slices whose f64 o values the exact mer
 // The exact kernel's slices: runs of whole 64-key tiles (a wavefront's page each per tile). The
 // finest split that fills P slices costs a second round trip in the merge past EXACT_CHUNK
 // slices; longer runs that keep one round trip are taken unless they add more than two pages per
-// wavefront per extra round trip saved (a page costs about 1.5 us, a round trip about 3 us). On
+// wavefront per extra round trip saved (a page costs about 1.5 us, a round trip about 3 us). Two
+// tiles stay in one slice: a second page per wavefront costs less than the cross-slice merge. On
 // MI355X at 8 kv heads, P 64, against runs of at least 4 tiles: 164 keys 12.8 -> 11.5 us, 300
 // keys 17.4 -> 11.4, 1024 keys 18.1 -> 12.8, 2048 keys 18.8 -> 15.6; 8k to 32k unchanged.
 __device__ __forceinline__ Split split_exact(uint32_t ctx, uint32_t P) {
     Split s;
     s.ntiles = (ctx + X0NE_SPLIT_TILE - 1) / X0NE_SPLIT_TILE;
+    if (s.ntiles <= 2) {
+        s.per = s.ntiles;
+        s.active = 1;
+        return s;
+    }
     const uint32_t fine = (s.ntiles + P - 1) / P;
     const uint32_t cap = min(P, EXACT_CHUNK);
     const uint32_t one = (s.ntiles + cap - 1) / cap;
